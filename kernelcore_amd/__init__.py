@@ -1,0 +1,236 @@
+"""Python bindings of libkernelcore_amd.so (the kc* C ABI in include/kernelcore/kc.h).
+
+The library is the product: HIP kernels for gfx950 plus the kc* runtime in C++. This module is a
+thin ctypes layer for tests and benchmarks; it holds no compute of its own and never falls back
+to a CPU path. If the shared library is missing it raises, and on a machine without a GPU
+``kcInit`` returns an error that surfaces as ``KcError``.
+
+Struct layouts mirror include/kernelcore/llm_kernels.h (which keeps the field order of the
+reference's llm/llm_kernels.hpp).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+LIB_PATH = os.path.join(HERE, "libkernelcore_amd.so")
+HEADERS = [os.path.join(ROOT, "include", "kernelcore", n) for n in ("kc.h", "llm_kernels.h")]
+
+ERRORS = ["Success", "NotInitialized", "InvalidValue", "InvalidDevice", "OutOfMemory", "InvalidPointer",
+          "InvalidResourceHandle", "UnsupportedOperation", "InvalidKernelImage", "KernelNotFound",
+          "DynamicCodeBlocked", "LaunchFailure", "KernelFault", "ContextPoisoned", "NotReady", "InternalError"]
+ERR = {name: i for i, name in enumerate(ERRORS)}
+HOST_TO_DEVICE, DEVICE_TO_HOST, DEVICE_TO_DEVICE, HOST_TO_HOST = range(4)
+QTYPE = {"q4k": 12, "q6k": 14}
+BLOCK_BYTES = {"q4k": 144, "q6k": 210}
+
+_p = C.c_void_p
+_i = C.c_int
+_f = C.c_float
+
+
+class KcError(RuntimeError):
+    def __init__(self, fn, code, detail):
+        self.code = code
+        self.name = ERRORS[code] if 0 <= code < len(ERRORS) else f"error {code}"
+        super().__init__(f"{fn}: {self.name}" + (f" ({detail})" if detail else ""))
+
+
+# ---- argument structs (include/kernelcore/llm_kernels.h) -----------------------------------------
+
+def _struct(name, fields):
+    return type(name, (C.Structure,), {"_fields_": fields})
+
+
+VectorAddArgs = _struct("VectorAddArgs", [("a", _p), ("b", _p), ("out", _p), ("count", _i)])
+QuantizeArgs = _struct("QuantizeArgs", [("x", _p), ("xq", _p), ("xd", _p), ("count", _i)])
+MatvecQ4Q8Args = _struct("MatvecQ4Q8Args", [("qw", _p), ("xq", _p), ("xd", _p), ("y", _p), ("dims", _p),
+                                            ("rows", _i), ("k", _i)])
+MatmulKQ8Args = _struct("MatmulKQ8Args", [("qw", _p), ("xq", _p), ("y", _p), ("dims", _p), ("rows", _i), ("k", _i),
+                                          ("ncols", _i), ("row_block", _i)])
+QuantizeColsArgs = _struct("QuantizeColsArgs", [("x", _p), ("q", _p), ("dims", _p), ("k", _i), ("ncols", _i)])
+RmsNormArgs = _struct("RmsNormArgs", [("x", _p), ("w", _p), ("y", _p), ("n", _i), ("rows", _i), ("eps", _f)])
+MulRowsArgs = _struct("MulRowsArgs", [("x", _p), ("w", _p), ("y", _p), ("n", _i), ("count", _i)])
+RopeGgmlArgs = _struct("RopeGgmlArgs", [("x", _p), ("y", _p), ("pos", _p), ("ff", _p), ("dims", _p), ("head_dim", _i),
+                                        ("n_head", _i), ("n_tokens", _i), ("log2_base", _f), ("neox", C.c_bool)])
+AddSumsqFArgs = _struct("AddSumsqFArgs", [("a", _p), ("b", _p), ("out", _p), ("q", _p), ("dims", _p), ("n", _i),
+                                          ("rows", _i)])
+SumsqPartArgs = _struct("SumsqPartArgs", [("x", _p), ("q", _p), ("dims", _p), ("n", _i), ("rows", _i)])
+NormMulQ8Args = _struct("NormMulQ8Args", [("x", _p), ("w", _p), ("y", _p), ("q", _p), ("dims", _p), ("n", _i),
+                                          ("rows", _i), ("eps", _f)])
+SiluMulQ8FArgs = _struct("SiluMulQ8FArgs", [("g", _p), ("u", _p), ("y", _p), ("q", _p), ("dims", _p), ("n", _i),
+                                            ("cols", _i)])
+SiluMulArgs = _struct("SiluMulArgs", [("g", _p), ("u", _p), ("out", _p), ("count", _i)])
+SetRowsF16Args = _struct("SetRowsF16Args", [("src", _p), ("idx", _p), ("dst", _p), ("dims", _p), ("pairs", _i),
+                                            ("rows", _i), ("src_row", _i), ("dst_row", _i), ("dst_rows", _i)])
+FaDims = _struct("FaDims", [(n, _i) for n in ("H", "T", "D", "group", "tp", "k_row", "k_head", "v_row", "v_head",
+                                              "N", "q_tok", "q_head", "m_row", "has_mask", "H_kv")])
+FaScoresArgs = _struct("FaScoresArgs", [("q", _p), ("k", _p), ("mask", _p), ("s", _p), ("dims", _p), ("d", FaDims),
+                                        ("scale", _f)])
+FaMaxArgs = _struct("FaMaxArgs", [("s", _p), ("m", _p), ("dims", _p), ("d", FaDims)])
+FaExpArgs = _struct("FaExpArgs", [("s", _p), ("m", _p), ("dims", _p), ("d", FaDims)])
+FaValuesArgs = _struct("FaValuesArgs", [("p", _p), ("v", _p), ("out", _p), ("dims", _p), ("d", FaDims)])
+KquantRepackArgs = _struct("KquantRepackArgs", [("src", _p), ("dst", _p), ("qtype", _i), ("rows", _i), ("k", _i)])
+DeviceProperties = _struct("DeviceProperties", [("name", C.c_char * 128), ("worker_count", C.c_uint),
+                                                ("performance_workers", C.c_uint), ("total_memory", C.c_size_t),
+                                                ("is_hardware_gpu", C.c_bool), ("guard_pages", C.c_bool),
+                                                ("large_pages", C.c_bool), ("kernel_stack_bytes", C.c_size_t)])
+KernelEntry = _struct("KernelEntry", [("name", C.c_char_p), ("validate", _p), ("launch", _p), ("chunkable", _i)])
+
+# ---- library ----------------------------------------------------------------------------------------
+
+_LIB = None
+
+
+def build(jobs: int = 8) -> None:
+    """Compiles libkernelcore_amd.so for gfx950 (make -C kernelcore_amd)."""
+    subprocess.run(["make", "-s", "-C", HERE, f"-j{jobs}"], check=True)
+
+
+def declared_symbols():
+    """Every function the public headers declare with KC_API."""
+    names = set()
+    for h in HEADERS:
+        text = open(h).read()
+        for m in re.finditer(r"KC_API\s+[^;(]*?\b(kc\w+)\s*\(", text):
+            names.add(m.group(1))
+    return sorted(names)
+
+
+def lib():
+    """The loaded library; raises if it was not built (there is no fallback)."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is missing: build it with __graft_entry__.build() or make -C kernelcore_amd")
+        L = C.CDLL(LIB_PATH)
+        for name in declared_symbols():
+            getattr(L, name).restype = _i
+        for name in ("kcGetErrorString", "kcCodegenName", "kcGetLastErrorDetail"):
+            getattr(L, name).restype = C.c_char_p
+        L.kcMalloc.argtypes = [C.POINTER(_p), C.c_size_t]
+        L.kcFree.argtypes = [_p]
+        L.kcMemcpy.argtypes = [_p, _p, C.c_size_t, _i]
+        L.kcMemset.argtypes = [_p, _i, C.c_size_t]
+        L.kcLaunchKernel.argtypes = [C.c_char_p, _p, _p]
+        L.kcLaunchKernelChunked.argtypes = [C.c_char_p, _p, C.c_uint, C.c_int64, _p]
+        L.kcKquantStreamBytes.argtypes = [_i, _i, _i, C.POINTER(C.c_size_t)]
+        L.kcEventElapsedTime.argtypes = [C.POINTER(_f), _p, _p]
+        for n in ("kcEventRecord", "kcStreamWaitEvent"):
+            getattr(L, n).argtypes = [_p, _p]
+        L.kcSetKernelOption.argtypes = [C.c_char_p, _i]
+        L.kcGetKernelOption.argtypes = [C.c_char_p, C.POINTER(_i)]
+        L.kcGetErrorString.argtypes = [_i]
+        L.kcCodegenName.argtypes = [_i]
+        _LIB = L
+    return _LIB
+
+
+def check(fn, code):
+    if code != 0:
+        raise KcError(fn, code, lib().kcGetLastErrorDetail().decode(errors="replace"))
+
+
+def call(fn, *args):
+    """Calls kc<fn>(*args) and raises KcError on failure."""
+    check(fn, getattr(lib(), fn)(*args))
+
+
+def status(fn, *args):
+    """Calls kc<fn>(*args) and returns the error name ("Success", "InvalidValue", ...)."""
+    return ERRORS[getattr(lib(), fn)(*args)]
+
+
+def stream_bytes(qtype, rows, k):
+    n = C.c_size_t()
+    call("kcKquantStreamBytes", QTYPE[qtype], rows, k, C.byref(n))
+    return n.value
+
+
+class Buffer:
+    """A kcMalloc allocation with numpy transfers."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        p = _p()
+        call("kcMalloc", C.byref(p), max(self.nbytes, 1))
+        self.ptr = p.value
+
+    @classmethod
+    def of(cls, array):
+        a = np.ascontiguousarray(array)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, array, offset=0):
+        a = np.ascontiguousarray(array)
+        if a.nbytes:
+            call("kcMemcpy", self.ptr + offset, a.ctypes.data, a.nbytes, HOST_TO_DEVICE)
+
+    def download(self, dtype, count=None, offset=0):
+        dtype = np.dtype(dtype)
+        if count is None:
+            count = (self.nbytes - offset) // dtype.itemsize
+        out = np.empty(count, dtype)
+        if out.nbytes:
+            call("kcMemcpy", out.ctypes.data, self.ptr + offset, out.nbytes, DEVICE_TO_HOST)
+        return out
+
+    def at(self, offset):
+        return self.ptr + offset
+
+    def free(self):
+        if self.ptr:
+            lib().kcFree(self.ptr)
+            self.ptr = None
+
+
+def init():
+    call("kcInit")
+
+
+def launch(name, args, stream=None):
+    check(f"kcLaunchKernel({name})", lib().kcLaunchKernel(name.encode(), C.byref(args), stream))
+
+
+def launch_status(name, args, stream=None):
+    return ERRORS[lib().kcLaunchKernel(name.encode(), C.byref(args), stream)]
+
+
+def synchronize():
+    call("kcDeviceSynchronize")
+
+
+def set_option(name, value):
+    call("kcSetKernelOption", name.encode(), value)
+
+
+def device_properties():
+    p = DeviceProperties()
+    call("kcGetDeviceProperties", C.byref(p), 0)
+    return p
+
+
+# ---- typed helpers over the built-in kernels ---------------------------------------------------------
+
+def repack(qtype, blocks: Buffer, rows, k, stream=None):
+    """ggml blocks (rows x k/256, device) -> a new weight-stream Buffer."""
+    out = Buffer(stream_bytes(qtype, rows, k))
+    launch("repack_kquant", KquantRepackArgs(blocks.ptr, out.ptr, QTYPE[qtype], rows, k), stream)
+    return out
+
+
+def upload_weights(qtype, blocks_np, rows, k):
+    """Uploads raw ggml block bytes and repacks them on the GPU; returns the stream Buffer."""
+    raw = Buffer.of(np.ascontiguousarray(blocks_np, np.uint8))
+    try:
+        return repack(qtype, raw, rows, k)
+    finally:
+        raw.free()

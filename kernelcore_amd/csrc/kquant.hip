@@ -1,0 +1,445 @@
+// kquant.hip -- K-quant weight streams, activation quantizers and the decode matvecs (gfx950).
+//
+// Arithmetic follows the reference kernels operation by operation (arasheedu/Kernelcore
+// kernels/llm/quantize_q8x4.cu, quantize_cols.cu, quantize_cols_k.cu, matvec_q4k_q8.cu,
+// matvec_q6k_q8.cu; C++ mirror llm/llm_reference.cpp:79-104, 413-527). The library is built with
+// -ffp-contract=off so no multiply-add is fused: quantized bytes, scales and matvec outputs are
+// bit-identical to the reference. Only the work distribution is new:
+//   - quantizers: 8 lanes per block of 32 (per-32) or one wavefront per 256 (per-256), with the
+//     max and the sums reduced across lanes (both are order-independent: max and integer sums);
+//   - matvecs: one lane per (row, super-block), 16 rows x 4 super-blocks per wavefront, weights
+//     streamed from the slab layout of kquant.hpp with one coalesced dwordx4 load per slab.
+//     Each lane writes its super-block's float term (d*fd - dmin*fm, or the two Q6_K halves)
+//     to LDS; the row sums are then added in super-block order, the reference's order.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "internal.hpp"
+#include "kquant.hpp"
+#include "launch.hpp"
+
+namespace kcamd {
+namespace {
+
+constexpr uint32_t kLow4 = 0x0F0F0F0Fu;  // reference: 252645135
+constexpr int kXsStride = 68;            // LDS ints per super-block of activations (64 + 4 pad)
+
+__device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+__device__ __forceinline__ float f16bits(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (unsigned short)h); }
+__device__ __forceinline__ int sbyte(int w, int i) { return (w << (24 - 8 * i)) >> 24; }
+
+// ---------------------------------------------------------------- weight streams
+
+// One thread per 16-byte piece of the stream. Q6_K segments end with 8 pieces holding the
+// 64 fp16 d values.
+template <bool Q6>
+__global__ void repack_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int rows, int nsb,
+                              int ngroups, long long pieces, bool unpack) {
+    const long long p = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= pieces) return;
+    constexpr int kSlabs = Q6 ? kQ6kSlabs : kQ4kSlabs;
+    constexpr int kPer = kSlabs * 64 + (Q6 ? 8 : 0);
+    constexpr int kBlock = Q6 ? kQ6kBlock : kQ4kBlock;
+    constexpr int kSeg = Q6 ? kQ6kSeg : kQ4kSeg;
+    const long long seg = p / kPer;
+    const int q = (int)(p - seg * kPer);
+    const int tile = (int)(seg / ngroups);
+    const int g = (int)(seg - (long long)tile * ngroups);
+    uint8_t* out = dst + seg * kSeg;
+    if (q < kSlabs * 64) {
+        const int c = q >> 6, lane = q & 63;
+        const int row = tile * kTileRows + (lane & 15), s = g * kGroupSb + (lane >> 4);
+        uint8_t* piece = out + c * 1024 + lane * 16;
+        const bool real = row < rows && s < nsb;
+        const size_t boff = ((size_t)row * nsb + s) * kBlock + 16 * c;
+        if (!unpack) {
+            for (int i = 0; i < 16; ++i) piece[i] = real ? src[boff + i] : 0;
+        } else if (real) {
+            const uint8_t* in = src + seg * kSeg + c * 1024 + lane * 16;
+            for (int i = 0; i < 16; ++i) dst[boff + i] = in[i];
+        }
+        if (unpack) return;
+    } else {  // Q6_K d plane: 8 lanes per piece
+        const int j = q - kSlabs * 64;
+        for (int i = 0; i < 8; ++i) {
+            const int lane = j * 8 + i;
+            const int row = tile * kTileRows + (lane & 15), s = g * kGroupSb + (lane >> 4);
+            const bool real = row < rows && s < nsb;
+            const size_t boff = ((size_t)row * nsb + s) * kBlock + 208;
+            if (!unpack) {
+                uint8_t* d = out + kSlabs * 1024 + lane * 2;
+                d[0] = real ? src[boff] : 0;
+                d[1] = real ? src[boff + 1] : 0;
+            } else if (real) {
+                const uint8_t* in = src + seg * kSeg + kSlabs * 1024 + lane * 2;
+                dst[boff] = in[0];
+                dst[boff + 1] = in[1];
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------- activation quantizers
+
+// q = x * id rounded half away from zero, clamped to +-127 (quantize_q8x4.cu:22-33).
+__device__ __forceinline__ int q8round(float v, float id) {
+    const float t = v * id;
+    int q;
+    if (t >= 0.0f) q = (int)(t + 0.5f);
+    else q = (int)(t - 0.5f);
+    return q > 127 ? 127 : (q < -127 ? -127 : q);
+}
+__device__ __forceinline__ float absmax4(float4 v) {
+    float a = fmaxf(0.0f, fmaxf(v.x, 0.0f - v.x));
+    a = fmaxf(a, fmaxf(v.y, 0.0f - v.y));
+    a = fmaxf(a, fmaxf(v.z, 0.0f - v.z));
+    return fmaxf(a, fmaxf(v.w, 0.0f - v.w));
+}
+__device__ __forceinline__ int pack4(float4 v, float id, int* sum) {
+    const int a = q8round(v.x, id), b = q8round(v.y, id), c = q8round(v.z, id), d = q8round(v.w, id);
+    *sum = a + b + c + d;
+    return (a & 255) | ((b & 255) << 8) | ((c & 255) << 16) | ((d & 255) << 24);
+}
+
+// Per-32 blocks: 8 lanes per block, lane w packs word w. Column c of `ncols` (k values each)
+// writes its slot (xq at q + c * slot, xd after the nb * 8 words); count = nb * ncols.
+// With slot == 0 the blocks are contiguous (quantize_q8x4: xq, xd separate arrays).
+__device__ __forceinline__ float4 load4(const float* p, bool vec) {
+    if (vec) return *reinterpret_cast<const float4*>(p);
+    return make_float4(p[0], p[1], p[2], p[3]);
+}
+
+template <bool Vec>  // Vec: x is 16-byte aligned, one dwordx4 load per lane
+__global__ void quantize_q8_kernel(const float* __restrict__ x, int* __restrict__ xq, float* __restrict__ xd,
+                                   int count, int nb, int slot) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    const int b = t >> 3, w = t & 7;
+    const bool live = b < count;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (live) v = load4(x + ((size_t)b * 8 + w) * 4, Vec);
+    float amax = absmax4(v);
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
+    const float d = amax / 127.0f;
+    float id;
+    if (d > 0.0f) id = 1.0f / d;
+    else id = 0.0f;
+    int sum;
+    const int word = pack4(v, id, &sum);
+    sum += __shfl_xor(sum, 1, 8);
+    sum += __shfl_xor(sum, 2, 8);
+    sum += __shfl_xor(sum, 4, 8);
+    if (!live) return;
+    int* wq;
+    float* wd;
+    if (slot) {
+        const int c = b / nb, bl = b - c * nb;
+        int* base = xq + (size_t)c * slot;
+        wq = base + bl * 8;
+        wd = reinterpret_cast<float*>(base + nb * 8) + bl * 2;
+    } else {
+        wq = xq + (size_t)b * 8;
+        wd = xd + (size_t)b * 2;
+    }
+    wq[w] = word;
+    if (w == 0) {
+        wd[0] = d;
+        wd[1] = (float)sum;
+    }
+}
+
+// Per-256 slots (quantize_cols_k.cu:20-74): one wavefront per (column, super-block); lane L packs
+// word L (values 4L..4L+3), sums of 16 come from lanes 4g..4g+3, sums of 32 from lanes 8i..8i+7.
+template <bool Vec>
+__global__ void quantize_k_kernel(const float* __restrict__ x, int* __restrict__ q, int nsb, int count) {
+    const int wid = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int lane = threadIdx.x & 63;
+    if (wid >= count) return;  // whole wavefronts
+    const int c = wid / nsb, s = wid - c * nsb;
+    const float4 v = load4(x + (size_t)c * nsb * 256 + (size_t)s * 256 + lane * 4, Vec);
+    float amax = absmax4(v);
+    for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    const float d = amax / 127.0f;
+    float id;
+    if (d > 0.0f) id = 1.0f / d;
+    else id = 0.0f;
+    int s4;
+    const int word = pack4(v, id, &s4);
+    int s16 = s4 + __shfl_xor(s4, 1);
+    s16 += __shfl_xor(s16, 2);
+    int s32 = s16 + __shfl_xor(s16, 4);
+    int* qc = q + (size_t)c * nsb * 85;
+    qc[s * 64 + lane] = word;
+    if ((lane & 3) == 0) qc[nsb * 65 + s * 16 + (lane >> 2)] = s16;
+    // Lane 0 gathers B_i (lanes 8i): words [B>>6 of sums 0-3 | of 4-7 | B&63 of 0-3 | of 4-7].
+    int pw[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int b = __shfl(s32, 8 * i);
+        const int sh = 8 * (i & 3);
+        pw[i >> 2] |= ((b >> 6) & 255) << sh;
+        pw[2 + (i >> 2)] |= (b & 63) << sh;
+    }
+    if (lane == 0) {
+        for (int i = 0; i < 4; ++i) qc[nsb * 81 + s * 4 + i] = pw[i];
+        reinterpret_cast<float*>(qc + nsb * 64)[s] = d;
+    }
+}
+
+// ---------------------------------------------------------------- decode matvecs
+
+// LDS layout (ints), nsbp = padded super-blocks:
+//   xs   [nsbp][68]  q8 words of each super-block (64 + pad: 4 lanes groups read 4 different
+//                    super-blocks per ds_read_b128 without bank conflicts)
+//   dx   [nsbp * 8]  block scales d
+//   aux  [nsbp * 8]  Q4_K: d * sum (the reference's xd[2b] * xd[2b+1]); Q6_K: (int) sum of 32
+//   s16  [nsbp * 8]  Q6_K: sum of the first 16 values of each block
+//   terms[WT][nt][16] per-super-block float terms, nt = nsbp (Q4_K) or 2 * nsbp (Q6_K)
+__device__ __forceinline__ float q4k_term(const uint32_t* c, const int* xs, const float* dx, const float* dxs) {
+    const uint32_t h = c[0];
+    const float d = f16bits(h & 0xFFFFu), dmin = f16bits(h >> 16);
+    const int s0 = (int)c[1], s1 = (int)c[2], s2 = (int)c[3];
+    const int sclo = s0 & 0x3F3F3F3F;
+    const int mlo = s1 & 0x3F3F3F3F;
+    const int schi = (s2 & 0x0F0F0F0F) | ((s0 >> 2) & 0x30303030);
+    const int mhi = ((s2 >> 4) & 0x0F0F0F0F) | ((s1 >> 2) & 0x30303030);
+    float fd = 0.0f, fm = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int4* xa = reinterpret_cast<const int4*>(xs + 16 * j);
+        const int4 a0 = xa[0], a1 = xa[1], b0 = xa[2], b1 = xa[3];
+        const int xaw[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        const int xbw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+        int da = 0, db = 0;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+            const uint32_t q = c[4 + 8 * j + w];
+            da = dot4((int)(q & kLow4), xaw[w], da);
+            db = dot4((int)((q >> 4) & kLow4), xbw[w], db);
+        }
+        const int sh = 16 * (j & 1);
+        const int scw = j < 2 ? sclo : schi;
+        const int mw = j < 2 ? mlo : mhi;
+        const int sca = (scw >> sh) & 255, scb = (scw >> (sh + 8)) & 255;
+        const int ma = (mw >> sh) & 255, mb = (mw >> (sh + 8)) & 255;
+        fd += (float)(sca * da) * dx[2 * j] + (float)(scb * db) * dx[2 * j + 1];
+        fm += (float)ma * dxs[2 * j] + (float)mb * dxs[2 * j + 1];
+    }
+    return d * fd - dmin * fm;
+}
+
+// The two halves of a Q6_K super-block (matvec_q6k_q8.cu:33-105): out[n] = d * (sum_t is_t * dx_t).
+__device__ __forceinline__ void q6k_terms(const uint32_t* c, uint32_t dbits, const int* xs, const float* dx,
+                                          const int* sum32, const int* s16, float* out0, float* out1) {
+    const float d = f16bits(dbits);
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+        int da[4] = {0, 0, 0, 0}, db[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int4* xr = reinterpret_cast<const int4*>(xs + (4 * n + t) * 8);
+            const int4 x0 = xr[0], x1 = xr[1];
+            const int xw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int w = 0; w < 8; ++w) {
+                const int qa = (int)c[16 * n + w];
+                const int qc = (int)c[16 * n + 8 + w];
+                const int h = (int)c[32 + 8 * n + w];
+                int q;
+                if (t == 0) q = (qa & 0x0F0F0F0F) | ((h << 4) & 0x30303030);
+                else if (t == 1) q = (qc & 0x0F0F0F0F) | ((h << 2) & 0x30303030);
+                else if (t == 2) q = ((qa >> 4) & 0x0F0F0F0F) | (h & 0x30303030);
+                else q = ((qc >> 4) & 0x0F0F0F0F) | ((h >> 2) & 0x30303030);
+                if (w < 4) da[t] = dot4(q, xw[w], da[t]);
+                else db[t] = dot4(q, xw[w], db[t]);
+            }
+        }
+        const int sw0 = (int)c[48 + 2 * n], sw1 = (int)c[48 + 2 * n + 1];
+        int is[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int sw = t < 2 ? sw0 : sw1;
+            const int lo = 2 * (t & 1);
+            const int sa = s16[4 * n + t];
+            const int sb = sum32[4 * n + t] - sa;
+            is[t] = sbyte(sw, lo) * (da[t] - 32 * sa) + sbyte(sw, lo + 1) * (db[t] - 32 * sb);
+        }
+        const float v = d * ((float)is[0] * dx[4 * n] + (float)is[1] * dx[4 * n + 1] + (float)is[2] * dx[4 * n + 2] +
+                             (float)is[3] * dx[4 * n + 3]);
+        if (n == 0) *out0 = v;
+        else *out1 = v;
+    }
+}
+
+template <bool Q6, int WT>
+__global__ __launch_bounds__(256) void matvec_kq_kernel(const uint8_t* __restrict__ qw, const int* __restrict__ xq,
+                                                        const float* __restrict__ xd, float* __restrict__ y, int rows,
+                                                        int nsb, int ntiles) {
+    constexpr int WK = 4 / WT;  // waves of one tile splitting its super-block groups
+    constexpr int kSlabs = Q6 ? kQ6kSlabs : kQ4kSlabs;
+    constexpr int kSeg = Q6 ? kQ6kSeg : kQ4kSeg;
+    extern __shared__ int4 lds4[];
+    int* lds = reinterpret_cast<int*>(lds4);
+    const int ngroups = (nsb + kGroupSb - 1) / kGroupSb;
+    const int nsbp = ngroups * kGroupSb;
+    const int nt = Q6 ? 2 * nsbp : nsbp;
+    int* xs = lds;
+    float* dx = reinterpret_cast<float*>(xs + nsbp * kXsStride);
+    float* aux = dx + nsbp * 8;
+    int* s16 = reinterpret_cast<int*>(aux + nsbp * 8);
+    float* terms = reinterpret_cast<float*>(s16 + nsbp * 8);
+
+    const int tid = threadIdx.x;
+    for (int i = tid; i < nsbp * 64; i += 256) {  // 4-byte loads: xq needs no 16-byte alignment
+        const int s = i >> 6, w = i & 63;
+        xs[s * kXsStride + w] = s < nsb ? xq[i] : 0;
+    }
+    for (int b = tid; b < nsbp * 8; b += 256) {
+        float d = 0.0f, sm = 0.0f;
+        if (b < nsb * 8) {
+            d = xd[2 * b];
+            sm = xd[2 * b + 1];
+        }
+        dx[b] = d;
+        if (Q6) {
+            reinterpret_cast<int*>(aux)[b] = (int)sm;
+            int a = 0;
+            if (b < nsb * 8)
+                for (int w = 0; w < 4; ++w) a = dot4(0x01010101, xq[b * 8 + w], a);
+            s16[b] = a;
+        } else {
+            aux[b] = d * sm;
+        }
+    }
+    __syncthreads();
+
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wt = wave % WT, wk = wave / WT;
+    const int tile = blockIdx.x * WT + wt;
+    const int kq = lane >> 4, r = lane & 15;
+    float* tterms = terms + wt * nt * 16;
+    if (tile < ntiles) {
+        const uint8_t* seg0 = qw + (size_t)tile * ngroups * kSeg;
+        for (int g = wk; g < ngroups; g += WK) {
+            const uint8_t* seg = seg0 + (size_t)g * kSeg;
+            uint4 cv[kSlabs];
+#pragma unroll
+            for (int i = 0; i < kSlabs; ++i) cv[i] = *reinterpret_cast<const uint4*>(seg + i * 1024 + lane * 16);
+            const uint32_t* c = reinterpret_cast<const uint32_t*>(cv);
+            const int s = g * kGroupSb + kq;
+            if (Q6) {
+                const uint32_t dbits = *reinterpret_cast<const uint16_t*>(seg + kSlabs * 1024 + lane * 2);
+                float t0, t1;
+                q6k_terms(c, dbits, xs + s * kXsStride, dx + 8 * s, reinterpret_cast<const int*>(aux) + 8 * s,
+                          s16 + 8 * s, &t0, &t1);
+                tterms[(2 * s) * 16 + r] = t0;
+                tterms[(2 * s + 1) * 16 + r] = t1;
+            } else {
+                tterms[s * 16 + r] = q4k_term(c, xs + s * kXsStride, dx + 8 * s, aux + 8 * s);
+            }
+        }
+    }
+    __syncthreads();
+    if (tile < ntiles && wk == 0 && kq == 0) {
+        const int row = tile * kTileRows + r;
+        const int nreal = Q6 ? 2 * nsb : nsb;
+        float acc = 0.0f;
+        for (int t = 0; t < nreal; ++t) acc += tterms[t * 16 + r];
+        if (row < rows) y[row] = acc;
+    }
+}
+
+constexpr size_t kMatvecMaxLds = 65536;
+
+size_t matvecLds(bool q6, int nsb, int wt) {
+    const int nsbp = groupsOf(nsb) * kGroupSb;
+    const int nt = q6 ? 2 * nsbp : nsbp;
+    return sizeof(int) * (size_t(nsbp) * (kXsStride + 24) + size_t(wt) * nt * 16);
+}
+
+template <bool Q6, int WT>
+int runMatvec(const kcMatvecQ4Q8Args& a, hipStream_t s) {
+    const int nsb = a.k / 256;
+    const int ntiles = tilesOf(a.rows);
+    const size_t lds = matvecLds(Q6, nsb, WT);
+    const int blocks = (ntiles + WT - 1) / WT;
+    hipLaunchKernelGGL((matvec_kq_kernel<Q6, WT>), dim3(blocks), dim3(256), lds, s,
+                       reinterpret_cast<const uint8_t*>(a.qw), a.xq, a.xd, a.y, a.rows, nsb, ntiles);
+    return fromHip(hipGetLastError(), Q6 ? "matvec_q6k_q8" : "matvec_q4k_q8");
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- launchers
+
+int launchRepack(const kcKquantRepackArgs& a, bool unpack, hipStream_t s) {
+    const bool q6 = a.qtype == KC_QTYPE_Q6_K;
+    const int nsb = a.k / 256;
+    const int ngroups = groupsOf(nsb);
+    const long long segs = (long long)tilesOf(a.rows) * ngroups;
+    const long long pieces = segs * (q6 ? kQ6kSlabs * 64 + 8 : kQ4kSlabs * 64);
+    const unsigned blocks = (unsigned)((pieces + 255) / 256);
+    if (pieces == 0) return 0;
+    const uint8_t* src = static_cast<const uint8_t*>(a.src);
+    uint8_t* dst = static_cast<uint8_t*>(a.dst);
+    if (q6)
+        hipLaunchKernelGGL(repack_kernel<true>, dim3(blocks), dim3(256), 0, s, src, dst, a.rows, nsb, ngroups, pieces,
+                           unpack);
+    else
+        hipLaunchKernelGGL(repack_kernel<false>, dim3(blocks), dim3(256), 0, s, src, dst, a.rows, nsb, ngroups, pieces,
+                           unpack);
+    return fromHip(hipGetLastError(), unpack ? "unpack_kquant" : "repack_kquant");
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+static void quantizeQ8(const float* x, int* xq, float* xd, int count, int nb, int slot, hipStream_t s) {
+    const long long threads = (long long)count * 8;
+    const dim3 grid((unsigned)((threads + 255) / 256));
+    if (aligned16(x)) hipLaunchKernelGGL(quantize_q8_kernel<true>, grid, dim3(256), 0, s, x, xq, xd, count, nb, slot);
+    else hipLaunchKernelGGL(quantize_q8_kernel<false>, grid, dim3(256), 0, s, x, xq, xd, count, nb, slot);
+}
+
+int launchQuantizeQ8x4(const float* x, int* xq, float* xd, int count, hipStream_t s) {
+    if (count == 0) return 0;
+    quantizeQ8(x, xq, xd, count, 0, 0, s);
+    return fromHip(hipGetLastError(), "quantize_q8x4");
+}
+
+int launchQuantizeCols(const float* x, int* q, int k, int ncols, hipStream_t s) {
+    const int nb = k / 32;
+    quantizeQ8(x, q, nullptr, nb * ncols, nb, nb * 11, s);
+    return fromHip(hipGetLastError(), "quantize_cols");
+}
+
+int launchQuantizeColsK(const float* x, int* q, int k, int ncols, hipStream_t s) {
+    const int nsb = k / 256;
+    const long long waves = (long long)nsb * ncols;
+    const dim3 grid((unsigned)((waves + 3) / 4));
+    if (aligned16(x)) hipLaunchKernelGGL(quantize_k_kernel<true>, grid, dim3(256), 0, s, x, q, nsb, (int)waves);
+    else hipLaunchKernelGGL(quantize_k_kernel<false>, grid, dim3(256), 0, s, x, q, nsb, (int)waves);
+    return fromHip(hipGetLastError(), "quantize_cols_k");
+}
+
+int launchMatvecKq(bool q6k, const kcMatvecQ4Q8Args& a, hipStream_t s) {
+    if (a.rows == 0) return 0;
+    // Tiles per workgroup: 4 when there are enough tiles to fill the GPU, else fewer, with the
+    // remaining waves splitting the super-block groups of one tile.
+    const int ntiles = tilesOf(a.rows);
+    int wt = option("matvec_waves");  // forced tiles per workgroup (1, 2 or 4)
+    if (wt != 1 && wt != 2 && wt != 4) wt = ntiles >= 2048 ? 4 : (ntiles >= 1024 ? 2 : 1);
+    while (wt > 1 && matvecLds(q6k, a.k / 256, wt) > kMatvecMaxLds) wt /= 2;
+    if (q6k) {
+        if (wt == 4) return runMatvec<true, 4>(a, s);
+        if (wt == 2) return runMatvec<true, 2>(a, s);
+        return runMatvec<true, 1>(a, s);
+    }
+    if (wt == 4) return runMatvec<false, 4>(a, s);
+    if (wt == 2) return runMatvec<false, 2>(a, s);
+    return runMatvec<false, 1>(a, s);
+}
+
+}  // namespace kcamd

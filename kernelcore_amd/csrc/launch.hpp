@@ -1,0 +1,20 @@
+// launch.hpp -- host-side launchers of the HIP kernels, called by the built-in kernel table
+// (llm_kernels.cpp) after argument validation. Each returns a kc error code (0 = success) and
+// only enqueues work on `s`.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <kernelcore/llm_kernels.h>
+
+namespace kcamd {
+
+// kquant.hip
+int launchRepack(const kcKquantRepackArgs& a, bool unpack, hipStream_t s);
+int launchQuantizeQ8x4(const float* x, int* xq, float* xd, int count, hipStream_t s);
+int launchQuantizeCols(const float* x, int* q, int k, int ncols, hipStream_t s);
+int launchQuantizeColsK(const float* x, int* q, int k, int ncols, hipStream_t s);
+int launchMatvecKq(bool q6k, const kcMatvecQ4Q8Args& a, hipStream_t s);
+// Largest k the matvec's activation staging accepts.
+constexpr int kMatvecMaxK = 32768;
+
+}  // namespace kcamd
