@@ -273,12 +273,30 @@ __device__ __forceinline__ void q6k_terms(const uint32_t* c, uint32_t dbits, con
     }
 }
 
-template <bool Q6, int WT>
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// The slabs of one (tile, group) segment held by a lane: its 16-byte piece of every slab (and the
+// Q6_K d). NT: non-temporal loads (the weights are read once per matvec).
+template <bool Q6, bool NT>
+struct Pieces {
+    static constexpr int kSlabs = Q6 ? kQ6kSlabs : kQ4kSlabs;
+    u32x4 c[kSlabs];
+    uint32_t dbits;
+    __device__ __forceinline__ void load(const uint8_t* seg, int lane) {
+#pragma unroll
+        for (int i = 0; i < kSlabs; ++i) {
+            const u32x4* p = reinterpret_cast<const u32x4*>(seg + i * 1024 + lane * 16);
+            c[i] = NT ? __builtin_nontemporal_load(p) : *p;
+        }
+        if (Q6) dbits = *reinterpret_cast<const uint16_t*>(seg + kSlabs * 1024 + lane * 2);
+    }
+};
+
+template <bool Q6, int WT, bool PIPE, bool NT>
 __global__ __launch_bounds__(256) void matvec_kq_kernel(const uint8_t* __restrict__ qw, const int* __restrict__ xq,
                                                         const float* __restrict__ xd, float* __restrict__ y, int rows,
                                                         int nsb, int ntiles) {
     constexpr int WK = 4 / WT;  // waves of one tile splitting its super-block groups
-    constexpr int kSlabs = Q6 ? kQ6kSlabs : kQ4kSlabs;
     constexpr int kSeg = Q6 ? kQ6kSeg : kQ4kSeg;
     extern __shared__ int4 lds4[];
     int* lds = reinterpret_cast<int*>(lds4);
@@ -292,6 +310,19 @@ __global__ __launch_bounds__(256) void matvec_kq_kernel(const uint8_t* __restric
     float* terms = reinterpret_cast<float*>(s16 + nsbp * 8);
 
     const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wt = wave % WT, wk = wave / WT;
+    const int tile = blockIdx.x * WT + wt;
+    const int kq = lane >> 4, r = lane & 15;
+    const bool live = tile < ntiles;
+    const uint8_t* seg0 = qw + (size_t)(live ? tile : 0) * ngroups * kSeg;
+
+    // The first segment's loads go out before the activations are staged, so both latencies overlap.
+    Pieces<Q6, NT> cur;
+    int g = wk;
+    if (live && g < ngroups) cur.load(seg0 + (size_t)g * kSeg, lane);
+
     for (int i = tid; i < nsbp * 64; i += 256) {  // 4-byte loads: xq needs no 16-byte alignment
         const int s = i >> 6, w = i & 63;
         xs[s * kXsStride + w] = s < nsb ? xq[i] : 0;
@@ -315,35 +346,30 @@ __global__ __launch_bounds__(256) void matvec_kq_kernel(const uint8_t* __restric
     }
     __syncthreads();
 
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wt = wave % WT, wk = wave / WT;
-    const int tile = blockIdx.x * WT + wt;
-    const int kq = lane >> 4, r = lane & 15;
     float* tterms = terms + wt * nt * 16;
-    if (tile < ntiles) {
-        const uint8_t* seg0 = qw + (size_t)tile * ngroups * kSeg;
-        for (int g = wk; g < ngroups; g += WK) {
-            const uint8_t* seg = seg0 + (size_t)g * kSeg;
-            uint4 cv[kSlabs];
-#pragma unroll
-            for (int i = 0; i < kSlabs; ++i) cv[i] = *reinterpret_cast<const uint4*>(seg + i * 1024 + lane * 16);
-            const uint32_t* c = reinterpret_cast<const uint32_t*>(cv);
+    if (live) {
+        while (g < ngroups) {
+            const int gn = g + WK;
+            Pieces<Q6, NT> nxt;
+            if (PIPE && gn < ngroups) nxt.load(seg0 + (size_t)gn * kSeg, lane);
+            const uint32_t* c = reinterpret_cast<const uint32_t*>(cur.c);
             const int s = g * kGroupSb + kq;
             if (Q6) {
-                const uint32_t dbits = *reinterpret_cast<const uint16_t*>(seg + kSlabs * 1024 + lane * 2);
                 float t0, t1;
-                q6k_terms(c, dbits, xs + s * kXsStride, dx + 8 * s, reinterpret_cast<const int*>(aux) + 8 * s,
+                q6k_terms(c, cur.dbits, xs + s * kXsStride, dx + 8 * s, reinterpret_cast<const int*>(aux) + 8 * s,
                           s16 + 8 * s, &t0, &t1);
                 tterms[(2 * s) * 16 + r] = t0;
                 tterms[(2 * s + 1) * 16 + r] = t1;
             } else {
                 tterms[s * 16 + r] = q4k_term(c, xs + s * kXsStride, dx + 8 * s, aux + 8 * s);
             }
+            if (PIPE) cur = nxt;
+            else if (gn < ngroups) cur.load(seg0 + (size_t)gn * kSeg, lane);
+            g = gn;
         }
     }
     __syncthreads();
-    if (tile < ntiles && wk == 0 && kq == 0) {
+    if (live && wk == 0 && kq == 0) {
         const int row = tile * kTileRows + r;
         const int nreal = Q6 ? 2 * nsb : nsb;
         float acc = 0.0f;
@@ -360,15 +386,28 @@ size_t matvecLds(bool q6, int nsb, int wt) {
     return sizeof(int) * (size_t(nsbp) * (kXsStride + 24) + size_t(wt) * nt * 16);
 }
 
-template <bool Q6, int WT>
+template <bool Q6, int WT, bool PIPE, bool NT>
 int runMatvec(const kcMatvecQ4Q8Args& a, hipStream_t s) {
     const int nsb = a.k / 256;
     const int ntiles = tilesOf(a.rows);
     const size_t lds = matvecLds(Q6, nsb, WT);
     const int blocks = (ntiles + WT - 1) / WT;
-    hipLaunchKernelGGL((matvec_kq_kernel<Q6, WT>), dim3(blocks), dim3(256), lds, s,
+    hipLaunchKernelGGL((matvec_kq_kernel<Q6, WT, PIPE, NT>), dim3(blocks), dim3(256), lds, s,
                        reinterpret_cast<const uint8_t*>(a.qw), a.xq, a.xd, a.y, a.rows, nsb, ntiles);
     return fromHip(hipGetLastError(), Q6 ? "matvec_q6k_q8" : "matvec_q4k_q8");
+}
+
+template <bool Q6, int WT>
+int pickVariant(const kcMatvecQ4Q8Args& a, bool pipe, bool nt, hipStream_t s) {
+    if (pipe) return nt ? runMatvec<Q6, WT, true, true>(a, s) : runMatvec<Q6, WT, true, false>(a, s);
+    return nt ? runMatvec<Q6, WT, false, true>(a, s) : runMatvec<Q6, WT, false, false>(a, s);
+}
+
+template <bool Q6>
+int pickShape(const kcMatvecQ4Q8Args& a, int wt, bool pipe, bool nt, hipStream_t s) {
+    if (wt == 4) return pickVariant<Q6, 4>(a, pipe, nt, s);
+    if (wt == 2) return pickVariant<Q6, 2>(a, pipe, nt, s);
+    return pickVariant<Q6, 1>(a, pipe, nt, s);
 }
 
 }  // namespace
@@ -426,20 +465,19 @@ int launchQuantizeColsK(const float* x, int* q, int k, int ncols, hipStream_t s)
 
 int launchMatvecKq(bool q6k, const kcMatvecQ4Q8Args& a, hipStream_t s) {
     if (a.rows == 0) return 0;
-    // Tiles per workgroup: 4 when there are enough tiles to fill the GPU, else fewer, with the
-    // remaining waves splitting the super-block groups of one tile.
+    // Tiles per workgroup: 4 when there are enough tiles to fill the GPU several times over,
+    // else fewer, with the remaining waves splitting the super-block groups of one tile
+    // (measured on MI355X: 128256 rows best at 4, 1024-16384 rows best at 1).
     const int ntiles = tilesOf(a.rows);
     int wt = option("matvec_waves");  // forced tiles per workgroup (1, 2 or 4)
-    if (wt != 1 && wt != 2 && wt != 4) wt = ntiles >= 2048 ? 4 : (ntiles >= 1024 ? 2 : 1);
+    if (wt != 1 && wt != 2 && wt != 4) wt = ntiles >= 4096 ? 4 : (ntiles >= 2048 ? 2 : 1);
     while (wt > 1 && matvecLds(q6k, a.k / 256, wt) > kMatvecMaxLds) wt /= 2;
-    if (q6k) {
-        if (wt == 4) return runMatvec<true, 4>(a, s);
-        if (wt == 2) return runMatvec<true, 2>(a, s);
-        return runMatvec<true, 1>(a, s);
-    }
-    if (wt == 4) return runMatvec<false, 4>(a, s);
-    if (wt == 2) return runMatvec<false, 2>(a, s);
-    return runMatvec<false, 1>(a, s);
+    // 0 = default, 1 = off, 2 = on. Defaults: non-temporal weight loads (about 10% faster at
+    // config 2), no software pipelining (it costs occupancy and measured slower).
+    const int po = option("matvec_pipe"), no = option("matvec_nt");
+    const bool pipe = po == 2;
+    const bool nt = no != 1;
+    return q6k ? pickShape<true>(a, wt, pipe, nt, s) : pickShape<false>(a, wt, pipe, nt, s);
 }
 
 }  // namespace kcamd

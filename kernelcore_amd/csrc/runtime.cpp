@@ -540,7 +540,7 @@ kcError_t kcGetDeviceProperties(kcDeviceProperties* props, int device) noexcept 
         hipDeviceProp_t hp{};
         if (int e = kcamd::fromHip(hipGetDeviceProperties(&hp, r.device), "hipGetDeviceProperties")) return err(e);
         kcDeviceProperties p{};
-        std::snprintf(p.name, sizeof p.name, "%s (%s)", hp.name, hp.gcnArchName);
+        std::snprintf(p.name, sizeof p.name, "%s (%s)", hp.name[0] ? hp.name : "AMD GPU", hp.gcnArchName);
         p.worker_count = static_cast<unsigned>(hp.multiProcessorCount);
         p.performance_workers = p.worker_count;
         p.total_memory = hp.totalGlobalMem;
@@ -1185,7 +1185,7 @@ const char* kcCodegenName(kcCodegen_t codegen) noexcept {
 
 kcError_t kcSetKernelOption(const char* option, int value) noexcept {
     return api("kcSetKernelOption", [&] {
-        static const char* known[] = {"matvec_waves", "matmul_tile_n"};
+        static const char* known[] = {"matvec_waves", "matvec_pipe", "matvec_nt", "matmul_tile_n"};
         if (!option) return kc::Error::InvalidValue;
         bool found = false;
         for (const char* k : known) found |= std::strcmp(k, option) == 0;
