@@ -14,6 +14,10 @@ int launchQuantizeQ8x4(const float* x, int* xq, float* xd, int count, hipStream_
 int launchQuantizeCols(const float* x, int* q, int k, int ncols, hipStream_t s);
 int launchQuantizeColsK(const float* x, int* q, int k, int ncols, hipStream_t s);
 int launchMatvecKq(bool q6k, const kcMatvecQ4Q8Args& a, hipStream_t s);
+// kmatmul.hip: column-tiled matmul (any ncols; bit-identical per column to the reference).
+int launchMatmulCols(bool q6k, bool per256, const kcMatmulKQ8Args& a, hipStream_t s);
+// The matmul names: column tiles for small batches and per-32 slots, MFMA for large per-256 batches.
+int launchMatmulKq(bool q6k, bool per256, const kcMatmulKQ8Args& a, hipStream_t s);
 // Largest k the matvec's activation staging accepts.
 constexpr int kMatvecMaxK = 32768;
 

@@ -102,6 +102,29 @@ int kquantLaunch(const void* p, void* s) {
     return kcamd::launchMatvecKq(Q6, *static_cast<const kcMatvecQ4Q8Args*>(p), hs(s));
 }
 
+// ---- matmul_{q4k,q6k}_q8{,k}x{4,8} (llm_kernels.cpp:290-312: matmulKMarshal)
+
+template <bool Q6, bool K8>
+int matmulValidate(const void* p, const kcLaunchContext*) {
+    const auto& a = *static_cast<const kcMatmulKQ8Args*>(p);
+    if (a.rows <= 0 || a.rows % 8 != 0 || a.k <= 0 || a.k % 256 != 0 || a.ncols <= 0 || a.row_block <= 0 ||
+        !fitsIndex(a.rows, a.k))
+        return invalid("rows must be a positive multiple of 8, k a positive multiple of 256, ncols and row_block > 0");
+    const int64_t slot = K8 ? int64_t(a.k / 256) * 85 : int64_t(a.k / 32) * 11;
+    if (!fitsIndex(slot, a.ncols) || !fitsIndex(a.rows, a.ncols) || a.ncols > 65535 * 8)
+        return invalid("ncols out of range");
+    if (reinterpret_cast<uintptr_t>(a.qw) % 16) return invalid("qw (a weight stream) must be 16-byte aligned");
+    KC_TRY(checkRange(a.qw, kcamd::streamBytes(Q6, a.rows, a.k), "qw"));
+    KC_TRY(checkRange(a.xq, i32Bytes(slot * a.ncols), "xq"));
+    KC_TRY(checkRange(a.y, f32Bytes(int64_t(a.rows) * a.ncols), "y"));
+    const int want[4] = {a.rows, a.k, a.ncols, a.row_block};
+    return checkDims(a.dims, want, 4);
+}
+template <bool Q6, bool K8>
+int matmulLaunch(const void* p, void* s) {
+    return kcamd::launchMatmulKq(Q6, K8, *static_cast<const kcMatmulKQ8Args*>(p), hs(s));
+}
+
 // ---- quantize_cols / quantize_cols_k (llm_kernels.cpp:331-345: quantColsMarshal)
 
 template <int kBlock>
@@ -149,6 +172,14 @@ const kcKernelEntry kTable[] = {
     {"quantize_cols_k", quantColsValidate<256>, quantColsLaunch<256>, 1},
     {"matvec_q4k_q8", kquantValidate<false>, kquantLaunch<false>, 1},
     {"matvec_q6k_q8", kquantValidate<true>, kquantLaunch<true>, 1},
+    {"matmul_q4k_q8x4", matmulValidate<false, false>, matmulLaunch<false, false>, 1},
+    {"matmul_q4k_q8x8", matmulValidate<false, false>, matmulLaunch<false, false>, 1},
+    {"matmul_q6k_q8x4", matmulValidate<true, false>, matmulLaunch<true, false>, 1},
+    {"matmul_q6k_q8x8", matmulValidate<true, false>, matmulLaunch<true, false>, 1},
+    {"matmul_q4k_q8kx4", matmulValidate<false, true>, matmulLaunch<false, true>, 1},
+    {"matmul_q4k_q8kx8", matmulValidate<false, true>, matmulLaunch<false, true>, 1},
+    {"matmul_q6k_q8kx4", matmulValidate<true, true>, matmulLaunch<true, true>, 1},
+    {"matmul_q6k_q8kx8", matmulValidate<true, true>, matmulLaunch<true, true>, 1},
     {"repack_kquant", repackValidate<false>, repackLaunch<false>, 0},
     {"unpack_kquant", repackValidate<true>, repackLaunch<true>, 0},
 };
