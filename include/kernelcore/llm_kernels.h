@@ -62,8 +62,9 @@ typedef struct kcMatvecQ4Q8Args {
 
 /* matmul_{q4k,q6k}_q8x{4,8} (per-32 slots) and matmul_{q4k,q6k}_q8kx{4,8} (per-256 slots),
  * llm_kernels.hpp:262-271: Y = W X, column c from slot xq + c * slot_ints, written to y + c * rows.
- * On the GPU all four tile names run the same MFMA kernel per activation format; row_block is
- * validated (> 0) and otherwise unused. */
+ * On the GPU the x4 / x8 names are the same kernels (a column-tiled kernel, bit-exact per column,
+ * and for Q4_K with per-256 slots and >= 32 columns the MFMA kernel); row_block is validated
+ * (> 0) and otherwise unused. */
 typedef struct kcMatmulKQ8Args {
     const int* qw;
     const int* xq;
@@ -223,13 +224,27 @@ typedef struct kcFaValuesArgs {
     kcFaDims d;
 } kcFaValuesArgs;
 
+/* flash_attn_f16 (no reference counterpart beyond the four fa_* kernels it fuses): the same
+ * FLASH_ATTN_EXT result, out[N][H][D], in one kernel; d.T <= 16384. */
+typedef struct kcFlashAttnArgs {
+    const float* q;
+    const int* k;
+    const int* v;
+    const int* mask;
+    float* out;
+    const int* dims;
+    kcFaDims d;
+    float scale;
+} kcFlashAttnArgs;
+
 /* ---- K-quant weight streams (this device's layout; no reference counterpart beyond
  * llm::ref::repackQ4K/Q6K and the ggml backend's unpack_stream, ggml-kernelcore.cpp:124-154) ----
- * Rows are grouped in tiles of 64 (the last tile padded with zero blocks). For tile t and
- * super-block s the 64 rows' blocks are stored as consecutive 1 KiB slabs: slab c holds bytes
- * [16c, 16c + 16) of every row's ggml block, row after row, so one 16-byte load per lane reads a
- * whole slab. Q4_K: 9 slabs (144 B). Q6_K: 13 slabs (bytes 0..207) then the 64 fp16 `d` (128 B).
- * The stream holds exactly the ggml bytes plus the padding rows. */
+ * Rows are grouped in tiles of 16 and super-blocks in groups of 4 (padding rows and super-blocks
+ * are zero blocks). For tile t and group g the 64 (super-block, row) pairs are the 64 lanes of a
+ * wavefront (lane = kq * 16 + r), and their ggml blocks are stored as 1 KiB slabs: slab c holds
+ * bytes [16c, 16c + 16) of the 64 blocks in lane order, so one 16-byte load per lane reads a
+ * whole slab. Q4_K: 9 slabs (144 B per block). Q6_K: 13 slabs (bytes 0..207) then the 64 fp16
+ * `d` values (128 B). The stream must be 16-byte aligned. */
 #define KC_QTYPE_Q4_K 12 /* ggml type ids */
 #define KC_QTYPE_Q6_K 14
 typedef struct kcKquantRepackArgs {
@@ -266,6 +281,7 @@ typedef ::kcFaMaxArgs FaMaxArgs;
 typedef ::kcFaExpArgs FaExpArgs;
 typedef ::kcFaValuesArgs FaValuesArgs;
 typedef ::kcKquantRepackArgs KquantRepackArgs;
+typedef ::kcFlashAttnArgs FlashAttnArgs;
 inline int scratchInts(int nb) { return nb * 11; }
 inline float* scratchScales(int* q, int nb) { return reinterpret_cast<float*>(q + nb * 8); }
 inline int scratchKInts(int nsb) { return nsb * 85; }

@@ -76,6 +76,8 @@ FaScoresArgs = _struct("FaScoresArgs", [("q", _p), ("k", _p), ("mask", _p), ("s"
 FaMaxArgs = _struct("FaMaxArgs", [("s", _p), ("m", _p), ("dims", _p), ("d", FaDims)])
 FaExpArgs = _struct("FaExpArgs", [("s", _p), ("m", _p), ("dims", _p), ("d", FaDims)])
 FaValuesArgs = _struct("FaValuesArgs", [("p", _p), ("v", _p), ("out", _p), ("dims", _p), ("d", FaDims)])
+FlashAttnArgs = _struct("FlashAttnArgs", [("q", _p), ("k", _p), ("v", _p), ("mask", _p), ("out", _p), ("dims", _p),
+                                          ("d", FaDims), ("scale", _f)])
 KquantRepackArgs = _struct("KquantRepackArgs", [("src", _p), ("dst", _p), ("qtype", _i), ("rows", _i), ("k", _i)])
 DeviceProperties = _struct("DeviceProperties", [("name", C.c_char * 128), ("worker_count", C.c_uint),
                                                 ("performance_workers", C.c_uint), ("total_memory", C.c_size_t),

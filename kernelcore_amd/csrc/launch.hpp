@@ -16,8 +16,26 @@ int launchQuantizeColsK(const float* x, int* q, int k, int ncols, hipStream_t s)
 int launchMatvecKq(bool q6k, const kcMatvecQ4Q8Args& a, hipStream_t s);
 // kmatmul.hip: column-tiled matmul (any ncols; bit-identical per column to the reference).
 int launchMatmulCols(bool q6k, bool per256, const kcMatmulKQ8Args& a, hipStream_t s);
+// kmatmul_mfma.hip: Q4_K x per-256 activations on MFMA (large batches).
+int launchMatmulQ4kMfma(const kcMatmulKQ8Args& a, hipStream_t s);
 // The matmul names: column tiles for small batches and per-32 slots, MFMA for large per-256 batches.
 int launchMatmulKq(bool q6k, bool per256, const kcMatmulKQ8Args& a, hipStream_t s);
+// layer_ops.hip
+int launchVectorAdd(const float* a, const float* b, float* out, int count, hipStream_t s);
+int launchAddSumsq(const float* a, const float* b, float* out, int* q, int n, int rows, hipStream_t s);
+int launchNormMulQ8(bool per256, const kcNormMulQ8Args& a, hipStream_t s);
+int launchSiluMulQ8(bool per256, const kcSiluMulQ8FArgs& a, hipStream_t s);
+int launchMulRows(const kcMulRowsArgs& a, hipStream_t s);
+int launchSiluMul(const kcSiluMulArgs& a, hipStream_t s);
+int launchRmsNorm(const kcRmsNormArgs& a, hipStream_t s);
+int launchRope(const kcRopeGgmlArgs& a, hipStream_t s);
+int launchSetRows(const kcSetRowsF16Args& a, hipStream_t s);
+int launchFaScores(const kcFaScoresArgs& a, hipStream_t s);
+int launchFaMax(const kcFaMaxArgs& a, hipStream_t s);
+int launchFaExp(const kcFaExpArgs& a, hipStream_t s);
+int launchFaValues(const kcFaValuesArgs& a, hipStream_t s);
+int launchFlashAttn(const kcFlashAttnArgs& a, hipStream_t s);
+constexpr int kFlashAttnMaxT = 16384;
 // Largest k the matvec's activation staging accepts.
 constexpr int kMatvecMaxK = 32768;
 

@@ -1,5 +1,18 @@
-// layer_ops.hip -- bandwidth-bound elementwise and row kernels around the K-quant matvecs (gfx950).
+// layer_ops.hip -- the bandwidth-bound layer kernels around the K-quant matmuls (gfx950):
+// residual add + RMS partial sums, RMS norm x weight fused with the 8-bit quantization (per 32 or
+// per 256 values), SwiGLU fused with the quantization, ggml RoPE, the fp16 KV-cache SET_ROWS,
+// FLASH_ATTN_EXT (the reference's four kernels and a fused single-kernel form), and plain
+// rms_norm / mul_rows / silu_mul / vector_add.
+//
+// Float operations follow the reference kernels in order (arasheedu/Kernelcore
+// kernels/llm/add_sumsq_f.cu, sumsq_part.cu, norm_mul_q8_f.cu, norm_mul_q8k_f.cu,
+// silu_mul_q8x4f.cu, silu_mul_q8kf.cu, rope_ggml.cu, set_rows_f16.cu, fa_*.cu, rms_norm.cu,
+// mul_rows.cu, silu_mul.cu): sums of squares and the row total run sequentially per thread as
+// there, so the norms and their quantized bytes are bit-identical; exp2f / sinf / cosf use the
+// GPU's own math library, within a few ulps of the CPU's.
 #include <hip/hip_runtime.h>
+
+#include <cstdint>
 
 #include "internal.hpp"
 #include "launch.hpp"
@@ -7,19 +20,486 @@
 namespace kcamd {
 namespace {
 
-// kernels/vector_add.cu: out[i] = a[i] + b[i].
+constexpr float kLog2e = 1.44269504f;
+
+__device__ __forceinline__ int q8r(float t) {
+    int q;
+    if (t >= 0.0f) q = (int)(t + 0.5f);
+    else q = (int)(t - 0.5f);
+    return q > 127 ? 127 : (q < -127 ? -127 : q);
+}
+
+// One block of 32 values of y quantized into a per-32 slot (quantize_q8x4.cu:15-40).
+__device__ __forceinline__ void quant32(const float* yb, int* qw, float* xd2) {
+    float amax = 0.0f;
+    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fmaxf(yb[i], 0.0f - yb[i]));
+    const float d = amax / 127.0f;
+    float id;
+    if (d > 0.0f) id = 1.0f / d;
+    else id = 0.0f;
+    int sum = 0;
+    for (int k = 0; k < 8; ++k) {
+        int word = 0;
+        for (int i = 0; i < 4; ++i) {
+            const int c = q8r(yb[4 * k + i] * id);
+            sum += c;
+            word |= (c & 255) << (8 * i);
+        }
+        qw[k] = word;
+    }
+    xd2[0] = d;
+    xd2[1] = (float)sum;
+}
+
+// One super-block of 256 values of y into a per-256 slot of nsb super-blocks (quantize_cols_k.cu).
+__device__ __forceinline__ void quant256(const float* yb, int* qc, int nsb, int s) {
+    float amax = 0.0f;
+    for (int i = 0; i < 256; ++i) amax = fmaxf(amax, fmaxf(yb[i], 0.0f - yb[i]));
+    const float d = amax / 127.0f;
+    float id;
+    if (d > 0.0f) id = 1.0f / d;
+    else id = 0.0f;
+    int b16[16];
+    for (int g = 0; g < 16; ++g) {
+        int sum = 0;
+        for (int k = 0; k < 4; ++k) {
+            int word = 0;
+            for (int i = 0; i < 4; ++i) {
+                const int c = q8r(yb[16 * g + 4 * k + i] * id);
+                sum += c;
+                word |= (c & 255) << (8 * i);
+            }
+            qc[s * 64 + g * 4 + k] = word;
+        }
+        qc[nsb * 65 + s * 16 + g] = sum;
+        b16[g] = sum;
+    }
+    int pw[4] = {0, 0, 0, 0};
+    for (int i = 0; i < 8; ++i) {
+        const int b = b16[2 * i] + b16[2 * i + 1];
+        pw[i >> 2] |= ((b >> 6) & 255) << (8 * (i & 3));
+        pw[2 + (i >> 2)] |= (b & 63) << (8 * (i & 3));
+    }
+    for (int i = 0; i < 4; ++i) qc[nsb * 81 + s * 4 + i] = pw[i];
+    reinterpret_cast<float*>(qc + nsb * 64)[s] = d;
+}
+
+__device__ __forceinline__ float rmsScale(const float* ss, int nb, int n, float eps) {
+    float tot = 0.0f;
+    for (int j = 0; j < nb; ++j) tot += ss[j];
+    return 1.0f / sqrtf(tot / (float)n + eps);
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + exp2f(-g * kLog2e)); }
+
+// ---------------------------------------------------------------- residual add + RMS norm
+
+// out = a + b and per-32 sums of out^2 into the row's slot tail (add_sumsq_f.cu). a may be null:
+// then x = b and only the sums are written (sumsq_part.cu).
+__global__ void add_sumsq_kernel(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ out,
+                                 int* __restrict__ q, int n, int rows) {
+    const int nb = n / 32;
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= nb * rows) return;
+    const int row = idx / nb, bl = idx - row * nb;
+    const size_t o = (size_t)row * n + bl * 32;
+    float s = 0.0f;
+    for (int i = 0; i < 32; ++i) {
+        float v;
+        if (a) {
+            v = a[o + i] + b[o + i];
+            out[o + i] = v;
+        } else {
+            v = b[o + i];
+        }
+        s += v * v;
+    }
+    reinterpret_cast<float*>(q + (size_t)row * nb * 11 + nb * 10)[bl] = s;
+}
+
+// y = x * r * w, quantized per 32 into the row's slot (norm_mul_q8_f.cu).
+__global__ void norm_mul_q8_kernel(const float* __restrict__ x, const float* __restrict__ w, float* __restrict__ y,
+                                   int* __restrict__ q, int n, int rows, float eps) {
+    const int nb = n / 32;
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= nb * rows) return;
+    const int row = idx / nb, bl = idx - row * nb;
+    int* qr = q + (size_t)row * nb * 11;
+    const float r = rmsScale(reinterpret_cast<const float*>(qr + nb * 10), nb, n, eps);
+    const size_t o = (size_t)row * n + bl * 32;
+    float v[32];
+    for (int i = 0; i < 32; ++i) {
+        v[i] = x[o + i] * r * w[bl * 32 + i];
+        y[o + i] = v[i];
+    }
+    quant32(v, qr + bl * 8, reinterpret_cast<float*>(qr + nb * 8) + bl * 2);
+}
+
+// The same with per-256 slots (norm_mul_q8k_f.cu): q holds rows slots of nsb*85 ints, then the
+// rows per-32 slots whose tails hold the partial sums.
+__global__ void norm_mul_q8k_kernel(const float* __restrict__ x, const float* __restrict__ w, float* __restrict__ y,
+                                    int* __restrict__ q, int n, int rows, float eps) {
+    const int nsb = n / 256, nb = n / 32;
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= nsb * rows) return;
+    const int row = idx / nsb, s = idx - row * nsb;
+    const float* ss = reinterpret_cast<const float*>(q + (size_t)rows * nsb * 85 + (size_t)row * nb * 11 + nb * 10);
+    const float r = rmsScale(ss, nb, n, eps);
+    const size_t o = (size_t)row * n + s * 256;
+    for (int i = 0; i < 256; ++i) y[o + i] = x[o + i] * r * w[s * 256 + i];
+    quant256(y + o, q + (size_t)row * nsb * 85, nsb, s);
+}
+
+// SwiGLU, quantized per 32 (silu_mul_q8x4f.cu) or per 256 (silu_mul_q8kf.cu); columns of n.
+__global__ void silu_mul_q8_kernel(const float* __restrict__ g, const float* __restrict__ u, float* __restrict__ y,
+                                   int* __restrict__ q, int n, int cols) {
+    const int nb = n / 32;
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= nb * cols) return;
+    const int c = idx / nb, b = idx - c * nb;
+    const size_t o = (size_t)c * n + b * 32;
+    float v[32];
+    for (int i = 0; i < 32; ++i) {
+        v[i] = silu(g[o + i]) * u[o + i];
+        y[o + i] = v[i];
+    }
+    int* qc = q + (size_t)c * nb * 11;
+    quant32(v, qc + b * 8, reinterpret_cast<float*>(qc + nb * 8) + b * 2);
+}
+
+__global__ void silu_mul_q8k_kernel(const float* __restrict__ g, const float* __restrict__ u, float* __restrict__ y,
+                                    int* __restrict__ q, int n, int cols) {
+    const int nsb = n / 256;
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= nsb * cols) return;
+    const int c = idx / nsb, s = idx - c * nsb;
+    const size_t o = (size_t)c * n + s * 256;
+    for (int i = 0; i < 256; ++i) y[o + i] = silu(g[o + i]) * u[o + i];
+    quant256(y + o, q + (size_t)c * nsb * 85, nsb, s);
+}
+
+// ---------------------------------------------------------------- elementwise and row ops
+
 __global__ void vector_add_kernel(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ out,
                                   int count) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < count) out[i] = a[i] + b[i];
 }
 
+__global__ void mul_rows_kernel(const float* __restrict__ x, const float* __restrict__ w, float* __restrict__ y, int n,
+                                int count) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < count) y[i] = x[i] * w[i % n];
+}
+
+__global__ void silu_mul_kernel(const float* __restrict__ g, const float* __restrict__ u, float* __restrict__ out,
+                                int count) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < count) out[i] = silu(g[i]) * u[i];
+}
+
+// One thread per row, sequential sums as rms_norm.cu (bit-identical).
+__global__ void rms_norm_kernel(const float* __restrict__ x, const float* __restrict__ w, float* __restrict__ y, int n,
+                                int rows, float eps) {
+    const int row = blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= rows) return;
+    const float* xr = x + (size_t)row * n;
+    float ss = 0.0f;
+    for (int j = 0; j < n; ++j) ss += xr[j] * xr[j];
+    const float r = 1.0f / sqrtf(ss / (float)n + eps);
+    float* yr = y + (size_t)row * n;
+    for (int j = 0; j < n; ++j) yr[j] = xr[j] * r * w[j];
+}
+
+// ggml ROPE (rope_ggml.cu): one thread per (token, pair), applied to the pair of every head.
+__global__ void rope_kernel(const float* __restrict__ x, float* __restrict__ y, const int* __restrict__ pos,
+                            const float* __restrict__ ff, int pairs, int nh, int count, float log2_base, int m1,
+                            int m2) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= count) return;
+    const int t = idx / pairs, i = idx - t * pairs;
+    const float theta = (float)pos[t] * exp2f(-(float)i / (float)pairs * log2_base) / ff[i];
+    const float c = cosf(theta), s = sinf(theta);
+    for (int h = 0; h < nh; ++h) {
+        const size_t a = 2 * ((size_t)t * nh + h) * pairs + (size_t)i * m1;
+        const float x0 = x[a], x1 = x[a + m2];
+        y[a] = x0 * c - x1 * s;
+        y[a + m2] = x0 * s + x1 * c;
+    }
+}
+
+// fp32 -> fp16 bits as set_rows_f16.cu: nearest even, |x| >= 65520 -> +-0x7bff, -0 -> +0.
+__device__ __forceinline__ uint32_t f2h(float x) {
+    if (x == 0.0f) return 0;
+    const uint32_t sign = x < 0.0f ? 0x8000u : 0u;
+    if (!(fabsf(x) < 65520.0f)) return sign | 0x7bffu;
+    return __builtin_bit_cast(unsigned short, (_Float16)x);
+}
+
+// ggml SET_ROWS into fp16 (set_rows_f16.cu): one thread per (row, pair) writes one 32-bit word.
+__global__ void set_rows_kernel(const float* __restrict__ src, const int* __restrict__ idx, int* __restrict__ dst,
+                                int pairs, int rows, int src_row, int dst_row, int dst_rows) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= pairs * rows) return;
+    const int r = i / pairs, j = i - r * pairs;
+    const int row = idx[2 * r];  // low word of the int64 row number
+    if (row < 0 || row >= dst_rows) return;
+    const float* sp = src + (size_t)r * src_row + 2 * j;
+    dst[(size_t)row * dst_row + j] = (int)(f2h(sp[0]) | (f2h(sp[1]) << 16));
+}
+
+// ---------------------------------------------------------------- FLASH_ATTN_EXT over an fp16 cache
+
+__device__ __forceinline__ float h2f(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (unsigned short)h); }
+
+struct Fa {  // kcFaDims, as kernel arguments
+    int H, T, D, group, tp, k_row, k_head, v_row, v_head, N, q_tok, q_head, m_row, has_mask, H_kv;
+};
+
+__device__ __forceinline__ float maskAt(const int* mask, const Fa& d, int i, int t) {
+    if (!d.has_mask) return 0.0f;
+    const uint32_t w = (uint32_t)mask[(size_t)i * d.m_row + t / 2];
+    return h2f((w >> ((t & 1) * 16)) & 0xFFFFu);
+}
+
+// s[(h * N + i) * tp + t] = scale * q.K + mask (fa_scores.cu): one thread per (head, query, t).
+__global__ void fa_scores_kernel(const float* __restrict__ q, const int* __restrict__ k, const int* __restrict__ mask,
+                                 float* __restrict__ s, Fa d, float scale) {
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long per = (long long)d.N * d.tp;
+    if (idx >= (long long)d.H * per) return;
+    const int h = (int)(idx / per);
+    const int r = (int)(idx - (long long)h * per);
+    const int i = r / d.tp, t = r - i * d.tp;
+    if (t >= d.T) return;
+    const int kvh = h / d.group;
+    const float* qh = q + (size_t)i * d.q_tok + (size_t)h * d.q_head;
+    const int* kr = k + (size_t)t * d.k_row + (size_t)kvh * d.k_head;
+    float a = 0.0f;
+    for (int j = 0; j < d.D / 2; ++j) {
+        const uint32_t w = (uint32_t)kr[j];
+        a += qh[2 * j] * h2f(w & 0xFFFFu) + qh[2 * j + 1] * h2f(w >> 16);
+    }
+    s[idx] = scale * a + maskAt(mask, d, i, t);
+}
+
+__global__ void fa_max_kernel(const float* __restrict__ s, float* __restrict__ m, Fa d) {
+    const int row = blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= d.H * d.N) return;
+    const float* sr = s + (size_t)row * d.tp;
+    float mx = sr[0];
+    for (int t = 1; t < d.T; ++t) mx = fmaxf(mx, sr[t]);
+    m[row] = mx;
+}
+
+__global__ void fa_exp_kernel(float* __restrict__ s, const float* __restrict__ m, Fa d) {
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long long)d.H * d.N * d.tp) return;
+    const int row = (int)(idx / d.tp), t = (int)(idx - (long long)row * d.tp);
+    if (t < d.T) s[idx] = exp2f((s[idx] - m[row]) * kLog2e);
+}
+
+// out[(i * H + h) * D + dd] = sum_t p * V / sum_t p (fa_values.cu): one thread per (query, head, dd).
+__global__ void fa_values_kernel(const float* __restrict__ p, const int* __restrict__ v, float* __restrict__ out,
+                                 Fa d) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= d.N * d.H * d.D) return;
+    const int i = idx / (d.H * d.D);
+    const int r = idx - i * d.H * d.D;
+    const int h = r / d.D, dd = r - h * d.D;
+    const int kvh = h / d.group;
+    const float* pr = p + ((size_t)h * d.N + i) * d.tp;
+    const int* vc = v + (size_t)kvh * d.v_head + dd / 2;
+    const int sh = (dd & 1) * 16;
+    float a = 0.0f, sum = 0.0f;
+    for (int t = 0; t < d.T; ++t) {
+        const float x = h2f(((uint32_t)vc[(size_t)t * d.v_row] >> sh) & 0xFFFFu);
+        a += pr[t] * x;
+        sum += pr[t];
+    }
+    out[idx] = a / sum;
+}
+
+// Fused single-kernel attention for decode and short prefills: one workgroup per (query, head).
+// Scores go to LDS (T <= kFaMaxT), the softmax uses the row maximum and exp2 as the four-kernel
+// path does, and the value sums run over t with the workgroup's threads split over (dd, t-slices).
+constexpr int kFaMaxT = 16384;
+__global__ __launch_bounds__(256) void flash_attn_kernel(const float* __restrict__ q, const int* __restrict__ k,
+                                                         const int* __restrict__ v, const int* __restrict__ mask,
+                                                         float* __restrict__ out, Fa d, float scale) {
+    extern __shared__ float lds[];
+    float* sc = lds;              // [T]
+    float* red = lds + d.T;       // [256] reduction scratch
+    const int i = blockIdx.x / d.H, h = blockIdx.x - i * d.H;
+    const int kvh = h / d.group;
+    const int tid = threadIdx.x;
+    const float* qh = q + (size_t)i * d.q_tok + (size_t)h * d.q_head;
+    // scores: one thread per position, q from L1
+    float mx = -INFINITY;
+    for (int t = tid; t < d.T; t += 256) {
+        const int* kr = k + (size_t)t * d.k_row + (size_t)kvh * d.k_head;
+        float a = 0.0f;
+        for (int j = 0; j < d.D / 2; ++j) {
+            const uint32_t w = (uint32_t)kr[j];
+            a += qh[2 * j] * h2f(w & 0xFFFFu) + qh[2 * j + 1] * h2f(w >> 16);
+        }
+        const float sv = scale * a + maskAt(mask, d, i, t);
+        sc[t] = sv;
+        mx = fmaxf(mx, sv);
+    }
+    red[tid] = mx;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (tid < o) red[tid] = fmaxf(red[tid], red[tid + o]);
+        __syncthreads();
+    }
+    const float m = red[0];
+    __syncthreads();
+    for (int t = tid; t < d.T; t += 256) sc[t] = exp2f((sc[t] - m) * kLog2e);
+    __syncthreads();
+    // values: threads split as (dd, slice); each slice sums a strided subset of t
+    const int slices = 256 / d.D > 0 ? 256 / d.D : 1;
+    for (int dd0 = 0; dd0 < d.D; dd0 += 256 / slices) {
+        const int dd = dd0 + tid % (256 / slices);
+        const int sl = tid / (256 / slices);
+        float a = 0.0f, sum = 0.0f;
+        if (dd < d.D && sl < slices) {
+            const int* vc = v + (size_t)kvh * d.v_head + dd / 2;
+            const int sh = (dd & 1) * 16;
+            for (int t = sl; t < d.T; t += slices) {
+                const float x = h2f(((uint32_t)vc[(size_t)t * d.v_row] >> sh) & 0xFFFFu);
+                a += sc[t] * x;
+                sum += sc[t];
+            }
+        }
+        red[tid] = a;
+        __syncthreads();
+        if (sl == 0 && dd < d.D) {
+            float at = 0.0f;
+            for (int j = 0; j < slices; ++j) at += red[j * (256 / slices) + tid % (256 / slices)];
+            red[tid] = at;
+        }
+        // row sum of p: one more pass over the same slices
+        __syncthreads();
+        const float at = (sl == 0 && dd < d.D) ? red[tid] : 0.0f;
+        __syncthreads();
+        red[tid] = sum;
+        __syncthreads();
+        if (sl == 0 && dd < d.D) {
+            float st = 0.0f;
+            for (int j = 0; j < slices; ++j) st += red[j * (256 / slices) + tid % (256 / slices)];
+            out[((size_t)i * d.H + h) * d.D + dd] = at / st;
+        }
+        __syncthreads();
+    }
+}
+
+Fa toFa(const kcFaDims& x) {
+    return Fa{x.H, x.T, x.D, x.group, x.tp, x.k_row, x.k_head, x.v_row, x.v_head, x.N, x.q_tok, x.q_head, x.m_row,
+              x.has_mask, x.H_kv};
+}
+
+unsigned blocksFor(long long threads) { return (unsigned)((threads + 255) / 256); }
+
 }  // namespace
 
 int launchVectorAdd(const float* a, const float* b, float* out, int count, hipStream_t s) {
     if (count == 0) return 0;
-    hipLaunchKernelGGL(vector_add_kernel, dim3((count + 255) / 256), dim3(256), 0, s, a, b, out, count);
+    hipLaunchKernelGGL(vector_add_kernel, dim3(blocksFor(count)), dim3(256), 0, s, a, b, out, count);
     return fromHip(hipGetLastError(), "vector_add");
+}
+
+int launchAddSumsq(const float* a, const float* b, float* out, int* q, int n, int rows, hipStream_t s) {
+    hipLaunchKernelGGL(add_sumsq_kernel, dim3(blocksFor((long long)(n / 32) * rows)), dim3(256), 0, s, a, b, out, q, n,
+                       rows);
+    return fromHip(hipGetLastError(), a ? "add_sumsq_f" : "sumsq_part");
+}
+
+int launchNormMulQ8(bool per256, const kcNormMulQ8Args& a, hipStream_t s) {
+    if (per256)
+        hipLaunchKernelGGL(norm_mul_q8k_kernel, dim3(blocksFor((long long)(a.n / 256) * a.rows)), dim3(256), 0, s, a.x,
+                           a.w, a.y, a.q, a.n, a.rows, a.eps);
+    else
+        hipLaunchKernelGGL(norm_mul_q8_kernel, dim3(blocksFor((long long)(a.n / 32) * a.rows)), dim3(256), 0, s, a.x,
+                           a.w, a.y, a.q, a.n, a.rows, a.eps);
+    return fromHip(hipGetLastError(), per256 ? "norm_mul_q8k_f" : "norm_mul_q8_f");
+}
+
+int launchSiluMulQ8(bool per256, const kcSiluMulQ8FArgs& a, hipStream_t s) {
+    if (per256)
+        hipLaunchKernelGGL(silu_mul_q8k_kernel, dim3(blocksFor((long long)(a.n / 256) * a.cols)), dim3(256), 0, s, a.g,
+                           a.u, a.y, a.q, a.n, a.cols);
+    else
+        hipLaunchKernelGGL(silu_mul_q8_kernel, dim3(blocksFor((long long)(a.n / 32) * a.cols)), dim3(256), 0, s, a.g,
+                           a.u, a.y, a.q, a.n, a.cols);
+    return fromHip(hipGetLastError(), per256 ? "silu_mul_q8kf" : "silu_mul_q8x4f");
+}
+
+int launchMulRows(const kcMulRowsArgs& a, hipStream_t s) {
+    if (a.count == 0) return 0;
+    hipLaunchKernelGGL(mul_rows_kernel, dim3(blocksFor(a.count)), dim3(256), 0, s, a.x, a.w, a.y, a.n, a.count);
+    return fromHip(hipGetLastError(), "mul_rows");
+}
+
+int launchSiluMul(const kcSiluMulArgs& a, hipStream_t s) {
+    if (a.count == 0) return 0;
+    hipLaunchKernelGGL(silu_mul_kernel, dim3(blocksFor(a.count)), dim3(256), 0, s, a.g, a.u, a.out, a.count);
+    return fromHip(hipGetLastError(), "silu_mul");
+}
+
+int launchRmsNorm(const kcRmsNormArgs& a, hipStream_t s) {
+    if (a.rows == 0) return 0;
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(blocksFor(a.rows)), dim3(256), 0, s, a.x, a.w, a.y, a.n, a.rows, a.eps);
+    return fromHip(hipGetLastError(), "rms_norm");
+}
+
+int launchRope(const kcRopeGgmlArgs& a, hipStream_t s) {
+    const int pairs = a.head_dim / 2;
+    const int count = pairs * a.n_tokens;
+    if (count == 0) return 0;
+    hipLaunchKernelGGL(rope_kernel, dim3(blocksFor(count)), dim3(256), 0, s, a.x, a.y, a.pos, a.ff, pairs, a.n_head,
+                       count, a.log2_base, a.neox ? 1 : 2, a.neox ? pairs : 1);
+    return fromHip(hipGetLastError(), "rope_ggml");
+}
+
+int launchSetRows(const kcSetRowsF16Args& a, hipStream_t s) {
+    hipLaunchKernelGGL(set_rows_kernel, dim3(blocksFor((long long)a.pairs * a.rows)), dim3(256), 0, s, a.src, a.idx,
+                       a.dst, a.pairs, a.rows, a.src_row, a.dst_row, a.dst_rows);
+    return fromHip(hipGetLastError(), "set_rows_f16");
+}
+
+int launchFaScores(const kcFaScoresArgs& a, hipStream_t s) {
+    const Fa d = toFa(a.d);
+    hipLaunchKernelGGL(fa_scores_kernel, dim3(blocksFor((long long)d.H * d.N * d.tp)), dim3(256), 0, s, a.q, a.k,
+                       a.mask, a.s, d, a.scale);
+    return fromHip(hipGetLastError(), "fa_scores");
+}
+
+int launchFaMax(const kcFaMaxArgs& a, hipStream_t s) {
+    const Fa d = toFa(a.d);
+    hipLaunchKernelGGL(fa_max_kernel, dim3(blocksFor((long long)d.H * d.N)), dim3(256), 0, s, a.s, a.m, d);
+    return fromHip(hipGetLastError(), "fa_max");
+}
+
+int launchFaExp(const kcFaExpArgs& a, hipStream_t s) {
+    const Fa d = toFa(a.d);
+    hipLaunchKernelGGL(fa_exp_kernel, dim3(blocksFor((long long)d.H * d.N * d.tp)), dim3(256), 0, s, a.s, a.m, d);
+    return fromHip(hipGetLastError(), "fa_exp");
+}
+
+int launchFaValues(const kcFaValuesArgs& a, hipStream_t s) {
+    const Fa d = toFa(a.d);
+    hipLaunchKernelGGL(fa_values_kernel, dim3(blocksFor((long long)d.N * d.H * d.D)), dim3(256), 0, s, a.p, a.v,
+                       a.out, d);
+    return fromHip(hipGetLastError(), "fa_values");
+}
+
+int launchFlashAttn(const kcFlashAttnArgs& a, hipStream_t s) {
+    const Fa d = toFa(a.d);
+    const size_t lds = sizeof(float) * ((size_t)d.T + 256);
+    hipLaunchKernelGGL(flash_attn_kernel, dim3(d.N * d.H), dim3(256), lds, s, a.q, a.k, a.v, a.mask, a.out, d,
+                       a.scale);
+    return fromHip(hipGetLastError(), "flash_attn_f16");
 }
 
 }  // namespace kcamd

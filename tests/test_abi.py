@@ -80,7 +80,7 @@ def test_codegen_cpu_paths_are_unsupported():
 STRUCTS = ["VectorAddArgs", "QuantizeArgs", "MatvecQ4Q8Args", "MatmulKQ8Args", "QuantizeColsArgs", "RmsNormArgs",
            "MulRowsArgs", "RopeGgmlArgs", "AddSumsqFArgs", "SumsqPartArgs", "NormMulQ8Args", "SiluMulQ8FArgs",
            "SiluMulArgs", "SetRowsF16Args", "FaDims", "FaScoresArgs", "FaMaxArgs", "FaExpArgs", "FaValuesArgs",
-           "KquantRepackArgs", "DeviceProperties"]
+           "KquantRepackArgs", "FlashAttnArgs", "DeviceProperties"]
 
 
 def test_struct_layouts_match_the_c_header(tmp_path):

@@ -136,3 +136,37 @@ def test_matmul_argument_validation():
     assert kc.launch_status("matmul_q4k_q8kx8", A(stream.ptr, bq.ptr, by.ptr, bad.ptr, rows, k, ncols, 8)) == "InvalidValue"
     for b in (stream, bq, by, dims, bad):
         b.free()
+
+
+# ---- the MFMA path (Q4_K, per-256 slots, ncols >= 32) ---------------------------------------------
+
+MFMA_CASES = [(8, 256, 32), (40, 768, 33), (128, 3072, 100), (1000, 1024, 128), (136, 8192, 200), (3072, 3072, 64)]
+
+
+@pytest.mark.parametrize("rows,k,ncols", MFMA_CASES)
+def test_mfma_matmul_matches_oracle(rows, k, ncols):
+    note(f"mfma q4k {rows}x{k} ncols={ncols}")
+    w = kq.random_blocks("q4k", rows, k, seed=rows + 3 * k + ncols)
+    x = kq.randn(k * ncols, ncols + 5, 1.5)
+    kc.set_option("matmul_path", 2)
+    y, _ = run_matmul("q4k", True, w, x, rows, k, ncols)
+    kc.set_option("matmul_path", 1)
+    yc, _ = run_matmul("q4k", True, w, x, rows, k, ncols)
+    kc.set_option("matmul_path", 0)
+    want = oracle_matmul("q4k", True, w, oracle_slots(x, k, ncols, True), rows, k, ncols)
+    assert np.array_equal(kq.bits(yc), kq.bits(want))  # the column-tile path stays bit-exact
+    assert kq.rel_diff(y, want) < TOL
+    assert kq.rel_diff(y, want) < 1e-5  # exact integers; only the final float combine differs
+
+
+def test_mfma_matmul_config3_shapes():
+    """512 tokens through gate/up (8192 x 3072) and down (3072 x 8192), Q4_K."""
+    ncols = 512
+    for rows, k, seed in ((8192, 3072, 301), (3072, 8192, 302)):
+        note(f"mfma cfg3 {rows}x{k}x{ncols}")
+        w = kq.random_blocks("q4k", rows, k, seed=seed)
+        x = kq.randn(k * ncols, seed + 1)
+        y, slots = run_matmul("q4k", True, w, x, rows, k, ncols)
+        want = np.zeros(rows * ncols, np.float32)
+        O.kco_matmul_q4k_q8k_mt(w, slots, want, rows, k, ncols, O.kco_max_threads())
+        assert kq.rel_diff(y, want.reshape(ncols, rows)) < TOL
