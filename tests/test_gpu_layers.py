@@ -231,7 +231,8 @@ def test_layer_argument_validation():
     x = B.new(4096)
     q = B.new(4096)
     assert kc.launch_status("add_sumsq_f", kc.AddSumsqFArgs(x.ptr, x.ptr, x.ptr, q.ptr, None, 100, 1)) == "InvalidValue"
-    assert kc.launch_status("sumsq_part", kc.SumsqPartArgs(x.ptr, q.ptr, None, 256, 4)) == "InvalidPointer"
+    assert kc.launch_status("sumsq_part", kc.SumsqPartArgs(x.ptr, q.ptr, None, 256, 4)) == "Success"
+    assert kc.launch_status("sumsq_part", kc.SumsqPartArgs(x.ptr, q.ptr, None, 256, 5)) == "InvalidPointer"
     assert kc.launch_status("rope_ggml", kc.RopeGgmlArgs(x.ptr, x.ptr, q.ptr, q.ptr, None, 24, 1, 1, 1.0, False)) == "InvalidValue"
     d = kc.FaDims(H=3, T=8, D=8, group=2, tp=8, k_row=4, k_head=4, v_row=4, v_head=4, N=1, q_tok=24, q_head=8,
                   m_row=4, has_mask=0, H_kv=2)  # H != H_kv * group
