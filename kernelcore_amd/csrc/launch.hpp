@@ -16,8 +16,8 @@ int launchQuantizeColsK(const float* x, int* q, int k, int ncols, hipStream_t s)
 int launchMatvecKq(bool q6k, const kcMatvecQ4Q8Args& a, hipStream_t s);
 // kmatmul.hip: column-tiled matmul (any ncols; bit-identical per column to the reference).
 int launchMatmulCols(bool q6k, bool per256, const kcMatmulKQ8Args& a, hipStream_t s);
-// kmatmul_mfma.hip: Q4_K x per-256 activations on MFMA (large batches).
-int launchMatmulQ4kMfma(const kcMatmulKQ8Args& a, hipStream_t s);
+// kmatmul_mfma.hip: K-quant x per-256 activations on MFMA (large batches).
+int launchMatmulMfma(bool q6k, const kcMatmulKQ8Args& a, hipStream_t s);
 // The matmul names: column tiles for small batches and per-32 slots, MFMA for large per-256 batches.
 int launchMatmulKq(bool q6k, bool per256, const kcMatmulKQ8Args& a, hipStream_t s);
 // layer_ops.hip

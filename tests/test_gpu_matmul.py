@@ -138,22 +138,23 @@ def test_matmul_argument_validation():
         b.free()
 
 
-# ---- the MFMA path (Q4_K, per-256 slots, ncols >= 32) ---------------------------------------------
+# ---- the MFMA path (per-256 slots, ncols >= 64 by default) ---------------------------------------------
 
 MFMA_CASES = [(8, 256, 32), (40, 768, 33), (128, 3072, 100), (1000, 1024, 128), (136, 8192, 200), (3072, 3072, 64)]
 
 
+@pytest.mark.parametrize("qtype", ["q4k", "q6k"])
 @pytest.mark.parametrize("rows,k,ncols", MFMA_CASES)
-def test_mfma_matmul_matches_oracle(rows, k, ncols):
-    note(f"mfma q4k {rows}x{k} ncols={ncols}")
-    w = kq.random_blocks("q4k", rows, k, seed=rows + 3 * k + ncols)
+def test_mfma_matmul_matches_oracle(qtype, rows, k, ncols):
+    note(f"mfma {qtype} {rows}x{k} ncols={ncols}")
+    w = kq.random_blocks(qtype, rows, k, seed=rows + 3 * k + ncols)
     x = kq.randn(k * ncols, ncols + 5, 1.5)
     kc.set_option("matmul_path", 2)
-    y, _ = run_matmul("q4k", True, w, x, rows, k, ncols)
+    y, _ = run_matmul(qtype, True, w, x, rows, k, ncols)
     kc.set_option("matmul_path", 1)
-    yc, _ = run_matmul("q4k", True, w, x, rows, k, ncols)
+    yc, _ = run_matmul(qtype, True, w, x, rows, k, ncols)
     kc.set_option("matmul_path", 0)
-    want = oracle_matmul("q4k", True, w, oracle_slots(x, k, ncols, True), rows, k, ncols)
+    want = oracle_matmul(qtype, True, w, oracle_slots(x, k, ncols, True), rows, k, ncols)
     assert np.array_equal(kq.bits(yc), kq.bits(want))  # the column-tile path stays bit-exact
     assert kq.rel_diff(y, want) < TOL
     assert kq.rel_diff(y, want) < 1e-5  # exact integers; only the final float combine differs
