@@ -20,7 +20,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB_PATH = os.path.join(HERE, "libkernelcore_amd.so")
-HEADERS = [os.path.join(ROOT, "include", "kernelcore", n) for n in ("kc.h", "llm_kernels.h")]
+HEADERS = [os.path.join(ROOT, "include", "kernelcore", n) for n in ("kc.h", "llm_kernels.h", "model.h")]
 
 ERRORS = ["Success", "NotInitialized", "InvalidValue", "InvalidDevice", "OutOfMemory", "InvalidPointer",
           "InvalidResourceHandle", "UnsupportedOperation", "InvalidKernelImage", "KernelNotFound",
@@ -83,6 +83,12 @@ DeviceProperties = _struct("DeviceProperties", [("name", C.c_char * 128), ("work
                                                 ("performance_workers", C.c_uint), ("total_memory", C.c_size_t),
                                                 ("is_hardware_gpu", C.c_bool), ("guard_pages", C.c_bool),
                                                 ("large_pages", C.c_bool), ("kernel_stack_bytes", C.c_size_t)])
+ModelConfig = _struct("ModelConfig", [("n_layer", _i), ("n_embd", _i), ("n_head", _i), ("n_head_kv", _i),
+                                      ("head_dim", _i), ("n_ff", _i), ("n_vocab", _i), ("norm_eps", _f),
+                                      ("rope_theta", _f), ("rope_neox", _i), ("qk_norm", _i), ("max_ctx", _i),
+                                      ("max_batch", _i)])
+TENSORS = {"token_embd": 0, "output_norm": 1, "output": 2, "attn_norm": 3, "wq": 4, "wk": 5, "wv": 6, "wo": 7,
+           "ffn_norm": 8, "w_gate": 9, "w_up": 10, "w_down": 11, "q_norm": 12, "k_norm": 13}
 KernelEntry = _struct("KernelEntry", [("name", C.c_char_p), ("validate", _p), ("launch", _p), ("chunkable", _i)])
 
 # ---- library ----------------------------------------------------------------------------------------
@@ -128,6 +134,15 @@ def lib():
             getattr(L, n).argtypes = [_p, _p]
         L.kcSetKernelOption.argtypes = [C.c_char_p, _i]
         L.kcGetKernelOption.argtypes = [C.c_char_p, C.POINTER(_i)]
+        L.kcModelCreate.argtypes = [C.POINTER(ModelConfig), C.POINTER(_p)]
+        L.kcModelDestroy.argtypes = [_p]
+        L.kcModelTensorInfo.argtypes = [_p, _i, _i, C.POINTER(_i), C.POINTER(_i), C.POINTER(_i), C.POINTER(C.c_size_t)]
+        L.kcModelSetTensor.argtypes = [_p, _i, _i, _p, C.c_size_t]
+        L.kcModelForward.argtypes = [_p, _p, _i, _p]
+        L.kcModelGenerate.argtypes = [_p, _i, _p]
+        L.kcModelPosition.argtypes = [_p, C.POINTER(_i)]
+        L.kcModelReset.argtypes = [_p]
+        L.kcModelStream.argtypes = [_p, C.POINTER(_p)]
         L.kcGetErrorString.argtypes = [_i]
         L.kcCodegenName.argtypes = [_i]
         _LIB = L
@@ -236,3 +251,52 @@ def upload_weights(qtype, blocks_np, rows, k):
         return repack(qtype, raw, rows, k)
     finally:
         raw.free()
+
+
+class Model:
+    """The decode driver (include/kernelcore/model.h)."""
+
+    def __init__(self, **cfg):
+        self.cfg = ModelConfig(**cfg)
+        h = _p()
+        call("kcModelCreate", C.byref(self.cfg), C.byref(h))
+        self.h = h
+
+    def tensor_info(self, tensor, layer=-1):
+        qt, rows, k, nb = _i(), _i(), _i(), C.c_size_t()
+        call("kcModelTensorInfo", self.h, TENSORS.get(tensor, tensor), layer, C.byref(qt), C.byref(rows), C.byref(k),
+             C.byref(nb))
+        return qt.value, rows.value, k.value, nb.value
+
+    def set_tensor(self, tensor, layer, data):
+        a = np.ascontiguousarray(data)
+        call("kcModelSetTensor", self.h, TENSORS.get(tensor, tensor), layer, a.ctypes.data, a.nbytes)
+
+    def forward(self, tokens, want_logits=True):
+        t = np.ascontiguousarray(tokens, np.int32)
+        out = np.zeros(self.cfg.n_vocab, np.float32) if want_logits else None
+        call("kcModelForward", self.h, t.ctypes.data, t.size, out.ctypes.data if want_logits else None)
+        return out
+
+    def generate(self, steps):
+        out = np.zeros(steps, np.int32)
+        call("kcModelGenerate", self.h, steps, out.ctypes.data)
+        return out
+
+    def position(self):
+        p = _i()
+        call("kcModelPosition", self.h, C.byref(p))
+        return p.value
+
+    def reset(self):
+        call("kcModelReset", self.h)
+
+    def stream(self):
+        s = _p()
+        call("kcModelStream", self.h, C.byref(s))
+        return s
+
+    def close(self):
+        if self.h:
+            lib().kcModelDestroy(self.h)
+            self.h = None

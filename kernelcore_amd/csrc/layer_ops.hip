@@ -96,8 +96,9 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + exp2f(-g * k
 
 // out = a + b and per-32 sums of out^2 into the row's slot tail (add_sumsq_f.cu). a may be null:
 // then x = b and only the sums are written (sumsq_part.cu).
-__global__ void add_sumsq_kernel(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ out,
-                                 int* __restrict__ q, int n, int rows) {
+// a and out may be the same buffer (the residual stream updated in place).
+__global__ void add_sumsq_kernel(const float* a, const float* __restrict__ b, float* out, int* __restrict__ q, int n,
+                                 int rows) {
     const int nb = n / 32;
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= nb * rows) return;
@@ -323,7 +324,6 @@ __global__ void fa_values_kernel(const float* __restrict__ p, const int* __restr
 // Fused single-kernel attention for decode and short prefills: one workgroup per (query, head).
 // Scores go to LDS (T <= kFaMaxT), the softmax uses the row maximum and exp2 as the four-kernel
 // path does, and the value sums run over t with the workgroup's threads split over (dd, t-slices).
-constexpr int kFaMaxT = 16384;
 __global__ __launch_bounds__(256) void flash_attn_kernel(const float* __restrict__ q, const int* __restrict__ k,
                                                          const int* __restrict__ v, const int* __restrict__ mask,
                                                          float* __restrict__ out, Fa d, float scale) {
@@ -497,6 +497,9 @@ int launchFaValues(const kcFaValuesArgs& a, hipStream_t s) {
 int launchFlashAttn(const kcFlashAttnArgs& a, hipStream_t s) {
     const Fa d = toFa(a.d);
     const size_t lds = sizeof(float) * ((size_t)d.T + 256);
+    static const int attr = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(flash_attn_kernel),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (attr != 0) return fromHip(attr, "flash_attn_f16: LDS size");
     hipLaunchKernelGGL(flash_attn_kernel, dim3(d.N * d.H), dim3(256), lds, s, a.q, a.k, a.v, a.mask, a.out, d,
                        a.scale);
     return fromHip(hipGetLastError(), "flash_attn_f16");

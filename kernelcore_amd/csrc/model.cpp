@@ -1,0 +1,525 @@
+// model.cpp -- the decode driver (include/kernelcore/model.h): a Llama / Qwen3-architecture
+// transformer with K-quant weights on the kc* runtime and the built-in kernels.
+//
+// Op order follows the reference's ggml backend graph for one layer (docs/cuda_cpu_poc_plan.md:1158
+// in arasheedu/Kernelcore; backend dispatch ggml-kernelcore.cpp:555-589, fusions :743-769):
+// single tokens take per-32 activation slots and the matvecs (mul_mat_impl with ncols == 1),
+// batches take per-256 slots and the matmuls (batch_k256). As llama.cpp does for a prompt, the
+// last layer continues after the attention output projection with the last token only, so
+// its FFN, the output norm and the head run on one row (the decode kernels).
+#include <hip/hip_runtime.h>
+#include <kernelcore/model.h>
+
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <new>
+#include <vector>
+
+#include "internal.hpp"
+#include "kquant.hpp"
+#include "launch.hpp"
+#include "model_kernels.hpp"
+
+namespace {
+
+struct Layer {
+    void *wq = nullptr, *wk = nullptr, *wv = nullptr, *wo = nullptr, *wg = nullptr, *wu = nullptr, *wd = nullptr;
+    float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+    int *kcache = nullptr, *vcache = nullptr;
+};
+
+int qtypeOf(int tensor) {
+    switch (tensor) {
+        case KC_TENSOR_OUTPUT_NORM:
+        case KC_TENSOR_ATTN_NORM:
+        case KC_TENSOR_FFN_NORM:
+        case KC_TENSOR_Q_NORM:
+        case KC_TENSOR_K_NORM: return KC_QTYPE_F32;
+        case KC_TENSOR_OUTPUT:
+        case KC_TENSOR_WV:
+        case KC_TENSOR_W_DOWN: return KC_QTYPE_Q6_K;
+        default: return KC_QTYPE_Q4_K;
+    }
+}
+
+bool perLayer(int tensor) { return tensor >= KC_TENSOR_ATTN_NORM; }
+
+}  // namespace
+
+struct kcModel_st {
+    kcModelConfig c{};
+    kcStream_t ks = nullptr;
+    hipStream_t s = nullptr;
+    std::vector<Layer> L;
+    void *tok_embd = nullptr, *output = nullptr;
+    float* out_norm = nullptr;
+    float* ones = nullptr;  // rope frequency factors (none in these models)
+    // activations, sized for max_batch tokens
+    float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *qr = nullptr, *kr = nullptr;
+    float *att = nullptr, *o = nullptr, *gate = nullptr, *up = nullptr, *sw = nullptr, *down = nullptr;
+    float* logits = nullptr;
+    int *slotE32 = nullptr, *slotEK = nullptr, *slotQ32 = nullptr, *slotQK = nullptr, *slotF32 = nullptr,
+        *slotFK = nullptr;
+    int *tokens = nullptr, *pos = nullptr, *n_past = nullptr, *n_ctx = nullptr, *gen = nullptr, *step = nullptr;
+    long long* idx = nullptr;
+    int max_gen = 4096;
+    int pos_host = 0;
+    kcGraph_t step_graph = nullptr;
+    std::vector<void*> allocs;
+};
+
+namespace {
+
+using E = kcError_t;
+constexpr E ok = kc::Error::Success;
+inline E err(int c) { return static_cast<E>(c); }
+
+#define KM_TRY(expr)                    \
+    do {                                \
+        if (int e_ = (expr)) return err(e_); \
+    } while (0)
+#define KI_TRY(expr)                    \
+    do {                                \
+        if (int e_ = (expr)) return e_; \
+    } while (0)
+#define KM_TRYE(expr)                   \
+    do {                                \
+        if (E e_ = (expr); e_ != ok) return e_; \
+    } while (0)
+
+E alloc(kcModel_st* m, void** p, size_t bytes) {
+    KM_TRYE(kcMalloc(p, bytes));
+    m->allocs.push_back(*p);
+    return ok;
+}
+template <class T>
+E allocT(kcModel_st* m, T** p, size_t count) {
+    void* v = nullptr;
+    KM_TRYE(alloc(m, &v, count * sizeof(T)));
+    *p = static_cast<T*>(v);
+    return ok;
+}
+
+void shapeOf(const kcModelConfig& c, int tensor, int* rows, int* k) {
+    const int Q = c.n_head * c.head_dim, KV = c.n_head_kv * c.head_dim;
+    switch (tensor) {
+        case KC_TENSOR_TOKEN_EMBD:
+        case KC_TENSOR_OUTPUT: *rows = c.n_vocab, *k = c.n_embd; return;
+        case KC_TENSOR_OUTPUT_NORM:
+        case KC_TENSOR_ATTN_NORM:
+        case KC_TENSOR_FFN_NORM: *rows = 1, *k = c.n_embd; return;
+        case KC_TENSOR_Q_NORM:
+        case KC_TENSOR_K_NORM: *rows = 1, *k = c.head_dim; return;
+        case KC_TENSOR_WQ: *rows = Q, *k = c.n_embd; return;
+        case KC_TENSOR_WK:
+        case KC_TENSOR_WV: *rows = KV, *k = c.n_embd; return;
+        case KC_TENSOR_WO: *rows = c.n_embd, *k = Q; return;
+        case KC_TENSOR_W_GATE:
+        case KC_TENSOR_W_UP: *rows = c.n_ff, *k = c.n_embd; return;
+        case KC_TENSOR_W_DOWN: *rows = c.n_embd, *k = c.n_ff; return;
+        default: *rows = *k = 0;
+    }
+}
+
+size_t ggmlBytes(int qtype, int rows, int k) {
+    if (qtype == KC_QTYPE_F32) return size_t(rows) * k * 4;
+    return size_t(rows) * (k / 256) * (qtype == KC_QTYPE_Q6_K ? 210 : 144);
+}
+
+// ---- one decode step (one token, per-32 slots, matvecs) -----------------------------------
+
+int matvec(bool q6, const void* w, const int* slot, float* y, int rows, int k, hipStream_t s) {
+    kcMatvecQ4Q8Args a{static_cast<const int*>(w), slot, reinterpret_cast<const float*>(slot + k / 32 * 8), y, nullptr,
+                       rows, k};
+    return kcamd::launchMatvecKq(q6, a, s);
+}
+
+int matmul(bool q6, const void* w, const int* slots, float* y, int rows, int k, int n, hipStream_t s) {
+    kcMatmulKQ8Args a{static_cast<const int*>(w), slots, y, nullptr, rows, k, n, 8};
+    return kcamd::launchMatmulKq(q6, true, a, s);
+}
+
+int normQ8(const float* x, const float* w, float* y, int* slot, int n, float eps, hipStream_t s) {
+    kcNormMulQ8Args a{x, w, y, slot, nullptr, n, 1, eps};
+    return kcamd::launchNormMulQ8(false, a, s);
+}
+
+// FFN of one token (row x of the residual stream, whose per-32 partial sums are in slotE32):
+// norm, gate/up, SwiGLU + quantization, down. Leaves the result in m->down (1 row).
+int ffnOne(kcModel_st* m, const Layer& l, float* x, hipStream_t s) {
+    const auto& c = m->c;
+    KI_TRY(normQ8(x, l.ffn_norm, m->xn, m->slotE32, c.n_embd, c.norm_eps, s));
+    KI_TRY(matvec(false, l.wg, m->slotE32, m->gate, c.n_ff, c.n_embd, s));
+    KI_TRY(matvec(false, l.wu, m->slotE32, m->up, c.n_ff, c.n_embd, s));
+    kcSiluMulQ8FArgs sa{m->gate, m->up, m->sw, m->slotF32, nullptr, c.n_ff, 1};
+    KI_TRY(kcamd::launchSiluMulQ8(false, sa, s));
+    return matvec(true, l.wd, m->slotF32, m->down, c.n_embd, c.n_ff, s);
+}
+
+// Output norm + head for the row x (partial sums in slotE32) into m->logits.
+int headOne(kcModel_st* m, float* x, hipStream_t s) {
+    const auto& c = m->c;
+    KI_TRY(normQ8(x, m->out_norm, m->xn, m->slotE32, c.n_embd, c.norm_eps, s));
+    return matvec(true, m->output, m->slotE32, m->logits, c.n_vocab, c.n_embd, s);
+}
+
+// RoPE of q and k (after the optional per-head norm) into m->qr / m->kr.
+int ropeQK(kcModel_st* m, int n, hipStream_t s) {
+    const auto& c = m->c;
+    const float l2b = std::log2(c.rope_theta);
+    const float* qin = c.qk_norm ? m->att : m->q;  // the normed q lives in m->att until attention
+    const float* kin = c.qk_norm ? m->kr : m->k;
+    float* kout = c.qk_norm ? m->k : m->kr;
+    kcRopeGgmlArgs rq{qin, m->qr, m->pos, m->ones, nullptr, c.head_dim, c.n_head, n, l2b, c.rope_neox != 0};
+    KI_TRY(kcamd::launchRope(rq, s));
+    kcRopeGgmlArgs rk{kin, kout, m->pos, m->ones, nullptr, c.head_dim, c.n_head_kv, n, l2b, c.rope_neox != 0};
+    return kcamd::launchRope(rk, s);
+}
+
+// Qwen3: per-head RMS norm of q (into m->att, free until the attention) and k (into m->kr).
+int qkNorm(kcModel_st* m, const Layer& l, int n, hipStream_t s) {
+    const auto& c = m->c;
+    if (!c.qk_norm) return 0;
+    kcRmsNormArgs qa{m->q, l.q_norm, m->att, c.head_dim, c.n_head * n, c.norm_eps};
+    KI_TRY(kcamd::launchRmsNorm(qa, s));
+    kcRmsNormArgs ka{m->k, l.k_norm, m->kr, c.head_dim, c.n_head_kv * n, c.norm_eps};
+    return kcamd::launchRmsNorm(ka, s);
+}
+
+// The roped k of this step: m->kr, or m->k when the per-head norm used m->kr.
+const float* ropedK(const kcModel_st* m) { return m->c.qk_norm ? m->k : m->kr; }
+
+int kvStore(kcModel_st* m, const Layer& l, int n, hipStream_t s) {
+    const auto& c = m->c;
+    const int KV = c.n_head_kv * c.head_dim;
+    kcSetRowsF16Args ka{ropedK(m), reinterpret_cast<const int*>(m->idx), l.kcache, nullptr, KV / 2, n, KV, KV / 2,
+                        c.max_ctx};
+    KI_TRY(kcamd::launchSetRows(ka, s));
+    kcSetRowsF16Args va{m->v, reinterpret_cast<const int*>(m->idx), l.vcache, nullptr, KV / 2, n, KV, KV / 2,
+                        c.max_ctx};
+    return kcamd::launchSetRows(va, s);
+}
+
+int attention(kcModel_st* m, const Layer& l, int n, hipStream_t s) {
+    const auto& c = m->c;
+    kcamd::AttnShape a{n, c.n_head, c.n_head_kv, c.head_dim, c.n_head * c.head_dim, c.n_head_kv * c.head_dim / 2,
+                       c.max_ctx, n > 1 ? 1 : 0, 1.0f / std::sqrt((float)c.head_dim)};
+    return kcamd::launchAttn(m->qr, l.kcache, l.vcache, m->att, m->n_ctx, a, s);
+}
+
+// The kernels of one token at position *n_past, reading its id from m->tokens[0]; leaves the
+// logits in m->logits.
+int decodeStep(kcModel_st* m, hipStream_t s) {
+    const auto& c = m->c;
+    const int Q = c.n_head * c.head_dim, KV = c.n_head_kv * c.head_dim;
+    KI_TRY(kcamd::launchPositions(m->n_past, 1, m->pos, m->idx, m->n_ctx, s));
+    KI_TRY(kcamd::launchGetRows(false, m->tok_embd, m->tokens, m->x, 1, c.n_embd, s));
+    for (int li = 0; li < c.n_layer; ++li) {
+        const Layer& l = m->L[li];
+        if (li == 0) KI_TRY(kcamd::launchAddSumsq(nullptr, m->x, nullptr, m->slotE32, c.n_embd, 1, s));
+        else KI_TRY(kcamd::launchAddSumsq(m->x, m->down, m->x, m->slotE32, c.n_embd, 1, s));
+        KI_TRY(normQ8(m->x, l.attn_norm, m->xn, m->slotE32, c.n_embd, c.norm_eps, s));
+        KI_TRY(matvec(false, l.wq, m->slotE32, m->q, Q, c.n_embd, s));
+        KI_TRY(matvec(false, l.wk, m->slotE32, m->k, KV, c.n_embd, s));
+        KI_TRY(matvec(true, l.wv, m->slotE32, m->v, KV, c.n_embd, s));
+        KI_TRY(qkNorm(m, l, 1, s));
+        KI_TRY(ropeQK(m, 1, s));
+        KI_TRY(kvStore(m, l, 1, s));
+        KI_TRY(attention(m, l, 1, s));
+        KI_TRY(kcamd::launchQuantizeQ8x4(m->att, m->slotQ32, reinterpret_cast<float*>(m->slotQ32 + Q / 32 * 8), Q / 32, s));
+        KI_TRY(matvec(false, l.wo, m->slotQ32, m->o, c.n_embd, Q, s));
+        KI_TRY(kcamd::launchAddSumsq(m->x, m->o, m->x, m->slotE32, c.n_embd, 1, s));
+        KI_TRY(ffnOne(m, l, m->x, s));
+    }
+    KI_TRY(kcamd::launchAddSumsq(m->x, m->down, m->x, m->slotE32, c.n_embd, 1, s));
+    return headOne(m, m->x, s);
+}
+
+// n > 1 tokens (m->tokens[0..n)) at positions *n_past ..: per-256 slots and the matmuls.
+int batchStep(kcModel_st* m, int n, hipStream_t s) {
+    const auto& c = m->c;
+    const int Q = c.n_head * c.head_dim, KV = c.n_head_kv * c.head_dim;
+    const int E_ = c.n_embd;
+    int* sums = m->slotEK + (size_t)n * (E_ / 256) * 85;  // per-32 slots holding the partial sums
+    KI_TRY(kcamd::launchPositions(m->n_past, n, m->pos, m->idx, m->n_ctx, s));
+    KI_TRY(kcamd::launchGetRows(false, m->tok_embd, m->tokens, m->x, n, E_, s));
+    float* x_last = m->x + (size_t)(n - 1) * E_;
+    for (int li = 0; li < c.n_layer; ++li) {
+        const Layer& l = m->L[li];
+        if (li == 0) KI_TRY(kcamd::launchAddSumsq(nullptr, m->x, nullptr, sums, E_, n, s));
+        else KI_TRY(kcamd::launchAddSumsq(m->x, m->down, m->x, sums, E_, n, s));
+        kcNormMulQ8Args na{m->x, l.attn_norm, m->xn, m->slotEK, nullptr, E_, n, c.norm_eps};
+        KI_TRY(kcamd::launchNormMulQ8(true, na, s));
+        KI_TRY(matmul(false, l.wq, m->slotEK, m->q, Q, E_, n, s));
+        KI_TRY(matmul(false, l.wk, m->slotEK, m->k, KV, E_, n, s));
+        KI_TRY(matmul(true, l.wv, m->slotEK, m->v, KV, E_, n, s));
+        KI_TRY(qkNorm(m, l, n, s));
+        KI_TRY(ropeQK(m, n, s));
+        KI_TRY(kvStore(m, l, n, s));
+        KI_TRY(attention(m, l, n, s));
+        KI_TRY(kcamd::launchQuantizeColsK(m->att, m->slotQK, Q, n, s));
+        KI_TRY(matmul(false, l.wo, m->slotQK, m->o, E_, Q, n, s));
+        if (li + 1 < c.n_layer) {
+            KI_TRY(kcamd::launchAddSumsq(m->x, m->o, m->x, sums, E_, n, s));
+            kcNormMulQ8Args fa{m->x, l.ffn_norm, m->xn, m->slotEK, nullptr, E_, n, c.norm_eps};
+            KI_TRY(kcamd::launchNormMulQ8(true, fa, s));
+            KI_TRY(matmul(false, l.wg, m->slotEK, m->gate, c.n_ff, E_, n, s));
+            KI_TRY(matmul(false, l.wu, m->slotEK, m->up, c.n_ff, E_, n, s));
+            kcSiluMulQ8FArgs sa{m->gate, m->up, m->sw, m->slotFK, nullptr, c.n_ff, n};
+            KI_TRY(kcamd::launchSiluMulQ8(true, sa, s));
+            KI_TRY(matmul(true, l.wd, m->slotFK, m->down, E_, c.n_ff, n, s));
+        } else {  // the last layer continues with the last token only
+            KI_TRY(kcamd::launchAddSumsq(x_last, m->o + (size_t)(n - 1) * E_, x_last, m->slotE32, E_, 1, s));
+            KI_TRY(ffnOne(m, l, x_last, s));
+        }
+    }
+    KI_TRY(kcamd::launchAddSumsq(x_last, m->down, x_last, m->slotE32, E_, 1, s));
+    return headOne(m, x_last, s);
+}
+
+E checkModel(kcModel_t m) {
+    if (!m) {
+        kcamd::setDetail("model is null");
+        return kc::Error::InvalidValue;
+    }
+    return ok;
+}
+
+E syncModel(kcModel_t m) { return kcStreamSynchronize(m->ks); }
+
+}  // namespace
+
+kcError_t kcModelCreate(const kcModelConfig* cfg, kcModel_t* out) noexcept {
+    if (!cfg || !out) return kc::Error::InvalidValue;
+    *out = nullptr;
+    const kcModelConfig& c = *cfg;
+    if (c.n_layer <= 0 || c.n_embd <= 0 || c.n_embd % 256 || c.n_head <= 0 || c.n_head_kv <= 0 ||
+        c.n_head % c.n_head_kv || c.head_dim <= 0 || c.head_dim % 16 || c.head_dim > 256 ||
+        (c.n_head * c.head_dim) % 256 || (c.n_head_kv * c.head_dim) % 16 || c.n_ff <= 0 || c.n_ff % 256 ||
+        c.n_vocab <= 0 || c.n_vocab % 8 || c.max_ctx <= 0 || c.max_ctx > 16384 || c.max_batch <= 0 ||
+        c.max_batch > c.max_ctx || !(c.rope_theta > 0.0f)) {
+        kcamd::setDetail("model config out of range (dims multiples of 256, head_dim a multiple of 16, max_ctx <= 16384)");
+        return kc::Error::InvalidValue;
+    }
+    if (256 % c.head_dim && c.head_dim != 256) {
+        kcamd::setDetail("head_dim must divide 256");
+        return kc::Error::InvalidValue;
+    }
+    auto m = std::unique_ptr<kcModel_st>(new (std::nothrow) kcModel_st);
+    if (!m) return kc::Error::OutOfMemory;
+    m->c = c;
+    auto fail = [&](E e) {
+        for (void* p : m->allocs) (void)kcFree(p);
+        if (m->ks) (void)kcStreamDestroy(m->ks);
+        return e;
+    };
+    if (E e = kcStreamCreate(&m->ks); e != ok) return e;
+    void* hs = nullptr;
+    if (E e = kcStreamGetNative(m->ks, &hs); e != ok) return fail(e);
+    m->s = static_cast<hipStream_t>(hs);
+    const int B = c.max_batch, E_ = c.n_embd, Q = c.n_head * c.head_dim, KV = c.n_head_kv * c.head_dim, F = c.n_ff;
+    m->L.resize(c.n_layer);
+#define KM_A(ptr, count) \
+    if (E e = allocT(m.get(), &(ptr), (size_t)(count)); e != ok) return fail(e)
+    KM_A(m->x, (size_t)B * E_);
+    KM_A(m->xn, (size_t)B * E_);
+    KM_A(m->q, (size_t)B * Q);
+    KM_A(m->qr, (size_t)B * Q);
+    KM_A(m->k, (size_t)B * KV);
+    KM_A(m->kr, (size_t)B * KV);
+    KM_A(m->v, (size_t)B * KV);
+    KM_A(m->att, (size_t)B * Q);
+    KM_A(m->o, (size_t)B * E_);
+    KM_A(m->gate, (size_t)B * F);
+    KM_A(m->up, (size_t)B * F);
+    KM_A(m->sw, (size_t)B * F);
+    KM_A(m->down, (size_t)B * E_);
+    KM_A(m->logits, (size_t)c.n_vocab);
+    KM_A(m->slotE32, (size_t)E_ / 32 * 11);
+    KM_A(m->slotEK, (size_t)B * (E_ / 256 * 85 + E_ / 32 * 11));
+    KM_A(m->slotQ32, (size_t)Q / 32 * 11);
+    KM_A(m->slotQK, (size_t)B * Q / 256 * 85);
+    KM_A(m->slotF32, (size_t)F / 32 * 11);
+    KM_A(m->slotFK, (size_t)B * F / 256 * 85);
+    KM_A(m->tokens, (size_t)B);
+    KM_A(m->pos, (size_t)B);
+    KM_A(m->idx, (size_t)B);
+    KM_A(m->n_past, 1);
+    KM_A(m->n_ctx, 1);
+    KM_A(m->gen, (size_t)m->max_gen);
+    KM_A(m->step, 1);
+    KM_A(m->ones, (size_t)c.head_dim / 2);
+    for (auto& l : m->L) {
+        KM_A(l.kcache, (size_t)c.max_ctx * KV / 2);
+        KM_A(l.vcache, (size_t)c.max_ctx * KV / 2);
+    }
+#undef KM_A
+    std::vector<float> ones(c.head_dim / 2, 1.0f);
+    if (E e = kcMemcpy(m->ones, ones.data(), ones.size() * 4, kc::CopyKind::HostToDevice); e != ok) return fail(e);
+    const int zero = 0;
+    if (E e = kcMemcpy(m->n_past, &zero, 4, kc::CopyKind::HostToDevice); e != ok) return fail(e);
+    *out = m.release();
+    return ok;
+}
+
+kcError_t kcModelDestroy(kcModel_t m) noexcept {
+    if (!m) return kc::Error::Success;
+    (void)kcStreamSynchronize(m->ks);
+    if (m->step_graph) (void)kcGraphDestroy(m->step_graph);
+    for (void* p : m->allocs) (void)kcFree(p);
+    (void)kcStreamDestroy(m->ks);
+    delete m;
+    return kc::Error::Success;
+}
+
+kcError_t kcModelTensorInfo(kcModel_t m, int tensor, int layer, int* qtype, int* rows, int* k,
+                            size_t* bytes) noexcept {
+    if (E e = checkModel(m); e != ok) return e;
+    if (tensor < 0 || tensor >= KC_TENSOR_COUNT || (perLayer(tensor) && (layer < 0 || layer >= m->c.n_layer)))
+        return kc::Error::InvalidValue;
+    int r = 0, kk = 0;
+    shapeOf(m->c, tensor, &r, &kk);
+    const int qt = qtypeOf(tensor);
+    if (qtype) *qtype = qt;
+    if (rows) *rows = r;
+    if (k) *k = kk;
+    if (bytes) *bytes = ggmlBytes(qt, r, kk);
+    return ok;
+}
+
+kcError_t kcModelSetTensor(kcModel_t m, int tensor, int layer, const void* host, size_t bytes) noexcept {
+    if (E e = checkModel(m); e != ok) return e;
+    int qt = 0, r = 0, kk = 0;
+    size_t want = 0;
+    if (E e = kcModelTensorInfo(m, tensor, layer, &qt, &r, &kk, &want); e != ok) return e;
+    if (!host || bytes != want) {
+        kcamd::setDetail("tensor %d: expected %zu bytes", tensor, want);
+        return kc::Error::InvalidValue;
+    }
+    if ((tensor == KC_TENSOR_Q_NORM || tensor == KC_TENSOR_K_NORM) && !m->c.qk_norm) return kc::Error::InvalidValue;
+    Layer* l = perLayer(tensor) ? &m->L[layer] : nullptr;
+    void** slot = nullptr;
+    switch (tensor) {
+        case KC_TENSOR_TOKEN_EMBD: slot = &m->tok_embd; break;
+        case KC_TENSOR_OUTPUT: slot = &m->output; break;
+        case KC_TENSOR_OUTPUT_NORM: slot = reinterpret_cast<void**>(&m->out_norm); break;
+        case KC_TENSOR_ATTN_NORM: slot = reinterpret_cast<void**>(&l->attn_norm); break;
+        case KC_TENSOR_FFN_NORM: slot = reinterpret_cast<void**>(&l->ffn_norm); break;
+        case KC_TENSOR_Q_NORM: slot = reinterpret_cast<void**>(&l->q_norm); break;
+        case KC_TENSOR_K_NORM: slot = reinterpret_cast<void**>(&l->k_norm); break;
+        case KC_TENSOR_WQ: slot = &l->wq; break;
+        case KC_TENSOR_WK: slot = &l->wk; break;
+        case KC_TENSOR_WV: slot = &l->wv; break;
+        case KC_TENSOR_WO: slot = &l->wo; break;
+        case KC_TENSOR_W_GATE: slot = &l->wg; break;
+        case KC_TENSOR_W_UP: slot = &l->wu; break;
+        case KC_TENSOR_W_DOWN: slot = &l->wd; break;
+        default: return kc::Error::InvalidValue;
+    }
+    if (*slot) return kc::Error::InvalidValue;  // each tensor is set once
+    if (qt == KC_QTYPE_F32) {
+        KM_TRYE(alloc(m, slot, bytes));
+        return kcMemcpy(*slot, host, bytes, kc::CopyKind::HostToDevice);
+    }
+    size_t sb = 0;
+    KM_TRYE(kcKquantStreamBytes(qt, r, kk, &sb));
+    void* raw = nullptr;
+    KM_TRYE(kcMalloc(&raw, bytes));
+    E e = kcMemcpy(raw, host, bytes, kc::CopyKind::HostToDevice);
+    if (e == ok) e = alloc(m, slot, sb);
+    if (e == ok) {
+        kcKquantRepackArgs ra{raw, *slot, qt, r, kk};
+        e = kcLaunchKernel("repack_kquant", &ra, m->ks);
+        if (e == ok) e = syncModel(m);
+    }
+    (void)kcFree(raw);
+    return e;
+}
+
+static E checkLoaded(kcModel_t m) {
+    bool okw = m->tok_embd && m->output && m->out_norm;
+    for (const auto& l : m->L)
+        okw = okw && l.wq && l.wk && l.wv && l.wo && l.wg && l.wu && l.wd && l.attn_norm && l.ffn_norm &&
+              (!m->c.qk_norm || (l.q_norm && l.k_norm));
+    if (!okw) {
+        kcamd::setDetail("not every tensor has been set");
+        return kc::Error::InvalidValue;
+    }
+    return ok;
+}
+
+kcError_t kcModelForward(kcModel_t m, const int* tokens, int n, float* logits) noexcept {
+    if (E e = checkModel(m); e != ok) return e;
+    if (E e = checkLoaded(m); e != ok) return e;
+    if (!tokens || n <= 0 || n > m->c.max_batch || m->pos_host + n > m->c.max_ctx) {
+        kcamd::setDetail("n_tokens must be in [1, max_batch] and fit the cache");
+        return kc::Error::InvalidValue;
+    }
+    for (int i = 0; i < n; ++i)
+        if (tokens[i] < 0 || tokens[i] >= m->c.n_vocab) return kc::Error::InvalidValue;
+    KM_TRYE(syncModel(m));
+    KM_TRYE(kcMemcpy(m->tokens, tokens, sizeof(int) * n, kc::CopyKind::HostToDevice));
+    KM_TRYE(kcMemcpy(m->n_past, &m->pos_host, sizeof(int), kc::CopyKind::HostToDevice));
+    KM_TRY(n == 1 ? decodeStep(m, m->s) : batchStep(m, n, m->s));
+    KM_TRYE(syncModel(m));
+    m->pos_host += n;
+    if (logits) KM_TRYE(kcMemcpy(logits, m->logits, sizeof(float) * m->c.n_vocab, kc::CopyKind::DeviceToHost));
+    return ok;
+}
+
+kcError_t kcModelGenerate(kcModel_t m, int steps, int* tokens_out) noexcept {
+    if (E e = checkModel(m); e != ok) return e;
+    if (E e = checkLoaded(m); e != ok) return e;
+    if (steps <= 0 || steps > m->max_gen || m->pos_host == 0 || m->pos_host + steps - 1 > m->c.max_ctx) {
+        kcamd::setDetail("steps must be in [1, 4096], after a forward, and fit the cache");
+        return kc::Error::InvalidValue;
+    }
+    KM_TRYE(syncModel(m));
+    const int zero = 0;
+    KM_TRYE(kcMemcpy(m->step, &zero, sizeof(int), kc::CopyKind::HostToDevice));
+    KM_TRYE(kcMemcpy(m->n_past, &m->pos_host, sizeof(int), kc::CopyKind::HostToDevice));
+    // the first token: argmax of the last forward's logits (no position consumed)
+    KM_TRY(kcamd::launchArgmaxStep(m->logits, m->c.n_vocab, m->tokens, m->gen, m->step, nullptr, m->max_gen, m->s));
+    if (!m->step_graph) {
+        KM_TRYE(kcStreamBeginCapture(m->ks));
+        int e1 = decodeStep(m, m->s);
+        if (!e1)
+            e1 = kcamd::launchArgmaxStep(m->logits, m->c.n_vocab, m->tokens, m->gen, m->step, m->n_past, m->max_gen,
+                                         m->s);
+        kcGraph_t g = nullptr;
+        const E e2 = kcStreamEndCapture(m->ks, &g);
+        if (e1) {
+            if (g) (void)kcGraphDestroy(g);
+            return err(e1);
+        }
+        if (e2 != ok) return e2;
+        m->step_graph = g;
+    }
+    for (int i = 1; i < steps; ++i) KM_TRYE(kcGraphLaunch(m->step_graph, m->ks));
+    KM_TRYE(syncModel(m));
+    m->pos_host += steps - 1;
+    if (tokens_out) KM_TRYE(kcMemcpy(tokens_out, m->gen, sizeof(int) * steps, kc::CopyKind::DeviceToHost));
+    return ok;
+}
+
+kcError_t kcModelPosition(kcModel_t m, int* pos) noexcept {
+    if (E e = checkModel(m); e != ok) return e;
+    if (!pos) return kc::Error::InvalidValue;
+    *pos = m->pos_host;
+    return ok;
+}
+
+kcError_t kcModelReset(kcModel_t m) noexcept {
+    if (E e = checkModel(m); e != ok) return e;
+    KM_TRYE(syncModel(m));
+    m->pos_host = 0;
+    return ok;
+}
+
+kcError_t kcModelStream(kcModel_t m, kcStream_t* stream) noexcept {
+    if (E e = checkModel(m); e != ok) return e;
+    if (!stream) return kc::Error::InvalidValue;
+    *stream = m->ks;
+    return ok;
+}

@@ -184,7 +184,7 @@ __global__ __launch_bounds__(1024) void argmax_step_kernel(const float* __restri
         const int st = *step;
         if (st < max_gen) gen[st] = tokn;
         *step = st + 1;
-        *n_past = *n_past + 1;
+        if (n_past) *n_past = *n_past + 1;
     }
 }
 
@@ -213,6 +213,9 @@ int launchGetRows(bool q6k, const void* qw, const int* tok, float* y, int n, int
 int launchAttn(const float* q, const int* k, const int* v, float* out, const int* n_ctx, const AttnShape& a,
                hipStream_t s) {
     const size_t lds = sizeof(float) * ((size_t)a.max_t + 256 + 64);
+    static const int attr = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(attn_kernel),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (attr != 0) return fromHip(attr, "attn: LDS size");
     hipLaunchKernelGGL(attn_kernel, dim3(a.N * a.H), dim3(256), lds, s, q, k, v, out, n_ctx, a);
     return fromHip(hipGetLastError(), "attn");
 }
