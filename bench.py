@@ -29,6 +29,7 @@ sys.path.insert(0, HERE)
 import kernelcore_amd as kc  # noqa: E402
 
 PEAK_HBM_GBS = 8000.0
+PEAK_F16_TFLOPS = 2500.0  # dense fp16 MFMA
 METRIC = "Q4_K matvec HBM GB/s (% of peak); decode tok/s, 3B-shape Q4_K_M, 1 GPU"
 
 
@@ -150,6 +151,157 @@ def cpu_baseline(rows, k, seconds=10.0):
                       f"{per * 1e3:.1f} ms each, OpenMP over {threads} threads of {model}"}
 
 
+# Llama-3.2-3B architecture, Q4_K_M layout (Q6_K for attn_v / ffn_down / output)
+LLAMA32_3B = dict(n_layer=28, n_embd=3072, n_head=24, n_head_kv=8, head_dim=128, n_ff=8192, n_vocab=128256,
+                  norm_eps=1e-5, rope_theta=500000.0, rope_neox=0, qk_norm=0, max_ctx=1024, max_batch=512)
+
+
+def model_weights(m, cfg, seed):
+    """{(tensor id, layer): bytes} for every tensor of model m: random ggml blocks (random_blocks)
+    or norm weights in [0.8, 1.2); shapes from kcModelTensorInfo."""
+    rng = np.random.default_rng(seed)
+    out = {}
+    ids = [(t, -1) for t in (0, 1, 2)]
+    per_layer = [3, 4, 5, 6, 7, 8, 9, 10, 11] + ([12, 13] if cfg["qk_norm"] else [])
+    ids += [(t, l) for l in range(cfg["n_layer"]) for t in per_layer]
+    for tid, layer in ids:
+        qt, rows, k, _ = m.tensor_info(tid, layer)
+        if qt == 0:
+            out[(tid, layer)] = rng.uniform(0.8, 1.2, k).astype(np.float32)
+        else:
+            out[(tid, layer)] = random_blocks("q6k" if qt == 14 else "q4k", rows, k, seed + 1000 * tid + layer + 1)
+    return out
+
+
+def decode_bytes(w, cfg, ctx):
+    """HBM bytes one decode token reads: every weight tensor but the embedding (one row of it),
+    the f16 K and V caches over ctx positions, and the logits written."""
+    emb_row = cfg["n_embd"] // 256 * 144
+    wb = sum(a.nbytes for (tid, _), a in w.items() if tid != 0) + emb_row
+    kv = 2 * cfg["n_layer"] * ctx * cfg["n_head_kv"] * cfg["head_dim"] * 2
+    return wb + kv + cfg["n_vocab"] * 4
+
+
+def model_run(cfg, n_prompt, n_decode, seed, cpu_seconds, eager=False):
+    """a random n_prompt-token prompt (one batched forward), then n_decode greedy
+    decode steps (graph-replayed, argmax on the device). A warm-up prompt + 4 steps first (builds
+    the decode graph), then the cache is reset and the timed prompt and decode run."""
+    m = kc.Model(**cfg)
+    t0 = time.perf_counter()
+    w = model_weights(m, cfg, seed)
+    for (tid, layer), a in w.items():
+        m.set_tensor(tid, layer, a)
+    kc.synchronize()
+    setup_s = time.perf_counter() - t0
+    prompt = np.random.default_rng(seed + 7).integers(0, cfg["n_vocab"], n_prompt).astype(np.int32)
+    m.forward(prompt)
+    if not eager:
+        m.generate(4)
+    m.reset()
+    kc.synchronize()
+    t = Timer(m.stream())
+    e = [t.event() for _ in range(3)]
+    w0 = time.perf_counter()
+    t.record(e[0])
+    logits = m.forward(prompt)
+    t.record(e[1])
+    w1 = time.perf_counter()
+    if eager:  # one kcModelForward per token, argmax on the host (kernel tracing without graphs)
+        toks = [int(np.argmax(logits))]
+        for _ in range(n_decode):
+            toks.append(int(np.argmax(m.forward([toks[-1]]))))
+    else:
+        toks = m.generate(n_decode + 1)  # the first token comes from the prompt's logits
+    t.record(e[2])
+    kc.call("kcStreamSynchronize", m.stream())
+    w2 = time.perf_counter()
+    prefill_ms, decode_ms = Timer.ms(e[0], e[1]), Timer.ms(e[1], e[2])
+    for x in e:
+        kc.call("kcEventDestroy", x)
+    assert m.position() == n_prompt + n_decode
+    m.close()
+    bpt = decode_bytes(w, cfg, n_prompt + n_decode // 2)
+    dec_s = w2 - w1
+    gbs = bpt * n_decode / dec_s / 1e9
+    out = {"workload": f"BASELINE config 4: {cfg['n_layer']}-layer Llama-3.2-3B shape, Q4_K_M random weights, "
+                       f"{n_prompt}-token prompt then {n_decode} greedy decode steps, f16 KV cache",
+           "prefill_tok_s": round(n_prompt / (w1 - w0), 1), "decode_tok_s": round(n_decode / dec_s, 1),
+           "prefill_ms": round((w1 - w0) * 1e3, 3), "ms_per_decode_token": round(dec_s / n_decode * 1e3, 4),
+           "gpu_event_ms": {"prefill": round(prefill_ms, 3), "decode": round(decode_ms, 3)},
+           "decode_bytes_per_token": bpt, "decode_hbm_gbs": round(gbs, 1), "decode_frac": round(gbs / PEAK_HBM_GBS, 4),
+           "setup_s": round(setup_s, 2), "finite": bool(np.all(np.isfinite(logits))),
+           "first_tokens": [int(x) for x in toks[:4]], "decode": "eager" if eager else "graph"}
+    if cpu_seconds > 0:
+        out["cpu_baseline"] = cpu_decode_baseline(cfg, w, cpu_seconds)
+    return out
+
+
+def cpu_decode_baseline(cfg, w, seconds):
+    """The oracle model's decode (oracle/model.py: the same step on the host, OpenMP matvecs) from
+    an empty cache, a bounded number of tokens."""
+    import oracle
+    from oracle.model import OracleModel
+
+    threads = int(oracle.lib().kco_max_threads())
+    o = OracleModel(cfg, w, threads=threads)
+    o.forward([1])  # warm
+    n, t0 = 0, time.perf_counter()
+    tok = 1
+    while True:
+        tok = int(np.argmax(o.forward([tok])))
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= 64:
+            break
+    return {"value": round(n / el, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{n} greedy decode tokens at context 2..{n + 1} (the GPU decodes at {cfg['max_batch']}+), "
+                      f"{el / n * 1e3:.0f} ms each; the matvecs OpenMP over {threads} threads"}
+
+
+def prefill_matmul_run(steps, seed):
+    """the FFN of one layer over a 512-token prompt on the MFMA matmul --
+    gate and up (8192 x 3072) and down (3072 x 8192), Q4_K, per-256 int8 activations. One step
+    = the three matmuls; 2 * rows * k * 512 operations each."""
+    n = 512
+    shapes = [(8192, 3072), (8192, 3072), (3072, 8192)]
+    ws = [kc.upload_weights("q4k", random_blocks("q4k", r, k, seed + i), r, k) for i, (r, k) in enumerate(shapes)]
+    rng = np.random.default_rng(seed + 50)
+    xs = [kc.Buffer.of(rng.standard_normal(k * n).astype(np.float32)) for k in (3072, 8192)]
+    qs = [kc.Buffer(n * k // 256 * 85 * 4) for k in (3072, 8192)]
+    ys = [kc.Buffer(r * n * 4) for r, _ in shapes]
+    s = C.c_void_p()
+    kc.call("kcStreamCreate", C.byref(s))
+    for x, q, k in zip(xs, qs, (3072, 8192)):
+        kc.launch("quantize_cols_k", kc.QuantizeColsArgs(x.ptr, q.ptr, None, k, n), s)
+    args = [kc.MatmulKQ8Args(wt.ptr, qs[0 if k == 3072 else 1].ptr, y.ptr, None, r, k, n, 8)
+            for wt, y, (r, k) in zip(ws, ys, shapes)]
+    for _ in range(2):
+        for a in args:
+            kc.launch("matmul_q4k_q8kx8", a, s)
+    t = Timer(s)
+    e0, e1 = t.event(), t.event()
+    kc.call("kcStreamSynchronize", s)
+    t.record(e0)
+    for _ in range(steps):
+        for a in args:
+            kc.launch("matmul_q4k_q8kx8", a, s)
+    t.record(e1)
+    kc.call("kcStreamSynchronize", s)
+    ms = Timer.ms(e0, e1) / steps
+    for x in (e0, e1):
+        kc.call("kcEventDestroy", x)
+    kc.call("kcStreamDestroy", s)
+    finite = all(np.all(np.isfinite(y.download(np.float32))) for y in ys)
+    for b in ws + xs + qs + ys:
+        b.free()
+    ops = sum(2 * r * k * n for r, k in shapes)
+    tops = ops / (ms * 1e-3) / 1e12
+    return {"workload": "BASELINE config 3: gate + up (8192x3072) + down (3072x8192) Q4_K matmuls, 512 tokens",
+            "ms_per_step": round(ms, 4), "ops_per_step": ops, "achieved_tops": round(tops, 1),
+            "peak_tops": PEAK_F16_TFLOPS, "mfma_util": round(tops / PEAK_F16_TFLOPS, 4),
+            "mfma": "v_mfma_f32_32x32x16_f16 on exact small-integer operands", "finite": bool(finite)}
+
+
 def bytes_cfg2(rows=128256, k=3072):
     return rows * (k // 256) * 210 + k * 4 + rows * 4
 
@@ -175,6 +327,12 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--calibrate", action="store_true", help="also run a known-size vector_add (PMC scaling)")
     ap.add_argument("--skip-cfg1", action="store_true", help="only the config-2 workload (short profiling runs)")
+    ap.add_argument("--skip-model", action="store_true", help="skip the config-3 matmul and config-4 model legs")
+    ap.add_argument("--decode-steps", type=int, default=128)
+    ap.add_argument("--eager-decode", action="store_true",
+                    help="decode with one kcModelForward per token instead of the replayed graph")
+    ap.add_argument("--only-model", action="store_true",
+                    help="run only the config-3 matmul and config-4 model legs (profiling); prints their JSON")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -183,6 +341,11 @@ def main():
     kc.init()
     props = kc.device_properties()
     print(f"# device: {props.name.decode()} ({props.worker_count} CUs)", file=sys.stderr, flush=True)
+    if args.only_model:
+        mm = prefill_matmul_run(max(args.steps // 5, 5), seed=7000)
+        mdl = model_run(LLAMA32_3B, 512, args.decode_steps, seed=9000, cpu_seconds=0, eager=args.eager_decode)
+        print(json.dumps({"prefill_matmul_cfg3": mm, "model_cfg4": mdl}), flush=True)
+        return
     rows2, k2 = 128256, 3072
     r2 = matvec_run("q6k", rows2, k2, copies=2, steps=args.steps, warmup=args.warmup, seed=1000)
     print(f"# cfg2 done: kernel {r2['kernel_ms'] * 1e3:.1f} us", file=sys.stderr, flush=True)
@@ -194,6 +357,14 @@ def main():
                         seed=5000)
         print(f"# cfg1 done: kernel {r1['kernel_ms'] * 1e3:.2f} us", file=sys.stderr, flush=True)
     cal = calibrate() if args.calibrate else None
+    mm = mdl = None
+    if not args.skip_model:
+        mm = prefill_matmul_run(max(args.steps // 5, 5), seed=7000)
+        print(f"# cfg3 done: {mm['achieved_tops']} TOP/s", file=sys.stderr, flush=True)
+        mdl = model_run(LLAMA32_3B, 512, args.decode_steps, seed=9000, cpu_seconds=0 if args.no_cpu else 10.0,
+                        eager=args.eager_decode)
+        print(f"# cfg4 done: prefill {mdl['prefill_tok_s']} tok/s, decode {mdl['decode_tok_s']} tok/s",
+              file=sys.stderr, flush=True)
 
     b2 = bytes_cfg2(rows2, k2)
     ms_step = r2["region_ms"] / args.steps
@@ -214,11 +385,16 @@ def main():
         out["q4k_matvec_cfg1"] = {"achieved_gbs": round(a1, 1), "frac": round(a1 / PEAK_HBM_GBS, 4),
                                   "kernel_us": round(r1["kernel_ms"] * 1e3, 3), "bytes": bytes_cfg1(rows1, k1),
                                   "rotation": f"{copies1} weight copies"}
+    if mm:
+        out["prefill_matmul_cfg3"] = mm
+    if mdl:
+        out["model_cfg4"] = mdl
     if cal:
         out["calibration"] = cal
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(rows2, k2)
-    if not (r2["finite"] and (r1 is None or r1["finite"])):
+    if not (r2["finite"] and (r1 is None or r1["finite"]) and (mm is None or mm["finite"])
+            and (mdl is None or mdl["finite"])):
         out["warning"] = "non-finite outputs"
     print(json.dumps(out), flush=True)
 

@@ -1,0 +1,750 @@
+// kdecode.hip -- the single-token decode kernels of the model driver (gfx950).
+//
+// One token is latency-bound: every launch costs a few microseconds whatever it moves, so the
+// layer is cut into seven kernels instead of the reference graph's sixteen nodes:
+//   1. dmv (norm prologue): RMS norm x weight + per-32 quantization of the residual row, done by
+//      every workgroup into its own LDS, then the q / k / v matvecs in one grid;
+//   2. qk_post: per-head q / k RMS norm (Qwen3), RoPE, fp16 conversion of k and v into the cache;
+//   3. attn_decode + attn_merge: attention split over the context in chunks of 64 positions, then
+//      the merge of the partial softmaxes and the per-32 quantization of the output;
+//   4. dmv (slot prologue, residual epilogue): attention output projection, x += o;
+//   5. dmv (norm prologue, SwiGLU epilogue): FFN norm, gate and up matvecs, silu(g) * u and its
+//      per-32 quantization;
+//   6. dmv (slot prologue, residual epilogue): down projection, x += down.
+// The matvec terms, norms, sums of squares and quantizations repeat the operations of the
+// reference kernels they replace (kernels/llm/add_sumsq_f.cu, sumsq_part.cu, norm_mul_q8_f.cu,
+// matvec_q4k_q8.cu, matvec_q6k_q8.cu, silu_mul_q8x4f.cu, rope_ggml.cu, set_rows_f16.cu in
+// arasheedu/Kernelcore) in the same order, so the residual stream matches the unfused kernels
+// bit for bit; the split softmax changes only the attention's rounding.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "internal.hpp"
+#include "kdecode.hpp"
+#include "kquant_device.hpp"
+
+namespace kcamd {
+namespace {
+
+constexpr int kXs = 68;  // LDS ints per super-block of activations (64 + 4 pad)
+constexpr float kLog2e = 1.44269504f;
+constexpr int kChunk = 64;  // attention positions per workgroup
+constexpr int kMaxGroup = 8;  // query heads per KV head
+
+__device__ __forceinline__ int q8r(float t) {
+    int q;
+    if (t >= 0.0f) q = (int)(t + 0.5f);
+    else q = (int)(t - 0.5f);
+    return q > 127 ? 127 : (q < -127 ? -127 : q);
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + exp2f(-g * kLog2e)); }
+
+// fp32 -> fp16 bits as set_rows_f16.cu: nearest even, |x| >= 65520 -> +-0x7bff, -0 -> +0.
+__device__ __forceinline__ uint32_t f2h(float x) {
+    if (x == 0.0f) return 0;
+    const uint32_t sign = x < 0.0f ? 0x8000u : 0u;
+    if (!(fabsf(x) < 65520.0f)) return sign | 0x7bffu;
+    return __builtin_bit_cast(unsigned short, (_Float16)x);
+}
+
+__device__ __forceinline__ float h2f(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (unsigned short)h); }
+
+// Quantization of one block of 32 values by one thread (quantize_q8x4.cu:15-40, the reference's
+// order): amax, d = amax / 127, q = round(v / d) packed four to a word; also the block's sum of q
+// and the sum of its first 16 values. One thread per block keeps the work free of cross-lane
+// traffic, whose latency would otherwise dominate these small kernels.
+struct Q32 {
+    int w[8];
+    int sum, s16;
+    float d;
+};
+__device__ __forceinline__ Q32 quant32Seq(const float* y) {
+    Q32 o;
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fmaxf(y[i], 0.0f - y[i]));
+    o.d = amax / 127.0f;
+    float id;
+    if (o.d > 0.0f) id = 1.0f / o.d;
+    else id = 0.0f;
+    int sum = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        int word = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = q8r(y[4 * k + i] * id);
+            sum += c;
+            word |= (c & 255) << (8 * i);
+        }
+        o.w[k] = word;
+        if (k == 3) o.s16 = sum;
+    }
+    o.sum = sum;
+    return o;
+}
+
+// Block b of a quantized row into a per-32 slot: words at b * 8, (d, sum) at nb * 8 + 2b.
+__device__ __forceinline__ void storeQ32(int* slot, int nb, int b, const Q32& q) {
+    int4* w = reinterpret_cast<int4*>(slot + b * 8);
+    w[0] = make_int4(q.w[0], q.w[1], q.w[2], q.w[3]);
+    w[1] = make_int4(q.w[4], q.w[5], q.w[6], q.w[7]);
+    *reinterpret_cast<float2*>(slot + nb * 8 + 2 * b) = make_float2(q.d, (float)q.sum);
+}
+
+// ---------------------------------------------------------------- fused decode matvec
+
+// Activations in LDS, the matvec layout: xs[nsbp][kXs] words, per block of 32 its d, d * sum
+// (Q4_K), sum (Q6_K) and the sum of its first 16 values (Q6_K).
+struct Act {
+    int* xs;
+    float* dx;
+    float* dsum;
+    int* isum;
+    int* s16;
+    __device__ Act(int* base, int nsbp) {
+        xs = base;
+        dx = reinterpret_cast<float*>(xs + nsbp * kXs);
+        dsum = dx + nsbp * 8;
+        isum = reinterpret_cast<int*>(dsum + nsbp * 8);
+        s16 = isum + nsbp * 8;
+    }
+    static constexpr int ints(int nsbp) { return nsbp * (kXs + 32); }
+};
+
+// Staging is split in two: the global loads into registers (issued before the weights' loads,
+// so that waiting for them does not wait for the weights: the load counter drains in order),
+// then the LDS work. Up to four 16-byte words per thread per array; the launchers check the fit.
+// Loads are unconditional (clamped index): on this GPU a load under a branch gets a wait of its
+// own, and each wait costs a memory round trip of about a microsecond.
+typedef int i32x4 __attribute__((ext_vector_type(4)));  // (HIP's int4 struct copies through the stack)
+struct StageRegs {
+    i32x4 v[4];
+    i32x4 u[4];
+};
+
+// x and w (the norm weight), n / 4 float4 each.
+__device__ __forceinline__ void loadNorm(StageRegs& r, const float* x, const float* w, int n) {
+    const int tid = threadIdx.x, nth = blockDim.x, n4 = n / 4;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int i = min(u * nth + tid, n4 - 1);
+        r.v[u] = reinterpret_cast<const i32x4*>(x)[i];
+        r.u[u] = reinterpret_cast<const i32x4*>(w)[i];
+    }
+}
+
+// A per-32 slot: nsb * 16 int4 of words, nsb * 4 int4 of (d, sum) pairs.
+__device__ __forceinline__ void loadSlot(StageRegs& r, const int* xq, const float* xd, int nsb) {
+    const int tid = threadIdx.x, nth = blockDim.x, n4 = nsb * 16;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) r.v[u] = reinterpret_cast<const i32x4*>(xq)[min(u * nth + tid, n4 - 1)];
+    r.u[0] = reinterpret_cast<const i32x4*>(xd)[min(tid, nsb * 4 - 1)];
+    r.u[1] = r.u[2] = r.u[3] = i32x4{0, 0, 0, 0};
+}
+
+// From a per-32 slot (xq words, xd = d, sum pairs). raw: LDS scratch of nsb * 16 floats and a
+// dummy 16-byte word after them, the target of out-of-range stores: the stores are unconditional
+// so that the compiler keeps their loads together at the top.
+__device__ __forceinline__ void stageSlot(const Act& A, float* raw, const StageRegs& r, int nsb, int nsbp) {
+    const int tid = threadIdx.x, nth = blockDim.x, n4 = nsb * 16;
+    i32x4* dummy = reinterpret_cast<i32x4*>(raw + nsb * 16);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {  // xs rows are kXs = 68 ints apart: 16 words of 16 B per super-block
+        const int i = u * nth + tid;
+        i32x4* dst = i < n4 ? reinterpret_cast<i32x4*>(A.xs + (i >> 4) * kXs + (i & 15) * 4) : dummy;
+        *dst = r.v[u];
+    }
+    *(tid < nsb * 4 ? reinterpret_cast<i32x4*>(raw) + tid : dummy) = r.u[0];
+    for (int i = nsb * 64 + tid; i < nsbp * 64; i += nth) A.xs[(i >> 6) * kXs + (i & 63)] = 0;
+    __syncthreads();
+    for (int b = tid; b < nsbp * 8; b += nth) {
+        float d = 0.0f, sm = 0.0f;
+        int a = 0;
+        if (b < nsb * 8) {
+            d = raw[2 * b];
+            sm = raw[2 * b + 1];
+            const int* xw = A.xs + (b >> 3) * kXs + (b & 7) * 8;
+            for (int w = 0; w < 4; ++w) a = dot4(0x01010101, xw[w], a);
+        }
+        A.dx[b] = d;
+        A.dsum[b] = d * sm;
+        A.isum[b] = (int)sm;
+        A.s16[b] = a;
+    }
+}
+
+// From the residual row x: per-32 sums of squares in order (sumsq_part.cu / add_sumsq_f.cu),
+// their total in order, r = 1 / sqrt(total / n + eps), y = x * r * w and its per-32
+// quantization (norm_mul_q8_f.cu). Scratch (LDS): xf = x and wf = w in blocks of 32 values
+// 33 floats apart (nb * 33 each), ss (nb), then 4 dummy floats (unconditional stores).
+__device__ __forceinline__ void stageNorm(const Act& A, float* xf, float* wf, float* ss, const StageRegs& st, int n, float eps,
+                          int nsbp) {
+    const int tid = threadIdx.x, nth = blockDim.x;
+    const int nb = n / 32, n4 = n / 4;
+    float* dummy = ss + nsbp * 8;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int i = u * nth + tid;
+        float* o = i < n4 ? xf + (i >> 3) * 33 + (i & 7) * 4 : dummy;
+        float* ow = i < n4 ? wf + (i >> 3) * 33 + (i & 7) * 4 : dummy;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            // (an element is copied out first: __builtin_bit_cast of a vector element lvalue
+            // reads element 0 with this compiler)
+            const int xe = st.v[u][e], we = st.u[u][e];
+            o[e] = __builtin_bit_cast(float, xe);
+            ow[e] = __builtin_bit_cast(float, we);
+        }
+    }
+    __syncthreads();
+    for (int b = tid; b < nb; b += nth) {
+        float s = 0.0f;
+        for (int i = 0; i < 32; ++i) {
+            const float v = xf[b * 33 + i];
+            s += v * v;
+        }
+        ss[b] = s;
+    }
+    __syncthreads();
+    float tot = 0.0f;
+    for (int j = 0; j < nb; ++j) tot += ss[j];
+    const float r = 1.0f / sqrtf(tot / (float)n + eps);
+    for (int b = tid; b < nsbp * 8; b += nth) {
+        float y[32];
+#pragma unroll
+        for (int i = 0; i < 32; ++i) y[i] = b < nb ? xf[b * 33 + i] * r * wf[b * 33 + i] : 0.0f;
+        const Q32 q = quant32Seq(y);
+        int4* xw = reinterpret_cast<int4*>(A.xs + (b >> 3) * kXs + (b & 7) * 8);
+        xw[0] = make_int4(q.w[0], q.w[1], q.w[2], q.w[3]);
+        xw[1] = make_int4(q.w[4], q.w[5], q.w[6], q.w[7]);
+        A.dx[b] = q.d;
+        A.dsum[b] = q.d * (float)q.sum;
+        A.isum[b] = q.sum;
+        A.s16[b] = q.s16;
+    }
+}
+
+// LDS floats the staging needs beyond Act: stageNorm xf + wf + ss, stageSlot raw.
+__host__ __device__ constexpr int stageFloats(int pro, int nsbp) {
+    return pro == kProNorm ? 2 * nsbp * 8 * 33 + nsbp * 8 + 4 : nsbp * 16 + 4;
+}
+
+// The workgroup's tile slots: for a plain matvec TPW tiles of one part; for SwiGLU TPW tiles of
+// the gate (part 0) then the same TPW tiles of the up projection (part 1).
+struct Slot {
+    const uint8_t* qw;
+    int tile, live;
+};
+
+template <int EPI>
+__device__ __forceinline__ Slot slotOf(const DmvArgs& a, int part, int j) {
+    Slot s;
+    if (EPI == kEpiSwiglu) {
+        const bool up = j >= a.tpw;
+        s.qw = static_cast<const uint8_t*>(up ? a.p1.qw : a.p0.qw);
+        s.tile = blockIdx.x * a.tpw + (up ? j - a.tpw : j);
+        s.live = s.tile < a.p0.tiles;
+    } else {
+        const DmvPart& p = part == 2 ? a.p2 : (part == 1 ? a.p1 : a.p0);
+        s.qw = static_cast<const uint8_t*>(p.qw);
+        s.tile = (blockIdx.x - p.wg0) * a.tpw + j;
+        s.live = s.tile < p.tiles;
+    }
+    return s;
+}
+
+// Items of the workgroup: (slot j, group g), item i -> j = i % NS, g = i / NS; wave w takes
+// items w, w + nw, ...; each writes its lanes' per-super-block terms to LDS in super-block order.
+template <bool Q6, int EPI>
+__device__ __forceinline__ void dmvItems(const DmvArgs& a, int part, const Act& A, float* terms, int ns,
+                                         Pieces<Q6, true>& first, bool first_live) {
+    constexpr int kSeg = Q6 ? kQ6kSeg : kQ4kSeg;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int kq = lane >> 4, r = lane & 15;
+    const int ngroups = a.ngroups, ntmax = 2 * ngroups * kGroupSb;
+    const int nitems = ns * ngroups;
+    Pieces<Q6, true> cur = first;
+    bool cur_live = first_live;
+    for (int i = wave; i < nitems; i += nw) {
+        const int in = i + nw;
+        Pieces<Q6, true> nxt;
+        bool nxt_live = false;
+        if (in < nitems) {
+            const Slot sn = slotOf<EPI>(a, part, in % ns);
+            nxt_live = sn.live;
+            if (nxt_live) nxt.load(sn.qw + ((size_t)sn.tile * ngroups + in / ns) * kSeg, lane);
+        }
+        if (cur_live) {
+            const int j = i % ns, g = i / ns;
+            const int s = g * kGroupSb + kq;
+            const uint32_t* c = reinterpret_cast<const uint32_t*>(cur.c);
+            float* tt = terms + j * ntmax * 16;
+            if (Q6) {
+                float t0, t1;
+                q6k_terms(c, cur.dbits, A.xs + s * kXs, A.dx + 8 * s, A.isum + 8 * s, A.s16 + 8 * s, &t0, &t1);
+                tt[(2 * s) * 16 + r] = t0;
+                tt[(2 * s + 1) * 16 + r] = t1;
+            } else {
+                tt[s * 16 + r] = q4k_term(c, A.xs + s * kXs, A.dx + 8 * s, A.dsum + 8 * s);
+            }
+        }
+        cur = nxt;
+        cur_live = nxt_live;
+    }
+}
+
+template <int PRO, int EPI>
+__global__ __launch_bounds__(512) void dmv_kernel(DmvArgs a) {
+    extern __shared__ int4 lds4[];
+    int* lds = reinterpret_cast<int*>(lds4);
+    const int nsbp = a.ngroups * kGroupSb;
+    const int ntmax = 2 * nsbp;
+    const int ns = EPI == kEpiSwiglu ? 2 * a.tpw : a.tpw;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    Act A(lds, nsbp);
+    float* terms = reinterpret_cast<float*>(lds + Act::ints(nsbp));
+    float* extra = terms + ns * ntmax * 16;  // norm scratch, or the SwiGLU row values
+    int part = 0;
+    if (EPI != kEpiSwiglu) {
+        if (a.nparts > 2 && (int)blockIdx.x >= a.p2.wg0) part = 2;
+        else if (a.nparts > 1 && (int)blockIdx.x >= a.p1.wg0) part = 1;
+    }
+    const DmvPart& P = part == 2 ? a.p2 : (part == 1 ? a.p1 : a.p0);
+    const bool q6 = P.q6 != 0;
+
+    // Loads in order: the residual row value, the activations, then the first item's weights.
+    bool row_ok = false;
+    int row = 0;
+    float y_old = 0.0f;
+    if (EPI != kEpiSwiglu && tid < ns * 16) {
+        const Slot s = slotOf<EPI>(a, part, tid >> 4);
+        row = s.tile * kTileRows + (tid & 15);
+        row_ok = s.live && row < P.rows;
+        if (EPI == kEpiResid) y_old = P.y[row_ok ? row : 0];
+    }
+    StageRegs st;
+    if (PRO == kProNorm) loadNorm(st, a.x, a.nw, a.k);
+    else loadSlot(st, a.xq, a.xd, a.k / 256);
+    // The first item (wave < nw <= items always): 13 slabs and a Q6_K d read for either type
+    // with no branch (a Q4_K segment rereads its last slab, and its d address is slab 0), so the
+    // staging below waits for its own loads only. A dead tile reads tile 0.
+    Pieces<true, true> f6;
+    Pieces<false, true> f4;
+    bool first_live;
+    {
+        const Slot s0 = slotOf<EPI>(a, part, wave % ns);
+        first_live = s0.live;
+        const int seg = q6 ? kQ6kSeg : kQ4kSeg, nsl = q6 ? kQ6kSlabs : kQ4kSlabs;
+        const uint8_t* p0 = s0.qw + ((size_t)(s0.live ? s0.tile : 0) * a.ngroups + wave / ns) * seg;
+#pragma unroll
+        for (int i = 0; i < kQ6kSlabs; ++i)
+            f6.c[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p0 + min(i, nsl - 1) * 1024 + lane * 16));
+        f6.dbits = *reinterpret_cast<const uint16_t*>(p0 + (q6 ? kQ6kSlabs * 1024 + lane * 2 : 0));
+#pragma unroll
+        for (int i = 0; i < kQ4kSlabs; ++i) f4.c[i] = f6.c[i];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (PRO == kProNorm) stageNorm(A, extra, extra + nsbp * 8 * 33, extra + 2 * nsbp * 8 * 33, st, a.k, a.eps, nsbp);
+    else stageSlot(A, extra, st, a.k / 256, nsbp);
+    __syncthreads();
+    if (q6) dmvItems<true, EPI>(a, part, A, terms, ns, f6, first_live);
+    else dmvItems<false, EPI>(a, part, A, terms, ns, f4, first_live);
+    __syncthreads();
+
+    const int nreal = q6 ? 2 * (a.k / 256) : a.k / 256;
+    if (tid < ns * 16) {  // one thread per output row (the launcher keeps ns * 16 <= threads)
+        const int j = tid >> 4, r = tid & 15;
+        const float* tt = terms + j * ntmax * 16;
+        float acc = 0.0f;
+        for (int u = 0; u < nreal; ++u) acc += tt[u * 16 + r];
+        if (EPI == kEpiSwiglu) {
+            extra[tid] = acc;
+        } else if (row_ok) {
+            if (EPI == kEpiResid) P.y[row] = y_old + acc;
+            else P.y[row] = acc;
+        }
+    }
+    if (EPI == kEpiSwiglu) {
+        // silu(gate) * up for the workgroup's TPW * 16 rows (one lane each), then one thread per
+        // block of 32 quantizes it (silu_mul_q8x4f.cu).
+        __syncthreads();
+        const int nrow = a.tpw * kTileRows;
+        float* vb = extra + 2 * nrow;  // blocks of 32 values, 33 floats apart
+        if (tid < nrow) vb[(tid >> 5) * 33 + (tid & 31)] = silu(extra[tid]) * extra[nrow + tid];
+        __syncthreads();
+        const int b = tid, bg = blockIdx.x * (nrow / 32) + b;
+        if (b < nrow / 32 && bg < a.p0.rows / 32) storeQ32(a.qout, a.p0.rows / 32, bg, quant32Seq(vb + b * 33));
+    }
+}
+
+// ---------------------------------------------------------------- standalone norm + quantization
+
+// add_sumsq (sums only) + norm_mul_q8 of one row into a per-32 slot [nb*8 words | nb*2 floats |
+// nb floats: the sums of squares].
+__global__ __launch_bounds__(512) void rms_q8_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                     int* __restrict__ slot, int n, float eps) {
+    extern __shared__ int4 lds4[];
+    int* lds = reinterpret_cast<int*>(lds4);
+    const int nsbp = (n / 256 + kGroupSb - 1) / kGroupSb * kGroupSb;
+    Act A(lds, nsbp);
+    float* xf = reinterpret_cast<float*>(lds + Act::ints(nsbp));
+    float* wf = xf + nsbp * 8 * 33;
+    float* ss = wf + nsbp * 8 * 33;
+    StageRegs st;
+    loadNorm(st, x, w, n);
+    stageNorm(A, xf, wf, ss, st, n, eps, nsbp);
+    __syncthreads();
+    const int nb = n / 32;
+    for (int i = threadIdx.x; i < nb * 8; i += blockDim.x) slot[i] = A.xs[(i >> 6) * kXs + (i & 63)];
+    float* xd = reinterpret_cast<float*>(slot + nb * 8);
+    for (int b = threadIdx.x; b < nb; b += blockDim.x) {
+        xd[2 * b] = A.dx[b];
+        xd[2 * b + 1] = (float)A.isum[b];
+        xd[2 * nb + b] = ss[b];
+    }
+}
+
+// ---------------------------------------------------------------- q / k post-processing
+
+// One wavefront per head: workgroups [0, H) are query heads, [H, H + Hkv) key heads,
+// [H + Hkv, H + 2 Hkv) value heads. q / k: optional per-head RMS norm (rms_norm.cu: sequential
+// sum of squares), then ggml RoPE at position pos[0] (rope_ggml.cu); q into qr (f32), k and v
+// converted to fp16 into row pos[0] of the caches.
+__global__ __launch_bounds__(64) void qk_post_kernel(QkPostArgs a) {
+    __shared__ float hv[256];
+    __shared__ float out[256];
+    const int h = blockIdx.x, lane = threadIdx.x;
+    const int D = a.D, pairs = D / 2;
+    const float* src;
+    const float* nw = nullptr;
+    int kind, hh;  // kind 0 q, 1 k, 2 v; hh the head within its kind
+    if (h < a.H) {
+        kind = 0, hh = h, nw = a.q_norm;
+        src = a.q + (size_t)hh * D;
+    } else if (h < a.H + a.Hkv) {
+        kind = 1, hh = h - a.H, nw = a.k_norm;
+        src = a.k + (size_t)hh * D;
+    } else {
+        kind = 2, hh = h - a.H - a.Hkv;
+        src = a.v + (size_t)hh * D;
+    }
+    const bool norm = kind < 2 && a.qk_norm;
+    // every global load first: position, the head's values, norm weights, frequency factors
+    const int p = a.pos[0];
+    float xv[4], wv[4], fv[2];
+    const float* nwp = norm ? nw : src;  // unconditional, in-range loads; unused values ignored
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int i = min(lane + 64 * u, D - 1);
+        xv[u] = src[i];
+        wv[u] = nwp[i];
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) fv[u] = a.ff[min(lane + 64 * u, pairs - 1)];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+        if (lane + 64 * u < D) hv[lane + 64 * u] = xv[u];
+    __syncthreads();
+    if (norm) {
+        float ss = 0.0f;
+        for (int j = 0; j < D; ++j) ss += hv[j] * hv[j];
+        const float r = 1.0f / sqrtf(ss / (float)D + a.eps);
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (lane + 64 * u < D) hv[lane + 64 * u] = hv[lane + 64 * u] * r * wv[u];
+        __syncthreads();
+    }
+    if (kind == 2) {
+        int* dst = a.vcache + (size_t)p * a.kv_row + (size_t)hh * pairs;
+        for (int j = lane; j < pairs; j += 64) dst[j] = (int)(f2h(hv[2 * j]) | (f2h(hv[2 * j + 1]) << 16));
+        return;
+    }
+    const int m1 = a.neox ? 1 : 2, m2 = a.neox ? pairs : 1;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int i = lane + 64 * u;
+        if (i < pairs) {
+            const float theta = (float)p * exp2f(-(float)i / (float)pairs * a.log2_base) / fv[u];
+            const float c = cosf(theta), s = sinf(theta);
+            const int o = i * m1;
+            const float x0 = hv[o], x1 = hv[o + m2];
+            out[o] = x0 * c - x1 * s;
+            out[o + m2] = x0 * s + x1 * c;
+        }
+    }
+    __syncthreads();
+    if (kind == 0) {
+        for (int i = lane; i < D; i += 64) a.qr[(size_t)hh * D + i] = out[i];
+    } else {
+        int* dst = a.kcache + (size_t)p * a.kv_row + (size_t)hh * pairs;
+        for (int j = lane; j < pairs; j += 64) dst[j] = (int)(f2h(out[2 * j]) | (f2h(out[2 * j + 1]) << 16));
+    }
+}
+
+// ---------------------------------------------------------------- split-context attention
+
+// Workgroup (chunk c, KV head g) of 256 threads: the G = H / Hkv query heads of g against
+// positions [64c, 64c + 64) of the context T = *n_ctx (FLASH_ATTN_EXT: s = scale q.k,
+// softmax, sum p v). Partial results (max, sum of exp, unnormalized output) go to part, which
+// attn_merge_kernel combines.
+// LP lanes hold one position's D values, 8 each (D = 8 LP).
+template <int D>
+__global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
+    constexpr int LP = D / 8;           // lanes per position
+    constexpr int PPI = 64 / LP;        // positions per wave instruction
+    constexpr int NI = (kChunk / 4) / PPI;  // instructions per wave (16 positions per wave)
+    __shared__ float sc[kMaxGroup][kChunk];
+    __shared__ float red[4][kMaxGroup * D];
+    __shared__ float mg[kMaxGroup], lg[kMaxGroup];
+    const int T = *a.n_ctx;
+    const int nch = (T + kChunk - 1) / kChunk;
+    const int c = blockIdx.x, kvh = blockIdx.y;
+    if (c >= nch) return;
+    const int G = a.G;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int sub = lane / LP, l = lane % LP;
+    const int t0 = c * kChunk + wave * 16;
+    // K rows: 16-byte pieces, all loads issued first
+    // Loads are unconditional (positions past T read row T - 1 and are masked below): a load
+    // under a branch gets its own wait, which would serialize them.
+    u32x4 kp[NI];
+#pragma unroll
+    for (int n = 0; n < NI; ++n) {
+        const int t = min(t0 + n * PPI + sub, T - 1);
+        kp[n] = *reinterpret_cast<const u32x4*>(a.kcache + (size_t)t * a.kv_row + (size_t)kvh * (D / 2) + l * 4);
+    }
+    float qv[kMaxGroup][8];
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; ++g) {
+        const float4* qp = reinterpret_cast<const float4*>(a.q + (size_t)(kvh * G + min(g, G - 1)) * D + l * 8);
+        const float4 lo = qp[0], hi = qp[1];
+        qv[g][0] = lo.x, qv[g][1] = lo.y, qv[g][2] = lo.z, qv[g][3] = lo.w;
+        qv[g][4] = hi.x, qv[g][5] = hi.y, qv[g][6] = hi.z, qv[g][7] = hi.w;
+    }
+#pragma unroll
+    for (int n = 0; n < NI; ++n) {
+        const int tl = wave * 16 + n * PPI + sub;
+        float kf[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            kf[2 * e] = h2f(kp[n][e] & 0xFFFFu);
+            kf[2 * e + 1] = h2f(kp[n][e] >> 16);
+        }
+#pragma unroll
+        for (int g = 0; g < kMaxGroup; ++g) {
+            if (g < G) {
+                float s = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) s += qv[g][e] * kf[e];
+#pragma unroll
+                for (int o = 1; o < LP; o <<= 1) s += __shfl_xor(s, o, LP);
+                if (l == 0) sc[g][tl] = c * kChunk + tl < T ? a.scale * s : -INFINITY;
+            }
+        }
+    }
+    // V rows, issued before the softmax
+    u32x4 vp[NI];
+#pragma unroll
+    for (int n = 0; n < NI; ++n) {
+        const int t = min(t0 + n * PPI + sub, T - 1);  // past T: p = 0 below
+        vp[n] = *reinterpret_cast<const u32x4*>(a.vcache + (size_t)t * a.kv_row + (size_t)kvh * (D / 2) + l * 4);
+    }
+    __syncthreads();
+    for (int g = wave; g < G; g += 4) {  // one wavefront per head: lane = position
+        const float s = sc[g][lane];
+        float m = s;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+        const float p = s == -INFINITY ? 0.0f : exp2f((s - m) * kLog2e);
+        float sum = p;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) sum += __shfl_xor(sum, o);
+        sc[g][lane] = p;
+        if (lane == 0) {
+            mg[g] = m;
+            lg[g] = sum;
+        }
+    }
+    __syncthreads();
+    float acc[kMaxGroup][8];
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
+#pragma unroll
+    for (int n = 0; n < NI; ++n) {
+        const int tl = wave * 16 + n * PPI + sub;
+        float vf[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            vf[2 * e] = h2f(vp[n][e] & 0xFFFFu);
+            vf[2 * e + 1] = h2f(vp[n][e] >> 16);
+        }
+#pragma unroll
+        for (int g = 0; g < kMaxGroup; ++g) {
+            if (g < G) {
+                const float p = sc[g][tl];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[g][e] += p * vf[e];
+            }
+        }
+    }
+    // reduce over the position slots of the wave, then over the four waves
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; ++g) {
+        if (g < G) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float v = acc[g][e];
+#pragma unroll
+                for (int o = LP; o < 64; o <<= 1) v += __shfl_xor(v, o);
+                acc[g][e] = v;
+            }
+            if (sub == 0)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) red[wave][g * D + l * 8 + e] = acc[g][e];
+        }
+    }
+    __syncthreads();
+    float* pp = a.part + ((size_t)kvh * a.max_chunks + c) * kMaxGroup * (D + 2);
+    for (int i = tid; i < G * D; i += 256) pp[(i / D) * (D + 2) + i % D] = red[0][i] + red[1][i] + red[2][i] + red[3][i];
+    if (tid < G) {
+        pp[tid * (D + 2) + D] = mg[tid];
+        pp[tid * (D + 2) + D + 1] = lg[tid];
+    }
+}
+
+// Merge of the chunk partials of KV head blockIdx.x (its G query heads), in chunk order with a
+// running max and rescaled sums, and the per-32 quantization of the outputs into the slot.
+template <int D>
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnDecodeArgs a) {
+    __shared__ float vb[kMaxGroup * D / 32 * 33];
+    const int T = *a.n_ctx;
+    const int nch = (T + kChunk - 1) / kChunk;
+    const int kvh = blockIdx.x, G = a.G, tid = threadIdx.x;
+    const float* base = a.part + (size_t)kvh * a.max_chunks * kMaxGroup * (D + 2);
+    for (int i = tid; i < G * D; i += 256) {
+        const int g = i / D, d = i % D;
+        float M = -INFINITY, L = 0.0f, O = 0.0f;
+        for (int c0 = 0; c0 < nch; c0 += 16) {
+            float mv[16], lv[16], ov[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {  // unconditional loads (chunks past nch reread the last)
+                const float* pc = base + ((size_t)min(c0 + u, nch - 1) * kMaxGroup + g) * (D + 2);
+                mv[u] = pc[D];
+                lv[u] = pc[D + 1];
+                ov[u] = pc[d];
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                if (c0 + u < nch) {
+                    if (mv[u] > M) {
+                        const float sc = exp2f((M - mv[u]) * kLog2e);
+                        L *= sc;
+                        O *= sc;
+                        M = mv[u];
+                    }
+                    const float f = exp2f((mv[u] - M) * kLog2e);
+                    L += lv[u] * f;
+                    O += ov[u] * f;
+                }
+            }
+        }
+        vb[(i >> 5) * 33 + (i & 31)] = O / L;
+    }
+    __syncthreads();
+    const int nbl = G * D / 32;
+    if (tid < nbl) storeQ32(a.slot, a.nq, kvh * nbl + tid, quant32Seq(vb + tid * 33));
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- launchers
+
+size_t dmvLds(int pro, int epi, int k, int tpw) {
+    const int nsbp = (k / 256 + kGroupSb - 1) / kGroupSb * kGroupSb;
+    const int ns = epi == kEpiSwiglu ? 2 * tpw : tpw;
+    size_t ints = (size_t)Act::ints(nsbp) + (size_t)ns * 2 * nsbp * 16;
+    size_t extra = stageFloats(pro, nsbp);
+    const size_t swi = (size_t)ns * kTileRows + (size_t)tpw * kTileRows / 32 * 33 + 33;
+    if (epi == kEpiSwiglu && extra < swi) extra = swi;
+    return 4 * (ints + extra);
+}
+
+int launchDecodeMatvec(int pro, int epi, DmvArgs a, hipStream_t s) {
+    a.ngroups = (a.k / 256 + kGroupSb - 1) / kGroupSb;
+    int wgs = 0;
+    if (epi == kEpiSwiglu) {
+        a.p0.tiles = tilesOf(a.p0.rows);
+        wgs = (a.p0.tiles + a.tpw - 1) / a.tpw;
+    } else {
+        DmvPart* ps[3] = {&a.p0, &a.p1, &a.p2};
+        for (int i = 0; i < a.nparts; ++i) {
+            ps[i]->tiles = tilesOf(ps[i]->rows);
+            ps[i]->wg0 = wgs;
+            wgs += (ps[i]->tiles + a.tpw - 1) / a.tpw;
+        }
+    }
+    const int ns = epi == kEpiSwiglu ? 2 * a.tpw : a.tpw;
+    int nw = ns * a.ngroups;
+    if (nw > 8) nw = 8;
+    if (ns * kTileRows > 64 * nw || ns > 8 || (epi == kEpiSwiglu && a.tpw % 2))
+        return fromHip(hipErrorInvalidValue, "decode matvec: tiles per workgroup");
+    const int nsb = a.k / 256, nth = 64 * nw;
+    if ((pro == kProNorm && a.k / 4 > 4 * nth) || (pro == kProSlot && (nsb * 16 > 4 * nth || nsb * 4 > nth)))
+        return fromHip(hipErrorInvalidValue, "decode matvec: activations exceed the staging registers");
+    const size_t lds = dmvLds(pro, epi, a.k, a.tpw);
+    if (lds > 65536) return fromHip(hipErrorInvalidValue, "decode matvec: activations exceed LDS");
+    const dim3 grid(wgs), block(64 * nw);
+#define KC_DMV(P, Q)                                                                                         \
+    if (pro == P && epi == Q) hipLaunchKernelGGL((dmv_kernel<P, Q>), grid, block, lds, s, a);
+    KC_DMV(kProSlot, kEpiStore)
+    KC_DMV(kProSlot, kEpiResid)
+    KC_DMV(kProNorm, kEpiStore)
+    KC_DMV(kProNorm, kEpiResid)
+    KC_DMV(kProNorm, kEpiSwiglu)
+    KC_DMV(kProSlot, kEpiSwiglu)
+#undef KC_DMV
+    return fromHip(hipGetLastError(), "decode matvec");
+}
+
+int launchRmsQ8(const float* x, const float* w, int* slot, int n, float eps, hipStream_t s) {
+    const int nsbp = (n / 256 + kGroupSb - 1) / kGroupSb * kGroupSb;
+    const size_t lds = 4 * ((size_t)Act::ints(nsbp) + stageFloats(kProNorm, nsbp));
+    const int threads = n <= 4096 ? 256 : 512;
+    if (lds > 65536 || n / 4 > 4 * threads) return fromHip(hipErrorInvalidValue, "rms_q8: row too long");
+    hipLaunchKernelGGL(rms_q8_kernel, dim3(1), dim3(threads), lds, s, x, w, slot, n, eps);
+    return fromHip(hipGetLastError(), "rms_q8");
+}
+
+int launchQkPost(const QkPostArgs& a, hipStream_t s) {
+    if (a.D > 256 || a.D % 2) return fromHip(hipErrorInvalidValue, "qk_post: head_dim");
+    hipLaunchKernelGGL(qk_post_kernel, dim3(a.H + 2 * a.Hkv), dim3(64), 0, s, a);
+    return fromHip(hipGetLastError(), "qk_post");
+}
+
+bool attnDecodeSupports(int D, int G) { return (D == 64 || D == 128) && G >= 1 && G <= kMaxGroup; }
+
+size_t attnDecodePartFloats(int Hkv, int max_ctx, int D) {
+    return (size_t)Hkv * ((max_ctx + kChunk - 1) / kChunk) * kMaxGroup * (D + 2);
+}
+
+int launchAttnDecode(AttnDecodeArgs a, int D, int Hkv, int max_ctx, hipStream_t s) {
+    if (!attnDecodeSupports(D, a.G)) return fromHip(hipErrorInvalidValue, "attn_decode: shape");
+    a.max_chunks = (max_ctx + kChunk - 1) / kChunk;
+    const dim3 grid(a.max_chunks, Hkv);
+    if (D == 128) {
+        hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL(attn_merge_kernel<128>, dim3(Hkv), dim3(256), 0, s, a);
+    } else {
+        hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL(attn_merge_kernel<64>, dim3(Hkv), dim3(256), 0, s, a);
+    }
+    return fromHip(hipGetLastError(), "attn_decode");
+}
+
+}  // namespace kcamd

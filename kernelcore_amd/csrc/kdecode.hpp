@@ -1,0 +1,71 @@
+// kdecode.hpp -- launchers of the fused single-token decode kernels (kdecode.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+
+namespace kcamd {
+
+// Prologue: where the matvec's activations come from.
+constexpr int kProSlot = 0;  // a per-32 slot (xq words, xd = d / sum pairs)
+constexpr int kProNorm = 1;  // RMS norm x weight of the residual row x, quantized per 32 in LDS
+// Epilogue: what happens to each output row.
+constexpr int kEpiStore = 0;   // y[row] = acc
+constexpr int kEpiResid = 1;   // y[row] += acc (the residual stream)
+constexpr int kEpiSwiglu = 2;  // part 0 = gate, part 1 = up: silu(g) * u quantized per 32 into qout
+
+// One weight matrix of a grouped matvec (device stream of kcamd::streamBytes layout).
+struct DmvPart {
+    const void* qw;
+    float* y;
+    int rows;
+    int q6;     // Q6_K (else Q4_K)
+    int tiles;  // set by the launcher
+    int wg0;    // first workgroup (set by the launcher)
+};
+
+struct DmvArgs {
+    DmvPart p0, p1, p2;
+    int nparts;
+    int k;        // input length, a multiple of 256, shared by the parts
+    int tpw;      // 16-row tiles per workgroup (per part for SwiGLU: 2 for whole blocks of 32)
+    int ngroups;  // set by the launcher
+    const float* x;   // kProNorm: residual row
+    const float* nw;  // kProNorm: norm weight
+    float eps;
+    const int* xq;    // kProSlot
+    const float* xd;  // kProSlot
+    int* qout;        // kEpiSwiglu: per-32 slot of p0.rows values
+};
+
+struct QkPostArgs {
+    const float *q, *k, *v;  // one token: [H * D], [Hkv * D], [Hkv * D]
+    float* qr;               // roped q
+    int *kcache, *vcache;    // fp16 pairs, kv_row words per position
+    const int* pos;          // pos[0]: the token's position (device)
+    const float* ff;         // RoPE frequency factors [D / 2]
+    const float *q_norm, *k_norm;
+    int H, Hkv, D, kv_row, qk_norm, neox;
+    float log2_base, eps;
+};
+
+struct AttnDecodeArgs {
+    const float* q;  // roped q of one token [H * D]
+    const int *kcache, *vcache;
+    const int* n_ctx;  // context length (device)
+    float* part;       // partial results, attnDecodePartFloats floats
+    int* slot;         // per-32 slot of the H * D outputs
+    int G, kv_row, max_chunks, nq;
+    float scale;
+};
+
+size_t dmvLds(int pro, int epi, int k, int tpw);
+int launchDecodeMatvec(int pro, int epi, DmvArgs a, hipStream_t s);
+int launchRmsQ8(const float* x, const float* w, int* slot, int n, float eps, hipStream_t s);
+int launchQkPost(const QkPostArgs& a, hipStream_t s);
+bool attnDecodeSupports(int D, int G);
+size_t attnDecodePartFloats(int Hkv, int max_ctx, int D);
+int launchAttnDecode(AttnDecodeArgs a, int D, int Hkv, int max_ctx, hipStream_t s);
+
+}  // namespace kcamd

@@ -17,6 +17,7 @@
 #include <vector>
 
 #include "internal.hpp"
+#include "kdecode.hpp"
 #include "kquant.hpp"
 #include "launch.hpp"
 #include "model_kernels.hpp"
@@ -62,6 +63,7 @@ struct kcModel_st {
     int *slotE32 = nullptr, *slotEK = nullptr, *slotQ32 = nullptr, *slotQK = nullptr, *slotF32 = nullptr,
         *slotFK = nullptr;
     int *tokens = nullptr, *pos = nullptr, *n_past = nullptr, *n_ctx = nullptr, *gen = nullptr, *step = nullptr;
+    float* attn_part = nullptr;  // split-context attention partials (fused decode)
     long long* idx = nullptr;
     int max_gen = 4096;
     int pos_host = 0;
@@ -236,6 +238,82 @@ int decodeStep(kcModel_st* m, hipStream_t s) {
     return headOne(m, m->x, s);
 }
 
+// The same step in seven launches per layer (kdecode.hip): norm + q/k/v matvecs, q/k norm + RoPE +
+// cache store, split-context attention, its merge + quantization, output projection + residual,
+// norm + gate/up + SwiGLU + quantization, down projection + residual.
+bool fusedDecode(const kcModel_st* m) {
+    const auto& c = m->c;
+    return kcamd::option("decode_path") != 1 && kcamd::attnDecodeSupports(c.head_dim, c.n_head / c.n_head_kv);
+}
+
+int decodeStepFused(kcModel_st* m, hipStream_t s) {
+    const auto& c = m->c;
+    const int E_ = c.n_embd, Q = c.n_head * c.head_dim, KV = c.n_head_kv * c.head_dim, F = c.n_ff;
+    KI_TRY(kcamd::launchPositions(m->n_past, 1, m->pos, m->idx, m->n_ctx, s));
+    KI_TRY(kcamd::launchGetRows(false, m->tok_embd, m->tokens, m->x, 1, E_, s));
+    for (int li = 0; li < c.n_layer; ++li) {
+        const Layer& l = m->L[li];
+        kcamd::DmvArgs qa{};
+        qa.p0 = {l.wq, m->q, Q, 0, 0, 0};
+        qa.p1 = {l.wk, m->k, KV, 0, 0, 0};
+        qa.p2 = {l.wv, m->v, KV, 1, 0, 0};
+        qa.nparts = 3;
+        qa.k = E_;
+        qa.tpw = 1;
+        qa.x = m->x;
+        qa.nw = l.attn_norm;
+        qa.eps = c.norm_eps;
+        KI_TRY(kcamd::launchDecodeMatvec(kcamd::kProNorm, kcamd::kEpiStore, qa, s));
+        if (kcamd::option("decode_path") == 2) {  // diagnostic: the unfused attention kernels
+            KI_TRY(qkNorm(m, l, 1, s));
+            KI_TRY(ropeQK(m, 1, s));
+            KI_TRY(kvStore(m, l, 1, s));
+            KI_TRY(attention(m, l, 1, s));
+            KI_TRY(kcamd::launchQuantizeQ8x4(m->att, m->slotQ32, reinterpret_cast<float*>(m->slotQ32 + Q / 32 * 8),
+                                             Q / 32, s));
+        } else {
+        kcamd::QkPostArgs pa{m->q, m->k, m->v, m->qr, l.kcache, l.vcache, m->pos, m->ones, l.q_norm, l.k_norm,
+                             c.n_head, c.n_head_kv, c.head_dim, KV / 2, c.qk_norm, c.rope_neox,
+                             std::log2(c.rope_theta), c.norm_eps};
+        KI_TRY(kcamd::launchQkPost(pa, s));
+        kcamd::AttnDecodeArgs aa{m->qr, l.kcache, l.vcache, m->n_ctx, m->attn_part, m->slotQ32,
+                                 c.n_head / c.n_head_kv, KV / 2, 0, Q / 32, 1.0f / std::sqrt((float)c.head_dim)};
+        KI_TRY(kcamd::launchAttnDecode(aa, c.head_dim, c.n_head_kv, c.max_ctx, s));
+        }
+        kcamd::DmvArgs oa{};
+        oa.p0 = {l.wo, m->x, E_, 0, 0, 0};
+        oa.nparts = 1;
+        oa.k = Q;
+        oa.tpw = 1;
+        oa.xq = m->slotQ32;
+        oa.xd = reinterpret_cast<const float*>(m->slotQ32 + Q / 32 * 8);
+        KI_TRY(kcamd::launchDecodeMatvec(kcamd::kProSlot, kcamd::kEpiResid, oa, s));
+        kcamd::DmvArgs fa{};
+        fa.p0 = {l.wg, nullptr, F, 0, 0, 0};
+        fa.p1 = {l.wu, nullptr, F, 0, 0, 0};
+        fa.nparts = 2;
+        fa.k = E_;
+        fa.tpw = 2;
+        fa.x = m->x;
+        fa.nw = l.ffn_norm;
+        fa.eps = c.norm_eps;
+        fa.qout = m->slotF32;
+        KI_TRY(kcamd::launchDecodeMatvec(kcamd::kProNorm, kcamd::kEpiSwiglu, fa, s));
+        kcamd::DmvArgs da{};
+        da.p0 = {l.wd, m->x, E_, 1, 0, 0};
+        da.nparts = 1;
+        da.k = F;
+        da.tpw = 1;
+        da.xq = m->slotF32;
+        da.xd = reinterpret_cast<const float*>(m->slotF32 + F / 32 * 8);
+        KI_TRY(kcamd::launchDecodeMatvec(kcamd::kProSlot, kcamd::kEpiResid, da, s));
+    }
+    KI_TRY(kcamd::launchRmsQ8(m->x, m->out_norm, m->slotE32, E_, c.norm_eps, s));
+    return matvec(true, m->output, m->slotE32, m->logits, c.n_vocab, E_, s);
+}
+
+int decodeAny(kcModel_st* m, hipStream_t s) { return fusedDecode(m) ? decodeStepFused(m, s) : decodeStep(m, s); }
+
 // n > 1 tokens (m->tokens[0..n)) at positions *n_past ..: per-256 slots and the matmuls.
 int batchStep(kcModel_st* m, int n, hipStream_t s) {
     const auto& c = m->c;
@@ -350,6 +428,7 @@ kcError_t kcModelCreate(const kcModelConfig* cfg, kcModel_t* out) noexcept {
     KM_A(m->gen, (size_t)m->max_gen);
     KM_A(m->step, 1);
     KM_A(m->ones, (size_t)c.head_dim / 2);
+    KM_A(m->attn_part, kcamd::attnDecodePartFloats(c.n_head_kv, c.max_ctx, c.head_dim));
     for (auto& l : m->L) {
         KM_A(l.kcache, (size_t)c.max_ctx * KV / 2);
         KM_A(l.vcache, (size_t)c.max_ctx * KV / 2);
@@ -461,7 +540,7 @@ kcError_t kcModelForward(kcModel_t m, const int* tokens, int n, float* logits) n
     KM_TRYE(syncModel(m));
     KM_TRYE(kcMemcpy(m->tokens, tokens, sizeof(int) * n, kc::CopyKind::HostToDevice));
     KM_TRYE(kcMemcpy(m->n_past, &m->pos_host, sizeof(int), kc::CopyKind::HostToDevice));
-    KM_TRY(n == 1 ? decodeStep(m, m->s) : batchStep(m, n, m->s));
+    KM_TRY(n == 1 ? decodeAny(m, m->s) : batchStep(m, n, m->s));
     KM_TRYE(syncModel(m));
     m->pos_host += n;
     if (logits) KM_TRYE(kcMemcpy(logits, m->logits, sizeof(float) * m->c.n_vocab, kc::CopyKind::DeviceToHost));
@@ -483,7 +562,7 @@ kcError_t kcModelGenerate(kcModel_t m, int steps, int* tokens_out) noexcept {
     KM_TRY(kcamd::launchArgmaxStep(m->logits, m->c.n_vocab, m->tokens, m->gen, m->step, nullptr, m->max_gen, m->s));
     if (!m->step_graph) {
         KM_TRYE(kcStreamBeginCapture(m->ks));
-        int e1 = decodeStep(m, m->s);
+        int e1 = decodeAny(m, m->s);
         if (!e1)
             e1 = kcamd::launchArgmaxStep(m->logits, m->c.n_vocab, m->tokens, m->gen, m->step, m->n_past, m->max_gen,
                                          m->s);

@@ -29,11 +29,14 @@ def shapes(cfg):
 
 
 class OracleModel:
-    def __init__(self, cfg, tensors):
-        """tensors[(id, layer)] = raw ggml bytes (uint8) or float32 arrays; global ids use layer -1."""
+    def __init__(self, cfg, tensors, threads=0):
+        """tensors[(id, layer)] = raw ggml bytes (uint8) or float32 arrays; global ids use layer -1.
+        threads > 0 runs the single-row matvecs with the OpenMP variants (the same per-row
+        arithmetic, rows split over threads) -- the bench's CPU baseline."""
         self.cfg = cfg
         self.t = tensors
         self.L = lib()
+        self.threads = threads
         self.pos = 0
         kvd = cfg["n_head_kv"] * cfg["head_dim"]
         self.kc = [np.zeros(cfg["max_ctx"] * kvd, np.uint16) for _ in range(cfg["n_layer"])]
@@ -47,9 +50,14 @@ class OracleModel:
         qt = shapes(self.cfg)[tid][0]
         nb = k // 32
         y = np.zeros(rows, np.float32)
-        fn = self.L.kco_matvec_q6k_q8 if qt == Q6K else self.L.kco_matvec_q4k_q8
-        fn(self.w(tid, layer), np.ascontiguousarray(slot[:nb * 8]), np.ascontiguousarray(slot[nb * 8:nb * 10].view(np.float32)),
-           y, rows, k)
+        xq = np.ascontiguousarray(slot[:nb * 8])
+        xd = np.ascontiguousarray(slot[nb * 8:nb * 10].view(np.float32))
+        if self.threads > 0:
+            fn = self.L.kco_matvec_q6k_q8_mt if qt == Q6K else self.L.kco_matvec_q4k_q8_mt
+            fn(self.w(tid, layer), xq, xd, y, rows, k, self.threads)
+        else:
+            fn = self.L.kco_matvec_q6k_q8 if qt == Q6K else self.L.kco_matvec_q4k_q8
+            fn(self.w(tid, layer), xq, xd, y, rows, k)
         return y
 
     def matmul(self, tid, layer, slots, rows, k, n):
@@ -139,8 +147,8 @@ class OracleModel:
         n = len(tokens)
         p0 = self.pos
         E, Q, KV = c["n_embd"], c["n_head"] * c["head_dim"], c["n_head_kv"] * c["head_dim"]
-        emb = dequant(self.L, "q4k", self.w(0), c["n_vocab"], E)
-        x = np.ascontiguousarray(emb[np.asarray(tokens)], np.float32)
+        emb = np.ascontiguousarray(self.w(0)).reshape(c["n_vocab"], -1)  # ggml rows of the embedding
+        x = np.concatenate([dequant(self.L, "q4k", emb[t], 1, E) for t in tokens]).astype(np.float32)
         eps = np.float32(c["norm_eps"])
         down = None
         if n == 1:

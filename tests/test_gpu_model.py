@@ -15,9 +15,9 @@ from tests.model_weights import random_weights
 pytestmark = pytest.mark.gpu
 
 LLAMA = dict(n_layer=2, n_embd=512, n_head=8, n_head_kv=2, head_dim=64, n_ff=1024, n_vocab=1024, norm_eps=1e-5,
-             rope_theta=500000.0, rope_neox=0, qk_norm=0, max_ctx=256, max_batch=64)
+             rope_theta=500000.0, rope_neox=0, qk_norm=0, max_ctx=256, max_batch=128)
 QWEN = dict(n_layer=2, n_embd=512, n_head=4, n_head_kv=2, head_dim=128, n_ff=768, n_vocab=1536, norm_eps=1e-6,
-            rope_theta=1000000.0, rope_neox=1, qk_norm=1, max_ctx=256, max_batch=64)
+            rope_theta=1000000.0, rope_neox=1, qk_norm=1, max_ctx=256, max_batch=128)
 
 
 def note(msg):
@@ -45,18 +45,24 @@ def build(cfg, seed):
     return m, OracleModel(cfg, w)
 
 
-@pytest.mark.parametrize("name,cfg", [("llama", LLAMA), ("qwen3", QWEN)])
-def test_model_prompt_decode_generate(name, cfg):
+# prompt lengths below 64 run the column-tiled matmul, 64 and above the MFMA matmul; the second
+# chunk continues the prompt at a nonzero position (causal attention over cache + chunk)
+@pytest.mark.parametrize("name,cfg,n_prompt,n_chunk", [("llama", LLAMA, 37, 0), ("qwen3", QWEN, 37, 0),
+                                                       ("llama", LLAMA, 100, 24), ("qwen3", QWEN, 90, 64)])
+def test_model_prompt_decode_generate(name, cfg, n_prompt, n_chunk):
     note(f"model {name}: building")
     m, o = build(cfg, 7)
     rng = np.random.default_rng(3)
-    prompt = rng.integers(0, cfg["n_vocab"], 37).astype(np.int32)
-    note(f"model {name}: prompt of {prompt.size}")
-    lg = m.forward(prompt)
-    lo = o.forward(prompt)
-    assert np.all(np.isfinite(lg))
-    assert rel_l2(lg, lo) < 1e-2, rel_l2(lg, lo)
-    note(f"model {name}: prompt rel L2 {rel_l2(lg, lo):.2e}")
+    prompt = rng.integers(0, cfg["n_vocab"], n_prompt + n_chunk).astype(np.int32)
+    note(f"model {name}: prompt of {n_prompt} + {n_chunk}")
+    for part in (prompt[:n_prompt], prompt[n_prompt:]):
+        if part.size == 0:
+            continue
+        lg = m.forward(part)
+        lo = o.forward(part)
+        assert np.all(np.isfinite(lg))
+        assert rel_l2(lg, lo) < 1e-2, rel_l2(lg, lo)
+        note(f"model {name}: chunk of {part.size} rel L2 {rel_l2(lg, lo):.2e}")
     for step in range(3):  # single tokens: the decode path
         t = int(rng.integers(0, cfg["n_vocab"]))
         lg = m.forward([t])
@@ -113,3 +119,61 @@ def test_model_argument_validation():
     with pytest.raises(kc.KcError):  # wrong size
         m.set_tensor("wv", 0, np.zeros(nbytes - 1, np.uint8))
     m.close()
+
+
+def test_model_3b_shape_two_layers():
+    """Two layers at the full Llama-3.2-3B widths (3072 / 24 heads / 8 KV heads / 8192 FFN / 128256
+    vocab): an 8-token prompt and two decode steps against the oracle."""
+    cfg = dict(n_layer=2, n_embd=3072, n_head=24, n_head_kv=8, head_dim=128, n_ff=8192, n_vocab=128256,
+               norm_eps=1e-5, rope_theta=500000.0, rope_neox=0, qk_norm=0, max_ctx=64, max_batch=16)
+    note("model 3b-shape: building")
+    m, o = build(cfg, 21)
+    prompt = np.random.default_rng(5).integers(0, cfg["n_vocab"], 8).astype(np.int32)
+    lg, lo = m.forward(prompt), o.forward(prompt)
+    assert rel_l2(lg, lo) < 1e-2, rel_l2(lg, lo)
+    note(f"model 3b-shape: prompt rel L2 {rel_l2(lg, lo):.2e}")
+    for _ in range(2):
+        t = int(np.argmax(lo))
+        lg, lo = m.forward([t]), o.forward([t])
+        assert rel_l2(lg, lo) < 1e-2, rel_l2(lg, lo)
+    m.close()
+
+
+@pytest.mark.parametrize("name,cfg", [("llama", LLAMA), ("qwen3", QWEN)])
+def test_model_unfused_decode_path(name, cfg):
+    """decode_path = 1 runs the one-kernel-per-reference-op decode step (add_sumsq, norm_mul_q8,
+    the matvecs, rope, set_rows, attention, quantize_q8x4, silu_mul_q8): same oracle bar."""
+    kc.set_option("decode_path", 1)
+    try:
+        m, o = build(cfg, 5)
+        prompt = np.arange(3, 3 + 21, dtype=np.int32)
+        lg, lo = m.forward(prompt), o.forward(prompt)
+        for _ in range(3):
+            t = int(np.argmax(lo))
+            lg, lo = m.forward([t]), o.forward([t])
+            assert rel_l2(lg, lo) < 1e-2, rel_l2(lg, lo)
+        gen = m.generate(4)
+        want = []
+        for _ in range(4):
+            want.append(int(np.argmax(lo)))
+            lo = o.forward([want[-1]])
+        assert list(gen) == want
+        m.close()
+    finally:
+        kc.set_option("decode_path", 0)
+
+
+def test_model_fused_matvecs_unfused_attention():
+    """decode_path = 2: the fused matvec kernels with the one-op-per-kernel attention."""
+    kc.set_option("decode_path", 2)
+    try:
+        m, o = build(LLAMA, 5)
+        prompt = np.arange(3, 3 + 21, dtype=np.int32)
+        lg, lo = m.forward(prompt), o.forward(prompt)
+        for _ in range(3):
+            t = int(np.argmax(lo))
+            lg, lo = m.forward([t]), o.forward([t])
+            assert rel_l2(lg, lo) < 1e-2, rel_l2(lg, lo)
+        m.close()
+    finally:
+        kc.set_option("decode_path", 0)
