@@ -1,12 +1,12 @@
 // kdecode.hip -- the single-token decode kernels of the model driver (gfx950).
 //
 // One token is latency-bound: every launch costs a few microseconds whatever it moves, so the
-// layer is cut into seven kernels instead of the reference graph's sixteen nodes:
+// layer is cut into six kernels instead of the reference graph's sixteen nodes:
 //   1. dmv (norm prologue): RMS norm x weight + per-32 quantization of the residual row, done by
 //      every workgroup into its own LDS, then the q / k / v matvecs in one grid;
-//   2. qk_post: per-head q / k RMS norm (Qwen3), RoPE, fp16 conversion of k and v into the cache;
-//   3. attn_decode + attn_merge: attention split over the context in chunks of 64 positions, then
-//      the merge of the partial softmaxes and the per-32 quantization of the output;
+//   2. attn_decode: per-head q / k RMS norm (Qwen3), RoPE, k and v into the fp16 cache, and the
+//      attention split over the context in chunks of 64 positions;
+//   3. attn_merge: the merge of the partial softmaxes and the per-32 quantization of the output;
 //   4. dmv (slot prologue, residual epilogue): attention output projection, x += o;
 //   5. dmv (norm prologue, SwiGLU epilogue): FFN norm, gate and up matvecs, silu(g) * u and its
 //      per-32 quantization;
@@ -61,28 +61,36 @@ struct Q32 {
     float d;
 };
 __device__ __forceinline__ Q32 quant32Seq(const float* y) {
-    Q32 o;
-    float amax = 0.0f;
+    // max and integer sums as balanced trees: both are exact, so the order does not matter and
+    // the dependency chains stay short
+    float m[16];
 #pragma unroll
-    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fmaxf(y[i], 0.0f - y[i]));
-    o.d = amax / 127.0f;
+    for (int i = 0; i < 16; ++i)
+        m[i] = fmaxf(fmaxf(y[i], 0.0f - y[i]), fmaxf(y[i + 16], 0.0f - y[i + 16]));
+#pragma unroll
+    for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+        for (int i = 0; i < w; ++i) m[i] = fmaxf(m[i], m[i + w]);
+    Q32 o;
+    o.d = fmaxf(0.0f, m[0]) / 127.0f;
     float id;
     if (o.d > 0.0f) id = 1.0f / o.d;
     else id = 0.0f;
-    int sum = 0;
+    int q[32];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        int word = 0;
+    for (int i = 0; i < 32; ++i) q[i] = q8r(y[i] * id);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = q8r(y[4 * k + i] * id);
-            sum += c;
-            word |= (c & 255) << (8 * i);
+    for (int k = 0; k < 8; ++k)
+        o.w[k] = (q[4 * k] & 255) | ((q[4 * k + 1] & 255) << 8) | ((q[4 * k + 2] & 255) << 16) | (q[4 * k + 3] << 24);
+#pragma unroll
+    for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+        for (int i = 0; i < w; ++i) {
+            q[i] += q[i + w];
+            q[16 + i] += q[16 + i + w];
         }
-        o.w[k] = word;
-        if (k == 3) o.s16 = sum;
-    }
-    o.sum = sum;
+    o.s16 = q[0];
+    o.sum = q[0] + q[16];
     return o;
 }
 
@@ -125,14 +133,17 @@ struct StageRegs {
     i32x4 u[4];
 };
 
-// x and w (the norm weight), n / 4 float4 each.
-__device__ __forceinline__ void loadNorm(StageRegs& r, const float* x, const float* w, int n) {
-    const int tid = threadIdx.x, nth = blockDim.x, n4 = n / 4;
+// The norm prologue holds block b = threadIdx.x (32 values of x and of w) in registers; the
+// launchers keep n / 32 <= threads.
+struct NormRegs {
+    i32x4 x[8], w[8];
+};
+__device__ __forceinline__ void loadNorm(NormRegs& r, const float* x, const float* w, int n) {
+    const int b = min((int)threadIdx.x, n / 32 - 1);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int i = min(u * nth + tid, n4 - 1);
-        r.v[u] = reinterpret_cast<const i32x4*>(x)[i];
-        r.u[u] = reinterpret_cast<const i32x4*>(w)[i];
+    for (int k = 0; k < 8; ++k) {
+        r.x[k] = reinterpret_cast<const i32x4*>(x)[b * 8 + k];
+        r.w[k] = reinterpret_cast<const i32x4*>(w)[b * 8 + k];
     }
 }
 
@@ -178,58 +189,73 @@ __device__ __forceinline__ void stageSlot(const Act& A, float* raw, const StageR
 
 // From the residual row x: per-32 sums of squares in order (sumsq_part.cu / add_sumsq_f.cu),
 // their total in order, r = 1 / sqrt(total / n + eps), y = x * r * w and its per-32
-// quantization (norm_mul_q8_f.cu). Scratch (LDS): xf = x and wf = w in blocks of 32 values
-// 33 floats apart (nb * 33 each), ss (nb), then 4 dummy floats (unconditional stores).
-__device__ __forceinline__ void stageNorm(const Act& A, float* xf, float* wf, float* ss, const StageRegs& st, int n, float eps,
-                          int nsbp) {
+// quantization (norm_mul_q8_f.cu), thread b on block b from registers. ss: LDS scratch of
+// nsbp * 8 floats (16-byte aligned); the blocks' sums of squares are also returned there.
+__device__ __forceinline__ void stageNorm(const Act& A, float* ss, const NormRegs& st, int n, float eps, int nsbp) {
     const int tid = threadIdx.x, nth = blockDim.x;
-    const int nb = n / 32, n4 = n / 4;
-    float* dummy = ss + nsbp * 8;
+    const int nb = n / 32;
+    float xv[32];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int i = u * nth + tid;
-        float* o = i < n4 ? xf + (i >> 3) * 33 + (i & 7) * 4 : dummy;
-        float* ow = i < n4 ? wf + (i >> 3) * 33 + (i & 7) * 4 : dummy;
+    for (int k = 0; k < 8; ++k)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            // (an element is copied out first: __builtin_bit_cast of a vector element lvalue
-            // reads element 0 with this compiler)
-            const int xe = st.v[u][e], we = st.u[u][e];
-            o[e] = __builtin_bit_cast(float, xe);
-            ow[e] = __builtin_bit_cast(float, we);
+            const int v = st.x[k][e];  // (copied out: bit_cast of a vector element reads element 0)
+            xv[4 * k + e] = __builtin_bit_cast(float, v);
         }
-    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) s += xv[i] * xv[i];
+    if (tid < nb) ss[tid] = s;
+    for (int b = nb + tid; b < nsbp * 8; b += nth) ss[b] = 0.0f;
     __syncthreads();
-    for (int b = tid; b < nb; b += nth) {
-        float s = 0.0f;
-        for (int i = 0; i < 32; ++i) {
-            const float v = xf[b * 33 + i];
-            s += v * v;
-        }
-        ss[b] = s;
-    }
-    __syncthreads();
+    // the total in block order; 16-byte reads, all issued before the adds. ss is zero from nb
+    // to the next multiple of 32 (inside nsbp * 8), and tot + 0 = tot (tot >= 0).
     float tot = 0.0f;
-    for (int j = 0; j < nb; ++j) tot += ss[j];
+    for (int j0 = 0; j0 < nb; j0 += 32) {
+        float4 q[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) q[k] = reinterpret_cast<const float4*>(ss + j0)[k];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            tot += q[k].x;
+            tot += q[k].y;
+            tot += q[k].z;
+            tot += q[k].w;
+        }
+    }
     const float r = 1.0f / sqrtf(tot / (float)n + eps);
-    for (int b = tid; b < nsbp * 8; b += nth) {
+    if (tid < nb) {
         float y[32];
 #pragma unroll
-        for (int i = 0; i < 32; ++i) y[i] = b < nb ? xf[b * 33 + i] * r * wf[b * 33 + i] : 0.0f;
+        for (int k = 0; k < 8; ++k)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int wv = st.w[k][e];
+                y[4 * k + e] = xv[4 * k + e] * r * __builtin_bit_cast(float, wv);
+            }
         const Q32 q = quant32Seq(y);
-        int4* xw = reinterpret_cast<int4*>(A.xs + (b >> 3) * kXs + (b & 7) * 8);
-        xw[0] = make_int4(q.w[0], q.w[1], q.w[2], q.w[3]);
-        xw[1] = make_int4(q.w[4], q.w[5], q.w[6], q.w[7]);
+        const int b = tid;
+        i32x4* xw = reinterpret_cast<i32x4*>(A.xs + (b >> 3) * kXs + (b & 7) * 8);
+        xw[0] = i32x4{q.w[0], q.w[1], q.w[2], q.w[3]};
+        xw[1] = i32x4{q.w[4], q.w[5], q.w[6], q.w[7]};
         A.dx[b] = q.d;
         A.dsum[b] = q.d * (float)q.sum;
         A.isum[b] = q.sum;
         A.s16[b] = q.s16;
     }
+    for (int b = nb + tid; b < nsbp * 8; b += nth) {  // padding blocks of the last group
+        i32x4* xw = reinterpret_cast<i32x4*>(A.xs + (b >> 3) * kXs + (b & 7) * 8);
+        xw[0] = xw[1] = i32x4{0, 0, 0, 0};
+        A.dx[b] = 0.0f;
+        A.dsum[b] = 0.0f;
+        A.isum[b] = 0;
+        A.s16[b] = 0;
+    }
 }
 
-// LDS floats the staging needs beyond Act: stageNorm xf + wf + ss, stageSlot raw.
+// LDS floats the staging needs beyond Act: stageNorm ss, stageSlot raw (+ its dummy word).
 __host__ __device__ constexpr int stageFloats(int pro, int nsbp) {
-    return pro == kProNorm ? 2 * nsbp * 8 * 33 + nsbp * 8 + 4 : nsbp * 16 + 4;
+    return pro == kProNorm ? nsbp * 8 : nsbp * 16 + 4;
 }
 
 // The workgroup's tile slots: for a plain matvec TPW tiles of one part; for SwiGLU TPW tiles of
@@ -281,14 +307,14 @@ __device__ __forceinline__ void dmvItems(const DmvArgs& a, int part, const Act& 
             const int j = i % ns, g = i / ns;
             const int s = g * kGroupSb + kq;
             const uint32_t* c = reinterpret_cast<const uint32_t*>(cur.c);
-            float* tt = terms + j * ntmax * 16;
+            float* tt = terms + (j * 16 + r) * (ntmax + 4);  // one row's terms, contiguous
             if (Q6) {
                 float t0, t1;
                 q6k_terms(c, cur.dbits, A.xs + s * kXs, A.dx + 8 * s, A.isum + 8 * s, A.s16 + 8 * s, &t0, &t1);
-                tt[(2 * s) * 16 + r] = t0;
-                tt[(2 * s + 1) * 16 + r] = t1;
+                tt[2 * s] = t0;
+                tt[2 * s + 1] = t1;
             } else {
-                tt[s * 16 + r] = q4k_term(c, A.xs + s * kXs, A.dx + 8 * s, A.dsum + 8 * s);
+                tt[s] = q4k_term(c, A.xs + s * kXs, A.dx + 8 * s, A.dsum + 8 * s);
             }
         }
         cur = nxt;
@@ -297,7 +323,7 @@ __device__ __forceinline__ void dmvItems(const DmvArgs& a, int part, const Act& 
 }
 
 template <int PRO, int EPI>
-__global__ __launch_bounds__(512) void dmv_kernel(DmvArgs a) {
+__global__ __launch_bounds__(EPI == kEpiSwiglu ? 768 : 512) void dmv_kernel(DmvArgs a) {
     extern __shared__ int4 lds4[];
     int* lds = reinterpret_cast<int*>(lds4);
     const int nsbp = a.ngroups * kGroupSb;
@@ -306,7 +332,7 @@ __global__ __launch_bounds__(512) void dmv_kernel(DmvArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     Act A(lds, nsbp);
     float* terms = reinterpret_cast<float*>(lds + Act::ints(nsbp));
-    float* extra = terms + ns * ntmax * 16;  // norm scratch, or the SwiGLU row values
+    float* extra = terms + ns * 16 * (ntmax + 4);  // norm scratch, or the SwiGLU row values
     int part = 0;
     if (EPI != kEpiSwiglu) {
         if (a.nparts > 2 && (int)blockIdx.x >= a.p2.wg0) part = 2;
@@ -326,7 +352,8 @@ __global__ __launch_bounds__(512) void dmv_kernel(DmvArgs a) {
         if (EPI == kEpiResid) y_old = P.y[row_ok ? row : 0];
     }
     StageRegs st;
-    if (PRO == kProNorm) loadNorm(st, a.x, a.nw, a.k);
+    NormRegs nr;
+    if (PRO == kProNorm) loadNorm(nr, a.x, a.nw, a.k);
     else loadSlot(st, a.xq, a.xd, a.k / 256);
     // The first item (wave < nw <= items always): 13 slabs and a Q6_K d read for either type
     // with no branch (a Q4_K segment rereads its last slab, and its d address is slab 0), so the
@@ -347,7 +374,7 @@ __global__ __launch_bounds__(512) void dmv_kernel(DmvArgs a) {
         for (int i = 0; i < kQ4kSlabs; ++i) f4.c[i] = f6.c[i];
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (PRO == kProNorm) stageNorm(A, extra, extra + nsbp * 8 * 33, extra + 2 * nsbp * 8 * 33, st, a.k, a.eps, nsbp);
+    if (PRO == kProNorm) stageNorm(A, extra, nr, a.k, a.eps, nsbp);
     else stageSlot(A, extra, st, a.k / 256, nsbp);
     __syncthreads();
     if (q6) dmvItems<true, EPI>(a, part, A, terms, ns, f6, first_live);
@@ -356,10 +383,23 @@ __global__ __launch_bounds__(512) void dmv_kernel(DmvArgs a) {
 
     const int nreal = q6 ? 2 * (a.k / 256) : a.k / 256;
     if (tid < ns * 16) {  // one thread per output row (the launcher keeps ns * 16 <= threads)
-        const int j = tid >> 4, r = tid & 15;
-        const float* tt = terms + j * ntmax * 16;
+        // the row's terms in super-block order; 16-byte reads, eight issued before their adds
+        const float4* tt = reinterpret_cast<const float4*>(terms + tid * (ntmax + 4));
+        const int n4 = ntmax / 4;
         float acc = 0.0f;
-        for (int u = 0; u < nreal; ++u) acc += tt[u * 16 + r];
+        for (int u0 = 0; u0 < nreal; u0 += 32) {
+            float4 q[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) q[k] = tt[min(u0 / 4 + k, n4 - 1)];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int u = u0 + 4 * k;
+                if (u < nreal) acc += q[k].x;
+                if (u + 1 < nreal) acc += q[k].y;
+                if (u + 2 < nreal) acc += q[k].z;
+                if (u + 3 < nreal) acc += q[k].w;
+            }
+        }
         if (EPI == kEpiSwiglu) {
             extra[tid] = acc;
         } else if (row_ok) {
@@ -390,12 +430,10 @@ __global__ __launch_bounds__(512) void rms_q8_kernel(const float* __restrict__ x
     int* lds = reinterpret_cast<int*>(lds4);
     const int nsbp = (n / 256 + kGroupSb - 1) / kGroupSb * kGroupSb;
     Act A(lds, nsbp);
-    float* xf = reinterpret_cast<float*>(lds + Act::ints(nsbp));
-    float* wf = xf + nsbp * 8 * 33;
-    float* ss = wf + nsbp * 8 * 33;
-    StageRegs st;
+    float* ss = reinterpret_cast<float*>(lds + Act::ints(nsbp));
+    NormRegs st;
     loadNorm(st, x, w, n);
-    stageNorm(A, xf, wf, ss, st, n, eps, nsbp);
+    stageNorm(A, ss, st, n, eps, nsbp);
     __syncthreads();
     const int nb = n / 32;
     for (int i = threadIdx.x; i < nb * 8; i += blockDim.x) slot[i] = A.xs[(i >> 6) * kXs + (i & 63)];
@@ -407,132 +445,125 @@ __global__ __launch_bounds__(512) void rms_q8_kernel(const float* __restrict__ x
     }
 }
 
-// ---------------------------------------------------------------- q / k post-processing
-
-// One wavefront per head: workgroups [0, H) are query heads, [H, H + Hkv) key heads,
-// [H + Hkv, H + 2 Hkv) value heads. q / k: optional per-head RMS norm (rms_norm.cu: sequential
-// sum of squares), then ggml RoPE at position pos[0] (rope_ggml.cu); q into qr (f32), k and v
-// converted to fp16 into row pos[0] of the caches.
-__global__ __launch_bounds__(64) void qk_post_kernel(QkPostArgs a) {
-    __shared__ float hv[256];
-    __shared__ float out[256];
-    const int h = blockIdx.x, lane = threadIdx.x;
-    const int D = a.D, pairs = D / 2;
-    const float* src;
-    const float* nw = nullptr;
-    int kind, hh;  // kind 0 q, 1 k, 2 v; hh the head within its kind
-    if (h < a.H) {
-        kind = 0, hh = h, nw = a.q_norm;
-        src = a.q + (size_t)hh * D;
-    } else if (h < a.H + a.Hkv) {
-        kind = 1, hh = h - a.H, nw = a.k_norm;
-        src = a.k + (size_t)hh * D;
-    } else {
-        kind = 2, hh = h - a.H - a.Hkv;
-        src = a.v + (size_t)hh * D;
-    }
-    const bool norm = kind < 2 && a.qk_norm;
-    // every global load first: position, the head's values, norm weights, frequency factors
-    const int p = a.pos[0];
-    float xv[4], wv[4], fv[2];
-    const float* nwp = norm ? nw : src;  // unconditional, in-range loads; unused values ignored
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int i = min(lane + 64 * u, D - 1);
-        xv[u] = src[i];
-        wv[u] = nwp[i];
-    }
-#pragma unroll
-    for (int u = 0; u < 2; ++u) fv[u] = a.ff[min(lane + 64 * u, pairs - 1)];
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-        if (lane + 64 * u < D) hv[lane + 64 * u] = xv[u];
-    __syncthreads();
-    if (norm) {
-        float ss = 0.0f;
-        for (int j = 0; j < D; ++j) ss += hv[j] * hv[j];
-        const float r = 1.0f / sqrtf(ss / (float)D + a.eps);
-        __syncthreads();
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-            if (lane + 64 * u < D) hv[lane + 64 * u] = hv[lane + 64 * u] * r * wv[u];
-        __syncthreads();
-    }
-    if (kind == 2) {
-        int* dst = a.vcache + (size_t)p * a.kv_row + (size_t)hh * pairs;
-        for (int j = lane; j < pairs; j += 64) dst[j] = (int)(f2h(hv[2 * j]) | (f2h(hv[2 * j + 1]) << 16));
-        return;
-    }
-    const int m1 = a.neox ? 1 : 2, m2 = a.neox ? pairs : 1;
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int i = lane + 64 * u;
-        if (i < pairs) {
-            const float theta = (float)p * exp2f(-(float)i / (float)pairs * a.log2_base) / fv[u];
-            const float c = cosf(theta), s = sinf(theta);
-            const int o = i * m1;
-            const float x0 = hv[o], x1 = hv[o + m2];
-            out[o] = x0 * c - x1 * s;
-            out[o + m2] = x0 * s + x1 * c;
-        }
-    }
-    __syncthreads();
-    if (kind == 0) {
-        for (int i = lane; i < D; i += 64) a.qr[(size_t)hh * D + i] = out[i];
-    } else {
-        int* dst = a.kcache + (size_t)p * a.kv_row + (size_t)hh * pairs;
-        for (int j = lane; j < pairs; j += 64) dst[j] = (int)(f2h(out[2 * j]) | (f2h(out[2 * j + 1]) << 16));
-    }
-}
-
 // ---------------------------------------------------------------- split-context attention
 
-// Workgroup (chunk c, KV head g) of 256 threads: the G = H / Hkv query heads of g against
-// positions [64c, 64c + 64) of the context T = *n_ctx (FLASH_ATTN_EXT: s = scale q.k,
-// softmax, sum p v). Partial results (max, sum of exp, unnormalized output) go to part, which
-// attn_merge_kernel combines.
+// Sums over the 16 (or 8) lanes of a DPP row group with row-local DPP moves (no LDS traffic):
+// pairs, quads, mirrored halves of 8, mirrored halves of 16; every lane ends with the total.
+template <int CTRL>
+__device__ __forceinline__ float dppMove(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+template <int LANES>
+__device__ __forceinline__ float dppSum(float v) {
+    v += dppMove<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+    v += dppMove<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+    v += dppMove<0x141>(v);  // row_half_mirror
+    if (LANES == 16) v += dppMove<0x140>(v);  // row_mirror
+    return v;
+}
+
+// Workgroup (chunk c, KV head g) of 256 threads: the attention of one token at position p = pos[0]
+// against positions [64c, 64c + 64) of the context T = p + 1 (FLASH_ATTN_EXT: s = scale q.k,
+// softmax, sum p v) for the G = H / Hkv query heads of g. Each workgroup first normalizes
+// (Qwen3, rms_norm.cu) and ropes (rope_ggml.cu) its query heads; the workgroup of the last chunk
+// does the same for k, stores k and v as fp16 into cache row p (set_rows_f16.cu) and takes
+// position p from LDS, the others read positions below p from the cache. Partial results (max,
+// sum of exp, unnormalized output) go to part, which attn_merge_kernel combines.
 // LP lanes hold one position's D values, 8 each (D = 8 LP).
 template <int D>
 __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
     constexpr int LP = D / 8;           // lanes per position
     constexpr int PPI = 64 / LP;        // positions per wave instruction
     constexpr int NI = (kChunk / 4) / PPI;  // instructions per wave (16 positions per wave)
+    constexpr int pairs = D / 2;
     __shared__ float sc[kMaxGroup][kChunk];
     __shared__ float red[4][kMaxGroup * D];
     __shared__ float mg[kMaxGroup], lg[kMaxGroup];
-    const int T = *a.n_ctx;
+    __shared__ float qs[kMaxGroup * D];
+    __shared__ float raw[(kMaxGroup + 2) * D];
+    __shared__ float nwl[2 * D];
+    __shared__ float kn[D], vn[D], rn[kMaxGroup + 1];
+    const QkPostArgs& q = a.qp;
+    const int p = q.pos[0], T = p + 1;
     const int nch = (T + kChunk - 1) / kChunk;
     const int c = blockIdx.x, kvh = blockIdx.y;
     if (c >= nch) return;
+    const bool last = c == nch - 1;
     const int G = a.G;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int sub = lane / LP, l = lane % LP;
     const int t0 = c * kChunk + wave * 16;
-    // K rows: 16-byte pieces, all loads issued first
-    // Loads are unconditional (positions past T read row T - 1 and are masked below): a load
-    // under a branch gets its own wait, which would serialize them.
-    u32x4 kp[NI];
+    // Every global load first, unconditional (clamped rows; position p and rows past it are
+    // replaced or masked below): a load under a branch gets a wait of its own.
+    const int tmax = max(p - 1, 0);
+    u32x4 kp[NI], vp[NI];
 #pragma unroll
     for (int n = 0; n < NI; ++n) {
-        const int t = min(t0 + n * PPI + sub, T - 1);
-        kp[n] = *reinterpret_cast<const u32x4*>(a.kcache + (size_t)t * a.kv_row + (size_t)kvh * (D / 2) + l * 4);
+        const size_t row = (size_t)min(t0 + n * PPI + sub, tmax) * q.kv_row + (size_t)kvh * pairs + l * 4;
+        kp[n] = *reinterpret_cast<const u32x4*>(q.kcache + row);
+        vp[n] = *reinterpret_cast<const u32x4*>(q.vcache + row);
     }
+    for (int i = tid; i < (G + 2) * D; i += 256) {
+        const float* src = i < G * D ? q.q + (size_t)kvh * G * D + i
+                                     : (i < (G + 1) * D ? q.k + (size_t)kvh * D + (i - G * D)
+                                                        : q.v + (size_t)kvh * D + (i - (G + 1) * D));
+        raw[i] = *src;
+    }
+    if (tid < 2 * D) {
+        const float* nw = q.qk_norm ? (tid < D ? q.q_norm + tid : q.k_norm + tid - D) : q.q + (tid % D);
+        nwl[tid] = *nw;
+    }
+    __syncthreads();
+    if (q.qk_norm) {
+        if (tid <= G) {  // heads 0..G-1: q, head G: k; sequential sums as rms_norm.cu
+            float ss = 0.0f;
+            for (int j = 0; j < D; ++j) ss += raw[tid * D + j] * raw[tid * D + j];
+            rn[tid] = 1.0f / sqrtf(ss / (float)D + q.eps);
+        }
+        __syncthreads();
+        for (int i = tid; i < (G + 1) * D; i += 256) {
+            const int h = i / D, e = i % D;
+            raw[i] = raw[i] * rn[h] * nwl[(h < G ? 0 : D) + e];
+        }
+        __syncthreads();
+    }
+    const int m1 = q.neox ? 1 : 2, m2 = q.neox ? pairs : 1;
+    for (int i = tid; i < (G + 1) * pairs; i += 256) {
+        const int h = i / pairs, j = i % pairs;
+        const float theta = (float)p * exp2f(-(float)j / (float)pairs * q.log2_base) / q.ff[j];
+        const float cs = cosf(theta), sn = sinf(theta);
+        const int o = j * m1;
+        const float x0 = raw[h * D + o], x1 = raw[h * D + o + m2];
+        const float y0 = x0 * cs - x1 * sn, y1 = x0 * sn + x1 * cs;
+        if (h < G) {
+            qs[h * D + o] = y0;
+            qs[h * D + o + m2] = y1;
+        } else {
+            kn[o] = h2f(f2h(y0));
+            kn[o + m2] = h2f(f2h(y1));
+        }
+    }
+    for (int e = tid; e < D; e += 256) vn[e] = h2f(f2h(raw[(G + 1) * D + e]));
+    __syncthreads();
+    if (last)
+        for (int j = tid; j < pairs; j += 256) {
+            const size_t w = (size_t)p * q.kv_row + (size_t)kvh * pairs + j;
+            q.kcache[w] = (int)(f2h(kn[2 * j]) | (f2h(kn[2 * j + 1]) << 16));
+            q.vcache[w] = (int)(f2h(vn[2 * j]) | (f2h(vn[2 * j + 1]) << 16));
+        }
     float qv[kMaxGroup][8];
 #pragma unroll
-    for (int g = 0; g < kMaxGroup; ++g) {
-        const float4* qp = reinterpret_cast<const float4*>(a.q + (size_t)(kvh * G + min(g, G - 1)) * D + l * 8);
-        const float4 lo = qp[0], hi = qp[1];
-        qv[g][0] = lo.x, qv[g][1] = lo.y, qv[g][2] = lo.z, qv[g][3] = lo.w;
-        qv[g][4] = hi.x, qv[g][5] = hi.y, qv[g][6] = hi.z, qv[g][7] = hi.w;
-    }
+    for (int g = 0; g < kMaxGroup; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qv[g][e] = qs[min(g, G - 1) * D + l * 8 + e];
 #pragma unroll
     for (int n = 0; n < NI; ++n) {
-        const int tl = wave * 16 + n * PPI + sub;
+        const int tl = wave * 16 + n * PPI + sub, t = c * kChunk + tl;
         float kf[8];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            kf[2 * e] = h2f(kp[n][e] & 0xFFFFu);
-            kf[2 * e + 1] = h2f(kp[n][e] >> 16);
+            kf[2 * e] = t == p ? kn[l * 8 + 2 * e] : h2f(kp[n][e] & 0xFFFFu);
+            kf[2 * e + 1] = t == p ? kn[l * 8 + 2 * e + 1] : h2f(kp[n][e] >> 16);
         }
 #pragma unroll
         for (int g = 0; g < kMaxGroup; ++g) {
@@ -540,18 +571,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
                 float s = 0.0f;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) s += qv[g][e] * kf[e];
-#pragma unroll
-                for (int o = 1; o < LP; o <<= 1) s += __shfl_xor(s, o, LP);
-                if (l == 0) sc[g][tl] = c * kChunk + tl < T ? a.scale * s : -INFINITY;
+                s = dppSum<LP>(s);
+                if (l == 0) sc[g][tl] = t < T ? a.scale * s : -INFINITY;
             }
         }
-    }
-    // V rows, issued before the softmax
-    u32x4 vp[NI];
-#pragma unroll
-    for (int n = 0; n < NI; ++n) {
-        const int t = min(t0 + n * PPI + sub, T - 1);  // past T: p = 0 below
-        vp[n] = *reinterpret_cast<const u32x4*>(a.vcache + (size_t)t * a.kv_row + (size_t)kvh * (D / 2) + l * 4);
     }
     __syncthreads();
     for (int g = wave; g < G; g += 4) {  // one wavefront per head: lane = position
@@ -559,11 +582,11 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
         float m = s;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
-        const float p = s == -INFINITY ? 0.0f : exp2f((s - m) * kLog2e);
-        float sum = p;
+        const float pr = s == -INFINITY ? 0.0f : exp2f((s - m) * kLog2e);
+        float sum = pr;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) sum += __shfl_xor(sum, o);
-        sc[g][lane] = p;
+        sc[g][lane] = pr;
         if (lane == 0) {
             mg[g] = m;
             lg[g] = sum;
@@ -577,19 +600,19 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
         for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
 #pragma unroll
     for (int n = 0; n < NI; ++n) {
-        const int tl = wave * 16 + n * PPI + sub;
+        const int tl = wave * 16 + n * PPI + sub, t = c * kChunk + tl;
         float vf[8];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            vf[2 * e] = h2f(vp[n][e] & 0xFFFFu);
-            vf[2 * e + 1] = h2f(vp[n][e] >> 16);
+            vf[2 * e] = t == p ? vn[l * 8 + 2 * e] : h2f(vp[n][e] & 0xFFFFu);
+            vf[2 * e + 1] = t == p ? vn[l * 8 + 2 * e + 1] : h2f(vp[n][e] >> 16);
         }
 #pragma unroll
         for (int g = 0; g < kMaxGroup; ++g) {
             if (g < G) {
-                const float p = sc[g][tl];
+                const float pr = sc[g][tl];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) acc[g][e] += p * vf[e];
+                for (int e = 0; e < 8; ++e) acc[g][e] += pr * vf[e];
             }
         }
     }
@@ -623,7 +646,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
 template <int D>
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnDecodeArgs a) {
     __shared__ float vb[kMaxGroup * D / 32 * 33];
-    const int T = *a.n_ctx;
+    const int T = a.qp.pos[0] + 1;
     const int nch = (T + kChunk - 1) / kChunk;
     const int kvh = blockIdx.x, G = a.G, tid = threadIdx.x;
     const float* base = a.part + (size_t)kvh * a.max_chunks * kMaxGroup * (D + 2);
@@ -661,6 +684,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnDecodeArgs a) {
     if (tid < nbl) storeQ32(a.slot, a.nq, kvh * nbl + tid, quant32Seq(vb + tid * 33));
 }
 
+
 }  // namespace
 
 // ---------------------------------------------------------------- launchers
@@ -668,7 +692,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnDecodeArgs a) {
 size_t dmvLds(int pro, int epi, int k, int tpw) {
     const int nsbp = (k / 256 + kGroupSb - 1) / kGroupSb * kGroupSb;
     const int ns = epi == kEpiSwiglu ? 2 * tpw : tpw;
-    size_t ints = (size_t)Act::ints(nsbp) + (size_t)ns * 2 * nsbp * 16;
+    size_t ints = (size_t)Act::ints(nsbp) + (size_t)ns * 16 * (2 * nsbp + 4);
     size_t extra = stageFloats(pro, nsbp);
     const size_t swi = (size_t)ns * kTileRows + (size_t)tpw * kTileRows / 32 * 33 + 33;
     if (epi == kEpiSwiglu && extra < swi) extra = swi;
@@ -691,11 +715,11 @@ int launchDecodeMatvec(int pro, int epi, DmvArgs a, hipStream_t s) {
     }
     const int ns = epi == kEpiSwiglu ? 2 * a.tpw : a.tpw;
     int nw = ns * a.ngroups;
-    if (nw > 8) nw = 8;
+    if (nw > (epi == kEpiSwiglu ? 12 : 8)) nw = epi == kEpiSwiglu ? 12 : 8;
     if (ns * kTileRows > 64 * nw || ns > 8 || (epi == kEpiSwiglu && a.tpw % 2))
         return fromHip(hipErrorInvalidValue, "decode matvec: tiles per workgroup");
     const int nsb = a.k / 256, nth = 64 * nw;
-    if ((pro == kProNorm && a.k / 4 > 4 * nth) || (pro == kProSlot && (nsb * 16 > 4 * nth || nsb * 4 > nth)))
+    if ((pro == kProNorm && a.k / 32 > nth) || (pro == kProSlot && (nsb * 16 > 4 * nth || nsb * 4 > nth)))
         return fromHip(hipErrorInvalidValue, "decode matvec: activations exceed the staging registers");
     const size_t lds = dmvLds(pro, epi, a.k, a.tpw);
     if (lds > 65536) return fromHip(hipErrorInvalidValue, "decode matvec: activations exceed LDS");
@@ -715,16 +739,10 @@ int launchDecodeMatvec(int pro, int epi, DmvArgs a, hipStream_t s) {
 int launchRmsQ8(const float* x, const float* w, int* slot, int n, float eps, hipStream_t s) {
     const int nsbp = (n / 256 + kGroupSb - 1) / kGroupSb * kGroupSb;
     const size_t lds = 4 * ((size_t)Act::ints(nsbp) + stageFloats(kProNorm, nsbp));
-    const int threads = n <= 4096 ? 256 : 512;
-    if (lds > 65536 || n / 4 > 4 * threads) return fromHip(hipErrorInvalidValue, "rms_q8: row too long");
+    const int threads = n <= 8192 ? 256 : 512;
+    if (lds > 65536 || n / 32 > threads) return fromHip(hipErrorInvalidValue, "rms_q8: row too long");
     hipLaunchKernelGGL(rms_q8_kernel, dim3(1), dim3(threads), lds, s, x, w, slot, n, eps);
     return fromHip(hipGetLastError(), "rms_q8");
-}
-
-int launchQkPost(const QkPostArgs& a, hipStream_t s) {
-    if (a.D > 256 || a.D % 2) return fromHip(hipErrorInvalidValue, "qk_post: head_dim");
-    hipLaunchKernelGGL(qk_post_kernel, dim3(a.H + 2 * a.Hkv), dim3(64), 0, s, a);
-    return fromHip(hipGetLastError(), "qk_post");
 }
 
 bool attnDecodeSupports(int D, int G) { return (D == 64 || D == 128) && G >= 1 && G <= kMaxGroup; }
@@ -748,3 +766,4 @@ int launchAttnDecode(AttnDecodeArgs a, int D, int Hkv, int max_ctx, hipStream_t 
 }
 
 }  // namespace kcamd
+

@@ -41,7 +41,7 @@ struct DmvArgs {
 
 struct QkPostArgs {
     const float *q, *k, *v;  // one token: [H * D], [Hkv * D], [Hkv * D]
-    float* qr;               // roped q
+    float* qr;               // (unused by the fused attention)
     int *kcache, *vcache;    // fp16 pairs, kv_row words per position
     const int* pos;          // pos[0]: the token's position (device)
     const float* ff;         // RoPE frequency factors [D / 2]
@@ -51,19 +51,17 @@ struct QkPostArgs {
 };
 
 struct AttnDecodeArgs {
-    const float* q;  // roped q of one token [H * D]
-    const int *kcache, *vcache;
-    const int* n_ctx;  // context length (device)
-    float* part;       // partial results, attnDecodePartFloats floats
-    int* slot;         // per-32 slot of the H * D outputs
-    int G, kv_row, max_chunks, nq;
+    QkPostArgs qp;  // the token's q, k, v (before RoPE), caches, position, RoPE / norm parameters
+    float* part;    // partial results, attnDecodePartFloats floats
+    int* slot;      // per-32 slot of the H * D outputs
+    int G, max_chunks, nq;
     float scale;
 };
 
 size_t dmvLds(int pro, int epi, int k, int tpw);
+
 int launchDecodeMatvec(int pro, int epi, DmvArgs a, hipStream_t s);
 int launchRmsQ8(const float* x, const float* w, int* slot, int n, float eps, hipStream_t s);
-int launchQkPost(const QkPostArgs& a, hipStream_t s);
 bool attnDecodeSupports(int D, int G);
 size_t attnDecodePartFloats(int Hkv, int max_ctx, int D);
 int launchAttnDecode(AttnDecodeArgs a, int D, int Hkv, int max_ctx, hipStream_t s);

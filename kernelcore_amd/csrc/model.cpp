@@ -275,9 +275,8 @@ int decodeStepFused(kcModel_st* m, hipStream_t s) {
         kcamd::QkPostArgs pa{m->q, m->k, m->v, m->qr, l.kcache, l.vcache, m->pos, m->ones, l.q_norm, l.k_norm,
                              c.n_head, c.n_head_kv, c.head_dim, KV / 2, c.qk_norm, c.rope_neox,
                              std::log2(c.rope_theta), c.norm_eps};
-        KI_TRY(kcamd::launchQkPost(pa, s));
-        kcamd::AttnDecodeArgs aa{m->qr, l.kcache, l.vcache, m->n_ctx, m->attn_part, m->slotQ32,
-                                 c.n_head / c.n_head_kv, KV / 2, 0, Q / 32, 1.0f / std::sqrt((float)c.head_dim)};
+        kcamd::AttnDecodeArgs aa{pa, m->attn_part, m->slotQ32, c.n_head / c.n_head_kv, 0, Q / 32,
+                                 1.0f / std::sqrt((float)c.head_dim)};
         KI_TRY(kcamd::launchAttnDecode(aa, c.head_dim, c.n_head_kv, c.max_ctx, s));
         }
         kcamd::DmvArgs oa{};

@@ -177,3 +177,17 @@ def test_model_fused_matvecs_unfused_attention():
         m.close()
     finally:
         kc.set_option("decode_path", 0)
+
+
+def test_model_long_context_split_attention():
+    """A cache too large for the one-workgroup attention's LDS scores (max_ctx 12288 with 4 query
+    heads per KV head) takes the split-context attention and its merge kernel."""
+    cfg = dict(LLAMA, n_layer=1, max_ctx=12288)
+    m, o = build(cfg, 9)
+    prompt = np.arange(40, 40 + 70, dtype=np.int32)  # 70 positions: two chunks of 64
+    lg, lo = m.forward(prompt), o.forward(prompt)
+    for _ in range(3):
+        t = int(np.argmax(lo))
+        lg, lo = m.forward([t]), o.forward([t])
+        assert rel_l2(lg, lo) < 1e-2, rel_l2(lg, lo)
+    m.close()
