@@ -200,6 +200,151 @@ __global__ void positions_kernel(const int* __restrict__ n_past, int n, int* pos
     if (i == 0) *n_ctx = p0 + n;
 }
 
+
+// Causal attention of a batch of N queries (positions p0 .. p0 + N - 1, p0 = T - N, T = *n_ctx)
+// on the matrix cores, v_mfma_f32_32x32x16_f16. Workgroup (query tile of 32, KV head) with one
+// wavefront per query head of the group. Pass 1 finds each query's maximum score over its keys,
+// pass 2 forms p = exp(s - max), its sum, and sum p V; the output is divided by the sum at the
+// end, so the softmax is FLASH_ATTN_EXT's exact one. k and v are fp16 in the cache; q and p are
+// each split into two fp16 operands, hi = fp16(x) and lo = fp16(x - hi), and every product runs as
+// two MFMAs, which keeps them within about 2^-22 of fp32 (one fp16 rounding of q or p would be
+// 2^-11: enough to flip the 8-bit quantization of the attention output downstream). p is scaled
+// by 2^10 before the split so that lo stays in fp16's normal range; the sum is divided back.
+// Scores are computed transposed, S^T = K Q^T (A = K rows from the cache, B = q as fp16 in
+// registers), which leaves each lane one query and 16 of the 32 keys of a block: lane (j, h)
+// holds keys 8a + 4h + b (value 4a + b). Those registers are directly the A operand of P V when
+// the MFMA's k index runs over the keys in that order, kappa(k) = {0,1,2,3,8,9,10,11 |
+// 4,5,6,7,12,13,14,15} (+16 for the second half of the block); the B operand (V) is read in the
+// same key order from a transposed copy of the V block in LDS.
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <int D, int G>
+__global__ __launch_bounds__(64 * G) void attn_prefill_kernel(const float* __restrict__ q, const int* __restrict__ kc,
+                                                              const int* __restrict__ vc, float* __restrict__ out,
+                                                              const int* __restrict__ n_ctx, AttnShape a) {
+    constexpr int KS = D / 16, DB = D / 32;
+    constexpr int kVtStride = 40;  // halves per transposed V row (32 keys + 8 pad)
+    __shared__ _Float16 vt[D * kVtStride];
+    __shared__ float lsum[G][32];
+    const int T = *n_ctx, N = a.N, p0 = T - N;
+    const int i0 = blockIdx.x * 32, kvh = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5;
+    const int head = kvh * G + wave;
+    const int* kb0 = kc + (size_t)kvh * (D / 2);
+    const int* vb0 = vc + (size_t)kvh * (D / 2);
+    // q of this lane's query as the B operand (hi and lo parts): d = 16 ks + 8 h .. + 7
+    h8 qb[KS], ql[KS];
+    {
+        const bool live = i0 + j < N;
+        const float* qp = q + (size_t)min(i0 + j, N - 1) * a.q_tok + (size_t)head * D + 8 * h;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const float4 lo = *reinterpret_cast<const float4*>(qp + 16 * ks);
+            const float4 hi = *reinterpret_cast<const float4*>(qp + 16 * ks + 4);
+            const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float x = live ? v[e] : 0.0f;
+                const _Float16 hi = (_Float16)x;
+                qb[ks][e] = hi;
+                ql[ks][e] = (_Float16)(x - (float)hi);
+            }
+        }
+    }
+    const int qpos = p0 + i0 + j;
+    const int nkb = min(p0 + i0 + 31, T - 1) / 32 + 1;
+    f32x16 zero;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) zero[v] = 0.0f;
+    auto scores = [&](int kb) {
+        const int key = min(kb * 32 + j, T - 1);
+        const int* kr = kb0 + (size_t)key * a.kv_row + 4 * h;
+        h8 ka[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) ka[ks] = *reinterpret_cast<const h8*>(kr + 8 * ks);
+        f32x16 sacc = zero;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks], qb[ks], sacc, 0, 0, 0);
+            sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks], ql[ks], sacc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int key_abs = kb * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+            sacc[v] = key_abs <= qpos && key_abs < T ? a.scale * sacc[v] : -INFINITY;
+        }
+        return sacc;
+    };
+    // ---- pass 1: the maximum score of each query
+    float m = -INFINITY;
+    for (int kb = 0; kb < nkb; ++kb) {
+        const f32x16 sacc = scores(kb);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) m = fmaxf(m, sacc[v]);
+    }
+    m = fmaxf(m, __shfl_xor(m, 32));
+    // ---- pass 2: p = exp(s - m), its sum, and sum p V
+    f32x16 o[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) o[db] = zero;
+    float l = 0.0f;
+    for (int kb = 0; kb < nkb; ++kb) {
+        __syncthreads();  // the previous block's V reads are done
+        for (int c = threadIdx.x; c < 32 * (D / 8); c += 64 * G) {  // V block, transposed into LDS
+            const int kk = c / (D / 8), d0 = (c % (D / 8)) * 8;
+            const int key = kb * 32 + kk;
+            const uint4 w = *reinterpret_cast<const uint4*>(vb0 + (size_t)min(key, T - 1) * a.kv_row + d0 / 2);
+            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t wv = key < T ? ws[e] : 0u;  // keys past T: zeros (their p is 0)
+                vt[(d0 + 2 * e) * kVtStride + kk] = __builtin_bit_cast(_Float16, (unsigned short)(wv & 0xFFFFu));
+                vt[(d0 + 2 * e + 1) * kVtStride + kk] = __builtin_bit_cast(_Float16, (unsigned short)(wv >> 16));
+            }
+        }
+        const f32x16 sacc = scores(kb);
+        h8 pa[2], pl[2];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const float pv = sacc[v] == -INFINITY ? 0.0f : exp2f((sacc[v] - m) * kLog2e);
+            l += pv;
+            const float ps = pv * 1024.0f;
+            const _Float16 hi = (_Float16)ps;
+            pa[v >> 3][v & 7] = hi;
+            pl[v >> 3][v & 7] = (_Float16)(ps - (float)hi);
+        }
+        __syncthreads();  // V block staged
+#pragma unroll
+        for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                const _Float16* vr = vt + (32 * db + j) * kVtStride + 16 * mm + 4 * h;
+                h8 vbv;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    vbv[e] = vr[e];
+                    vbv[4 + e] = vr[8 + e];
+                }
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[mm], vbv, o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pl[mm], vbv, o[db], 0, 0, 0);
+            }
+    }
+    l += __shfl_xor(l, 32);
+    if (h == 0) lsum[wave][j] = l;
+    __syncthreads();
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const int qi = 8 * (v >> 2) + 4 * h + (v & 3);
+        if (i0 + qi < N) {
+            const float inv = 1.0f / (lsum[wave][qi] * 1024.0f);
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+                out[(size_t)(i0 + qi) * a.q_tok + (size_t)head * D + 32 * db + j] = o[db][v] * inv;
+        }
+    }
+}
+
 }  // namespace
 
 int launchGetRows(bool q6k, const void* qw, const int* tok, float* y, int n, int k, hipStream_t s) {
@@ -210,8 +355,24 @@ int launchGetRows(bool q6k, const void* qw, const int* tok, float* y, int n, int
     return fromHip(hipGetLastError(), "get_rows");
 }
 
+template <int D, int G>
+static int runPrefill(const float* q, const int* k, const int* v, float* out, const int* n_ctx, const AttnShape& a,
+                      hipStream_t s) {
+    const dim3 grid((a.N + 31) / 32, a.H_kv);
+    hipLaunchKernelGGL((attn_prefill_kernel<D, G>), grid, dim3(64 * G), 0, s, q, k, v, out, n_ctx, a);
+    return fromHip(hipGetLastError(), "attn (prefill)");
+}
+
 int launchAttn(const float* q, const int* k, const int* v, float* out, const int* n_ctx, const AttnShape& a,
                hipStream_t s) {
+    const int G = a.H / a.H_kv;
+    if (a.N > 1 && a.causal && option("attn_path") != 1) {  // the matrix-core prefill attention
+#define KC_AP(DD, GG) \
+        if (a.D == DD && G == GG) return runPrefill<DD, GG>(q, k, v, out, n_ctx, a, s);
+        KC_AP(128, 1) KC_AP(128, 2) KC_AP(128, 3) KC_AP(128, 4) KC_AP(128, 8)
+        KC_AP(64, 1) KC_AP(64, 2) KC_AP(64, 3) KC_AP(64, 4) KC_AP(64, 8)
+#undef KC_AP
+    }
     const size_t lds = sizeof(float) * ((size_t)a.max_t + 256 + 64);
     static const int attr = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(attn_kernel),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
