@@ -51,39 +51,6 @@ __device__ __forceinline__ void quant32(const float* yb, int* qw, float* xd2) {
     xd2[1] = (float)sum;
 }
 
-// One super-block of 256 values of y into a per-256 slot of nsb super-blocks (quantize_cols_k.cu).
-__device__ __forceinline__ void quant256(const float* yb, int* qc, int nsb, int s) {
-    float amax = 0.0f;
-    for (int i = 0; i < 256; ++i) amax = fmaxf(amax, fmaxf(yb[i], 0.0f - yb[i]));
-    const float d = amax / 127.0f;
-    float id;
-    if (d > 0.0f) id = 1.0f / d;
-    else id = 0.0f;
-    int b16[16];
-    for (int g = 0; g < 16; ++g) {
-        int sum = 0;
-        for (int k = 0; k < 4; ++k) {
-            int word = 0;
-            for (int i = 0; i < 4; ++i) {
-                const int c = q8r(yb[16 * g + 4 * k + i] * id);
-                sum += c;
-                word |= (c & 255) << (8 * i);
-            }
-            qc[s * 64 + g * 4 + k] = word;
-        }
-        qc[nsb * 65 + s * 16 + g] = sum;
-        b16[g] = sum;
-    }
-    int pw[4] = {0, 0, 0, 0};
-    for (int i = 0; i < 8; ++i) {
-        const int b = b16[2 * i] + b16[2 * i + 1];
-        pw[i >> 2] |= ((b >> 6) & 255) << (8 * (i & 3));
-        pw[2 + (i >> 2)] |= (b & 63) << (8 * (i & 3));
-    }
-    for (int i = 0; i < 4; ++i) qc[nsb * 81 + s * 4 + i] = pw[i];
-    reinterpret_cast<float*>(qc + nsb * 64)[s] = d;
-}
-
 __device__ __forceinline__ float rmsScale(const float* ss, int nb, int n, float eps) {
     float tot = 0.0f;
     for (int j = 0; j < nb; ++j) tot += ss[j];
@@ -92,30 +59,105 @@ __device__ __forceinline__ float rmsScale(const float* ss, int nb, int n, float 
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + exp2f(-g * kLog2e)); }
 
+// ---------------------------------------------------------------- wavefront helpers
+
+template <int CTRL>
+__device__ __forceinline__ int dppI(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+template <int CTRL>
+__device__ __forceinline__ float dppF(float v) {
+    return __builtin_bit_cast(float, dppI<CTRL>(__builtin_bit_cast(int, v)));
+}
+__device__ __forceinline__ float laneF(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+// The maximum over the wavefront (every lane gets it): within rows of 16 by DPP (pairs, quads,
+// mirrored halves), then the four rows' results read back as scalars.
+__device__ __forceinline__ float waveMax(float v) {
+    v = fmaxf(v, dppF<0xB1>(v));
+    v = fmaxf(v, dppF<0x4E>(v));
+    v = fmaxf(v, dppF<0x141>(v));
+    v = fmaxf(v, dppF<0x140>(v));
+    return fmaxf(fmaxf(laneF(v, 0), laneF(v, 16)), fmaxf(laneF(v, 32), laneF(v, 48)));
+}
+
+// One super-block of 256 values, four per lane (lane L holds values 4L .. 4L + 3), into a
+// per-256 slot of nsb super-blocks (quantize_cols_k.cu / quant256 above): the same values, the
+// max and the integer sums taken across lanes (both exact in any order).
+__device__ __forceinline__ void quant256Wave(float y0, float y1, float y2, float y3, int* qc, int nsb, int s) {
+    const int lane = threadIdx.x & 63;
+    float am = fmaxf(fmaxf(fmaxf(y0, 0.0f - y0), fmaxf(y1, 0.0f - y1)), fmaxf(fmaxf(y2, 0.0f - y2), fmaxf(y3, 0.0f - y3)));
+    am = waveMax(am);
+    const float d = fmaxf(0.0f, am) / 127.0f;
+    float id;
+    if (d > 0.0f) id = 1.0f / d;
+    else id = 0.0f;
+    const int c0 = q8r(y0 * id), c1 = q8r(y1 * id), c2 = q8r(y2 * id), c3 = q8r(y3 * id);
+    qc[s * 64 + lane] = (c0 & 255) | ((c1 & 255) << 8) | ((c2 & 255) << 16) | ((c3 & 255) << 24);
+    int s16 = c0 + c1 + c2 + c3;
+    s16 += dppI<0xB1>(s16);
+    s16 += dppI<0x4E>(s16);  // the 16 values of lanes 4g .. 4g + 3
+    if ((lane & 3) == 0) qc[nsb * 65 + s * 16 + (lane >> 2)] = s16;
+    const int b32 = s16 + __shfl_down(s16, 4);  // lanes 8i: the sum of 32 values 32i .. 32i + 31
+    int pw[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int b = __builtin_amdgcn_readlane(b32, 8 * i);
+        pw[i >> 2] |= ((b >> 6) & 255) << (8 * (i & 3));
+        pw[2 + (i >> 2)] |= (b & 63) << (8 * (i & 3));
+    }
+    if (lane < 4) qc[nsb * 81 + s * 4 + lane] = lane == 0 ? pw[0] : (lane == 1 ? pw[1] : (lane == 2 ? pw[2] : pw[3]));
+    if (lane == 0) reinterpret_cast<float*>(qc + nsb * 64)[s] = d;
+}
+
+// Four consecutive floats at p (16-byte aligned when A16).
+template <bool A16>
+__device__ __forceinline__ float4 load4(const float* p) {
+    if (A16) return *reinterpret_cast<const float4*>(p);
+    return make_float4(p[0], p[1], p[2], p[3]);
+}
+template <bool A16>
+__device__ __forceinline__ void store4(float* p, float4 v) {
+    if (A16) *reinterpret_cast<float4*>(p) = v;
+    else p[0] = v.x, p[1] = v.y, p[2] = v.z, p[3] = v.w;
+}
+
 // ---------------------------------------------------------------- residual add + RMS norm
 
 // out = a + b and per-32 sums of out^2 into the row's slot tail (add_sumsq_f.cu). a may be null:
-// then x = b and only the sums are written (sumsq_part.cu).
-// a and out may be the same buffer (the residual stream updated in place).
-__global__ void add_sumsq_kernel(const float* a, const float* __restrict__ b, float* out, int* __restrict__ q, int n,
-                                 int rows) {
+// then x = b and only the sums are written (sumsq_part.cu). a and out may be the same buffer (the
+// residual stream updated in place). One thread per block of 32, whose values it loads at once
+// and sums of squares in order.
+template <bool A16>
+__global__ void add_sumsq_kernel(const float* a, const float* b, float* out, int* __restrict__ q, int n, int rows) {
     const int nb = n / 32;
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= nb * rows) return;
     const int row = idx / nb, bl = idx - row * nb;
     const size_t o = (size_t)row * n + bl * 32;
-    float s = 0.0f;
-    for (int i = 0; i < 32; ++i) {
-        float v;
-        if (a) {
-            v = a[o + i] + b[o + i];
-            out[o + i] = v;
-        } else {
-            v = b[o + i];
-        }
-        s += v * v;
+    float v[32];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const float4 bv = load4<A16>(b + o + 4 * k);
+        v[4 * k] = bv.x, v[4 * k + 1] = bv.y, v[4 * k + 2] = bv.z, v[4 * k + 3] = bv.w;
     }
-    reinterpret_cast<float*>(q + (size_t)row * nb * 11 + nb * 10)[bl] = s;
+    if (a) {
+        float av[32];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float4 x = load4<A16>(a + o + 4 * k);
+            av[4 * k] = x.x, av[4 * k + 1] = x.y, av[4 * k + 2] = x.z, av[4 * k + 3] = x.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 32; ++i) v[i] = av[i] + v[i];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) store4<A16>(out + o + 4 * k, make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]));
+    }
+    float sq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) sq += v[i] * v[i];
+    reinterpret_cast<float*>(q + (size_t)row * nb * 11 + nb * 10)[bl] = sq;
 }
 
 // y = x * r * w, quantized per 32 into the row's slot (norm_mul_q8_f.cu).
@@ -137,18 +179,35 @@ __global__ void norm_mul_q8_kernel(const float* __restrict__ x, const float* __r
 }
 
 // The same with per-256 slots (norm_mul_q8k_f.cu): q holds rows slots of nsb*85 ints, then the
-// rows per-32 slots whose tails hold the partial sums.
-__global__ void norm_mul_q8k_kernel(const float* __restrict__ x, const float* __restrict__ w, float* __restrict__ y,
-                                    int* __restrict__ q, int n, int rows, float eps) {
+// rows per-32 slots whose tails hold the partial sums. One workgroup of four wavefronts per row;
+// each wavefront takes super-blocks w, w + 4, ... with four values per lane. The row total is
+// summed in block order from values read back lane by lane.
+template <bool A16>
+__global__ __launch_bounds__(256) void norm_mul_q8k_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                           float* __restrict__ y, int* __restrict__ q, int n, int rows,
+                                                           float eps) {
     const int nsb = n / 256, nb = n / 32;
-    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= nsb * rows) return;
-    const int row = idx / nsb, s = idx - row * nsb;
+    const int row = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const float* ss = reinterpret_cast<const float*>(q + (size_t)rows * nsb * 85 + (size_t)row * nb * 11 + nb * 10);
-    const float r = rmsScale(ss, nb, n, eps);
-    const size_t o = (size_t)row * n + s * 256;
-    for (int i = 0; i < 256; ++i) y[o + i] = x[o + i] * r * w[s * 256 + i];
-    quant256(y + o, q + (size_t)row * nsb * 85, nsb, s);
+    float tot = 0.0f;
+    for (int j0 = 0; j0 < nb; j0 += 256) {
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = ss[min(j0 + 4 * lane + e, nb - 1)];
+        const int cnt = min(256, nb - j0) / 4;  // nb is a multiple of 8
+        for (int L = 0; L < cnt; ++L)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) tot += laneF(v[e], L);
+    }
+    const float r = 1.0f / sqrtf(tot / (float)n + eps);
+    int* qr = q + (size_t)row * nsb * 85;
+    for (int sb = wave; sb < nsb; sb += 4) {
+        const size_t o = (size_t)row * n + sb * 256 + 4 * lane;
+        const float4 xv = load4<A16>(x + o), wv = load4<A16>(w + sb * 256 + 4 * lane);
+        const float4 yv = make_float4(xv.x * r * wv.x, xv.y * r * wv.y, xv.z * r * wv.z, xv.w * r * wv.w);
+        store4<A16>(y + o, yv);
+        quant256Wave(yv.x, yv.y, yv.z, yv.w, qr, nsb, sb);
+    }
 }
 
 // SwiGLU, quantized per 32 (silu_mul_q8x4f.cu) or per 256 (silu_mul_q8kf.cu); columns of n.
@@ -168,15 +227,19 @@ __global__ void silu_mul_q8_kernel(const float* __restrict__ g, const float* __r
     quant32(v, qc + b * 8, reinterpret_cast<float*>(qc + nb * 8) + b * 2);
 }
 
-__global__ void silu_mul_q8k_kernel(const float* __restrict__ g, const float* __restrict__ u, float* __restrict__ y,
-                                    int* __restrict__ q, int n, int cols) {
+template <bool A16>
+__global__ __launch_bounds__(256) void silu_mul_q8k_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                           float* __restrict__ y, int* __restrict__ q, int n, int cols) {
     const int nsb = n / 256;
-    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= nsb * cols) return;
-    const int c = idx / nsb, s = idx - c * nsb;
-    const size_t o = (size_t)c * n + s * 256;
-    for (int i = 0; i < 256; ++i) y[o + i] = silu(g[o + i]) * u[o + i];
-    quant256(y + o, q + (size_t)c * nsb * 85, nsb, s);
+    const int c = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int* qc = q + (size_t)c * nsb * 85;
+    for (int sb = wave; sb < nsb; sb += 4) {
+        const size_t o = (size_t)c * n + sb * 256 + 4 * lane;
+        const float4 gv = load4<A16>(g + o), uv = load4<A16>(u + o);
+        const float4 yv = make_float4(silu(gv.x) * uv.x, silu(gv.y) * uv.y, silu(gv.z) * uv.z, silu(gv.w) * uv.w);
+        store4<A16>(y + o, yv);
+        quant256Wave(yv.x, yv.y, yv.z, yv.w, qc, nsb, sb);
+    }
 }
 
 // ---------------------------------------------------------------- elementwise and row ops
@@ -409,27 +472,38 @@ int launchVectorAdd(const float* a, const float* b, float* out, int count, hipSt
     return fromHip(hipGetLastError(), "vector_add");
 }
 
+static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 int launchAddSumsq(const float* a, const float* b, float* out, int* q, int n, int rows, hipStream_t s) {
-    hipLaunchKernelGGL(add_sumsq_kernel, dim3(blocksFor((long long)(n / 32) * rows)), dim3(256), 0, s, a, b, out, q, n,
-                       rows);
+    const dim3 grid(blocksFor((long long)(n / 32) * rows));
+    if (al16(b) && (!a || (al16(a) && al16(out))))
+        hipLaunchKernelGGL(add_sumsq_kernel<true>, grid, dim3(256), 0, s, a, b, out, q, n, rows);
+    else
+        hipLaunchKernelGGL(add_sumsq_kernel<false>, grid, dim3(256), 0, s, a, b, out, q, n, rows);
     return fromHip(hipGetLastError(), a ? "add_sumsq_f" : "sumsq_part");
 }
 
 int launchNormMulQ8(bool per256, const kcNormMulQ8Args& a, hipStream_t s) {
-    if (per256)
-        hipLaunchKernelGGL(norm_mul_q8k_kernel, dim3(blocksFor((long long)(a.n / 256) * a.rows)), dim3(256), 0, s, a.x,
-                           a.w, a.y, a.q, a.n, a.rows, a.eps);
-    else
+    if (per256 && a.rows > 0) {
+        if (al16(a.x) && al16(a.w) && al16(a.y))
+            hipLaunchKernelGGL(norm_mul_q8k_kernel<true>, dim3(a.rows), dim3(256), 0, s, a.x, a.w, a.y, a.q, a.n,
+                               a.rows, a.eps);
+        else
+            hipLaunchKernelGGL(norm_mul_q8k_kernel<false>, dim3(a.rows), dim3(256), 0, s, a.x, a.w, a.y, a.q, a.n,
+                               a.rows, a.eps);
+    } else if (!per256)
         hipLaunchKernelGGL(norm_mul_q8_kernel, dim3(blocksFor((long long)(a.n / 32) * a.rows)), dim3(256), 0, s, a.x,
                            a.w, a.y, a.q, a.n, a.rows, a.eps);
     return fromHip(hipGetLastError(), per256 ? "norm_mul_q8k_f" : "norm_mul_q8_f");
 }
 
 int launchSiluMulQ8(bool per256, const kcSiluMulQ8FArgs& a, hipStream_t s) {
-    if (per256)
-        hipLaunchKernelGGL(silu_mul_q8k_kernel, dim3(blocksFor((long long)(a.n / 256) * a.cols)), dim3(256), 0, s, a.g,
-                           a.u, a.y, a.q, a.n, a.cols);
-    else
+    if (per256 && a.cols > 0) {
+        if (al16(a.g) && al16(a.u) && al16(a.y))
+            hipLaunchKernelGGL(silu_mul_q8k_kernel<true>, dim3(a.cols), dim3(256), 0, s, a.g, a.u, a.y, a.q, a.n, a.cols);
+        else
+            hipLaunchKernelGGL(silu_mul_q8k_kernel<false>, dim3(a.cols), dim3(256), 0, s, a.g, a.u, a.y, a.q, a.n, a.cols);
+    } else if (!per256)
         hipLaunchKernelGGL(silu_mul_q8_kernel, dim3(blocksFor((long long)(a.n / 32) * a.cols)), dim3(256), 0, s, a.g,
                            a.u, a.y, a.q, a.n, a.cols);
     return fromHip(hipGetLastError(), per256 ? "silu_mul_q8kf" : "silu_mul_q8x4f");
