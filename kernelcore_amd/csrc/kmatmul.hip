@@ -160,9 +160,10 @@ int launchMatmulCols(bool q6k, bool per256, const kcMatmulKQ8Args& a, hipStream_
 }
 
 int launchMatmulKq(bool q6k, bool per256, const kcMatmulKQ8Args& a, hipStream_t s) {
-    // "matmul_path": 0 default (MFMA from 64 columns with per-256 slots), 1 column tiles, 2 MFMA.
+    // "matmul_path": 0 default (MFMA from 64 columns with per-256 slots), 1 column tiles, 2 MFMA,
+    // 3 MFMA with the four-wavefront tiles.
     const int path = option("matmul_path");
-    const bool mfma = per256 && (path == 2 || (path == 0 && a.ncols >= 64));
+    const bool mfma = per256 && (path >= 2 || (path == 0 && a.ncols >= 64));
     if (mfma) return launchMatmulMfma(q6k, a, s);
     return launchMatmulCols(q6k, per256, a, s);
 }

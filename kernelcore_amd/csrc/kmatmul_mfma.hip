@@ -31,7 +31,9 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <mutex>
 #include <type_traits>
+#include <vector>
 
 #include "internal.hpp"
 #include "kquant.hpp"
@@ -84,8 +86,9 @@ __device__ __forceinline__ h8 dequant8(uint2 q, bool hiNib, _Float16 sc) {
 }
 
 // One wavefront's view of 32 weight rows for one super-block: lane -> row lane % 32 and k-half
-// lane / 32. Rows past the stream (padding of the last 16-row tile and beyond) read as zeros;
-// their loads go to the first row instead, so every address stays inside the stream.
+// lane / 32. Rows past the stream (padding of the last 16-row tile and beyond) read the first
+// row instead, so every address stays inside the stream; their outputs are never stored. (No
+// select on the loaded values: it would make the prefetch wait for its own loads.)
 struct Rows32 {
     uint2 qs[4][2];  // [j'][u]: qs bytes 32j' + 16u + 8h .. +7
     float d, dmin;
@@ -95,15 +98,11 @@ struct Rows32 {
         const int rr = live ? row : 0;
         const int tile = rr >> 4, r = rr & 15, g = s >> 2, kq = s & 3;
         const uint8_t* piece = qw + ((size_t)tile * ngroups + g) * kQ4kSeg + (kq * 16 + r) * 16;
-        uint4 hdr = *reinterpret_cast<const uint4*>(piece);
-        if (!live) hdr = make_uint4(0, 0, 0, 0);
+        const uint4 hdr = *reinterpret_cast<const uint4*>(piece);
 #pragma unroll
         for (int a = 0; a < 4; ++a)
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const uint2 v = *reinterpret_cast<const uint2*>(piece + (1 + 2 * a + u) * 1024 + 8 * h);
-                qs[a][u] = live ? v : make_uint2(0, 0);
-            }
+            for (int u = 0; u < 2; ++u) qs[a][u] = *reinterpret_cast<const uint2*>(piece + (1 + 2 * a + u) * 1024 + 8 * h);
         d = (float)__builtin_bit_cast(_Float16, (unsigned short)(hdr.x & 0xFFFFu));
         dmin = (float)__builtin_bit_cast(_Float16, (unsigned short)(hdr.x >> 16));
         const int s0 = (int)hdr.y, s1 = (int)hdr.z, s2 = (int)hdr.w;
@@ -135,24 +134,19 @@ struct Rows32Q6 {
 #pragma unroll
             for (int a = 0; a < 2; ++a)
 #pragma unroll
-                for (int u = 0; u < 2; ++u) {
-                    const uint2 v = *reinterpret_cast<const uint2*>(piece + (4 * n + 2 * a + u) * 1024 + 8 * h);
-                    ql[n][a][u] = live ? v : make_uint2(0, 0);
-                }
+                for (int u = 0; u < 2; ++u)
+                    ql[n][a][u] = *reinterpret_cast<const uint2*>(piece + (4 * n + 2 * a + u) * 1024 + 8 * h);
 #pragma unroll
         for (int n = 0; n < 2; ++n)
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const uint2 v = *reinterpret_cast<const uint2*>(piece + (8 + 2 * n + u) * 1024 + 8 * h);
-                qh[n][u] = live ? v : make_uint2(0, 0);
-            }
+            for (int u = 0; u < 2; ++u) qh[n][u] = *reinterpret_cast<const uint2*>(piece + (8 + 2 * n + u) * 1024 + 8 * h);
         const uint4 sc = *reinterpret_cast<const uint4*>(piece + 12 * 1024);
-        sw[0] = live ? (int)sc.x : 0;
-        sw[1] = live ? (int)sc.y : 0;
-        sw[2] = live ? (int)sc.z : 0;
-        sw[3] = live ? (int)sc.w : 0;
+        sw[0] = (int)sc.x;
+        sw[1] = (int)sc.y;
+        sw[2] = (int)sc.z;
+        sw[3] = (int)sc.w;
         const uint32_t dbits = *reinterpret_cast<const uint16_t*>(seg + kQ6kSlabs * 1024 + (kq * 16 + r) * 2);
-        d = live ? (float)__builtin_bit_cast(_Float16, (unsigned short)dbits) : 0.0f;
+        d = (float)__builtin_bit_cast(_Float16, (unsigned short)dbits);
     }
     // K-step t as two exact fp16 operands: 16 sh (q - 32) and sl (q - 32), sc_t = 16 sh + sl.
     __device__ __forceinline__ void dequant(int t, h8& b1, h8& b2) const {
@@ -348,6 +342,498 @@ __global__ __launch_bounds__(256) void matmul_kq_mfma_kernel(const uint8_t* __re
     }
 }
 
+// Row-wavefront variant: the same 128 x 128 tile per workgroup, each wavefront 32 weight rows x
+// all 128 columns (four 32 x 32 blocks, so one dequantized weight fragment feeds four MFMAs).
+// NG = 2: eight wavefronts, the super-blocks split by parity between wavefronts 0-3 and 4-7
+// (two per SIMD, overlapping each other's vector and matrix work); both groups' activations are
+// staged per iteration and the two partial sums are added at the end.
+constexpr int kLdsGrp = kBN * kXStride * 2 + kBN * 16 * 2 + kBN * 4;
+
+template <bool Q6, int NG>
+__global__ __launch_bounds__(256 * NG) void matmul_kq_mfma8_kernel(const uint8_t* __restrict__ qw,
+                                                              const int* __restrict__ xq, float* __restrict__ y,
+                                                              int rows, int nsb, int ncols) {
+    extern __shared__ int4 lds4[];
+    _Float16* xa0 = reinterpret_cast<_Float16*>(lds4);             // [NG][kBN][kXStride]
+    _Float16* xm0 = xa0 + NG * kBN * kXStride;                       // [NG][kBN][16]
+    float* xd0 = reinterpret_cast<float*>(xm0 + NG * kBN * 16);      // [NG][kBN]
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    constexpr int NT = 256 * NG;  // threads
+    const int grp = wave >> 2, wr = wave & 3;
+    const int h = lane >> 5, l32 = lane & 31;
+    const int row = blockIdx.x * kBM + wr * 32 + l32;  // this lane's weight row
+    const int col0 = blockIdx.y * kBN;
+    const int ngroups = (nsb + kGroupSb - 1) / kGroupSb;
+    const int rows_stream = ((rows + kTileRows - 1) / kTileRows) * kTileRows;
+    const int slot_ints = nsb * 85;
+    const int iters = (nsb + NG - 1) / NG;
+    const _Float16* xa = xa0 + grp * kBN * kXStride;
+    const _Float16* xm = xm0 + grp * kBN * 16;
+    const float* xdl = xd0 + grp * kBN;
+
+    f16v acc[4];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[cb][i] = 0.0f;
+    const f16v zero = acc[0];
+
+    // activations of both super-blocks of an iteration: 32 words per thread, and for 256 threads
+    // one column's mins words and scale
+    constexpr int kWords = NG * kBN * 64 / NT;
+    int xw[kWords];
+    int xp[4] = {0, 0, 0, 0};
+    float xdv = 0.0f;
+    auto fetchX = [&](int it) {
+#pragma unroll
+        for (int i = 0; i < kWords; ++i) {
+            const int idx = i * NT + tid;
+            const int sb = idx >> 13, rem = idx & 8191;
+            const int c = rem >> 6, w = rem & 63;
+            const int sx = NG * it + sb;
+            const bool live = col0 + c < ncols && sx < nsb;  // dead columns / super-blocks: never stored
+            xw[i] = xq[(size_t)(live ? col0 + c : 0) * slot_ints + (live ? sx : 0) * 64 + w];
+        }
+        if (tid < NG * kBN) {
+            const int sb = tid >> 7, c = tid & 127, sx = NG * it + sb;
+            const bool live = col0 + c < ncols && sx < nsb;
+            const int* slot = xq + (size_t)(live ? col0 + c : 0) * slot_ints;
+            const int sxc = live ? sx : 0;
+            xdv = reinterpret_cast<const float*>(slot + nsb * 64)[sxc];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xp[j] = slot[nsb * 81 + sxc * 4 + j];
+        }
+    };
+    using Rows = typename std::conditional<Q6, Rows32Q6, Rows32>::type;
+    Rows wcur, wnext;
+    fetchX(0);
+    if (grp < nsb) wnext.load(qw, row, rows_stream, ngroups, grp, h);
+
+    for (int it = 0; it < iters; ++it) {
+        // ---- stage this iteration's two super-blocks (in registers) into LDS as fp16
+#pragma unroll
+        for (int i = 0; i < kWords; ++i) {
+            const int idx = i * NT + tid;
+            const int sb = idx >> 13, rem = idx & 8191;
+            const int c = rem >> 6, w = rem & 63;
+            *reinterpret_cast<uint2*>(xa0 + (sb * kBN + c) * kXStride + 4 * w) = i8x4_to_h4((uint32_t)xw[i]);
+        }
+        if (tid < NG * kBN) {
+            const int sb = tid >> 7, c = tid & 127;
+            if (!Q6) {  // [B>>6 of 0-3 | of 4-7 | B&63 of 0-3 | of 4-7]
+                h8 mlo, mhi;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int hb = (xp[j >> 2] << (24 - 8 * (j & 3))) >> 24;  // signed byte
+                    const int lb = (xp[2 + (j >> 2)] >> (8 * (j & 3))) & 255;
+                    mlo[j] = (_Float16)(float)(64 * hb);
+                    mhi[j] = (_Float16)(float)lb;
+                }
+                *reinterpret_cast<h8*>(xm0 + (sb * kBN + c) * 16) = mlo;
+                *reinterpret_cast<h8*>(xm0 + (sb * kBN + c) * 16 + 8) = mhi;
+            }
+            xd0[sb * kBN + c] = xdv;
+        }
+        __syncthreads();
+        const int s = NG * it + grp;  // this wavefront's super-block
+        const bool active = s < nsb;
+        wcur = wnext;
+        if (it + 1 < iters) {
+            fetchX(it + 1);
+            if (s + NG < nsb) wnext.load(qw, row, rows_stream, ngroups, s + NG, h);
+        }
+        if constexpr (!Q6 && NG == 2) {
+          if (active) {
+            // Q4_K with two wavefronts per SIMD: the super-block's 16 weight fragments are
+            // dequantized first (64 registers), then each column block runs its 16 MFMAs into one
+            // accumulator and is combined at once, so only one block's partial sums are live.
+            h8 bwa[16];
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                const int j = t >> 1, u = t & 1;
+                bwa[t] = dequant8(wcur.qs[j >> 1][u], j & 1, wcur.sc(j));
+            }
+            h8 bm;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) bm[e] = wcur.m(e);
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) {
+                f16v isb = zero;
+#pragma unroll
+                for (int t = 0; t < 16; ++t) {
+                    const h8 av = *reinterpret_cast<const h8*>(xa + (cb * 32 + l32) * kXStride + 16 * t + 8 * h);
+                    isb = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bwa[t], isb, 0, 0, 0);
+                }
+                const h8 am = *reinterpret_cast<const h8*>(xm + (cb * 32 + l32) * 16 + 8 * h);
+                const f16v im = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, zero, 0, 0, 0);
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    const float4 xd4 = *reinterpret_cast<const float4*>(xdl + cb * 32 + q4 * 8 + h * 4);
+                    const float xdv4[4] = {xd4.x, xd4.y, xd4.z, xd4.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int i = 4 * q4 + e;
+                        const float t2 = __builtin_fmaf(-wcur.dmin, im[i], wcur.d * isb[i]);
+                        acc[cb][i] = __builtin_fmaf(xdv4[e], t2, acc[cb][i]);
+                    }
+                }
+            }
+          }
+        } else if (active) {
+            f16v is[4];
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                h8 av[4];
+#pragma unroll
+                for (int cb = 0; cb < 4; ++cb)
+                    av[cb] = *reinterpret_cast<const h8*>(xa + (cb * 32 + l32) * kXStride + 16 * t + 8 * h);
+                if constexpr (Q6) {
+                    h8 b1, b2;
+                    wcur.dequant(t, b1, b2);
+#pragma unroll
+                    for (int cb = 0; cb < 4; ++cb) {
+                        is[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[cb], b1, t == 0 ? zero : is[cb], 0, 0, 0);
+                        is[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[cb], b2, is[cb], 0, 0, 0);
+                    }
+                } else {
+                    const int j = t >> 1, u = t & 1;
+                    const h8 bw = dequant8(wcur.qs[j >> 1][u], j & 1, wcur.sc(j));
+#pragma unroll
+                    for (int cb = 0; cb < 4; ++cb)
+                        is[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[cb], bw, t == 0 ? zero : is[cb], 0, 0, 0);
+                }
+            }
+            h8 bm;
+            if constexpr (!Q6) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) bm[e] = wcur.m(e);
+            }
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) {
+                f16v im;
+                if constexpr (!Q6) {
+                    const h8 am = *reinterpret_cast<const h8*>(xm + (cb * 32 + l32) * 16 + 8 * h);
+                    im = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, zero, 0, 0, 0);
+                }
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    const float4 xd4 = *reinterpret_cast<const float4*>(xdl + cb * 32 + q4 * 8 + h * 4);
+                    const float xdv4[4] = {xd4.x, xd4.y, xd4.z, xd4.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int i = 4 * q4 + e;
+                        if constexpr (Q6) {
+                            acc[cb][i] = __builtin_fmaf(wcur.d * xdv4[e], is[cb][i], acc[cb][i]);
+                        } else {
+                            const float t2 = __builtin_fmaf(-wcur.dmin, im[i], wcur.d * is[cb][i]);
+                            acc[cb][i] = __builtin_fmaf(xdv4[e], t2, acc[cb][i]);
+                        }
+                    }
+                }
+            }
+        }
+        __syncthreads();  // the next iteration overwrites the staged activations
+    }
+    // ---- group 1 hands its partial sums to group 0 through LDS (the activations are done)
+    float* red = reinterpret_cast<float*>(lds4);
+    if (NG == 2 && grp == 1)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) red[((wr * 64 + lane) * 4 + cb) * 16 + i] = acc[cb][i];
+    if (NG == 2) __syncthreads();
+    if (grp == 0 && row < rows) {
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int c = col0 + cb * 32 + (i >> 2) * 8 + h * 4 + (i & 3);
+                const float v = NG == 2 ? acc[cb][i] + red[((wr * 64 + lane) * 4 + cb) * 16 + i] : acc[cb][i];
+                if (c < ncols) y[(size_t)c * rows + row] = v;
+            }
+    }
+}
+
+template <bool Q6, int NG>
+int runMfma8(const kcMatmulKQ8Args& a, hipStream_t s) {
+    static const int attr = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(matmul_kq_mfma8_kernel<Q6, NG>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, NG * kLdsGrp);
+    if (attr != 0) return fromHip(attr, "matmul (MFMA): LDS size");
+    const dim3 grid((a.rows + kBM - 1) / kBM, (a.ncols + kBN - 1) / kBN);
+    hipLaunchKernelGGL((matmul_kq_mfma8_kernel<Q6, NG>), grid, dim3(256 * NG), NG * kLdsGrp, s,
+                       reinterpret_cast<const uint8_t*>(a.qw), a.xq, a.y, a.rows, a.k / 256, a.ncols);
+    return fromHip(hipGetLastError(), Q6 ? "matmul_q6k_q8k (MFMA)" : "matmul_q4k_q8k (MFMA)");
+}
+
+// ---------------------------------------------------------------- fp16-activation variant
+// The activations are first converted once per matmul to fp16 (act[c][k]; for Q4_K also the mins
+// operand of every (column, super-block), act_to_f16_kernel), so the matmul stages them with
+// direct global-to-LDS loads (no registers, no per-workgroup conversion) into a double-buffered
+// LDS tile: super-block s + 1 streams in while s is computed. One direct load fills 1 KB: the two
+// columns of a pair, 512 B each; pairs are 1040 B apart (16 B of padding), which spreads the 32
+// columns read by one ds_read_b128 over the banks and lets every read use an immediate offset.
+// Each wavefront computes 32 weight rows x 128 columns (four 32 x 32 blocks); the A operands of
+// K-step t + 1 are read while K-step t runs.
+
+// act[c][s * 256 ..] = the 256 int8 activations of super-block s of column c, as fp16; for Q4_K,
+// mins[c][s][16] = [64 (B_j >> 6) for j < 8 | B_j & 63 for j < 8] (B_j = sum of the 32 values of
+// sub-block j, the reference's byte split).
+__global__ void act_to_f16_kernel(const int* __restrict__ xq, uint2* __restrict__ act, h8* __restrict__ mins,
+                                  int nsb, long long words, int ncols) {
+    const long long i = blockIdx.x * 256LL + threadIdx.x;
+    const long long per = (long long)nsb * 64;
+    if (i < words) {
+        const long long c = i / per, w = i - c * per;
+        act[i] = i8x4_to_h4((uint32_t)xq[c * nsb * 85 + w]);
+    }
+    if (mins && i < (long long)ncols * nsb) {
+        const long long c = i / nsb, sx = i - c * nsb;
+        const int* pw = xq + c * nsb * 85 + nsb * 81 + sx * 4;
+        const int w0 = pw[0], w1 = pw[1], w2 = pw[2], w3 = pw[3];
+        h8 lo, hi;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int hb = ((j < 4 ? w0 : w1) << (24 - 8 * (j & 3))) >> 24;
+            const int lb = ((j < 4 ? w2 : w3) >> (8 * (j & 3))) & 255;
+            lo[j] = (_Float16)(float)(64 * hb);
+            hi[j] = (_Float16)(float)lb;
+        }
+        mins[2 * i] = lo;
+        mins[2 * i + 1] = hi;
+    }
+}
+
+constexpr int kPair = 1040;                       // bytes per column pair in LDS
+constexpr int kActB = 64 * kPair;                 // 128 columns of one super-block
+constexpr int kHBuf = kActB + 128 * 32 + 128 * 4; // + mins operands + scales
+constexpr int kLdsH = 2 * kHBuf;
+
+// Eight 4-bit weights (nibble hiNib of 8 bytes) times a sub-block scale: m2 / s2 precomputed.
+__device__ __forceinline__ h8 dequant8s(uint2 q, bool hiNib, h2 m2, h2 s2) {
+    const uint32_t mask = hiNib ? 0xFFF0FFF0u : 0xFF0FFF0Fu;
+    h8 r;
+    const uint32_t w[2] = {q.x, q.y};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const h2 a = bits_h2(__builtin_amdgcn_perm(0x64646464u, w[i], 0x04010400u) & mask);
+        const h2 b = bits_h2(__builtin_amdgcn_perm(0x64646464u, w[i], 0x04030402u) & mask);
+        const h2 ra = __builtin_elementwise_fma(a, m2, s2);
+        const h2 rb = __builtin_elementwise_fma(b, m2, s2);
+        r[4 * i + 0] = ra[0];
+        r[4 * i + 1] = ra[1];
+        r[4 * i + 2] = rb[0];
+        r[4 * i + 3] = rb[1];
+    }
+    return r;
+}
+
+template <bool Q6>
+__global__ __launch_bounds__(256) void matmul_kq_mfma_h_kernel(const uint8_t* __restrict__ qw,
+                                                               const int* __restrict__ xq,
+                                                               const _Float16* __restrict__ act,
+                                                               const _Float16* __restrict__ mins,
+                                                               float* __restrict__ y, int rows, int nsb, int ncols) {
+    extern __shared__ int4 lds4[];
+    char* lbase = reinterpret_cast<char*>(lds4);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = lane >> 5, l32 = lane & 31;
+    const int row = blockIdx.x * kBM + wave * 32 + l32;
+    const int col0 = blockIdx.y * kBN;
+    const int ngroups = (nsb + kGroupSb - 1) / kGroupSb;
+    const int rows_stream = ((rows + kTileRows - 1) / kTileRows) * kTileRows;
+    const int slot_ints = nsb * 85;
+    const int k = nsb * 256;
+
+    // direct loads of super-block s into stage buffer b (columns past ncols read column 0)
+    auto stage = [&](int s, int b) {
+        char* buf = lbase + b * kHBuf;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int pp = wave * 16 + r;  // the column pair of this load
+            const int c = 2 * pp + (lane >> 5);
+            const int cc = col0 + c < ncols ? col0 + c : 0;
+            __builtin_amdgcn_global_load_lds(act + (size_t)cc * k + s * 256 + (lane & 31) * 8, buf + pp * kPair, 16, 0,
+                                             0);
+        }
+        if (!Q6) {
+            const int p = wave * 64 + lane, c = p >> 1;
+            const int cc = col0 + c < ncols ? col0 + c : 0;
+            __builtin_amdgcn_global_load_lds(mins + ((size_t)cc * nsb + s) * 16 + (p & 1) * 8, buf + kActB + wave * 1024,
+                                             16, 0, 0);
+        }
+        if (wave < 2) {
+            const int c = wave * 64 + lane;
+            const int cc = col0 + c < ncols ? col0 + c : 0;
+            __builtin_amdgcn_global_load_lds(xq + (size_t)cc * slot_ints + nsb * 64 + s, buf + kActB + 4096 + wave * 256,
+                                             4, 0, 0);
+        }
+    };
+
+    f16v acc[4];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[cb][i] = 0.0f;
+    const f16v zero = acc[0];
+    using Rows = typename std::conditional<Q6, Rows32Q6, Rows32>::type;
+    Rows wcur, wnext;
+    stage(0, 0);
+    wnext.load(qw, row, rows_stream, ngroups, 0, h);
+    // this lane's A-operand byte offset in a stage for column block cb (K-step t adds 32 t)
+    int aoff[4];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
+        const int c = cb * 32 + l32;
+        aoff[cb] = (c >> 1) * kPair + (c & 1) * 512 + h * 16;
+    }
+
+    for (int s = 0; s < nsb; ++s) {
+        const int b = s & 1;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wavefront's loads of stage s
+        __syncthreads();  // everyone's: stage s is complete, stage b ^ 1 is no longer read
+        wcur = wnext;
+        if (s + 1 < nsb) {
+            stage(s + 1, b ^ 1);
+            wnext.load(qw, row, rows_stream, ngroups, s + 1, h);
+        }
+        const char* buf = lbase + b * kHBuf;
+        f16v is[4];
+        h2 m2[8], s2[8];  // Q4_K: per sub-block (1024 + q) -> sc * q constants
+        if constexpr (!Q6) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const _Float16 sc = wcur.sc(j);
+                const bool hiNib = j & 1;
+                const _Float16 mul = hiNib ? sc * (_Float16)0.0625f : sc;
+                const _Float16 sub = hiNib ? sc * (_Float16)(-64.0f) : sc * (_Float16)(-1024.0f);
+                m2[j] = h2{mul, mul};
+                s2[j] = h2{sub, sub};
+            }
+        }
+        h8 av[4], an[4];
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) av[cb] = *reinterpret_cast<const h8*>(buf + aoff[cb]);
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            if (t + 1 < 16)
+#pragma unroll
+                for (int cb = 0; cb < 4; ++cb) an[cb] = *reinterpret_cast<const h8*>(buf + aoff[cb] + 32 * (t + 1));
+            if constexpr (Q6) {
+                h8 b1, b2;
+                wcur.dequant(t, b1, b2);
+#pragma unroll
+                for (int cb = 0; cb < 4; ++cb) {
+                    is[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[cb], b1, t == 0 ? zero : is[cb], 0, 0, 0);
+                    is[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[cb], b2, is[cb], 0, 0, 0);
+                }
+            } else {
+                const int j = t >> 1, u = t & 1;
+                const h8 bw = dequant8s(wcur.qs[j >> 1][u], j & 1, m2[j], s2[j]);
+#pragma unroll
+                for (int cb = 0; cb < 4; ++cb)
+                    is[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[cb], bw, t == 0 ? zero : is[cb], 0, 0, 0);
+            }
+            if (t + 1 < 16)
+#pragma unroll
+                for (int cb = 0; cb < 4; ++cb) av[cb] = an[cb];
+        }
+        h8 bm;
+        if constexpr (!Q6) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) bm[e] = wcur.m(e);
+        }
+        const _Float16* xm = reinterpret_cast<const _Float16*>(buf + kActB);
+        const float* xdl = reinterpret_cast<const float*>(buf + kActB + 4096);
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+            f16v im;
+            if constexpr (!Q6) {
+                const h8 am = *reinterpret_cast<const h8*>(xm + (cb * 32 + l32) * 16 + 8 * h);
+                im = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, zero, 0, 0, 0);
+            }
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const float4 xd4 = *reinterpret_cast<const float4*>(xdl + cb * 32 + q4 * 8 + h * 4);
+                const float xdv4[4] = {xd4.x, xd4.y, xd4.z, xd4.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int i = 4 * q4 + e;
+                    if constexpr (Q6) {
+                        acc[cb][i] = __builtin_fmaf(wcur.d * xdv4[e], is[cb][i], acc[cb][i]);
+                    } else {
+                        const float t2 = __builtin_fmaf(-wcur.dmin, im[i], wcur.d * is[cb][i]);
+                        acc[cb][i] = __builtin_fmaf(xdv4[e], t2, acc[cb][i]);
+                    }
+                }
+            }
+        }
+    }
+    if (row < rows) {
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int c = col0 + cb * 32 + (i >> 2) * 8 + h * 4 + (i & 3);
+                if (c < ncols) y[(size_t)c * rows + row] = acc[cb][i];
+            }
+    }
+}
+
+// Per-stream fp16 activation buffers (grown on demand, never while the stream is capturing).
+struct ActBuf {
+    hipStream_t s;
+    int dev;
+    void* p;
+    size_t bytes;
+};
+std::mutex g_act_mu;
+std::vector<ActBuf> g_act;
+
+void* actBuffer(hipStream_t s, size_t bytes) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lk(g_act_mu);
+    for (auto& b : g_act)
+        if (b.s == s && b.dev == dev) {
+            if (b.bytes >= bytes) return b.p;
+            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+            if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+            if (hipStreamSynchronize(s) != hipSuccess) return nullptr;
+            (void)hipFree(b.p);
+            b.p = nullptr;
+            b.bytes = 0;
+            if (hipMalloc(&b.p, bytes) != hipSuccess) return b.p = nullptr;
+            b.bytes = bytes;
+            return b.p;
+        }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+    void* p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
+    g_act.push_back({s, dev, p, bytes});
+    return p;
+}
+
+// The fp16 activation buffer: ncols * k halves, then (Q4_K) ncols * nsb * 16 halves of mins.
+size_t actBytes(int ncols, int k) { return (size_t)ncols * k * 2 + (size_t)ncols * (k / 256) * 32; }
+
+template <bool Q6>
+int runMfmaH(const kcMatmulKQ8Args& a, void* act, hipStream_t s) {
+    static const int attr = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(matmul_kq_mfma_h_kernel<Q6>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, kLdsH);
+    if (attr != 0) return fromHip(attr, "matmul (MFMA): LDS size");
+    const int nsb = a.k / 256;
+    const long long words = (long long)a.ncols * nsb * 64;
+    _Float16* mins = static_cast<_Float16*>(act) + (size_t)a.ncols * a.k;
+    hipLaunchKernelGGL(act_to_f16_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, s, a.xq,
+                       static_cast<uint2*>(act), Q6 ? nullptr : reinterpret_cast<h8*>(mins), nsb, words, a.ncols);
+    const dim3 grid((a.rows + kBM - 1) / kBM, (a.ncols + kBN - 1) / kBN);
+    hipLaunchKernelGGL(matmul_kq_mfma_h_kernel<Q6>, grid, dim3(256), kLdsH, s, reinterpret_cast<const uint8_t*>(a.qw),
+                       a.xq, static_cast<const _Float16*>(act), mins, a.y, a.rows, nsb, a.ncols);
+    return fromHip(hipGetLastError(), Q6 ? "matmul_q6k_q8k (MFMA)" : "matmul_q4k_q8k (MFMA)");
+}
+
 template <bool Q6>
 int runMfma(const kcMatmulKQ8Args& a, hipStream_t s) {
     static const int attr = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(matmul_kq_mfma_kernel<Q6>),
@@ -362,7 +848,14 @@ int runMfma(const kcMatmulKQ8Args& a, hipStream_t s) {
 }  // namespace
 
 int launchMatmulMfma(bool q6k, const kcMatmulKQ8Args& a, hipStream_t s) {
-    return q6k ? runMfma<true>(a, s) : runMfma<false>(a, s);
+    const int path = option("matmul_path");
+    if (path == 3) return q6k ? runMfma<true>(a, s) : runMfma<false>(a, s);  // 2 x 2 blocks per wavefront
+    if (path == 4) return q6k ? runMfma8<true, 2>(a, s) : runMfma8<false, 2>(a, s);
+    if (path != 5) {  // fp16 activations staged by direct loads (needs a per-stream buffer)
+        if (void* act = actBuffer(s, actBytes(a.ncols, a.k)))
+            return q6k ? runMfmaH<true>(a, act, s) : runMfmaH<false>(a, act, s);
+    }
+    return q6k ? runMfma8<true, 1>(a, s) : runMfma8<false, 1>(a, s);
 }
 
 }  // namespace kcamd
