@@ -45,6 +45,7 @@ namespace {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f16v __attribute__((ext_vector_type(16)));
+typedef uint32_t u32v4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBM = 128;         // weight rows per workgroup
 constexpr int kBN = 128;         // activation columns per workgroup
@@ -89,8 +90,11 @@ __device__ __forceinline__ h8 dequant8(uint2 q, bool hiNib, _Float16 sc) {
 // lane / 32. Rows past the stream (padding of the last 16-row tile and beyond) read the first
 // row instead, so every address stays inside the stream; their outputs are never stored. (No
 // select on the loaded values: it would make the prefetch wait for its own loads.)
+// load() only issues the loads (nothing reads the loaded words until decode(), so the loads of
+// the next super-block stay in flight behind the current one's compute).
 struct Rows32 {
     uint2 qs[4][2];  // [j'][u]: qs bytes 32j' + 16u + 8h .. +7
+    uint4 hdr;       // d, dmin (fp16) and the 12 packed scale / min bytes
     float d, dmin;
     int scw[2], mw[2];  // scales / mins of sub-blocks 0-3 and 4-7, one byte each
     __device__ __forceinline__ void load(const uint8_t* qw, int row, int rows_stream, int ngroups, int s, int h) {
@@ -98,11 +102,13 @@ struct Rows32 {
         const int rr = live ? row : 0;
         const int tile = rr >> 4, r = rr & 15, g = s >> 2, kq = s & 3;
         const uint8_t* piece = qw + ((size_t)tile * ngroups + g) * kQ4kSeg + (kq * 16 + r) * 16;
-        const uint4 hdr = *reinterpret_cast<const uint4*>(piece);
+        hdr = *reinterpret_cast<const uint4*>(piece);
 #pragma unroll
         for (int a = 0; a < 4; ++a)
 #pragma unroll
             for (int u = 0; u < 2; ++u) qs[a][u] = *reinterpret_cast<const uint2*>(piece + (1 + 2 * a + u) * 1024 + 8 * h);
+    }
+    __device__ __forceinline__ void decode() {
         d = (float)__builtin_bit_cast(_Float16, (unsigned short)(hdr.x & 0xFFFFu));
         dmin = (float)__builtin_bit_cast(_Float16, (unsigned short)(hdr.x >> 16));
         const int s0 = (int)hdr.y, s1 = (int)hdr.z, s2 = (int)hdr.w;
@@ -122,6 +128,7 @@ struct Rows32Q6 {
     uint2 ql[2][2][2];  // [n][quad & 1][t & 1]
     uint2 qh[2][2];     // [n][t & 1]
     int sw[4];          // the 16 int8 scales
+    uint32_t dbits;     // d (fp16)
     float d;
     __device__ __forceinline__ void load(const uint8_t* qw, int row, int rows_stream, int ngroups, int s, int h) {
         const bool live = row < rows_stream;
@@ -145,9 +152,9 @@ struct Rows32Q6 {
         sw[1] = (int)sc.y;
         sw[2] = (int)sc.z;
         sw[3] = (int)sc.w;
-        const uint32_t dbits = *reinterpret_cast<const uint16_t*>(seg + kQ6kSlabs * 1024 + (kq * 16 + r) * 2);
-        d = (float)__builtin_bit_cast(_Float16, (unsigned short)dbits);
+        dbits = *reinterpret_cast<const uint16_t*>(seg + kQ6kSlabs * 1024 + (kq * 16 + r) * 2);
     }
+    __device__ __forceinline__ void decode() { d = (float)__builtin_bit_cast(_Float16, (unsigned short)dbits); }
     // K-step t as two exact fp16 operands: 16 sh (q - 32) and sl (q - 32), sc_t = 16 sh + sl.
     __device__ __forceinline__ void dequant(int t, h8& b1, h8& b2) const {
         const int n = t >> 3, quad = (t >> 1) & 3, u = t & 1;
@@ -257,6 +264,8 @@ __global__ __launch_bounds__(256) void matmul_kq_mfma_kernel(const uint8_t* __re
         if (tid < kBN) xdl[tid] = xdv;
         __syncthreads();
         Rows wrow[2] = {wnext[0], wnext[1]};
+        wrow[0].decode();
+        wrow[1].decode();
         if (s + 1 < nsb) {
             fetchX(s + 1);
 #pragma unroll
@@ -439,6 +448,7 @@ __global__ __launch_bounds__(256 * NG) void matmul_kq_mfma8_kernel(const uint8_t
         const int s = NG * it + grp;  // this wavefront's super-block
         const bool active = s < nsb;
         wcur = wnext;
+        wcur.decode();
         if (it + 1 < iters) {
             fetchX(it + 1);
             if (s + NG < nsb) wnext.load(qw, row, rows_stream, ngroups, s + NG, h);
@@ -570,22 +580,29 @@ int runMfma8(const kcMatmulKQ8Args& a, hipStream_t s) {
 // The activations are first converted once per matmul to fp16 (act[c][k]; for Q4_K also the mins
 // operand of every (column, super-block), act_to_f16_kernel), so the matmul stages them with
 // direct global-to-LDS loads (no registers, no per-workgroup conversion) into a double-buffered
-// LDS tile: super-block s + 1 streams in while s is computed. One direct load fills 1 KB: the two
-// columns of a pair, 512 B each; pairs are 1040 B apart (16 B of padding), which spreads the 32
-// columns read by one ds_read_b128 over the banks and lets every read use an immediate offset.
+// LDS tile: super-block s + 1 streams in while s is computed. A column's 256 values (32 chunks of
+// 16 B) sit 528 B apart (one chunk of padding), so the 16 columns read by a quarter-wavefront's
+// ds_read_b128 start 16 B apart modulo 256 B (no bank conflicts) and every read of a lane is its
+// base plus an immediate offset. One direct load fills 1 KB (64 lanes x 16 B) and each lane picks
+// the chunk of that layout it fetches: 66 loads fill a stage (pad chunks re-read chunk 0).
 // Each wavefront computes 32 weight rows x 128 columns (four 32 x 32 blocks); the A operands of
 // K-step t + 1 are read while K-step t runs.
 
 // act[c][s * 256 ..] = the 256 int8 activations of super-block s of column c, as fp16; for Q4_K,
 // mins[c][s][16] = [64 (B_j >> 6) for j < 8 | B_j & 63 for j < 8] (B_j = sum of the 32 values of
-// sub-block j, the reference's byte split).
+// sub-block j, the reference's byte split); xdT[s][c] = the scale of column c's super-block s
+// (0 for the padding columns ncols <= c < ncp).
 __global__ void act_to_f16_kernel(const int* __restrict__ xq, uint2* __restrict__ act, h8* __restrict__ mins,
-                                  int nsb, long long words, int ncols) {
+                                  float* __restrict__ xdT, int nsb, long long words, int ncols, int ncp) {
     const long long i = blockIdx.x * 256LL + threadIdx.x;
     const long long per = (long long)nsb * 64;
     if (i < words) {
         const long long c = i / per, w = i - c * per;
         act[i] = i8x4_to_h4((uint32_t)xq[c * nsb * 85 + w]);
+    }
+    if (i < (long long)nsb * ncp) {
+        const long long sx = i / ncp, c = i - sx * ncp;
+        xdT[i] = c < ncols ? reinterpret_cast<const float*>(xq + c * nsb * 85 + nsb * 64)[sx] : 0.0f;
     }
     if (mins && i < (long long)ncols * nsb) {
         const long long c = i / nsb, sx = i - c * nsb;
@@ -604,9 +621,11 @@ __global__ void act_to_f16_kernel(const int* __restrict__ xq, uint2* __restrict_
     }
 }
 
-constexpr int kPair = 1040;                       // bytes per column pair in LDS
-constexpr int kActB = 64 * kPair;                 // 128 columns of one super-block
-constexpr int kHBuf = kActB + 128 * 32 + 128 * 4; // + mins operands + scales
+constexpr int kColB = 528;                        // bytes per column in LDS: 32 chunks + 1 pad chunk
+constexpr int kActLoads = 128 * 33 / 64;          // direct loads of 1 KB per stage
+constexpr int kActB = kActLoads * 1024;           // 128 columns of one super-block
+constexpr int kActPerWave = (kActLoads + 3) / 4;  // loads per wavefront (the last ones repeat load 65)
+constexpr int kHBuf = kActB + 128 * 32 + 1024;    // + mins operands + scales (one 1 KB load)
 constexpr int kLdsH = 2 * kHBuf;
 
 // Eight 4-bit weights (nibble hiNib of 8 bytes) times a sub-block scale: m2 / s2 precomputed.
@@ -630,10 +649,10 @@ __device__ __forceinline__ h8 dequant8s(uint2 q, bool hiNib, h2 m2, h2 s2) {
 
 template <bool Q6>
 __global__ __launch_bounds__(256) void matmul_kq_mfma_h_kernel(const uint8_t* __restrict__ qw,
-                                                               const int* __restrict__ xq,
                                                                const _Float16* __restrict__ act,
                                                                const _Float16* __restrict__ mins,
-                                                               float* __restrict__ y, int rows, int nsb, int ncols) {
+                                                               const float* __restrict__ xdT, float* __restrict__ y,
+                                                               int rows, int nsb, int ncols, int ncp) {
     extern __shared__ int4 lds4[];
     char* lbase = reinterpret_cast<char*>(lds4);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -642,19 +661,26 @@ __global__ __launch_bounds__(256) void matmul_kq_mfma_h_kernel(const uint8_t* __
     const int col0 = blockIdx.y * kBN;
     const int ngroups = (nsb + kGroupSb - 1) / kGroupSb;
     const int rows_stream = ((rows + kTileRows - 1) / kTileRows) * kTileRows;
-    const int slot_ints = nsb * 85;
     const int k = nsb * 256;
 
-    // direct loads of super-block s into stage buffer b (columns past ncols read column 0)
+    // this lane's byte offset into act of each of its direct loads (super-block 0); columns past
+    // ncols read column 0
+    uint32_t goff[kActPerWave];
+#pragma unroll
+    for (int r = 0; r < kActPerWave; ++r) {
+        const int g = min(r * 4 + wave, kActLoads - 1);
+        const int slot = g * 64 + lane, c = slot / 33, kc = slot - 33 * c;
+        const int cc = col0 + c < ncols ? col0 + c : 0;
+        goff[r] = (uint32_t)cc * (uint32_t)k * 2u + (uint32_t)(kc == 32 ? 0 : kc) * 16u;
+    }
+    // direct loads of super-block s into stage buffer b
     auto stage = [&](int s, int b) {
         char* buf = lbase + b * kHBuf;
+        const char* src = reinterpret_cast<const char*>(act) + (size_t)s * 512;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int pp = wave * 16 + r;  // the column pair of this load
-            const int c = 2 * pp + (lane >> 5);
-            const int cc = col0 + c < ncols ? col0 + c : 0;
-            __builtin_amdgcn_global_load_lds(act + (size_t)cc * k + s * 256 + (lane & 31) * 8, buf + pp * kPair, 16, 0,
-                                             0);
+        for (int r = 0; r < kActPerWave; ++r) {
+            const int g = min(r * 4 + wave, kActLoads - 1);
+            __builtin_amdgcn_global_load_lds(src + goff[r], buf + g * 1024, 16, 0, 0);
         }
         if (!Q6) {
             const int p = wave * 64 + lane, c = p >> 1;
@@ -662,12 +688,8 @@ __global__ __launch_bounds__(256) void matmul_kq_mfma_h_kernel(const uint8_t* __
             __builtin_amdgcn_global_load_lds(mins + ((size_t)cc * nsb + s) * 16 + (p & 1) * 8, buf + kActB + wave * 1024,
                                              16, 0, 0);
         }
-        if (wave < 2) {
-            const int c = wave * 64 + lane;
-            const int cc = col0 + c < ncols ? col0 + c : 0;
-            __builtin_amdgcn_global_load_lds(xq + (size_t)cc * slot_ints + nsb * 64 + s, buf + kActB + 4096 + wave * 256,
-                                             4, 0, 0);
-        }
+        // the 128 column scales: every wavefront writes the same 1 KB (lanes 32-63 repeat 0-31)
+        __builtin_amdgcn_global_load_lds(xdT + (size_t)s * ncp + col0 + l32 * 4, buf + kActB + 4096, 16, 0, 0);
     };
 
     f16v acc[4];
@@ -685,7 +707,7 @@ __global__ __launch_bounds__(256) void matmul_kq_mfma_h_kernel(const uint8_t* __
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) {
         const int c = cb * 32 + l32;
-        aoff[cb] = (c >> 1) * kPair + (c & 1) * 512 + h * 16;
+        aoff[cb] = c * kColB + h * 16;
     }
 
     for (int s = 0; s < nsb; ++s) {
@@ -693,6 +715,7 @@ __global__ __launch_bounds__(256) void matmul_kq_mfma_h_kernel(const uint8_t* __
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wavefront's loads of stage s
         __syncthreads();  // everyone's: stage s is complete, stage b ^ 1 is no longer read
         wcur = wnext;
+        wcur.decode();
         if (s + 1 < nsb) {
             stage(s + 1, b ^ 1);
             wnext.load(qw, row, rows_stream, ngroups, s + 1, h);
@@ -744,7 +767,7 @@ __global__ __launch_bounds__(256) void matmul_kq_mfma_h_kernel(const uint8_t* __
             for (int e = 0; e < 8; ++e) bm[e] = wcur.m(e);
         }
         const _Float16* xm = reinterpret_cast<const _Float16*>(buf + kActB);
-        const float* xdl = reinterpret_cast<const float*>(buf + kActB + 4096);
+        const char* xdl = buf + kActB + 4096;
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb) {
             f16v im;
@@ -754,8 +777,14 @@ __global__ __launch_bounds__(256) void matmul_kq_mfma_h_kernel(const uint8_t* __
             }
 #pragma unroll
             for (int q4 = 0; q4 < 4; ++q4) {
-                const float4 xd4 = *reinterpret_cast<const float4*>(xdl + cb * 32 + q4 * 8 + h * 4);
-                const float xdv4[4] = {xd4.x, xd4.y, xd4.z, xd4.w};
+                const h8 xd8 = *reinterpret_cast<const h8*>(xdl + (cb * 32 + q4 * 8 + h * 4) * 4);
+                const u32v4 xdw = __builtin_bit_cast(u32v4, xd8);
+                float xdv4[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t wv = xdw[e];
+                    xdv4[e] = __builtin_bit_cast(float, wv);
+                }
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int i = 4 * q4 + e;
@@ -816,7 +845,12 @@ void* actBuffer(hipStream_t s, size_t bytes) {
 }
 
 // The fp16 activation buffer: ncols * k halves, then (Q4_K) ncols * nsb * 16 halves of mins.
-size_t actBytes(int ncols, int k) { return (size_t)ncols * k * 2 + (size_t)ncols * (k / 256) * 32; }
+// The fp16 activation buffer: ncols * k halves, then (Q4_K) ncols * nsb * 16 halves of mins, then
+// nsb * ncp floats of column scales (ncp = ncols rounded up to whole 128-column tiles).
+int actCols(int ncols) { return (ncols + kBN - 1) / kBN * kBN; }
+size_t actBytes(int ncols, int k) {
+    return (size_t)ncols * k * 2 + (size_t)ncols * (k / 256) * 32 + (size_t)(k / 256) * actCols(ncols) * 4;
+}
 
 template <bool Q6>
 int runMfmaH(const kcMatmulKQ8Args& a, void* act, hipStream_t s) {
@@ -826,11 +860,14 @@ int runMfmaH(const kcMatmulKQ8Args& a, void* act, hipStream_t s) {
     const int nsb = a.k / 256;
     const long long words = (long long)a.ncols * nsb * 64;
     _Float16* mins = static_cast<_Float16*>(act) + (size_t)a.ncols * a.k;
+    float* xdT = reinterpret_cast<float*>(mins + (size_t)a.ncols * nsb * 16);
+    const int ncp = actCols(a.ncols);
     hipLaunchKernelGGL(act_to_f16_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, s, a.xq,
-                       static_cast<uint2*>(act), Q6 ? nullptr : reinterpret_cast<h8*>(mins), nsb, words, a.ncols);
+                       static_cast<uint2*>(act), Q6 ? nullptr : reinterpret_cast<h8*>(mins), xdT, nsb, words, a.ncols,
+                       ncp);
     const dim3 grid((a.rows + kBM - 1) / kBM, (a.ncols + kBN - 1) / kBN);
     hipLaunchKernelGGL(matmul_kq_mfma_h_kernel<Q6>, grid, dim3(256), kLdsH, s, reinterpret_cast<const uint8_t*>(a.qw),
-                       a.xq, static_cast<const _Float16*>(act), mins, a.y, a.rows, nsb, a.ncols);
+                       static_cast<const _Float16*>(act), mins, xdT, a.y, a.rows, nsb, a.ncols, ncp);
     return fromHip(hipGetLastError(), Q6 ? "matmul_q6k_q8k (MFMA)" : "matmul_q4k_q8k (MFMA)");
 }
 
@@ -851,7 +888,8 @@ int launchMatmulMfma(bool q6k, const kcMatmulKQ8Args& a, hipStream_t s) {
     const int path = option("matmul_path");
     if (path == 3) return q6k ? runMfma<true>(a, s) : runMfma<false>(a, s);  // 2 x 2 blocks per wavefront
     if (path == 4) return q6k ? runMfma8<true, 2>(a, s) : runMfma8<false, 2>(a, s);
-    if (path != 5) {  // fp16 activations staged by direct loads (needs a per-stream buffer)
+    // fp16 activations staged by direct loads (a per-stream buffer, addressed with 32-bit offsets)
+    if (path != 5 && (size_t)a.ncols * a.k * 2 < (1ull << 32)) {
         if (void* act = actBuffer(s, actBytes(a.ncols, a.k)))
             return q6k ? runMfmaH<true>(a, act, s) : runMfmaH<false>(a, act, s);
     }
