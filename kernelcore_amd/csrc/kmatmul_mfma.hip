@@ -621,12 +621,20 @@ __global__ void act_to_f16_kernel(const int* __restrict__ xq, uint2* __restrict_
     }
 }
 
-constexpr int kColB = 528;                        // bytes per column in LDS: 32 chunks + 1 pad chunk
-constexpr int kActLoads = 128 * 33 / 64;          // direct loads of 1 KB per stage
-constexpr int kActB = kActLoads * 1024;           // 128 columns of one super-block
-constexpr int kActPerWave = (kActLoads + 3) / 4;  // loads per wavefront (the last ones repeat load 65)
-constexpr int kHBuf = kActB + 128 * 32 + 1024;    // + mins operands + scales (one 1 KB load)
-constexpr int kLdsH = 2 * kHBuf;
+constexpr int kColB = 528;  // bytes per column in LDS: 32 chunks + 1 pad chunk
+
+// LDS geometry of the fp16-activation kernel with CB column blocks of 32 per wavefront (every
+// wavefront of a workgroup covers the same 32 CB columns, each its own 32 weight rows).
+template <int CB>
+struct HGeo {
+    static constexpr int kCols = 32 * CB;                   // activation columns per workgroup
+    static constexpr int kActLoads = kCols * 33 / 64;       // direct loads of 1 KB per stage
+    static constexpr int kActB = kActLoads * 1024;          // the stage's activation tile
+    static constexpr int kPerWave = (kActLoads + 3) / 4;    // loads per wavefront (the last ones repeat)
+    static constexpr int kMinB = kCols * 32;                // Q4_K min operands
+    static constexpr int kBuf = kActB + kMinB + 1024;       // + column scales (one 1 KB load)
+    static constexpr int kLds = 2 * kBuf;
+};
 
 // Eight 4-bit weights (nibble hiNib of 8 bytes) times a sub-block scale: m2 / s2 precomputed.
 __device__ __forceinline__ h8 dequant8s(uint2 q, bool hiNib, h2 m2, h2 s2) {
@@ -647,68 +655,70 @@ __device__ __forceinline__ h8 dequant8s(uint2 q, bool hiNib, h2 m2, h2 s2) {
     return r;
 }
 
-template <bool Q6>
-__global__ __launch_bounds__(256) void matmul_kq_mfma_h_kernel(const uint8_t* __restrict__ qw,
-                                                               const _Float16* __restrict__ act,
-                                                               const _Float16* __restrict__ mins,
-                                                               const float* __restrict__ xdT, float* __restrict__ y,
-                                                               int rows, int nsb, int ncols, int ncp) {
+// Direct loads of super-block s into stage buffer buf: the activation tile (goff = this lane's
+// byte offsets of its loads in act at super-block 0), the Q4_K min operands and the column scales.
+template <bool Q6, int CB>
+__device__ __forceinline__ void stageH(char* buf, const _Float16* act, const _Float16* mins, const float* xdT,
+                                       const uint32_t (&goff)[HGeo<CB>::kPerWave], int s, int wave, int lane,
+                                       int col0, int ncols, int nsb, int ncp) {
+    using G = HGeo<CB>;
+    const char* src = reinterpret_cast<const char*>(act) + (size_t)s * 512;
+#pragma unroll
+    for (int r = 0; r < G::kPerWave; ++r) {
+        const int g = min(r * 4 + wave, G::kActLoads - 1);
+        __builtin_amdgcn_global_load_lds(src + goff[r], buf + g * 1024, 16, 0, 0);
+    }
+    if constexpr (!Q6) {  // 32 columns per load; wavefronts past CB repeat the loads of wavefront wave % CB
+        const int wq = wave % CB, p = wq * 64 + lane, c = p >> 1;
+        const int cc = col0 + c < ncols ? col0 + c : 0;
+        __builtin_amdgcn_global_load_lds(mins + ((size_t)cc * nsb + s) * 16 + (p & 1) * 8, buf + G::kActB + wq * 1024,
+                                         16, 0, 0);
+    }
+    // the column scales: every wavefront writes the same 1 KB (lanes past the tile repeat)
+    __builtin_amdgcn_global_load_lds(xdT + (size_t)s * ncp + col0 + ((lane & 31) % (8 * CB)) * 4,
+                                     buf + G::kActB + G::kMinB, 16, 0, 0);
+}
+
+template <bool Q6, int CB>
+__global__ __launch_bounds__(256) void matmul_kq_mfma_h_kernel(
+    const uint8_t* __restrict__ qw, const _Float16* __restrict__ act, const _Float16* __restrict__ mins,
+    const float* __restrict__ xdT, float* __restrict__ y, int rows, int nsb, int ncols, int ncp) {
+    using G = HGeo<CB>;
     extern __shared__ int4 lds4[];
     char* lbase = reinterpret_cast<char*>(lds4);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = lane >> 5, l32 = lane & 31;
     const int row = blockIdx.x * kBM + wave * 32 + l32;
-    const int col0 = blockIdx.y * kBN;
+    const int col0 = blockIdx.y * G::kCols;
     const int ngroups = (nsb + kGroupSb - 1) / kGroupSb;
     const int rows_stream = ((rows + kTileRows - 1) / kTileRows) * kTileRows;
     const int k = nsb * 256;
 
     // this lane's byte offset into act of each of its direct loads (super-block 0); columns past
     // ncols read column 0
-    uint32_t goff[kActPerWave];
+    uint32_t goff[G::kPerWave];
 #pragma unroll
-    for (int r = 0; r < kActPerWave; ++r) {
-        const int g = min(r * 4 + wave, kActLoads - 1);
+    for (int r = 0; r < G::kPerWave; ++r) {
+        const int g = min(r * 4 + wave, G::kActLoads - 1);
         const int slot = g * 64 + lane, c = slot / 33, kc = slot - 33 * c;
         const int cc = col0 + c < ncols ? col0 + c : 0;
         goff[r] = (uint32_t)cc * (uint32_t)k * 2u + (uint32_t)(kc == 32 ? 0 : kc) * 16u;
     }
-    // direct loads of super-block s into stage buffer b
-    auto stage = [&](int s, int b) {
-        char* buf = lbase + b * kHBuf;
-        const char* src = reinterpret_cast<const char*>(act) + (size_t)s * 512;
-#pragma unroll
-        for (int r = 0; r < kActPerWave; ++r) {
-            const int g = min(r * 4 + wave, kActLoads - 1);
-            __builtin_amdgcn_global_load_lds(src + goff[r], buf + g * 1024, 16, 0, 0);
-        }
-        if (!Q6) {
-            const int p = wave * 64 + lane, c = p >> 1;
-            const int cc = col0 + c < ncols ? col0 + c : 0;
-            __builtin_amdgcn_global_load_lds(mins + ((size_t)cc * nsb + s) * 16 + (p & 1) * 8, buf + kActB + wave * 1024,
-                                             16, 0, 0);
-        }
-        // the 128 column scales: every wavefront writes the same 1 KB (lanes 32-63 repeat 0-31)
-        __builtin_amdgcn_global_load_lds(xdT + (size_t)s * ncp + col0 + l32 * 4, buf + kActB + 4096, 16, 0, 0);
-    };
 
-    f16v acc[4];
+    f16v acc[CB];
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
+    for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[cb][i] = 0.0f;
     const f16v zero = acc[0];
     using Rows = typename std::conditional<Q6, Rows32Q6, Rows32>::type;
     Rows wcur, wnext;
-    stage(0, 0);
+    stageH<Q6, CB>(lbase, act, mins, xdT, goff, 0, wave, lane, col0, ncols, nsb, ncp);
     wnext.load(qw, row, rows_stream, ngroups, 0, h);
     // this lane's A-operand byte offset in a stage for column block cb (K-step t adds 32 t)
-    int aoff[4];
+    int aoff[CB];
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) {
-        const int c = cb * 32 + l32;
-        aoff[cb] = c * kColB + h * 16;
-    }
+    for (int cb = 0; cb < CB; ++cb) aoff[cb] = (cb * 32 + l32) * kColB + h * 16;
 
     for (int s = 0; s < nsb; ++s) {
         const int b = s & 1;
@@ -717,11 +727,11 @@ __global__ __launch_bounds__(256) void matmul_kq_mfma_h_kernel(const uint8_t* __
         wcur = wnext;
         wcur.decode();
         if (s + 1 < nsb) {
-            stage(s + 1, b ^ 1);
+            stageH<Q6, CB>(lbase + (b ^ 1) * G::kBuf, act, mins, xdT, goff, s + 1, wave, lane, col0, ncols, nsb, ncp);
             wnext.load(qw, row, rows_stream, ngroups, s + 1, h);
         }
-        const char* buf = lbase + b * kHBuf;
-        f16v is[4];
+        const char* buf = lbase + b * G::kBuf;
+        f16v is[CB];
         h2 m2[8], s2[8];  // Q4_K: per sub-block (1024 + q) -> sc * q constants
         if constexpr (!Q6) {
 #pragma unroll
@@ -734,19 +744,19 @@ __global__ __launch_bounds__(256) void matmul_kq_mfma_h_kernel(const uint8_t* __
                 s2[j] = h2{sub, sub};
             }
         }
-        h8 av[4], an[4];
+        h8 av[CB], an[CB];
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) av[cb] = *reinterpret_cast<const h8*>(buf + aoff[cb]);
+        for (int cb = 0; cb < CB; ++cb) av[cb] = *reinterpret_cast<const h8*>(buf + aoff[cb]);
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
             if (t + 1 < 16)
 #pragma unroll
-                for (int cb = 0; cb < 4; ++cb) an[cb] = *reinterpret_cast<const h8*>(buf + aoff[cb] + 32 * (t + 1));
+                for (int cb = 0; cb < CB; ++cb) an[cb] = *reinterpret_cast<const h8*>(buf + aoff[cb] + 32 * (t + 1));
             if constexpr (Q6) {
                 h8 b1, b2;
                 wcur.dequant(t, b1, b2);
 #pragma unroll
-                for (int cb = 0; cb < 4; ++cb) {
+                for (int cb = 0; cb < CB; ++cb) {
                     is[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[cb], b1, t == 0 ? zero : is[cb], 0, 0, 0);
                     is[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[cb], b2, is[cb], 0, 0, 0);
                 }
@@ -754,22 +764,22 @@ __global__ __launch_bounds__(256) void matmul_kq_mfma_h_kernel(const uint8_t* __
                 const int j = t >> 1, u = t & 1;
                 const h8 bw = dequant8s(wcur.qs[j >> 1][u], j & 1, m2[j], s2[j]);
 #pragma unroll
-                for (int cb = 0; cb < 4; ++cb)
+                for (int cb = 0; cb < CB; ++cb)
                     is[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[cb], bw, t == 0 ? zero : is[cb], 0, 0, 0);
             }
             if (t + 1 < 16)
 #pragma unroll
-                for (int cb = 0; cb < 4; ++cb) av[cb] = an[cb];
+                for (int cb = 0; cb < CB; ++cb) av[cb] = an[cb];
         }
         h8 bm;
         if constexpr (!Q6) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) bm[e] = wcur.m(e);
         }
-        const _Float16* xm = reinterpret_cast<const _Float16*>(buf + kActB);
-        const char* xdl = buf + kActB + 4096;
+        const _Float16* xm = reinterpret_cast<const _Float16*>(buf + G::kActB);
+        const char* xdl = buf + G::kActB + G::kMinB;
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) {
+        for (int cb = 0; cb < CB; ++cb) {
             f16v im;
             if constexpr (!Q6) {
                 const h8 am = *reinterpret_cast<const h8*>(xm + (cb * 32 + l32) * 16 + 8 * h);
@@ -777,6 +787,8 @@ __global__ __launch_bounds__(256) void matmul_kq_mfma_h_kernel(const uint8_t* __
             }
 #pragma unroll
             for (int q4 = 0; q4 < 4; ++q4) {
+                // (an ext_vector read: HIP's float4 struct here made the compiler wait for the
+                // direct loads in flight before this read)
                 const h8 xd8 = *reinterpret_cast<const h8*>(xdl + (cb * 32 + q4 * 8 + h * 4) * 4);
                 const u32v4 xdw = __builtin_bit_cast(u32v4, xd8);
                 float xdv4[4];
@@ -800,7 +812,7 @@ __global__ __launch_bounds__(256) void matmul_kq_mfma_h_kernel(const uint8_t* __
     }
     if (row < rows) {
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb)
+        for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int c = col0 + cb * 32 + (i >> 2) * 8 + h * 4 + (i & 3);
@@ -844,18 +856,18 @@ void* actBuffer(hipStream_t s, size_t bytes) {
     return p;
 }
 
-// The fp16 activation buffer: ncols * k halves, then (Q4_K) ncols * nsb * 16 halves of mins.
 // The fp16 activation buffer: ncols * k halves, then (Q4_K) ncols * nsb * 16 halves of mins, then
 // nsb * ncp floats of column scales (ncp = ncols rounded up to whole 128-column tiles).
-int actCols(int ncols) { return (ncols + kBN - 1) / kBN * kBN; }
+int actCols(int ncols) { return (ncols + 127) / 128 * 128; }
 size_t actBytes(int ncols, int k) {
     return (size_t)ncols * k * 2 + (size_t)ncols * (k / 256) * 32 + (size_t)(k / 256) * actCols(ncols) * 4;
 }
 
-template <bool Q6>
+template <bool Q6, int CB>
 int runMfmaH(const kcMatmulKQ8Args& a, void* act, hipStream_t s) {
-    static const int attr = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(matmul_kq_mfma_h_kernel<Q6>),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, kLdsH);
+    using G = HGeo<CB>;
+    static const int attr = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(matmul_kq_mfma_h_kernel<Q6, CB>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, G::kLds);
     if (attr != 0) return fromHip(attr, "matmul (MFMA): LDS size");
     const int nsb = a.k / 256;
     const long long words = (long long)a.ncols * nsb * 64;
@@ -865,9 +877,10 @@ int runMfmaH(const kcMatmulKQ8Args& a, void* act, hipStream_t s) {
     hipLaunchKernelGGL(act_to_f16_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, s, a.xq,
                        static_cast<uint2*>(act), Q6 ? nullptr : reinterpret_cast<h8*>(mins), xdT, nsb, words, a.ncols,
                        ncp);
-    const dim3 grid((a.rows + kBM - 1) / kBM, (a.ncols + kBN - 1) / kBN);
-    hipLaunchKernelGGL(matmul_kq_mfma_h_kernel<Q6>, grid, dim3(256), kLdsH, s, reinterpret_cast<const uint8_t*>(a.qw),
-                       static_cast<const _Float16*>(act), mins, xdT, a.y, a.rows, nsb, a.ncols, ncp);
+    const dim3 grid((a.rows + kBM - 1) / kBM, (a.ncols + G::kCols - 1) / G::kCols);
+    hipLaunchKernelGGL((matmul_kq_mfma_h_kernel<Q6, CB>), grid, dim3(256), G::kLds, s,
+                       reinterpret_cast<const uint8_t*>(a.qw), static_cast<const _Float16*>(act), mins, xdT, a.y,
+                       a.rows, nsb, a.ncols, ncp);
     return fromHip(hipGetLastError(), Q6 ? "matmul_q6k_q8k (MFMA)" : "matmul_q4k_q8k (MFMA)");
 }
 
@@ -890,8 +903,10 @@ int launchMatmulMfma(bool q6k, const kcMatmulKQ8Args& a, hipStream_t s) {
     if (path == 4) return q6k ? runMfma8<true, 2>(a, s) : runMfma8<false, 2>(a, s);
     // fp16 activations staged by direct loads (a per-stream buffer, addressed with 32-bit offsets)
     if (path != 5 && (size_t)a.ncols * a.k * 2 < (1ull << 32)) {
-        if (void* act = actBuffer(s, actBytes(a.ncols, a.k)))
-            return q6k ? runMfmaH<true>(a, act, s) : runMfmaH<false>(a, act, s);
+        if (void* act = actBuffer(s, actBytes(a.ncols, a.k))) {
+            if (path == 6) return q6k ? runMfmaH<true, 4>(a, act, s) : runMfmaH<false, 4>(a, act, s);
+            return q6k ? runMfmaH<true, 2>(a, act, s) : runMfmaH<false, 2>(a, act, s);
+        }
     }
     return q6k ? runMfma8<true, 1>(a, s) : runMfma8<false, 1>(a, s);
 }
