@@ -679,17 +679,18 @@ __device__ __forceinline__ void stageH(char* buf, const _Float16* act, const _Fl
                                      buf + G::kActB + G::kMinB, 16, 0, 0);
 }
 
+// One workgroup's tile: weight rows rowTile * 128 .., columns colTile * 32 CB .., super-blocks
+// [sb0, sb1) of the nsb (y = the partial sum over that range).
 template <bool Q6, int CB>
-__global__ __launch_bounds__(256) void matmul_kq_mfma_h_kernel(
-    const uint8_t* __restrict__ qw, const _Float16* __restrict__ act, const _Float16* __restrict__ mins,
-    const float* __restrict__ xdT, float* __restrict__ y, int rows, int nsb, int ncols, int ncp) {
+__device__ __forceinline__ void hTile(char* lbase, const uint8_t* __restrict__ qw, const _Float16* __restrict__ act,
+                                      const _Float16* __restrict__ mins, const float* __restrict__ xdT,
+                                      float* __restrict__ y, int rows, int nsb, int ncols, int ncp, int rowTile,
+                                      int colTile, int sb0, int sb1) {
     using G = HGeo<CB>;
-    extern __shared__ int4 lds4[];
-    char* lbase = reinterpret_cast<char*>(lds4);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = lane >> 5, l32 = lane & 31;
-    const int row = blockIdx.x * kBM + wave * 32 + l32;
-    const int col0 = blockIdx.y * G::kCols;
+    const int row = rowTile * kBM + wave * 32 + l32;
+    const int col0 = colTile * G::kCols;
     const int ngroups = (nsb + kGroupSb - 1) / kGroupSb;
     const int rows_stream = ((rows + kTileRows - 1) / kTileRows) * kTileRows;
     const int k = nsb * 256;
@@ -713,20 +714,20 @@ __global__ __launch_bounds__(256) void matmul_kq_mfma_h_kernel(
     const f16v zero = acc[0];
     using Rows = typename std::conditional<Q6, Rows32Q6, Rows32>::type;
     Rows wcur, wnext;
-    stageH<Q6, CB>(lbase, act, mins, xdT, goff, 0, wave, lane, col0, ncols, nsb, ncp);
-    wnext.load(qw, row, rows_stream, ngroups, 0, h);
+    stageH<Q6, CB>(lbase, act, mins, xdT, goff, sb0, wave, lane, col0, ncols, nsb, ncp);
+    wnext.load(qw, row, rows_stream, ngroups, sb0, h);
     // this lane's A-operand byte offset in a stage for column block cb (K-step t adds 32 t)
     int aoff[CB];
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) aoff[cb] = (cb * 32 + l32) * kColB + h * 16;
 
-    for (int s = 0; s < nsb; ++s) {
-        const int b = s & 1;
+    for (int s = sb0; s < sb1; ++s) {
+        const int b = (s - sb0) & 1;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wavefront's loads of stage s
         __syncthreads();  // everyone's: stage s is complete, stage b ^ 1 is no longer read
         wcur = wnext;
         wcur.decode();
-        if (s + 1 < nsb) {
+        if (s + 1 < sb1) {
             stageH<Q6, CB>(lbase + (b ^ 1) * G::kBuf, act, mins, xdT, goff, s + 1, wave, lane, col0, ncols, nsb, ncp);
             wnext.load(qw, row, rows_stream, ngroups, s + 1, h);
         }
@@ -821,6 +822,39 @@ __global__ __launch_bounds__(256) void matmul_kq_mfma_h_kernel(
     }
 }
 
+// Up to three weight matrices over the same activations, each split over K into ks ranges
+// (blockIdx.z; split z writes its partial sums to y[z]).
+struct HPart {
+    const uint8_t* qw;
+    float* y[2];
+    int rows;
+    int q6;
+    int tile0;  // first row tile (blockIdx.x) of this matrix
+};
+struct HGroup {
+    HPart p[3];
+    int nparts;
+    int ks;
+};
+
+__global__ __launch_bounds__(256) void matmul_kq_mfma_h_kernel(HGroup g, const _Float16* __restrict__ act,
+                                                               const _Float16* __restrict__ mins,
+                                                               const float* __restrict__ xdT, int nsb, int ncols,
+                                                               int ncp) {
+    extern __shared__ int4 lds4[];
+    char* lbase = reinterpret_cast<char*>(lds4);
+    const int bx = blockIdx.x;
+    const int pi = (g.nparts > 2 && bx >= g.p[2].tile0) ? 2 : (g.nparts > 1 && bx >= g.p[1].tile0) ? 1 : 0;
+    const HPart& p = g.p[pi];
+    const int z = blockIdx.z, sb0 = z * nsb / g.ks, sb1 = (z + 1) * nsb / g.ks;
+    if (p.q6)
+        hTile<true, 2>(lbase, p.qw, act, mins, xdT, p.y[z], p.rows, nsb, ncols, ncp, bx - p.tile0, blockIdx.y, sb0,
+                       sb1);
+    else
+        hTile<false, 2>(lbase, p.qw, act, mins, xdT, p.y[z], p.rows, nsb, ncols, ncp, bx - p.tile0, blockIdx.y, sb0,
+                        sb1);
+}
+
 // Per-stream fp16 activation buffers (grown on demand, never while the stream is capturing).
 struct ActBuf {
     hipStream_t s;
@@ -863,25 +897,36 @@ size_t actBytes(int ncols, int k) {
     return (size_t)ncols * k * 2 + (size_t)ncols * (k / 256) * 32 + (size_t)(k / 256) * actCols(ncols) * 4;
 }
 
-template <bool Q6, int CB>
-int runMfmaH(const kcMatmulKQ8Args& a, void* act, hipStream_t s) {
-    using G = HGeo<CB>;
-    static const int attr = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(matmul_kq_mfma_h_kernel<Q6, CB>),
+// The fp16-activation kernel over parts[0..nparts) (one conversion of the activations), K split
+// into ks ranges.
+int runMfmaH(const MmPart* parts, int nparts, const int* xq, int k, int ncols, int ks, void* act, hipStream_t s) {
+    using G = HGeo<2>;
+    static const int attr = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(matmul_kq_mfma_h_kernel),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, G::kLds);
     if (attr != 0) return fromHip(attr, "matmul (MFMA): LDS size");
-    const int nsb = a.k / 256;
-    const long long words = (long long)a.ncols * nsb * 64;
-    _Float16* mins = static_cast<_Float16*>(act) + (size_t)a.ncols * a.k;
-    float* xdT = reinterpret_cast<float*>(mins + (size_t)a.ncols * nsb * 16);
-    const int ncp = actCols(a.ncols);
-    hipLaunchKernelGGL(act_to_f16_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, s, a.xq,
-                       static_cast<uint2*>(act), Q6 ? nullptr : reinterpret_cast<h8*>(mins), xdT, nsb, words, a.ncols,
-                       ncp);
-    const dim3 grid((a.rows + kBM - 1) / kBM, (a.ncols + G::kCols - 1) / G::kCols);
-    hipLaunchKernelGGL((matmul_kq_mfma_h_kernel<Q6, CB>), grid, dim3(256), G::kLds, s,
-                       reinterpret_cast<const uint8_t*>(a.qw), static_cast<const _Float16*>(act), mins, xdT, a.y,
-                       a.rows, nsb, a.ncols, ncp);
-    return fromHip(hipGetLastError(), Q6 ? "matmul_q6k_q8k (MFMA)" : "matmul_q4k_q8k (MFMA)");
+    const int nsb = k / 256;
+    HGroup g{};
+    bool any_q4 = false;
+    int tiles = 0;
+    for (int i = 0; i < nparts; ++i) {
+        g.p[i] = HPart{static_cast<const uint8_t*>(parts[i].qw), {parts[i].y[0], parts[i].y[1]}, parts[i].rows,
+                       parts[i].q6, tiles};
+        tiles += (parts[i].rows + kBM - 1) / kBM;
+        any_q4 |= !parts[i].q6;
+    }
+    g.nparts = nparts;
+    g.ks = ks;
+    const long long words = (long long)ncols * nsb * 64;
+    _Float16* mins = static_cast<_Float16*>(act) + (size_t)ncols * k;
+    float* xdT = reinterpret_cast<float*>(mins + (size_t)ncols * nsb * 16);
+    const int ncp = actCols(ncols);
+    hipLaunchKernelGGL(act_to_f16_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, s, xq,
+                       static_cast<uint2*>(act), any_q4 ? reinterpret_cast<h8*>(mins) : nullptr, xdT, nsb, words,
+                       ncols, ncp);
+    const dim3 grid(tiles, (ncols + G::kCols - 1) / G::kCols, ks);
+    hipLaunchKernelGGL(matmul_kq_mfma_h_kernel, grid, dim3(256), G::kLds, s, g, static_cast<const _Float16*>(act),
+                       mins, xdT, nsb, ncols, ncp);
+    return fromHip(hipGetLastError(), "matmul_q4k/q6k_q8k (MFMA)");
 }
 
 template <bool Q6>
@@ -897,6 +942,8 @@ int runMfma(const kcMatmulKQ8Args& a, hipStream_t s) {
 
 }  // namespace
 
+bool mfmaHUsable(int ncols, int k) { return option("matmul_path") == 0 && (size_t)ncols * k * 2 < (1ull << 32); }
+
 int launchMatmulMfma(bool q6k, const kcMatmulKQ8Args& a, hipStream_t s) {
     const int path = option("matmul_path");
     if (path == 3) return q6k ? runMfma<true>(a, s) : runMfma<false>(a, s);  // 2 x 2 blocks per wavefront
@@ -904,11 +951,31 @@ int launchMatmulMfma(bool q6k, const kcMatmulKQ8Args& a, hipStream_t s) {
     // fp16 activations staged by direct loads (a per-stream buffer, addressed with 32-bit offsets)
     if (path != 5 && (size_t)a.ncols * a.k * 2 < (1ull << 32)) {
         if (void* act = actBuffer(s, actBytes(a.ncols, a.k))) {
-            if (path == 6) return q6k ? runMfmaH<true, 4>(a, act, s) : runMfmaH<false, 4>(a, act, s);
-            return q6k ? runMfmaH<true, 2>(a, act, s) : runMfmaH<false, 2>(a, act, s);
+            const MmPart part{a.qw, {a.y, nullptr}, a.rows, q6k ? 1 : 0};
+            return runMfmaH(&part, 1, a.xq, a.k, a.ncols, 1, act, s);
         }
     }
     return q6k ? runMfma8<true, 1>(a, s) : runMfma8<false, 1>(a, s);
+}
+
+int launchMatmulGroup(const MmPart* parts, int nparts, const int* xq, int k, int ncols, int ks, int* used_ks,
+                      hipStream_t s) {
+    *used_ks = 1;
+    if (nparts < 1 || nparts > 3 || ks < 1 || ks > 2 || k % 256 != 0) return fromHip(hipErrorInvalidValue, "matmul group");
+    if (ncols >= 64 && mfmaHUsable(ncols, k)) {
+        if (void* act = actBuffer(s, actBytes(ncols, k))) {
+            if (ks > k / 256) ks = 1;
+            *used_ks = ks;
+            return runMfmaH(parts, nparts, xq, k, ncols, ks, act, s);
+        }
+    }
+    for (int i = 0; i < nparts; ++i) {  // one matmul per part, no K split
+        const kcMatmulKQ8Args a{static_cast<const int*>(parts[i].qw), xq, parts[i].y[0], nullptr, parts[i].rows, k,
+                                ncols, 8};
+        const int st = launchMatmulKq(parts[i].q6 != 0, true, a, s);
+        if (st) return st;
+    }
+    return 0;
 }
 
 }  // namespace kcamd

@@ -20,9 +20,23 @@ int launchMatmulCols(bool q6k, bool per256, const kcMatmulKQ8Args& a, hipStream_
 int launchMatmulMfma(bool q6k, const kcMatmulKQ8Args& a, hipStream_t s);
 // The matmul names: column tiles for small batches and per-32 slots, MFMA for large per-256 batches.
 int launchMatmulKq(bool q6k, bool per256, const kcMatmulKQ8Args& a, hipStream_t s);
+// One weight matrix of a grouped matmul: y[z] receives the partial sums of K range z.
+struct MmPart {
+    const void* qw;  // device stream of kcamd::streamBytes layout
+    float* y[2];
+    int rows;
+    int q6;  // Q6_K (else Q4_K)
+};
+// parts[0..nparts) (at most 3) times the same per-256 activations (ncols columns of length k) in
+// one launch where the MFMA kernel applies, K split into ks <= 2 ranges: *used_ks = the split
+// taken (1: each y[0] holds the whole product; 2: y[0] + y[1] is the product).
+int launchMatmulGroup(const MmPart* parts, int nparts, const int* xq, int k, int ncols, int ks, int* used_ks,
+                      hipStream_t s);
 // layer_ops.hip
 int launchVectorAdd(const float* a, const float* b, float* out, int count, hipStream_t s);
-int launchAddSumsq(const float* a, const float* b, float* out, int* q, int n, int rows, hipStream_t s);
+// out = a + (b + b2) (b2 may be null: out = a + b; a null: the sums of squares of b (+ b2) only).
+int launchAddSumsq(const float* a, const float* b, float* out, int* q, int n, int rows, hipStream_t s,
+                   const float* b2 = nullptr);
 int launchNormMulQ8(bool per256, const kcNormMulQ8Args& a, hipStream_t s);
 int launchSiluMulQ8(bool per256, const kcSiluMulQ8FArgs& a, hipStream_t s);
 int launchMulRows(const kcMulRowsArgs& a, hipStream_t s);

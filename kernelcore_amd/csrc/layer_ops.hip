@@ -130,7 +130,8 @@ __device__ __forceinline__ void store4(float* p, float4 v) {
 // residual stream updated in place). One thread per block of 32, whose values it loads at once
 // and sums of squares in order.
 template <bool A16>
-__global__ void add_sumsq_kernel(const float* a, const float* b, float* out, int* __restrict__ q, int n, int rows) {
+__global__ void add_sumsq_kernel(const float* a, const float* b, const float* b2, float* out, int* __restrict__ q, int n,
+                                 int rows) {
     const int nb = n / 32;
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= nb * rows) return;
@@ -141,6 +142,13 @@ __global__ void add_sumsq_kernel(const float* a, const float* b, float* out, int
     for (int k = 0; k < 8; ++k) {
         const float4 bv = load4<A16>(b + o + 4 * k);
         v[4 * k] = bv.x, v[4 * k + 1] = bv.y, v[4 * k + 2] = bv.z, v[4 * k + 3] = bv.w;
+    }
+    if (b2) {  // a product split in two partial sums
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float4 bv = load4<A16>(b2 + o + 4 * k);
+            v[4 * k] += bv.x, v[4 * k + 1] += bv.y, v[4 * k + 2] += bv.z, v[4 * k + 3] += bv.w;
+        }
     }
     if (a) {
         float av[32];
@@ -474,12 +482,13 @@ int launchVectorAdd(const float* a, const float* b, float* out, int count, hipSt
 
 static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-int launchAddSumsq(const float* a, const float* b, float* out, int* q, int n, int rows, hipStream_t s) {
+int launchAddSumsq(const float* a, const float* b, float* out, int* q, int n, int rows, hipStream_t s,
+                   const float* b2) {
     const dim3 grid(blocksFor((long long)(n / 32) * rows));
-    if (al16(b) && (!a || (al16(a) && al16(out))))
-        hipLaunchKernelGGL(add_sumsq_kernel<true>, grid, dim3(256), 0, s, a, b, out, q, n, rows);
+    if (al16(b) && (!b2 || al16(b2)) && (!a || (al16(a) && al16(out))))
+        hipLaunchKernelGGL(add_sumsq_kernel<true>, grid, dim3(256), 0, s, a, b, b2, out, q, n, rows);
     else
-        hipLaunchKernelGGL(add_sumsq_kernel<false>, grid, dim3(256), 0, s, a, b, out, q, n, rows);
+        hipLaunchKernelGGL(add_sumsq_kernel<false>, grid, dim3(256), 0, s, a, b, b2, out, q, n, rows);
     return fromHip(hipGetLastError(), a ? "add_sumsq_f" : "sumsq_part");
 }
 

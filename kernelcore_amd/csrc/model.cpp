@@ -59,6 +59,7 @@ struct kcModel_st {
     // activations, sized for max_batch tokens
     float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *qr = nullptr, *kr = nullptr;
     float *att = nullptr, *o = nullptr, *gate = nullptr, *up = nullptr, *sw = nullptr, *down = nullptr;
+    float *o2 = nullptr, *down2 = nullptr;  // second K-range partial sums of the batch's o / down products
     float* logits = nullptr;
     int *slotE32 = nullptr, *slotEK = nullptr, *slotQ32 = nullptr, *slotQK = nullptr, *slotF32 = nullptr,
         *slotFK = nullptr;
@@ -135,11 +136,6 @@ int matvec(bool q6, const void* w, const int* slot, float* y, int rows, int k, h
     kcMatvecQ4Q8Args a{static_cast<const int*>(w), slot, reinterpret_cast<const float*>(slot + k / 32 * 8), y, nullptr,
                        rows, k};
     return kcamd::launchMatvecKq(q6, a, s);
-}
-
-int matmul(bool q6, const void* w, const int* slots, float* y, int rows, int k, int n, hipStream_t s) {
-    kcMatmulKQ8Args a{static_cast<const int*>(w), slots, y, nullptr, rows, k, n, 8};
-    return kcamd::launchMatmulKq(q6, true, a, s);
 }
 
 int normQ8(const float* x, const float* w, float* y, int* slot, int n, float eps, hipStream_t s) {
@@ -322,32 +318,41 @@ int batchStep(kcModel_st* m, int n, hipStream_t s) {
     KI_TRY(kcamd::launchPositions(m->n_past, n, m->pos, m->idx, m->n_ctx, s));
     KI_TRY(kcamd::launchGetRows(false, m->tok_embd, m->tokens, m->x, n, E_, s));
     float* x_last = m->x + (size_t)(n - 1) * E_;
+    // the products that read the same activations share one launch; o and down split K in two
+    // (the two partial sums are added in the residual add that consumes them)
+    const float* down2 = nullptr;
+    int ks = 1;
     for (int li = 0; li < c.n_layer; ++li) {
         const Layer& l = m->L[li];
         if (li == 0) KI_TRY(kcamd::launchAddSumsq(nullptr, m->x, nullptr, sums, E_, n, s));
-        else KI_TRY(kcamd::launchAddSumsq(m->x, m->down, m->x, sums, E_, n, s));
+        else KI_TRY(kcamd::launchAddSumsq(m->x, m->down, m->x, sums, E_, n, s, down2));
         kcNormMulQ8Args na{m->x, l.attn_norm, m->xn, m->slotEK, nullptr, E_, n, c.norm_eps};
         KI_TRY(kcamd::launchNormMulQ8(true, na, s));
-        KI_TRY(matmul(false, l.wq, m->slotEK, m->q, Q, E_, n, s));
-        KI_TRY(matmul(false, l.wk, m->slotEK, m->k, KV, E_, n, s));
-        KI_TRY(matmul(true, l.wv, m->slotEK, m->v, KV, E_, n, s));
+        const kcamd::MmPart qkv[3] = {{l.wq, {m->q, nullptr}, Q, 0}, {l.wk, {m->k, nullptr}, KV, 0},
+                                      {l.wv, {m->v, nullptr}, KV, 1}};
+        KI_TRY(kcamd::launchMatmulGroup(qkv, 3, m->slotEK, E_, n, 1, &ks, s));
         KI_TRY(qkNorm(m, l, n, s));
         KI_TRY(ropeQK(m, n, s));
         KI_TRY(kvStore(m, l, n, s));
         KI_TRY(attention(m, l, n, s));
         KI_TRY(kcamd::launchQuantizeColsK(m->att, m->slotQK, Q, n, s));
-        KI_TRY(matmul(false, l.wo, m->slotQK, m->o, E_, Q, n, s));
+        const kcamd::MmPart op{l.wo, {m->o, m->o2}, E_, 0};
+        KI_TRY(kcamd::launchMatmulGroup(&op, 1, m->slotQK, Q, n, 2, &ks, s));
+        const float* o2 = ks == 2 ? m->o2 : nullptr;
         if (li + 1 < c.n_layer) {
-            KI_TRY(kcamd::launchAddSumsq(m->x, m->o, m->x, sums, E_, n, s));
+            KI_TRY(kcamd::launchAddSumsq(m->x, m->o, m->x, sums, E_, n, s, o2));
             kcNormMulQ8Args fa{m->x, l.ffn_norm, m->xn, m->slotEK, nullptr, E_, n, c.norm_eps};
             KI_TRY(kcamd::launchNormMulQ8(true, fa, s));
-            KI_TRY(matmul(false, l.wg, m->slotEK, m->gate, c.n_ff, E_, n, s));
-            KI_TRY(matmul(false, l.wu, m->slotEK, m->up, c.n_ff, E_, n, s));
+            const kcamd::MmPart gu[2] = {{l.wg, {m->gate, nullptr}, c.n_ff, 0}, {l.wu, {m->up, nullptr}, c.n_ff, 0}};
+            KI_TRY(kcamd::launchMatmulGroup(gu, 2, m->slotEK, E_, n, 1, &ks, s));
             kcSiluMulQ8FArgs sa{m->gate, m->up, m->sw, m->slotFK, nullptr, c.n_ff, n};
             KI_TRY(kcamd::launchSiluMulQ8(true, sa, s));
-            KI_TRY(matmul(true, l.wd, m->slotFK, m->down, E_, c.n_ff, n, s));
+            const kcamd::MmPart dp{l.wd, {m->down, m->down2}, E_, 1};
+            KI_TRY(kcamd::launchMatmulGroup(&dp, 1, m->slotFK, c.n_ff, n, 2, &ks, s));
+            down2 = ks == 2 ? m->down2 : nullptr;
         } else {  // the last layer continues with the last token only
-            KI_TRY(kcamd::launchAddSumsq(x_last, m->o + (size_t)(n - 1) * E_, x_last, m->slotE32, E_, 1, s));
+            KI_TRY(kcamd::launchAddSumsq(x_last, m->o + (size_t)(n - 1) * E_, x_last, m->slotE32, E_, 1, s,
+                                         o2 ? o2 + (size_t)(n - 1) * E_ : nullptr));
             KI_TRY(ffnOne(m, l, x_last, s));
         }
     }
@@ -408,10 +413,12 @@ kcError_t kcModelCreate(const kcModelConfig* cfg, kcModel_t* out) noexcept {
     KM_A(m->v, (size_t)B * KV);
     KM_A(m->att, (size_t)B * Q);
     KM_A(m->o, (size_t)B * E_);
+    KM_A(m->o2, (size_t)B * E_);
     KM_A(m->gate, (size_t)B * F);
     KM_A(m->up, (size_t)B * F);
     KM_A(m->sw, (size_t)B * F);
     KM_A(m->down, (size_t)B * E_);
+    KM_A(m->down2, (size_t)B * E_);
     KM_A(m->logits, (size_t)c.n_vocab);
     KM_A(m->slotE32, (size_t)E_ / 32 * 11);
     KM_A(m->slotEK, (size_t)B * (E_ / 256 * 85 + E_ / 32 * 11));
