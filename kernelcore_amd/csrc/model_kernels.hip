@@ -201,39 +201,52 @@ __global__ void positions_kernel(const int* __restrict__ n_past, int n, int* pos
 }
 
 
-// Causal attention of a batch of N queries (positions p0 .. p0 + N - 1, p0 = T - N, T = *n_ctx)
-// on the matrix cores, v_mfma_f32_32x32x16_f16. Workgroup (query tile of 32, KV head) with one
-// wavefront per query head of the group. Pass 1 finds each query's maximum score over its keys,
-// pass 2 forms p = exp(s - max), its sum, and sum p V; the output is divided by the sum at the
-// end, so the softmax is FLASH_ATTN_EXT's exact one. k and v are fp16 in the cache; q and p are
-// each split into two fp16 operands, hi = fp16(x) and lo = fp16(x - hi), and every product runs as
-// two MFMAs, which keeps them within about 2^-22 of fp32 (one fp16 rounding of q or p would be
-// 2^-11: enough to flip the 8-bit quantization of the attention output downstream). p is scaled
-// by 2^10 before the split so that lo stays in fp16's normal range; the sum is divided back.
-// Scores are computed transposed, S^T = K Q^T (A = K rows from the cache, B = q as fp16 in
-// registers), which leaves each lane one query and 16 of the 32 keys of a block: lane (j, h)
-// holds keys 8a + 4h + b (value 4a + b). Those registers are directly the A operand of P V when
-// the MFMA's k index runs over the keys in that order, kappa(k) = {0,1,2,3,8,9,10,11 |
-// 4,5,6,7,12,13,14,15} (+16 for the second half of the block); the B operand (V) is read in the
-// same key order from a transposed copy of the V block in LDS.
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-template <int D, int G>
-__global__ __launch_bounds__(64 * G) void attn_prefill_kernel(const float* __restrict__ q, const int* __restrict__ kc,
-                                                              const int* __restrict__ vc, float* __restrict__ out,
-                                                              const int* __restrict__ n_ctx, AttnShape a) {
+// Causal attention of a batch of N queries (positions p0 .. p0 + N - 1, p0 = T - N, T = *n_ctx)
+// on the matrix cores, v_mfma_f32_32x32x16_f16, in one pass over the keys per (query tile of 32,
+// query head) workgroup of W wavefronts. k and v are fp16 in the cache; q and p are each split
+// into two fp16 operands, hi = fp16(x) and lo = fp16(x - hi), and every product runs as two MFMAs,
+// which keeps them within about 2^-22 of fp32 (one fp16 rounding of q or p would be 2^-11: enough
+// to flip the 8-bit quantization of the attention output downstream). p is scaled by 2^10 before
+// the split so that lo stays in fp16's normal range; the sum is divided back. Scores are computed
+// transposed, S^T = K Q^T (A = K rows from the cache, B = q), which leaves each lane one query and
+// 16 of the 32 keys of a block: lane (j, h) holds keys 8a + 4h + b (value 4a + b). Those registers
+// are directly the A operand of P V when the MFMA's k index runs over the keys in that order,
+// kappa(k) = {0,1,2,3,8,9,10,11 | 4,5,6,7,12,13,14,15} (+16 for the second half of the block).
+// Wavefront w of the workgroup: wavefront w takes the key blocks kb = w, w + W, .. and keeps its own
+// running maximum m and sum l per query (FLASH_ATTN_EXT's online softmax, ggml-cpu/ops.cpp), its
+// output accumulators rescaled by exp(m_old - m_new) before each block's P V; at the end the
+// partial results are merged, o = sum_w o_w exp(m_w - M) over l = sum_w l_w exp(m_w - M). Each
+// wavefront loads the K fragments and V rows of its next block into registers while it computes
+// the current one; V goes to the wavefront's own LDS buffer row-major (rows padded by 8 halves, so
+// the two halves of the wavefront read different banks) and each lane gathers its B operand,
+// V[keys kappa(k)][d], from there. Query tiles are dispatched longest first.
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
+template <int D, int W>
+__global__ __launch_bounds__(64 * W) void attn_prefill_kernel(const float* __restrict__ q, const int* __restrict__ kc,
+                                                               const int* __restrict__ vc, float* __restrict__ out,
+                                                               const int* __restrict__ n_ctx, AttnShape a) {
     constexpr int KS = D / 16, DB = D / 32;
-    constexpr int kVtStride = 40;  // halves per transposed V row (32 keys + 8 pad)
-    __shared__ _Float16 vt[D * kVtStride];
-    __shared__ float lsum[G][32];
+    constexpr int VR = D + 8;        // halves per V row in LDS
+    constexpr int CPR = D / 8;       // 16-byte chunks per V row
+    constexpr int RPL = 64 / CPR;    // V rows per wavefront load
+    constexpr int VL = 32 / RPL;     // loads per V block
+    // the V buffers, reused by the merge for the partial outputs of wavefronts 1 ..
+    constexpr int kLdsHalves = W * 32 * VR > (W - 1) * 32 * D * 2 ? W * 32 * VR : (W - 1) * 32 * D * 2;
+    __shared__ __attribute__((aligned(16))) _Float16 vsall[kLdsHalves];
+    __shared__ __attribute__((aligned(16))) float qx[W][4][32];
     const int T = *n_ctx, N = a.N, p0 = T - N;
-    const int i0 = blockIdx.x * 32, kvh = blockIdx.y;
+    const int tiles = (N + 31) / 32;
+    const int i0 = (tiles - 1 - (int)blockIdx.x) * 32;
+    const int head = blockIdx.y, kvh = head / (a.H / a.H_kv);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5;
-    const int head = kvh * G + wave;
+    _Float16* vs = vsall + wave * 32 * VR;
+    float* qw = qx[wave][0];
     const int* kb0 = kc + (size_t)kvh * (D / 2);
     const int* vb0 = vc + (size_t)kvh * (D / 2);
-    // q of this lane's query as the B operand (hi and lo parts): d = 16 ks + 8 h .. + 7
     h8 qb[KS], ql[KS];
     {
         const bool live = i0 + j < N;
@@ -246,9 +259,9 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(const float* __res
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const float x = live ? v[e] : 0.0f;
-                const _Float16 hi = (_Float16)x;
-                qb[ks][e] = hi;
-                ql[ks][e] = (_Float16)(x - (float)hi);
+                const _Float16 hq = (_Float16)x;
+                qb[ks][e] = hq;
+                ql[ks][e] = (_Float16)(x - (float)hq);
             }
         }
     }
@@ -257,90 +270,149 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(const float* __res
     f32x16 zero;
 #pragma unroll
     for (int v = 0; v < 16; ++v) zero[v] = 0.0f;
-    auto scores = [&](int kb) {
-        const int key = min(kb * 32 + j, T - 1);
-        const int* kr = kb0 + (size_t)key * a.kv_row + 4 * h;
-        h8 ka[KS];
+    h8 ka[KS], kn[KS];
+    u32x4v vr[VL];
+    auto loadK = [&](int kb, h8* dst) {
+        const int* kr = kb0 + (size_t)min(kb * 32 + j, T - 1) * a.kv_row + 4 * h;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) ka[ks] = *reinterpret_cast<const h8*>(kr + 8 * ks);
-        f32x16 sacc = zero;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks], qb[ks], sacc, 0, 0, 0);
-            sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks], ql[ks], sacc, 0, 0, 0);
-        }
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int key_abs = kb * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-            sacc[v] = key_abs <= qpos && key_abs < T ? a.scale * sacc[v] : -INFINITY;
-        }
-        return sacc;
+        for (int ks = 0; ks < KS; ++ks) dst[ks] = *reinterpret_cast<const h8*>(kr + 8 * ks);
     };
-    // ---- pass 1: the maximum score of each query
-    float m = -INFINITY;
-    for (int kb = 0; kb < nkb; ++kb) {
-        const f32x16 sacc = scores(kb);
+    auto loadV = [&](int kb) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) m = fmaxf(m, sacc[v]);
+        for (int r = 0; r < VL; ++r) {
+            const int key = min(kb * 32 + r * RPL + lane / CPR, T - 1);
+            vr[r] = *reinterpret_cast<const u32x4v*>(vb0 + (size_t)key * a.kv_row + (lane % CPR) * 4);
+        }
+    };
+    // LDS ordering among the lanes of this wavefront (its own buffers; waves run different counts)
+    auto waveSync = [] {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    if (wave < nkb) {
+        loadK(wave, ka);
+        loadV(wave);
     }
-    m = fmaxf(m, __shfl_xor(m, 32));
-    // ---- pass 2: p = exp(s - m), its sum, and sum p V
     f32x16 o[DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db) o[db] = zero;
-    float l = 0.0f;
-    for (int kb = 0; kb < nkb; ++kb) {
-        __syncthreads();  // the previous block's V reads are done
-        for (int c = threadIdx.x; c < 32 * (D / 8); c += 64 * G) {  // V block, transposed into LDS
-            const int kk = c / (D / 8), d0 = (c % (D / 8)) * 8;
-            const int key = kb * 32 + kk;
-            const uint4 w = *reinterpret_cast<const uint4*>(vb0 + (size_t)min(key, T - 1) * a.kv_row + d0 / 2);
-            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    float m = -INFINITY, l = 0.0f;
+    for (int kb = wave; kb < nkb; kb += W) {
+        waveSync();  // the previous block's LDS reads are done
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint32_t wv = key < T ? ws[e] : 0u;  // keys past T: zeros (their p is 0)
-                vt[(d0 + 2 * e) * kVtStride + kk] = __builtin_bit_cast(_Float16, (unsigned short)(wv & 0xFFFFu));
-                vt[(d0 + 2 * e + 1) * kVtStride + kk] = __builtin_bit_cast(_Float16, (unsigned short)(wv >> 16));
-            }
+        for (int r = 0; r < VL; ++r)
+            *reinterpret_cast<u32x4v*>(vs + (r * RPL + lane / CPR) * VR + (lane % CPR) * 8) = vr[r];
+        if (kb + W < nkb) {
+            loadK(kb + W, kn);
+            loadV(kb + W);
         }
-        const f32x16 sacc = scores(kb);
-        h8 pa[2], pl[2];
+        f32x16 sh = zero, sl = zero;  // two independent chains (q hi, q lo)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            sh = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks], qb[ks], sh, 0, 0, 0);
+            sl = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks], ql[ks], sl, 0, 0, 0);
+        }
+        f32x16 sacc;
+        float bm = -INFINITY;
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-            const float pv = sacc[v] == -INFINITY ? 0.0f : exp2f((sacc[v] - m) * kLog2e);
-            l += pv;
-            const float ps = pv * 1024.0f;
-            const _Float16 hi = (_Float16)ps;
-            pa[v >> 3][v & 7] = hi;
-            pl[v >> 3][v & 7] = (_Float16)(ps - (float)hi);
+            const int key_abs = kb * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+            sacc[v] = key_abs <= qpos && key_abs < T ? a.scale * (sh[v] + sl[v]) : -INFINITY;
+            bm = fmaxf(bm, sacc[v]);
         }
-        __syncthreads();  // V block staged
+        bm = fmaxf(bm, __shfl_xor(bm, 32));
+        const float mn = fmaxf(m, bm);
+        const float alpha = m == -INFINITY ? 0.0f : exp2f((m - mn) * kLog2e);
+        m = mn;
+        h8 pa[2], pl[2];
+        float ls = 0.0f;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const float pv = sacc[v] == -INFINITY ? 0.0f : exp2f((sacc[v] - mn) * kLog2e);
+            ls += pv;
+            const float ps = pv * 1024.0f;
+            const _Float16 hp = (_Float16)ps;
+            pa[v >> 3][v & 7] = hp;
+            pl[v >> 3][v & 7] = (_Float16)(ps - (float)hp);
+        }
+        l = l * alpha + ls;
+        if (h == 0) qw[j] = alpha;
+        waveSync();  // V block and the alphas staged
+        // rescale: this lane's accumulators hold queries 8 (v / 4) + 4 h + v % 4
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+            const float4 al = *reinterpret_cast<const float4*>(qw + 8 * g4 + 4 * h);
+            const float alv[4] = {al.x, al.y, al.z, al.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int db = 0; db < DB; ++db) o[db][4 * g4 + e] *= alv[e];
+        }
 #pragma unroll
         for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
-                const _Float16* vr = vt + (32 * db + j) * kVtStride + 16 * mm + 4 * h;
+                const _Float16* vp = vs + (16 * mm + 4 * h) * VR + 32 * db + j;
                 h8 vbv;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    vbv[e] = vr[e];
-                    vbv[4 + e] = vr[8 + e];
+                    vbv[e] = vp[e * VR];
+                    vbv[4 + e] = vp[(8 + e) * VR];
                 }
                 o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[mm], vbv, o[db], 0, 0, 0);
                 o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pl[mm], vbv, o[db], 0, 0, 0);
             }
+        if (kb + W < nkb)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) ka[ks] = kn[ks];
     }
+    // ---- merge: wavefronts 1.. hand (m, l, o) to wavefront 0 through LDS
     l += __shfl_xor(l, 32);
-    if (h == 0) lsum[wave][j] = l;
+    __syncthreads();  // every wavefront is done with its V buffer
+    if (h == 0) {
+        qx[wave][1][j] = m;
+        qx[wave][2][j] = l;
+    }
+    float* ob = reinterpret_cast<float*>(vsall);  // [W - 1][32 queries][D]
+    if (wave > 0) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int qi = 8 * (v >> 2) + 4 * h + (v & 3);
+#pragma unroll
+            for (int db = 0; db < DB; ++db) ob[((wave - 1) * 32 + qi) * D + 32 * db + j] = o[db][v];
+        }
+    }
     __syncthreads();
+    if (wave != 0) return;
+    if (h == 0) {  // per query: the merged maximum, each wavefront's factor and the merged sum
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < W; ++w) M = fmaxf(M, qx[w][1][j]);
+        float L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            const float mw = qx[w][1][j];
+            const float c = mw == -INFINITY ? 0.0f : exp2f((mw - M) * kLog2e);
+            qx[w][3][j] = c;
+            L += qx[w][2][j] * c;
+        }
+        qx[0][0][j] = L;
+    }
+    waveSync();
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
         const int qi = 8 * (v >> 2) + 4 * h + (v & 3);
         if (i0 + qi < N) {
-            const float inv = 1.0f / (lsum[wave][qi] * 1024.0f);
+            const float inv = 1.0f / (qx[0][0][qi] * 1024.0f);
+            const float c0 = qx[0][3][qi];
 #pragma unroll
-            for (int db = 0; db < DB; ++db)
-                out[(size_t)(i0 + qi) * a.q_tok + (size_t)head * D + 32 * db + j] = o[db][v] * inv;
+            for (int db = 0; db < DB; ++db) {
+                float acc = o[db][v] * c0;
+#pragma unroll
+                for (int w = 1; w < W; ++w) acc += ob[((w - 1) * 32 + qi) * D + 32 * db + j] * qx[w][3][qi];
+                out[(size_t)(i0 + qi) * a.q_tok + (size_t)head * D + 32 * db + j] = acc * inv;
+            }
         }
     }
 }
@@ -355,23 +427,24 @@ int launchGetRows(bool q6k, const void* qw, const int* tok, float* y, int n, int
     return fromHip(hipGetLastError(), "get_rows");
 }
 
-template <int D, int G>
+template <int D>
 static int runPrefill(const float* q, const int* k, const int* v, float* out, const int* n_ctx, const AttnShape& a,
-                      hipStream_t s) {
-    const dim3 grid((a.N + 31) / 32, a.H_kv);
-    hipLaunchKernelGGL((attn_prefill_kernel<D, G>), grid, dim3(64 * G), 0, s, q, k, v, out, n_ctx, a);
+                       hipStream_t s) {
+    const dim3 grid((a.N + 31) / 32, a.H);
+    // key blocks split over 2 wavefronts for D = 128 (registers: one wavefront per SIMD), over 4
+    // for D = 64 (two per SIMD)
+    if (D == 128)
+        hipLaunchKernelGGL((attn_prefill_kernel<D, 2>), grid, dim3(128), 0, s, q, k, v, out, n_ctx, a);
+    else
+        hipLaunchKernelGGL((attn_prefill_kernel<D, 4>), grid, dim3(256), 0, s, q, k, v, out, n_ctx, a);
     return fromHip(hipGetLastError(), "attn (prefill)");
 }
 
 int launchAttn(const float* q, const int* k, const int* v, float* out, const int* n_ctx, const AttnShape& a,
                hipStream_t s) {
-    const int G = a.H / a.H_kv;
-    if (a.N > 1 && a.causal && option("attn_path") != 1) {  // the matrix-core prefill attention
-#define KC_AP(DD, GG) \
-        if (a.D == DD && G == GG) return runPrefill<DD, GG>(q, k, v, out, n_ctx, a, s);
-        KC_AP(128, 1) KC_AP(128, 2) KC_AP(128, 3) KC_AP(128, 4) KC_AP(128, 8)
-        KC_AP(64, 1) KC_AP(64, 2) KC_AP(64, 3) KC_AP(64, 4) KC_AP(64, 8)
-#undef KC_AP
+    const int ap = option("attn_path");
+    if (a.N > 1 && a.causal && ap == 0 && (a.D == 64 || a.D == 128)) {  // matrix cores, one pass
+        return a.D == 128 ? runPrefill<128>(q, k, v, out, n_ctx, a, s) : runPrefill<64>(q, k, v, out, n_ctx, a, s);
     }
     const size_t lds = sizeof(float) * ((size_t)a.max_t + 256 + 64);
     static const int attr = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(attn_kernel),
