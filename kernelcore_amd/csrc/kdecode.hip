@@ -462,13 +462,37 @@ __device__ __forceinline__ float dppSum(float v) {
     return v;
 }
 
+// Maximum / sum over the 64 lanes of a wavefront: row-local DPP moves, then the four row results
+// read back with readlane (scalar), so no LDS permutes.
+__device__ __forceinline__ float waveMax64(float v) {
+    v = fmaxf(v, dppMove<0xB1>(v));
+    v = fmaxf(v, dppMove<0x4E>(v));
+    v = fmaxf(v, dppMove<0x141>(v));
+    v = fmaxf(v, dppMove<0x140>(v));
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+__device__ __forceinline__ float waveSum64(float v) {
+    v = dppSum<16>(v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
 // Workgroup (chunk c, KV head g) of 256 threads: the attention of one token at position p = pos[0]
 // against positions [64c, 64c + 64) of the context T = p + 1 (FLASH_ATTN_EXT: s = scale q.k,
 // softmax, sum p v) for the G = H / Hkv query heads of g. Each workgroup first normalizes
 // (Qwen3, rms_norm.cu) and ropes (rope_ggml.cu) its query heads; the workgroup of the last chunk
 // does the same for k, stores k and v as fp16 into cache row p (set_rows_f16.cu) and takes
 // position p from LDS, the others read positions below p from the cache. Partial results (max,
-// sum of exp, unnormalized output) go to part, which attn_merge_kernel combines.
+// sum of exp, unnormalized output) go to part, which attn_merge_kernel combines. (Merging in the
+// workgroup that arrives last, counted with a device-scope atomic, was slower here: the release
+// fence each workgroup needs writes the XCD's L2 back.)
 // LP lanes hold one position's D values, 8 each (D = 8 LP).
 template <int D>
 __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
@@ -477,7 +501,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
     constexpr int NI = (kChunk / 4) / PPI;  // instructions per wave (16 positions per wave)
     constexpr int pairs = D / 2;
     __shared__ float sc[kMaxGroup][kChunk];
-    __shared__ float red[4][kMaxGroup * D];
+    __shared__ float red[16][kMaxGroup * D];  // [wave * 4 + row of 16 lanes][head * D + d]
     __shared__ float mg[kMaxGroup], lg[kMaxGroup];
     __shared__ float qs[kMaxGroup * D];
     __shared__ float raw[(kMaxGroup + 2) * D];
@@ -579,13 +603,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
     __syncthreads();
     for (int g = wave; g < G; g += 4) {  // one wavefront per head: lane = position
         const float s = sc[g][lane];
-        float m = s;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+        const float m = waveMax64(s);
         const float pr = s == -INFINITY ? 0.0f : exp2f((s - m) * kLog2e);
-        float sum = pr;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) sum += __shfl_xor(sum, o);
+        const float sum = waveSum64(pr);
         sc[g][lane] = pr;
         if (lane == 0) {
             mg[g] = m;
@@ -616,25 +636,26 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
             }
         }
     }
-    // reduce over the position slots of the wave, then over the four waves
+    // the position slots through LDS, one row of 16 lanes per LDS row (for D = 64 the two slots of
+    // a row are added first, lane l + 8 into lane l), summed in row order
+    static_assert(LP == 8 || LP == 16, "lanes per position");
 #pragma unroll
-    for (int g = 0; g < kMaxGroup; ++g) {
-        if (g < G) {
+    for (int g = 0; g < kMaxGroup; ++g)
+        if (g < G)
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 float v = acc[g][e];
-#pragma unroll
-                for (int o = LP; o < 64; o <<= 1) v += __shfl_xor(v, o);
-                acc[g][e] = v;
+                if (LP == 8) v += dppMove<0x128>(v);  // row_ror:8
+                if (LP == 16 || (lane & 8) == 0) red[wave * 4 + (lane >> 4)][g * D + l * 8 + e] = v;
             }
-            if (sub == 0)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) red[wave][g * D + l * 8 + e] = acc[g][e];
-        }
-    }
     __syncthreads();
     float* pp = a.part + ((size_t)kvh * a.max_chunks + c) * kMaxGroup * (D + 2);
-    for (int i = tid; i < G * D; i += 256) pp[(i / D) * (D + 2) + i % D] = red[0][i] + red[1][i] + red[2][i] + red[3][i];
+    for (int i = tid; i < G * D; i += 256) {
+        float v = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) v += red[r][i];
+        pp[(i / D) * (D + 2) + i % D] = v;
+    }
     if (tid < G) {
         pp[tid * (D + 2) + D] = mg[tid];
         pp[tid * (D + 2) + D + 1] = lg[tid];
@@ -666,9 +687,9 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnDecodeArgs a) {
             for (int u = 0; u < 16; ++u) {
                 if (c0 + u < nch) {
                     if (mv[u] > M) {
-                        const float sc = exp2f((M - mv[u]) * kLog2e);
-                        L *= sc;
-                        O *= sc;
+                        const float f = exp2f((M - mv[u]) * kLog2e);
+                        L *= f;
+                        O *= f;
                         M = mv[u];
                     }
                     const float f = exp2f((mv[u] - M) * kLog2e);
@@ -683,7 +704,6 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnDecodeArgs a) {
     const int nbl = G * D / 32;
     if (tid < nbl) storeQ32(a.slot, a.nq, kvh * nbl + tid, quant32Seq(vb + tid * 33));
 }
-
 
 }  // namespace
 
