@@ -320,6 +320,100 @@ __global__ void set_rows_kernel(const float* __restrict__ src, const int* __rest
     dst[(size_t)row * dst_row + j] = (int)(f2h(sp[0]) | (f2h(sp[1]) << 16));
 }
 
+// ---------------------------------------------------------------- fused batch kernels (model path)
+
+// RoPE of q (nh heads) and k (nkv heads) of a batch, and the fp16 stores of the roped k and of v
+// into the cache rows pos[t] (rope_ggml.cu, set_rows_f16.cu): one thread per (token, group of 4
+// heads, pair), which takes theta, its cosine and sine once for its heads (q heads first, then the
+// k heads with their v). Rows outside [0, dst_rows) are not stored.
+__global__ void rope_qk_store_kernel(const float* __restrict__ q, float* __restrict__ qr, const float* __restrict__ k,
+                                     const float* __restrict__ v, unsigned short* __restrict__ kc,
+                                     unsigned short* __restrict__ vc, const int* __restrict__ pos,
+                                     const float* __restrict__ ff, int pairs, int nh, int nkv, int n, float log2_base,
+                                     int m1, int m2, int dst_row, int dst_rows) {
+    const int ng = (nh + nkv + 3) / 4;
+    const long long idx = blockIdx.x * (long long)blockDim.x + threadIdx.x;
+    if (idx >= (long long)n * ng * pairs) return;
+    const int i = (int)(idx % pairs);
+    const long long tg = idx / pairs;
+    const int hg = (int)(tg % ng), t = (int)(tg / ng);
+    const int p = pos[t];
+    const float theta = (float)p * exp2f(-(float)i / (float)pairs * log2_base) / ff[i];
+    const float c = cosf(theta), sn = sinf(theta);
+    const bool store = p >= 0 && p < dst_rows;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int h = hg * 4 + u;
+        if (h < nh) {
+            const size_t a = 2 * ((size_t)t * nh + h) * pairs + (size_t)i * m1;
+            const float x0 = q[a], x1 = q[a + m2];
+            qr[a] = x0 * c - x1 * sn;
+            qr[a + m2] = x0 * sn + x1 * c;
+        } else if (h < nh + nkv && store) {
+            const int hk = h - nh;
+            const size_t a = 2 * ((size_t)t * nkv + hk) * pairs + (size_t)i * m1;
+            const size_t e = (size_t)p * dst_row * 2 + 2 * (size_t)hk * pairs + (size_t)i * m1;
+            const float x0 = k[a], x1 = k[a + m2];
+            kc[e] = (unsigned short)f2h(x0 * c - x1 * sn);
+            kc[e + m2] = (unsigned short)f2h(x0 * sn + x1 * c);
+            vc[e] = (unsigned short)f2h(v[a]);
+            vc[e + m2] = (unsigned short)f2h(v[a + m2]);
+        }
+    }
+}
+
+// Residual add + RMS norm + per-256 quantization of a batch (add_sumsq_f.cu then norm_mul_q8k_f.cu
+// in one workgroup per row): x = a + (b [+ b2]) (a null: x = b, not stored), the per-32 sums of
+// squares in order, their total in block order, y = x r w quantized per 256 into the row's slot.
+// The row is loaded with all 256 threads (coalesced) into LDS, blocks of 32 padded to 36 floats
+// so that the per-block sums (one thread each, in order) read different banks.
+template <bool A16>
+__global__ __launch_bounds__(256) void add_norm_q8k_kernel(const float* a, const float* b, const float* b2, float* out,
+                                                           const float* __restrict__ w, int* __restrict__ q, int n,
+                                                           float eps) {
+    extern __shared__ float xs[];  // n / 32 blocks of 36 floats, then n / 32 sums of squares
+    const int nsb = n / 256, nb = n / 32;
+    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float* ss = xs + nb * 36;
+    const size_t r0 = (size_t)row * n;
+    for (int i = 4 * tid; i < n; i += 1024) {
+        float4 v = load4<A16>(b + r0 + i);
+        if (b2) {
+            const float4 u = load4<A16>(b2 + r0 + i);
+            v.x += u.x, v.y += u.y, v.z += u.z, v.w += u.w;
+        }
+        if (a) {
+            const float4 x = load4<A16>(a + r0 + i);
+            v = make_float4(x.x + v.x, x.y + v.y, x.z + v.z, x.w + v.w);
+            store4<A16>(out + r0 + i, v);
+        }
+        *reinterpret_cast<float4*>(xs + (i >> 5) * 36 + (i & 31)) = v;
+    }
+    __syncthreads();
+    for (int bl = tid; bl < nb; bl += 256) {
+        const float* xb = xs + bl * 36;
+        float sq = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float4 v = *reinterpret_cast<const float4*>(xb + 4 * k);
+            sq += v.x * v.x;
+            sq += v.y * v.y;
+            sq += v.z * v.z;
+            sq += v.w * v.w;
+        }
+        ss[bl] = sq;
+    }
+    __syncthreads();
+    const float r = rmsScale(ss, nb, n, eps);
+    int* qr = q + (size_t)row * nsb * 85;
+    for (int sb = wave; sb < nsb; sb += 4) {
+        const int e = sb * 256 + 4 * lane;
+        const float4 xv = *reinterpret_cast<const float4*>(xs + (e >> 5) * 36 + (e & 31));
+        const float4 wv = load4<A16>(w + e);
+        quant256Wave(xv.x * r * wv.x, xv.y * r * wv.y, xv.z * r * wv.z, xv.w * r * wv.w, qr, nsb, sb);
+    }
+}
+
 // ---------------------------------------------------------------- FLASH_ATTN_EXT over an fp16 cache
 
 __device__ __forceinline__ float h2f(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (unsigned short)h); }
@@ -543,6 +637,29 @@ int launchRope(const kcRopeGgmlArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(rope_kernel, dim3(blocksFor(count)), dim3(256), 0, s, a.x, a.y, a.pos, a.ff, pairs, a.n_head,
                        count, a.log2_base, a.neox ? 1 : 2, a.neox ? pairs : 1);
     return fromHip(hipGetLastError(), "rope_ggml");
+}
+
+int launchRopeQKStore(const float* q, float* qr, const float* k, const float* v, int* kcache, int* vcache,
+                      const int* pos, const float* ff, int head_dim, int nh, int nkv, int n, float log2_base, int neox,
+                      int dst_row, int dst_rows, hipStream_t s) {
+    const int pairs = head_dim / 2;
+    const long long threads = (long long)n * ((nh + nkv + 3) / 4) * pairs;
+    hipLaunchKernelGGL(rope_qk_store_kernel, dim3(blocksFor(threads)), dim3(256), 0, s, q, qr, k, v,
+                       reinterpret_cast<unsigned short*>(kcache), reinterpret_cast<unsigned short*>(vcache), pos, ff,
+                       pairs, nh, nkv, n, log2_base, neox ? 1 : 2, neox ? pairs : 1, dst_row, dst_rows);
+    return fromHip(hipGetLastError(), "rope + kv store");
+}
+
+int launchAddNormQ8K(const float* a, const float* b, const float* b2, float* out, const float* w, int* q, int n,
+                     int rows, float eps, hipStream_t s) {
+    if (rows <= 0) return 0;
+    const size_t lds = sizeof(float) * ((size_t)n / 32 * 37);
+    if (n % 256 || lds > 65536) return fromHip(hipErrorInvalidValue, "add + norm: row length");
+    if (al16(b) && (!b2 || al16(b2)) && (!a || (al16(a) && al16(out))) && al16(w))
+        hipLaunchKernelGGL(add_norm_q8k_kernel<true>, dim3(rows), dim3(256), lds, s, a, b, b2, out, w, q, n, eps);
+    else
+        hipLaunchKernelGGL(add_norm_q8k_kernel<false>, dim3(rows), dim3(256), lds, s, a, b, b2, out, w, q, n, eps);
+    return fromHip(hipGetLastError(), "add + norm");
 }
 
 int launchSetRows(const kcSetRowsF16Args& a, hipStream_t s) {

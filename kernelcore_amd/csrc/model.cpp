@@ -314,7 +314,6 @@ int batchStep(kcModel_st* m, int n, hipStream_t s) {
     const auto& c = m->c;
     const int Q = c.n_head * c.head_dim, KV = c.n_head_kv * c.head_dim;
     const int E_ = c.n_embd;
-    int* sums = m->slotEK + (size_t)n * (E_ / 256) * 85;  // per-32 slots holding the partial sums
     KI_TRY(kcamd::launchPositions(m->n_past, n, m->pos, m->idx, m->n_ctx, s));
     KI_TRY(kcamd::launchGetRows(false, m->tok_embd, m->tokens, m->x, n, E_, s));
     float* x_last = m->x + (size_t)(n - 1) * E_;
@@ -324,25 +323,25 @@ int batchStep(kcModel_st* m, int n, hipStream_t s) {
     int ks = 1;
     for (int li = 0; li < c.n_layer; ++li) {
         const Layer& l = m->L[li];
-        if (li == 0) KI_TRY(kcamd::launchAddSumsq(nullptr, m->x, nullptr, sums, E_, n, s));
-        else KI_TRY(kcamd::launchAddSumsq(m->x, m->down, m->x, sums, E_, n, s, down2));
-        kcNormMulQ8Args na{m->x, l.attn_norm, m->xn, m->slotEK, nullptr, E_, n, c.norm_eps};
-        KI_TRY(kcamd::launchNormMulQ8(true, na, s));
+        // residual add (layer 0: the embeddings) + RMS norm + per-256 quantization in one kernel
+        if (li == 0) KI_TRY(kcamd::launchAddNormQ8K(nullptr, m->x, nullptr, nullptr, l.attn_norm, m->slotEK, E_, n,
+                                                    c.norm_eps, s));
+        else KI_TRY(kcamd::launchAddNormQ8K(m->x, m->down, down2, m->x, l.attn_norm, m->slotEK, E_, n, c.norm_eps, s));
         const kcamd::MmPart qkv[3] = {{l.wq, {m->q, nullptr}, Q, 0}, {l.wk, {m->k, nullptr}, KV, 0},
                                       {l.wv, {m->v, nullptr}, KV, 1}};
         KI_TRY(kcamd::launchMatmulGroup(qkv, 3, m->slotEK, E_, n, 1, &ks, s));
         KI_TRY(qkNorm(m, l, n, s));
-        KI_TRY(ropeQK(m, n, s));
-        KI_TRY(kvStore(m, l, n, s));
+        // RoPE of q and k with the fp16 cache stores of k and v in one kernel
+        KI_TRY(kcamd::launchRopeQKStore(c.qk_norm ? m->att : m->q, m->qr, c.qk_norm ? m->kr : m->k, m->v, l.kcache,
+                                        l.vcache, m->pos, m->ones, c.head_dim, c.n_head, c.n_head_kv, n,
+                                        std::log2(c.rope_theta), c.rope_neox, KV / 2, c.max_ctx, s));
         KI_TRY(attention(m, l, n, s));
         KI_TRY(kcamd::launchQuantizeColsK(m->att, m->slotQK, Q, n, s));
         const kcamd::MmPart op{l.wo, {m->o, m->o2}, E_, 0};
         KI_TRY(kcamd::launchMatmulGroup(&op, 1, m->slotQK, Q, n, 2, &ks, s));
         const float* o2 = ks == 2 ? m->o2 : nullptr;
         if (li + 1 < c.n_layer) {
-            KI_TRY(kcamd::launchAddSumsq(m->x, m->o, m->x, sums, E_, n, s, o2));
-            kcNormMulQ8Args fa{m->x, l.ffn_norm, m->xn, m->slotEK, nullptr, E_, n, c.norm_eps};
-            KI_TRY(kcamd::launchNormMulQ8(true, fa, s));
+            KI_TRY(kcamd::launchAddNormQ8K(m->x, m->o, o2, m->x, l.ffn_norm, m->slotEK, E_, n, c.norm_eps, s));
             const kcamd::MmPart gu[2] = {{l.wg, {m->gate, nullptr}, c.n_ff, 0}, {l.wu, {m->up, nullptr}, c.n_ff, 0}};
             KI_TRY(kcamd::launchMatmulGroup(gu, 2, m->slotEK, E_, n, 1, &ks, s));
             kcSiluMulQ8FArgs sa{m->gate, m->up, m->sw, m->slotFK, nullptr, c.n_ff, n};
