@@ -899,7 +899,8 @@ size_t actBytes(int ncols, int k) {
 
 // The fp16-activation kernel over parts[0..nparts) (one conversion of the activations), K split
 // into ks ranges.
-int runMfmaH(const MmPart* parts, int nparts, const int* xq, int k, int ncols, int ks, void* act, hipStream_t s) {
+int runMfmaH(const MmPart* parts, int nparts, const int* xq, int k, int ncols, int ks, void* act, hipStream_t s,
+             const ActF16* pre = nullptr) {
     using G = HGeo<2>;
     static const int attr = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(matmul_kq_mfma_h_kernel),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, G::kLds);
@@ -917,12 +918,22 @@ int runMfmaH(const MmPart* parts, int nparts, const int* xq, int k, int ncols, i
     g.nparts = nparts;
     g.ks = ks;
     const long long words = (long long)ncols * nsb * 64;
-    _Float16* mins = static_cast<_Float16*>(act) + (size_t)ncols * k;
-    float* xdT = reinterpret_cast<float*>(mins + (size_t)ncols * nsb * 16);
-    const int ncp = actCols(ncols);
-    hipLaunchKernelGGL(act_to_f16_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, s, xq,
-                       static_cast<uint2*>(act), any_q4 ? reinterpret_cast<h8*>(mins) : nullptr, xdT, nsb, words,
-                       ncols, ncp);
+    _Float16* mins;
+    float* xdT;
+    int ncp;
+    if (pre) {  // written by the quantizer
+        act = pre->act;
+        mins = static_cast<_Float16*>(pre->mins);
+        xdT = pre->xdT;
+        ncp = pre->ncp;
+    } else {
+        mins = static_cast<_Float16*>(act) + (size_t)ncols * k;
+        xdT = reinterpret_cast<float*>(mins + (size_t)ncols * nsb * 16);
+        ncp = actCols(ncols);
+        hipLaunchKernelGGL(act_to_f16_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, s, xq,
+                           static_cast<uint2*>(act), any_q4 ? reinterpret_cast<h8*>(mins) : nullptr, xdT, nsb, words,
+                           ncols, ncp);
+    }
     const dim3 grid(tiles, (ncols + G::kCols - 1) / G::kCols, ks);
     hipLaunchKernelGGL(matmul_kq_mfma_h_kernel, grid, dim3(256), G::kLds, s, g, static_cast<const _Float16*>(act),
                        mins, xdT, nsb, ncols, ncp);
@@ -959,12 +970,16 @@ int launchMatmulMfma(bool q6k, const kcMatmulKQ8Args& a, hipStream_t s) {
 }
 
 int launchMatmulGroup(const MmPart* parts, int nparts, const int* xq, int k, int ncols, int ks, int* used_ks,
-                      hipStream_t s) {
+                      hipStream_t s, const ActF16* pre) {
     *used_ks = 1;
     if (nparts < 1 || nparts > 3 || ks < 1 || ks > 2 || k % 256 != 0) return fromHip(hipErrorInvalidValue, "matmul group");
     if (ncols >= 64 && mfmaHUsable(ncols, k)) {
+        if (ks > k / 256) ks = 1;
+        if (pre) {
+            *used_ks = ks;
+            return runMfmaH(parts, nparts, xq, k, ncols, ks, nullptr, s, pre);
+        }
         if (void* act = actBuffer(s, actBytes(ncols, k))) {
-            if (ks > k / 256) ks = 1;
             *used_ks = ks;
             return runMfmaH(parts, nparts, xq, k, ncols, ks, act, s);
         }

@@ -148,8 +148,11 @@ __global__ void quantize_q8_kernel(const float* __restrict__ x, int* __restrict_
 
 // Per-256 slots (quantize_cols_k.cu:20-74): one wavefront per (column, super-block); lane L packs
 // word L (values 4L..4L+3), sums of 16 come from lanes 4g..4g+3, sums of 32 from lanes 8i..8i+7.
+// ao (has_ao): the same codes also in the MFMA matmul's layout (ActF16): fp16 codes, the min
+// operands 64 (B_i >> 6) and B_i & 63 from lanes 8i, the scale from lane 0.
 template <bool Vec>
-__global__ void quantize_k_kernel(const float* __restrict__ x, int* __restrict__ q, int nsb, int count) {
+__global__ void quantize_k_kernel(const float* __restrict__ x, int* __restrict__ q, int nsb, int count, ActF16 ao,
+                                  int has_ao) {
     const int wid = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     const int lane = threadIdx.x & 63;
     if (wid >= count) return;  // whole wavefronts
@@ -181,6 +184,20 @@ __global__ void quantize_k_kernel(const float* __restrict__ x, int* __restrict__
     if (lane == 0) {
         for (int i = 0; i < 4; ++i) qc[nsb * 81 + s * 4 + i] = pw[i];
         reinterpret_cast<float*>(qc + nsb * 64)[s] = d;
+    }
+    if (has_ao) {
+        const int k = nsb * 256;
+        typedef _Float16 hv4 __attribute__((ext_vector_type(4)));
+        hv4 hq;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) hq[e] = (_Float16)(float)((word << (24 - 8 * e)) >> 24);
+        *reinterpret_cast<hv4*>(static_cast<_Float16*>(ao.act) + (size_t)c * k + s * 256 + 4 * lane) = hq;
+        if ((lane & 7) == 0) {
+            _Float16* mn = static_cast<_Float16*>(ao.mins) + ((size_t)c * nsb + s) * 16 + (lane >> 3);
+            mn[0] = (_Float16)(float)(64 * (s32 >> 6));
+            mn[8] = (_Float16)(float)(s32 & 63);
+        }
+        if (lane == 0) ao.xdT[(size_t)s * ao.ncp + c] = d;
     }
 }
 
@@ -348,12 +365,14 @@ int launchQuantizeCols(const float* x, int* q, int k, int ncols, hipStream_t s) 
     return fromHip(hipGetLastError(), "quantize_cols");
 }
 
-int launchQuantizeColsK(const float* x, int* q, int k, int ncols, hipStream_t s) {
+int launchQuantizeColsK(const float* x, int* q, int k, int ncols, hipStream_t s, const ActF16* ao) {
     const int nsb = k / 256;
     const long long waves = (long long)nsb * ncols;
     const dim3 grid((unsigned)((waves + 3) / 4));
-    if (aligned16(x)) hipLaunchKernelGGL(quantize_k_kernel<true>, grid, dim3(256), 0, s, x, q, nsb, (int)waves);
-    else hipLaunchKernelGGL(quantize_k_kernel<false>, grid, dim3(256), 0, s, x, q, nsb, (int)waves);
+    const ActF16 a = ao ? *ao : ActF16{};
+    if (aligned16(x))
+        hipLaunchKernelGGL(quantize_k_kernel<true>, grid, dim3(256), 0, s, x, q, nsb, (int)waves, a, ao ? 1 : 0);
+    else hipLaunchKernelGGL(quantize_k_kernel<false>, grid, dim3(256), 0, s, x, q, nsb, (int)waves, a, ao ? 1 : 0);
     return fromHip(hipGetLastError(), "quantize_cols_k");
 }
 

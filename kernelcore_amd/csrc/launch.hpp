@@ -8,11 +8,34 @@
 
 namespace kcamd {
 
+// The MFMA matmul's activation operands of a batch of ncols per-256-quantized columns of length k,
+// as a quantizer can write them next to the slots: the int8 values as fp16 act[ncols][k], the
+// Q4_K min operands mins[ncols][k / 256][16] (fp16: 64 (B_j >> 6) for the 8 sums B_j of 32, then
+// B_j & 63) and the scales xdT[k / 256][ncp], ncp = ncols rounded up to 128.
+struct ActF16 {
+    void* act;
+    void* mins;
+    float* xdT;
+    int ncp;
+};
+inline int actF16Cols(int ncols) { return (ncols + 127) / 128 * 128; }
+// Bytes of an ActF16 buffer for up to max_cols columns (act, then mins, then xdT).
+inline size_t actF16Bytes(int max_cols, int k) {
+    return (size_t)max_cols * k * 2 + (size_t)max_cols * (k / 256) * 32 + (size_t)(k / 256) * actF16Cols(max_cols) * 4;
+}
+// The ActF16 view of such a buffer for ncols columns.
+inline ActF16 actF16View(void* base, int max_cols, int k, int ncols) {
+    char* b = static_cast<char*>(base);
+    return ActF16{b, b + (size_t)max_cols * k * 2, reinterpret_cast<float*>(b + (size_t)max_cols * k * 2 + (size_t)max_cols * (k / 256) * 32),
+                  actF16Cols(ncols)};
+}
+
+
 // kquant.hip
 int launchRepack(const kcKquantRepackArgs& a, bool unpack, hipStream_t s);
 int launchQuantizeQ8x4(const float* x, int* xq, float* xd, int count, hipStream_t s);
 int launchQuantizeCols(const float* x, int* q, int k, int ncols, hipStream_t s);
-int launchQuantizeColsK(const float* x, int* q, int k, int ncols, hipStream_t s);
+int launchQuantizeColsK(const float* x, int* q, int k, int ncols, hipStream_t s, const ActF16* ao = nullptr);
 int launchMatvecKq(bool q6k, const kcMatvecQ4Q8Args& a, hipStream_t s);
 // kmatmul.hip: column-tiled matmul (any ncols; bit-identical per column to the reference).
 int launchMatmulCols(bool q6k, bool per256, const kcMatmulKQ8Args& a, hipStream_t s);
@@ -30,8 +53,9 @@ struct MmPart {
 // parts[0..nparts) (at most 3) times the same per-256 activations (ncols columns of length k) in
 // one launch where the MFMA kernel applies, K split into ks <= 2 ranges: *used_ks = the split
 // taken (1: each y[0] holds the whole product; 2: y[0] + y[1] is the product).
+// pre (may be null): the activations already in the MFMA layout (then no conversion is launched).
 int launchMatmulGroup(const MmPart* parts, int nparts, const int* xq, int k, int ncols, int ks, int* used_ks,
-                      hipStream_t s);
+                      hipStream_t s, const ActF16* pre = nullptr);
 // layer_ops.hip
 int launchVectorAdd(const float* a, const float* b, float* out, int count, hipStream_t s);
 // out = a + (b + b2) (b2 may be null: out = a + b; a null: the sums of squares of b (+ b2) only).
@@ -41,8 +65,10 @@ int launchNormMulQ8(bool per256, const kcNormMulQ8Args& a, hipStream_t s);
 // Batch fusions of the model path: x = a + (b [+ b2]) into out (a null: x = b), RMS norm with w
 // and per-256 quantization into q (rows slots of n / 256 * 85 ints); RoPE of q into qr and of k,
 // with k and v stored as fp16 into cache rows pos[t] (dst_row 32-bit words per row).
+// (ao, when given, also receives the MFMA layout of the quantized rows.)
 int launchAddNormQ8K(const float* a, const float* b, const float* b2, float* out, const float* w, int* q, int n,
-                     int rows, float eps, hipStream_t s);
+                     int rows, float eps, hipStream_t s, const ActF16* ao = nullptr);
+int launchSiluMulQ8KAct(const kcSiluMulQ8FArgs& a, const ActF16* ao, hipStream_t s);
 int launchRopeQKStore(const float* q, float* qr, const float* k, const float* v, int* kcache, int* vcache,
                       const int* pos, const float* ff, int head_dim, int nh, int nkv, int n, float log2_base, int neox,
                       int dst_row, int dst_rows, hipStream_t s);

@@ -12,6 +12,7 @@
 // GPU's own math library, within a few ulps of the CPU's.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 
 #include "internal.hpp"
@@ -82,10 +83,34 @@ __device__ __forceinline__ float waveMax(float v) {
     return fmaxf(fmaxf(laneF(v, 0), laneF(v, 16)), fmaxf(laneF(v, 32), laneF(v, 48)));
 }
 
+// The MFMA layout of one quantized super-block (ActF16): lane L's four codes as fp16, lanes 8i
+// (holding the sum B_i of values 32i .. 32i + 31 in b32) the two min operands of sub-block i,
+// lane 0 the scale.
+__device__ __forceinline__ void actF16Store(const ActF16& ao, int nsb, int s, int col, int lane, int c0, int c1, int c2,
+                                            int c3, int b32, float d) {
+    const int k = nsb * 256;
+    typedef _Float16 hv4 __attribute__((ext_vector_type(4)));
+    hv4 hq;
+    hq[0] = (_Float16)(float)c0;
+    hq[1] = (_Float16)(float)c1;
+    hq[2] = (_Float16)(float)c2;
+    hq[3] = (_Float16)(float)c3;
+    *reinterpret_cast<hv4*>(static_cast<_Float16*>(ao.act) + (size_t)col * k + s * 256 + 4 * lane) = hq;
+    if ((lane & 7) == 0) {
+        _Float16* mn = static_cast<_Float16*>(ao.mins) + ((size_t)col * nsb + s) * 16 + (lane >> 3);
+        mn[0] = (_Float16)(float)(64 * (b32 >> 6));
+        mn[8] = (_Float16)(float)(b32 & 63);
+    }
+    if (lane == 0) ao.xdT[(size_t)s * ao.ncp + col] = d;
+}
+
 // One super-block of 256 values, four per lane (lane L holds values 4L .. 4L + 3), into a
 // per-256 slot of nsb super-blocks (quantize_cols_k.cu / quant256 above): the same values, the
 // max and the integer sums taken across lanes (both exact in any order).
-__device__ __forceinline__ void quant256Wave(float y0, float y1, float y2, float y3, int* qc, int nsb, int s) {
+// ao (optional): the same codes as fp16, the min operands and the scale in the MFMA matmul's
+// layout (ActF16) for column col.
+__device__ __forceinline__ void quant256Wave(float y0, float y1, float y2, float y3, int* qc, int nsb, int s,
+                                             const ActF16* ao = nullptr, int col = 0) {
     const int lane = threadIdx.x & 63;
     float am = fmaxf(fmaxf(fmaxf(y0, 0.0f - y0), fmaxf(y1, 0.0f - y1)), fmaxf(fmaxf(y2, 0.0f - y2), fmaxf(y3, 0.0f - y3)));
     am = waveMax(am);
@@ -109,6 +134,7 @@ __device__ __forceinline__ void quant256Wave(float y0, float y1, float y2, float
     }
     if (lane < 4) qc[nsb * 81 + s * 4 + lane] = lane == 0 ? pw[0] : (lane == 1 ? pw[1] : (lane == 2 ? pw[2] : pw[3]));
     if (lane == 0) reinterpret_cast<float*>(qc + nsb * 64)[s] = d;
+    if (ao) actF16Store(*ao, nsb, s, col, lane, c0, c1, c2, c3, b32, d);
 }
 
 // Four consecutive floats at p (16-byte aligned when A16).
@@ -236,17 +262,19 @@ __global__ void silu_mul_q8_kernel(const float* __restrict__ g, const float* __r
 }
 
 template <bool A16>
-__global__ __launch_bounds__(256) void silu_mul_q8k_kernel(const float* __restrict__ g, const float* __restrict__ u,
-                                                           float* __restrict__ y, int* __restrict__ q, int n, int cols) {
+__global__ __launch_bounds__(1024) void silu_mul_q8k_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                           float* __restrict__ y, int* __restrict__ q, int n, int cols,
+                                                           ActF16 ao, int has_ao) {
     const int nsb = n / 256;
     const int c = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     int* qc = q + (size_t)c * nsb * 85;
-    for (int sb = wave; sb < nsb; sb += 4) {
+    const int nw = blockDim.x >> 6;
+    for (int sb = wave; sb < nsb; sb += nw) {
         const size_t o = (size_t)c * n + sb * 256 + 4 * lane;
         const float4 gv = load4<A16>(g + o), uv = load4<A16>(u + o);
         const float4 yv = make_float4(silu(gv.x) * uv.x, silu(gv.y) * uv.y, silu(gv.z) * uv.z, silu(gv.w) * uv.w);
-        store4<A16>(y + o, yv);
-        quant256Wave(yv.x, yv.y, yv.z, yv.w, qc, nsb, sb);
+        if (y) store4<A16>(y + o, yv);
+        quant256Wave(yv.x, yv.y, yv.z, yv.w, qc, nsb, sb, has_ao ? &ao : nullptr, c);
     }
 }
 
@@ -368,15 +396,16 @@ __global__ void rope_qk_store_kernel(const float* __restrict__ q, float* __restr
 // The row is loaded with all 256 threads (coalesced) into LDS, blocks of 32 padded to 36 floats
 // so that the per-block sums (one thread each, in order) read different banks.
 template <bool A16>
-__global__ __launch_bounds__(256) void add_norm_q8k_kernel(const float* a, const float* b, const float* b2, float* out,
+__global__ __launch_bounds__(1024) void add_norm_q8k_kernel(const float* a, const float* b, const float* b2, float* out,
                                                            const float* __restrict__ w, int* __restrict__ q, int n,
-                                                           float eps) {
+                                                           float eps, ActF16 ao, int has_ao) {
     extern __shared__ float xs[];  // n / 32 blocks of 36 floats, then n / 32 sums of squares
     const int nsb = n / 256, nb = n / 32;
     const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float* ss = xs + nb * 36;
     const size_t r0 = (size_t)row * n;
-    for (int i = 4 * tid; i < n; i += 1024) {
+    const int nt = blockDim.x;
+    for (int i = 4 * tid; i < n; i += 4 * nt) {
         float4 v = load4<A16>(b + r0 + i);
         if (b2) {
             const float4 u = load4<A16>(b2 + r0 + i);
@@ -390,7 +419,7 @@ __global__ __launch_bounds__(256) void add_norm_q8k_kernel(const float* a, const
         *reinterpret_cast<float4*>(xs + (i >> 5) * 36 + (i & 31)) = v;
     }
     __syncthreads();
-    for (int bl = tid; bl < nb; bl += 256) {
+    for (int bl = tid; bl < nb; bl += nt) {
         const float* xb = xs + bl * 36;
         float sq = 0.0f;
 #pragma unroll
@@ -406,11 +435,12 @@ __global__ __launch_bounds__(256) void add_norm_q8k_kernel(const float* a, const
     __syncthreads();
     const float r = rmsScale(ss, nb, n, eps);
     int* qr = q + (size_t)row * nsb * 85;
-    for (int sb = wave; sb < nsb; sb += 4) {
+    for (int sb = wave; sb < nsb; sb += nt >> 6) {
         const int e = sb * 256 + 4 * lane;
         const float4 xv = *reinterpret_cast<const float4*>(xs + (e >> 5) * 36 + (e & 31));
         const float4 wv = load4<A16>(w + e);
-        quant256Wave(xv.x * r * wv.x, xv.y * r * wv.y, xv.z * r * wv.z, xv.w * r * wv.w, qr, nsb, sb);
+        quant256Wave(xv.x * r * wv.x, xv.y * r * wv.y, xv.z * r * wv.z, xv.w * r * wv.w, qr, nsb, sb,
+                     has_ao ? &ao : nullptr, row);
     }
 }
 
@@ -565,6 +595,9 @@ Fa toFa(const kcFaDims& x) {
 }
 
 unsigned blocksFor(long long threads) { return (unsigned)((threads + 255) / 256); }
+// Threads of a workgroup that handles one row of n values per 256 with one wavefront per
+// super-block (at most 16 wavefronts, at least 4).
+int waveThreads(int n) { return 64 * std::min(16, std::max(4, n / 256)); }
 
 }  // namespace
 
@@ -603,13 +636,26 @@ int launchNormMulQ8(bool per256, const kcNormMulQ8Args& a, hipStream_t s) {
 int launchSiluMulQ8(bool per256, const kcSiluMulQ8FArgs& a, hipStream_t s) {
     if (per256 && a.cols > 0) {
         if (al16(a.g) && al16(a.u) && al16(a.y))
-            hipLaunchKernelGGL(silu_mul_q8k_kernel<true>, dim3(a.cols), dim3(256), 0, s, a.g, a.u, a.y, a.q, a.n, a.cols);
+            hipLaunchKernelGGL(silu_mul_q8k_kernel<true>, dim3(a.cols), dim3(256), 0, s, a.g, a.u, a.y, a.q, a.n, a.cols,
+                               ActF16{}, 0);
         else
-            hipLaunchKernelGGL(silu_mul_q8k_kernel<false>, dim3(a.cols), dim3(256), 0, s, a.g, a.u, a.y, a.q, a.n, a.cols);
+            hipLaunchKernelGGL(silu_mul_q8k_kernel<false>, dim3(a.cols), dim3(256), 0, s, a.g, a.u, a.y, a.q, a.n, a.cols,
+                               ActF16{}, 0);
     } else if (!per256)
         hipLaunchKernelGGL(silu_mul_q8_kernel, dim3(blocksFor((long long)(a.n / 32) * a.cols)), dim3(256), 0, s, a.g,
                            a.u, a.y, a.q, a.n, a.cols);
     return fromHip(hipGetLastError(), per256 ? "silu_mul_q8kf" : "silu_mul_q8x4f");
+}
+
+int launchSiluMulQ8KAct(const kcSiluMulQ8FArgs& a, const ActF16* ao, hipStream_t s) {
+    if (a.cols <= 0) return 0;
+    if (al16(a.g) && al16(a.u) && (!a.y || al16(a.y)))
+        hipLaunchKernelGGL(silu_mul_q8k_kernel<true>, dim3(a.cols), dim3(waveThreads(a.n)), 0, s, a.g, a.u, a.y, a.q,
+                           a.n, a.cols, ao ? *ao : ActF16{}, ao ? 1 : 0);
+    else
+        hipLaunchKernelGGL(silu_mul_q8k_kernel<false>, dim3(a.cols), dim3(waveThreads(a.n)), 0, s, a.g, a.u, a.y, a.q,
+                           a.n, a.cols, ao ? *ao : ActF16{}, ao ? 1 : 0);
+    return fromHip(hipGetLastError(), "silu_mul_q8kf");
 }
 
 int launchMulRows(const kcMulRowsArgs& a, hipStream_t s) {
@@ -651,14 +697,16 @@ int launchRopeQKStore(const float* q, float* qr, const float* k, const float* v,
 }
 
 int launchAddNormQ8K(const float* a, const float* b, const float* b2, float* out, const float* w, int* q, int n,
-                     int rows, float eps, hipStream_t s) {
+                     int rows, float eps, hipStream_t s, const ActF16* ao) {
     if (rows <= 0) return 0;
     const size_t lds = sizeof(float) * ((size_t)n / 32 * 37);
     if (n % 256 || lds > 65536) return fromHip(hipErrorInvalidValue, "add + norm: row length");
     if (al16(b) && (!b2 || al16(b2)) && (!a || (al16(a) && al16(out))) && al16(w))
-        hipLaunchKernelGGL(add_norm_q8k_kernel<true>, dim3(rows), dim3(256), lds, s, a, b, b2, out, w, q, n, eps);
+        hipLaunchKernelGGL(add_norm_q8k_kernel<true>, dim3(rows), dim3(waveThreads(n)), lds, s, a, b, b2, out, w, q, n,
+                           eps, ao ? *ao : ActF16{}, ao ? 1 : 0);
     else
-        hipLaunchKernelGGL(add_norm_q8k_kernel<false>, dim3(rows), dim3(256), lds, s, a, b, b2, out, w, q, n, eps);
+        hipLaunchKernelGGL(add_norm_q8k_kernel<false>, dim3(rows), dim3(waveThreads(n)), lds, s, a, b, b2, out, w, q, n,
+                           eps, ao ? *ao : ActF16{}, ao ? 1 : 0);
     return fromHip(hipGetLastError(), "add + norm");
 }
 

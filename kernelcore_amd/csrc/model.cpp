@@ -60,6 +60,9 @@ struct kcModel_st {
     float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *qr = nullptr, *kr = nullptr;
     float *att = nullptr, *o = nullptr, *gate = nullptr, *up = nullptr, *sw = nullptr, *down = nullptr;
     float *o2 = nullptr, *down2 = nullptr;  // second K-range partial sums of the batch's o / down products
+    // the batch's quantized activations in the MFMA matmul's layout (kcamd::ActF16), for inputs of
+    // n_embd, n_head * head_dim and n_ff values
+    char *actE = nullptr, *actQ = nullptr, *actF = nullptr;
     float* logits = nullptr;
     int *slotE32 = nullptr, *slotEK = nullptr, *slotQ32 = nullptr, *slotQK = nullptr, *slotF32 = nullptr,
         *slotFK = nullptr;
@@ -321,33 +324,40 @@ int batchStep(kcModel_st* m, int n, hipStream_t s) {
     // (the two partial sums are added in the residual add that consumes them)
     const float* down2 = nullptr;
     int ks = 1;
+    // the quantizers also write the MFMA layout, so the matmuls launch no conversion
+    const int B = c.max_batch;
+    const kcamd::ActF16 vE = kcamd::actF16View(m->actE, B, E_, n), vQ = kcamd::actF16View(m->actQ, B, Q, n),
+                        vF = kcamd::actF16View(m->actF, B, c.n_ff, n);
+    const bool pre = kcamd::option("prefill_act") == 0;  // 1: the matmuls convert the slots themselves
+    const kcamd::ActF16 *aE = pre ? &vE : nullptr, *aQ = pre ? &vQ : nullptr, *aF = pre ? &vF : nullptr;
     for (int li = 0; li < c.n_layer; ++li) {
         const Layer& l = m->L[li];
         // residual add (layer 0: the embeddings) + RMS norm + per-256 quantization in one kernel
         if (li == 0) KI_TRY(kcamd::launchAddNormQ8K(nullptr, m->x, nullptr, nullptr, l.attn_norm, m->slotEK, E_, n,
-                                                    c.norm_eps, s));
-        else KI_TRY(kcamd::launchAddNormQ8K(m->x, m->down, down2, m->x, l.attn_norm, m->slotEK, E_, n, c.norm_eps, s));
+                                                    c.norm_eps, s, aE));
+        else KI_TRY(kcamd::launchAddNormQ8K(m->x, m->down, down2, m->x, l.attn_norm, m->slotEK, E_, n, c.norm_eps, s,
+                                            aE));
         const kcamd::MmPart qkv[3] = {{l.wq, {m->q, nullptr}, Q, 0}, {l.wk, {m->k, nullptr}, KV, 0},
                                       {l.wv, {m->v, nullptr}, KV, 1}};
-        KI_TRY(kcamd::launchMatmulGroup(qkv, 3, m->slotEK, E_, n, 1, &ks, s));
+        KI_TRY(kcamd::launchMatmulGroup(qkv, 3, m->slotEK, E_, n, 1, &ks, s, aE));
         KI_TRY(qkNorm(m, l, n, s));
         // RoPE of q and k with the fp16 cache stores of k and v in one kernel
         KI_TRY(kcamd::launchRopeQKStore(c.qk_norm ? m->att : m->q, m->qr, c.qk_norm ? m->kr : m->k, m->v, l.kcache,
                                         l.vcache, m->pos, m->ones, c.head_dim, c.n_head, c.n_head_kv, n,
                                         std::log2(c.rope_theta), c.rope_neox, KV / 2, c.max_ctx, s));
         KI_TRY(attention(m, l, n, s));
-        KI_TRY(kcamd::launchQuantizeColsK(m->att, m->slotQK, Q, n, s));
+        KI_TRY(kcamd::launchQuantizeColsK(m->att, m->slotQK, Q, n, s, aQ));
         const kcamd::MmPart op{l.wo, {m->o, m->o2}, E_, 0};
-        KI_TRY(kcamd::launchMatmulGroup(&op, 1, m->slotQK, Q, n, 2, &ks, s));
+        KI_TRY(kcamd::launchMatmulGroup(&op, 1, m->slotQK, Q, n, 2, &ks, s, aQ));
         const float* o2 = ks == 2 ? m->o2 : nullptr;
         if (li + 1 < c.n_layer) {
-            KI_TRY(kcamd::launchAddNormQ8K(m->x, m->o, o2, m->x, l.ffn_norm, m->slotEK, E_, n, c.norm_eps, s));
+            KI_TRY(kcamd::launchAddNormQ8K(m->x, m->o, o2, m->x, l.ffn_norm, m->slotEK, E_, n, c.norm_eps, s, aE));
             const kcamd::MmPart gu[2] = {{l.wg, {m->gate, nullptr}, c.n_ff, 0}, {l.wu, {m->up, nullptr}, c.n_ff, 0}};
-            KI_TRY(kcamd::launchMatmulGroup(gu, 2, m->slotEK, E_, n, 1, &ks, s));
-            kcSiluMulQ8FArgs sa{m->gate, m->up, m->sw, m->slotFK, nullptr, c.n_ff, n};
-            KI_TRY(kcamd::launchSiluMulQ8(true, sa, s));
+            KI_TRY(kcamd::launchMatmulGroup(gu, 2, m->slotEK, E_, n, 1, &ks, s, aE));
+            kcSiluMulQ8FArgs sa{m->gate, m->up, nullptr, m->slotFK, nullptr, c.n_ff, n};  // no f32 output needed
+            KI_TRY(kcamd::launchSiluMulQ8KAct(sa, aF, s));
             const kcamd::MmPart dp{l.wd, {m->down, m->down2}, E_, 1};
-            KI_TRY(kcamd::launchMatmulGroup(&dp, 1, m->slotFK, c.n_ff, n, 2, &ks, s));
+            KI_TRY(kcamd::launchMatmulGroup(&dp, 1, m->slotFK, c.n_ff, n, 2, &ks, s, aF));
             down2 = ks == 2 ? m->down2 : nullptr;
         } else {  // the last layer continues with the last token only
             KI_TRY(kcamd::launchAddSumsq(x_last, m->o + (size_t)(n - 1) * E_, x_last, m->slotE32, E_, 1, s,
@@ -418,6 +428,9 @@ kcError_t kcModelCreate(const kcModelConfig* cfg, kcModel_t* out) noexcept {
     KM_A(m->sw, (size_t)B * F);
     KM_A(m->down, (size_t)B * E_);
     KM_A(m->down2, (size_t)B * E_);
+    KM_A(m->actE, kcamd::actF16Bytes(B, E_));
+    KM_A(m->actQ, kcamd::actF16Bytes(B, Q));
+    KM_A(m->actF, kcamd::actF16Bytes(B, F));
     KM_A(m->logits, (size_t)c.n_vocab);
     KM_A(m->slotE32, (size_t)E_ / 32 * 11);
     KM_A(m->slotEK, (size_t)B * (E_ / 256 * 85 + E_ / 32 * 11));
@@ -443,6 +456,8 @@ kcError_t kcModelCreate(const kcModelConfig* cfg, kcModel_t* out) noexcept {
     if (E e = kcMemcpy(m->ones, ones.data(), ones.size() * 4, kc::CopyKind::HostToDevice); e != ok) return fail(e);
     const int zero = 0;
     if (E e = kcMemcpy(m->n_past, &zero, 4, kc::CopyKind::HostToDevice); e != ok) return fail(e);
+    for (auto [p, k] : {std::pair<void*, int>{m->actE, E_}, {m->actQ, Q}, {m->actF, F}})
+        if (E e = kcMemset(p, 0, kcamd::actF16Bytes(B, k)); e != ok) return fail(e);
     *out = m.release();
     return ok;
 }
