@@ -154,6 +154,11 @@ def cpu_baseline(rows, k, seconds=10.0):
 # Llama-3.2-3B architecture, Q4_K_M layout (Q6_K for attn_v / ffn_down / output)
 LLAMA32_3B = dict(n_layer=28, n_embd=3072, n_head=24, n_head_kv=8, head_dim=128, n_ff=8192, n_vocab=128256,
                   norm_eps=1e-5, rope_theta=500000.0, rope_neox=0, qk_norm=0, max_ctx=1024, max_batch=512)
+CFG5_NAME = "BASELINE config 5: 36-layer Qwen3-8B shape (per-head q/k RMSNorm, NEOX RoPE)"
+# Qwen3-8B architecture (per-head q/k RMSNorm, NEOX RoPE), 1024-token prefill
+# then 256 decode steps (context up to 1280)
+QWEN3_8B = dict(n_layer=36, n_embd=4096, n_head=32, n_head_kv=8, head_dim=128, n_ff=12288, n_vocab=151936,
+                norm_eps=1e-6, rope_theta=1000000.0, rope_neox=1, qk_norm=1, max_ctx=1536, max_batch=1024)
 
 
 def model_weights(m, cfg, seed):
@@ -182,7 +187,8 @@ def decode_bytes(w, cfg, ctx):
     return wb + kv + cfg["n_vocab"] * 4
 
 
-def model_run(cfg, n_prompt, n_decode, seed, cpu_seconds, eager=False):
+def model_run(cfg, n_prompt, n_decode, seed, cpu_seconds, eager=False,
+              name="BASELINE config 4: 28-layer Llama-3.2-3B shape"):
     """a random n_prompt-token prompt (one batched forward), then n_decode greedy
     decode steps (graph-replayed, argmax on the device). A warm-up prompt + 4 steps first (builds
     the decode graph), then the cache is reset and the timed prompt and decode run."""
@@ -223,7 +229,7 @@ def model_run(cfg, n_prompt, n_decode, seed, cpu_seconds, eager=False):
     bpt = decode_bytes(w, cfg, n_prompt + n_decode // 2)
     dec_s = w2 - w1
     gbs = bpt * n_decode / dec_s / 1e9
-    out = {"workload": f"BASELINE config 4: {cfg['n_layer']}-layer Llama-3.2-3B shape, Q4_K_M random weights, "
+    out = {"workload": f"{name}, Q4_K_M random weights, "
                        f"{n_prompt}-token prompt then {n_decode} greedy decode steps, f16 KV cache",
            "prefill_tok_s": round(n_prompt / (w1 - w0), 1), "decode_tok_s": round(n_decode / dec_s, 1),
            "prefill_ms": round((w1 - w0) * 1e3, 3), "ms_per_decode_token": round(dec_s / n_decode * 1e3, 4),
@@ -329,6 +335,8 @@ def main():
     ap.add_argument("--skip-cfg1", action="store_true", help="only the config-2 workload (short profiling runs)")
     ap.add_argument("--skip-model", action="store_true", help="skip the config-3 matmul and config-4 model legs")
     ap.add_argument("--decode-steps", type=int, default=128)
+    ap.add_argument("--decode-steps5", type=int, default=256, help="decode steps of the config-5 leg")
+    ap.add_argument("--skip-cfg5", action="store_true", help="skip the config-5 (Qwen3-8B shape) model leg")
     ap.add_argument("--eager-decode", action="store_true",
                     help="decode with one kcModelForward per token instead of the replayed graph")
     ap.add_argument("--only-model", action="store_true",
@@ -344,7 +352,11 @@ def main():
     if args.only_model:
         mm = prefill_matmul_run(max(args.steps // 5, 5), seed=7000)
         mdl = model_run(LLAMA32_3B, 512, args.decode_steps, seed=9000, cpu_seconds=0, eager=args.eager_decode)
-        print(json.dumps({"prefill_matmul_cfg3": mm, "model_cfg4": mdl}), flush=True)
+        res = {"prefill_matmul_cfg3": mm, "model_cfg4": mdl}
+        if not args.skip_cfg5:
+            res["model_cfg5"] = model_run(QWEN3_8B, 1024, args.decode_steps5, seed=9500, cpu_seconds=0,
+                                          eager=args.eager_decode, name=CFG5_NAME)
+        print(json.dumps(res), flush=True)
         return
     rows2, k2 = 128256, 3072
     r2 = matvec_run("q6k", rows2, k2, copies=2, steps=args.steps, warmup=args.warmup, seed=1000)
@@ -357,7 +369,7 @@ def main():
                         seed=5000)
         print(f"# cfg1 done: kernel {r1['kernel_ms'] * 1e3:.2f} us", file=sys.stderr, flush=True)
     cal = calibrate() if args.calibrate else None
-    mm = mdl = None
+    mm = mdl = mdl5 = None
     if not args.skip_model:
         mm = prefill_matmul_run(max(args.steps // 5, 5), seed=7000)
         print(f"# cfg3 done: {mm['achieved_tops']} TOP/s", file=sys.stderr, flush=True)
@@ -365,6 +377,11 @@ def main():
                         eager=args.eager_decode)
         print(f"# cfg4 done: prefill {mdl['prefill_tok_s']} tok/s, decode {mdl['decode_tok_s']} tok/s",
               file=sys.stderr, flush=True)
+        if not args.skip_cfg5:
+            mdl5 = model_run(QWEN3_8B, 1024, args.decode_steps5, seed=9500,
+                             cpu_seconds=0 if args.no_cpu else 10.0, eager=args.eager_decode, name=CFG5_NAME)
+            print(f"# cfg5 done: prefill {mdl5['prefill_tok_s']} tok/s, decode {mdl5['decode_tok_s']} tok/s",
+                  file=sys.stderr, flush=True)
 
     b2 = bytes_cfg2(rows2, k2)
     ms_step = r2["region_ms"] / args.steps
@@ -389,12 +406,14 @@ def main():
         out["prefill_matmul_cfg3"] = mm
     if mdl:
         out["model_cfg4"] = mdl
+    if mdl5:
+        out["model_cfg5"] = mdl5
     if cal:
         out["calibration"] = cal
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(rows2, k2)
     if not (r2["finite"] and (r1 is None or r1["finite"]) and (mm is None or mm["finite"])
-            and (mdl is None or mdl["finite"])):
+            and (mdl is None or mdl["finite"]) and (mdl5 is None or mdl5["finite"])):
         out["warning"] = "non-finite outputs"
     print(json.dumps(out), flush=True)
 

@@ -139,6 +139,25 @@ def test_model_3b_shape_two_layers():
     m.close()
 
 
+def test_model_qwen3_8b_shape_two_layers():
+    """Two layers at the Qwen3-8B widths (4096 / 32 heads / 8 KV heads / 12288 FFN / 151936 vocab,
+    per-head q/k RMS norm, NEOX RoPE): a 70-token prompt (the MFMA matmuls, K split for o and down)
+    and two decode steps against the oracle."""
+    cfg = dict(n_layer=2, n_embd=4096, n_head=32, n_head_kv=8, head_dim=128, n_ff=12288, n_vocab=151936,
+               norm_eps=1e-6, rope_theta=1000000.0, rope_neox=1, qk_norm=1, max_ctx=128, max_batch=80)
+    note("model 8b-shape: building")
+    m, o = build(cfg, 23)
+    prompt = np.random.default_rng(6).integers(0, cfg["n_vocab"], 70).astype(np.int32)
+    lg, lo = m.forward(prompt), o.forward(prompt)
+    assert rel_l2(lg, lo) < 1e-2, rel_l2(lg, lo)
+    note(f"model 8b-shape: prompt rel L2 {rel_l2(lg, lo):.2e}")
+    for _ in range(2):
+        t = int(np.argmax(lo))
+        lg, lo = m.forward([t]), o.forward([t])
+        assert rel_l2(lg, lo) < 1e-2, rel_l2(lg, lo)
+    m.close()
+
+
 @pytest.mark.parametrize("name,cfg", [("llama", LLAMA), ("qwen3", QWEN)])
 def test_model_unfused_decode_path(name, cfg):
     """decode_path = 1 runs the one-kernel-per-reference-op decode step (add_sumsq, norm_mul_q8,
