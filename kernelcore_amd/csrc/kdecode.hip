@@ -494,26 +494,25 @@ __device__ __forceinline__ float waveSum64(float v) {
 // workgroup that arrives last, counted with a device-scope atomic, was slower here: the release
 // fence each workgroup needs writes the XCD's L2 back.)
 // LP lanes hold one position's D values, 8 each (D = 8 LP).
-template <int D>
+template <int D, int G>
 __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
     constexpr int LP = D / 8;           // lanes per position
     constexpr int PPI = 64 / LP;        // positions per wave instruction
     constexpr int NI = (kChunk / 4) / PPI;  // instructions per wave (16 positions per wave)
     constexpr int pairs = D / 2;
-    __shared__ float sc[kMaxGroup][kChunk];
-    __shared__ float red[16][kMaxGroup * D];  // [wave * 4 + row of 16 lanes][head * D + d]
-    __shared__ float mg[kMaxGroup], lg[kMaxGroup];
-    __shared__ float qs[kMaxGroup * D];
-    __shared__ float raw[(kMaxGroup + 2) * D];
+    __shared__ float sc[G][kChunk];
+    __shared__ float red[16][G * D];  // [wave * 4 + row of 16 lanes][head * D + d]
+    __shared__ float mg[G], lg[G];
+    __shared__ float qs[G * D];
+    __shared__ float raw[(G + 2) * D];
     __shared__ float nwl[2 * D];
-    __shared__ float kn[D], vn[D], rn[kMaxGroup + 1];
+    __shared__ float kn[D], vn[D], rn[G + 1];
     const QkPostArgs& q = a.qp;
     const int p = q.pos[0], T = p + 1;
     const int nch = (T + kChunk - 1) / kChunk;
     const int c = blockIdx.x, kvh = blockIdx.y;
     if (c >= nch) return;
     const bool last = c == nch - 1;
-    const int G = a.G;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int sub = lane / LP, l = lane % LP;
     const int t0 = c * kChunk + wave * 16;
@@ -575,11 +574,11 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
             q.kcache[w] = (int)(f2h(kn[2 * j]) | (f2h(kn[2 * j + 1]) << 16));
             q.vcache[w] = (int)(f2h(vn[2 * j]) | (f2h(vn[2 * j + 1]) << 16));
         }
-    float qv[kMaxGroup][8];
+    float qv[G][8];
 #pragma unroll
-    for (int g = 0; g < kMaxGroup; ++g)
+    for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) qv[g][e] = qs[min(g, G - 1) * D + l * 8 + e];
+        for (int e = 0; e < 8; ++e) qv[g][e] = qs[g * D + l * 8 + e];
 #pragma unroll
     for (int n = 0; n < NI; ++n) {
         const int tl = wave * 16 + n * PPI + sub, t = c * kChunk + tl;
@@ -590,14 +589,12 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
             kf[2 * e + 1] = t == p ? kn[l * 8 + 2 * e + 1] : h2f(kp[n][e] >> 16);
         }
 #pragma unroll
-        for (int g = 0; g < kMaxGroup; ++g) {
-            if (g < G) {
-                float s = 0.0f;
+        for (int g = 0; g < G; ++g) {
+            float s = 0.0f;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) s += qv[g][e] * kf[e];
-                s = dppSum<LP>(s);
-                if (l == 0) sc[g][tl] = t < T ? a.scale * s : -INFINITY;
-            }
+            for (int e = 0; e < 8; ++e) s += qv[g][e] * kf[e];
+            s = dppSum<LP>(s);
+            if (l == 0) sc[g][tl] = t < T ? a.scale * s : -INFINITY;
         }
     }
     __syncthreads();
@@ -613,9 +610,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
         }
     }
     __syncthreads();
-    float acc[kMaxGroup][8];
+    float acc[G][8];
 #pragma unroll
-    for (int g = 0; g < kMaxGroup; ++g)
+    for (int g = 0; g < G; ++g)
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
 #pragma unroll
@@ -628,20 +625,17 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
             vf[2 * e + 1] = t == p ? vn[l * 8 + 2 * e + 1] : h2f(vp[n][e] >> 16);
         }
 #pragma unroll
-        for (int g = 0; g < kMaxGroup; ++g) {
-            if (g < G) {
-                const float pr = sc[g][tl];
+        for (int g = 0; g < G; ++g) {
+            const float pr = sc[g][tl];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) acc[g][e] += pr * vf[e];
-            }
+            for (int e = 0; e < 8; ++e) acc[g][e] += pr * vf[e];
         }
     }
     // the position slots through LDS, one row of 16 lanes per LDS row (for D = 64 the two slots of
     // a row are added first, lane l + 8 into lane l), summed in row order
     static_assert(LP == 8 || LP == 16, "lanes per position");
 #pragma unroll
-    for (int g = 0; g < kMaxGroup; ++g)
-        if (g < G)
+    for (int g = 0; g < G; ++g)
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 float v = acc[g][e];
@@ -775,13 +769,13 @@ int launchAttnDecode(AttnDecodeArgs a, int D, int Hkv, int max_ctx, hipStream_t 
     if (!attnDecodeSupports(D, a.G)) return fromHip(hipErrorInvalidValue, "attn_decode: shape");
     a.max_chunks = (max_ctx + kChunk - 1) / kChunk;
     const dim3 grid(a.max_chunks, Hkv);
-    if (D == 128) {
-        hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(256), 0, s, a);
-        hipLaunchKernelGGL(attn_merge_kernel<128>, dim3(Hkv), dim3(256), 0, s, a);
-    } else {
-        hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(256), 0, s, a);
-        hipLaunchKernelGGL(attn_merge_kernel<64>, dim3(Hkv), dim3(256), 0, s, a);
-    }
+#define KC_AD(DD, GG) \
+    if (D == DD && a.G == GG) hipLaunchKernelGGL((attn_decode_kernel<DD, GG>), grid, dim3(256), 0, s, a);
+    KC_AD(128, 1) KC_AD(128, 2) KC_AD(128, 3) KC_AD(128, 4) KC_AD(128, 5) KC_AD(128, 6) KC_AD(128, 7) KC_AD(128, 8)
+    KC_AD(64, 1) KC_AD(64, 2) KC_AD(64, 3) KC_AD(64, 4) KC_AD(64, 5) KC_AD(64, 6) KC_AD(64, 7) KC_AD(64, 8)
+#undef KC_AD
+    if (D == 128) hipLaunchKernelGGL(attn_merge_kernel<128>, dim3(Hkv), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(attn_merge_kernel<64>, dim3(Hkv), dim3(256), 0, s, a);
     return fromHip(hipGetLastError(), "attn_decode");
 }
 
