@@ -655,28 +655,40 @@ __device__ __forceinline__ h8 dequant8s(uint2 q, bool hiNib, h2 m2, h2 s2) {
     return r;
 }
 
+// Buffer resources of the three staged arrays (raw buffers: the hardware checks every offset
+// against the byte size and returns zero past it).
+typedef __attribute__((address_space(3))) void* LdsPtr;
+struct HRes {
+    __amdgpu_buffer_rsrc_t act, mins, xd;
+};
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t bufRes(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
 // Direct loads of super-block s into stage buffer buf: the activation tile (goff = this lane's
 // byte offsets of its loads in act at super-block 0), the Q4_K min operands and the column scales.
+// They are buffer loads into LDS rather than global_load_lds: the compiler counts the latter as
+// possibly LDS-side operations and then waits for every LDS read in flight (lgkmcnt(0)) before
+// each use, which serializes the A-operand reads of the K loop with the matrix ops.
 template <bool Q6, int CB>
-__device__ __forceinline__ void stageH(char* buf, const _Float16* act, const _Float16* mins, const float* xdT,
-                                       const uint32_t (&goff)[HGeo<CB>::kPerWave], int s, int wave, int lane,
-                                       int col0, int ncols, int nsb, int ncp) {
+__device__ __forceinline__ void stageH(char* buf, const HRes& rs, const uint32_t (&goff)[HGeo<CB>::kPerWave], int s,
+                                       int wave, int lane, int col0, int ncols, int nsb, int ncp) {
     using G = HGeo<CB>;
-    const char* src = reinterpret_cast<const char*>(act) + (size_t)s * 512;
 #pragma unroll
     for (int r = 0; r < G::kPerWave; ++r) {
         const int g = min(r * 4 + wave, G::kActLoads - 1);
-        __builtin_amdgcn_global_load_lds(src + goff[r], buf + g * 1024, 16, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs.act, (LdsPtr)(buf + g * 1024), 16, goff[r], (uint32_t)s * 512u, 0,
+                                                 0);
     }
     if constexpr (!Q6) {  // 32 columns per load; wavefronts past CB repeat the loads of wavefront wave % CB
         const int wq = wave % CB, p = wq * 64 + lane, c = p >> 1;
         const int cc = col0 + c < ncols ? col0 + c : 0;
-        __builtin_amdgcn_global_load_lds(mins + ((size_t)cc * nsb + s) * 16 + (p & 1) * 8, buf + G::kActB + wq * 1024,
-                                         16, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs.mins, (LdsPtr)(buf + G::kActB + wq * 1024), 16,
+                                                 (uint32_t)(((cc * nsb + s) * 16 + (p & 1) * 8) * 2), 0, 0, 0);
     }
     // the column scales: every wavefront writes the same 1 KB (lanes past the tile repeat)
-    __builtin_amdgcn_global_load_lds(xdT + (size_t)s * ncp + col0 + ((lane & 31) % (8 * CB)) * 4,
-                                     buf + G::kActB + G::kMinB, 16, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs.xd, (LdsPtr)(buf + G::kActB + G::kMinB), 16,
+                                             (uint32_t)((s * ncp + col0 + ((lane & 31) % (8 * CB)) * 4) * 4), 0, 0, 0);
 }
 
 // One workgroup's tile: weight rows rowTile * 128 .., columns colTile * 32 CB .., super-blocks
@@ -694,6 +706,8 @@ __device__ __forceinline__ void hTile(char* lbase, const uint8_t* __restrict__ q
     const int ngroups = (nsb + kGroupSb - 1) / kGroupSb;
     const int rows_stream = ((rows + kTileRows - 1) / kTileRows) * kTileRows;
     const int k = nsb * 256;
+    const HRes rs{bufRes(act, (uint32_t)ncols * (uint32_t)k * 2u), bufRes(mins, (uint32_t)ncols * (uint32_t)nsb * 32u),
+                  bufRes(xdT, (uint32_t)nsb * (uint32_t)ncp * 4u)};
 
     // this lane's byte offset into act of each of its direct loads (super-block 0); columns past
     // ncols read column 0
@@ -714,7 +728,7 @@ __device__ __forceinline__ void hTile(char* lbase, const uint8_t* __restrict__ q
     const f16v zero = acc[0];
     using Rows = typename std::conditional<Q6, Rows32Q6, Rows32>::type;
     Rows wcur, wnext;
-    stageH<Q6, CB>(lbase, act, mins, xdT, goff, sb0, wave, lane, col0, ncols, nsb, ncp);
+    stageH<Q6, CB>(lbase, rs, goff, sb0, wave, lane, col0, ncols, nsb, ncp);
     wnext.load(qw, row, rows_stream, ngroups, sb0, h);
     // this lane's A-operand byte offset in a stage for column block cb (K-step t adds 32 t)
     int aoff[CB];
@@ -728,7 +742,7 @@ __device__ __forceinline__ void hTile(char* lbase, const uint8_t* __restrict__ q
         wcur = wnext;
         wcur.decode();
         if (s + 1 < sb1) {
-            stageH<Q6, CB>(lbase + (b ^ 1) * G::kBuf, act, mins, xdT, goff, s + 1, wave, lane, col0, ncols, nsb, ncp);
+            stageH<Q6, CB>(lbase + (b ^ 1) * G::kBuf, rs, goff, s + 1, wave, lane, col0, ncols, nsb, ncp);
             wnext.load(qw, row, rows_stream, ngroups, s + 1, h);
         }
         const char* buf = lbase + b * G::kBuf;
@@ -745,32 +759,41 @@ __device__ __forceinline__ void hTile(char* lbase, const uint8_t* __restrict__ q
                 s2[j] = h2{sub, sub};
             }
         }
+        // Software pipeline over the 16 K-steps: step t runs its matrix ops while the B operand of
+        // t + 1 is dequantized and the A operand of t + 1 is read from LDS (no dependence between
+        // the three, so the scheduler interleaves them; the barrier keeps each step's reads ahead).
         h8 av[CB], an[CB];
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb) av[cb] = *reinterpret_cast<const h8*>(buf + aoff[cb]);
+        h8 bq, bq2, bn, bn2;  // B operands of steps t and t + 1 (Q6_K: two per step)
+        if constexpr (Q6)
+            wcur.dequant(0, bq, bq2);
+        else
+            bq = dequant8s(wcur.qs[0][0], false, m2[0], s2[0]);
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
-            if (t + 1 < 16)
+            if (t + 1 < 16) {
 #pragma unroll
                 for (int cb = 0; cb < CB; ++cb) an[cb] = *reinterpret_cast<const h8*>(buf + aoff[cb] + 32 * (t + 1));
-            if constexpr (Q6) {
-                h8 b1, b2;
-                wcur.dequant(t, b1, b2);
-#pragma unroll
-                for (int cb = 0; cb < CB; ++cb) {
-                    is[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[cb], b1, t == 0 ? zero : is[cb], 0, 0, 0);
-                    is[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[cb], b2, is[cb], 0, 0, 0);
+                if constexpr (Q6) {
+                    wcur.dequant(t + 1, bn, bn2);
+                } else {
+                    const int j = (t + 1) >> 1, u = (t + 1) & 1;
+                    bn = dequant8s(wcur.qs[j >> 1][u], j & 1, m2[j], s2[j]);
                 }
-            } else {
-                const int j = t >> 1, u = t & 1;
-                const h8 bw = dequant8s(wcur.qs[j >> 1][u], j & 1, m2[j], s2[j]);
-#pragma unroll
-                for (int cb = 0; cb < CB; ++cb)
-                    is[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[cb], bw, t == 0 ? zero : is[cb], 0, 0, 0);
             }
-            if (t + 1 < 16)
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+                is[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[cb], bq, t == 0 ? zero : is[cb], 0, 0, 0);
+                if constexpr (Q6) is[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[cb], bq2, is[cb], 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (t + 1 < 16) {
 #pragma unroll
                 for (int cb = 0; cb < CB; ++cb) av[cb] = an[cb];
+                bq = bn;
+                if constexpr (Q6) bq2 = bn2;
+            }
         }
         h8 bm;
         if constexpr (!Q6) {
