@@ -6,7 +6,8 @@
 //      every workgroup into its own LDS, then the q / k / v matvecs in one grid;
 //   2. attn_decode: per-head q / k RMS norm (Qwen3), RoPE, k and v into the fp16 cache, and the
 //      attention split over the context in chunks of 64 positions;
-//   3. attn_merge: the merge of the partial softmaxes and the per-32 quantization of the output;
+//   3. attn_merge_wave: the merge of the partial softmaxes and the per-32 quantization of the
+//      output, one wavefront per 64 outputs;
 //   4. dmv (slot prologue, residual epilogue): attention output projection, x += o;
 //   5. dmv (norm prologue, SwiGLU epilogue): FFN norm, gate and up matvecs, silu(g) * u and its
 //      per-32 quantization;
@@ -31,6 +32,9 @@ constexpr int kXs = 68;  // LDS ints per super-block of activations (64 + 4 pad)
 constexpr float kLog2e = 1.44269504f;
 constexpr int kChunk = 64;  // attention positions per workgroup
 constexpr int kMaxGroup = 8;  // query heads per KV head
+// One (chunk, query head) row of the attention partials: D unnormalized output sums, then the
+// running max and the sum of exponentials.
+__host__ __device__ constexpr int partRow(int D) { return D + 2; }
 
 __device__ __forceinline__ int q8r(float t) {
     int q;
@@ -643,16 +647,16 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
                 if (LP == 16 || (lane & 8) == 0) red[wave * 4 + (lane >> 4)][g * D + l * 8 + e] = v;
             }
     __syncthreads();
-    float* pp = a.part + ((size_t)kvh * a.max_chunks + c) * kMaxGroup * (D + 2);
+    float* pp = a.part + ((size_t)kvh * a.max_chunks + c) * kMaxGroup * partRow(D);
     for (int i = tid; i < G * D; i += 256) {
         float v = 0.0f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) v += red[r][i];
-        pp[(i / D) * (D + 2) + i % D] = v;
+        pp[(i / D) * partRow(D) + i % D] = v;
     }
     if (tid < G) {
-        pp[tid * (D + 2) + D] = mg[tid];
-        pp[tid * (D + 2) + D + 1] = lg[tid];
+        pp[tid * partRow(D) + D] = mg[tid];
+        pp[tid * partRow(D) + D + 1] = lg[tid];
     }
 }
 
@@ -664,7 +668,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnDecodeArgs a) {
     const int T = a.qp.pos[0] + 1;
     const int nch = (T + kChunk - 1) / kChunk;
     const int kvh = blockIdx.x, G = a.G, tid = threadIdx.x;
-    const float* base = a.part + (size_t)kvh * a.max_chunks * kMaxGroup * (D + 2);
+    const float* base = a.part + (size_t)kvh * a.max_chunks * kMaxGroup * partRow(D);
     for (int i = tid; i < G * D; i += 256) {
         const int g = i / D, d = i % D;
         float M = -INFINITY, L = 0.0f, O = 0.0f;
@@ -672,7 +676,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnDecodeArgs a) {
             float mv[16], lv[16], ov[16];
 #pragma unroll
             for (int u = 0; u < 16; ++u) {  // unconditional loads (chunks past nch reread the last)
-                const float* pc = base + ((size_t)min(c0 + u, nch - 1) * kMaxGroup + g) * (D + 2);
+                const float* pc = base + ((size_t)min(c0 + u, nch - 1) * kMaxGroup + g) * partRow(D);
                 mv[u] = pc[D];
                 lv[u] = pc[D + 1];
                 ov[u] = pc[d];
@@ -697,6 +701,80 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnDecodeArgs a) {
     __syncthreads();
     const int nbl = G * D / 32;
     if (tid < nbl) storeQ32(a.slot, a.nq, kvh * nbl + tid, quant32Seq(vb + tid * 33));
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dppMoveI(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+
+// The same merge with one wavefront per 64 consecutive outputs of one query head (blockIdx.x =
+// h * (D / 64) + j): each lane runs attn_merge_kernel's chunk-order recurrence for one output,
+// with every load of a group of 16 chunks issued before the arithmetic, and the wavefront then
+// quantizes its two blocks of 32 (lanes 0-31, 32-63) with cross-lane moves. The block maximum
+// and the integer sums do not depend on the order of their terms, so the bytes, scales and sums
+// equal quant32Seq's: the slot is bit-identical to attn_merge_kernel's, from 2-4 times as many
+// workgroups and without the per-thread loops.
+template <int D>
+__global__ __launch_bounds__(64) void attn_merge_wave_kernel(AttnDecodeArgs a) {
+    const int T = a.qp.pos[0] + 1;
+    const int nch = (T + kChunk - 1) / kChunk;
+    const int lane = threadIdx.x, h = blockIdx.x / (D / 64), d0 = (blockIdx.x % (D / 64)) * 64;
+    const size_t row = (size_t)kMaxGroup * partRow(D);  // floats per (KV head, chunk)
+    const float* base = a.part + (size_t)(h / a.G) * a.max_chunks * row + (h % a.G) * partRow(D);
+    float M = -INFINITY, L = 0.0f, O = 0.0f;
+    for (int c0 = 0; c0 < nch; c0 += 16) {
+        float ov[16], mv[16], lv[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {  // unconditional loads (chunks past nch reread the last)
+            const float* pc = base + (size_t)min(c0 + u, nch - 1) * row;
+            ov[u] = pc[d0 + lane];
+            mv[u] = pc[D];
+            lv[u] = pc[D + 1];
+        }
+        // Branch-free, so that no load moves under a branch (and waits alone there): a chunk
+        // past nch rereads the last one, whose max is already M (no rescale), and gets weight 0,
+        // which adds +0 to L and O: unchanged (the sign of a zero O does not reach the bytes).
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            if (mv[u] > M) {
+                const float f = exp2f((M - mv[u]) * kLog2e);
+                L *= f;
+                O *= f;
+                M = mv[u];
+            }
+            float f = exp2f((mv[u] - M) * kLog2e);
+            if (c0 + u >= nch) f = 0.0f;
+            L += lv[u] * f;
+            O += ov[u] * f;
+        }
+    }
+    const float v = O / L;
+    // block maximum of |v| over 32 lanes: the 16-lane row by DPP, then the row pair
+    float m = fmaxf(v, 0.0f - v);
+    m = fmaxf(m, dppMove<0xB1>(m));
+    m = fmaxf(m, dppMove<0x4E>(m));
+    m = fmaxf(m, dppMove<0x141>(m));
+    m = fmaxf(m, dppMove<0x140>(m));
+    m = fmaxf(m, __shfl_xor(m, 16));
+    const float dq = fmaxf(0.0f, m) / 127.0f;
+    float id;
+    if (dq > 0.0f) id = 1.0f / dq;
+    else id = 0.0f;
+    const int q = q8r(v * id);
+    // the block's sum of q, the same way
+    int sq = q;
+    sq += dppMoveI<0xB1>(sq);
+    sq += dppMoveI<0x4E>(sq);
+    sq += dppMoveI<0x141>(sq);
+    sq += dppMoveI<0x140>(sq);
+    sq += __shfl_xor(sq, 16);
+    // the four bytes of a word from the lanes of a quad (quad_perm [1,1,1,1], [2,...], [3,...])
+    const int q1 = dppMoveI<0x55>(q), q2 = dppMoveI<0xAA>(q), q3 = dppMoveI<0xFF>(q);
+    const int b = (h * D + d0) / 32 + (lane >> 5);
+    if ((lane & 3) == 0)
+        a.slot[b * 8 + ((lane & 31) >> 2)] = (q & 255) | ((q1 & 255) << 8) | ((q2 & 255) << 16) | (q3 << 24);
+    if ((lane & 31) == 0) *reinterpret_cast<float2*>(a.slot + a.nq * 8 + 2 * b) = make_float2(dq, (float)sq);
 }
 
 }  // namespace
@@ -762,10 +840,10 @@ int launchRmsQ8(const float* x, const float* w, int* slot, int n, float eps, hip
 bool attnDecodeSupports(int D, int G) { return (D == 64 || D == 128) && G >= 1 && G <= kMaxGroup; }
 
 size_t attnDecodePartFloats(int Hkv, int max_ctx, int D) {
-    return (size_t)Hkv * ((max_ctx + kChunk - 1) / kChunk) * kMaxGroup * (D + 2);
+    return (size_t)Hkv * ((max_ctx + kChunk - 1) / kChunk) * kMaxGroup * partRow(D);
 }
 
-int launchAttnDecode(AttnDecodeArgs a, int D, int Hkv, int max_ctx, hipStream_t s) {
+int launchAttnDecode(AttnDecodeArgs a, int D, int Hkv, int max_ctx, hipStream_t s, bool seq_merge) {
     if (!attnDecodeSupports(D, a.G)) return fromHip(hipErrorInvalidValue, "attn_decode: shape");
     a.max_chunks = (max_ctx + kChunk - 1) / kChunk;
     const dim3 grid(a.max_chunks, Hkv);
@@ -774,8 +852,14 @@ int launchAttnDecode(AttnDecodeArgs a, int D, int Hkv, int max_ctx, hipStream_t 
     KC_AD(128, 1) KC_AD(128, 2) KC_AD(128, 3) KC_AD(128, 4) KC_AD(128, 5) KC_AD(128, 6) KC_AD(128, 7) KC_AD(128, 8)
     KC_AD(64, 1) KC_AD(64, 2) KC_AD(64, 3) KC_AD(64, 4) KC_AD(64, 5) KC_AD(64, 6) KC_AD(64, 7) KC_AD(64, 8)
 #undef KC_AD
-    if (D == 128) hipLaunchKernelGGL(attn_merge_kernel<128>, dim3(Hkv), dim3(256), 0, s, a);
-    else hipLaunchKernelGGL(attn_merge_kernel<64>, dim3(Hkv), dim3(256), 0, s, a);
+    if (seq_merge) {
+        if (D == 128) hipLaunchKernelGGL(attn_merge_kernel<128>, dim3(Hkv), dim3(256), 0, s, a);
+        else hipLaunchKernelGGL(attn_merge_kernel<64>, dim3(Hkv), dim3(256), 0, s, a);
+    } else {
+        const dim3 grid(Hkv * a.G * D / 64);
+        if (D == 128) hipLaunchKernelGGL(attn_merge_wave_kernel<128>, grid, dim3(64), 0, s, a);
+        else hipLaunchKernelGGL(attn_merge_wave_kernel<64>, grid, dim3(64), 0, s, a);
+    }
     return fromHip(hipGetLastError(), "attn_decode");
 }
 

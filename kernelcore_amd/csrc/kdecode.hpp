@@ -64,6 +64,8 @@ int launchDecodeMatvec(int pro, int epi, DmvArgs a, hipStream_t s);
 int launchRmsQ8(const float* x, const float* w, int* slot, int n, float eps, hipStream_t s);
 bool attnDecodeSupports(int D, int G);
 size_t attnDecodePartFloats(int Hkv, int max_ctx, int D);
-int launchAttnDecode(AttnDecodeArgs a, int D, int Hkv, int max_ctx, hipStream_t s);
+// seq_merge: the merge in one workgroup per KV head with one thread per block quantizing (the
+// first form, kept as a diagnostic); else one wavefront per 64 outputs (same results, bit for bit).
+int launchAttnDecode(AttnDecodeArgs a, int D, int Hkv, int max_ctx, hipStream_t s, bool seq_merge = false);
 
 }  // namespace kcamd

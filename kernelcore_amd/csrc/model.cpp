@@ -237,9 +237,10 @@ int decodeStep(kcModel_st* m, hipStream_t s) {
     return headOne(m, m->x, s);
 }
 
-// The same step in seven launches per layer (kdecode.hip): norm + q/k/v matvecs, q/k norm + RoPE +
-// cache store, split-context attention, its merge + quantization, output projection + residual,
-// norm + gate/up + SwiGLU + quantization, down projection + residual.
+// The same step in six launches per layer (kdecode.hip): norm + q/k/v matvecs; q/k norm + RoPE +
+// cache store + split-context attention; its merge + quantization; output projection + residual;
+// norm + gate/up + SwiGLU + quantization; down projection + residual. decode_path 3 runs the
+// merge's first form (one workgroup per KV head), bit-identical.
 bool fusedDecode(const kcModel_st* m) {
     const auto& c = m->c;
     return kcamd::option("decode_path") != 1 && kcamd::attnDecodeSupports(c.head_dim, c.n_head / c.n_head_kv);
@@ -276,7 +277,7 @@ int decodeStepFused(kcModel_st* m, hipStream_t s) {
                              std::log2(c.rope_theta), c.norm_eps};
         kcamd::AttnDecodeArgs aa{pa, m->attn_part, m->slotQ32, c.n_head / c.n_head_kv, 0, Q / 32,
                                  1.0f / std::sqrt((float)c.head_dim)};
-        KI_TRY(kcamd::launchAttnDecode(aa, c.head_dim, c.n_head_kv, c.max_ctx, s));
+        KI_TRY(kcamd::launchAttnDecode(aa, c.head_dim, c.n_head_kv, c.max_ctx, s, kcamd::option("decode_path") == 3));
         }
         kcamd::DmvArgs oa{};
         oa.p0 = {l.wo, m->x, E_, 0, 0, 0};

@@ -198,6 +198,37 @@ def test_model_fused_matvecs_unfused_attention():
         kc.set_option("decode_path", 0)
 
 
+@pytest.mark.parametrize("name,cfg", [("llama", LLAMA), ("qwen3", QWEN)])
+def test_model_attention_merge_forms_agree(name, cfg):
+    """The decode step merges the split attention's chunk partials with one wavefront per 64
+    outputs (cross-lane quantization); decode_path = 3 runs the first form, one workgroup per KV
+    head with one thread per block of 32. Same operations in the same order: the logits agree bit
+    for bit, over steps that cross a chunk boundary (positions 100..139, chunks of 64)."""
+    m0, o = build(cfg, 11)
+    m3, _ = build(cfg, 11)
+    prompt = np.arange(5, 5 + 100, dtype=np.int32)
+    a, b = m0.forward(prompt), m3.forward(prompt)
+    assert np.array_equal(a, b)
+    lo = o.forward(prompt)
+    try:
+        for step in range(40):
+            t = int(np.argmax(a))
+            kc.set_option("decode_path", 0)
+            a = m0.forward([t])
+            kc.set_option("decode_path", 3)
+            b = m3.forward([t])
+            kc.set_option("decode_path", 0)
+            assert np.array_equal(a, b), (step, float(np.max(np.abs(a - b))))
+            if step < 3:  # and the oracle's bar on the first steps
+                lo = o.forward([t])
+                assert rel_l2(a, lo) < 1e-2, rel_l2(a, lo)
+    finally:
+        kc.set_option("decode_path", 0)
+    note(f"model {name}: the two merge forms agree over 40 steps")
+    m0.close()
+    m3.close()
+
+
 def test_model_long_context_split_attention():
     """A cache too large for the one-workgroup attention's LDS scores (max_ctx 12288 with 4 query
     heads per KV head) takes the split-context attention and its merge kernel."""
