@@ -36,11 +36,18 @@ constexpr int kMaxGroup = 8;  // query heads per KV head
 // running max and the sum of exponentials.
 __host__ __device__ constexpr int partRow(int D) { return D + 2; }
 
+// Round half away from zero and clamp to [-127, 127] (quantize_q8x4.cu): t + copysign(0.5, t) is
+// t + 0.5 for t >= 0 and t - 0.5 below; for t = -0 it is -0.5, which truncates to the same 0.
 __device__ __forceinline__ int q8r(float t) {
-    int q;
-    if (t >= 0.0f) q = (int)(t + 0.5f);
-    else q = (int)(t - 0.5f);
+    const int q = (int)(t + __builtin_copysignf(0.5f, t));
     return q > 127 ? 127 : (q < -127 ? -127 : q);
+}
+
+// The low bytes of a, b, c, d as one word (a in the low byte): three byte permutes.
+__device__ __forceinline__ int pack4(int a, int b, int c, int d) {
+    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x0c0c0400u);
+    return (int)__builtin_amdgcn_perm(hi, lo, 0x05040100u);
 }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + exp2f(-g * kLog2e)); }
@@ -67,10 +74,11 @@ struct Q32 {
 __device__ __forceinline__ Q32 quant32Seq(const float* y) {
     // max and integer sums as balanced trees: both are exact, so the order does not matter and
     // the dependency chains stay short
+    // (|y| here and max(y, 0 - y) in the reference differ only in the sign of a zero maximum,
+    // which d = max(0, m) / 127 maps to the same 0)
     float m[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
-        m[i] = fmaxf(fmaxf(y[i], 0.0f - y[i]), fmaxf(y[i + 16], 0.0f - y[i + 16]));
+    for (int i = 0; i < 16; ++i) m[i] = fmaxf(fabsf(y[i]), fabsf(y[i + 16]));
 #pragma unroll
     for (int w = 8; w >= 1; w >>= 1)
 #pragma unroll
@@ -84,8 +92,7 @@ __device__ __forceinline__ Q32 quant32Seq(const float* y) {
 #pragma unroll
     for (int i = 0; i < 32; ++i) q[i] = q8r(y[i] * id);
 #pragma unroll
-    for (int k = 0; k < 8; ++k)
-        o.w[k] = (q[4 * k] & 255) | ((q[4 * k + 1] & 255) << 8) | ((q[4 * k + 2] & 255) << 16) | (q[4 * k + 3] << 24);
+    for (int k = 0; k < 8; ++k) o.w[k] = pack4(q[4 * k], q[4 * k + 1], q[4 * k + 2], q[4 * k + 3]);
 #pragma unroll
     for (int w = 8; w >= 1; w >>= 1)
 #pragma unroll
@@ -751,7 +758,7 @@ __global__ __launch_bounds__(64) void attn_merge_wave_kernel(AttnDecodeArgs a) {
     }
     const float v = O / L;
     // block maximum of |v| over 32 lanes: the 16-lane row by DPP, then the row pair
-    float m = fmaxf(v, 0.0f - v);
+    float m = fabsf(v);
     m = fmaxf(m, dppMove<0xB1>(m));
     m = fmaxf(m, dppMove<0x4E>(m));
     m = fmaxf(m, dppMove<0x141>(m));
@@ -773,7 +780,7 @@ __global__ __launch_bounds__(64) void attn_merge_wave_kernel(AttnDecodeArgs a) {
     const int q1 = dppMoveI<0x55>(q), q2 = dppMoveI<0xAA>(q), q3 = dppMoveI<0xFF>(q);
     const int b = (h * D + d0) / 32 + (lane >> 5);
     if ((lane & 3) == 0)
-        a.slot[b * 8 + ((lane & 31) >> 2)] = (q & 255) | ((q1 & 255) << 8) | ((q2 & 255) << 16) | (q3 << 24);
+        a.slot[b * 8 + ((lane & 31) >> 2)] = pack4(q, q1, q2, q3);
     if ((lane & 31) == 0) *reinterpret_cast<float2*>(a.slot + a.nq * 8 + 2 * b) = make_float2(dq, (float)sq);
 }
 
