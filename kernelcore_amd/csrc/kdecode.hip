@@ -517,7 +517,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
     __shared__ float qs[G * D];
     __shared__ float raw[(G + 2) * D];
     __shared__ float nwl[2 * D];
-    __shared__ float kn[D], vn[D], rn[G + 1];
+    __shared__ float kn[D], vn[D], rn[G + 1], ffl[D / 2];
     const QkPostArgs& q = a.qp;
     const int p = q.pos[0], T = p + 1;
     const int nch = (T + kChunk - 1) / kChunk;
@@ -529,6 +529,22 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
     const int t0 = c * kChunk + wave * 16;
     // Every global load first, unconditional (clamped rows; position p and rows past it are
     // replaced or masked below): a load under a branch gets a wait of its own.
+    // The token's q, k, v (NR words per thread), the q / k norm weights and the RoPE frequency
+    // factors first, then the cache rows: waiting for the small loads (the load counter drains
+    // in order) leaves the cache rows in flight behind the RoPE work.
+    constexpr int NR = ((G + 2) * D + 255) / 256;
+    float rv[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        const int i = min(tid + r * 256, (G + 2) * D - 1);
+        const float* src = i < G * D ? q.q + (size_t)kvh * G * D + i
+                                     : (i < (G + 1) * D ? q.k + (size_t)kvh * D + (i - G * D)
+                                                        : q.v + (size_t)kvh * D + (i - (G + 1) * D));
+        rv[r] = *src;
+    }
+    const int tn = tid % (2 * D);
+    const float nwv = *(q.qk_norm ? (tn < D ? q.q_norm + tn : q.k_norm + tn - D) : q.q + (tn % D));
+    const float ffv = q.ff[tid % pairs];
     const int tmax = max(p - 1, 0);
     u32x4 kp[NI], vp[NI];
 #pragma unroll
@@ -537,16 +553,11 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
         kp[n] = *reinterpret_cast<const u32x4*>(q.kcache + row);
         vp[n] = *reinterpret_cast<const u32x4*>(q.vcache + row);
     }
-    for (int i = tid; i < (G + 2) * D; i += 256) {
-        const float* src = i < G * D ? q.q + (size_t)kvh * G * D + i
-                                     : (i < (G + 1) * D ? q.k + (size_t)kvh * D + (i - G * D)
-                                                        : q.v + (size_t)kvh * D + (i - (G + 1) * D));
-        raw[i] = *src;
-    }
-    if (tid < 2 * D) {
-        const float* nw = q.qk_norm ? (tid < D ? q.q_norm + tid : q.k_norm + tid - D) : q.q + (tid % D);
-        nwl[tid] = *nw;
-    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r)
+        if (tid + r * 256 < (G + 2) * D) raw[tid + r * 256] = rv[r];
+    if (tid < 2 * D) nwl[tid] = nwv;
+    if (tid < pairs) ffl[tid] = ffv;
     __syncthreads();
     if (q.qk_norm) {
         if (tid <= G) {  // heads 0..G-1: q, head G: k; sequential sums as rms_norm.cu
@@ -564,8 +575,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
     const int m1 = q.neox ? 1 : 2, m2 = q.neox ? pairs : 1;
     for (int i = tid; i < (G + 1) * pairs; i += 256) {
         const int h = i / pairs, j = i % pairs;
-        const float theta = (float)p * exp2f(-(float)j / (float)pairs * q.log2_base) / q.ff[j];
-        const float cs = cosf(theta), sn = sinf(theta);
+        const float theta = (float)p * exp2f(-(float)j / (float)pairs * q.log2_base) / ffl[j];
+        float sn, cs;
+        sincosf(theta, &sn, &cs);  // one shared argument reduction for both
         const int o = j * m1;
         const float x0 = raw[h * D + o], x1 = raw[h * D + o + m2];
         const float y0 = x0 * cs - x1 * sn, y1 = x0 * sn + x1 * cs;
@@ -590,23 +602,47 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
     for (int g = 0; g < G; ++g)
 #pragma unroll
         for (int e = 0; e < 8; ++e) qv[g][e] = qs[g * D + l * 8 + e];
+    // this lane's 8 values of the token's k and v as the fp16 words the cache row p holds
+    // (kn = h2f(f2h(.)), so f2h(kn) gives back the stored bits): position p takes them with a
+    // select instead of a branch per value
+    u32x4 knw, vnw;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        knw[e] = f2h(kn[l * 8 + 2 * e]) | (f2h(kn[l * 8 + 2 * e + 1]) << 16);
+        vnw[e] = f2h(vn[l * 8 + 2 * e]) | (f2h(vn[l * 8 + 2 * e + 1]) << 16);
+    }
 #pragma unroll
     for (int n = 0; n < NI; ++n) {
         const int tl = wave * 16 + n * PPI + sub, t = c * kChunk + tl;
+        const u32x4 kw = t == p ? knw : kp[n];
         float kf[8];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            kf[2 * e] = t == p ? kn[l * 8 + 2 * e] : h2f(kp[n][e] & 0xFFFFu);
-            kf[2 * e + 1] = t == p ? kn[l * 8 + 2 * e + 1] : h2f(kp[n][e] >> 16);
+            kf[2 * e] = h2f(kw[e] & 0xFFFFu);
+            kf[2 * e + 1] = h2f(kw[e] >> 16);
         }
+        // the G dot products, then their row sums step by step across the heads (independent
+        // cross-lane moves back to back instead of one head's dependent chain at a time)
+        float sg[G];
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             float s = 0.0f;
 #pragma unroll
             for (int e = 0; e < 8; ++e) s += qv[g][e] * kf[e];
-            s = dppSum<LP>(s);
-            if (l == 0) sc[g][tl] = t < T ? a.scale * s : -INFINITY;
+            sg[g] = s;
         }
+#pragma unroll
+        for (int g = 0; g < G; ++g) sg[g] += dppMove<0xB1>(sg[g]);
+#pragma unroll
+        for (int g = 0; g < G; ++g) sg[g] += dppMove<0x4E>(sg[g]);
+#pragma unroll
+        for (int g = 0; g < G; ++g) sg[g] += dppMove<0x141>(sg[g]);
+        if (LP == 16)
+#pragma unroll
+            for (int g = 0; g < G; ++g) sg[g] += dppMove<0x140>(sg[g]);
+        if (l == 0)
+#pragma unroll
+            for (int g = 0; g < G; ++g) sc[g][tl] = t < T ? a.scale * sg[g] : -INFINITY;
     }
     __syncthreads();
     for (int g = wave; g < G; g += 4) {  // one wavefront per head: lane = position
@@ -629,11 +665,12 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeArgs a) {
 #pragma unroll
     for (int n = 0; n < NI; ++n) {
         const int tl = wave * 16 + n * PPI + sub, t = c * kChunk + tl;
+        const u32x4 vw = t == p ? vnw : vp[n];
         float vf[8];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            vf[2 * e] = t == p ? vn[l * 8 + 2 * e] : h2f(vp[n][e] & 0xFFFFu);
-            vf[2 * e + 1] = t == p ? vn[l * 8 + 2 * e + 1] : h2f(vp[n][e] >> 16);
+            vf[2 * e] = h2f(vw[e] & 0xFFFFu);
+            vf[2 * e + 1] = h2f(vw[e] >> 16);
         }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
