@@ -52,7 +52,8 @@ typedef struct kcModel_st* kcModel_t;
 #define KC_TENSOR_W_DOWN 11     /* Q6_K, n_embd x n_ff */
 #define KC_TENSOR_Q_NORM 12     /* f32 [head_dim] (qk_norm only) */
 #define KC_TENSOR_K_NORM 13     /* f32 [head_dim] (qk_norm only) */
-#define KC_TENSOR_COUNT 14
+#define KC_TENSOR_ROPE_FREQS 14 /* f32 [head_dim / 2], optional: RoPE frequency factors (theta_i / ff[i]) */
+#define KC_TENSOR_COUNT 15
 #define KC_QTYPE_F32 0
 
 KC_API kcError_t kcModelCreate(const kcModelConfig* cfg, kcModel_t* model) KC_NOEXCEPT;
@@ -62,6 +63,17 @@ KC_API kcError_t kcModelDestroy(kcModel_t model) KC_NOEXCEPT;
 KC_API kcError_t kcModelTensorInfo(kcModel_t model, int tensor, int layer, int* qtype, int* rows, int* k,
                                    size_t* bytes) KC_NOEXCEPT;
 KC_API kcError_t kcModelSetTensor(kcModel_t model, int tensor, int layer, const void* host, size_t bytes) KC_NOEXCEPT;
+/* The same with the weight type given: any matrix tensor takes KC_QTYPE_Q4_K or KC_QTYPE_Q6_K
+ * (a GGUF "Q4_K_M" file mixes them per layer), the f32 vectors KC_QTYPE_F32. (A layer whose gate
+ * and up matrices differ in type decodes single tokens with the unfused kernels.) */
+KC_API kcError_t kcModelSetTensorTyped(kcModel_t model, int tensor, int layer, int qtype, const void* host,
+                                       size_t bytes) KC_NOEXCEPT;
+/* Creates a model from a GGUF file (general.architecture "llama" or "qwen3"; Q4_K / Q6_K matrices,
+ * f32 norms; output.weight absent = tied to token_embd; rope_freqs.weight optional): the
+ * hyperparameters come from the file's metadata, max_ctx and max_batch from the caller. Errors
+ * (unreadable file, unsupported architecture or tensor type, shape mismatch) return InvalidValue
+ * with the reason in kcGetLastErrorDetail. The file is read once; the model does not keep it. */
+KC_API kcError_t kcModelLoadGguf(const char* path, int max_ctx, int max_batch, kcModel_t* model) KC_NOEXCEPT;
 /* Appends n_tokens (host ids) at the current position and returns the last token's logits
  * (host, n_vocab floats; may be NULL). n_tokens == 1: the decode path; more: the batch path. */
 KC_API kcError_t kcModelForward(kcModel_t model, const int* tokens, int n_tokens, float* logits) KC_NOEXCEPT;

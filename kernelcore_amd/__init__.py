@@ -20,7 +20,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB_PATH = os.path.join(HERE, "libkernelcore_amd.so")
-HEADERS = [os.path.join(ROOT, "include", "kernelcore", n) for n in ("kc.h", "llm_kernels.h", "model.h")]
+HEADERS = [os.path.join(ROOT, "include", "kernelcore", n) for n in ("kc.h", "llm_kernels.h", "model.h", "gguf.h")]
 
 ERRORS = ["Success", "NotInitialized", "InvalidValue", "InvalidDevice", "OutOfMemory", "InvalidPointer",
           "InvalidResourceHandle", "UnsupportedOperation", "InvalidKernelImage", "KernelNotFound",
@@ -88,7 +88,7 @@ ModelConfig = _struct("ModelConfig", [("n_layer", _i), ("n_embd", _i), ("n_head"
                                       ("rope_theta", _f), ("rope_neox", _i), ("qk_norm", _i), ("max_ctx", _i),
                                       ("max_batch", _i)])
 TENSORS = {"token_embd": 0, "output_norm": 1, "output": 2, "attn_norm": 3, "wq": 4, "wk": 5, "wv": 6, "wo": 7,
-           "ffn_norm": 8, "w_gate": 9, "w_up": 10, "w_down": 11, "q_norm": 12, "k_norm": 13}
+           "ffn_norm": 8, "w_gate": 9, "w_up": 10, "w_down": 11, "q_norm": 12, "k_norm": 13, "rope_freqs": 14}
 KernelEntry = _struct("KernelEntry", [("name", C.c_char_p), ("validate", _p), ("launch", _p), ("chunkable", _i)])
 
 # ---- library ----------------------------------------------------------------------------------------
@@ -138,6 +138,18 @@ def lib():
         L.kcModelDestroy.argtypes = [_p]
         L.kcModelTensorInfo.argtypes = [_p, _i, _i, C.POINTER(_i), C.POINTER(_i), C.POINTER(_i), C.POINTER(C.c_size_t)]
         L.kcModelSetTensor.argtypes = [_p, _i, _i, _p, C.c_size_t]
+        L.kcModelSetTensorTyped.argtypes = [_p, _i, _i, _i, _p, C.c_size_t]
+        L.kcModelLoadGguf.argtypes = [C.c_char_p, _i, _i, C.POINTER(_p)]
+        L.kcGgufOpen.argtypes = [C.c_char_p, C.POINTER(_p)]
+        L.kcGgufClose.argtypes = [_p]
+        L.kcGgufVersion.argtypes = [_p, C.POINTER(_i), C.POINTER(_i)]
+        L.kcGgufGetNum.argtypes = [_p, C.c_char_p, C.POINTER(C.c_double)]
+        L.kcGgufGetStr.argtypes = [_p, C.c_char_p, C.POINTER(C.c_char_p), C.POINTER(C.c_size_t)]
+        L.kcGgufGetArray.argtypes = [_p, C.c_char_p, C.POINTER(C.c_int64), C.POINTER(_i)]
+        L.kcGgufTensorCount.argtypes = [_p, C.POINTER(_i)]
+        L.kcGgufTensorName.argtypes = [_p, _i, C.POINTER(C.c_char_p)]
+        L.kcGgufTensorInfo.argtypes = [_p, C.c_char_p, C.POINTER(_i), C.POINTER(_i), C.POINTER(C.c_int64),
+                                       C.POINTER(C.c_size_t), C.POINTER(_p)]
         L.kcModelForward.argtypes = [_p, _p, _i, _p]
         L.kcModelGenerate.argtypes = [_p, _i, _p]
         L.kcModelPosition.argtypes = [_p, C.POINTER(_i)]
@@ -268,9 +280,27 @@ class Model:
              C.byref(nb))
         return qt.value, rows.value, k.value, nb.value
 
-    def set_tensor(self, tensor, layer, data):
+    def set_tensor(self, tensor, layer, data, qtype=None):
+        """Raw ggml blocks (or floats); qtype "q4k" / "q6k" picks a matrix's type (default: the
+        tensor's default type)."""
         a = np.ascontiguousarray(data)
-        call("kcModelSetTensor", self.h, TENSORS.get(tensor, tensor), layer, a.ctypes.data, a.nbytes)
+        t = TENSORS.get(tensor, tensor)
+        if qtype is None:
+            call("kcModelSetTensor", self.h, t, layer, a.ctypes.data, a.nbytes)
+        else:
+            call("kcModelSetTensorTyped", self.h, t, layer, QTYPE.get(qtype, qtype), a.ctypes.data, a.nbytes)
+
+    @classmethod
+    def load_gguf(cls, path, max_ctx, max_batch):
+        """kcModelLoadGguf: a model (and its config) from a GGUF file."""
+        self = cls.__new__(cls)
+        h = _p()
+        call("kcModelLoadGguf", os.fsencode(path), max_ctx, max_batch, C.byref(h))
+        self.h = h
+        n_vocab = _i()
+        call("kcModelTensorInfo", h, 0, 0, None, C.byref(n_vocab), None, None)
+        self.cfg = ModelConfig(n_vocab=n_vocab.value)
+        return self
 
     def forward(self, tokens, want_logits=True):
         t = np.ascontiguousarray(tokens, np.int32)
@@ -299,4 +329,56 @@ class Model:
     def close(self):
         if self.h:
             lib().kcModelDestroy(self.h)
+            self.h = None
+
+
+class Gguf:
+    """A GGUF file opened read-only (include/kernelcore/gguf.h)."""
+
+    def __init__(self, path):
+        h = _p()
+        call("kcGgufOpen", os.fsencode(path), C.byref(h))
+        self.h = h
+
+    def version(self):
+        v, a = _i(), _i()
+        call("kcGgufVersion", self.h, C.byref(v), C.byref(a))
+        return v.value, a.value
+
+    def num(self, key):
+        v = C.c_double()
+        call("kcGgufGetNum", self.h, key.encode(), C.byref(v))
+        return v.value
+
+    def str(self, key):
+        p, n = C.c_char_p(), C.c_size_t()
+        call("kcGgufGetStr", self.h, key.encode(), C.byref(p), C.byref(n))
+        return C.string_at(p, n.value).decode()
+
+    def array(self, key):
+        n, t = C.c_int64(), _i()
+        call("kcGgufGetArray", self.h, key.encode(), C.byref(n), C.byref(t))
+        return n.value, t.value
+
+    def tensor_names(self):
+        n = _i()
+        call("kcGgufTensorCount", self.h, C.byref(n))
+        out = []
+        for i in range(n.value):
+            p = C.c_char_p()
+            call("kcGgufTensorName", self.h, i, C.byref(p))
+            out.append(p.value.decode())
+        return out
+
+    def tensor(self, name):
+        """(ggml type, shape ne[:n_dims], the tensor's bytes as a uint8 array copied out of the map)"""
+        t, nd, nb, data = _i(), _i(), C.c_size_t(), _p()
+        ne = (C.c_int64 * 4)()
+        call("kcGgufTensorInfo", self.h, name.encode(), C.byref(t), C.byref(nd), ne, C.byref(nb), C.byref(data))
+        raw = np.frombuffer(C.string_at(data, nb.value), np.uint8).copy() if nb.value else np.zeros(0, np.uint8)
+        return t.value, tuple(ne[i] for i in range(nd.value)), raw
+
+    def close(self):
+        if self.h:
+            lib().kcGgufClose(self.h)
             self.h = None

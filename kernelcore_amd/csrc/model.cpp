@@ -28,15 +28,19 @@ struct Layer {
     void *wq = nullptr, *wk = nullptr, *wv = nullptr, *wo = nullptr, *wg = nullptr, *wu = nullptr, *wd = nullptr;
     float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
     int *kcache = nullptr, *vcache = nullptr;
+    int q6[KC_TENSOR_COUNT] = {};  // per matrix: 1 if its weights are Q6_K (set with the tensor)
 };
 
+// The type a tensor takes by default (kcModelSetTensor); kcModelSetTensorTyped may choose the
+// other K-quant for any matrix.
 int qtypeOf(int tensor) {
     switch (tensor) {
         case KC_TENSOR_OUTPUT_NORM:
         case KC_TENSOR_ATTN_NORM:
         case KC_TENSOR_FFN_NORM:
         case KC_TENSOR_Q_NORM:
-        case KC_TENSOR_K_NORM: return KC_QTYPE_F32;
+        case KC_TENSOR_K_NORM:
+        case KC_TENSOR_ROPE_FREQS: return KC_QTYPE_F32;
         case KC_TENSOR_OUTPUT:
         case KC_TENSOR_WV:
         case KC_TENSOR_W_DOWN: return KC_QTYPE_Q6_K;
@@ -44,7 +48,7 @@ int qtypeOf(int tensor) {
     }
 }
 
-bool perLayer(int tensor) { return tensor >= KC_TENSOR_ATTN_NORM; }
+bool perLayer(int tensor) { return tensor >= KC_TENSOR_ATTN_NORM && tensor != KC_TENSOR_ROPE_FREQS; }
 
 }  // namespace
 
@@ -54,8 +58,10 @@ struct kcModel_st {
     hipStream_t s = nullptr;
     std::vector<Layer> L;
     void *tok_embd = nullptr, *output = nullptr;
+    int q6_tok = 0, q6_out = 1;  // 1 if the embedding / head matrix is Q6_K
     float* out_norm = nullptr;
-    float* ones = nullptr;  // rope frequency factors (none in these models)
+    float* ones = nullptr;  // RoPE frequency factors: ones unless KC_TENSOR_ROPE_FREQS is set
+    bool rope_freqs_set = false;
     // activations, sized for max_batch tokens
     float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *qr = nullptr, *kr = nullptr;
     float *att = nullptr, *o = nullptr, *gate = nullptr, *up = nullptr, *sw = nullptr, *down = nullptr;
@@ -117,6 +123,7 @@ void shapeOf(const kcModelConfig& c, int tensor, int* rows, int* k) {
         case KC_TENSOR_FFN_NORM: *rows = 1, *k = c.n_embd; return;
         case KC_TENSOR_Q_NORM:
         case KC_TENSOR_K_NORM: *rows = 1, *k = c.head_dim; return;
+        case KC_TENSOR_ROPE_FREQS: *rows = 1, *k = c.head_dim / 2; return;
         case KC_TENSOR_WQ: *rows = Q, *k = c.n_embd; return;
         case KC_TENSOR_WK:
         case KC_TENSOR_WV: *rows = KV, *k = c.n_embd; return;
@@ -151,18 +158,18 @@ int normQ8(const float* x, const float* w, float* y, int* slot, int n, float eps
 int ffnOne(kcModel_st* m, const Layer& l, float* x, hipStream_t s) {
     const auto& c = m->c;
     KI_TRY(normQ8(x, l.ffn_norm, m->xn, m->slotE32, c.n_embd, c.norm_eps, s));
-    KI_TRY(matvec(false, l.wg, m->slotE32, m->gate, c.n_ff, c.n_embd, s));
-    KI_TRY(matvec(false, l.wu, m->slotE32, m->up, c.n_ff, c.n_embd, s));
+    KI_TRY(matvec(l.q6[KC_TENSOR_W_GATE], l.wg, m->slotE32, m->gate, c.n_ff, c.n_embd, s));
+    KI_TRY(matvec(l.q6[KC_TENSOR_W_UP], l.wu, m->slotE32, m->up, c.n_ff, c.n_embd, s));
     kcSiluMulQ8FArgs sa{m->gate, m->up, m->sw, m->slotF32, nullptr, c.n_ff, 1};
     KI_TRY(kcamd::launchSiluMulQ8(false, sa, s));
-    return matvec(true, l.wd, m->slotF32, m->down, c.n_embd, c.n_ff, s);
+    return matvec(l.q6[KC_TENSOR_W_DOWN], l.wd, m->slotF32, m->down, c.n_embd, c.n_ff, s);
 }
 
 // Output norm + head for the row x (partial sums in slotE32) into m->logits.
 int headOne(kcModel_st* m, float* x, hipStream_t s) {
     const auto& c = m->c;
     KI_TRY(normQ8(x, m->out_norm, m->xn, m->slotE32, c.n_embd, c.norm_eps, s));
-    return matvec(true, m->output, m->slotE32, m->logits, c.n_vocab, c.n_embd, s);
+    return matvec(m->q6_out, m->output, m->slotE32, m->logits, c.n_vocab, c.n_embd, s);
 }
 
 // RoPE of q and k (after the optional per-head norm) into m->qr / m->kr.
@@ -215,21 +222,21 @@ int decodeStep(kcModel_st* m, hipStream_t s) {
     const auto& c = m->c;
     const int Q = c.n_head * c.head_dim, KV = c.n_head_kv * c.head_dim;
     KI_TRY(kcamd::launchPositions(m->n_past, 1, m->pos, m->idx, m->n_ctx, s));
-    KI_TRY(kcamd::launchGetRows(false, m->tok_embd, m->tokens, m->x, 1, c.n_embd, s));
+    KI_TRY(kcamd::launchGetRows(m->q6_tok, m->tok_embd, m->tokens, m->x, 1, c.n_embd, s));
     for (int li = 0; li < c.n_layer; ++li) {
         const Layer& l = m->L[li];
         if (li == 0) KI_TRY(kcamd::launchAddSumsq(nullptr, m->x, nullptr, m->slotE32, c.n_embd, 1, s));
         else KI_TRY(kcamd::launchAddSumsq(m->x, m->down, m->x, m->slotE32, c.n_embd, 1, s));
         KI_TRY(normQ8(m->x, l.attn_norm, m->xn, m->slotE32, c.n_embd, c.norm_eps, s));
-        KI_TRY(matvec(false, l.wq, m->slotE32, m->q, Q, c.n_embd, s));
-        KI_TRY(matvec(false, l.wk, m->slotE32, m->k, KV, c.n_embd, s));
-        KI_TRY(matvec(true, l.wv, m->slotE32, m->v, KV, c.n_embd, s));
+        KI_TRY(matvec(l.q6[KC_TENSOR_WQ], l.wq, m->slotE32, m->q, Q, c.n_embd, s));
+        KI_TRY(matvec(l.q6[KC_TENSOR_WK], l.wk, m->slotE32, m->k, KV, c.n_embd, s));
+        KI_TRY(matvec(l.q6[KC_TENSOR_WV], l.wv, m->slotE32, m->v, KV, c.n_embd, s));
         KI_TRY(qkNorm(m, l, 1, s));
         KI_TRY(ropeQK(m, 1, s));
         KI_TRY(kvStore(m, l, 1, s));
         KI_TRY(attention(m, l, 1, s));
         KI_TRY(kcamd::launchQuantizeQ8x4(m->att, m->slotQ32, reinterpret_cast<float*>(m->slotQ32 + Q / 32 * 8), Q / 32, s));
-        KI_TRY(matvec(false, l.wo, m->slotQ32, m->o, c.n_embd, Q, s));
+        KI_TRY(matvec(l.q6[KC_TENSOR_WO], l.wo, m->slotQ32, m->o, c.n_embd, Q, s));
         KI_TRY(kcamd::launchAddSumsq(m->x, m->o, m->x, m->slotE32, c.n_embd, 1, s));
         KI_TRY(ffnOne(m, l, m->x, s));
     }
@@ -243,6 +250,8 @@ int decodeStep(kcModel_st* m, hipStream_t s) {
 // merge's first form (one workgroup per KV head), bit-identical.
 bool fusedDecode(const kcModel_st* m) {
     const auto& c = m->c;
+    for (const auto& l : m->L)  // the SwiGLU matvec runs gate and up as one type
+        if (l.q6[KC_TENSOR_W_GATE] != l.q6[KC_TENSOR_W_UP]) return false;
     return kcamd::option("decode_path") != 1 && kcamd::attnDecodeSupports(c.head_dim, c.n_head / c.n_head_kv);
 }
 
@@ -250,13 +259,13 @@ int decodeStepFused(kcModel_st* m, hipStream_t s) {
     const auto& c = m->c;
     const int E_ = c.n_embd, Q = c.n_head * c.head_dim, KV = c.n_head_kv * c.head_dim, F = c.n_ff;
     KI_TRY(kcamd::launchPositions(m->n_past, 1, m->pos, m->idx, m->n_ctx, s));
-    KI_TRY(kcamd::launchGetRows(false, m->tok_embd, m->tokens, m->x, 1, E_, s));
+    KI_TRY(kcamd::launchGetRows(m->q6_tok, m->tok_embd, m->tokens, m->x, 1, E_, s));
     for (int li = 0; li < c.n_layer; ++li) {
         const Layer& l = m->L[li];
         kcamd::DmvArgs qa{};
-        qa.p0 = {l.wq, m->q, Q, 0, 0, 0};
-        qa.p1 = {l.wk, m->k, KV, 0, 0, 0};
-        qa.p2 = {l.wv, m->v, KV, 1, 0, 0};
+        qa.p0 = {l.wq, m->q, Q, l.q6[KC_TENSOR_WQ], 0, 0};
+        qa.p1 = {l.wk, m->k, KV, l.q6[KC_TENSOR_WK], 0, 0};
+        qa.p2 = {l.wv, m->v, KV, l.q6[KC_TENSOR_WV], 0, 0};
         qa.nparts = 3;
         qa.k = E_;
         qa.tpw = 1;
@@ -280,7 +289,7 @@ int decodeStepFused(kcModel_st* m, hipStream_t s) {
         KI_TRY(kcamd::launchAttnDecode(aa, c.head_dim, c.n_head_kv, c.max_ctx, s, kcamd::option("decode_path") == 3));
         }
         kcamd::DmvArgs oa{};
-        oa.p0 = {l.wo, m->x, E_, 0, 0, 0};
+        oa.p0 = {l.wo, m->x, E_, l.q6[KC_TENSOR_WO], 0, 0};
         oa.nparts = 1;
         oa.k = Q;
         oa.tpw = 1;
@@ -288,8 +297,8 @@ int decodeStepFused(kcModel_st* m, hipStream_t s) {
         oa.xd = reinterpret_cast<const float*>(m->slotQ32 + Q / 32 * 8);
         KI_TRY(kcamd::launchDecodeMatvec(kcamd::kProSlot, kcamd::kEpiResid, oa, s));
         kcamd::DmvArgs fa{};
-        fa.p0 = {l.wg, nullptr, F, 0, 0, 0};
-        fa.p1 = {l.wu, nullptr, F, 0, 0, 0};
+        fa.p0 = {l.wg, nullptr, F, l.q6[KC_TENSOR_W_GATE], 0, 0};
+        fa.p1 = {l.wu, nullptr, F, l.q6[KC_TENSOR_W_UP], 0, 0};
         fa.nparts = 2;
         fa.k = E_;
         fa.tpw = 2;
@@ -299,7 +308,7 @@ int decodeStepFused(kcModel_st* m, hipStream_t s) {
         fa.qout = m->slotF32;
         KI_TRY(kcamd::launchDecodeMatvec(kcamd::kProNorm, kcamd::kEpiSwiglu, fa, s));
         kcamd::DmvArgs da{};
-        da.p0 = {l.wd, m->x, E_, 1, 0, 0};
+        da.p0 = {l.wd, m->x, E_, l.q6[KC_TENSOR_W_DOWN], 0, 0};
         da.nparts = 1;
         da.k = F;
         da.tpw = 1;
@@ -308,7 +317,7 @@ int decodeStepFused(kcModel_st* m, hipStream_t s) {
         KI_TRY(kcamd::launchDecodeMatvec(kcamd::kProSlot, kcamd::kEpiResid, da, s));
     }
     KI_TRY(kcamd::launchRmsQ8(m->x, m->out_norm, m->slotE32, E_, c.norm_eps, s));
-    return matvec(true, m->output, m->slotE32, m->logits, c.n_vocab, E_, s);
+    return matvec(m->q6_out, m->output, m->slotE32, m->logits, c.n_vocab, E_, s);
 }
 
 int decodeAny(kcModel_st* m, hipStream_t s) { return fusedDecode(m) ? decodeStepFused(m, s) : decodeStep(m, s); }
@@ -319,7 +328,7 @@ int batchStep(kcModel_st* m, int n, hipStream_t s) {
     const int Q = c.n_head * c.head_dim, KV = c.n_head_kv * c.head_dim;
     const int E_ = c.n_embd;
     KI_TRY(kcamd::launchPositions(m->n_past, n, m->pos, m->idx, m->n_ctx, s));
-    KI_TRY(kcamd::launchGetRows(false, m->tok_embd, m->tokens, m->x, n, E_, s));
+    KI_TRY(kcamd::launchGetRows(m->q6_tok, m->tok_embd, m->tokens, m->x, n, E_, s));
     float* x_last = m->x + (size_t)(n - 1) * E_;
     // the products that read the same activations share one launch; o and down split K in two
     // (the two partial sums are added in the residual add that consumes them)
@@ -338,8 +347,9 @@ int batchStep(kcModel_st* m, int n, hipStream_t s) {
                                                     c.norm_eps, s, aE));
         else KI_TRY(kcamd::launchAddNormQ8K(m->x, m->down, down2, m->x, l.attn_norm, m->slotEK, E_, n, c.norm_eps, s,
                                             aE));
-        const kcamd::MmPart qkv[3] = {{l.wq, {m->q, nullptr}, Q, 0}, {l.wk, {m->k, nullptr}, KV, 0},
-                                      {l.wv, {m->v, nullptr}, KV, 1}};
+        const kcamd::MmPart qkv[3] = {{l.wq, {m->q, nullptr}, Q, l.q6[KC_TENSOR_WQ]},
+                                      {l.wk, {m->k, nullptr}, KV, l.q6[KC_TENSOR_WK]},
+                                      {l.wv, {m->v, nullptr}, KV, l.q6[KC_TENSOR_WV]}};
         KI_TRY(kcamd::launchMatmulGroup(qkv, 3, m->slotEK, E_, n, 1, &ks, s, aE));
         KI_TRY(qkNorm(m, l, n, s));
         // RoPE of q and k with the fp16 cache stores of k and v in one kernel
@@ -348,16 +358,17 @@ int batchStep(kcModel_st* m, int n, hipStream_t s) {
                                         std::log2(c.rope_theta), c.rope_neox, KV / 2, c.max_ctx, s));
         KI_TRY(attention(m, l, n, s));
         KI_TRY(kcamd::launchQuantizeColsK(m->att, m->slotQK, Q, n, s, aQ));
-        const kcamd::MmPart op{l.wo, {m->o, m->o2}, E_, 0};
+        const kcamd::MmPart op{l.wo, {m->o, m->o2}, E_, l.q6[KC_TENSOR_WO]};
         KI_TRY(kcamd::launchMatmulGroup(&op, 1, m->slotQK, Q, n, 2, &ks, s, aQ));
         const float* o2 = ks == 2 ? m->o2 : nullptr;
         if (li + 1 < c.n_layer) {
             KI_TRY(kcamd::launchAddNormQ8K(m->x, m->o, o2, m->x, l.ffn_norm, m->slotEK, E_, n, c.norm_eps, s, aE));
-            const kcamd::MmPart gu[2] = {{l.wg, {m->gate, nullptr}, c.n_ff, 0}, {l.wu, {m->up, nullptr}, c.n_ff, 0}};
+            const kcamd::MmPart gu[2] = {{l.wg, {m->gate, nullptr}, c.n_ff, l.q6[KC_TENSOR_W_GATE]},
+                                         {l.wu, {m->up, nullptr}, c.n_ff, l.q6[KC_TENSOR_W_UP]}};
             KI_TRY(kcamd::launchMatmulGroup(gu, 2, m->slotEK, E_, n, 1, &ks, s, aE));
             kcSiluMulQ8FArgs sa{m->gate, m->up, nullptr, m->slotFK, nullptr, c.n_ff, n};  // no f32 output needed
             KI_TRY(kcamd::launchSiluMulQ8KAct(sa, aF, s));
-            const kcamd::MmPart dp{l.wd, {m->down, m->down2}, E_, 1};
+            const kcamd::MmPart dp{l.wd, {m->down, m->down2}, E_, l.q6[KC_TENSOR_W_DOWN]};
             KI_TRY(kcamd::launchMatmulGroup(&dp, 1, m->slotFK, c.n_ff, n, 2, &ks, s, aF));
             down2 = ks == 2 ? m->down2 : nullptr;
         } else {  // the last layer continues with the last token only
@@ -412,6 +423,8 @@ kcError_t kcModelCreate(const kcModelConfig* cfg, kcModel_t* out) noexcept {
     m->s = static_cast<hipStream_t>(hs);
     const int B = c.max_batch, E_ = c.n_embd, Q = c.n_head * c.head_dim, KV = c.n_head_kv * c.head_dim, F = c.n_ff;
     m->L.resize(c.n_layer);
+    for (auto& l : m->L)
+        for (int t = 0; t < KC_TENSOR_COUNT; ++t) l.q6[t] = qtypeOf(t) == KC_QTYPE_Q6_K;
 #define KM_A(ptr, count) \
     if (E e = allocT(m.get(), &(ptr), (size_t)(count)); e != ok) return fail(e)
     KM_A(m->x, (size_t)B * E_);
@@ -480,7 +493,13 @@ kcError_t kcModelTensorInfo(kcModel_t m, int tensor, int layer, int* qtype, int*
         return kc::Error::InvalidValue;
     int r = 0, kk = 0;
     shapeOf(m->c, tensor, &r, &kk);
-    const int qt = qtypeOf(tensor);
+    int qt = qtypeOf(tensor);  // the default, or the type the tensor was set with
+    if (qt != KC_QTYPE_F32) {
+        const int q6 = tensor == KC_TENSOR_TOKEN_EMBD ? m->q6_tok
+                       : tensor == KC_TENSOR_OUTPUT   ? m->q6_out
+                                                      : m->L[layer].q6[tensor];
+        qt = q6 ? KC_QTYPE_Q6_K : KC_QTYPE_Q4_K;
+    }
     if (qtype) *qtype = qt;
     if (rows) *rows = r;
     if (k) *k = kk;
@@ -489,15 +508,31 @@ kcError_t kcModelTensorInfo(kcModel_t m, int tensor, int layer, int* qtype, int*
 }
 
 kcError_t kcModelSetTensor(kcModel_t m, int tensor, int layer, const void* host, size_t bytes) noexcept {
+    if (tensor < 0 || tensor >= KC_TENSOR_COUNT) return kc::Error::InvalidValue;
+    return kcModelSetTensorTyped(m, tensor, layer, qtypeOf(tensor), host, bytes);
+}
+
+kcError_t kcModelSetTensorTyped(kcModel_t m, int tensor, int layer, int qt, const void* host, size_t bytes) noexcept {
     if (E e = checkModel(m); e != ok) return e;
-    int qt = 0, r = 0, kk = 0;
-    size_t want = 0;
-    if (E e = kcModelTensorInfo(m, tensor, layer, &qt, &r, &kk, &want); e != ok) return e;
+    int r = 0, kk = 0;
+    if (E e = kcModelTensorInfo(m, tensor, layer, nullptr, &r, &kk, nullptr); e != ok) return e;
+    const bool vec = qtypeOf(tensor) == KC_QTYPE_F32;
+    if (vec ? qt != KC_QTYPE_F32 : (qt != KC_QTYPE_Q4_K && qt != KC_QTYPE_Q6_K)) {
+        kcamd::setDetail("tensor %d: type %d not accepted (%s)", tensor, qt, vec ? "f32 only" : "Q4_K or Q6_K");
+        return kc::Error::InvalidValue;
+    }
+    const size_t want = ggmlBytes(qt, r, kk);
     if (!host || bytes != want) {
         kcamd::setDetail("tensor %d: expected %zu bytes", tensor, want);
         return kc::Error::InvalidValue;
     }
     if ((tensor == KC_TENSOR_Q_NORM || tensor == KC_TENSOR_K_NORM) && !m->c.qk_norm) return kc::Error::InvalidValue;
+    if (tensor == KC_TENSOR_ROPE_FREQS) {  // into the factors the kernels read (ones by default)
+        if (m->rope_freqs_set) return kc::Error::InvalidValue;
+        KM_TRYE(kcMemcpy(m->ones, host, bytes, kc::CopyKind::HostToDevice));
+        m->rope_freqs_set = true;
+        return ok;
+    }
     Layer* l = perLayer(tensor) ? &m->L[layer] : nullptr;
     void** slot = nullptr;
     switch (tensor) {
@@ -518,6 +553,10 @@ kcError_t kcModelSetTensor(kcModel_t m, int tensor, int layer, const void* host,
         default: return kc::Error::InvalidValue;
     }
     if (*slot) return kc::Error::InvalidValue;  // each tensor is set once
+    const int q6 = qt == KC_QTYPE_Q6_K;
+    if (tensor == KC_TENSOR_TOKEN_EMBD) m->q6_tok = q6;
+    else if (tensor == KC_TENSOR_OUTPUT) m->q6_out = q6;
+    else if (l) l->q6[tensor] = q6;
     if (qt == KC_QTYPE_F32) {
         KM_TRYE(alloc(m, slot, bytes));
         return kcMemcpy(*slot, host, bytes, kc::CopyKind::HostToDevice);

@@ -29,12 +29,15 @@ def shapes(cfg):
 
 
 class OracleModel:
-    def __init__(self, cfg, tensors, threads=0):
-        """tensors[(id, layer)] = raw ggml bytes (uint8) or float32 arrays; global ids use layer -1.
-        threads > 0 runs the single-row matvecs with the OpenMP variants (the same per-row
-        arithmetic, rows split over threads) -- the bench's CPU baseline."""
+    def __init__(self, cfg, tensors, threads=0, types=None):
+        """tensors[(id, layer)] = raw ggml bytes (uint8) or float32 arrays; global ids use layer -1;
+        (14, -1), when present, holds the RoPE frequency factors. types[(id, layer)] = Q4K / Q6K
+        overrides a matrix's default type (a GGUF Q4_K_M file mixes them). threads > 0 runs the
+        single-row matvecs with the OpenMP variants (the same per-row arithmetic, rows split over
+        threads) -- the bench's CPU baseline."""
         self.cfg = cfg
         self.t = tensors
+        self.types = dict(types or {})
         self.L = lib()
         self.threads = threads
         self.pos = 0
@@ -46,8 +49,11 @@ class OracleModel:
     def w(self, tid, layer=-1):
         return self.t[(tid, layer)]
 
+    def qt(self, tid, layer=-1):
+        return self.types.get((tid, layer), shapes(self.cfg)[tid][0])
+
     def matvec(self, tid, layer, slot, rows, k):
-        qt = shapes(self.cfg)[tid][0]
+        qt = self.qt(tid, layer)
         nb = k // 32
         y = np.zeros(rows, np.float32)
         xq = np.ascontiguousarray(slot[:nb * 8])
@@ -61,7 +67,7 @@ class OracleModel:
         return y
 
     def matmul(self, tid, layer, slots, rows, k, n):
-        qt = shapes(self.cfg)[tid][0]
+        qt = self.qt(tid, layer)
         y = np.zeros(rows * n, np.float32)
         fn = self.L.kco_matmul_q6k_q8k if qt == Q6K else self.L.kco_matmul_q4k_q8k
         fn(self.w(tid, layer), slots, y, rows, k, n)
@@ -70,7 +76,7 @@ class OracleModel:
     def rope(self, x, n_head, pos):
         c = self.cfg
         y = np.zeros_like(x)
-        ff = np.ones(c["head_dim"] // 2, np.float32)
+        ff = np.ascontiguousarray(self.t.get((14, -1), np.ones(c["head_dim"] // 2, np.float32)), np.float32)
         self.L.kco_rope_ggml(np.ascontiguousarray(x, np.float32), y, np.asarray(pos, np.int32), ff, c["head_dim"], n_head,
                              len(pos), np.log2(np.float32(c["rope_theta"])), int(c["rope_neox"]))
         return y
@@ -148,7 +154,8 @@ class OracleModel:
         p0 = self.pos
         E, Q, KV = c["n_embd"], c["n_head"] * c["head_dim"], c["n_head_kv"] * c["head_dim"]
         emb = np.ascontiguousarray(self.w(0)).reshape(c["n_vocab"], -1)  # ggml rows of the embedding
-        x = np.concatenate([dequant(self.L, "q4k", emb[t], 1, E) for t in tokens]).astype(np.float32)
+        et = "q6k" if self.qt(0) == Q6K else "q4k"
+        x = np.concatenate([dequant(self.L, et, emb[t], 1, E) for t in tokens]).astype(np.float32)
         eps = np.float32(c["norm_eps"])
         down = None
         if n == 1:

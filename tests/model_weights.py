@@ -6,15 +6,18 @@ import numpy as np
 from oracle.model import F32, Q6K, shapes
 
 
-def random_weights(cfg, seed):
+def random_weights(cfg, seed, types=None):
+    """types[(id, layer)] = Q4K / Q6K overrides a matrix's default type."""
     rng = np.random.default_rng(seed)
     out = {}
     table = shapes(cfg)
+    types = types or {}
     ids_global = [0, 1, 2]
     ids_layer = [3, 4, 5, 6, 7, 8, 9, 10, 11] + ([12, 13] if cfg["qk_norm"] else [])
     keys = [(t, -1) for t in ids_global] + [(t, l) for l in range(cfg["n_layer"]) for t in ids_layer]
     for tid, layer in keys:
         qt, rows, k = table[tid]
+        qt = types.get((tid, layer), qt)
         if qt == F32:
             out[(tid, layer)] = rng.uniform(0.8, 1.2, k).astype(np.float32)
             continue
