@@ -264,6 +264,144 @@ __device__ __forceinline__ void stageNorm(const Act& A, float* ss, const NormReg
     }
 }
 
+// Block quantization by the 8 lanes of an aligned group (lane j holds values 4j .. 4j+3 of the
+// block): the same arithmetic as quant32Seq (the block maximum and the integer sums do not depend
+// on the order of their terms; every value takes the same rounding), with the cross-lane steps as
+// DPP moves inside a row of 16 lanes. Returns this lane's word (values 4j .. 4j+3); every lane gets
+// d, the block's sum of q and the sum of its first 16 values.
+struct Q8L {
+    int w, sum, s16;
+    float d;
+};
+template <int CTRL>
+__device__ __forceinline__ int dppMovI(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+template <int CTRL>
+__device__ __forceinline__ float dppMovF(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ Q8L quant8(const float (&y)[4]) {
+    float m = fmaxf(fmaxf(fabsf(y[0]), fabsf(y[1])), fmaxf(fabsf(y[2]), fabsf(y[3])));
+    m = fmaxf(m, dppMovF<0xB1>(m));   // quad_perm [1,0,3,2]
+    m = fmaxf(m, dppMovF<0x4E>(m));   // quad_perm [2,3,0,1]
+    m = fmaxf(m, dppMovF<0x141>(m));  // row_half_mirror: the other quad of the 8
+    Q8L o;
+    o.d = fmaxf(0.0f, m) / 127.0f;
+    float id;
+    if (o.d > 0.0f) id = 1.0f / o.d;
+    else id = 0.0f;
+    const int q0 = q8r(y[0] * id), q1 = q8r(y[1] * id), q2 = q8r(y[2] * id), q3 = q8r(y[3] * id);
+    o.w = pack4(q0, q1, q2, q3);
+    int s = (q0 + q1) + (q2 + q3);
+    s += dppMovI<0xB1>(s);
+    s += dppMovI<0x4E>(s);  // every lane of the quad: the quad's sum (lanes 0-3: values 0-15)
+    o.s16 = s;  // lane 0 (the lane that stores the block's scalars): the sum of values 0-15
+    s += dppMovI<0x141>(s);
+    o.sum = s;
+    return o;
+}
+
+// The norm prologue with 8 lanes per block (thread t: block t / 8, values 4 (t % 8) .. +3; at most
+// four passes of the workgroup): the per-32 sums of squares in element order as a chain through
+// the 8 lanes (each lane continues the running sum it receives from its left neighbour: the same
+// additions as one thread over 32 values), their total in block order, r, y = x * r * w and the
+// 8-lane quantization. The x / w words of every pass are loaded first (NormRegs8).
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+template <int NP>
+struct NormRegs8 {
+    i32x4 x[NP], w[NP];
+};
+template <int NP>
+__device__ __forceinline__ void loadNorm8(NormRegs8<NP>& r, const float* x, const float* w, int n) {
+    const int nth = blockDim.x, last = n / 4 - 1;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        const int t = min((int)threadIdx.x + p * nth, last);
+        r.x[p] = reinterpret_cast<const i32x4*>(x)[t];
+        r.w[p] = reinterpret_cast<const i32x4*>(w)[t];
+    }
+}
+template <int NP>
+__device__ __forceinline__ void stageNorm8(const Act& A, float* ss, const NormRegs8<NP>& st, int n, float eps,
+                                           int nsbp) {
+    const int tid = threadIdx.x, nth = blockDim.x, nb = n / 32, nq = n / 4;
+    const int j = tid & 7;
+    const int np = (nq + nth - 1) / nth;  // passes (<= NP: the launchers check)
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        if (p >= np) break;
+        float xv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int v = st.x[p][e];
+            xv[e] = __builtin_bit_cast(float, v);
+        }
+        // the running sum passes from lane j - 1 to lane j, eight steps; step k completes lane k
+        float s = 0.0f, t = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            t = s;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) t += xv[e] * xv[e];
+            const float left = dppMovF<0x111>(t);  // row_shr:1: lane i - 1's value
+            if (j == k + 1) s = left;
+        }
+        const int q = tid + p * nth;
+        if (j == 7 && q < nq) ss[q >> 3] = t;
+    }
+    for (int b = nb + tid; b < nsbp * 8; b += nth) ss[b] = 0.0f;
+    __syncthreads();
+    // the total in block order; every 16-byte read issued before the adds (ss is zero past nb up
+    // to a multiple of 32 inside nsbp * 8, and tot + 0 = tot)
+    float tot = 0.0f;
+    for (int j0 = 0; j0 < nb; j0 += 48) {
+        f32x4v q[12];
+#pragma unroll
+        for (int k = 0; k < 12; ++k) q[k] = reinterpret_cast<const f32x4v*>(ss + j0)[min(k, (nsbp * 8 - j0) / 4 - 1)];
+#pragma unroll
+        for (int k = 0; k < 12; ++k) {
+            if (j0 + 4 * k < nb) {
+                tot += q[k][0];
+                tot += q[k][1];
+                tot += q[k][2];
+                tot += q[k][3];
+            }
+        }
+    }
+    const float r = 1.0f / sqrtf(tot / (float)n + eps);
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        if (p >= np) break;
+        const int q = tid + p * nth;
+        float y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int xv = st.x[p][e], wv = st.w[p][e];
+            y[e] = __builtin_bit_cast(float, xv) * r * __builtin_bit_cast(float, wv);
+        }
+        const Q8L o = quant8(y);
+        if (q < nq) {
+            const int b = q >> 3;
+            A.xs[(b >> 3) * kXs + (b & 7) * 8 + j] = o.w;
+            if (j == 0) {
+                A.dx[b] = o.d;
+                A.dsum[b] = o.d * (float)o.sum;
+                A.isum[b] = o.sum;
+                A.s16[b] = o.s16;
+            }
+        }
+    }
+    for (int b = nb + tid; b < nsbp * 8; b += nth) {  // padding blocks of the last group
+        i32x4* xw = reinterpret_cast<i32x4*>(A.xs + (b >> 3) * kXs + (b & 7) * 8);
+        xw[0] = xw[1] = i32x4{0, 0, 0, 0};
+        A.dx[b] = 0.0f;
+        A.dsum[b] = 0.0f;
+        A.isum[b] = 0;
+        A.s16[b] = 0;
+    }
+}
+
 // LDS floats the staging needs beyond Act: stageNorm ss, stageSlot raw (+ its dummy word).
 __host__ __device__ constexpr int stageFloats(int pro, int nsbp) {
     return pro == kProNorm ? nsbp * 8 : nsbp * 16 + 4;
@@ -362,9 +500,14 @@ __global__ __launch_bounds__(EPI == kEpiSwiglu ? 768 : 512) void dmv_kernel(DmvA
         row_ok = s.live && row < P.rows;
         if (EPI == kEpiResid) y_old = P.y[row_ok ? row : 0];
     }
+    // The norm prologue: with 8 lanes per block in the wide SwiGLU workgroups (at most two passes:
+    // the launcher checks n / 4 <= 2 * threads), one thread per block in the others (where 8 lanes
+    // per block would take up to four passes of their serial steps).
     StageRegs st;
+    NormRegs8<2> nr8;
     NormRegs nr;
-    if (PRO == kProNorm) loadNorm(nr, a.x, a.nw, a.k);
+    if (PRO == kProNorm && EPI == kEpiSwiglu) loadNorm8(nr8, a.x, a.nw, a.k);
+    else if (PRO == kProNorm) loadNorm(nr, a.x, a.nw, a.k);
     else loadSlot(st, a.xq, a.xd, a.k / 256);
     // The first item (wave < nw <= items always): 13 slabs and a Q6_K d read for either type
     // with no branch (a Q4_K segment rereads its last slab, and its d address is slab 0), so the
@@ -385,7 +528,8 @@ __global__ __launch_bounds__(EPI == kEpiSwiglu ? 768 : 512) void dmv_kernel(DmvA
         for (int i = 0; i < kQ4kSlabs; ++i) f4.c[i] = f6.c[i];
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (PRO == kProNorm) stageNorm(A, extra, nr, a.k, a.eps, nsbp);
+    if (PRO == kProNorm && EPI == kEpiSwiglu) stageNorm8(A, extra, nr8, a.k, a.eps, nsbp);
+    else if (PRO == kProNorm) stageNorm(A, extra, nr, a.k, a.eps, nsbp);
     else stageSlot(A, extra, st, a.k / 256, nsbp);
     __syncthreads();
     if (q6) dmvItems<true, EPI>(a, part, A, terms, ns, f6, first_live);
@@ -426,8 +570,18 @@ __global__ __launch_bounds__(EPI == kEpiSwiglu ? 768 : 512) void dmv_kernel(DmvA
         float* vb = extra + 2 * nrow;  // blocks of 32 values, 33 floats apart
         if (tid < nrow) vb[(tid >> 5) * 33 + (tid & 31)] = silu(extra[tid]) * extra[nrow + tid];
         __syncthreads();
-        const int b = tid, bg = blockIdx.x * (nrow / 32) + b;
-        if (b < nrow / 32 && bg < a.p0.rows / 32) storeQ32(a.qout, a.p0.rows / 32, bg, quant32Seq(vb + b * 33));
+        // eight lanes per block of 32 (quant8: the same bytes, scale and sum as quant32Seq)
+        if (tid < nrow / 4) {
+            const int b = tid >> 3, j = tid & 7, bg = blockIdx.x * (nrow / 32) + b, nbo = a.p0.rows / 32;
+            float y[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) y[e] = vb[b * 33 + 4 * j + e];
+            const Q8L o = quant8(y);
+            if (bg < nbo) {
+                a.qout[bg * 8 + j] = o.w;
+                if (j == 0) *reinterpret_cast<float2*>(a.qout + nbo * 8 + 2 * bg) = make_float2(o.d, (float)o.sum);
+            }
+        }
     }
 }
 
@@ -855,7 +1009,8 @@ int launchDecodeMatvec(int pro, int epi, DmvArgs a, hipStream_t s) {
     if (ns * kTileRows > 64 * nw || ns > 8 || (epi == kEpiSwiglu && a.tpw % 2))
         return fromHip(hipErrorInvalidValue, "decode matvec: tiles per workgroup");
     const int nsb = a.k / 256, nth = 64 * nw;
-    if ((pro == kProNorm && a.k / 32 > nth) || (pro == kProSlot && (nsb * 16 > 4 * nth || nsb * 4 > nth)))
+    if ((pro == kProNorm && (epi == kEpiSwiglu ? a.k / 4 > 2 * nth : a.k / 32 > nth)) ||
+        (pro == kProSlot && (nsb * 16 > 4 * nth || nsb * 4 > nth)))
         return fromHip(hipErrorInvalidValue, "decode matvec: activations exceed the staging registers");
     const size_t lds = dmvLds(pro, epi, a.k, a.tpw);
     if (lds > 65536) return fromHip(hipErrorInvalidValue, "decode matvec: activations exceed LDS");
