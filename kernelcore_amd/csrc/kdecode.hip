@@ -510,12 +510,15 @@ __global__ __launch_bounds__(EPI == kEpiSwiglu ? 768 : 512) void dmv_kernel(DmvA
     else if (PRO == kProNorm) loadNorm(nr, a.x, a.nw, a.k);
     else loadSlot(st, a.xq, a.xd, a.k / 256);
     // The first item (wave < nw <= items always): 13 slabs and a Q6_K d read for either type
-    // with no branch (a Q4_K segment rereads its last slab, and its d address is slab 0), so the
-    // staging below waits for its own loads only. A dead tile reads tile 0.
+    // with no branch (a Q4_K segment rereads its last slab, and its d address is slab 0). A dead
+    // tile reads tile 0. Issued before the staging, so that the item's weights stream in while
+    // the activations are staged (the staging waits for its own loads only) -- except in the
+    // SwiGLU workgroups, whose 28 MB of weights issued all at once queue the activations' small
+    // loads behind them: there the weights are issued once the activations are staged.
     Pieces<true, true> f6;
     Pieces<false, true> f4;
-    bool first_live;
-    {
+    bool first_live = false;
+    auto loadFirst = [&]() {
         const Slot s0 = slotOf<EPI>(a, part, wave % ns);
         first_live = s0.live;
         const int seg = q6 ? kQ6kSeg : kQ4kSeg, nsl = q6 ? kQ6kSlabs : kQ4kSlabs;
@@ -526,12 +529,14 @@ __global__ __launch_bounds__(EPI == kEpiSwiglu ? 768 : 512) void dmv_kernel(DmvA
         f6.dbits = *reinterpret_cast<const uint16_t*>(p0 + (q6 ? kQ6kSlabs * 1024 + lane * 2 : 0));
 #pragma unroll
         for (int i = 0; i < kQ4kSlabs; ++i) f4.c[i] = f6.c[i];
-    }
+    };
+    if constexpr (EPI != kEpiSwiglu) loadFirst();
     __builtin_amdgcn_sched_barrier(0);
     if (PRO == kProNorm && EPI == kEpiSwiglu) stageNorm8(A, extra, nr8, a.k, a.eps, nsbp);
     else if (PRO == kProNorm) stageNorm(A, extra, nr, a.k, a.eps, nsbp);
     else stageSlot(A, extra, st, a.k / 256, nsbp);
     __syncthreads();
+    if constexpr (EPI == kEpiSwiglu) loadFirst();
     if (q6) dmvItems<true, EPI>(a, part, A, terms, ns, f6, first_live);
     else dmvItems<false, EPI>(a, part, A, terms, ns, f4, first_live);
     __syncthreads();
