@@ -25,6 +25,12 @@
 // MFMAs into the same accumulator: with (16 sh)(q - 32) and with sl (q - 32), both exact fp16
 // integers. acc += (d * xd) * is, as a fused multiply-add.
 //
+// The fp16-activation kernels (matmul_kq_mfma_h_kernel) read the activations converted once to
+// fp16 as 16 x (exact: |16 x| <= 2032). Their weight operands are scaled to match: sc q / 16
+// (Q4_K) and sh (q - 32), sl (q - 32) / 16 (Q6_K), all still exact fp16 values, so every product
+// is the same integer as above; the Q6_K operands then need no x16 product, and their constants
+// are fp16 products of small integers.
+//
 // Tiling: a workgroup of 4 wavefronts computes 128 weight rows x 128 activation columns; each
 // wavefront 64 x 64 as 2 x 2 blocks of 32 x 32. The output's lane index runs along weight rows,
 // so stores of y (column-major, y + c * rows) are contiguous 128-byte runs.
@@ -61,6 +67,16 @@ __device__ __forceinline__ uint2 i8x4_to_h4(uint32_t w) {
     const h2 off = {(_Float16)(-1152.0f), (_Float16)(-1152.0f)};
     const h2 lo = bits_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) + off;
     const h2 hi = bits_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) + off;
+    return make_uint2(h2_bits(lo), h2_bits(hi));
+}
+
+// Four int8 activations -> four fp16 values 16 x (exact): (x ^ 0x80) | 0x6400 is 1024 + x + 128,
+// and (1152 + x) * 16 - 18432 = 16 x in one fused multiply-add.
+__device__ __forceinline__ uint2 i8x4_to_h4x16(uint32_t w) {
+    const uint32_t u = w ^ 0x80808080u;
+    const h2 m = {(_Float16)16.0f, (_Float16)16.0f}, c = {(_Float16)(-18432.0f), (_Float16)(-18432.0f)};
+    const h2 lo = __builtin_elementwise_fma(bits_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)), m, c);
+    const h2 hi = __builtin_elementwise_fma(bits_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)), m, c);
     return make_uint2(h2_bits(lo), h2_bits(hi));
 }
 
@@ -155,6 +171,36 @@ struct Rows32Q6 {
         dbits = *reinterpret_cast<const uint16_t*>(seg + kQ6kSlabs * 1024 + (kq * 16 + r) * 2);
     }
     __device__ __forceinline__ void decode() { d = (float)__builtin_bit_cast(_Float16, (unsigned short)dbits); }
+    // K-step t for activations 16 x: sh (q - 32) and sl (q - 32) / 16 (so 16 x times them gives
+    // 16 sh (q - 32) x and sl (q - 32) x, sc_t = 16 sh + sl), both exact fp16; the constants sh,
+    // -1056 sh, sl / 16 and -66 sl are fp16 products of small integers (exact).
+    __device__ __forceinline__ void dequantA16(int t, h8& b1, h8& b2) const {
+        const int n = t >> 3, quad = (t >> 1) & 3, u = t & 1;
+        const uint2 l = ql[n][quad & 1][u], hb = qh[n][u];
+        const int w = sw[t >> 2];
+        const int sh = (w << (24 - 8 * (t & 3))) >> 28, sl = (w >> (8 * (t & 3))) & 15;
+        const _Float16 fh = (_Float16)(short)sh, fl = (_Float16)(short)sl;
+        const h2 mh = {fh, fh}, ml = {fl * (_Float16)0.0625f, fl * (_Float16)0.0625f};
+        const h2 ch = {fh * (_Float16)(-1056.0f), fh * (_Float16)(-1056.0f)};
+        const h2 cl = {fl * (_Float16)(-66.0f), fl * (_Float16)(-66.0f)};
+        const uint32_t lw[2] = {l.x, l.y}, hw[2] = {hb.x, hb.y};
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t q = ((lw[i] >> (4 * (quad >> 1))) & 0x0F0F0F0Fu) | (((hw[i] >> (2 * quad)) & 0x03030303u) << 4);
+            const h2 a = bits_h2(__builtin_amdgcn_perm(0x64646464u, q, 0x04010400u));  // 1024 + q
+            const h2 b = bits_h2(__builtin_amdgcn_perm(0x64646464u, q, 0x04030402u));
+            const h2 a1 = __builtin_elementwise_fma(a, mh, ch), b1v = __builtin_elementwise_fma(b, mh, ch);
+            const h2 a2 = __builtin_elementwise_fma(a, ml, cl), b2v = __builtin_elementwise_fma(b, ml, cl);
+            b1[4 * i + 0] = a1[0];
+            b1[4 * i + 1] = a1[1];
+            b1[4 * i + 2] = b1v[0];
+            b1[4 * i + 3] = b1v[1];
+            b2[4 * i + 0] = a2[0];
+            b2[4 * i + 1] = a2[1];
+            b2[4 * i + 2] = b2v[0];
+            b2[4 * i + 3] = b2v[1];
+        }
+    }
     // K-step t as two exact fp16 operands: 16 sh (q - 32) and sl (q - 32), sc_t = 16 sh + sl.
     __device__ __forceinline__ void dequant(int t, h8& b1, h8& b2) const {
         const int n = t >> 3, quad = (t >> 1) & 3, u = t & 1;
@@ -598,7 +644,7 @@ __global__ void act_to_f16_kernel(const int* __restrict__ xq, uint2* __restrict_
     const long long per = (long long)nsb * 64;
     if (i < words) {
         const long long c = i / per, w = i - c * per;
-        act[i] = i8x4_to_h4((uint32_t)xq[c * nsb * 85 + w]);
+        act[i] = i8x4_to_h4x16((uint32_t)xq[c * nsb * 85 + w]);
     }
     if (i < (long long)nsb * ncp) {
         const long long sx = i / ncp, c = i - sx * ncp;
@@ -751,10 +797,12 @@ __device__ __forceinline__ void hTile(char* lbase, const uint8_t* __restrict__ q
         if constexpr (!Q6) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
+                // sc q / 16 (the activations are 16 x): (1024 + q) sc / 16 - 64 sc for a low nibble,
+                // (1024 + 16 q) sc / 256 - 4 sc for a high one; exact (sc / 256 >= 2^-8, q sc <= 945)
                 const _Float16 sc = wcur.sc(j);
                 const bool hiNib = j & 1;
-                const _Float16 mul = hiNib ? sc * (_Float16)0.0625f : sc;
-                const _Float16 sub = hiNib ? sc * (_Float16)(-64.0f) : sc * (_Float16)(-1024.0f);
+                const _Float16 mul = hiNib ? sc * (_Float16)0.00390625f : sc * (_Float16)0.0625f;
+                const _Float16 sub = hiNib ? sc * (_Float16)(-4.0f) : sc * (_Float16)(-64.0f);
                 m2[j] = h2{mul, mul};
                 s2[j] = h2{sub, sub};
             }
@@ -767,7 +815,7 @@ __device__ __forceinline__ void hTile(char* lbase, const uint8_t* __restrict__ q
         for (int cb = 0; cb < CB; ++cb) av[cb] = *reinterpret_cast<const h8*>(buf + aoff[cb]);
         h8 bq, bq2, bn, bn2;  // B operands of steps t and t + 1 (Q6_K: two per step)
         if constexpr (Q6)
-            wcur.dequant(0, bq, bq2);
+            wcur.dequantA16(0, bq, bq2);
         else
             bq = dequant8s(wcur.qs[0][0], false, m2[0], s2[0]);
 #pragma unroll
@@ -776,7 +824,7 @@ __device__ __forceinline__ void hTile(char* lbase, const uint8_t* __restrict__ q
 #pragma unroll
                 for (int cb = 0; cb < CB; ++cb) an[cb] = *reinterpret_cast<const h8*>(buf + aoff[cb] + 32 * (t + 1));
                 if constexpr (Q6) {
-                    wcur.dequant(t + 1, bn, bn2);
+                    wcur.dequantA16(t + 1, bn, bn2);
                 } else {
                     const int j = (t + 1) >> 1, u = (t + 1) & 1;
                     bn = dequant8s(wcur.qs[j >> 1][u], j & 1, m2[j], s2[j]);

@@ -190,7 +190,7 @@ __global__ void quantize_k_kernel(const float* __restrict__ x, int* __restrict__
         typedef _Float16 hv4 __attribute__((ext_vector_type(4)));
         hv4 hq;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) hq[e] = (_Float16)(float)((word << (24 - 8 * e)) >> 24);
+        for (int e = 0; e < 4; ++e) hq[e] = (_Float16)(float)(16 * ((word << (24 - 8 * e)) >> 24));  // 16 x
         *reinterpret_cast<hv4*>(static_cast<_Float16*>(ao.act) + (size_t)c * k + s * 256 + 4 * lane) = hq;
         if ((lane & 7) == 0) {
             _Float16* mn = static_cast<_Float16*>(ao.mins) + ((size_t)c * nsb + s) * 16 + (lane >> 3);

@@ -9,7 +9,7 @@
 namespace kcamd {
 
 // The MFMA matmul's activation operands of a batch of ncols per-256-quantized columns of length k,
-// as a quantizer can write them next to the slots: the int8 values as fp16 act[ncols][k], the
+// as a quantizer can write them next to the slots: the int8 values x as fp16 16 x act[ncols][k], the
 // Q4_K min operands mins[ncols][k / 256][16] (fp16: 64 (B_j >> 6) for the 8 sums B_j of 32, then
 // B_j & 63) and the scales xdT[k / 256][ncp], ncp = ncols rounded up to 128.
 struct ActF16 {

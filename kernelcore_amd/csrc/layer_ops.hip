@@ -91,10 +91,10 @@ __device__ __forceinline__ void actF16Store(const ActF16& ao, int nsb, int s, in
     const int k = nsb * 256;
     typedef _Float16 hv4 __attribute__((ext_vector_type(4)));
     hv4 hq;
-    hq[0] = (_Float16)(float)c0;
-    hq[1] = (_Float16)(float)c1;
-    hq[2] = (_Float16)(float)c2;
-    hq[3] = (_Float16)(float)c3;
+    hq[0] = (_Float16)(float)(16 * c0);  // 16 x: exact, and the matmul's weight operand is then sc q / 16
+    hq[1] = (_Float16)(float)(16 * c1);
+    hq[2] = (_Float16)(float)(16 * c2);
+    hq[3] = (_Float16)(float)(16 * c3);
     *reinterpret_cast<hv4*>(static_cast<_Float16*>(ao.act) + (size_t)col * k + s * 256 + 4 * lane) = hq;
     if ((lane & 7) == 0) {
         _Float16* mn = static_cast<_Float16*>(ao.mins) + ((size_t)col * nsb + s) * 16 + (lane >> 3);
