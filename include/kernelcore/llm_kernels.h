@@ -76,6 +76,21 @@ typedef struct kcMatmulKQ8Args {
     int row_block KC_INIT(8);
 } kcMatmulKQ8Args;
 
+/* matmul_f16 (llm_kernels.hpp:285-296): Y = W X for fp16 weights and fp32 activations. qw: the
+ * weights in ggml's row-major F16 layout (rows x k halves, two per 32-bit word; the reference's
+ * load-time 8-row interleave, llm_reference.cpp:740-746, has no counterpart here); x: ncols columns
+ * of k floats; y: ncols columns of rows floats. rows % 8 == 0, k even; dims may be NULL, else
+ * {rows, k, ncols}. */
+typedef struct kcMatmulF16Args {
+    const int* qw;
+    const float* x;
+    float* y;
+    const int* dims;
+    int rows;
+    int k;
+    int ncols;
+} kcMatmulF16Args;
+
 /* quantize_cols / quantize_cols_k (llm_kernels.hpp:277-283). k % 256 == 0. */
 typedef struct kcQuantizeColsArgs {
     const float* x;
@@ -265,6 +280,7 @@ namespace llm {
 typedef ::kcQuantizeArgs QuantizeArgs;
 typedef ::kcMatvecQ4Q8Args MatvecQ4Q8Args;
 typedef ::kcMatmulKQ8Args MatmulKQ8Args;
+typedef ::kcMatmulF16Args MatmulF16Args;
 typedef ::kcQuantizeColsArgs QuantizeColsArgs;
 typedef ::kcRmsNormArgs RmsNormArgs;
 typedef ::kcMulRowsArgs MulRowsArgs;

@@ -54,6 +54,8 @@ MatvecQ4Q8Args = _struct("MatvecQ4Q8Args", [("qw", _p), ("xq", _p), ("xd", _p), 
                                             ("rows", _i), ("k", _i)])
 MatmulKQ8Args = _struct("MatmulKQ8Args", [("qw", _p), ("xq", _p), ("y", _p), ("dims", _p), ("rows", _i), ("k", _i),
                                           ("ncols", _i), ("row_block", _i)])
+MatmulF16Args = _struct("MatmulF16Args", [("qw", _p), ("x", _p), ("y", _p), ("dims", _p), ("rows", _i), ("k", _i),
+                                          ("ncols", _i)])
 QuantizeColsArgs = _struct("QuantizeColsArgs", [("x", _p), ("q", _p), ("dims", _p), ("k", _i), ("ncols", _i)])
 RmsNormArgs = _struct("RmsNormArgs", [("x", _p), ("w", _p), ("y", _p), ("n", _i), ("rows", _i), ("eps", _f)])
 MulRowsArgs = _struct("MulRowsArgs", [("x", _p), ("w", _p), ("y", _p), ("n", _i), ("count", _i)])

@@ -56,6 +56,9 @@ struct MmPart {
 // pre (may be null): the activations already in the MFMA layout (then no conversion is launched).
 int launchMatmulGroup(const MmPart* parts, int nparts, const int* xq, int k, int ncols, int ks, int* used_ks,
                       hipStream_t s, const ActF16* pre = nullptr);
+// kmatmul_f16.hip: Y [ncols][rows] = W X, W row-major fp16 [rows][k], x ncols columns of k floats;
+// rows % 8 == 0, k even.
+int launchMatmulF16(const void* w, const float* x, float* y, int rows, int k, int ncols, hipStream_t s);
 // layer_ops.hip
 int launchVectorAdd(const float* a, const float* b, float* out, int count, hipStream_t s);
 // out = a + (b + b2) (b2 may be null: out = a + b; a null: the sums of squares of b (+ b2) only).

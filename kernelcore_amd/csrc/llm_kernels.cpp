@@ -122,6 +122,29 @@ int matmulLaunch(const void* p, void* s) {
     return kcamd::launchMatmulKq(Q6, K8, *static_cast<const kcMatmulKQ8Args*>(p), hs(s));
 }
 
+// ---- matmul_f16 (llm_kernels.cpp:834-847: matmulF16Marshal). The reference's thread-count
+// limit (rows x column tiles of 4 below 2^24, a CPU chunking bound) is kept so that the same
+// launches are accepted.
+
+int matmulF16Validate(const void* p, const kcLaunchContext*) {
+    const auto& a = *static_cast<const kcMatmulF16Args*>(p);
+    if (a.rows <= 0 || a.rows % 8 || a.k <= 0 || a.k % 2 || a.ncols <= 0 || !fitsIndex(a.rows, a.k) ||
+        !fitsIndex(a.ncols, std::max(a.rows, a.k)) || int64_t(a.rows) * ((a.ncols + 3) / 4) >= (int64_t(1) << 24))
+        return invalid("rows must be a positive multiple of 8, k positive and even, ncols positive");
+    if (reinterpret_cast<uintptr_t>(a.qw) % 4 || reinterpret_cast<uintptr_t>(a.x) % 4 ||
+        reinterpret_cast<uintptr_t>(a.y) % 4)
+        return invalid("qw, x and y must be 4-byte aligned");
+    KC_TRY(checkRange(a.qw, i32Bytes(int64_t(a.rows) * (a.k / 2)), "qw"));
+    KC_TRY(checkRange(a.x, f32Bytes(int64_t(a.ncols) * a.k), "x"));
+    KC_TRY(checkRange(a.y, f32Bytes(int64_t(a.ncols) * a.rows), "y"));
+    const int want[3] = {a.rows, a.k, a.ncols};
+    return checkDims(a.dims, want, 3);
+}
+int matmulF16Launch(const void* p, void* s) {
+    const auto& a = *static_cast<const kcMatmulF16Args*>(p);
+    return kcamd::launchMatmulF16(a.qw, a.x, a.y, a.rows, a.k, a.ncols, hs(s));
+}
+
 // ---- quantize_cols / quantize_cols_k (llm_kernels.cpp:331-345: quantColsMarshal)
 
 template <int kBlock>
@@ -387,6 +410,7 @@ const kcKernelEntry kTable[] = {
     {"matmul_q4k_q8kx8", matmulValidate<false, true>, matmulLaunch<false, true>, 1},
     {"matmul_q6k_q8kx4", matmulValidate<true, true>, matmulLaunch<true, true>, 1},
     {"matmul_q6k_q8kx8", matmulValidate<true, true>, matmulLaunch<true, true>, 1},
+    {"matmul_f16", matmulF16Validate, matmulF16Launch, 1},
     {"add_sumsq_f", addSumsqValidate, addSumsqLaunch, 1},
     {"sumsq_part", sumsqValidate, sumsqLaunch, 1},
     {"norm_mul_q8_f", normMulValidate<false>, normMulLaunch<false>, 1},

@@ -62,6 +62,7 @@ def _sig(lib, prefix):
     s("silu_mul_q8f", None, _f32p, _f32p, _f32p, _i32p, _i, _i)
     s("silu_mul_q8k", None, _f32p, _f32p, _f32p, _i32p, _i, _i)
     s("set_rows_f16", None, _f32p, _i64p, _u16p, _i, _i, _i, _i, _i)
+    s("matmul_f16", None, _u16p, _f32p, _f32p, _i, _i, _i)
 
 
 def lib():
@@ -150,3 +151,11 @@ def dequant(L, qtype, w, rows, k):
         _fn(L, f"dequant_row_{qtype}")(np.ascontiguousarray(w[r]), k, row)
         out[r] = row
     return out
+
+
+def matmul_f16(L, w, x, rows, k, ncols):
+    """Y [ncols][rows] = W X for row-major fp16 weights (uint16 bits) and ncols columns of k floats."""
+    y = np.zeros(rows * ncols, np.float32)
+    _fn(L, "matmul_f16")(np.ascontiguousarray(w, np.uint16).reshape(-1), np.ascontiguousarray(x, np.float32).reshape(-1),
+                         y, rows, k, ncols)
+    return y.reshape(ncols, rows)

@@ -622,3 +622,20 @@ void kco_matmul_q4k_q8k_mt(const uint8_t* w, const int32_t* q, float* y, int row
         for (int r = 0; r < rows; ++r)
             y[(size_t)c * rows + r] = row_q4k_q8k(w + (size_t)r * nsb * 144, q + (size_t)c * nsb * 85, nsb);
 }
+
+/* llm/llm_reference.cpp:756-764: one pair of products per step, added to the running sum in order
+ * (no fused multiply-add: the file is compiled with -ffp-contract=off). */
+void kco_matmul_f16(const uint16_t* w, const float* x, float* y, int rows, int k, int ncols) {
+    for (int c = 0; c < ncols; ++c)
+        for (int r = 0; r < rows; ++r) {
+            const uint16_t* wr = w + (size_t)r * k;
+            const float* xc = x + (size_t)c * k;
+            float a = 0.0f;
+            for (int j = 0; j < k; j += 2) {
+                const float p0 = kco_f16_to_f32(wr[j]) * xc[j];
+                const float p1 = kco_f16_to_f32(wr[j + 1]) * xc[j + 1];
+                a += p0 + p1;
+            }
+            y[(size_t)c * rows + r] = a;
+        }
+}

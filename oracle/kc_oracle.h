@@ -53,6 +53,10 @@ void kco_quantize_cols_k(const float* x, int32_t* q, int k, int ncols);
  * matvec_q4k_q8: llm/llm_reference.cpp:413-445; matvec_q6k_q8: :447-489. */
 void kco_matvec_q4k_q8(const uint8_t* w, const int32_t* xq, const float* xd, float* y, int rows, int k);
 void kco_matvec_q6k_q8(const uint8_t* w, const int32_t* xq, const float* xd, float* y, int rows, int k);
+/* Y = W X for fp16 weights and fp32 activations (llm/llm_reference.cpp:756-764, the mirror of
+ * kernels/llm/matmul_f16.cu): w row-major ggml F16 [rows][k], x ncols columns of k floats, y ncols
+ * columns of rows floats; per output a += (w0 x0 + w1 x1) over the value pairs in order. k even. */
+void kco_matmul_f16(const uint16_t* w, const float* x, float* y, int rows, int k, int ncols);
 /* One column with per-256 activations (a quantize_cols_k slot), llm/llm_reference.cpp:529-596:
  * the per-column result of matmul_{q4k,q6k}_q8kx{4,8}. */
 void kco_matvec_q4k_q8k(const uint8_t* w, const int32_t* slot, float* y, int rows, int k);

@@ -40,6 +40,15 @@ void kcref_matvec_q6k_q8k(const uint8_t* w, const int* slot, float* y, int rows,
     repackQ6K(w, rows, k, qw.data());
     matvecQ6KQ8K(qw.data(), slot, y, rows, k);
 }
+// rows % 8 == 0; w row-major ggml F16, repacked by the reference's repackF16 for its own stream
+// round trip (unpackF16) before matmulF16 runs on the row-major values it returns.
+void kcref_matmul_f16(const uint16_t* w, const float* x, float* y, int rows, int k, int ncols) {
+    std::vector<int> qw(size_t(rows) * (k / 2));
+    repackF16(w, rows, k, qw.data());
+    std::vector<uint16_t> back(size_t(rows) * k);
+    unpackF16(qw.data(), rows, k, back.data());
+    matmulF16(back.data(), x, y, rows, k, ncols);
+}
 // The reference's stream itself, for layout tests.
 void kcref_repack_q4k(const uint8_t* w, int rows, int k, int* qw) { repackQ4K(w, rows, k, qw); }
 void kcref_repack_q6k(const uint8_t* w, int rows, int k, int* qw) { repackQ6K(w, rows, k, qw); }

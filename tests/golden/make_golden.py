@@ -67,6 +67,12 @@ def main():
     y = np.zeros(n * rows, np.float32)
     R.kcref_norm_mul_q8(s, w, y, qs, n, rows, np.float32(1e-5))
     np.savez_compressed(os.path.join(HERE, "norm_mul_q8.npz"), kind="norm", n=n, rows=rows, a=a, b=b, w=w, q=qs, y=y)
+    # fp16 weights x fp32 activations (matmul_f16), 24 rows x 96 values x 3 columns
+    rows, k, nc = 24, 96, 3
+    wf = (kq.randn(rows * k, 110) * np.float32(0.05)).astype(np.float16).view(np.uint16)
+    xf = kq.randn(nc * k, 111)
+    np.savez_compressed(os.path.join(HERE, "matmul_f16.npz"), kind="matmul_f16", rows=rows, k=k, ncols=nc, w=wf, x=xf,
+                        y=oracle.matmul_f16(R, wf, xf, rows, k, nc))
     print("fixtures written to", HERE)
 
 

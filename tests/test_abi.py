@@ -77,8 +77,9 @@ def test_codegen_cpu_paths_are_unsupported():
     assert L.kcSetKernelCodegen(0) == 0
 
 
-STRUCTS = ["VectorAddArgs", "QuantizeArgs", "MatvecQ4Q8Args", "MatmulKQ8Args", "QuantizeColsArgs", "RmsNormArgs",
-           "MulRowsArgs", "RopeGgmlArgs", "AddSumsqFArgs", "SumsqPartArgs", "NormMulQ8Args", "SiluMulQ8FArgs",
+STRUCTS = ["VectorAddArgs", "QuantizeArgs", "MatvecQ4Q8Args", "MatmulKQ8Args", "MatmulF16Args", "QuantizeColsArgs",
+           "RmsNormArgs", "MulRowsArgs", "RopeGgmlArgs", "AddSumsqFArgs", "SumsqPartArgs", "NormMulQ8Args",
+           "SiluMulQ8FArgs",
            "SiluMulArgs", "SetRowsF16Args", "FaDims", "FaScoresArgs", "FaMaxArgs", "FaExpArgs", "FaValuesArgs",
            "KquantRepackArgs", "FlashAttnArgs", "DeviceProperties"]
 

@@ -359,6 +359,42 @@ def test_flash_attn_matches_reference_bits():
     assert np.array_equal(kq.bits(a), kq.bits(b))
 
 
+# ---- fp16 weights (matmul_f16) ----------------------------------------------------------------
+
+F16_SHAPES = [(8, 2, 1), (16, 64, 3), (24, 130, 5), (64, 512, 8)]
+
+
+def _f16_case(rows, k, nc, seed):
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal(rows * k) * 0.05).astype(np.float16).view(np.uint16)
+    x = rng.standard_normal(nc * k).astype(np.float32)
+    return w, x
+
+
+@pytest.mark.parametrize("rows,k,nc", F16_SHAPES)
+def test_matmul_f16_close_to_float64(rows, k, nc):
+    """Against the float64 product of the same fp16 values (numpy's own binary16 decoding): an f32
+    running sum of k terms stays within k * 2^-24 of the sum of absolute products."""
+    w, x = _f16_case(rows, k, nc, 40 + k)
+    got = oracle.matmul_f16(L, w, x, rows, k, nc).astype(np.float64)
+    wd = w.view(np.float16).astype(np.float64).reshape(rows, k)
+    xd = x.astype(np.float64).reshape(nc, k)
+    want = xd @ wd.T
+    bound = (np.abs(xd) @ np.abs(wd).T) * (k * 2.0 ** -24) + 1e-30
+    assert np.all(np.abs(got - want) <= bound)
+    # a transposed operand or a dropped odd term fails by far more than the bound
+    assert not np.allclose(got, xd @ (wd * (np.arange(k) % 2 == 0)).T, rtol=1e-3)
+
+
+@need_ref
+@pytest.mark.parametrize("rows,k,nc", F16_SHAPES)
+def test_matmul_f16_matches_reference_bits(rows, k, nc):
+    w, x = _f16_case(rows, k, nc, 50 + rows)
+    a = oracle.matmul_f16(L, w, x, rows, k, nc)
+    b = oracle.matmul_f16(R, w, x, rows, k, nc)
+    assert np.array_equal(kq.bits(a), kq.bits(b))
+
+
 # ---- committed fixtures (made by tests/golden/make_golden.py from oracle/_ref) --------------------
 
 def _golden_files():
@@ -398,5 +434,8 @@ def test_oracle_matches_golden(path):
         y = np.zeros(n * rows, np.float32)
         L.kco_norm_mul_q8(out, g["w"], y, q, n, rows, 1e-5)
         assert np.array_equal(q, g["q"]) and np.array_equal(kq.bits(y), kq.bits(g["y"]))
+    elif kind == "matmul_f16":
+        rows, k, nc = int(g["rows"]), int(g["k"]), int(g["ncols"])
+        assert np.array_equal(kq.bits(oracle.matmul_f16(L, g["w"], g["x"], rows, k, nc)), kq.bits(g["y"]))
     else:
         pytest.fail(f"unknown fixture kind {kind}")
