@@ -55,21 +55,25 @@ typedef struct kcModel_st* kcModel_t;
 #define KC_TENSOR_ROPE_FREQS 14 /* f32 [head_dim / 2], optional: RoPE frequency factors (theta_i / ff[i]) */
 #define KC_TENSOR_COUNT 15
 #define KC_QTYPE_F32 0
+#define KC_QTYPE_F16 1 /* ggml F16: row-major fp16 values (per-layer matrices only; matmul_f16) */
 
 KC_API kcError_t kcModelCreate(const kcModelConfig* cfg, kcModel_t* model) KC_NOEXCEPT;
 KC_API kcError_t kcModelDestroy(kcModel_t model) KC_NOEXCEPT;
-/* What a tensor holds: qtype (KC_QTYPE_F32, KC_QTYPE_Q4_K, KC_QTYPE_Q6_K), rows and k (f32
- * vectors: rows = 1), and the bytes kcModelSetTensor expects (ggml blocks or floats). */
+/* What a tensor holds: qtype (KC_QTYPE_F32, KC_QTYPE_F16, KC_QTYPE_Q4_K, KC_QTYPE_Q6_K), rows and k
+ * (f32 vectors: rows = 1), and the bytes kcModelSetTensor expects (ggml blocks, halves or floats). */
 KC_API kcError_t kcModelTensorInfo(kcModel_t model, int tensor, int layer, int* qtype, int* rows, int* k,
                                    size_t* bytes) KC_NOEXCEPT;
 KC_API kcError_t kcModelSetTensor(kcModel_t model, int tensor, int layer, const void* host, size_t bytes) KC_NOEXCEPT;
 /* The same with the weight type given: any matrix tensor takes KC_QTYPE_Q4_K or KC_QTYPE_Q6_K
- * (a GGUF "Q4_K_M" file mixes them per layer), the f32 vectors KC_QTYPE_F32. (A layer whose gate
- * and up matrices differ in type decodes single tokens with the unfused kernels.) */
+ * (a GGUF "Q4_K_M" file mixes them per layer), the per-layer matrices also KC_QTYPE_F16 (ggml F16,
+ * e.g. a Qwen3 attn_v; multiplied by the f32 activations, as the reference's ggml backend does), the
+ * f32 vectors KC_QTYPE_F32. (A model with an F16 matrix, or a layer whose gate and up matrices differ
+ * in type, decodes single tokens with the unfused kernels.) */
 KC_API kcError_t kcModelSetTensorTyped(kcModel_t model, int tensor, int layer, int qtype, const void* host,
                                        size_t bytes) KC_NOEXCEPT;
 /* Creates a model from a GGUF file (general.architecture "llama" or "qwen3"; Q4_K / Q6_K matrices,
- * f32 norms; output.weight absent = tied to token_embd; rope_freqs.weight optional): the
+ * F16 per-layer matrices, f32 norms; output.weight absent = tied to token_embd; rope_freqs.weight
+ * optional): the
  * hyperparameters come from the file's metadata, max_ctx and max_batch from the caller. Errors
  * (unreadable file, unsupported architecture or tensor type, shape mismatch) return InvalidValue
  * with the reason in kcGetLastErrorDetail. The file is read once; the model does not keep it. */

@@ -27,7 +27,7 @@ ERRORS = ["Success", "NotInitialized", "InvalidValue", "InvalidDevice", "OutOfMe
           "DynamicCodeBlocked", "LaunchFailure", "KernelFault", "ContextPoisoned", "NotReady", "InternalError"]
 ERR = {name: i for i, name in enumerate(ERRORS)}
 HOST_TO_DEVICE, DEVICE_TO_HOST, DEVICE_TO_DEVICE, HOST_TO_HOST = range(4)
-QTYPE = {"q4k": 12, "q6k": 14}
+QTYPE = {"q4k": 12, "q6k": 14, "f16": 1}
 BLOCK_BYTES = {"q4k": 144, "q6k": 210}
 
 _p = C.c_void_p

@@ -36,6 +36,7 @@ E fail(const std::string& why) {
 int qtypeOfGgml(int t) {
     switch (t) {
         case KC_GGML_F32: return KC_QTYPE_F32;
+        case KC_GGML_F16: return KC_QTYPE_F16;
         case KC_GGML_Q4_K: return KC_QTYPE_Q4_K;
         case KC_GGML_Q6_K: return KC_QTYPE_Q6_K;
         default: return -1;
@@ -51,7 +52,7 @@ E setFrom(kcGguf_t g, kcModel_t m, const std::string& name, int id, int layer) {
     const void* data = nullptr;
     if (kcGgufTensorInfo(g, name.c_str(), &type, &nd, ne, &bytes, &data) != ok) return fail("missing tensor " + name);
     const int qt = qtypeOfGgml(type);
-    if (qt < 0) return fail("tensor " + name + ": ggml type " + std::to_string(type) + " not supported (Q4_K, Q6_K, F32)");
+    if (qt < 0) return fail("tensor " + name + ": ggml type " + std::to_string(type) + " not supported (Q4_K, Q6_K, F16, F32)");
     int want_qt = 0, rows = 0, k = 0;
     if (E e = kcModelTensorInfo(m, id, layer, &want_qt, &rows, &k, nullptr); e != ok) return e;
     const bool vec = want_qt == KC_QTYPE_F32;

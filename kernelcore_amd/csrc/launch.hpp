@@ -68,9 +68,10 @@ int launchNormMulQ8(bool per256, const kcNormMulQ8Args& a, hipStream_t s);
 // Batch fusions of the model path: x = a + (b [+ b2]) into out (a null: x = b), RMS norm with w
 // and per-256 quantization into q (rows slots of n / 256 * 85 ints); RoPE of q into qr and of k,
 // with k and v stored as fp16 into cache rows pos[t] (dst_row 32-bit words per row).
-// (ao, when given, also receives the MFMA layout of the quantized rows.)
+// (ao, when given, also receives the MFMA layout of the quantized rows; y, when given, the normed
+// rows x r w in f32, the values that are quantized.)
 int launchAddNormQ8K(const float* a, const float* b, const float* b2, float* out, const float* w, int* q, int n,
-                     int rows, float eps, hipStream_t s, const ActF16* ao = nullptr);
+                     int rows, float eps, hipStream_t s, const ActF16* ao = nullptr, float* y = nullptr);
 int launchSiluMulQ8KAct(const kcSiluMulQ8FArgs& a, const ActF16* ao, hipStream_t s);
 int launchRopeQKStore(const float* q, float* qr, const float* k, const float* v, int* kcache, int* vcache,
                       const int* pos, const float* ff, int head_dim, int nh, int nkv, int n, float log2_base, int neox,

@@ -398,7 +398,7 @@ __global__ void rope_qk_store_kernel(const float* __restrict__ q, float* __restr
 template <bool A16>
 __global__ __launch_bounds__(1024) void add_norm_q8k_kernel(const float* a, const float* b, const float* b2, float* out,
                                                            const float* __restrict__ w, int* __restrict__ q, int n,
-                                                           float eps, ActF16 ao, int has_ao) {
+                                                           float eps, ActF16 ao, int has_ao, float* __restrict__ y) {
     extern __shared__ float xs[];  // n / 32 blocks of 36 floats, then n / 32 sums of squares
     const int nsb = n / 256, nb = n / 32;
     const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -439,8 +439,9 @@ __global__ __launch_bounds__(1024) void add_norm_q8k_kernel(const float* a, cons
         const int e = sb * 256 + 4 * lane;
         const float4 xv = *reinterpret_cast<const float4*>(xs + (e >> 5) * 36 + (e & 31));
         const float4 wv = load4<A16>(w + e);
-        quant256Wave(xv.x * r * wv.x, xv.y * r * wv.y, xv.z * r * wv.z, xv.w * r * wv.w, qr, nsb, sb,
-                     has_ao ? &ao : nullptr, row);
+        const float4 yv = make_float4(xv.x * r * wv.x, xv.y * r * wv.y, xv.z * r * wv.z, xv.w * r * wv.w);
+        if (y) store4<A16>(y + r0 + e, yv);  // the normed row itself (the input of F16 matrices)
+        quant256Wave(yv.x, yv.y, yv.z, yv.w, qr, nsb, sb, has_ao ? &ao : nullptr, row);
     }
 }
 
@@ -697,16 +698,16 @@ int launchRopeQKStore(const float* q, float* qr, const float* k, const float* v,
 }
 
 int launchAddNormQ8K(const float* a, const float* b, const float* b2, float* out, const float* w, int* q, int n,
-                     int rows, float eps, hipStream_t s, const ActF16* ao) {
+                     int rows, float eps, hipStream_t s, const ActF16* ao, float* y) {
     if (rows <= 0) return 0;
     const size_t lds = sizeof(float) * ((size_t)n / 32 * 37);
     if (n % 256 || lds > 65536) return fromHip(hipErrorInvalidValue, "add + norm: row length");
-    if (al16(b) && (!b2 || al16(b2)) && (!a || (al16(a) && al16(out))) && al16(w))
+    if (al16(b) && (!b2 || al16(b2)) && (!a || (al16(a) && al16(out))) && al16(w) && (!y || al16(y)))
         hipLaunchKernelGGL(add_norm_q8k_kernel<true>, dim3(rows), dim3(waveThreads(n)), lds, s, a, b, b2, out, w, q, n,
-                           eps, ao ? *ao : ActF16{}, ao ? 1 : 0);
+                           eps, ao ? *ao : ActF16{}, ao ? 1 : 0, y);
     else
         hipLaunchKernelGGL(add_norm_q8k_kernel<false>, dim3(rows), dim3(waveThreads(n)), lds, s, a, b, b2, out, w, q, n,
-                           eps, ao ? *ao : ActF16{}, ao ? 1 : 0);
+                           eps, ao ? *ao : ActF16{}, ao ? 1 : 0, y);
     return fromHip(hipGetLastError(), "add + norm");
 }
 

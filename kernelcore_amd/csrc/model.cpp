@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 #include <kernelcore/model.h>
 
+#include <array>
 #include <cmath>
 #include <cstring>
 #include <memory>
@@ -28,7 +29,8 @@ struct Layer {
     void *wq = nullptr, *wk = nullptr, *wv = nullptr, *wo = nullptr, *wg = nullptr, *wu = nullptr, *wd = nullptr;
     float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
     int *kcache = nullptr, *vcache = nullptr;
-    int q6[KC_TENSOR_COUNT] = {};  // per matrix: 1 if its weights are Q6_K (set with the tensor)
+    int q6[KC_TENSOR_COUNT] = {};   // per matrix: 1 if its weights are Q6_K (set with the tensor)
+    int f16[KC_TENSOR_COUNT] = {};  // per matrix: 1 if its weights are F16 (row-major, matmul_f16)
 };
 
 // The type a tensor takes by default (kcModelSetTensor); kcModelSetTensorTyped may choose the
@@ -137,6 +139,7 @@ void shapeOf(const kcModelConfig& c, int tensor, int* rows, int* k) {
 
 size_t ggmlBytes(int qtype, int rows, int k) {
     if (qtype == KC_QTYPE_F32) return size_t(rows) * k * 4;
+    if (qtype == KC_QTYPE_F16) return size_t(rows) * k * 2;
     return size_t(rows) * (k / 256) * (qtype == KC_QTYPE_Q6_K ? 210 : 144);
 }
 
@@ -146,6 +149,22 @@ int matvec(bool q6, const void* w, const int* slot, float* y, int rows, int k, h
     kcMatvecQ4Q8Args a{static_cast<const int*>(w), slot, reinterpret_cast<const float*>(slot + k / 32 * 8), y, nullptr,
                        rows, k};
     return kcamd::launchMatvecKq(q6, a, s);
+}
+
+// Layer matrix t times one token: a K-quant matvec of the per-32 slot, or for F16 weights
+// matmul_f16 of the same activations in f32 (xf), as the reference's MUL_MAT dispatch does
+// (ggml-kernelcore.cpp:559-566).
+int proj(const Layer& l, int t, const void* w, const int* slot, const float* xf, float* y, int rows, int k,
+         hipStream_t s) {
+    if (l.f16[t]) return kcamd::launchMatmulF16(w, xf, y, rows, k, 1, s);
+    return matvec(l.q6[t], w, slot, y, rows, k, s);
+}
+
+bool anyF16(const kcModel_st* m) {
+    for (const auto& l : m->L)
+        for (int t = 0; t < KC_TENSOR_COUNT; ++t)
+            if (l.f16[t]) return true;
+    return false;
 }
 
 int normQ8(const float* x, const float* w, float* y, int* slot, int n, float eps, hipStream_t s) {
@@ -158,11 +177,11 @@ int normQ8(const float* x, const float* w, float* y, int* slot, int n, float eps
 int ffnOne(kcModel_st* m, const Layer& l, float* x, hipStream_t s) {
     const auto& c = m->c;
     KI_TRY(normQ8(x, l.ffn_norm, m->xn, m->slotE32, c.n_embd, c.norm_eps, s));
-    KI_TRY(matvec(l.q6[KC_TENSOR_W_GATE], l.wg, m->slotE32, m->gate, c.n_ff, c.n_embd, s));
-    KI_TRY(matvec(l.q6[KC_TENSOR_W_UP], l.wu, m->slotE32, m->up, c.n_ff, c.n_embd, s));
+    KI_TRY(proj(l, KC_TENSOR_W_GATE, l.wg, m->slotE32, m->xn, m->gate, c.n_ff, c.n_embd, s));
+    KI_TRY(proj(l, KC_TENSOR_W_UP, l.wu, m->slotE32, m->xn, m->up, c.n_ff, c.n_embd, s));
     kcSiluMulQ8FArgs sa{m->gate, m->up, m->sw, m->slotF32, nullptr, c.n_ff, 1};
     KI_TRY(kcamd::launchSiluMulQ8(false, sa, s));
-    return matvec(l.q6[KC_TENSOR_W_DOWN], l.wd, m->slotF32, m->down, c.n_embd, c.n_ff, s);
+    return proj(l, KC_TENSOR_W_DOWN, l.wd, m->slotF32, m->sw, m->down, c.n_embd, c.n_ff, s);
 }
 
 // Output norm + head for the row x (partial sums in slotE32) into m->logits.
@@ -228,15 +247,15 @@ int decodeStep(kcModel_st* m, hipStream_t s) {
         if (li == 0) KI_TRY(kcamd::launchAddSumsq(nullptr, m->x, nullptr, m->slotE32, c.n_embd, 1, s));
         else KI_TRY(kcamd::launchAddSumsq(m->x, m->down, m->x, m->slotE32, c.n_embd, 1, s));
         KI_TRY(normQ8(m->x, l.attn_norm, m->xn, m->slotE32, c.n_embd, c.norm_eps, s));
-        KI_TRY(matvec(l.q6[KC_TENSOR_WQ], l.wq, m->slotE32, m->q, Q, c.n_embd, s));
-        KI_TRY(matvec(l.q6[KC_TENSOR_WK], l.wk, m->slotE32, m->k, KV, c.n_embd, s));
-        KI_TRY(matvec(l.q6[KC_TENSOR_WV], l.wv, m->slotE32, m->v, KV, c.n_embd, s));
+        KI_TRY(proj(l, KC_TENSOR_WQ, l.wq, m->slotE32, m->xn, m->q, Q, c.n_embd, s));
+        KI_TRY(proj(l, KC_TENSOR_WK, l.wk, m->slotE32, m->xn, m->k, KV, c.n_embd, s));
+        KI_TRY(proj(l, KC_TENSOR_WV, l.wv, m->slotE32, m->xn, m->v, KV, c.n_embd, s));
         KI_TRY(qkNorm(m, l, 1, s));
         KI_TRY(ropeQK(m, 1, s));
         KI_TRY(kvStore(m, l, 1, s));
         KI_TRY(attention(m, l, 1, s));
         KI_TRY(kcamd::launchQuantizeQ8x4(m->att, m->slotQ32, reinterpret_cast<float*>(m->slotQ32 + Q / 32 * 8), Q / 32, s));
-        KI_TRY(matvec(l.q6[KC_TENSOR_WO], l.wo, m->slotQ32, m->o, c.n_embd, Q, s));
+        KI_TRY(proj(l, KC_TENSOR_WO, l.wo, m->slotQ32, m->att, m->o, c.n_embd, Q, s));
         KI_TRY(kcamd::launchAddSumsq(m->x, m->o, m->x, m->slotE32, c.n_embd, 1, s));
         KI_TRY(ffnOne(m, l, m->x, s));
     }
@@ -252,6 +271,7 @@ bool fusedDecode(const kcModel_st* m) {
     const auto& c = m->c;
     for (const auto& l : m->L)  // the SwiGLU matvec runs gate and up as one type
         if (l.q6[KC_TENSOR_W_GATE] != l.q6[KC_TENSOR_W_UP]) return false;
+    if (anyF16(m)) return false;  // the fused matvecs take K-quant weights only
     return kcamd::option("decode_path") != 1 && kcamd::attnDecodeSupports(c.head_dim, c.n_head / c.n_head_kv);
 }
 
@@ -322,6 +342,21 @@ int decodeStepFused(kcModel_st* m, hipStream_t s) {
 
 int decodeAny(kcModel_st* m, hipStream_t s) { return fusedDecode(m) ? decodeStepFused(m, s) : decodeStep(m, s); }
 
+// The matrices t[0..nm) of a layer that read the same batch activations: the K-quant ones in one
+// grouped MFMA launch on the per-256 slots, each F16 one as matmul_f16 of the f32 rows xf.
+int batchProj(kcModel_st* m, const Layer& l, std::array<int, 3> t, std::array<const void*, 3> w,
+              std::array<float*, 3> y, std::array<int, 3> rows, int nm, const int* slot, const float* xf, int k, int n,
+              hipStream_t s, const kcamd::ActF16* act) {
+    kcamd::MmPart parts[3];
+    int np = 0;
+    for (int i = 0; i < nm; ++i) {
+        if (l.f16[t[i]]) KI_TRY(kcamd::launchMatmulF16(w[i], xf, y[i], rows[i], k, n, s));
+        else parts[np++] = kcamd::MmPart{w[i], {y[i], nullptr}, rows[i], l.q6[t[i]]};
+    }
+    int ks = 1;
+    return np ? kcamd::launchMatmulGroup(parts, np, slot, k, n, 1, &ks, s, act) : 0;
+}
+
 // n > 1 tokens (m->tokens[0..n)) at positions *n_past ..: per-256 slots and the matmuls.
 int batchStep(kcModel_st* m, int n, hipStream_t s) {
     const auto& c = m->c;
@@ -343,34 +378,48 @@ int batchStep(kcModel_st* m, int n, hipStream_t s) {
     for (int li = 0; li < c.n_layer; ++li) {
         const Layer& l = m->L[li];
         // residual add (layer 0: the embeddings) + RMS norm + per-256 quantization in one kernel
+        // (also the normed rows in f32 when an F16 matrix reads them)
+        const bool f16_qkv = l.f16[KC_TENSOR_WQ] || l.f16[KC_TENSOR_WK] || l.f16[KC_TENSOR_WV];
+        float* yq = f16_qkv ? m->xn : nullptr;
         if (li == 0) KI_TRY(kcamd::launchAddNormQ8K(nullptr, m->x, nullptr, nullptr, l.attn_norm, m->slotEK, E_, n,
-                                                    c.norm_eps, s, aE));
+                                                    c.norm_eps, s, aE, yq));
         else KI_TRY(kcamd::launchAddNormQ8K(m->x, m->down, down2, m->x, l.attn_norm, m->slotEK, E_, n, c.norm_eps, s,
-                                            aE));
-        const kcamd::MmPart qkv[3] = {{l.wq, {m->q, nullptr}, Q, l.q6[KC_TENSOR_WQ]},
-                                      {l.wk, {m->k, nullptr}, KV, l.q6[KC_TENSOR_WK]},
-                                      {l.wv, {m->v, nullptr}, KV, l.q6[KC_TENSOR_WV]}};
-        KI_TRY(kcamd::launchMatmulGroup(qkv, 3, m->slotEK, E_, n, 1, &ks, s, aE));
+                                            aE, yq));
+        KI_TRY(batchProj(m, l, {KC_TENSOR_WQ, KC_TENSOR_WK, KC_TENSOR_WV}, {l.wq, l.wk, l.wv}, {m->q, m->k, m->v},
+                         {Q, KV, KV}, 3, m->slotEK, m->xn, E_, n, s, aE));
         KI_TRY(qkNorm(m, l, n, s));
         // RoPE of q and k with the fp16 cache stores of k and v in one kernel
         KI_TRY(kcamd::launchRopeQKStore(c.qk_norm ? m->att : m->q, m->qr, c.qk_norm ? m->kr : m->k, m->v, l.kcache,
                                         l.vcache, m->pos, m->ones, c.head_dim, c.n_head, c.n_head_kv, n,
                                         std::log2(c.rope_theta), c.rope_neox, KV / 2, c.max_ctx, s));
         KI_TRY(attention(m, l, n, s));
-        KI_TRY(kcamd::launchQuantizeColsK(m->att, m->slotQK, Q, n, s, aQ));
-        const kcamd::MmPart op{l.wo, {m->o, m->o2}, E_, l.q6[KC_TENSOR_WO]};
-        KI_TRY(kcamd::launchMatmulGroup(&op, 1, m->slotQK, Q, n, 2, &ks, s, aQ));
-        const float* o2 = ks == 2 ? m->o2 : nullptr;
+        const float* o2 = nullptr;
+        if (l.f16[KC_TENSOR_WO]) {
+            KI_TRY(kcamd::launchMatmulF16(l.wo, m->att, m->o, E_, Q, n, s));
+        } else {
+            KI_TRY(kcamd::launchQuantizeColsK(m->att, m->slotQK, Q, n, s, aQ));
+            const kcamd::MmPart op{l.wo, {m->o, m->o2}, E_, l.q6[KC_TENSOR_WO]};
+            KI_TRY(kcamd::launchMatmulGroup(&op, 1, m->slotQK, Q, n, 2, &ks, s, aQ));
+            o2 = ks == 2 ? m->o2 : nullptr;
+        }
         if (li + 1 < c.n_layer) {
-            KI_TRY(kcamd::launchAddNormQ8K(m->x, m->o, o2, m->x, l.ffn_norm, m->slotEK, E_, n, c.norm_eps, s, aE));
-            const kcamd::MmPart gu[2] = {{l.wg, {m->gate, nullptr}, c.n_ff, l.q6[KC_TENSOR_W_GATE]},
-                                         {l.wu, {m->up, nullptr}, c.n_ff, l.q6[KC_TENSOR_W_UP]}};
-            KI_TRY(kcamd::launchMatmulGroup(gu, 2, m->slotEK, E_, n, 1, &ks, s, aE));
-            kcSiluMulQ8FArgs sa{m->gate, m->up, nullptr, m->slotFK, nullptr, c.n_ff, n};  // no f32 output needed
+            const bool f16_gu = l.f16[KC_TENSOR_W_GATE] || l.f16[KC_TENSOR_W_UP];
+            KI_TRY(kcamd::launchAddNormQ8K(m->x, m->o, o2, m->x, l.ffn_norm, m->slotEK, E_, n, c.norm_eps, s, aE,
+                                           f16_gu ? m->xn : nullptr));
+            KI_TRY(batchProj(m, l, {KC_TENSOR_W_GATE, KC_TENSOR_W_UP, 0}, {l.wg, l.wu, nullptr},
+                             {m->gate, m->up, nullptr}, {c.n_ff, c.n_ff, 0}, 2, m->slotEK, m->xn, E_, n, s, aE));
+            // SwiGLU straight into the quantized form (and into f32 when the down matrix is F16)
+            const bool f16_d = l.f16[KC_TENSOR_W_DOWN];
+            kcSiluMulQ8FArgs sa{m->gate, m->up, f16_d ? m->sw : nullptr, m->slotFK, nullptr, c.n_ff, n};
             KI_TRY(kcamd::launchSiluMulQ8KAct(sa, aF, s));
-            const kcamd::MmPart dp{l.wd, {m->down, m->down2}, E_, l.q6[KC_TENSOR_W_DOWN]};
-            KI_TRY(kcamd::launchMatmulGroup(&dp, 1, m->slotFK, c.n_ff, n, 2, &ks, s, aF));
-            down2 = ks == 2 ? m->down2 : nullptr;
+            if (f16_d) {
+                KI_TRY(kcamd::launchMatmulF16(l.wd, m->sw, m->down, E_, c.n_ff, n, s));
+                down2 = nullptr;
+            } else {
+                const kcamd::MmPart dp{l.wd, {m->down, m->down2}, E_, l.q6[KC_TENSOR_W_DOWN]};
+                KI_TRY(kcamd::launchMatmulGroup(&dp, 1, m->slotFK, c.n_ff, n, 2, &ks, s, aF));
+                down2 = ks == 2 ? m->down2 : nullptr;
+            }
         } else {  // the last layer continues with the last token only
             KI_TRY(kcamd::launchAddSumsq(x_last, m->o + (size_t)(n - 1) * E_, x_last, m->slotE32, E_, 1, s,
                                          o2 ? o2 + (size_t)(n - 1) * E_ : nullptr));
@@ -499,6 +548,7 @@ kcError_t kcModelTensorInfo(kcModel_t m, int tensor, int layer, int* qtype, int*
                        : tensor == KC_TENSOR_OUTPUT   ? m->q6_out
                                                       : m->L[layer].q6[tensor];
         qt = q6 ? KC_QTYPE_Q6_K : KC_QTYPE_Q4_K;
+        if (perLayer(tensor) && m->L[layer].f16[tensor]) qt = KC_QTYPE_F16;
     }
     if (qtype) *qtype = qt;
     if (rows) *rows = r;
@@ -517,8 +567,11 @@ kcError_t kcModelSetTensorTyped(kcModel_t m, int tensor, int layer, int qt, cons
     int r = 0, kk = 0;
     if (E e = kcModelTensorInfo(m, tensor, layer, nullptr, &r, &kk, nullptr); e != ok) return e;
     const bool vec = qtypeOf(tensor) == KC_QTYPE_F32;
-    if (vec ? qt != KC_QTYPE_F32 : (qt != KC_QTYPE_Q4_K && qt != KC_QTYPE_Q6_K)) {
-        kcamd::setDetail("tensor %d: type %d not accepted (%s)", tensor, qt, vec ? "f32 only" : "Q4_K or Q6_K");
+    const bool f16_ok = !vec && perLayer(tensor);  // F16: the per-layer matrices
+    if (vec ? qt != KC_QTYPE_F32
+            : (qt != KC_QTYPE_Q4_K && qt != KC_QTYPE_Q6_K && !(f16_ok && qt == KC_QTYPE_F16))) {
+        kcamd::setDetail("tensor %d: type %d not accepted (%s)", tensor, qt,
+                         vec ? "f32 only" : (f16_ok ? "Q4_K, Q6_K or F16" : "Q4_K or Q6_K"));
         return kc::Error::InvalidValue;
     }
     const size_t want = ggmlBytes(qt, r, kk);
@@ -556,8 +609,11 @@ kcError_t kcModelSetTensorTyped(kcModel_t m, int tensor, int layer, int qt, cons
     const int q6 = qt == KC_QTYPE_Q6_K;
     if (tensor == KC_TENSOR_TOKEN_EMBD) m->q6_tok = q6;
     else if (tensor == KC_TENSOR_OUTPUT) m->q6_out = q6;
-    else if (l) l->q6[tensor] = q6;
-    if (qt == KC_QTYPE_F32) {
+    else if (l) {
+        l->q6[tensor] = q6;
+        l->f16[tensor] = qt == KC_QTYPE_F16;
+    }
+    if (qt == KC_QTYPE_F32 || qt == KC_QTYPE_F16) {  // uploaded as they are (F16: row-major halves)
         KM_TRYE(alloc(m, slot, bytes));
         return kcMemcpy(*slot, host, bytes, kc::CopyKind::HostToDevice);
     }

@@ -13,9 +13,9 @@ import ctypes as C
 
 import numpy as np
 
-from . import FaDims, dequant, lib, quantize_q8x4, quantize_q8k
+from . import FaDims, dequant, lib, matmul_f16, quantize_q8x4, quantize_q8k
 
-Q4K, Q6K, F32 = 12, 14, 0
+Q4K, Q6K, F32, F16 = 12, 14, 0, 1
 BB = {Q4K: 144, Q6K: 210}
 
 
@@ -32,7 +32,9 @@ class OracleModel:
     def __init__(self, cfg, tensors, threads=0, types=None):
         """tensors[(id, layer)] = raw ggml bytes (uint8) or float32 arrays; global ids use layer -1;
         (14, -1), when present, holds the RoPE frequency factors. types[(id, layer)] = Q4K / Q6K
-        overrides a matrix's default type (a GGUF Q4_K_M file mixes them). threads > 0 runs the
+        overrides a matrix's default type (a GGUF Q4_K_M file mixes them); F16 (per-layer matrices,
+        row-major halves) multiplies the f32 activations instead of the quantized ones, as the
+        reference's MUL_MAT dispatch does (ggml-kernelcore.cpp:559-566). threads > 0 runs the
         single-row matvecs with the OpenMP variants (the same per-row arithmetic, rows split over
         threads) -- the bench's CPU baseline."""
         self.cfg = cfg
@@ -52,8 +54,10 @@ class OracleModel:
     def qt(self, tid, layer=-1):
         return self.types.get((tid, layer), shapes(self.cfg)[tid][0])
 
-    def matvec(self, tid, layer, slot, rows, k):
+    def matvec(self, tid, layer, slot, rows, k, xf=None):
         qt = self.qt(tid, layer)
+        if qt == F16:
+            return matmul_f16(self.L, self.w(tid, layer).view(np.uint16), xf, rows, k, 1)[0]
         nb = k // 32
         y = np.zeros(rows, np.float32)
         xq = np.ascontiguousarray(slot[:nb * 8])
@@ -66,8 +70,10 @@ class OracleModel:
             fn(self.w(tid, layer), xq, xd, y, rows, k)
         return y
 
-    def matmul(self, tid, layer, slots, rows, k, n):
+    def matmul(self, tid, layer, slots, rows, k, n, xf=None):
         qt = self.qt(tid, layer)
+        if qt == F16:
+            return matmul_f16(self.L, self.w(tid, layer).view(np.uint16), xf, rows, k, n)
         y = np.zeros(rows * n, np.float32)
         fn = self.L.kco_matmul_q6k_q8k if qt == Q6K else self.L.kco_matmul_q4k_q8k
         fn(self.w(tid, layer), slots, y, rows, k, n)
@@ -115,21 +121,21 @@ class OracleModel:
         self.L.kco_sumsq_part(x, slot, E, 1)
         y = np.zeros(E, np.float32)
         self.L.kco_norm_mul_q8(x, wt, y, slot, E, 1, np.float32(self.cfg["norm_eps"]))
-        return slot
+        return slot, y
 
     def _ffn_one(self, l, x):
         c = self.cfg
-        slot = self._norm32(x, self.w(8, l))
-        g = self.matvec(9, l, slot, c["n_ff"], c["n_embd"])
-        u = self.matvec(10, l, slot, c["n_ff"], c["n_embd"])
+        slot, y = self._norm32(x, self.w(8, l))
+        g = self.matvec(9, l, slot, c["n_ff"], c["n_embd"], y)
+        u = self.matvec(10, l, slot, c["n_ff"], c["n_embd"], y)
         s = np.zeros(c["n_ff"], np.float32)
         q = np.zeros(c["n_ff"] // 32 * 11, np.int32)
         self.L.kco_silu_mul_q8f(g, u, s, q, c["n_ff"], 1)
-        return self.matvec(11, l, q, c["n_embd"], c["n_ff"])
+        return self.matvec(11, l, q, c["n_embd"], c["n_ff"], s)
 
     def _head(self, x):
         c = self.cfg
-        slot = self._norm32(x, self.w(1))
+        slot, _ = self._norm32(x, self.w(1))
         return self.matvec(2, -1, slot, c["n_vocab"], c["n_embd"])
 
     def _qkv_post(self, l, q, k, n, p0):
@@ -163,16 +169,16 @@ class OracleModel:
             for l in range(c["n_layer"]):
                 if l > 0:
                     x = x + down
-                slot = self._norm32(x, self.w(3, l))
-                q = self.matvec(4, l, slot, Q, E)
-                k = self.matvec(5, l, slot, KV, E)
-                v = self.matvec(6, l, slot, KV, E)
+                slot, xn = self._norm32(x, self.w(3, l))
+                q = self.matvec(4, l, slot, Q, E, xn)
+                k = self.matvec(5, l, slot, KV, E, xn)
+                v = self.matvec(6, l, slot, KV, E, xn)
                 qr, kr = self._qkv_post(l, q.reshape(1, -1), k.reshape(1, -1), 1, p0)
                 self.set_rows(l, kr, v.reshape(1, -1), p0)
                 att = self.attention(l, qr, 1, p0).reshape(-1)
                 xq, xd = quantize_q8x4(self.L, att)
                 aslot = np.concatenate([xq, xd.view(np.int32), np.zeros(Q // 32, np.int32)])
-                o = self.matvec(7, l, aslot, E, Q)
+                o = self.matvec(7, l, aslot, E, Q, att)
                 x = x + o
                 down = self._ffn_one(l, x)
             x = x + down
@@ -187,27 +193,27 @@ class OracleModel:
                 slots = np.zeros(n * nsb * 85, np.int32)
                 y = np.zeros(n * E, np.float32)
                 self.L.kco_norm_mul_q8k(np.ascontiguousarray(x.reshape(-1)), self.w(3, l), y, slots, sq, E, n, eps)
-                q = self.matmul(4, l, slots, Q, E, n)
-                k = self.matmul(5, l, slots, KV, E, n)
-                v = self.matmul(6, l, slots, KV, E, n)
+                q = self.matmul(4, l, slots, Q, E, n, y)
+                k = self.matmul(5, l, slots, KV, E, n, y)
+                v = self.matmul(6, l, slots, KV, E, n, y)
                 qr, kr = self._qkv_post(l, q, k, n, p0)
                 self.set_rows(l, kr, v, p0)
                 att = self.attention(l, qr.reshape(-1), n, p0)
                 aslots = np.zeros(n * Q // 256 * 85, np.int32)
                 self.L.kco_quantize_cols_k(np.ascontiguousarray(att.reshape(-1)), aslots, Q, n)
-                o = self.matmul(7, l, aslots, E, Q, n)
+                o = self.matmul(7, l, aslots, E, Q, n, att)
                 if l + 1 < c["n_layer"]:
                     x = x + o
                     sq = np.zeros(n * nb * 11, np.int32)
                     self.L.kco_sumsq_part(np.ascontiguousarray(x.reshape(-1)), sq, E, n)
                     self.L.kco_norm_mul_q8k(np.ascontiguousarray(x.reshape(-1)), self.w(8, l), y, slots, sq, E, n, eps)
-                    g = self.matmul(9, l, slots, c["n_ff"], E, n)
-                    u = self.matmul(10, l, slots, c["n_ff"], E, n)
+                    g = self.matmul(9, l, slots, c["n_ff"], E, n, y)
+                    u = self.matmul(10, l, slots, c["n_ff"], E, n, y)
                     s = np.zeros(n * c["n_ff"], np.float32)
                     fslots = np.zeros(n * c["n_ff"] // 256 * 85, np.int32)
                     self.L.kco_silu_mul_q8k(np.ascontiguousarray(g.reshape(-1)), np.ascontiguousarray(u.reshape(-1)), s,
                                             fslots, c["n_ff"], n)
-                    down = self.matmul(11, l, fslots, E, c["n_ff"], n)
+                    down = self.matmul(11, l, fslots, E, c["n_ff"], n, s)
                 else:
                     x = (x[n - 1] + o[n - 1]).astype(np.float32)
                     down = self._ffn_one(l, x)

@@ -3,11 +3,12 @@ bounded fp16 scales (the reference tests' generator, tests/test_llm_kernels.cpp:
 weights near 1. Returns {(tensor_id, layer): array} in the layout kcModelSetTensor expects."""
 import numpy as np
 
-from oracle.model import F32, Q6K, shapes
+from oracle.model import F16, F32, Q6K, shapes
 
 
 def random_weights(cfg, seed, types=None):
-    """types[(id, layer)] = Q4K / Q6K overrides a matrix's default type."""
+    """types[(id, layer)] = Q4K / Q6K / F16 overrides a matrix's default type (F16: row-major
+    halves ~ N(0, 0.02), as uint8 bytes)."""
     rng = np.random.default_rng(seed)
     out = {}
     table = shapes(cfg)
@@ -20,6 +21,9 @@ def random_weights(cfg, seed, types=None):
         qt = types.get((tid, layer), qt)
         if qt == F32:
             out[(tid, layer)] = rng.uniform(0.8, 1.2, k).astype(np.float32)
+            continue
+        if qt == F16:
+            out[(tid, layer)] = (rng.standard_normal(rows * k) * 0.02).astype(np.float16).view(np.uint8)
             continue
         bb = 210 if qt == Q6K else 144
         n = rows * (k // 256)

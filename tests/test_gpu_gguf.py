@@ -1,5 +1,5 @@
 """kcModelLoadGguf on the GPU: synthetic model files (tests/gguf_writer.py, the llama.cpp layout)
-with mixed Q4_K / Q6_K matrices as in a Q4_K_M file, RoPE frequency factors, and a tied head.
+with mixed Q4_K / Q6_K matrices as in a Q4_K_M file (and F16 attn_v, as some Qwen3 files carry), RoPE frequency factors, and a tied head.
 The loaded model must give the same logits, bit for bit, as the same weights set through
 kcModelSetTensorTyped, and meet the oracle's bar (1e-2 relative L2) with the same per-tensor types
 (the reference loader: llm/gguf_model.cpp:51-106)."""
@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import kernelcore_amd as kc
-from oracle.model import F32, Q4K, Q6K, OracleModel, shapes
+from oracle.model import F16, F32, Q4K, Q6K, OracleModel, shapes
 from tests import gguf_writer as gw
 from tests.model_weights import random_weights
 
@@ -75,11 +75,15 @@ def run_pair(m_a, m_b, o, prompt, steps, cfg):
     assert list(m_a.generate(4)) == want
 
 
-@pytest.mark.parametrize("name,cfg,arch,tied,n_prompt", [("llama", LLAMA, "llama", False, 70),
-                                                         ("qwen3", QWEN, "qwen3", True, 40)])
-def test_load_gguf_matches_set_tensor_and_oracle(tmp_path, name, cfg, arch, tied, n_prompt):
+@pytest.mark.parametrize("name,cfg,arch,tied,n_prompt,f16_v", [("llama", LLAMA, "llama", False, 70, False),
+                                                               ("qwen3", QWEN, "qwen3", True, 40, False),
+                                                               ("qwen3-f16-v", QWEN, "qwen3", True, 40, True)])
+def test_load_gguf_matches_set_tensor_and_oracle(tmp_path, name, cfg, arch, tied, n_prompt, f16_v):
     rng = np.random.default_rng(21)
     types = mixed_types(cfg, rng)
+    if f16_v:  # F16 attn_v in every layer (matmul_f16 of the f32 activations)
+        for l in range(cfg["n_layer"]):
+            types[(6, l)] = F16
     w = random_weights(cfg, 13, types)
     if tied:  # the head is the embedding matrix, in its type
         w[(2, -1)] = w[(0, -1)]

@@ -241,3 +241,47 @@ def test_model_long_context_split_attention():
         lg, lo = m.forward([t]), o.forward([t])
         assert rel_l2(lg, lo) < 1e-2, rel_l2(lg, lo)
     m.close()
+
+
+@pytest.mark.parametrize("name,cfg,f16", [
+    ("llama-f16-v", LLAMA, [(6, 0), (6, 1)]),                                      # F16 attn_v (a Qwen3 GGUF case)
+    ("qwen3-f16-mixed", QWEN, [(6, 0), (7, 0), (9, 0), (10, 0), (11, 0), (4, 1)]),  # every matrix kind
+])
+def test_model_f16_matrices(name, cfg, f16):
+    """F16 per-layer matrices (kcModelSetTensorTyped with KC_QTYPE_F16): matmul_f16 of the f32
+    activations in the prompt (MFMA kernel), the single-token steps and the graph-replayed generate
+    (unfused decode, per-row kernel), against the oracle with the same types."""
+    from oracle.model import F16
+    note(f"model {name}: building")
+    types = {t: F16 for t in f16}
+    w = random_weights(cfg, 23, types)
+    m = kc.Model(**cfg)
+    for (tid, layer), data in w.items():
+        m.set_tensor(tid, layer, data, "f16" if (tid, layer) in types else None)
+    for t in f16:
+        qt, rows, k, nbytes = m.tensor_info(t[0], t[1])
+        assert qt == 1 and nbytes == rows * k * 2
+    o = OracleModel(cfg, w, types=types)
+    prompt = np.random.default_rng(9).integers(0, cfg["n_vocab"], 40).astype(np.int32)
+    lg, lo = m.forward(prompt), o.forward(prompt)
+    assert rel_l2(lg, lo) < 1e-2, rel_l2(lg, lo)
+    note(f"model {name}: prompt rel L2 {rel_l2(lg, lo):.2e}")
+    for _ in range(3):
+        t = int(np.argmax(lo))
+        lg, lo = m.forward([t]), o.forward([t])
+        assert rel_l2(lg, lo) < 1e-2, rel_l2(lg, lo)
+    want = []
+    for _ in range(5):
+        want.append(int(np.argmax(lo)))
+        lo = o.forward([want[-1]])
+    assert list(m.generate(5)) == want
+    m.close()
+
+
+def test_model_f16_rejected_for_global_matrices():
+    cfg = dict(LLAMA, n_layer=1)
+    m = kc.Model(**cfg)
+    _, rows, k, _ = m.tensor_info("output")
+    with pytest.raises(kc.KcError):
+        m.set_tensor("output", -1, np.zeros(rows * k * 2, np.uint8), "f16")
+    m.close()
