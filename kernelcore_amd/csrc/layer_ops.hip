@@ -109,8 +109,9 @@ __device__ __forceinline__ void actF16Store(const ActF16& ao, int nsb, int s, in
 // max and the integer sums taken across lanes (both exact in any order).
 // ao (optional): the same codes as fp16, the min operands and the scale in the MFMA matmul's
 // layout (ActF16) for column col.
+// (ao is taken by value: the address of a kernel argument would put it in scratch memory.)
 __device__ __forceinline__ void quant256Wave(float y0, float y1, float y2, float y3, int* qc, int nsb, int s,
-                                             const ActF16* ao = nullptr, int col = 0) {
+                                             ActF16 ao = ActF16{}, bool use_ao = false, int col = 0) {
     const int lane = threadIdx.x & 63;
     float am = fmaxf(fmaxf(fmaxf(y0, 0.0f - y0), fmaxf(y1, 0.0f - y1)), fmaxf(fmaxf(y2, 0.0f - y2), fmaxf(y3, 0.0f - y3)));
     am = waveMax(am);
@@ -134,7 +135,7 @@ __device__ __forceinline__ void quant256Wave(float y0, float y1, float y2, float
     }
     if (lane < 4) qc[nsb * 81 + s * 4 + lane] = lane == 0 ? pw[0] : (lane == 1 ? pw[1] : (lane == 2 ? pw[2] : pw[3]));
     if (lane == 0) reinterpret_cast<float*>(qc + nsb * 64)[s] = d;
-    if (ao) actF16Store(*ao, nsb, s, col, lane, c0, c1, c2, c3, b32, d);
+    if (use_ao) actF16Store(ao, nsb, s, col, lane, c0, c1, c2, c3, b32, d);
 }
 
 // Four consecutive floats at p (16-byte aligned when A16).
@@ -274,7 +275,7 @@ __global__ __launch_bounds__(1024) void silu_mul_q8k_kernel(const float* __restr
         const float4 gv = load4<A16>(g + o), uv = load4<A16>(u + o);
         const float4 yv = make_float4(silu(gv.x) * uv.x, silu(gv.y) * uv.y, silu(gv.z) * uv.z, silu(gv.w) * uv.w);
         if (y) store4<A16>(y + o, yv);
-        quant256Wave(yv.x, yv.y, yv.z, yv.w, qc, nsb, sb, has_ao ? &ao : nullptr, c);
+        quant256Wave(yv.x, yv.y, yv.z, yv.w, qc, nsb, sb, ao, has_ao != 0, c);
     }
 }
 
@@ -441,7 +442,7 @@ __global__ __launch_bounds__(1024) void add_norm_q8k_kernel(const float* a, cons
         const float4 wv = load4<A16>(w + e);
         const float4 yv = make_float4(xv.x * r * wv.x, xv.y * r * wv.y, xv.z * r * wv.z, xv.w * r * wv.w);
         if (y) store4<A16>(y + r0 + e, yv);  // the normed row itself (the input of F16 matrices)
-        quant256Wave(yv.x, yv.y, yv.z, yv.w, qr, nsb, sb, has_ao ? &ao : nullptr, row);
+        quant256Wave(yv.x, yv.y, yv.z, yv.w, qr, nsb, sb, ao, has_ao != 0, row);
     }
 }
 
