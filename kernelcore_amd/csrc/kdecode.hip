@@ -471,7 +471,9 @@ __device__ __forceinline__ void dmvItems(const DmvArgs& a, int part, const Act& 
     }
 }
 
-template <int PRO, int EPI>
+// N8: the norm prologue with 8 lanes per block of 32 (stageNorm8, at most two passes of the
+// workgroup), else one thread per block (stageNorm).
+template <int PRO, int EPI, bool N8>
 __global__ __launch_bounds__(EPI == kEpiSwiglu ? 768 : 512) void dmv_kernel(DmvArgs a) {
     extern __shared__ int4 lds4[];
     int* lds = reinterpret_cast<int*>(lds4);
@@ -506,7 +508,7 @@ __global__ __launch_bounds__(EPI == kEpiSwiglu ? 768 : 512) void dmv_kernel(DmvA
     StageRegs st;
     NormRegs8<2> nr8;
     NormRegs nr;
-    if (PRO == kProNorm && EPI == kEpiSwiglu) loadNorm8(nr8, a.x, a.nw, a.k);
+    if (PRO == kProNorm && N8) loadNorm8(nr8, a.x, a.nw, a.k);
     else if (PRO == kProNorm) loadNorm(nr, a.x, a.nw, a.k);
     else loadSlot(st, a.xq, a.xd, a.k / 256);
     // The first item (wave < nw <= items always): 13 slabs and a Q6_K d read for either type
@@ -532,7 +534,7 @@ __global__ __launch_bounds__(EPI == kEpiSwiglu ? 768 : 512) void dmv_kernel(DmvA
     };
     if constexpr (EPI != kEpiSwiglu) loadFirst();
     __builtin_amdgcn_sched_barrier(0);
-    if (PRO == kProNorm && EPI == kEpiSwiglu) stageNorm8(A, extra, nr8, a.k, a.eps, nsbp);
+    if (PRO == kProNorm && N8) stageNorm8(A, extra, nr8, a.k, a.eps, nsbp);
     else if (PRO == kProNorm) stageNorm(A, extra, nr, a.k, a.eps, nsbp);
     else stageSlot(A, extra, st, a.k / 256, nsbp);
     __syncthreads();
@@ -1014,14 +1016,19 @@ int launchDecodeMatvec(int pro, int epi, DmvArgs a, hipStream_t s) {
     if (ns * kTileRows > 64 * nw || ns > 8 || (epi == kEpiSwiglu && a.tpw % 2))
         return fromHip(hipErrorInvalidValue, "decode matvec: tiles per workgroup");
     const int nsb = a.k / 256, nth = 64 * nw;
-    if ((pro == kProNorm && (epi == kEpiSwiglu ? a.k / 4 > 2 * nth : a.k / 32 > nth)) ||
+    // the 8-lane norm prologue wherever two passes of the workgroup cover the row
+    const bool n8 = pro == kProNorm && (epi == kEpiSwiglu || a.k / 4 <= 2 * nth);
+    if ((pro == kProNorm && (n8 ? a.k / 4 > 2 * nth : a.k / 32 > nth)) ||
         (pro == kProSlot && (nsb * 16 > 4 * nth || nsb * 4 > nth)))
         return fromHip(hipErrorInvalidValue, "decode matvec: activations exceed the staging registers");
     const size_t lds = dmvLds(pro, epi, a.k, a.tpw);
     if (lds > 65536) return fromHip(hipErrorInvalidValue, "decode matvec: activations exceed LDS");
     const dim3 grid(wgs), block(64 * nw);
 #define KC_DMV(P, Q)                                                                                         \
-    if (pro == P && epi == Q) hipLaunchKernelGGL((dmv_kernel<P, Q>), grid, block, lds, s, a);
+    if (pro == P && epi == Q && n8 == (P == kProNorm && Q == kEpiSwiglu))                                    \
+        hipLaunchKernelGGL((dmv_kernel<P, Q, P == kProNorm && Q == kEpiSwiglu>), grid, block, lds, s, a);     \
+    if (pro == P && epi == Q && n8 && P == kProNorm && Q != kEpiSwiglu)                                        \
+        hipLaunchKernelGGL((dmv_kernel<P, Q, true>), grid, block, lds, s, a);
     KC_DMV(kProSlot, kEpiStore)
     KC_DMV(kProSlot, kEpiResid)
     KC_DMV(kProNorm, kEpiStore)

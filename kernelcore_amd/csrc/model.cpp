@@ -288,7 +288,7 @@ int decodeStepFused(kcModel_st* m, hipStream_t s) {
         qa.p2 = {l.wv, m->v, KV, l.q6[KC_TENSOR_WV], 0, 0};
         qa.nparts = 3;
         qa.k = E_;
-        qa.tpw = 1;
+        qa.tpw = kcamd::option("qkv_tiles") > 0 ? kcamd::option("qkv_tiles") : 2;  // 2 tiles: the 8-lane norm prologue
         qa.x = m->x;
         qa.nw = l.attn_norm;
         qa.eps = c.norm_eps;

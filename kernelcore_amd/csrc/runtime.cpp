@@ -1185,7 +1185,8 @@ const char* kcCodegenName(kcCodegen_t codegen) noexcept {
 
 kcError_t kcSetKernelOption(const char* option, int value) noexcept {
     return api("kcSetKernelOption", [&] {
-        static const char* known[] = {"matvec_waves", "matvec_pipe", "matvec_nt", "matmul_path", "decode_path", "attn_path", "prefill_act"};
+        static const char* known[] = {"matvec_waves", "matvec_pipe", "matvec_nt", "matmul_path", "decode_path", "attn_path", "prefill_act",
+                                      "qkv_tiles"};
         if (!option) return kc::Error::InvalidValue;
         bool found = false;
         for (const char* k : known) found |= std::strcmp(k, option) == 0;
