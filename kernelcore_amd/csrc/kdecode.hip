@@ -1012,7 +1012,14 @@ int launchDecodeMatvec(int pro, int epi, DmvArgs a, hipStream_t s) {
     }
     const int ns = epi == kEpiSwiglu ? 2 * a.tpw : a.tpw;
     int nw = ns * a.ngroups;
-    if (nw > (epi == kEpiSwiglu ? 12 : 8)) nw = epi == kEpiSwiglu ? 12 : 8;
+    // at most 12 (SwiGLU) or 8 wavefronts, a divisor of the items so that every wavefront has
+    // the same number of them
+    const int cap = epi == kEpiSwiglu ? 12 : 8;
+    if (nw > cap) {
+        const int items = nw;
+        nw = cap;
+        while (items % nw) --nw;
+    }
     if (ns * kTileRows > 64 * nw || ns > 8 || (epi == kEpiSwiglu && a.tpw % 2))
         return fromHip(hipErrorInvalidValue, "decode matvec: tiles per workgroup");
     const int nsb = a.k / 256, nth = 64 * nw;
