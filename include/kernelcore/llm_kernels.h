@@ -80,7 +80,8 @@ typedef struct kcMatmulKQ8Args {
  * weights in ggml's row-major F16 layout (rows x k halves, two per 32-bit word; the reference's
  * load-time 8-row interleave, llm_reference.cpp:740-746, has no counterpart here); x: ncols columns
  * of k floats; y: ncols columns of rows floats. rows % 8 == 0, k even; dims may be NULL, else
- * {rows, k, ncols}. */
+ * {rows, k, ncols}. From 9 columns (k % 16 == 0) the products run on the matrix cores with each
+ * activation split into two fp16 parts: activations must then stay below 65504 in magnitude. */
 typedef struct kcMatmulF16Args {
     const int* qw;
     const float* x;

@@ -344,7 +344,7 @@ int decodeAny(kcModel_st* m, hipStream_t s) { return fusedDecode(m) ? decodeStep
 
 // The matrices t[0..nm) of a layer that read the same batch activations: the K-quant ones in one
 // grouped MFMA launch on the per-256 slots, each F16 one as matmul_f16 of the f32 rows xf.
-int batchProj(kcModel_st* m, const Layer& l, std::array<int, 3> t, std::array<const void*, 3> w,
+int batchProj(const Layer& l, std::array<int, 3> t, std::array<const void*, 3> w,
               std::array<float*, 3> y, std::array<int, 3> rows, int nm, const int* slot, const float* xf, int k, int n,
               hipStream_t s, const kcamd::ActF16* act) {
     kcamd::MmPart parts[3];
@@ -385,7 +385,7 @@ int batchStep(kcModel_st* m, int n, hipStream_t s) {
                                                     c.norm_eps, s, aE, yq));
         else KI_TRY(kcamd::launchAddNormQ8K(m->x, m->down, down2, m->x, l.attn_norm, m->slotEK, E_, n, c.norm_eps, s,
                                             aE, yq));
-        KI_TRY(batchProj(m, l, {KC_TENSOR_WQ, KC_TENSOR_WK, KC_TENSOR_WV}, {l.wq, l.wk, l.wv}, {m->q, m->k, m->v},
+        KI_TRY(batchProj(l, {KC_TENSOR_WQ, KC_TENSOR_WK, KC_TENSOR_WV}, {l.wq, l.wk, l.wv}, {m->q, m->k, m->v},
                          {Q, KV, KV}, 3, m->slotEK, m->xn, E_, n, s, aE));
         KI_TRY(qkNorm(m, l, n, s));
         // RoPE of q and k with the fp16 cache stores of k and v in one kernel
@@ -406,7 +406,7 @@ int batchStep(kcModel_st* m, int n, hipStream_t s) {
             const bool f16_gu = l.f16[KC_TENSOR_W_GATE] || l.f16[KC_TENSOR_W_UP];
             KI_TRY(kcamd::launchAddNormQ8K(m->x, m->o, o2, m->x, l.ffn_norm, m->slotEK, E_, n, c.norm_eps, s, aE,
                                            f16_gu ? m->xn : nullptr));
-            KI_TRY(batchProj(m, l, {KC_TENSOR_W_GATE, KC_TENSOR_W_UP, 0}, {l.wg, l.wu, nullptr},
+            KI_TRY(batchProj(l, {KC_TENSOR_W_GATE, KC_TENSOR_W_UP, 0}, {l.wg, l.wu, nullptr},
                              {m->gate, m->up, nullptr}, {c.n_ff, c.n_ff, 0}, 2, m->slotEK, m->xn, E_, n, s, aE));
             // SwiGLU straight into the quantized form (and into f32 when the down matrix is F16)
             const bool f16_d = l.f16[KC_TENSOR_W_DOWN];
