@@ -3,7 +3,7 @@ reference's real-model check app/llm_real.cpp:292-343 in arasheedu/Kernelcore).
 
 Bars: the reference passes when at least 90% of the generated positions have the same top token
 (app/llm_real.cpp:341); its engine reaches a mean |log-prob difference| of 0.010-0.014 against
-llama.cpp (README.md:342-347). Here the reference run is the oracle on the same weights, so the
+llama.cpp (the reference's README.md:342-347). Here the reference run is the oracle on the same weights, so the
 bars are tighter: every top token equal, mean |delta log-prob| below 1e-3, top-5 overlap at least
 90%, and the free greedy run (graph-replayed generate) identical for every token."""
 import sys
