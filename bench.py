@@ -9,8 +9,10 @@ the GPU; two copies alternate so the 256 MB Infinity Cache cannot hold them.
 value = algorithmic bytes per step (ggml weight bytes + x + y, 323,730,432 B) / wall time per step,
 with every input resident in HBM. roofline: the same bytes over the matvec kernel's own average
 duration (HIP events around each launch on its stream) against the 8 TB/s HBM peak. Also reported:
-config 1 (Q4_K 3072 x 3072) rotated over >1 GB of weight copies, and the same-run CPU baseline
-(oracle/kc_oracle.c on the host cores, a bounded sample of config-2 matvecs).
+config 1 (Q4_K 3072 x 3072) rotated over >1 GB of weight copies, the Q4_K matvec at config 2's
+shape, config 3 (the prefill matmuls), configs 4 and 5 (prefill and decode of the Llama-3.2-3B and
+Qwen3-8B shapes), and the same-run CPU baselines (oracle/kc_oracle.c on the host cores, bounded
+samples of config-2 matvecs and of decode steps).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--calibrate]
 """
