@@ -59,6 +59,11 @@ typedef struct kcModel_st* kcModel_t;
 
 KC_API kcError_t kcModelCreate(const kcModelConfig* cfg, kcModel_t* model) KC_NOEXCEPT;
 KC_API kcError_t kcModelDestroy(kcModel_t model) KC_NOEXCEPT;
+/* Host-only check of a config (no device work, callable before kcInit): InvalidValue for widths the
+ * driver does not handle, else *fused = 1 when single tokens run the six fused kernels per layer
+ * and 0 when they run one kernel per op (both give the same results to the parity bars). A model
+ * with an F16 matrix, or gate and up matrices of different types, also takes the unfused path. */
+KC_API kcError_t kcModelPlanDecode(const kcModelConfig* cfg, int* fused) KC_NOEXCEPT;
 /* What a tensor holds: qtype (KC_QTYPE_F32, KC_QTYPE_F16, KC_QTYPE_Q4_K, KC_QTYPE_Q6_K), rows and k
  * (f32 vectors: rows = 1), and the bytes kcModelSetTensor expects (ggml blocks, halves or floats). */
 KC_API kcError_t kcModelTensorInfo(kcModel_t model, int tensor, int layer, int* qtype, int* rows, int* k,

@@ -138,6 +138,7 @@ def lib():
         L.kcGetKernelOption.argtypes = [C.c_char_p, C.POINTER(_i)]
         L.kcModelCreate.argtypes = [C.POINTER(ModelConfig), C.POINTER(_p)]
         L.kcModelDestroy.argtypes = [_p]
+        L.kcModelPlanDecode.argtypes = [C.POINTER(ModelConfig), C.POINTER(_i)]
         L.kcModelTensorInfo.argtypes = [_p, _i, _i, C.POINTER(_i), C.POINTER(_i), C.POINTER(_i), C.POINTER(C.c_size_t)]
         L.kcModelSetTensor.argtypes = [_p, _i, _i, _p, C.c_size_t]
         L.kcModelSetTensorTyped.argtypes = [_p, _i, _i, _i, _p, C.c_size_t]
@@ -265,6 +266,15 @@ def upload_weights(qtype, blocks_np, rows, k):
         return repack(qtype, raw, rows, k)
     finally:
         raw.free()
+
+
+def plan_decode(**cfg):
+    """kcModelPlanDecode (host only): 1 when single tokens take the fused kernels, else 0; raises
+    KcError (InvalidValue) for a config the driver rejects."""
+    c = ModelConfig(**cfg)
+    fused = _i()
+    call("kcModelPlanDecode", C.byref(c), C.byref(fused))
+    return fused.value
 
 
 class Model:

@@ -11,6 +11,8 @@
 // pairs and the per-head attn_q_norm / attn_k_norm), the architecture of BASELINE config 5.
 // Matrices may be Q4_K or Q6_K each (a Q4_K_M file mixes them); norms are f32.
 #include <cstring>
+#include <climits>
+#include <cmath>
 #include <string>
 
 #include "internal.hpp"
@@ -93,6 +95,22 @@ kcError_t kcModelLoadGguf(const char* path, int max_ctx, int max_batch, kcModel_
         num("attention.layer_norm_rms_epsilon", 1e-5, false, &eps);
         num("rope.freq_base", 10000.0, false, &theta);
         num("rope.dimension_count", head_dim, false, &rope_dims);
+        // every count must be a whole number in [1, INT_MAX] before it becomes an int
+        const struct {
+            const char* key;
+            double v;
+        } counts[] = {{"block_count", n_layer},
+                      {"embedding_length", n_embd},
+                      {"feed_forward_length", n_ff},
+                      {"attention.head_count", n_head},
+                      {"attention.head_count_kv", n_head_kv},
+                      {"attention.key_length", head_dim},
+                      {"rope.dimension_count", rope_dims}};
+        for (const auto& k : counts)
+            if (!std::isfinite(k.v) || k.v < 1.0 || k.v > double(INT_MAX) || k.v != std::floor(k.v))
+                return fail(arch + "." + k.key + " is not a whole number in [1, 2^31 - 1]");
+        if (!std::isfinite(eps) || !(eps > 0.0) || !std::isfinite(theta) || !(theta > 0.0) || theta > 3.0e38)
+            return fail("rms epsilon and rope.freq_base must be positive finite numbers");
         if (rope_dims != head_dim) return fail("partial rotary embeddings (rope.dimension_count) not supported");
         int type = 0, nd = 0;
         int64_t ne[4] = {};

@@ -23,6 +23,13 @@ int checkRange(const void* ptr, size_t bytes, const char* what);
 // compares them with `want`: returns false on a mismatch, true when they agree or no copy is held.
 bool dimsAgree(const int* dims, const int* want, int n);
 
+// Device scratch for a launch on HIP stream `stream` of at least `bytes`: the runtime's own memory
+// (not a kcMalloc allocation), one buffer per stream, reused by every launch on it. Returns nullptr
+// when the buffer would have to grow while the stream is capturing (or HIP fails): the caller then
+// takes a path without scratch. Freed by kcStreamDestroy, kcShutdown and kcDeviceReset; a buffer
+// that a capture may have recorded is kept until kcShutdown / kcDeviceReset.
+void* streamScratch(void* stream, size_t bytes);
+
 // Launch options (kcSetKernelOption).
 int option(const char* name);
 

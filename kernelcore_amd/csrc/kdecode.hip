@@ -19,6 +19,8 @@
 // bit for bit; the split softmax changes only the attention's rounding.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include <cstdint>
 
 #include "internal.hpp"
@@ -996,7 +998,55 @@ size_t dmvLds(int pro, int epi, int k, int tpw) {
     return 4 * (ints + extra);
 }
 
+DmvPlan planDecodeMatvec(int pro, int epi, int k, int tpw) {
+    DmvPlan p;
+    if (k <= 0 || k % 256 || tpw < 1) {
+        p.why = "decode matvec: k must be a positive multiple of 256 and tpw >= 1";
+        return p;
+    }
+    const int ngroups = (k / 256 + kGroupSb - 1) / kGroupSb, nsb = k / 256;
+    const int ns = epi == kEpiSwiglu ? 2 * tpw : tpw;
+    if (ns > 8 || (epi == kEpiSwiglu && tpw % 2)) {
+        p.why = "decode matvec: tiles per workgroup";
+        return p;
+    }
+    // whether nw wavefronts hold the tiles' row sums and stage the activations
+    auto fits = [&](int nw, bool* n8) {
+        const int nth = 64 * nw;
+        *n8 = pro == kProNorm && (epi == kEpiSwiglu || k / 4 <= 2 * nth);
+        if (ns * kTileRows > 64 * nw) return false;
+        if (pro == kProNorm && (*n8 ? k / 4 > 2 * nth : k / 32 > nth)) return false;
+        if (pro == kProSlot && (nsb * 16 > 4 * nth || nsb * 4 > nth)) return false;
+        return true;
+    };
+    // At most 12 (SwiGLU) or 8 wavefronts. Beyond that, a divisor of the items (from half the cap
+    // up) gives every wavefront the same number of them; where no divisor fits, the cap (the item
+    // loop strides by the wavefront count, so uneven shares are correct, only less balanced).
+    const int items = ns * ngroups, cap = epi == kEpiSwiglu ? 12 : 8;
+    int nw = items <= cap ? items : 0;
+    bool n8 = false;
+    if (!nw)
+        for (int d = cap; d >= (cap + 1) / 2 && !nw; --d)
+            if (items % d == 0 && fits(d, &n8)) nw = d;
+    if (!nw) nw = std::min(items, cap);
+    if (!fits(nw, &n8)) {
+        p.why = "decode matvec: activations exceed the staging registers";
+        return p;
+    }
+    const size_t lds = dmvLds(pro, epi, k, tpw);
+    if (lds > 65536) {
+        p.why = "decode matvec: activations exceed LDS";
+        return p;
+    }
+    p.nw = nw;
+    p.n8 = n8;
+    p.lds = lds;
+    return p;
+}
+
 int launchDecodeMatvec(int pro, int epi, DmvArgs a, hipStream_t s) {
+    const DmvPlan plan = planDecodeMatvec(pro, epi, a.k, a.tpw);
+    if (!plan.nw) return fromHip(hipErrorInvalidValue, plan.why);
     a.ngroups = (a.k / 256 + kGroupSb - 1) / kGroupSb;
     int wgs = 0;
     if (epi == kEpiSwiglu) {
@@ -1010,26 +1060,9 @@ int launchDecodeMatvec(int pro, int epi, DmvArgs a, hipStream_t s) {
             wgs += (ps[i]->tiles + a.tpw - 1) / a.tpw;
         }
     }
-    const int ns = epi == kEpiSwiglu ? 2 * a.tpw : a.tpw;
-    int nw = ns * a.ngroups;
-    // at most 12 (SwiGLU) or 8 wavefronts, a divisor of the items so that every wavefront has
-    // the same number of them
-    const int cap = epi == kEpiSwiglu ? 12 : 8;
-    if (nw > cap) {
-        const int items = nw;
-        nw = cap;
-        while (items % nw) --nw;
-    }
-    if (ns * kTileRows > 64 * nw || ns > 8 || (epi == kEpiSwiglu && a.tpw % 2))
-        return fromHip(hipErrorInvalidValue, "decode matvec: tiles per workgroup");
-    const int nsb = a.k / 256, nth = 64 * nw;
-    // the 8-lane norm prologue wherever two passes of the workgroup cover the row
-    const bool n8 = pro == kProNorm && (epi == kEpiSwiglu || a.k / 4 <= 2 * nth);
-    if ((pro == kProNorm && (n8 ? a.k / 4 > 2 * nth : a.k / 32 > nth)) ||
-        (pro == kProSlot && (nsb * 16 > 4 * nth || nsb * 4 > nth)))
-        return fromHip(hipErrorInvalidValue, "decode matvec: activations exceed the staging registers");
-    const size_t lds = dmvLds(pro, epi, a.k, a.tpw);
-    if (lds > 65536) return fromHip(hipErrorInvalidValue, "decode matvec: activations exceed LDS");
+    const int nw = plan.nw;
+    const bool n8 = plan.n8;
+    const size_t lds = plan.lds;
     const dim3 grid(wgs), block(64 * nw);
 #define KC_DMV(P, Q)                                                                                         \
     if (pro == P && epi == Q && n8 == (P == kProNorm && Q == kEpiSwiglu))                                    \
@@ -1046,11 +1079,17 @@ int launchDecodeMatvec(int pro, int epi, DmvArgs a, hipStream_t s) {
     return fromHip(hipGetLastError(), "decode matvec");
 }
 
+bool rmsQ8Supports(int n) {
+    const int nsbp = (n / 256 + kGroupSb - 1) / kGroupSb * kGroupSb;
+    const size_t lds = 4 * ((size_t)Act::ints(nsbp) + stageFloats(kProNorm, nsbp));
+    return n > 0 && n % 256 == 0 && lds <= 65536 && n / 32 <= (n <= 8192 ? 256 : 512);
+}
+
 int launchRmsQ8(const float* x, const float* w, int* slot, int n, float eps, hipStream_t s) {
     const int nsbp = (n / 256 + kGroupSb - 1) / kGroupSb * kGroupSb;
     const size_t lds = 4 * ((size_t)Act::ints(nsbp) + stageFloats(kProNorm, nsbp));
     const int threads = n <= 8192 ? 256 : 512;
-    if (lds > 65536 || n / 32 > threads) return fromHip(hipErrorInvalidValue, "rms_q8: row too long");
+    if (!rmsQ8Supports(n)) return fromHip(hipErrorInvalidValue, "rms_q8: row too long");
     hipLaunchKernelGGL(rms_q8_kernel, dim3(1), dim3(threads), lds, s, x, w, slot, n, eps);
     return fromHip(hipGetLastError(), "rms_q8");
 }

@@ -60,6 +60,18 @@ struct AttnDecodeArgs {
 
 size_t dmvLds(int pro, int epi, int k, int tpw);
 
+// The launch shape of a decode matvec (host only, no HIP call): wavefronts per workgroup, the
+// 8-lane norm prologue, LDS bytes; nw == 0 when no shape fits (`why` says which limit).
+struct DmvPlan {
+    int nw = 0;
+    bool n8 = false;
+    size_t lds = 0;
+    const char* why = nullptr;
+};
+DmvPlan planDecodeMatvec(int pro, int epi, int k, int tpw);
+// rms_q8 (the output norm before the head) handles rows up to this many values.
+bool rmsQ8Supports(int n);
+
 int launchDecodeMatvec(int pro, int epi, DmvArgs a, hipStream_t s);
 int launchRmsQ8(const float* x, const float* w, int* slot, int n, float eps, hipStream_t s);
 bool attnDecodeSupports(int D, int G);

@@ -37,7 +37,6 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
-#include <mutex>
 #include <type_traits>
 #include <vector>
 
@@ -926,41 +925,6 @@ __global__ __launch_bounds__(256) void matmul_kq_mfma_h_kernel(HGroup g, const _
                         sb1);
 }
 
-// Per-stream fp16 activation buffers (grown on demand, never while the stream is capturing).
-struct ActBuf {
-    hipStream_t s;
-    int dev;
-    void* p;
-    size_t bytes;
-};
-std::mutex g_act_mu;
-std::vector<ActBuf> g_act;
-
-void* actBuffer(hipStream_t s, size_t bytes) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
-    std::lock_guard<std::mutex> lk(g_act_mu);
-    for (auto& b : g_act)
-        if (b.s == s && b.dev == dev) {
-            if (b.bytes >= bytes) return b.p;
-            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-            if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
-            if (hipStreamSynchronize(s) != hipSuccess) return nullptr;
-            (void)hipFree(b.p);
-            b.p = nullptr;
-            b.bytes = 0;
-            if (hipMalloc(&b.p, bytes) != hipSuccess) return b.p = nullptr;
-            b.bytes = bytes;
-            return b.p;
-        }
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
-    void* p = nullptr;
-    if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
-    g_act.push_back({s, dev, p, bytes});
-    return p;
-}
-
 // The fp16 activation buffer: ncols * k halves, then (Q4_K) ncols * nsb * 16 halves of mins, then
 // nsb * ncp floats of column scales (ncp = ncols rounded up to whole 128-column tiles).
 int actCols(int ncols) { return (ncols + 127) / 128 * 128; }
@@ -1032,7 +996,7 @@ int launchMatmulMfma(bool q6k, const kcMatmulKQ8Args& a, hipStream_t s) {
     if (path == 4) return q6k ? runMfma8<true, 2>(a, s) : runMfma8<false, 2>(a, s);
     // fp16 activations staged by direct loads (a per-stream buffer, addressed with 32-bit offsets)
     if (path != 5 && (size_t)a.ncols * a.k * 2 < (1ull << 32)) {
-        if (void* act = actBuffer(s, actBytes(a.ncols, a.k))) {
+        if (void* act = streamScratch(s, actBytes(a.ncols, a.k))) {
             const MmPart part{a.qw, {a.y, nullptr}, a.rows, q6k ? 1 : 0};
             return runMfmaH(&part, 1, a.xq, a.k, a.ncols, 1, act, s);
         }
@@ -1050,7 +1014,7 @@ int launchMatmulGroup(const MmPart* parts, int nparts, const int* xq, int k, int
             *used_ks = ks;
             return runMfmaH(parts, nparts, xq, k, ncols, ks, nullptr, s, pre);
         }
-        if (void* act = actBuffer(s, actBytes(ncols, k))) {
+        if (void* act = streamScratch(s, actBytes(ncols, k))) {
             *used_ks = ks;
             return runMfmaH(parts, nparts, xq, k, ncols, ks, act, s);
         }

@@ -267,12 +267,23 @@ int decodeStep(kcModel_st* m, hipStream_t s) {
 // cache store + split-context attention; its merge + quantization; output projection + residual;
 // norm + gate/up + SwiGLU + quantization; down projection + residual. decode_path 3 runs the
 // merge's first form (one workgroup per KV head), bit-identical.
+int qkvTiles() { return kcamd::option("qkv_tiles") > 0 ? kcamd::option("qkv_tiles") : 2; }  // 2: the 8-lane norm prologue
+
+// Whether the six fused kernels have a launch shape for these widths (host only).
+bool fusedShapesFit(const kcModelConfig& c, int qkv_tiles) {
+    const int Q = c.n_head * c.head_dim;
+    return kcamd::planDecodeMatvec(kcamd::kProNorm, kcamd::kEpiStore, c.n_embd, qkv_tiles).nw &&
+           kcamd::planDecodeMatvec(kcamd::kProSlot, kcamd::kEpiResid, Q, 1).nw &&
+           kcamd::planDecodeMatvec(kcamd::kProNorm, kcamd::kEpiSwiglu, c.n_embd, 2).nw &&
+           kcamd::planDecodeMatvec(kcamd::kProSlot, kcamd::kEpiResid, c.n_ff, 1).nw && kcamd::rmsQ8Supports(c.n_embd) &&
+           kcamd::attnDecodeSupports(c.head_dim, c.n_head / c.n_head_kv);
+}
+
 bool fusedDecode(const kcModel_st* m) {
-    const auto& c = m->c;
     for (const auto& l : m->L)  // the SwiGLU matvec runs gate and up as one type
         if (l.q6[KC_TENSOR_W_GATE] != l.q6[KC_TENSOR_W_UP]) return false;
     if (anyF16(m)) return false;  // the fused matvecs take K-quant weights only
-    return kcamd::option("decode_path") != 1 && kcamd::attnDecodeSupports(c.head_dim, c.n_head / c.n_head_kv);
+    return kcamd::option("decode_path") != 1 && fusedShapesFit(m->c, qkvTiles());
 }
 
 int decodeStepFused(kcModel_st* m, hipStream_t s) {
@@ -288,7 +299,7 @@ int decodeStepFused(kcModel_st* m, hipStream_t s) {
         qa.p2 = {l.wv, m->v, KV, l.q6[KC_TENSOR_WV], 0, 0};
         qa.nparts = 3;
         qa.k = E_;
-        qa.tpw = kcamd::option("qkv_tiles") > 0 ? kcamd::option("qkv_tiles") : 2;  // 2 tiles: the 8-lane norm prologue
+        qa.tpw = qkvTiles();
         qa.x = m->x;
         qa.nw = l.attn_norm;
         qa.eps = c.norm_eps;
@@ -440,12 +451,9 @@ E checkModel(kcModel_t m) {
 
 E syncModel(kcModel_t m) { return kcStreamSynchronize(m->ks); }
 
-}  // namespace
-
-kcError_t kcModelCreate(const kcModelConfig* cfg, kcModel_t* out) noexcept {
-    if (!cfg || !out) return kc::Error::InvalidValue;
-    *out = nullptr;
-    const kcModelConfig& c = *cfg;
+// The widths every kernel of the driver handles. head_dim: 32, 64, 128 or 256 (the batch attention
+// kernel's lanes split a head row in 16 parts of at least 2 values).
+E checkConfig(const kcModelConfig& c) {
     if (c.n_layer <= 0 || c.n_embd <= 0 || c.n_embd % 256 || c.n_head <= 0 || c.n_head_kv <= 0 ||
         c.n_head % c.n_head_kv || c.head_dim <= 0 || c.head_dim % 16 || c.head_dim > 256 ||
         (c.n_head * c.head_dim) % 256 || (c.n_head_kv * c.head_dim) % 16 || c.n_ff <= 0 || c.n_ff % 256 ||
@@ -454,10 +462,20 @@ kcError_t kcModelCreate(const kcModelConfig* cfg, kcModel_t* out) noexcept {
         kcamd::setDetail("model config out of range (dims multiples of 256, head_dim a multiple of 16, max_ctx <= 16384)");
         return kc::Error::InvalidValue;
     }
-    if (256 % c.head_dim && c.head_dim != 256) {
-        kcamd::setDetail("head_dim must divide 256");
+    if (c.head_dim < 32 || 256 % c.head_dim) {
+        kcamd::setDetail("head_dim must be 32, 64, 128 or 256");
         return kc::Error::InvalidValue;
     }
+    return ok;
+}
+
+}  // namespace
+
+kcError_t kcModelCreate(const kcModelConfig* cfg, kcModel_t* out) noexcept {
+    if (!cfg || !out) return kc::Error::InvalidValue;
+    *out = nullptr;
+    const kcModelConfig& c = *cfg;
+    if (E e = checkConfig(c); e != ok) return e;
     auto m = std::unique_ptr<kcModel_st>(new (std::nothrow) kcModel_st);
     if (!m) return kc::Error::OutOfMemory;
     m->c = c;
@@ -522,6 +540,13 @@ kcError_t kcModelCreate(const kcModelConfig* cfg, kcModel_t* out) noexcept {
     for (auto [p, k] : {std::pair<void*, int>{m->actE, E_}, {m->actQ, Q}, {m->actF, F}})
         if (E e = kcMemset(p, 0, kcamd::actF16Bytes(B, k)); e != ok) return fail(e);
     *out = m.release();
+    return ok;
+}
+
+kcError_t kcModelPlanDecode(const kcModelConfig* cfg, int* fused) noexcept {
+    if (!cfg || !fused) return kc::Error::InvalidValue;
+    if (E e = checkConfig(*cfg); e != ok) return e;
+    *fused = fusedShapesFit(*cfg, qkvTiles()) ? 1 : 0;
     return ok;
 }
 

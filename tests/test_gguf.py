@@ -127,3 +127,36 @@ def test_load_gguf_rejects_before_gpu_work(tmp_path):
     with pytest.raises(kc.KcError) as e:
         kc.Model.load_gguf(path, 64, 8)
     assert "token_embd" in str(e.value)
+
+
+@pytest.mark.parametrize("key,value,vt", [("block_count", 1e12, "F64"), ("embedding_length", float("nan"), "F64"),
+                                          ("attention.head_count", 2.5, "F64"), ("feed_forward_length", 0, "U32"),
+                                          ("attention.head_count_kv", -3, "I32"),
+                                          ("attention.key_length", float("inf"), "F64"),
+                                          ("attention.head_count", 2**40, "U64")])
+def test_load_gguf_rejects_out_of_range_hyperparameters(tmp_path, key, value, vt):
+    """Counts read as doubles must be whole numbers in [1, 2^31 - 1] before they become ints."""
+    path = str(tmp_path / "h.gguf")
+    good = {"block_count": 1, "embedding_length": 256, "feed_forward_length": 256, "attention.head_count": 2}
+    kv = [("general.architecture", gw.STR, "llama")]
+    for k, v in good.items():
+        if k != key:
+            kv.append((f"llama.{k}", gw.U32, v))
+    kv.append((f"llama.{key}", getattr(gw, vt), value))
+    gw.write_gguf(path, kv, [])
+    with pytest.raises(kc.KcError) as e:
+        kc.Model.load_gguf(path, 64, 8)
+    assert e.value.name == "InvalidValue"
+    assert "whole number" in str(e.value), str(e.value)
+
+
+def test_load_gguf_rejects_non_finite_epsilon(tmp_path):
+    path = str(tmp_path / "e.gguf")
+    kv = [("general.architecture", gw.STR, "llama")] + [
+        (f"llama.{k}", gw.U32, v) for k, v in (("block_count", 1), ("embedding_length", 256),
+                                              ("feed_forward_length", 256), ("attention.head_count", 2))]
+    kv.append(("llama.attention.layer_norm_rms_epsilon", gw.F64, float("nan")))
+    gw.write_gguf(path, kv, [])
+    with pytest.raises(kc.KcError) as e:
+        kc.Model.load_gguf(path, 64, 8)
+    assert "positive finite" in str(e.value)

@@ -20,8 +20,18 @@ import oracle
 from tests import kq
 
 L = oracle.lib()
-R = oracle.ref()
-need_ref = pytest.mark.skipif(R is None, reason="oracle/_ref not built (reference tree absent)")
+
+
+@pytest.fixture(scope="module")
+def R():
+    """The reference's own llm_reference.cpp built into oracle/_ref: loaded only by the tests that
+    compare against it, and only in the container that holds the reference tree (the build never
+    travels to the GPU box)."""
+    r = oracle.ref()
+    if r is None:
+        pytest.skip("oracle/_ref not built (reference tree absent)")
+    return r
+
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 
 
@@ -36,8 +46,7 @@ def test_f16_to_f32_exhaustive_ieee():
     assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
 
 
-@need_ref
-def test_f16_to_f32_matches_reference_bits():
+def test_f16_to_f32_matches_reference_bits(R):
     for v in range(0, 65536, 7):
         a, b = L.kco_f16_to_f32(v), R.kcref_f16_to_f32(v)
         assert np.float32(a).view(np.uint32) == np.float32(b).view(np.uint32) or (np.isnan(a) and np.isnan(b))
@@ -55,8 +64,7 @@ def test_f32_to_f16_round_nearest_even_with_saturation():
     assert np.array_equal(got, want)
 
 
-@need_ref
-def test_f32_to_f16_matches_reference():
+def test_f32_to_f16_matches_reference(R):
     x = np.concatenate([kq.randn(20000, 4, 300.0), kq.randn(5000, 5, 1e-6)])
     for v in x:
         assert L.kco_f32_to_f16(float(v)) == R.kcref_f32_to_f16(float(v))
@@ -108,9 +116,8 @@ def test_dequant_textbook(qtype):
     assert np.allclose(got, want, rtol=3e-7, atol=3e-7 * np.abs(want).max())
 
 
-@need_ref
 @pytest.mark.parametrize("qtype", ["q4k", "q6k"])
-def test_dequant_matches_reference_bits(qtype):
+def test_dequant_matches_reference_bits(qtype, R):
     w = kq.random_blocks(qtype, 16, 1024, seed=12)
     assert np.array_equal(kq.bits(oracle.dequant(L, qtype, w, 16, 1024)), kq.bits(oracle.dequant(R, qtype, w, 16, 1024)))
 
@@ -159,8 +166,7 @@ def test_quantize_q8k_invariants():
     assert np.all(lo < 64)
 
 
-@need_ref
-def test_quantizers_match_reference_bits():
+def test_quantizers_match_reference_bits(R):
     x = kq.randn(256 * 12, 23, 2.0)
     a = oracle.quantize_q8x4(L, x)
     b = oracle.quantize_q8x4(R, x)
@@ -205,10 +211,9 @@ def test_matvec_close_to_dequantized_float64(qtype, rows, k):
     assert kq.rel_diff(y, exact) < 1e-5
 
 
-@need_ref
 @pytest.mark.parametrize("qtype", ["q4k", "q6k"])
 @pytest.mark.parametrize("rows,k", SHAPES)
-def test_matvec_matches_reference_bits(qtype, rows, k):
+def test_matvec_matches_reference_bits(qtype, rows, k, R):
     w = kq.random_blocks(qtype, rows, k, seed=rows + k + (qtype == "q6k"))
     x = kq.uniform(k, 62, -3, 3)
     xq, xd = oracle.quantize_q8x4(L, x)
@@ -224,8 +229,7 @@ def test_matvec_matches_reference_bits(qtype, rows, k):
 
 # ---- layer ops ------------------------------------------------------------------------------------
 
-@need_ref
-def test_layer_ops_match_reference_bits():
+def test_layer_ops_match_reference_bits(R):
     n, rows = 512, 3
     nb = n // 32
     a, b, w = kq.randn(n * rows, 31), kq.randn(n * rows, 32), kq.uniform(n, 33, 0.5, 1.5)
@@ -301,8 +305,7 @@ def test_rope_rotation_closed_form(neox):
     assert np.array_equal(y.reshape(nt, nh, hd)[0], x.reshape(nt, nh, hd)[0])  # position 0: identity
 
 
-@need_ref
-def test_rope_turns_variant_matches_reference_bits():
+def test_rope_turns_variant_matches_reference_bits(R):
     hd, nh, nt = 128, 2, 3
     x = kq.randn(hd * nh * nt, 39)
     pos = np.array([1, 300, 640], np.int32)
@@ -348,8 +351,7 @@ def test_flash_attn_closed_form():
     assert np.abs(out.reshape(want.shape) - want).max() < 1e-5
 
 
-@need_ref
-def test_flash_attn_matches_reference_bits():
+def test_flash_attn_matches_reference_bits(R):
     q, k, v, m, d = _fa_case(42)
     a = np.zeros(d.N * d.H * d.D, np.float32)
     b = np.zeros_like(a)
@@ -386,9 +388,8 @@ def test_matmul_f16_close_to_float64(rows, k, nc):
     assert not np.allclose(got, xd @ (wd * (np.arange(k) % 2 == 0)).T, rtol=1e-3)
 
 
-@need_ref
 @pytest.mark.parametrize("rows,k,nc", F16_SHAPES)
-def test_matmul_f16_matches_reference_bits(rows, k, nc):
+def test_matmul_f16_matches_reference_bits(rows, k, nc, R):
     w, x = _f16_case(rows, k, nc, 50 + rows)
     a = oracle.matmul_f16(L, w, x, rows, k, nc)
     b = oracle.matmul_f16(R, w, x, rows, k, nc)
