@@ -270,6 +270,21 @@ typedef struct kcKquantRepackArgs {
     int rows;
     int k;
 } kcKquantRepackArgs;
+/* get_rows_kquant: y[i][0..k) = the dequantized row ids[i] of a Q4_K / Q6_K weight stream, n rows.
+ * The block formula and float order of ggml's dequantize_row_q4_K / q6_K as the reference restates
+ * them (llm/llm_reference.cpp:342-383: d1 = d*sc, m1 = dmin*m, y = d1*q - m1; y = (d*sc)*q), so
+ * the values are bit-identical to it; the reference calls it for the token embedding
+ * (llm/gguf_model.cpp:96-104), ggml as GET_ROWS. ids are device ints; an id outside [0, rows)
+ * yields a row of zeros. */
+typedef struct kcGetRowsKquantArgs {
+    const void* qw;  /* the weight stream (repack_kquant) */
+    const int* ids;  /* n row ids */
+    float* y;        /* n x k floats */
+    int qtype;       /* KC_QTYPE_Q4_K or KC_QTYPE_Q6_K */
+    int rows;
+    int k;
+    int n;
+} kcGetRowsKquantArgs;
 /* Bytes of the weight stream of a rows x k matrix (buft_get_alloc_size, ggml-kernelcore.cpp:116-118). */
 KC_API kcError_t kcKquantStreamBytes(int qtype, int rows, int k, size_t* bytes) KC_NOEXCEPT;
 
@@ -298,6 +313,7 @@ typedef ::kcFaMaxArgs FaMaxArgs;
 typedef ::kcFaExpArgs FaExpArgs;
 typedef ::kcFaValuesArgs FaValuesArgs;
 typedef ::kcKquantRepackArgs KquantRepackArgs;
+typedef ::kcGetRowsKquantArgs GetRowsKquantArgs;
 typedef ::kcFlashAttnArgs FlashAttnArgs;
 inline int scratchInts(int nb) { return nb * 11; }
 inline float* scratchScales(int* q, int nb) { return reinterpret_cast<float*>(q + nb * 8); }

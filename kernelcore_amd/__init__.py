@@ -80,6 +80,8 @@ FaExpArgs = _struct("FaExpArgs", [("s", _p), ("m", _p), ("dims", _p), ("d", FaDi
 FaValuesArgs = _struct("FaValuesArgs", [("p", _p), ("v", _p), ("out", _p), ("dims", _p), ("d", FaDims)])
 FlashAttnArgs = _struct("FlashAttnArgs", [("q", _p), ("k", _p), ("v", _p), ("mask", _p), ("out", _p), ("dims", _p),
                                           ("d", FaDims), ("scale", _f)])
+GetRowsKquantArgs = _struct("GetRowsKquantArgs", [("qw", _p), ("ids", _p), ("y", _p), ("qtype", _i), ("rows", _i),
+                                                  ("k", _i), ("n", _i)])
 KquantRepackArgs = _struct("KquantRepackArgs", [("src", _p), ("dst", _p), ("qtype", _i), ("rows", _i), ("k", _i)])
 DeviceProperties = _struct("DeviceProperties", [("name", C.c_char * 128), ("worker_count", C.c_uint),
                                                 ("performance_workers", C.c_uint), ("total_memory", C.c_size_t),

@@ -14,6 +14,7 @@
 #include "internal.hpp"
 #include "kquant.hpp"
 #include "launch.hpp"
+#include "model_kernels.hpp"
 
 namespace {
 
@@ -395,6 +396,22 @@ int repackLaunch(const void* p, void* s) {
     return kcamd::launchRepack(*static_cast<const kcKquantRepackArgs*>(p), Unpack, hs(s));
 }
 
+// ---- get_rows_kquant (llm/llm_reference.cpp:342-383, used by llm/gguf_model.cpp:96-104)
+
+int getRowsValidate(const void* p, const kcLaunchContext*) {
+    const auto& a = *static_cast<const kcGetRowsKquantArgs*>(p);
+    if (a.qtype != KC_QTYPE_Q4_K && a.qtype != KC_QTYPE_Q6_K) return invalid("qtype must be Q4_K (12) or Q6_K (14)");
+    if (a.rows < 0 || a.n < 0 || a.k <= 0 || a.k % 256 != 0 || !fitsIndex(a.rows, a.k) || !fitsIndex(a.n, a.k))
+        return invalid("rows and n must be non-negative and k a positive multiple of 256");
+    KC_TRY(checkRange(a.qw, kcamd::streamBytes(a.qtype == KC_QTYPE_Q6_K, a.rows, a.k), "qw"));
+    KC_TRY(checkRange(a.ids, i32Bytes(a.n), "ids"));
+    return checkRange(a.y, f32Bytes(int64_t(a.n) * a.k), "y");
+}
+int getRowsLaunch(const void* p, void* s) {
+    const auto& a = *static_cast<const kcGetRowsKquantArgs*>(p);
+    return kcamd::launchGetRows(a.qtype == KC_QTYPE_Q6_K, a.qw, a.ids, a.y, a.n, a.k, a.rows, hs(s));
+}
+
 const kcKernelEntry kTable[] = {
     {"vector_add", vectorAddValidate, vectorAddLaunch, 1},
     {"quantize_q8x4", quantValidate, quantLaunch, 1},
@@ -429,6 +446,7 @@ const kcKernelEntry kTable[] = {
     {"flash_attn_f16", flashValidate, flashLaunch, 0},
     {"repack_kquant", repackValidate<false>, repackLaunch<false>, 0},
     {"unpack_kquant", repackValidate<true>, repackLaunch<true>, 0},
+    {"get_rows_kquant", getRowsValidate, getRowsLaunch, 0},
 };
 
 }  // namespace

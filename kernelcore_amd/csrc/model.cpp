@@ -241,7 +241,7 @@ int decodeStep(kcModel_st* m, hipStream_t s) {
     const auto& c = m->c;
     const int Q = c.n_head * c.head_dim, KV = c.n_head_kv * c.head_dim;
     KI_TRY(kcamd::launchPositions(m->n_past, 1, m->pos, m->idx, m->n_ctx, s));
-    KI_TRY(kcamd::launchGetRows(m->q6_tok, m->tok_embd, m->tokens, m->x, 1, c.n_embd, s));
+    KI_TRY(kcamd::launchGetRows(m->q6_tok, m->tok_embd, m->tokens, m->x, 1, c.n_embd, c.n_vocab, s));
     for (int li = 0; li < c.n_layer; ++li) {
         const Layer& l = m->L[li];
         if (li == 0) KI_TRY(kcamd::launchAddSumsq(nullptr, m->x, nullptr, m->slotE32, c.n_embd, 1, s));
@@ -290,7 +290,7 @@ int decodeStepFused(kcModel_st* m, hipStream_t s) {
     const auto& c = m->c;
     const int E_ = c.n_embd, Q = c.n_head * c.head_dim, KV = c.n_head_kv * c.head_dim, F = c.n_ff;
     KI_TRY(kcamd::launchPositions(m->n_past, 1, m->pos, m->idx, m->n_ctx, s));
-    KI_TRY(kcamd::launchGetRows(m->q6_tok, m->tok_embd, m->tokens, m->x, 1, E_, s));
+    KI_TRY(kcamd::launchGetRows(m->q6_tok, m->tok_embd, m->tokens, m->x, 1, E_, c.n_vocab, s));
     for (int li = 0; li < c.n_layer; ++li) {
         const Layer& l = m->L[li];
         kcamd::DmvArgs qa{};
@@ -374,7 +374,7 @@ int batchStep(kcModel_st* m, int n, hipStream_t s) {
     const int Q = c.n_head * c.head_dim, KV = c.n_head_kv * c.head_dim;
     const int E_ = c.n_embd;
     KI_TRY(kcamd::launchPositions(m->n_past, n, m->pos, m->idx, m->n_ctx, s));
-    KI_TRY(kcamd::launchGetRows(m->q6_tok, m->tok_embd, m->tokens, m->x, n, E_, s));
+    KI_TRY(kcamd::launchGetRows(m->q6_tok, m->tok_embd, m->tokens, m->x, n, E_, c.n_vocab, s));
     float* x_last = m->x + (size_t)(n - 1) * E_;
     // the products that read the same activations share one launch; o and down split K in two
     // (the two partial sums are added in the residual add that consumes them)

@@ -17,9 +17,10 @@ __device__ __forceinline__ float f16v(uint32_t h) { return (float)__builtin_bit_
 
 // y[i][:] = dequantized row tok[i] of a Q4_K / Q6_K stream (ggml dequantize_row_q4_K / q6_K with
 // the reference's operation order, llm/llm_reference.cpp:342-383). One thread per (token, 16 values).
+// A row id outside [0, rows) (the ids are device data no host check has seen) yields zeros.
 template <bool Q6>
 __global__ void get_rows_kernel(const uint8_t* __restrict__ qw, const int* __restrict__ tok, float* __restrict__ y,
-                                int n, int k) {
+                                int n, int k, int rows) {
     const int nsb = k / 256, ngroups = (nsb + kGroupSb - 1) / kGroupSb;
     const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (long long)n * (k / 16)) return;
@@ -27,6 +28,11 @@ __global__ void get_rows_kernel(const uint8_t* __restrict__ qw, const int* __res
     const int part = (int)(idx - (long long)i * (k / 16));  // 16 values
     const int s = part / 16, v0 = (part % 16) * 16;
     const int row = tok[i];
+    if (row < 0 || row >= rows) {
+        float* out = y + (size_t)i * k + part * 16;
+        for (int l = 0; l < 16; ++l) out[l] = 0.0f;
+        return;
+    }
     const int tile = row >> 4, r = row & 15, g = s >> 2, kq = s & 3;
     const uint8_t* seg = qw + ((size_t)tile * ngroups + g) * (Q6 ? kQ6kSeg : kQ4kSeg);
     const uint8_t* piece = seg + (kq * 16 + r) * 16;  // byte b of the block: slab b / 16, offset b % 16
@@ -419,11 +425,12 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(const float* __res
 
 }  // namespace
 
-int launchGetRows(bool q6k, const void* qw, const int* tok, float* y, int n, int k, hipStream_t s) {
+int launchGetRows(bool q6k, const void* qw, const int* tok, float* y, int n, int k, int rows, hipStream_t s) {
     const long long threads = (long long)n * (k / 16);
+    if (threads == 0) return 0;
     const dim3 grid((unsigned)((threads + 255) / 256));
-    if (q6k) hipLaunchKernelGGL(get_rows_kernel<true>, grid, dim3(256), 0, s, (const uint8_t*)qw, tok, y, n, k);
-    else hipLaunchKernelGGL(get_rows_kernel<false>, grid, dim3(256), 0, s, (const uint8_t*)qw, tok, y, n, k);
+    if (q6k) hipLaunchKernelGGL(get_rows_kernel<true>, grid, dim3(256), 0, s, (const uint8_t*)qw, tok, y, n, k, rows);
+    else hipLaunchKernelGGL(get_rows_kernel<false>, grid, dim3(256), 0, s, (const uint8_t*)qw, tok, y, n, k, rows);
     return fromHip(hipGetLastError(), "get_rows");
 }
 

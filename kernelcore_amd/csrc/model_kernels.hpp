@@ -12,7 +12,7 @@ struct AttnShape {
     float scale;
 };
 
-int launchGetRows(bool q6k, const void* qw, const int* tok, float* y, int n, int k, hipStream_t s);
+int launchGetRows(bool q6k, const void* qw, const int* tok, float* y, int n, int k, int rows, hipStream_t s);
 int launchAttn(const float* q, const int* k, const int* v, float* out, const int* n_ctx, const AttnShape& a,
                hipStream_t s);
 int launchArgmaxStep(const float* logits, int n, int* tokens, int* gen, int* step, int* n_past, int max_gen,

@@ -87,6 +87,11 @@ def lib():
             getattr(L, f"kco_matvec_{q}_q8_mt").argtypes = [_u8p, _i32p, _f32p, _f32p, _i, _i, _i]
         L.kco_matmul_q4k_q8k_mt.argtypes = [_u8p, _i32p, _f32p, _i, _i, _i, _i]
         L.kco_max_threads.restype = _i
+        L.kco_f32_to_f16_rne.restype = C.c_uint16
+        L.kco_f32_to_f16_rne.argtypes = [_f]
+        for q in ("q4k", "q6k"):
+            getattr(L, f"kco_quantize_row_{q}").argtypes = [_f32p, _u8p, _i]
+            getattr(L, f"kco_quantize_{q}_mt").argtypes = [_f32p, _u8p, _i, _i, _i]
         _LIB = L
     return _LIB
 
@@ -150,6 +155,15 @@ def dequant(L, qtype, w, rows, k):
         row = np.zeros(k, np.float32)
         _fn(L, f"dequant_row_{qtype}")(np.ascontiguousarray(w[r]), k, row)
         out[r] = row
+    return out
+
+
+def quantize_weights(L, qtype, x, rows, k, threads=0):
+    """rows x k floats -> ggml blocks (uint8, rows * k/256 * 144 or 210 bytes) with the restated
+    ggml reference quantizer."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    out = np.zeros(rows * (k // 256) * (144 if qtype == "q4k" else 210), np.uint8)
+    getattr(L, f"kco_quantize_{qtype}_mt")(x, out, rows, k, threads or L.kco_max_threads())
     return out
 
 

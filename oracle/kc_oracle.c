@@ -593,6 +593,253 @@ void kco_flash_attn_f16(const float* q, const uint16_t* k, const uint16_t* v, co
     free(s);
 }
 
+/* ---- f32 -> Q4_K / Q6_K weight quantizers ------------------------------------------------
+ *
+ * Third-party arithmetic: the reference has no quantizer (its tests fabricate random blocks,
+ * tests/test_llm_kernels.cpp:209-219); its weights come from GGUF files written by ggml
+ * (llama.cpp, not vendored, version unpinned; build ids c2eb060b2 / 8221f87ce in
+ * bench_chart/results.json:48,56). These restate the published steps of ggml's reference
+ * quantizers quantize_row_q4_K_ref and quantize_row_q6_K_ref with their scale searches
+ * (make_qkx2_quants for Q4_K: weighted least-squares fit of a scale and a min per sub-block of 32
+ * over 21 candidate inverse scales; make_qx_quants with rmse_type 1 for Q6_K: a scale per
+ * sub-block of 16 chosen among 19 candidates by the x^2-weighted fit). Parity with a given ggml
+ * build is unpinned; tests/test_quantizer.py pins the invariants the format and the method fix. */
+
+/* round half to even (ggml's nearest_int for |f| < 2^22) */
+static inline int nearest_even(float f) { return (int)rintf(f); }
+static inline int clampi(int v, int lo, int hi) { return v < lo ? lo : v > hi ? hi : v; }
+
+/* IEEE binary16, round to nearest even, overflow to infinity (ggml_fp32_to_fp16). */
+uint16_t kco_f32_to_f16_rne(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    const uint32_t sign = (u >> 16) & 0x8000u;
+    const uint32_t ax = u & 0x7fffffffu;
+    if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);          /* NaN */
+    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);         /* rounds to >= 65536: inf */
+    if (ax < 0x38800000u) {                                          /* below 2^-14: subnormal or 0 */
+        if (ax < 0x33000000u) return (uint16_t)sign;                   /* below 2^-25: rounds to 0 */
+        const uint32_t mant = (ax & 0x7fffffu) | 0x800000u;
+        const int shift = 126 - (int)(ax >> 23);                       /* 14..24 */
+        uint32_t h = mant >> shift;
+        const uint32_t rem = mant & ((1u << shift) - 1), half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (h & 1))) ++h;
+        return (uint16_t)(sign | h);
+    }
+    uint32_t h = ((ax >> 13) - (112u << 10));
+    const uint32_t rem = ax & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1))) ++h;
+    return (uint16_t)(sign | h);
+}
+
+/* One sub-block of 32 for Q4_K: L[i] in 0..15 and (scale, -min) so that x ~ scale * L + min,
+ * min <= 0; weights w. (make_qkx2_quants(32, 15, x, w, L, &the_min, Laux, -1, 0.1, 20, false).) */
+static float fit_q4_subblock(const float* x, const float* w, uint8_t* L, float* neg_min) {
+    float lo = x[0], hi = x[0], sw = w[0], sx = w[0] * x[0];
+    for (int i = 1; i < 32; ++i) {
+        if (x[i] < lo) lo = x[i];
+        if (x[i] > hi) hi = x[i];
+        sw += w[i];
+        sx += w[i] * x[i];
+    }
+    if (lo > 0.0f) lo = 0.0f;
+    if (hi == lo) {
+        memset(L, 0, 32);
+        *neg_min = -lo;
+        return 0.0f;
+    }
+    float iscale = 15.0f / (hi - lo);
+    float scale = 1.0f / iscale;
+    float best = 0.0f;
+    for (int i = 0; i < 32; ++i) {
+        const int l = clampi(nearest_even(iscale * (x[i] - lo)), 0, 15);
+        L[i] = (uint8_t)l;
+        const float diff = scale * (float)l + lo - x[i];
+        best += w[i] * (diff * diff);
+    }
+    uint8_t cand[32];
+    for (int step = 0; step <= 20; ++step) {
+        iscale = (-1.0f + 0.1f * (float)step + 15.0f) / (hi - lo);
+        float sl = 0.0f, sl2 = 0.0f, sxl = 0.0f;
+        for (int i = 0; i < 32; ++i) {
+            const int l = clampi(nearest_even(iscale * (x[i] - lo)), 0, 15);
+            cand[i] = (uint8_t)l;
+            sl += w[i] * (float)l;
+            sl2 += w[i] * (float)l * (float)l;
+            sxl += w[i] * (float)l * x[i];
+        }
+        const float det = sw * sl2 - sl * sl;
+        if (det > 0.0f) {
+            float s = (sw * sxl - sx * sl) / det;
+            float m = (sl2 * sx - sl * sxl) / det;
+            if (m > 0.0f) {
+                m = 0.0f;
+                s = sxl / sl2;
+            }
+            float err = 0.0f;
+            for (int i = 0; i < 32; ++i) {
+                const float diff = s * (float)cand[i] + m - x[i];
+                err += w[i] * (diff * diff);
+            }
+            if (err < best) {
+                memcpy(L, cand, 32);
+                best = err;
+                scale = s;
+                lo = m;
+            }
+        }
+    }
+    *neg_min = -lo;
+    return scale;
+}
+
+void kco_quantize_row_q4k(const float* x, uint8_t* out, int k) {
+    for (int sb = 0; sb < k / 256; ++sb) {
+        const float* xs = x + (size_t)sb * 256;
+        uint8_t* b = out + (size_t)sb * 144;
+        uint8_t L[256];
+        float scales[8], mins[8], w[32];
+        float max_scale = 0.0f, max_min = 0.0f;
+        for (int j = 0; j < 8; ++j) {
+            float sum_x2 = 0.0f;
+            for (int l = 0; l < 32; ++l) sum_x2 += xs[32 * j + l] * xs[32 * j + l];
+            const float av = sqrtf(sum_x2 / 32.0f);
+            for (int l = 0; l < 32; ++l) w[l] = av + fabsf(xs[32 * j + l]);
+            scales[j] = fit_q4_subblock(xs + 32 * j, w, L + 32 * j, &mins[j]);
+            if (scales[j] > max_scale) max_scale = scales[j];
+            if (mins[j] > max_min) max_min = mins[j];
+        }
+        const float inv_scale = max_scale > 0.0f ? 63.0f / max_scale : 0.0f;
+        const float inv_min = max_min > 0.0f ? 63.0f / max_min : 0.0f;
+        memset(b, 0, 144);
+        uint8_t* sc = b + 4;
+        for (int j = 0; j < 8; ++j) {
+            uint8_t ls = (uint8_t)nearest_even(inv_scale * scales[j]);
+            uint8_t lm = (uint8_t)nearest_even(inv_min * mins[j]);
+            if (ls > 63) ls = 63;
+            if (lm > 63) lm = 63;
+            if (j < 4) {
+                sc[j] = ls;
+                sc[j + 4] = lm;
+            } else {
+                sc[j + 4] = (uint8_t)((ls & 0xF) | ((lm & 0xF) << 4));
+                sc[j - 4] |= (uint8_t)((ls >> 4) << 6);
+                sc[j] |= (uint8_t)((lm >> 4) << 6);
+            }
+        }
+        const uint16_t d16 = kco_f32_to_f16_rne(max_scale / 63.0f), m16 = kco_f32_to_f16_rne(max_min / 63.0f);
+        b[0] = (uint8_t)d16, b[1] = (uint8_t)(d16 >> 8), b[2] = (uint8_t)m16, b[3] = (uint8_t)(m16 >> 8);
+        for (int j = 0; j < 8; ++j) {
+            int s6, m6;
+            scale_min_k4(j, sc, &s6, &m6);
+            const float d = kco_f16_to_f32(d16) * (float)s6;
+            if (d == 0.0f) continue;  /* the sub-block keeps the fit's L */
+            const float dm = kco_f16_to_f32(m16) * (float)m6;
+            for (int i = 0; i < 32; ++i) L[32 * j + i] = (uint8_t)clampi(nearest_even((xs[32 * j + i] + dm) / d), 0, 15);
+        }
+        uint8_t* q = b + 16;
+        for (int j = 0; j < 256; j += 64, q += 32)
+            for (int l = 0; l < 32; ++l) q[l] = (uint8_t)(L[j + l] | (L[j + l + 32] << 4));
+    }
+}
+
+/* One sub-block of 16 for Q6_K: L[i] = l + 32 with l in -32..31 and a scale so that x ~ scale * l,
+ * x^2-weighted. (make_qx_quants(16, 32, x, L, 1, NULL).) */
+static float fit_q6_subblock(const float* x, int8_t* L) {
+    float mx = 0.0f, amax = 0.0f;
+    for (int i = 0; i < 16; ++i) {
+        const float ax = fabsf(x[i]);
+        if (ax > amax) {
+            amax = ax;
+            mx = x[i];
+        }
+    }
+    if (amax < 1e-15f) {
+        memset(L, 0, 16);
+        return 0.0f;
+    }
+    float iscale = -32.0f / mx;
+    float sumlx = 0.0f, suml2 = 0.0f;
+    for (int i = 0; i < 16; ++i) {
+        const int l = clampi(nearest_even(iscale * x[i]), -32, 31);
+        L[i] = (int8_t)(l + 32);
+        const float w = x[i] * x[i];
+        sumlx += w * x[i] * (float)l;
+        suml2 += w * (float)l * (float)l;
+    }
+    float scale = suml2 != 0.0f ? sumlx / suml2 : 0.0f;
+    float best = scale * sumlx;
+    for (int step = -9; step <= 9; ++step) {
+        if (step == 0) continue;
+        iscale = -(32.0f + 0.1f * (float)step) / mx;
+        sumlx = suml2 = 0.0f;
+        for (int i = 0; i < 16; ++i) {
+            const int l = clampi(nearest_even(iscale * x[i]), -32, 31);
+            const float w = x[i] * x[i];
+            sumlx += w * x[i] * (float)l;
+            suml2 += w * (float)l * (float)l;
+        }
+        if (suml2 > 0.0f && sumlx * sumlx > best * suml2) {
+            for (int i = 0; i < 16; ++i) L[i] = (int8_t)(32 + clampi(nearest_even(iscale * x[i]), -32, 31));
+            scale = sumlx / suml2;
+            best = scale * sumlx;
+        }
+    }
+    return scale;
+}
+
+void kco_quantize_row_q6k(const float* x, uint8_t* out, int k) {
+    for (int sb = 0; sb < k / 256; ++sb) {
+        const float* xs = x + (size_t)sb * 256;
+        uint8_t* b = out + (size_t)sb * 210;
+        int8_t L[256];
+        float scales[16];
+        float max_scale = 0.0f, max_abs = 0.0f;
+        for (int g = 0; g < 16; ++g) {
+            scales[g] = fit_q6_subblock(xs + 16 * g, L + 16 * g);
+            const float a = fabsf(scales[g]);
+            if (a > max_abs) {
+                max_abs = a;
+                max_scale = scales[g];
+            }
+        }
+        memset(b, 0, 210);
+        if (max_abs < 1e-15f) continue;  /* all-zero block, d = 0 */
+        const float iscale = -128.0f / max_scale;
+        const uint16_t d16 = kco_f32_to_f16_rne(1.0f / iscale);
+        b[208] = (uint8_t)d16, b[209] = (uint8_t)(d16 >> 8);
+        int8_t* sc = (int8_t*)(b + 192);
+        for (int g = 0; g < 16; ++g) {
+            const int v = nearest_even(iscale * scales[g]);
+            sc[g] = (int8_t)(v < 127 ? v : 127);
+        }
+        for (int g = 0; g < 16; ++g) {
+            const float d = kco_f16_to_f32(d16) * (float)sc[g];
+            if (d == 0.0f) continue;
+            for (int i = 0; i < 16; ++i) L[16 * g + i] = (int8_t)(clampi(nearest_even(xs[16 * g + i] / d), -32, 31) + 32);
+        }
+        uint8_t* ql = b;
+        uint8_t* qh = b + 128;
+        for (int j = 0; j < 256; j += 128, ql += 64, qh += 32)
+            for (int l = 0; l < 32; ++l) {
+                const int q1 = L[j + l], q2 = L[j + l + 32], q3 = L[j + l + 64], q4 = L[j + l + 96];
+                ql[l] = (uint8_t)((q1 & 0xF) | ((q3 & 0xF) << 4));
+                ql[l + 32] = (uint8_t)((q2 & 0xF) | ((q4 & 0xF) << 4));
+                qh[l] = (uint8_t)((q1 >> 4) | ((q2 >> 4) << 2) | ((q3 >> 4) << 4) | ((q4 >> 4) << 6));
+            }
+    }
+}
+
+/* rows x k floats -> rows of blocks, rows over OpenMP threads */
+void kco_quantize_q4k_mt(const float* x, uint8_t* out, int rows, int k, int nthreads) {
+#pragma omp parallel for num_threads(nthreads) schedule(static)
+    for (int r = 0; r < rows; ++r) kco_quantize_row_q4k(x + (size_t)r * k, out + (size_t)r * (k / 256) * 144, k);
+}
+void kco_quantize_q6k_mt(const float* x, uint8_t* out, int rows, int k, int nthreads) {
+#pragma omp parallel for num_threads(nthreads) schedule(static)
+    for (int r = 0; r < rows; ++r) kco_quantize_row_q6k(x + (size_t)r * k, out + (size_t)r * (k / 256) * 210, k);
+}
+
 /* ---- CPU baseline (rows over OpenMP threads; per-row arithmetic as above) ---------------- */
 
 int kco_max_threads(void) {

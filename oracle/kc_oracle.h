@@ -34,6 +34,15 @@ float kco_f16_to_f32(uint16_t h);
  * even, |x| >= 65520 -> 0x7bff with sign, -0 -> +0. */
 uint16_t kco_f32_to_f16(float x);
 
+/* IEEE binary16 round to nearest even, overflow to infinity (ggml_fp32_to_fp16). */
+uint16_t kco_f32_to_f16_rne(float x);
+/* ggml's reference weight quantizers f32 -> block_q4_K / block_q6_K (quantize_row_q4_K_ref /
+ * quantize_row_q6_K_ref, third-party, restated; see kc_oracle.c). k % 256 == 0. */
+void kco_quantize_row_q4k(const float* x, uint8_t* blocks, int k);
+void kco_quantize_row_q6k(const float* x, uint8_t* blocks, int k);
+void kco_quantize_q4k_mt(const float* x, uint8_t* blocks, int rows, int k, int nthreads);
+void kco_quantize_q6k_mt(const float* x, uint8_t* blocks, int rows, int k, int nthreads);
+
 /* ggml dequantize_row_q4_K / q6_K (llm/llm_reference.cpp:342-383). k % 256 == 0. */
 void kco_dequant_row_q4k(const uint8_t* blocks, int k, float* out);
 void kco_dequant_row_q6k(const uint8_t* blocks, int k, float* out);

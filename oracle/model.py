@@ -113,6 +113,10 @@ class OracleModel:
             self.L.kco_set_rows_f16(np.ascontiguousarray(src, np.float32).reshape(-1), idx, cache, kvd // 2, n, kvd,
                                     kvd // 2, c["max_ctx"])
 
+    def residual(self, x, y):
+        """The residual stream's ADD (tests plant mistakes here by overriding it)."""
+        return x + y
+
     # ---- one row, per-32 path ---------------------------------------------------------------------
     def _norm32(self, x, wt):
         E = x.size
@@ -168,7 +172,7 @@ class OracleModel:
             x = x.reshape(-1).copy()
             for l in range(c["n_layer"]):
                 if l > 0:
-                    x = x + down
+                    x = self.residual(x, down)
                 slot, xn = self._norm32(x, self.w(3, l))
                 q = self.matvec(4, l, slot, Q, E, xn)
                 k = self.matvec(5, l, slot, KV, E, xn)
@@ -179,15 +183,15 @@ class OracleModel:
                 xq, xd = quantize_q8x4(self.L, att)
                 aslot = np.concatenate([xq, xd.view(np.int32), np.zeros(Q // 32, np.int32)])
                 o = self.matvec(7, l, aslot, E, Q, att)
-                x = x + o
+                x = self.residual(x, o)
                 down = self._ffn_one(l, x)
-            x = x + down
+            x = self.residual(x, down)
             logits = self._head(x)
         else:
             nsb, nb = E // 256, E // 32
             for l in range(c["n_layer"]):
                 if l > 0:
-                    x = x + down
+                    x = self.residual(x, down)
                 sq = np.zeros(n * nb * 11, np.int32)
                 self.L.kco_sumsq_part(np.ascontiguousarray(x.reshape(-1)), sq, E, n)
                 slots = np.zeros(n * nsb * 85, np.int32)
@@ -203,7 +207,7 @@ class OracleModel:
                 self.L.kco_quantize_cols_k(np.ascontiguousarray(att.reshape(-1)), aslots, Q, n)
                 o = self.matmul(7, l, aslots, E, Q, n, att)
                 if l + 1 < c["n_layer"]:
-                    x = x + o
+                    x = self.residual(x, o)
                     sq = np.zeros(n * nb * 11, np.int32)
                     self.L.kco_sumsq_part(np.ascontiguousarray(x.reshape(-1)), sq, E, n)
                     self.L.kco_norm_mul_q8k(np.ascontiguousarray(x.reshape(-1)), self.w(8, l), y, slots, sq, E, n, eps)
@@ -215,9 +219,9 @@ class OracleModel:
                                             fslots, c["n_ff"], n)
                     down = self.matmul(11, l, fslots, E, c["n_ff"], n, s)
                 else:
-                    x = (x[n - 1] + o[n - 1]).astype(np.float32)
+                    x = self.residual(x[n - 1], o[n - 1]).astype(np.float32)
                     down = self._ffn_one(l, x)
-            x = x + down
+            x = self.residual(x, down)
             logits = self._head(x)
         self.pos += n
         return logits

@@ -36,3 +36,31 @@ def random_weights(cfg, seed, types=None):
             b[:, 2:4] = half()
         out[(tid, layer)] = b.reshape(-1)
     return out
+
+
+def quantized_weights(cfg, seed, types=None, std=0.02):
+    """The configs' workload: every matrix drawn from N(0, std) and quantized to its ggml type
+    with the restated ggml reference quantizer (oracle.quantize_weights); norm weights
+    1 + 0.1 * U(-1, 1); F16 overrides keep the N(0, std) values as halves."""
+    import oracle
+
+    L = oracle.lib()
+    rng = np.random.default_rng(seed)
+    out = {}
+    table = shapes(cfg)
+    types = types or {}
+    ids_global = [0, 1, 2]
+    ids_layer = [3, 4, 5, 6, 7, 8, 9, 10, 11] + ([12, 13] if cfg["qk_norm"] else [])
+    keys = [(t, -1) for t in ids_global] + [(t, l) for l in range(cfg["n_layer"]) for t in ids_layer]
+    for tid, layer in keys:
+        qt, rows, k = table[tid]
+        qt = types.get((tid, layer), qt)
+        if qt == F32:
+            out[(tid, layer)] = (1.0 + 0.1 * rng.uniform(-1.0, 1.0, k)).astype(np.float32)
+            continue
+        x = (rng.standard_normal(rows * k, dtype=np.float32) * std).astype(np.float32)
+        if qt == F16:
+            out[(tid, layer)] = x.astype(np.float16).view(np.uint8)
+            continue
+        out[(tid, layer)] = oracle.quantize_weights(L, "q6k" if qt == Q6K else "q4k", x, rows, k)
+    return out

@@ -5,6 +5,7 @@ matvec, bit-exact, for several ncols and row counts; a dims mismatch is InvalidV
 (per-256 slots equal quantizeQ8K, matmuls equal matvecQ*KQ8K per column, error vs the exact product
 below 2% of the largest output and at most 4x the per-32 error). Bar: 1e-3 max relative error;
 the column-tiled kernel is also bit-exact and that is asserted where it runs."""
+import ctypes as C
 import sys
 
 import numpy as np
@@ -171,3 +172,49 @@ def test_mfma_matmul_config3_shapes():
         want = np.zeros(rows * ncols, np.float32)
         O.kco_matmul_q4k_q8k_mt(w, slots, want, rows, k, ncols, O.kco_max_threads())
         assert kq.rel_diff(y, want.reshape(ncols, rows)) < TOL
+
+
+def test_captured_matmul_keeps_its_scratch_after_an_eager_growth():
+    """The MFMA matmul stages fp16 activations in the runtime's per-stream scratch. A graph captured
+    with a 64-column matmul records that buffer; a later eager 512-column matmul on the same stream
+    grows the scratch. The graph must still read valid memory on every replay (the buffer a capture
+    may hold is retired, not freed), so each replay equals the oracle and the eager result."""
+    rows, k = 256, 1024
+    w = kq.random_blocks("q4k", rows, k, seed=77)
+    stream = kc.upload_weights("q4k", w, rows, k)
+    s = C.c_void_p()
+    kc.call("kcStreamCreate", C.byref(s))
+    bufs = [stream]
+    try:
+        x64 = kq.randn(64 * k, 78)
+        bq64 = gpu_slots(x64, k, 64, True)
+        by64 = kc.Buffer(rows * 64 * 4)
+        bufs += [bq64, by64]
+        want64 = np.zeros(rows * 64, np.float32)
+        O.kco_matmul_q4k_q8k(w, oracle_slots(x64, k, 64, True), want64, rows, k, 64)
+        note("capture: 64-column matmul")
+        kc.call("kcStreamBeginCapture", s)
+        kc.launch("matmul_q4k_q8kx8", kc.MatmulKQ8Args(stream.ptr, bq64.ptr, by64.ptr, None, rows, k, 64, 8), s)
+        g = C.c_void_p()
+        kc.call("kcStreamEndCapture", s, C.byref(g))
+        x512 = kq.randn(512 * k, 79)
+        bq512 = gpu_slots(x512, k, 512, True)
+        by512 = kc.Buffer(rows * 512 * 4)
+        bufs += [bq512, by512]
+        for rep in range(3):
+            kc.call("kcMemset", C.c_void_p(by64.ptr), 0, rows * 64 * 4)
+            note(f"eager 512-column matmul, then replay {rep}")
+            kc.launch("matmul_q4k_q8kx8", kc.MatmulKQ8Args(stream.ptr, bq512.ptr, by512.ptr, None, rows, k, 512, 8), s)
+            kc.call("kcGraphLaunch", g, s)
+            kc.call("kcStreamSynchronize", s)
+            got = by64.download(np.float32)
+            assert kq.rel_diff(got, want64) < TOL
+        want512 = np.zeros(rows * 512, np.float32)
+        O.kco_matmul_q4k_q8k(w, oracle_slots(x512, k, 512, True), want512, rows, k, 512)
+        assert kq.rel_diff(by512.download(np.float32), want512) < TOL
+        kc.call("kcGraphDestroy", g)
+    finally:
+        kc.call("kcStreamSynchronize", s)
+        kc.call("kcStreamDestroy", s)
+        for b in bufs:
+            b.free()

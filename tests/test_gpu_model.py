@@ -285,3 +285,28 @@ def test_model_f16_rejected_for_global_matrices():
     with pytest.raises(kc.KcError):
         m.set_tensor("output", -1, np.zeros(rows * k * 2, np.uint8), "f16")
     m.close()
+
+
+def test_model_llama2_ffn_width_decodes_fused():
+    """n_ff 11008 (Llama-2-7B): 43 super-blocks, 11 groups of 4 -- a prime above the wavefront cap of
+    the down-projection matvec. The plan keeps the fused single-token path (8 wavefronts, uneven
+    shares) and the decode matches the oracle."""
+    cfg = dict(n_layer=1, n_embd=512, n_head=8, n_head_kv=8, head_dim=64, n_ff=11008, n_vocab=1024, norm_eps=1e-5,
+               rope_theta=10000.0, rope_neox=0, qk_norm=0, max_ctx=64, max_batch=16)
+    assert kc.plan_decode(**cfg) == 1
+    note("model n_ff 11008: building")
+    m, o = build(cfg, 31)
+    prompt = np.random.default_rng(8).integers(0, cfg["n_vocab"], 9).astype(np.int32)
+    lg, lo = m.forward(prompt), o.forward(prompt)
+    assert rel_l2(lg, lo) < 1e-2, rel_l2(lg, lo)
+    for _ in range(3):
+        t = int(np.argmax(lo))
+        lg, lo = m.forward([t]), o.forward([t])
+        assert rel_l2(lg, lo) < 1e-2, rel_l2(lg, lo)
+    gen = m.generate(4)
+    want, logits = [], lo
+    for _ in range(4):
+        want.append(int(np.argmax(logits)))
+        logits = o.forward([want[-1]])
+    assert list(gen) == want
+    m.close()
