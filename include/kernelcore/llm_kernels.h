@@ -285,6 +285,27 @@ typedef struct kcGetRowsKquantArgs {
     int k;
     int n;
 } kcGetRowsKquantArgs;
+/* quantize_kquant: rows x k f32 values (row-major, k % 256 == 0) -> rows * k/256 ggml blocks
+ * (block_q4_K, 144 bytes, or block_q6_K, 210 bytes), as ggml's reference quantizers
+ * quantize_row_q4_K_ref / quantize_row_q6_K_ref compute them (third-party: the reference itself
+ * has no quantizer; its weights come from GGUF files written by ggml). For making the synthetic
+ * K-quant weights of the BASELINE configurations on the device. */
+typedef struct kcQuantizeKquantArgs {
+    const float* x;
+    void* blocks;
+    int qtype; /* KC_QTYPE_Q4_K or KC_QTYPE_Q6_K */
+    int rows;
+    int k;
+} kcQuantizeKquantArgs;
+/* fill_normal_f32: y[i] = mean + stdev * N(0, 1) for i < n, a deterministic function of (seed, i)
+ * (splitmix64 counter stream, Box-Muller): synthetic weights and activations of a given seed. */
+typedef struct kcFillNormalArgs {
+    float* y;
+    long long n;
+    unsigned long long seed;
+    float mean;
+    float stdev;
+} kcFillNormalArgs;
 /* Bytes of the weight stream of a rows x k matrix (buft_get_alloc_size, ggml-kernelcore.cpp:116-118). */
 KC_API kcError_t kcKquantStreamBytes(int qtype, int rows, int k, size_t* bytes) KC_NOEXCEPT;
 
@@ -314,6 +335,8 @@ typedef ::kcFaExpArgs FaExpArgs;
 typedef ::kcFaValuesArgs FaValuesArgs;
 typedef ::kcKquantRepackArgs KquantRepackArgs;
 typedef ::kcGetRowsKquantArgs GetRowsKquantArgs;
+typedef ::kcQuantizeKquantArgs QuantizeKquantArgs;
+typedef ::kcFillNormalArgs FillNormalArgs;
 typedef ::kcFlashAttnArgs FlashAttnArgs;
 inline int scratchInts(int nb) { return nb * 11; }
 inline float* scratchScales(int* q, int nb) { return reinterpret_cast<float*>(q + nb * 8); }

@@ -82,6 +82,9 @@ FlashAttnArgs = _struct("FlashAttnArgs", [("q", _p), ("k", _p), ("v", _p), ("mas
                                           ("d", FaDims), ("scale", _f)])
 GetRowsKquantArgs = _struct("GetRowsKquantArgs", [("qw", _p), ("ids", _p), ("y", _p), ("qtype", _i), ("rows", _i),
                                                   ("k", _i), ("n", _i)])
+QuantizeKquantArgs = _struct("QuantizeKquantArgs", [("x", _p), ("blocks", _p), ("qtype", _i), ("rows", _i), ("k", _i)])
+FillNormalArgs = _struct("FillNormalArgs", [("y", _p), ("n", C.c_longlong), ("seed", C.c_ulonglong), ("mean", _f),
+                                            ("stdev", _f)])
 KquantRepackArgs = _struct("KquantRepackArgs", [("src", _p), ("dst", _p), ("qtype", _i), ("rows", _i), ("k", _i)])
 DeviceProperties = _struct("DeviceProperties", [("name", C.c_char * 128), ("worker_count", C.c_uint),
                                                 ("performance_workers", C.c_uint), ("total_memory", C.c_size_t),

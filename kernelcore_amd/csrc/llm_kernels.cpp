@@ -14,6 +14,7 @@
 #include "internal.hpp"
 #include "kquant.hpp"
 #include "launch.hpp"
+#include "kquantize.hpp"
 #include "model_kernels.hpp"
 
 namespace {
@@ -412,6 +413,32 @@ int getRowsLaunch(const void* p, void* s) {
     return kcamd::launchGetRows(a.qtype == KC_QTYPE_Q6_K, a.qw, a.ids, a.y, a.n, a.k, a.rows, hs(s));
 }
 
+// ---- quantize_kquant / fill_normal_f32 (synthetic weights; no reference kernel)
+
+int quantKquantValidate(const void* p, const kcLaunchContext*) {
+    const auto& a = *static_cast<const kcQuantizeKquantArgs*>(p);
+    if (a.qtype != KC_QTYPE_Q4_K && a.qtype != KC_QTYPE_Q6_K) return invalid("qtype must be Q4_K (12) or Q6_K (14)");
+    if (a.rows < 0 || a.k <= 0 || a.k % 256 != 0 || !fitsIndex(a.rows, a.k / 256))
+        return invalid("rows must be non-negative and k a positive multiple of 256");
+    const size_t n = size_t(a.rows) * size_t(a.k);
+    KC_TRY(checkRange(a.x, n * sizeof(float), "x"));
+    return checkRange(a.blocks, n / 256 * (a.qtype == KC_QTYPE_Q6_K ? kcamd::kQ6kBlock : kcamd::kQ4kBlock), "blocks");
+}
+int quantKquantLaunch(const void* p, void* s) {
+    const auto& a = *static_cast<const kcQuantizeKquantArgs*>(p);
+    return kcamd::launchQuantizeKquant(a.qtype == KC_QTYPE_Q6_K, a.x, a.blocks, (long long)a.rows * (a.k / 256), hs(s));
+}
+
+int fillNormalValidate(const void* p, const kcLaunchContext*) {
+    const auto& a = *static_cast<const kcFillNormalArgs*>(p);
+    if (a.n < 0) return invalid("n < 0");
+    return checkRange(a.y, size_t(a.n) * sizeof(float), "y");
+}
+int fillNormalLaunch(const void* p, void* s) {
+    const auto& a = *static_cast<const kcFillNormalArgs*>(p);
+    return kcamd::launchFillNormal(a.y, a.n, a.seed, a.mean, a.stdev, hs(s));
+}
+
 const kcKernelEntry kTable[] = {
     {"vector_add", vectorAddValidate, vectorAddLaunch, 1},
     {"quantize_q8x4", quantValidate, quantLaunch, 1},
@@ -447,6 +474,8 @@ const kcKernelEntry kTable[] = {
     {"repack_kquant", repackValidate<false>, repackLaunch<false>, 0},
     {"unpack_kquant", repackValidate<true>, repackLaunch<true>, 0},
     {"get_rows_kquant", getRowsValidate, getRowsLaunch, 0},
+    {"quantize_kquant", quantKquantValidate, quantKquantLaunch, 0},
+    {"fill_normal_f32", fillNormalValidate, fillNormalLaunch, 0},
 };
 
 }  // namespace
