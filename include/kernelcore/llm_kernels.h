@@ -285,6 +285,18 @@ typedef struct kcGetRowsKquantArgs {
     int k;
     int n;
 } kcGetRowsKquantArgs;
+/* kcLaunchMatmulNoAlloc: the matmul names matmul_{q4k,q6k}_q8{,k}x{4,8} with kcMatmulKQ8Args, the same
+ * validation, kernels and results as kcLaunchKernel, but allocating nothing: no hipMalloc, hipFree or
+ * allocating library routine on any call. It has no counterpart in the reference; it is for callers
+ * that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Where kcLaunchKernel stages a batch's fp16 activations (per-256 slots, 64 columns and
+ * more) in the runtime's per-stream scratch, this stages them in a fixed 16 MiB device array that
+ * each GPU holds until the process ends: ncols * k * 2 + ncols * k / 8 + (k / 256) * 4 * ncols
+ * rounded up to 128 must be at most 16 MiB (e.g. 512 columns of 12288 values), else InvalidValue
+ * with the sizes in the detail text. Every call on a GPU shares that array, so calls that overlap
+ * on one GPU (concurrent streams, a graph replayed while another call runs) race; inside a
+ * concurrent group it returns UnsupportedOperation. */
+KC_API kcError_t kcLaunchMatmulNoAlloc(const char* name, const kcMatmulKQ8Args* args, kcStream_t stream) KC_NOEXCEPT;
 /* quantize_kquant: rows x k f32 values (row-major, k % 256 == 0) -> rows * k/256 ggml blocks
  * (block_q4_K, 144 bytes, or block_q6_K, 210 bytes), as ggml's reference quantizers
  * quantize_row_q4_K_ref / quantize_row_q6_K_ref compute them (third-party: the reference itself

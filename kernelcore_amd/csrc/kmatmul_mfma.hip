@@ -986,7 +986,59 @@ int runMfma(const kcMatmulKQ8Args& a, hipStream_t s) {
     return fromHip(hipGetLastError(), Q6 ? "matmul_q6k_q8k (MFMA)" : "matmul_q4k_q8k (MFMA)");
 }
 
+// ---- the fixed scratch of kcLaunchMatmulNoAlloc -----------------------------------------------
+//
+// The fp16 activations of one MFMA launch staged in a file-scope device array instead of the
+// runtime's per-stream scratch, for callers that cannot allocate. Each GPU holds its own copy of
+// the array until the process ends; its device address is looked up once per device when the
+// runtime starts (hipGetSymbolAddress; the array's name is only a host-side stand-in and must never
+// be passed to a kernel). Every call on a GPU shares it: calls that overlap on one GPU race. The
+// conversion kernel rewrites every byte the matmul reads on each call, so nothing needs clearing.
+constexpr size_t kFixedScratchBytes = size_t(16) << 20;
+constexpr int kMaxDevices = 16;
+static __device__ __align__(256) unsigned char scratch[kFixedScratchBytes];
+void* g_fixed_scratch[kMaxDevices] = {};
+
 }  // namespace
+
+int fixedScratchInit(int device) {
+    if (device < 0 || device >= kMaxDevices) return fromHip(hipErrorInvalidDevice, "fixed scratch: device index");
+    void* p = nullptr;
+    const hipError_t st = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (st != hipSuccess || !p) {
+        g_fixed_scratch[device] = nullptr;
+        return fromHip(st != hipSuccess ? st : hipErrorInvalidSymbol, "fixed scratch: hipGetSymbolAddress");
+    }
+    g_fixed_scratch[device] = p;
+    return 0;
+}
+
+size_t fixedScratchBytes() { return kFixedScratchBytes; }
+
+int launchMatmulKqNoAlloc(bool q6k, bool per256, const kcMatmulKQ8Args& a, hipStream_t s) {
+    const int path = option("matmul_path");
+    const bool mfma = per256 && (path >= 2 || (path == 0 && a.ncols >= 64));
+    if (!mfma) return launchMatmulCols(q6k, per256, a, s);  // the column kernel stages nothing
+    if (path == 3) return q6k ? runMfma<true>(a, s) : runMfma<false>(a, s);
+    if (path == 4) return q6k ? runMfma8<true, 2>(a, s) : runMfma8<false, 2>(a, s);
+    if (path == 5) return q6k ? runMfma8<true, 1>(a, s) : runMfma8<false, 1>(a, s);
+    const size_t need = actBytes(a.ncols, a.k);
+    if (need > kFixedScratchBytes) {
+        setDetail("matmul (no-alloc): %d columns of %d values need %zu bytes of staging, above the fixed %zu "
+                  "(ncols * k * 2 + ncols * k / 8 + k / 64 * ncols rounded up to 128)",
+                  a.ncols, a.k, need, kFixedScratchBytes);
+        return KC_ERROR_INVALID_VALUE;
+    }
+    int dev = 0;
+    if (int e = fromHip(hipGetDevice(&dev), "hipGetDevice")) return e;
+    void* p = dev >= 0 && dev < kMaxDevices ? g_fixed_scratch[dev] : nullptr;
+    if (!p) {
+        setDetail("matmul (no-alloc): the fixed scratch of device %d was not set up (kcInit)", dev);
+        return KC_ERROR_NOT_INITIALIZED;
+    }
+    const MmPart part{a.qw, {a.y, nullptr}, a.rows, q6k ? 1 : 0};
+    return runMfmaH(&part, 1, a.xq, a.k, a.ncols, 1, p, s);
+}
 
 bool mfmaHUsable(int ncols, int k) { return option("matmul_path") == 0 && (size_t)ncols * k * 2 < (1ull << 32); }
 

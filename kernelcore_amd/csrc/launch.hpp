@@ -43,6 +43,12 @@ int launchMatmulCols(bool q6k, bool per256, const kcMatmulKQ8Args& a, hipStream_
 int launchMatmulMfma(bool q6k, const kcMatmulKQ8Args& a, hipStream_t s);
 // The matmul names: column tiles for small batches and per-32 slots, MFMA for large per-256 batches.
 int launchMatmulKq(bool q6k, bool per256, const kcMatmulKQ8Args& a, hipStream_t s);
+// The same kernels with the MFMA activations staged in the fixed device array (kcLaunchMatmulNoAlloc):
+// no allocation; InvalidValue when the staging exceeds fixedScratchBytes().
+int launchMatmulKqNoAlloc(bool q6k, bool per256, const kcMatmulKQ8Args& a, hipStream_t s);
+// Looks up this device's address of the fixed array (once per device, with the device current).
+int fixedScratchInit(int device);
+size_t fixedScratchBytes();
 // One weight matrix of a grouped matmul: y[z] receives the partial sums of K range z.
 struct MmPart {
     const void* qw;  // device stream of kcamd::streamBytes layout
