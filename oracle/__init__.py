@@ -87,6 +87,13 @@ def lib():
             getattr(L, f"kco_matvec_{q}_q8_mt").argtypes = [_u8p, _i32p, _f32p, _f32p, _i, _i, _i]
         L.kco_matmul_q4k_q8k_mt.argtypes = [_u8p, _i32p, _f32p, _i, _i, _i, _i]
         L.kco_max_threads.restype = _i
+        L.kco_simd_level.restype = _i
+        L.kco_simd_cap.restype = _i
+        L.kco_simd_cap.argtypes = [_i]
+        for q in ("q4k", "q6k"):
+            getattr(L, f"kco_matmul_{q}_q8k_simd").argtypes = [_u8p, _i32p, _f32p, _i, _i, _i, _i]
+            getattr(L, f"kco_matvec_{q}_q8_simd").argtypes = [_u8p, _i32p, _f32p, _f32p, _i, _i, _i]
+        L.kco_flash_attn_f16_mt.argtypes = [_f32p, _u16p, _u16p, _u16p, _f32p, C.POINTER(FaDims), _f, _i]
         L.kco_f32_to_f16_rne.restype = C.c_uint16
         L.kco_f32_to_f16_rne.argtypes = [_f]
         for q in ("q4k", "q6k"):

@@ -119,6 +119,19 @@ void kco_matvec_q6k_q8_mt(const uint8_t* w, const int32_t* xq, const float* xd, 
 void kco_matmul_q4k_q8k_mt(const uint8_t* w, const int32_t* q, float* y, int rows, int k, int ncols, int nthreads);
 int  kco_max_threads(void);
 
+/* ---- vectorised, threaded forms (kc_oracle_simd.c), bit-identical to the scalar ones above -- */
+/* 2: AVX-512 VNNI, 1: AVX2, 0: scalar integer dots (the environment's KCO_SIMD caps it). */
+int kco_simd_level(void);
+int kco_simd_cap(int cap); /* caps the level for this process; returns the level in use */
+void kco_matmul_q4k_q8k_simd(const uint8_t* w, const int32_t* q, float* y, int rows, int k, int ncols, int nthreads);
+void kco_matmul_q6k_q8k_simd(const uint8_t* w, const int32_t* q, float* y, int rows, int k, int ncols, int nthreads);
+void kco_matvec_q4k_q8_simd(const uint8_t* w, const int32_t* xq, const float* xd, float* y, int rows, int k,
+                            int nthreads);
+void kco_matvec_q6k_q8_simd(const uint8_t* w, const int32_t* xq, const float* xd, float* y, int rows, int k,
+                            int nthreads);
+void kco_flash_attn_f16_mt(const float* q, const uint16_t* k, const uint16_t* v, const uint16_t* mask, float* out,
+                           const kco_fa_dims* d, float scale, int nthreads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -35,8 +35,9 @@ class OracleModel:
         overrides a matrix's default type (a GGUF Q4_K_M file mixes them); F16 (per-layer matrices,
         row-major halves) multiplies the f32 activations instead of the quantized ones, as the
         reference's MUL_MAT dispatch does (ggml-kernelcore.cpp:559-566). threads > 0 runs the
-        single-row matvecs with the OpenMP variants (the same per-row arithmetic, rows split over
-        threads) -- the bench's CPU baseline."""
+        matvecs, matmuls and attention with the vectorised, threaded forms (kc_oracle_simd.c:
+        bit-identical results, rows or (query, head) pairs split over threads) -- the full-size
+        GPU tests and the bench's CPU baseline."""
         self.cfg = cfg
         self.t = tensors
         self.types = dict(types or {})
@@ -63,7 +64,7 @@ class OracleModel:
         xq = np.ascontiguousarray(slot[:nb * 8])
         xd = np.ascontiguousarray(slot[nb * 8:nb * 10].view(np.float32))
         if self.threads > 0:
-            fn = self.L.kco_matvec_q6k_q8_mt if qt == Q6K else self.L.kco_matvec_q4k_q8_mt
+            fn = self.L.kco_matvec_q6k_q8_simd if qt == Q6K else self.L.kco_matvec_q4k_q8_simd
             fn(self.w(tid, layer), xq, xd, y, rows, k, self.threads)
         else:
             fn = self.L.kco_matvec_q6k_q8 if qt == Q6K else self.L.kco_matvec_q4k_q8
@@ -75,8 +76,12 @@ class OracleModel:
         if qt == F16:
             return matmul_f16(self.L, self.w(tid, layer).view(np.uint16), xf, rows, k, n)
         y = np.zeros(rows * n, np.float32)
-        fn = self.L.kco_matmul_q6k_q8k if qt == Q6K else self.L.kco_matmul_q4k_q8k
-        fn(self.w(tid, layer), slots, y, rows, k, n)
+        if self.threads > 0:
+            fn = self.L.kco_matmul_q6k_q8k_simd if qt == Q6K else self.L.kco_matmul_q4k_q8k_simd
+            fn(self.w(tid, layer), slots, y, rows, k, n, self.threads)
+        else:
+            fn = self.L.kco_matmul_q6k_q8k if qt == Q6K else self.L.kco_matmul_q4k_q8k
+            fn(self.w(tid, layer), slots, y, rows, k, n)
         return y.reshape(n, rows)
 
     def rope(self, x, n_head, pos):
@@ -100,8 +105,12 @@ class OracleModel:
         d = FaDims(H=H, T=T, D=D, group=H // Hkv, tp=tp, k_row=Hkv * D // 2, k_head=D // 2, v_row=Hkv * D // 2,
                    v_head=D // 2, N=n, q_tok=H * D, q_head=D, m_row=tp // 2, has_mask=int(n > 1), H_kv=Hkv)
         out = np.zeros(n * H * D, np.float32)
-        self.L.kco_flash_attn_f16(np.ascontiguousarray(q, np.float32), self.kc[l], self.vc[l], mask.view(np.uint16), out,
-                                  C.byref(d), np.float32(1.0 / np.sqrt(np.float32(D))))
+        args = (np.ascontiguousarray(q, np.float32), self.kc[l], self.vc[l], mask.view(np.uint16), out, C.byref(d),
+                np.float32(1.0 / np.sqrt(np.float32(D))))
+        if self.threads > 0:
+            self.L.kco_flash_attn_f16_mt(*args, self.threads)
+        else:
+            self.L.kco_flash_attn_f16(*args)
         return out.reshape(n, H * D)
 
     def set_rows(self, l, k, v, p0):
