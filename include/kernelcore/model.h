@@ -92,6 +92,10 @@ KC_API kcError_t kcModelGenerate(kcModel_t model, int steps, int* tokens_out) KC
 /* Current position (tokens in the KV cache); kcModelReset empties the cache. */
 KC_API kcError_t kcModelPosition(kcModel_t model, int* pos) KC_NOEXCEPT;
 KC_API kcError_t kcModelReset(kcModel_t model) KC_NOEXCEPT;
+/* Copies positions [pos0, pos0 + n) of a layer's fp16 KV cache (which: 0 k, 1 v) to host memory:
+ * n * n_head_kv * head_dim halves, in the ggml set_rows layout (a position's heads back to back). For
+ * checks and inspection; it waits for the model's queued work. */
+KC_API kcError_t kcModelReadCache(kcModel_t model, int layer, int which, int pos0, int n, void* host) KC_NOEXCEPT;
 /* The model's stream (its work is ordered on it), for timing with kcEventRecord. */
 KC_API kcError_t kcModelStream(kcModel_t model, kcStream_t* stream) KC_NOEXCEPT;
 

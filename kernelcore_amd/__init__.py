@@ -162,6 +162,7 @@ def lib():
         L.kcModelGenerate.argtypes = [_p, _i, _p]
         L.kcModelPosition.argtypes = [_p, C.POINTER(_i)]
         L.kcModelReset.argtypes = [_p]
+        L.kcModelReadCache.argtypes = [_p, _i, _i, _i, _i, _p]
         L.kcModelStream.argtypes = [_p, C.POINTER(_p)]
         L.kcGetErrorString.argtypes = [_i]
         L.kcCodegenName.argtypes = [_i]
@@ -334,6 +335,13 @@ class Model:
         p = _i()
         call("kcModelPosition", self.h, C.byref(p))
         return p.value
+
+    def read_cache(self, layer, which, pos0, n):
+        """fp16 bits (uint16) of positions [pos0, pos0 + n) of a layer's k (which 0) or v (1) cache."""
+        kvd = self.cfg.n_head_kv * self.cfg.head_dim
+        out = np.zeros(max(n, 1) * kvd, np.uint16)
+        call("kcModelReadCache", self.h, layer, which, pos0, n, out.ctypes.data)
+        return out[: n * kvd]
 
     def reset(self):
         call("kcModelReset", self.h)

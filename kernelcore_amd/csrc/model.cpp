@@ -730,6 +730,22 @@ kcError_t kcModelPosition(kcModel_t m, int* pos) noexcept {
     return ok;
 }
 
+kcError_t kcModelReadCache(kcModel_t m, int layer, int which, int pos0, int n, void* host) noexcept {
+    if (E e = checkModel(m); e != ok) return e;
+    const auto& c = m->c;
+    if (layer < 0 || layer >= c.n_layer || (which != 0 && which != 1) || pos0 < 0 || n < 0 || pos0 + n > c.max_ctx ||
+        (n > 0 && !host)) {
+        kcamd::setDetail("kcModelReadCache: layer, which (0 k, 1 v) or position range out of bounds");
+        return kc::Error::InvalidValue;
+    }
+    if (n == 0) return ok;
+    KM_TRYE(syncModel(m));
+    const size_t row = (size_t)c.n_head_kv * c.head_dim * 2;  // bytes per position
+    const int* base = which ? m->L[layer].vcache : m->L[layer].kcache;
+    return kcMemcpy(host, reinterpret_cast<const char*>(base) + (size_t)pos0 * row, (size_t)n * row,
+                    kc::CopyKind::DeviceToHost);
+}
+
 kcError_t kcModelReset(kcModel_t m) noexcept {
     if (E e = checkModel(m); e != ok) return e;
     KM_TRYE(syncModel(m));
