@@ -162,8 +162,8 @@ int launchMatmulCols(bool q6k, bool per256, const kcMatmulKQ8Args& a, hipStream_
 int launchMatmulKq(bool q6k, bool per256, const kcMatmulKQ8Args& a, hipStream_t s) {
     // "matmul_path": 0 default (MFMA from 64 columns with per-256 slots), 1 column tiles; 2 and up
     // force the MFMA kernels: 2 default MFMA kernel, 3 register-staged 2 x 2 blocks per wavefront,
-    // 4 / 5 register-staged one-wavefront-per-SIMD rows (two / one super-block groups), 6 the
-    // fp16-activation kernel with 128 columns per wavefront.
+    // 4 / 5 register-staged one-wavefront-per-SIMD rows (two / one super-block groups), 7 the
+    // wide-tile kernel (kmatmul_mfmaw.hip).
     const int path = option("matmul_path");
     const bool mfma = per256 && (path >= 2 || (path == 0 && a.ncols >= 64));
     if (mfma) return launchMatmulMfma(q6k, a, s);

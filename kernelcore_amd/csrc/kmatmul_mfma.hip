@@ -42,6 +42,7 @@
 
 #include "internal.hpp"
 #include "kquant.hpp"
+#include "kmatmul_mfma.hpp"
 #include "launch.hpp"
 
 namespace kcamd {
@@ -892,20 +893,8 @@ __device__ __forceinline__ void hTile(char* lbase, const uint8_t* __restrict__ q
     }
 }
 
-// Up to three weight matrices over the same activations, each split over K into ks ranges
-// (blockIdx.z; split z writes its partial sums to y[z]).
-struct HPart {
-    const uint8_t* qw;
-    float* y[2];
-    int rows;
-    int q6;
-    int tile0;  // first row tile (blockIdx.x) of this matrix
-};
-struct HGroup {
-    HPart p[3];
-    int nparts;
-    int ks;
-};
+using HPart = MfmaPart;
+using HGroup = MfmaGroup;
 
 __global__ __launch_bounds__(256) void matmul_kq_mfma_h_kernel(HGroup g, const _Float16* __restrict__ act,
                                                                const _Float16* __restrict__ mins,
@@ -969,6 +958,8 @@ int runMfmaH(const MmPart* parts, int nparts, const int* xq, int k, int ncols, i
                            static_cast<uint2*>(act), any_q4 ? reinterpret_cast<h8*>(mins) : nullptr, xdT, nsb, words,
                            ncols, ncp);
     }
+    if (option("matmul_path") == 7)  // the wide-tile kernel (every weight dequantized once per workgroup)
+        return launchMfmaW(g, tiles, act, mins, xdT, nsb, ncols, ncp, s);
     const dim3 grid(tiles, (ncols + G::kCols - 1) / G::kCols, ks);
     hipLaunchKernelGGL(matmul_kq_mfma_h_kernel, grid, dim3(256), G::kLds, s, g, static_cast<const _Float16*>(act),
                        mins, xdT, nsb, ncols, ncp);
@@ -1040,7 +1031,10 @@ int launchMatmulKqNoAlloc(bool q6k, bool per256, const kcMatmulKQ8Args& a, hipSt
     return runMfmaH(&part, 1, a.xq, a.k, a.ncols, 1, p, s);
 }
 
-bool mfmaHUsable(int ncols, int k) { return option("matmul_path") == 0 && (size_t)ncols * k * 2 < (1ull << 32); }
+bool mfmaHUsable(int ncols, int k) {
+    const int path = option("matmul_path");
+    return (path == 0 || path == 7) && (size_t)ncols * k * 2 < (1ull << 32);
+}
 
 int launchMatmulMfma(bool q6k, const kcMatmulKQ8Args& a, hipStream_t s) {
     const int path = option("matmul_path");

@@ -154,11 +154,14 @@ def test_mfma_matmul_matches_oracle(qtype, rows, k, ncols):
     y, _ = run_matmul(qtype, True, w, x, rows, k, ncols)
     kc.set_option("matmul_path", 1)
     yc, _ = run_matmul(qtype, True, w, x, rows, k, ncols)
+    kc.set_option("matmul_path", 7)  # the wide-tile kernel (kmatmul_mfmaw.hip)
+    yw, _ = run_matmul(qtype, True, w, x, rows, k, ncols)
     kc.set_option("matmul_path", 0)
     want = oracle_matmul(qtype, True, w, oracle_slots(x, k, ncols, True), rows, k, ncols)
     assert np.array_equal(kq.bits(yc), kq.bits(want))  # the column-tile path stays bit-exact
-    assert kq.rel_diff(y, want) < TOL
-    assert kq.rel_diff(y, want) < 1e-5  # exact integers; only the final float combine differs
+    for got in (y, yw):
+        assert kq.rel_diff(got, want) < TOL
+        assert kq.rel_diff(got, want) < 1e-5  # exact integers; only the final float combine differs
 
 
 def test_mfma_matmul_config3_shapes():

@@ -158,6 +158,24 @@ def test_model_qwen3_8b_shape_two_layers():
     m.close()
 
 
+def test_model_prefill_on_the_wide_tile_matmul():
+    """matmul_path = 7: the model's grouped prefill matmuls (q/k/v and gate/up in one launch, K
+    split for o and down) on the wide-tile MFMA kernel, a 70-token prompt at the Qwen3-8B widths
+    (two layers) against the oracle."""
+    cfg = dict(n_layer=2, n_embd=4096, n_head=32, n_head_kv=8, head_dim=128, n_ff=12288, n_vocab=151936,
+               norm_eps=1e-6, rope_theta=1000000.0, rope_neox=1, qk_norm=1, max_ctx=128, max_batch=80)
+    kc.set_option("matmul_path", 7)
+    try:
+        m, o = build(cfg, 23)
+        prompt = np.random.default_rng(6).integers(0, cfg["n_vocab"], 70).astype(np.int32)
+        lg, lo = m.forward(prompt), o.forward(prompt)
+        note(f"model 8b-shape, wide-tile matmul: prompt rel L2 {rel_l2(lg, lo):.2e}")
+        assert rel_l2(lg, lo) < 1e-2, rel_l2(lg, lo)
+        m.close()
+    finally:
+        kc.set_option("matmul_path", 0)
+
+
 @pytest.mark.parametrize("name,cfg", [("llama", LLAMA), ("qwen3", QWEN)])
 def test_model_unfused_decode_path(name, cfg):
     """decode_path = 1 runs the one-kernel-per-reference-op decode step (add_sumsq, norm_mul_q8,
