@@ -977,6 +977,46 @@ int runMfma(const kcMatmulKQ8Args& a, hipStream_t s) {
     return fromHip(hipGetLastError(), Q6 ? "matmul_q6k_q8k (MFMA)" : "matmul_q4k_q8k (MFMA)");
 }
 
+// The device's compute units (cached per device).
+int cuCount() {
+    static int cus[16] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+// y += p over n floats (the second K half of a split launch).
+__global__ void add_partial_kernel(float* __restrict__ y, const float* __restrict__ p, long long n) {
+    const long long i = blockIdx.x * 256LL + threadIdx.x;
+    if (i < n) y[i] += p[i];
+}
+
+// A by-name launch on the fp16-activation kernel: a grid under two workgroups per CU splits K in
+// two, the second half's partial sums staged after the activations and added into y by one more
+// kernel (fl(a + b): the same for either order).
+int stagedKs(const kcMatmulKQ8Args& a) {
+    const long long wgs = (long long)((a.rows + kBM - 1) / kBM) * ((a.ncols + 63) / 64);
+    return (a.k / 256 >= 2 && wgs < 2LL * cuCount()) ? 2 : 1;
+}
+size_t stagedActBytes(const kcMatmulKQ8Args& a) { return (actBytes(a.ncols, a.k) + 255) & ~size_t(255); }
+size_t stagedBytes(const kcMatmulKQ8Args& a, int ks) {
+    return stagedActBytes(a) + (ks == 2 ? (size_t)a.rows * a.ncols * 4 : 0);
+}
+int runStaged(bool q6k, const kcMatmulKQ8Args& a, int ks, void* buf, hipStream_t s) {
+    float* partial = ks == 2 ? reinterpret_cast<float*>(static_cast<char*>(buf) + stagedActBytes(a)) : nullptr;
+    const MmPart part{a.qw, {a.y, partial}, a.rows, q6k ? 1 : 0};
+    if (int st = runMfmaH(&part, 1, a.xq, a.k, a.ncols, ks, buf, s)) return st;
+    if (ks == 1) return 0;
+    const long long n = (long long)a.rows * a.ncols;
+    hipLaunchKernelGGL(add_partial_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a.y, partial, n);
+    return fromHip(hipGetLastError(), "matmul (MFMA, K split): partial sum");
+}
+
 // ---- the fixed scratch of kcLaunchMatmulNoAlloc -----------------------------------------------
 //
 // The fp16 activations of one MFMA launch staged in a file-scope device array instead of the
@@ -1013,7 +1053,10 @@ int launchMatmulKqNoAlloc(bool q6k, bool per256, const kcMatmulKQ8Args& a, hipSt
     if (path == 3) return q6k ? runMfma<true>(a, s) : runMfma<false>(a, s);
     if (path == 4) return q6k ? runMfma8<true, 2>(a, s) : runMfma8<false, 2>(a, s);
     if (path == 5) return q6k ? runMfma8<true, 1>(a, s) : runMfma8<false, 1>(a, s);
-    const size_t need = actBytes(a.ncols, a.k);
+    // the K split of launchMatmulMfma when its partial sums fit too, else one K range
+    int ks = stagedKs(a);
+    if (ks == 2 && stagedBytes(a, 2) > kFixedScratchBytes) ks = 1;
+    const size_t need = stagedBytes(a, ks);
     if (need > kFixedScratchBytes) {
         setDetail("matmul (no-alloc): %d columns of %d values need %zu bytes of staging, above the fixed %zu "
                   "(ncols * k * 2 + ncols * k / 8 + k / 64 * ncols rounded up to 128)",
@@ -1027,8 +1070,7 @@ int launchMatmulKqNoAlloc(bool q6k, bool per256, const kcMatmulKQ8Args& a, hipSt
         setDetail("matmul (no-alloc): the fixed scratch of device %d was not set up (kcInit)", dev);
         return KC_ERROR_NOT_INITIALIZED;
     }
-    const MmPart part{a.qw, {a.y, nullptr}, a.rows, q6k ? 1 : 0};
-    return runMfmaH(&part, 1, a.xq, a.k, a.ncols, 1, p, s);
+    return runStaged(q6k, a, ks, p, s);
 }
 
 bool mfmaHUsable(int ncols, int k) {
@@ -1036,16 +1078,15 @@ bool mfmaHUsable(int ncols, int k) {
     return (path == 0 || path == 7) && (size_t)ncols * k * 2 < (1ull << 32);
 }
 
+
 int launchMatmulMfma(bool q6k, const kcMatmulKQ8Args& a, hipStream_t s) {
     const int path = option("matmul_path");
     if (path == 3) return q6k ? runMfma<true>(a, s) : runMfma<false>(a, s);  // 2 x 2 blocks per wavefront
     if (path == 4) return q6k ? runMfma8<true, 2>(a, s) : runMfma8<false, 2>(a, s);
     // fp16 activations staged by direct loads (a per-stream buffer, addressed with 32-bit offsets)
     if (path != 5 && (size_t)a.ncols * a.k * 2 < (1ull << 32)) {
-        if (void* act = streamScratch(s, actBytes(a.ncols, a.k))) {
-            const MmPart part{a.qw, {a.y, nullptr}, a.rows, q6k ? 1 : 0};
-            return runMfmaH(&part, 1, a.xq, a.k, a.ncols, 1, act, s);
-        }
+        const int ks = stagedKs(a);
+        if (void* buf = streamScratch(s, stagedBytes(a, ks))) return runStaged(q6k, a, ks, buf, s);
     }
     return q6k ? runMfma8<true, 1>(a, s) : runMfma8<false, 1>(a, s);
 }
