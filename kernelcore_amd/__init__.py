@@ -20,7 +20,8 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB_PATH = os.path.join(HERE, "libkernelcore_amd.so")
-HEADERS = [os.path.join(ROOT, "include", "kernelcore", n) for n in ("kc.h", "llm_kernels.h", "model.h", "gguf.h")]
+HEADERS = [os.path.join(ROOT, "include", "kernelcore", n) for n in ("kc.h", "llm_kernels.h", "model.h", "gguf.h",
+                                                                                   "mul_mat.h")]
 
 ERRORS = ["Success", "NotInitialized", "InvalidValue", "InvalidDevice", "OutOfMemory", "InvalidPointer",
           "InvalidResourceHandle", "UnsupportedOperation", "InvalidKernelImage", "KernelNotFound",
@@ -164,6 +165,12 @@ def lib():
         L.kcModelReset.argtypes = [_p]
         L.kcModelReadCache.argtypes = [_p, _i, _i, _i, _i, _p]
         L.kcModelStream.argtypes = [_p, C.POINTER(_p)]
+        L.kcMulMatConfigFromEnv.argtypes = [C.POINTER(MulMatConfig)]
+        L.kcMulMatConfigFromEnv.restype = None
+        L.kcMulMatRecordingCreate.argtypes = [C.POINTER(_p), C.POINTER(MulMatConfig), _p]
+        L.kcMulMatRecordingReset.argtypes = [_p]
+        L.kcMulMatRecordingDestroy.argtypes = [_p]
+        L.kcMulMat.argtypes = [_p, C.POINTER(MulMatNode), C.POINTER(MulMatPlan)]
         L.kcGetErrorString.argtypes = [_i]
         L.kcCodegenName.argtypes = [_i]
         _LIB = L
@@ -281,6 +288,65 @@ def plan_decode(**cfg):
     fused = _i()
     call("kcModelPlanDecode", C.byref(c), C.byref(fused))
     return fused.value
+
+
+class MulMatConfig(C.Structure):
+    """kcMulMatConfig (include/kernelcore/mul_mat.h): the backend's switches."""
+    _fields_ = [("matvec_cols", _i), ("q8k", _i), ("tile", _i), ("row_block", _i)]
+
+
+class MulMatNode(C.Structure):
+    """kcMulMatNode: one MUL_MAT node (weights w: rows x k of wtype; input x: ncols columns)."""
+    _fields_ = [("wtype", _i), ("w", _p), ("rows", _i), ("k", _i), ("x", _p), ("ncols", C.c_longlong),
+                ("x_col_bytes", C.c_size_t), ("y", _p)]
+
+
+class MulMatPlan(C.Structure):
+    """kcMulMatPlan: what a node recorded."""
+    _fields_ = [("quantizer", C.c_char * 24), ("input_reused", _i), ("kernel", C.c_char * 24), ("launches", _i),
+                ("k256", _i)]
+
+    def as_dict(self):
+        return {"quantizer": self.quantizer.decode(), "input_reused": bool(self.input_reused),
+                "kernel": self.kernel.decode(), "launches": self.launches, "k256": bool(self.k256)}
+
+
+def mul_mat_config_from_env():
+    """kcMulMatConfigFromEnv (host only): the reference's defaults and GGML_KERNELCORE_* overrides."""
+    c = MulMatConfig()
+    lib().kcMulMatConfigFromEnv(C.byref(c))
+    return {"matvec_cols": c.matvec_cols, "q8k": c.q8k, "tile": c.tile, "row_block": c.row_block}
+
+
+class MulMatRecording:
+    """A kcMulMat recording: MUL_MAT nodes dispatched as the reference's ggml backend does, inputs
+    quantized once per recording (include/kernelcore/mul_mat.h)."""
+
+    def __init__(self, stream=None, **cfg):
+        c = None
+        if cfg:
+            base = mul_mat_config_from_env()
+            base.update(cfg)
+            c = MulMatConfig(**base)
+        h = _p()
+        call("kcMulMatRecordingCreate", C.byref(h), C.byref(c) if c is not None else None, stream)
+        self.h = h
+
+    def reset(self):
+        call("kcMulMatRecordingReset", self.h)
+
+    def mul_mat(self, wtype, w, rows, k, x, ncols, y, x_col_bytes=None):
+        """Records one node; returns its plan as a dict. wtype: "q4k", "q6k" or "f16" (or the id)."""
+        wt = {"q4k": 12, "q6k": 14, "f16": 1}.get(wtype, wtype)
+        node = MulMatNode(wt, w, rows, k, x, ncols, x_col_bytes if x_col_bytes is not None else 4 * k, y)
+        plan = MulMatPlan()
+        call("kcMulMat", self.h, C.byref(node), C.byref(plan))
+        return plan.as_dict()
+
+    def close(self):
+        if self.h:
+            call("kcMulMatRecordingDestroy", self.h)
+            self.h = None
 
 
 class Model:

@@ -1,0 +1,227 @@
+// mul_mat.cpp -- kcMulMat: the MUL_MAT dispatch of the reference's ggml backend over the public
+// kc* calls (integrations/llama.cpp/ggml/src/ggml-kernelcore/ggml-kernelcore.cpp: switches
+// :46-53 and :81-86, batch_k256 :424, scratch_take :431-449, quantized_input :471-497,
+// mul_mat_impl :555-589). The branch structure, the kernels each branch launches and their
+// arguments are the reference's (they are the interface a backend drives); the scratch, the input
+// cache and the validation are written for a GPU stream: launches are asynchronous, so growing the
+// scratch waits for the stream before the old buffer goes.
+#include <algorithm>
+#include <climits>
+#include <cstdlib>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "internal.hpp"
+#include "kernelcore/llm_kernels.h"
+#include "kernelcore/model.h"
+#include "kernelcore/mul_mat.h"
+
+struct kcMulMatRecording_st {
+    kcMulMatConfig cfg{};
+    kcStream_t stream = nullptr;
+    int* scratch = nullptr;
+    size_t cap = 0;   // ints
+    size_t used = 0;  // ints taken by this recording
+    struct Input {
+        const float* x;
+        long long ncols;
+        int k;
+        bool k256;
+        int* q;
+    };
+    std::vector<Input> inputs;  // the recording's quantized inputs
+};
+
+namespace {
+
+using E = kcError_t;
+constexpr E ok = kc::Error::Success;
+
+E bad(const char* why) {
+    kcamd::setDetail("mul_mat: %s", why);
+    return kc::Error::InvalidValue;
+}
+
+// Slot ints of one column: per 32 values nb * 11 (8 words of bytes, then d and the sum per block);
+// per 256 values nsb * 85 (the reference's scratchInts / scratchKInts, llm/llm_kernels.hpp:84-89).
+size_t slotInts(int k, bool k256) { return k256 ? size_t(k / 256) * 85 : size_t(k / 32) * 11; }
+
+// `ints` ints of the recording's scratch (64-byte multiples). Growing it: the stream finishes
+// the launches that read the old buffer, which is freed, and the cached inputs (in it) are dropped.
+E take(kcMulMatRecording_st& r, size_t ints, int** out) {
+    ints = (ints + 15) / 16 * 16;
+    if (r.used + ints > r.cap) {
+        if (r.scratch) {
+            if (E e = kcStreamSynchronize(r.stream); e != ok) return e;
+            if (E e = kcFree(r.scratch); e != ok) return e;
+            r.scratch = nullptr;
+        }
+        const size_t want = std::max(ints * 4, r.cap * 2);
+        r.cap = r.used = 0;
+        r.inputs.clear();
+        void* p = nullptr;
+        if (E e = kcMalloc(&p, want * sizeof(int)); e != ok) return e;
+        r.scratch = static_cast<int*>(p);
+        r.cap = want;
+    }
+    *out = r.scratch + r.used;
+    r.used += ints;
+    return ok;
+}
+
+void name(char (&dst)[24], const char* src) {
+    std::strncpy(dst, src, sizeof dst - 1);
+    dst[sizeof dst - 1] = '\0';
+}
+
+E launch(const kcMulMatRecording_st& r, const char* kernel, const void* args, kcMulMatPlan& plan) {
+    const E e = kcLaunchKernel(kernel, args, r.stream);
+    if (e == ok) ++plan.launches;
+    return e;
+}
+
+// The 8-bit form of the node's input, made once per recording.
+E quantizedInput(kcMulMatRecording_st& r, const kcMulMatNode& n, bool k256, int** q, kcMulMatPlan& plan) {
+    for (const auto& in : r.inputs)
+        if (in.x == n.x && in.ncols == n.ncols && in.k == n.k && in.k256 == k256) {
+            *q = in.q;
+            plan.input_reused = 1;
+            return ok;
+        }
+    const int nb = n.k / 32;
+    const size_t slot = slotInts(n.k, k256);
+    int* base = nullptr;
+    if (E e = take(r, slot * size_t(n.ncols), &base); e != ok) return e;
+    const bool contiguous = n.x_col_bytes == size_t(n.k) * sizeof(float);
+    if (k256) {
+        const kcQuantizeColsArgs a{n.x, base, nullptr, n.k, int(n.ncols)};
+        name(plan.quantizer, "quantize_cols_k");
+        if (E e = launch(r, "quantize_cols_k", &a, plan); e != ok) return e;
+    } else if (n.ncols > 1 && contiguous) {  // contiguous columns: one launch
+        const kcQuantizeColsArgs a{n.x, base, nullptr, n.k, int(n.ncols)};
+        name(plan.quantizer, "quantize_cols");
+        if (E e = launch(r, "quantize_cols", &a, plan); e != ok) return e;
+    } else {
+        name(plan.quantizer, "quantize_q8x4");
+        for (long long c = 0; c < n.ncols; ++c) {
+            int* qc = base + size_t(c) * slot;
+            const float* xc = reinterpret_cast<const float*>(reinterpret_cast<const char*>(n.x) + size_t(c) * n.x_col_bytes);
+            const kcQuantizeArgs a{xc, qc, reinterpret_cast<float*>(qc + nb * 8), nb};
+            if (E e = launch(r, "quantize_q8x4", &a, plan); e != ok) return e;
+        }
+    }
+    r.inputs.push_back({n.x, n.ncols, n.k, k256, base});
+    *q = base;
+    return ok;
+}
+
+E validate(const kcMulMatNode& n) {
+    const bool f16 = n.wtype == KC_QTYPE_F16;
+    if (!f16 && n.wtype != KC_QTYPE_Q4_K && n.wtype != KC_QTYPE_Q6_K)
+        return bad("weight type must be Q4_K (12), Q6_K (14) or F16 (1)");
+    if (!n.w || !n.x || !n.y) return bad("null weight, input or output pointer");
+    if (n.rows <= 0 || n.rows % 8) return bad("rows must be a positive multiple of 8");
+    if (n.k <= 0 || (f16 ? n.k % 2 : n.k % 256)) return bad("k must be a positive multiple of 256 (F16: even)");
+    if (n.ncols < 1 || n.ncols > INT_MAX) return bad("ncols must be in [1, INT_MAX]");
+    if (n.x_col_bytes < size_t(n.k) * sizeof(float) || n.x_col_bytes % sizeof(float))
+        return bad("x_col_bytes must be at least 4 k and a multiple of 4");
+    if (f16 && n.x_col_bytes != size_t(n.k) * sizeof(float)) return bad("F16 weights take contiguous input columns");
+    return ok;
+}
+
+E mulMat(kcMulMatRecording_st& r, const kcMulMatNode& n, kcMulMatPlan& plan) {
+    if (E e = validate(n); e != ok) return e;
+    const int ncols = int(n.ncols);
+    if (n.wtype == KC_QTYPE_F16) {  // f32 activations as they are
+        const kcMatmulF16Args a{static_cast<const int*>(n.w), n.x, n.y, nullptr, n.rows, n.k, ncols};
+        name(plan.kernel, "matmul_f16");
+        return launch(r, "matmul_f16", &a, plan);
+    }
+    const bool q4 = n.wtype == KC_QTYPE_Q4_K;
+    const bool contiguous = n.x_col_bytes == size_t(n.k) * sizeof(float);
+    // batch_k256: batches read activations scaled per 256 values unless matvec_cols or q8k = 0
+    const bool k256 = n.ncols > 1 && !r.cfg.matvec_cols && r.cfg.q8k && contiguous;
+    plan.k256 = k256;
+    int* base = nullptr;
+    if (E e = quantizedInput(r, n, k256, &base, plan); e != ok) return e;
+    if (n.ncols > 1 && !r.cfg.matvec_cols) {  // a batch: one matmul (weights read once per 4 or 8 columns)
+        const bool x8 = r.cfg.tile == 8 && n.ncols > 4;
+        const char* kernel = k256 ? (x8 ? (q4 ? "matmul_q4k_q8kx8" : "matmul_q6k_q8kx8")
+                                        : (q4 ? "matmul_q4k_q8kx4" : "matmul_q6k_q8kx4"))
+                                  : (x8 ? (q4 ? "matmul_q4k_q8x8" : "matmul_q6k_q8x8")
+                                        : (q4 ? "matmul_q4k_q8x4" : "matmul_q6k_q8x4"));
+        const kcMatmulKQ8Args a{static_cast<const int*>(n.w), base, n.y, nullptr, n.rows, n.k, ncols, r.cfg.row_block};
+        name(plan.kernel, kernel);
+        return launch(r, kernel, &a, plan);
+    }
+    const char* kernel = q4 ? "matvec_q4k_q8" : "matvec_q6k_q8";  // one matvec per column
+    name(plan.kernel, kernel);
+    const int nb = n.k / 32;
+    const size_t slot = slotInts(n.k, false);
+    for (int c = 0; c < ncols; ++c) {
+        const int* q = base + size_t(c) * slot;
+        const kcMatvecQ4Q8Args a{static_cast<const int*>(n.w), q, reinterpret_cast<const float*>(q + nb * 8),
+                                 n.y + size_t(c) * n.rows, nullptr, n.rows, n.k};
+        if (E e = launch(r, kernel, &a, plan); e != ok) return e;
+    }
+    return ok;
+}
+
+}  // namespace
+
+KC_API void kcMulMatConfigFromEnv(kcMulMatConfig* cfg) noexcept {
+    if (!cfg) return;
+    *cfg = kcMulMatConfig{0, 1, 8, 8};
+    if (const char* mc = std::getenv("GGML_KERNELCORE_MATVEC_COLS")) cfg->matvec_cols = std::strcmp(mc, "1") == 0;
+    if (const char* rb = std::getenv("GGML_KERNELCORE_ROW_BLOCK")) cfg->row_block = std::max(1, std::atoi(rb));
+    if (const char* qk = std::getenv("GGML_KERNELCORE_Q8K")) cfg->q8k = std::strcmp(qk, "0") != 0;
+    if (const char* tl = std::getenv("GGML_KERNELCORE_TILE")) cfg->tile = std::atoi(tl) == 4 ? 4 : 8;
+}
+
+KC_API kcError_t kcMulMatRecordingCreate(kcMulMatRecording_t* rec, const kcMulMatConfig* cfg,
+                                         kcStream_t stream) noexcept {
+    if (!rec) return bad("null recording pointer");
+    *rec = nullptr;
+    kcMulMatConfig c;
+    if (cfg) c = *cfg;
+    else kcMulMatConfigFromEnv(&c);
+    if (c.tile != 4 && c.tile != 8) return bad("tile must be 4 or 8");
+    if (c.row_block < 1) return bad("row_block must be at least 1");
+    c.matvec_cols = c.matvec_cols != 0;
+    c.q8k = c.q8k != 0;
+    auto* r = new (std::nothrow) kcMulMatRecording_st;
+    if (!r) return kc::Error::OutOfMemory;
+    r->cfg = c;
+    r->stream = stream;
+    *rec = r;
+    return ok;
+}
+
+KC_API kcError_t kcMulMatRecordingReset(kcMulMatRecording_t rec) noexcept {
+    if (!rec) return kc::Error::InvalidResourceHandle;
+    rec->inputs.clear();
+    rec->used = 0;  // same stream: the next recording's launches run after the last one's
+    return ok;
+}
+
+KC_API kcError_t kcMulMatRecordingDestroy(kcMulMatRecording_t rec) noexcept {
+    if (!rec) return ok;
+    E e = ok;
+    if (rec->scratch) {  // launches in flight may still read it
+        e = kcStreamSynchronize(rec->stream);
+        const E f = kcFree(rec->scratch);
+        if (e == ok) e = f;
+    }
+    delete rec;
+    return e;
+}
+
+KC_API kcError_t kcMulMat(kcMulMatRecording_t rec, const kcMulMatNode* node, kcMulMatPlan* plan) noexcept {
+    if (!rec) return kc::Error::InvalidResourceHandle;
+    if (!node) return bad("null node");
+    kcMulMatPlan p{};
+    const E e = mulMat(*rec, *node, p);
+    if (plan) *plan = p;
+    return e;
+}

@@ -81,12 +81,14 @@ STRUCTS = ["VectorAddArgs", "QuantizeArgs", "MatvecQ4Q8Args", "MatmulKQ8Args", "
            "RmsNormArgs", "MulRowsArgs", "RopeGgmlArgs", "AddSumsqFArgs", "SumsqPartArgs", "NormMulQ8Args",
            "SiluMulQ8FArgs",
            "SiluMulArgs", "SetRowsF16Args", "FaDims", "FaScoresArgs", "FaMaxArgs", "FaExpArgs", "FaValuesArgs",
-           "KquantRepackArgs", "GetRowsKquantArgs", "QuantizeKquantArgs", "FillNormalArgs", "FlashAttnArgs", "DeviceProperties"]
+           "KquantRepackArgs", "GetRowsKquantArgs", "QuantizeKquantArgs", "FillNormalArgs", "FlashAttnArgs", "DeviceProperties",
+           "MulMatConfig", "MulMatNode", "MulMatPlan"]
 
 
 def test_struct_layouts_match_the_c_header(tmp_path):
     """ctypes mirrors against what gcc makes of include/kernelcore/llm_kernels.h."""
-    lines = ["#include <stdio.h>", "#include <stddef.h>", "#include <kernelcore/llm_kernels.h>", "int main(void) {"]
+    lines = ["#include <stdio.h>", "#include <stddef.h>", "#include <kernelcore/llm_kernels.h>",
+             "#include <kernelcore/mul_mat.h>", "int main(void) {"]
     for s in STRUCTS:
         cls = getattr(kc, s)
         lines.append(f'printf("{s} %zu\\n", sizeof(kc{s}));')
