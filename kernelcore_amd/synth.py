@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import (QTYPE, Buffer, FillNormalArgs, QuantizeKquantArgs, launch, synchronize)
+from . import (QTYPE, Buffer, FillNormalArgs, QuantizeKquantArgs, launch, repack, synchronize)
 
 Q4K, Q6K, F32, F16 = 12, 14, 0, 1
 
@@ -48,6 +48,26 @@ def quantized_matrix(qtype, rows, k, seed, std=0.02, f32=None, blocks=None):
         synchronize()
         return blocks.download(np.uint8, nbytes)
     finally:
+        if own_f:
+            f32.free()
+        if own_b:
+            blocks.free()
+
+
+def quantized_stream(qtype, rows, k, seed, std=0.02, f32=None, blocks=None):
+    """The same matrix as quantized_matrix, left on the device as the repacked weight stream the
+    kernels read (a new Buffer); nothing crosses to the host. f32 / blocks: optional device Buffers
+    large enough to reuse."""
+    n = rows * k
+    own_f, own_b = f32 is None, blocks is None
+    f32 = f32 or Buffer(n * 4)
+    blocks = blocks or Buffer(rows * (k // 256) * (144 if qtype == "q4k" else 210))
+    try:
+        launch("fill_normal_f32", FillNormalArgs(f32.ptr, n, seed, 0.0, std))
+        launch("quantize_kquant", QuantizeKquantArgs(f32.ptr, blocks.ptr, QTYPE[qtype], rows, k))
+        return repack(qtype, blocks, rows, k)
+    finally:
+        synchronize()
         if own_f:
             f32.free()
         if own_b:
