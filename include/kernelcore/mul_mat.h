@@ -77,4 +77,37 @@ KC_API kcError_t kcMulMatRecordingDestroy(kcMulMatRecording_t rec) KC_NOEXCEPT;
  * kernels do not take, with the reason in kcGetLastErrorDetail. */
 KC_API kcError_t kcMulMat(kcMulMatRecording_t rec, const kcMulMatNode* node, kcMulMatPlan* plan) KC_NOEXCEPT;
 
+/* ADD (optional) + RMS_NORM + MUL by the norm weight, with the result also quantized for the
+ * MUL_MATs that read it (fused_norm, ggml-kernelcore.cpp:502-530): with a and b given, x = a + b
+ * (add_sumsq_f writes x and the per-32 partial sums of squares), else sumsq_part reads x; then
+ * y = x / rms(x) * w (norm_mul_q8k_f for a batch under batch_k256, else norm_mul_q8_f), whose
+ * 8-bit slots are registered under y: a kcMulMat of the same recording reading y (ncols = rows,
+ * k = n, contiguous) takes them without quantizing again. n % 256 == 0, n * rows < 2^24. */
+typedef struct kcMulMatNormNode {
+    const float* a; /* NULL: no ADD */
+    const float* b;
+    float* x;       /* the norm's input (with ADD: written, a + b) */
+    const float* w; /* the norm weight, n values */
+    float* y;
+    int n;
+    int rows;
+    float eps;
+} kcMulMatNormNode;
+/* plan: quantizer = the partial-sums kernel, kernel = the norm kernel. */
+KC_API kcError_t kcMulMatFusedNorm(kcMulMatRecording_t rec, const kcMulMatNormNode* node,
+                                   kcMulMatPlan* plan) KC_NOEXCEPT;
+
+/* SWIGLU (y = silu(g) * u over cols rows of n) with the result also quantized and registered under
+ * y as above (fused_swiglu, ggml-kernelcore.cpp:533-545: silu_mul_q8kf for a batch under
+ * batch_k256, else silu_mul_q8x4f). n % 256 == 0, n * cols < 2^24. */
+typedef struct kcMulMatSwigluNode {
+    const float* g;
+    const float* u;
+    float* y;
+    int n;
+    int cols;
+} kcMulMatSwigluNode;
+KC_API kcError_t kcMulMatFusedSwiglu(kcMulMatRecording_t rec, const kcMulMatSwigluNode* node,
+                                     kcMulMatPlan* plan) KC_NOEXCEPT;
+
 #endif /* KERNELCORE_MUL_MAT_H */

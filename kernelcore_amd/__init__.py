@@ -171,6 +171,8 @@ def lib():
         L.kcMulMatRecordingReset.argtypes = [_p]
         L.kcMulMatRecordingDestroy.argtypes = [_p]
         L.kcMulMat.argtypes = [_p, C.POINTER(MulMatNode), C.POINTER(MulMatPlan)]
+        L.kcMulMatFusedNorm.argtypes = [_p, C.POINTER(MulMatNormNode), C.POINTER(MulMatPlan)]
+        L.kcMulMatFusedSwiglu.argtypes = [_p, C.POINTER(MulMatSwigluNode), C.POINTER(MulMatPlan)]
         L.kcGetErrorString.argtypes = [_i]
         L.kcCodegenName.argtypes = [_i]
         _LIB = L
@@ -301,6 +303,16 @@ class MulMatNode(C.Structure):
                 ("x_col_bytes", C.c_size_t), ("y", _p)]
 
 
+class MulMatNormNode(C.Structure):
+    """kcMulMatNormNode: [ADD +] RMS_NORM + MUL, quantized for the MUL_MATs reading y."""
+    _fields_ = [("a", _p), ("b", _p), ("x", _p), ("w", _p), ("y", _p), ("n", _i), ("rows", _i), ("eps", _f)]
+
+
+class MulMatSwigluNode(C.Structure):
+    """kcMulMatSwigluNode: SWIGLU, quantized for the MUL_MATs reading y."""
+    _fields_ = [("g", _p), ("u", _p), ("y", _p), ("n", _i), ("cols", _i)]
+
+
 class MulMatPlan(C.Structure):
     """kcMulMatPlan: what a node recorded."""
     _fields_ = [("quantizer", C.c_char * 24), ("input_reused", _i), ("kernel", C.c_char * 24), ("launches", _i),
@@ -341,6 +353,18 @@ class MulMatRecording:
         node = MulMatNode(wt, w, rows, k, x, ncols, x_col_bytes if x_col_bytes is not None else 4 * k, y)
         plan = MulMatPlan()
         call("kcMulMat", self.h, C.byref(node), C.byref(plan))
+        return plan.as_dict()
+
+    def fused_norm(self, x, w, y, n, rows, eps, a=None, b=None):
+        """[x = a + b;] y = rms_norm(x) * w, its slots registered for the next MUL_MATs; the plan."""
+        plan = MulMatPlan()
+        call("kcMulMatFusedNorm", self.h, C.byref(MulMatNormNode(a, b, x, w, y, n, rows, eps)), C.byref(plan))
+        return plan.as_dict()
+
+    def fused_swiglu(self, g, u, y, n, cols):
+        """y = silu(g) * u, its slots registered for the next MUL_MATs; the plan."""
+        plan = MulMatPlan()
+        call("kcMulMatFusedSwiglu", self.h, C.byref(MulMatSwigluNode(g, u, y, n, cols)), C.byref(plan))
         return plan.as_dict()
 
     def close(self):

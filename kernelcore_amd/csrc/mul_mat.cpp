@@ -1,7 +1,7 @@
 // mul_mat.cpp -- kcMulMat: the MUL_MAT dispatch of the reference's ggml backend over the public
 // kc* calls (integrations/llama.cpp/ggml/src/ggml-kernelcore/ggml-kernelcore.cpp: switches
 // :46-53 and :81-86, batch_k256 :424, scratch_take :431-449, quantized_input :471-497,
-// mul_mat_impl :555-589). The branch structure, the kernels each branch launches and their
+// fused_norm :502-530, fused_swiglu :533-545, mul_mat_impl :555-589). The branch structure, the kernels each branch launches and their
 // arguments are the reference's (they are the interface a backend drives); the scratch, the input
 // cache and the validation are written for a GPU stream: launches are asynchronous, so growing the
 // scratch waits for the stream before the old buffer goes.
@@ -116,6 +116,63 @@ E quantizedInput(kcMulMatRecording_st& r, const kcMulMatNode& n, bool k256, int*
     return ok;
 }
 
+// batch_k256: batches read activations scaled per 256 values unless matvec_cols or q8k = 0
+bool batchK256(const kcMulMatRecording_st& r, long long ncols) { return ncols > 1 && !r.cfg.matvec_cols && r.cfg.q8k; }
+
+// Slots for the 8-bit form of y (ncols columns of k values) plus `extra` ints, registered under y
+// so that the MUL_MATs reading y find them (quantized_slots, :451-467).
+E registeredSlots(kcMulMatRecording_st& r, const float* y, int k, long long ncols, bool k256, size_t extra, int** q) {
+    if (E e = take(r, slotInts(k, k256) * size_t(ncols) + extra, q); e != ok) return e;
+    for (auto it = r.inputs.begin(); it != r.inputs.end(); ++it)  // y rewritten: older slots of it are stale
+        if (it->x == y && it->ncols == ncols && it->k == k && it->k256 == k256) {
+            r.inputs.erase(it);
+            break;
+        }
+    r.inputs.push_back({y, ncols, k, k256, *q});
+    return ok;
+}
+
+E fusedNorm(kcMulMatRecording_st& r, const kcMulMatNormNode& n, kcMulMatPlan& plan) {
+    if (!n.x || !n.w || !n.y || (n.a != nullptr) != (n.b != nullptr)) return bad("norm: null x, w or y, or one of a / b");
+    if (n.n <= 0 || n.n % 256 || n.rows <= 0 || (long long)n.n * n.rows >= (1 << 24))
+        return bad("norm: n must be a positive multiple of 256, rows positive, n * rows < 2^24");
+    const bool k256 = batchK256(r, n.rows);
+    plan.k256 = k256;
+    // per 256: the rows' slots, then the per-32 partial sums of squares; per 32: in the slots' tails
+    const size_t off = k256 ? size_t(n.rows) * slotInts(n.n, true) : 0;
+    int* qk = nullptr;
+    if (E e = registeredSlots(r, n.y, n.n, n.rows, k256, k256 ? size_t(n.rows) * slotInts(n.n, false) : 0, &qk); e != ok)
+        return e;
+    int* q = qk + off;
+    if (n.a) {
+        const kcAddSumsqFArgs a{n.a, n.b, n.x, q, nullptr, n.n, n.rows};
+        name(plan.quantizer, "add_sumsq_f");
+        if (E e = launch(r, "add_sumsq_f", &a, plan); e != ok) return e;
+    } else {
+        const kcSumsqPartArgs a{n.x, q, nullptr, n.n, n.rows};
+        name(plan.quantizer, "sumsq_part");
+        if (E e = launch(r, "sumsq_part", &a, plan); e != ok) return e;
+    }
+    const kcNormMulQ8Args a{n.x, n.w, n.y, qk, nullptr, n.n, n.rows, n.eps};
+    const char* kernel = k256 ? "norm_mul_q8k_f" : "norm_mul_q8_f";
+    name(plan.kernel, kernel);
+    return launch(r, kernel, &a, plan);
+}
+
+E fusedSwiglu(kcMulMatRecording_st& r, const kcMulMatSwigluNode& n, kcMulMatPlan& plan) {
+    if (!n.g || !n.u || !n.y) return bad("swiglu: null g, u or y");
+    if (n.n <= 0 || n.n % 256 || n.cols <= 0 || (long long)n.n * n.cols >= (1 << 24))
+        return bad("swiglu: n must be a positive multiple of 256, cols positive, n * cols < 2^24");
+    const bool k256 = batchK256(r, n.cols);
+    plan.k256 = k256;
+    int* q = nullptr;
+    if (E e = registeredSlots(r, n.y, n.n, n.cols, k256, 0, &q); e != ok) return e;
+    const kcSiluMulQ8FArgs a{n.g, n.u, n.y, q, nullptr, n.n, n.cols};
+    const char* kernel = k256 ? "silu_mul_q8kf" : "silu_mul_q8x4f";
+    name(plan.kernel, kernel);
+    return launch(r, kernel, &a, plan);
+}
+
 E validate(const kcMulMatNode& n) {
     const bool f16 = n.wtype == KC_QTYPE_F16;
     if (!f16 && n.wtype != KC_QTYPE_Q4_K && n.wtype != KC_QTYPE_Q6_K)
@@ -140,8 +197,7 @@ E mulMat(kcMulMatRecording_st& r, const kcMulMatNode& n, kcMulMatPlan& plan) {
     }
     const bool q4 = n.wtype == KC_QTYPE_Q4_K;
     const bool contiguous = n.x_col_bytes == size_t(n.k) * sizeof(float);
-    // batch_k256: batches read activations scaled per 256 values unless matvec_cols or q8k = 0
-    const bool k256 = n.ncols > 1 && !r.cfg.matvec_cols && r.cfg.q8k && contiguous;
+    const bool k256 = batchK256(r, n.ncols) && contiguous;
     plan.k256 = k256;
     int* base = nullptr;
     if (E e = quantizedInput(r, n, k256, &base, plan); e != ok) return e;
@@ -222,6 +278,25 @@ KC_API kcError_t kcMulMat(kcMulMatRecording_t rec, const kcMulMatNode* node, kcM
     if (!node) return bad("null node");
     kcMulMatPlan p{};
     const E e = mulMat(*rec, *node, p);
+    if (plan) *plan = p;
+    return e;
+}
+
+KC_API kcError_t kcMulMatFusedNorm(kcMulMatRecording_t rec, const kcMulMatNormNode* node, kcMulMatPlan* plan) noexcept {
+    if (!rec) return kc::Error::InvalidResourceHandle;
+    if (!node) return bad("null node");
+    kcMulMatPlan p{};
+    const E e = fusedNorm(*rec, *node, p);
+    if (plan) *plan = p;
+    return e;
+}
+
+KC_API kcError_t kcMulMatFusedSwiglu(kcMulMatRecording_t rec, const kcMulMatSwigluNode* node,
+                                     kcMulMatPlan* plan) noexcept {
+    if (!rec) return kc::Error::InvalidResourceHandle;
+    if (!node) return bad("null node");
+    kcMulMatPlan p{};
+    const E e = fusedSwiglu(*rec, *node, p);
     if (plan) *plan = p;
     return e;
 }

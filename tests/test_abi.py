@@ -82,7 +82,7 @@ STRUCTS = ["VectorAddArgs", "QuantizeArgs", "MatvecQ4Q8Args", "MatmulKQ8Args", "
            "SiluMulQ8FArgs",
            "SiluMulArgs", "SetRowsF16Args", "FaDims", "FaScoresArgs", "FaMaxArgs", "FaExpArgs", "FaValuesArgs",
            "KquantRepackArgs", "GetRowsKquantArgs", "QuantizeKquantArgs", "FillNormalArgs", "FlashAttnArgs", "DeviceProperties",
-           "MulMatConfig", "MulMatNode", "MulMatPlan"]
+           "MulMatConfig", "MulMatNode", "MulMatPlan", "MulMatNormNode", "MulMatSwigluNode"]
 
 
 def test_struct_layouts_match_the_c_header(tmp_path):

@@ -13,7 +13,11 @@ the input reuse) and its output against the oracle on the same inputs:
   - strided input columns (no per-256 slots): one quantize_q8x4 per column, then the per-32 matmul;
   - F16 weights: matmul_f16 on the f32 columns (the oracle's matmul_f16, 1e-3);
   - two matrices reading one input quantize it once per recording; a reset or a scratch growth
-    makes the next one quantize again."""
+    makes the next one quantize again;
+  - the fused producers (fused_norm :502-530, fused_swiglu :533-545): [ADD +] RMS_NORM + MUL and
+    SWIGLU write their f32 output (the norm bit-exact against the oracle's fused restatement, SwiGLU
+    within 2e-6: exp2 ulps) and its 8-bit slots, which the MUL_MAT reading that output then takes
+    without a quantizer -- its result bit-exact against the oracle on the same f32 values."""
 import sys
 
 import numpy as np
@@ -221,3 +225,85 @@ def test_scratch_growth_drops_the_cached_inputs():
     rec.close()
     small.free()
     big.free()
+
+
+@pytest.mark.parametrize("rows", [1, 6])
+@pytest.mark.parametrize("with_add", [False, True])
+def test_fused_norm_feeds_the_next_mul_mat(rows, with_add):
+    """[ADD +] RMS_NORM + MUL: one launch of the partial sums, one of the norm (per 256 values for a
+    batch, per 32 for one row); the q / k / v MUL_MATs after it reuse its slots."""
+    n = 1024
+    nb, nsb = n // 32, n // 256
+    a, b, w = kq.randn(n * rows, 101), kq.randn(n * rows, 102), kq.uniform(n, 103, 0.5, 1.5)
+    x0 = kq.randn(n * rows, 104)
+    ba, bb, bw = kc.Buffer.of(a), kc.Buffer.of(b), kc.Buffer.of(w)
+    bx = kc.Buffer.of(np.zeros(n * rows, np.float32) if with_add else x0)
+    by = kc.Buffer(n * rows * 4)
+    rec = kc.MulMatRecording()
+    plan = rec.fused_norm(bx.ptr, bw.ptr, by.ptr, n, rows, 1e-5, a=ba.ptr if with_add else None,
+                          b=bb.ptr if with_add else None)
+    k256 = rows > 1
+    assert plan == {"quantizer": "add_sumsq_f" if with_add else "sumsq_part", "input_reused": False,
+                    "kernel": "norm_mul_q8k_f" if k256 else "norm_mul_q8_f", "launches": 2, "k256": k256}
+    # the oracle's fused restatement of the same two steps
+    x = np.zeros(n * rows, np.float32)
+    sq = np.zeros(rows * nb * 11, np.int32)
+    if with_add:
+        O.kco_add_sumsq_f(a, b, x, sq, n, rows)
+    else:
+        x = x0.copy()
+        O.kco_sumsq_part(x, sq, n, rows)
+    y = np.zeros(n * rows, np.float32)
+    if k256:
+        qk = np.zeros(rows * nsb * 85, np.int32)
+        O.kco_norm_mul_q8k(x, w, y, qk, sq, n, rows, 1e-5)
+    else:
+        O.kco_norm_mul_q8(x, w, y, sq, n, rows, 1e-5)
+    kc.synchronize()
+    assert np.array_equal(kq.bits(bx.download(np.float32)), kq.bits(x))
+    assert np.array_equal(kq.bits(by.download(np.float32)), kq.bits(y))
+    # q (Q4_K 96 rows) and v (Q6_K 32 rows) read y: no quantizer, the norm's slots
+    for qt, r in (("q4k", 96), ("q6k", 32)):
+        c = Case(qt, r, n, rows, 110 + r)
+        c.bx.free()
+        c.bx, c.cols = by, y.reshape(rows, n)
+        p = c.run(rec)
+        assert p["input_reused"] is True and p["quantizer"] == "" and p["launches"] == (1 if k256 else rows)
+        want = c.matmul_k_oracle() if k256 else c.matvec_oracle()
+        assert np.array_equal(kq.bits(c.y()), kq.bits(want))
+        c.bx = kc.Buffer(4)
+        c.free()
+    rec.close()
+    for buf in (ba, bb, bw, bx, by):
+        buf.free()
+
+
+@pytest.mark.parametrize("cols", [1, 5])
+def test_fused_swiglu_feeds_the_down_projection(cols):
+    n = 2048
+    g, u = kq.randn(n * cols, 120, 3.0), kq.randn(n * cols, 121)
+    bg, bu, by = kc.Buffer.of(g), kc.Buffer.of(u), kc.Buffer(n * cols * 4)
+    rec = kc.MulMatRecording()
+    plan = rec.fused_swiglu(bg.ptr, bu.ptr, by.ptr, n, cols)
+    k256 = cols > 1
+    assert plan == {"quantizer": "", "input_reused": False, "kernel": "silu_mul_q8kf" if k256 else "silu_mul_q8x4f",
+                    "launches": 1, "k256": k256}
+    want_y = np.zeros(n * cols, np.float32)
+    O.kco_silu_mul(g, u, want_y, n * cols)
+    kc.synchronize()
+    y = by.download(np.float32)
+    # silu's exp2 on the GPU and on the host differ in the last ulps (the layer tests' bar); the down
+    # projection below reads the GPU's own y, so its check stays bit-exact
+    assert np.allclose(y, want_y, rtol=2e-6, atol=1e-30)
+    c = Case("q6k", 64, n, cols, 130)  # down (Q6_K) reads y
+    c.bx.free()
+    c.bx, c.cols = by, y.reshape(cols, n)
+    p = c.run(rec)
+    assert p["input_reused"] is True and p["quantizer"] == ""
+    want = c.matmul_k_oracle() if k256 else c.matvec_oracle()
+    assert np.array_equal(kq.bits(c.y()), kq.bits(want))
+    c.bx = kc.Buffer(4)
+    c.free()
+    rec.close()
+    for buf in (bg, bu, by):
+        buf.free()

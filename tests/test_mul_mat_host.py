@@ -57,3 +57,23 @@ def test_refused_nodes(node, why):
         rec.mul_mat(a["wtype"], a["w"], a["rows"], a["k"], a["x"], a["ncols"], a["y"], x_col_bytes=a["x_col_bytes"])
     assert e.value.name == "InvalidValue" and why in str(e.value), str(e.value)
     rec.close()
+
+
+@pytest.mark.parametrize("kind,args,why", [
+    ("norm", dict(n=300), "multiple of 256"), ("norm", dict(rows=0), "rows positive"),
+    ("norm", dict(n=4096, rows=4096), "2^24"), ("norm", dict(x=None), "null"), ("norm", dict(a=DUMMY), "one of a / b"),
+    ("swiglu", dict(n=100), "multiple of 256"), ("swiglu", dict(cols=0), "cols positive"), ("swiglu", dict(u=None), "null"),
+])
+def test_refused_fused_producers(kind, args, why):
+    rec = kc.MulMatRecording()
+    with pytest.raises(kc.KcError) as e:
+        if kind == "norm":
+            a = dict(x=DUMMY, w=DUMMY, y=DUMMY, n=1024, rows=2, eps=1e-5, a=None, b=None)
+            a.update(args)
+            rec.fused_norm(a["x"], a["w"], a["y"], a["n"], a["rows"], a["eps"], a=a["a"], b=a["b"])
+        else:
+            a = dict(g=DUMMY, u=DUMMY, y=DUMMY, n=1024, cols=2)
+            a.update(args)
+            rec.fused_swiglu(a["g"], a["u"], a["y"], a["n"], a["cols"])
+    assert e.value.name == "InvalidValue" and why in str(e.value), str(e.value)
+    rec.close()
