@@ -21,7 +21,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB_PATH = os.path.join(HERE, "libkernelcore_amd.so")
 HEADERS = [os.path.join(ROOT, "include", "kernelcore", n) for n in ("kc.h", "llm_kernels.h", "model.h", "gguf.h",
-                                                                                   "mul_mat.h")]
+                                                                                   "mul_mat.h", "weights.h")]
 
 ERRORS = ["Success", "NotInitialized", "InvalidValue", "InvalidDevice", "OutOfMemory", "InvalidPointer",
           "InvalidResourceHandle", "UnsupportedOperation", "InvalidKernelImage", "KernelNotFound",
@@ -171,6 +171,9 @@ def lib():
         L.kcMulMatRecordingReset.argtypes = [_p]
         L.kcMulMatRecordingDestroy.argtypes = [_p]
         L.kcMulMat.argtypes = [_p, C.POINTER(MulMatNode), C.POINTER(MulMatPlan)]
+        L.kcWeightAllocSize.argtypes = [_i, _i, _i, C.POINTER(C.c_size_t)]
+        L.kcWeightSetTensor.argtypes = [_i, _i, _i, _p, _p, C.c_size_t, C.c_size_t, _p]
+        L.kcWeightGetTensor.argtypes = [_i, _i, _i, _p, _p, C.c_size_t, C.c_size_t, _p]
         L.kcMulMatFusedNorm.argtypes = [_p, C.POINTER(MulMatNormNode), C.POINTER(MulMatPlan)]
         L.kcMulMatFusedSwiglu.argtypes = [_p, C.POINTER(MulMatSwigluNode), C.POINTER(MulMatPlan)]
         L.kcGetErrorString.argtypes = [_i]
@@ -290,6 +293,29 @@ def plan_decode(**cfg):
     fused = _i()
     call("kcModelPlanDecode", C.byref(c), C.byref(fused))
     return fused.value
+
+
+WEIGHT_TYPES = {"f32": 0, "f16": 1, "q4k": 12, "q6k": 14}
+
+
+def weight_alloc_size(qtype, rows, k):
+    """kcWeightAllocSize (host only): device bytes of a rows x k weight of qtype."""
+    n = C.c_size_t()
+    call("kcWeightAllocSize", WEIGHT_TYPES.get(qtype, qtype), rows, k, C.byref(n))
+    return n.value
+
+
+def weight_set(qtype, rows, k, dst, data, offset=0, stream=None):
+    """kcWeightSetTensor: host bytes (a numpy array) at `offset` of the tensor's ggml form into dst."""
+    a = np.ascontiguousarray(data)
+    call("kcWeightSetTensor", WEIGHT_TYPES.get(qtype, qtype), rows, k, dst, a.ctypes.data, offset, a.nbytes, stream)
+
+
+def weight_get(qtype, rows, k, src, offset, size, stream=None):
+    """kcWeightGetTensor: bytes [offset, offset + size) of the tensor's ggml form (uint8 array)."""
+    out = np.zeros(size, np.uint8)
+    call("kcWeightGetTensor", WEIGHT_TYPES.get(qtype, qtype), rows, k, src, out.ctypes.data, offset, size, stream)
+    return out
 
 
 class MulMatConfig(C.Structure):
