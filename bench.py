@@ -431,6 +431,8 @@ def main():
     ap.add_argument("--skip-cfg5", action="store_true", help="skip the config-5 (Qwen3-8B shape) model leg")
     ap.add_argument("--eager-decode", action="store_true",
                     help="decode with one kcModelForward per token instead of the replayed graph")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="time config 1 by eager launches only (no graph capture: for kernel traces)")
     ap.add_argument("--only-model", action="store_true",
                     help="run only the config-3 matmul and the model legs (profiling); prints their JSON")
     args = ap.parse_args()
@@ -476,7 +478,7 @@ def main():
     r1 = r1l = None
     if not args.skip_cfg1:
         r1 = matvec_run("q4k", rows1, k1, copies=copies1, steps=max(args.steps, copies1), warmup=args.warmup,
-                        seed=5000, reps=reps, graph=True)
+                        seed=5000, reps=reps, graph=not args.no_graph)
         note(f"# cfg1 done: kernel {r1['kernel_ms'] * 1e3:.2f} us")
         # The Q4_K kernel at a streaming size: config 2's shape (128256 x 3072) as Q4_K, 2 rotating
         # copies (369 MB > the 256 MB Infinity Cache).
@@ -502,6 +504,8 @@ def main():
     }
     if r1:
         b1 = bytes_cfg1(rows1, k1)
+        if "graph_kernel_ms" not in r1:
+            r1["graph_kernel_ms"] = r1["graph_floor_ms"] = float("nan")
         a1 = b1 / (r1["graph_kernel_ms"] * 1e-3) / 1e9
         out["q4k_matvec_cfg1"] = {
             "achieved_gbs": round(a1, 1), "frac": round(a1 / PEAK_HBM_GBS, 4),
