@@ -19,6 +19,8 @@
 // bit for bit; the split softmax changes only the attention's rounding.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include <algorithm>
 
 #include <cstdint>
@@ -475,7 +477,7 @@ __device__ __forceinline__ void dmvItems(const DmvArgs& a, int part, const Act& 
 
 // N8: the norm prologue with 8 lanes per block of 32 (stageNorm8, at most two passes of the
 // workgroup), else one thread per block (stageNorm).
-template <int PRO, int EPI, bool N8>
+template <int PRO, int EPI, bool N8, int PRE = 0>
 __global__ __launch_bounds__(EPI == kEpiSwiglu ? 768 : 512) void dmv_kernel(DmvArgs a) {
     extern __shared__ int4 lds4[];
     int* lds = reinterpret_cast<int*>(lds4);
@@ -522,25 +524,30 @@ __global__ __launch_bounds__(EPI == kEpiSwiglu ? 768 : 512) void dmv_kernel(DmvA
     Pieces<true, true> f6;
     Pieces<false, true> f4;
     bool first_live = false;
-    auto loadFirst = [&]() {
-        const Slot s0 = slotOf<EPI>(a, part, wave % ns);
-        first_live = s0.live;
-        const int seg = q6 ? kQ6kSeg : kQ4kSeg, nsl = q6 ? kQ6kSlabs : kQ4kSlabs;
-        const uint8_t* p0 = s0.qw + ((size_t)(s0.live ? s0.tile : 0) * a.ngroups + wave / ns) * seg;
+    // slabs [LO, HI) of the first item (SwiGLU: PRE of them before the staging, the rest after)
+    const Slot s0 = slotOf<EPI>(a, part, wave % ns);
+    const int seg = q6 ? kQ6kSeg : kQ4kSeg, nsl = q6 ? kQ6kSlabs : kQ4kSlabs;
+    const uint8_t* p0 = s0.qw + ((size_t)(s0.live ? s0.tile : 0) * a.ngroups + wave / ns) * seg;
+    first_live = s0.live;
+    auto loadFirst = [&](auto lo, auto hi) {
 #pragma unroll
-        for (int i = 0; i < kQ6kSlabs; ++i)
+        for (int i = decltype(lo)::value; i < decltype(hi)::value; ++i)
             f6.c[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p0 + min(i, nsl - 1) * 1024 + lane * 16));
-        f6.dbits = *reinterpret_cast<const uint16_t*>(p0 + (q6 ? kQ6kSlabs * 1024 + lane * 2 : 0));
-#pragma unroll
-        for (int i = 0; i < kQ4kSlabs; ++i) f4.c[i] = f6.c[i];
+        if constexpr (decltype(hi)::value == kQ6kSlabs)
+            f6.dbits = *reinterpret_cast<const uint16_t*>(p0 + (q6 ? kQ6kSlabs * 1024 + lane * 2 : 0));
     };
-    if constexpr (EPI != kEpiSwiglu) loadFirst();
+    using Lo = std::integral_constant<int, 0>;
+    using Pre = std::integral_constant<int, (EPI == kEpiSwiglu ? PRE : kQ6kSlabs)>;
+    using Hi = std::integral_constant<int, kQ6kSlabs>;
+    loadFirst(Lo{}, Pre{});
     __builtin_amdgcn_sched_barrier(0);
     if (PRO == kProNorm && N8) stageNorm8(A, extra, nr8, a.k, a.eps, nsbp);
     else if (PRO == kProNorm) stageNorm(A, extra, nr, a.k, a.eps, nsbp);
     else stageSlot(A, extra, st, a.k / 256, nsbp);
     __syncthreads();
-    if constexpr (EPI == kEpiSwiglu) loadFirst();
+    if constexpr (EPI == kEpiSwiglu) loadFirst(Pre{}, Hi{});
+#pragma unroll
+    for (int i = 0; i < kQ4kSlabs; ++i) f4.c[i] = f6.c[i];
     if (q6) dmvItems<true, EPI>(a, part, A, terms, ns, f6, first_live);
     else dmvItems<false, EPI>(a, part, A, terms, ns, f4, first_live);
     __syncthreads();
@@ -1069,6 +1076,19 @@ int launchDecodeMatvec(int pro, int epi, DmvArgs a, hipStream_t s) {
         hipLaunchKernelGGL((dmv_kernel<P, Q, P == kProNorm && Q == kEpiSwiglu>), grid, block, lds, s, a);     \
     if (pro == P && epi == Q && n8 && P == kProNorm && Q != kEpiSwiglu)                                        \
         hipLaunchKernelGGL((dmv_kernel<P, Q, true>), grid, block, lds, s, a);
+    // The SwiGLU workgroups issue 9 of the 13 slab loads of each wavefront's weights before the
+    // activations are staged and the rest after (config 4 decode, measured: 812 tok/s with all
+    // after, 819 with 3 or 6 before, 821 with 9, 803 with all 13: their 28 MB in flight then delay
+    // the activation loads). Option "swiglu_pre": 1-13 that many before, 14 none.
+    const int po = option("swiglu_pre");
+    const int pre = epi != kEpiSwiglu ? 0 : (po == 0 ? 9 : (po >= 14 ? 0 : po));
+    if (pre > 0 && pro == kProNorm && epi == kEpiSwiglu && n8) {
+        if (pre <= 3) hipLaunchKernelGGL((dmv_kernel<kProNorm, kEpiSwiglu, true, 3>), grid, block, lds, s, a);
+        else if (pre <= 6) hipLaunchKernelGGL((dmv_kernel<kProNorm, kEpiSwiglu, true, 6>), grid, block, lds, s, a);
+        else if (pre <= 9) hipLaunchKernelGGL((dmv_kernel<kProNorm, kEpiSwiglu, true, 9>), grid, block, lds, s, a);
+        else hipLaunchKernelGGL((dmv_kernel<kProNorm, kEpiSwiglu, true, 13>), grid, block, lds, s, a);
+        return fromHip(hipGetLastError(), "decode matvec");
+    }
     KC_DMV(kProSlot, kEpiStore)
     KC_DMV(kProSlot, kEpiResid)
     KC_DMV(kProNorm, kEpiStore)
