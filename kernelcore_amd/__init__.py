@@ -21,7 +21,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB_PATH = os.path.join(HERE, "libkernelcore_amd.so")
 HEADERS = [os.path.join(ROOT, "include", "kernelcore", n) for n in ("kc.h", "llm_kernels.h", "model.h", "gguf.h",
-                                                                                   "mul_mat.h", "weights.h")]
+                                                                                   "mul_mat.h", "weights.h",
+                                                                                   "ggml_backend.h")]
 
 ERRORS = ["Success", "NotInitialized", "InvalidValue", "InvalidDevice", "OutOfMemory", "InvalidPointer",
           "InvalidResourceHandle", "UnsupportedOperation", "InvalidKernelImage", "KernelNotFound",
@@ -176,6 +177,16 @@ def lib():
         L.kcWeightGetTensor.argtypes = [_i, _i, _i, _p, _p, C.c_size_t, C.c_size_t, _p]
         L.kcMulMatFusedNorm.argtypes = [_p, C.POINTER(MulMatNormNode), C.POINTER(MulMatPlan)]
         L.kcMulMatFusedSwiglu.argtypes = [_p, C.POINTER(MulMatSwigluNode), C.POINTER(MulMatPlan)]
+        L.kcGgmlConfigFromEnv.argtypes = [C.POINTER(GgmlConfig)]
+        L.kcGgmlConfigFromEnv.restype = None
+        L.kcGgmlSupportsOp.argtypes = [C.POINTER(GgmlConfig), C.POINTER(GgmlTensor)]
+        L.kcGgmlOffersKvBuffer.argtypes = [C.POINTER(GgmlConfig)]
+        L.kcGgmlGraphPlan.argtypes = [C.POINTER(GgmlConfig), _p, _i, C.c_char_p, C.c_size_t, C.POINTER(C.c_size_t),
+                                      C.POINTER(C.c_size_t)]
+        L.kcGgmlBackendCreate.argtypes = [C.POINTER(_p), C.POINTER(GgmlConfig), _p]
+        L.kcGgmlBackendDestroy.argtypes = [_p]
+        L.kcGgmlGraphCompute.argtypes = [_p, _p, _i]
+        L.kcGgmlBackendGetStats.argtypes = [_p, C.POINTER(GgmlStats)]
         L.kcGetErrorString.argtypes = [_i]
         L.kcCodegenName.argtypes = [_i]
         _LIB = L
@@ -396,6 +407,104 @@ class MulMatRecording:
     def close(self):
         if self.h:
             call("kcMulMatRecordingDestroy", self.h)
+            self.h = None
+
+
+# ---- the ggml backend core (include/kernelcore/ggml_backend.h) --------------------------------------
+
+GGML_OP = {"none": 0, "reshape": 1, "view": 2, "permute": 3, "transpose": 4, "mul_mat": 5, "add": 6, "rms_norm": 7,
+           "mul": 8, "rope": 9, "glu": 10, "set_rows": 11, "flash_attn_ext": 12, "other": 13}
+GGML_TYPE = {"f32": 0, "f16": 1, "q4k": 12, "q6k": 14, "i32": 26, "i64": 27}
+GGML_BUFFER = {"other": 0, "weights": 1, "kv": 2}
+
+
+class GgmlTensor(C.Structure):
+    """kcGgmlTensor: one ggml tensor as the backend core reads it."""
+
+
+GgmlTensor._fields_ = [("op", _i), ("type", _i), ("ne", C.c_int64 * 4), ("nb", C.c_size_t * 4), ("data", _p),
+                       ("src", C.POINTER(GgmlTensor) * 5), ("op_params", C.c_int32 * 16), ("buffer", _i),
+                       ("compute", _i), ("output", _i), ("view", _i), ("uses", _i)]
+
+
+class GgmlConfig(C.Structure):
+    """kcGgmlConfig: the backend's switches."""
+    _fields_ = [("mul_mat", MulMatConfig), ("disabled", _i), ("matmul_only", _i), ("attn", _i), ("attn_tokens", _i),
+                ("concurrent", _i), ("graphs", _i)]
+
+
+class GgmlStats(C.Structure):
+    """kcGgmlStats: what a backend's graph_compute calls did."""
+    _fields_ = [("computes", C.c_longlong), ("graphs_recorded", C.c_longlong), ("graphs_reused", C.c_longlong),
+                ("launches", C.c_longlong)]
+
+
+_MM_KEYS = ("matvec_cols", "q8k", "tile", "row_block")
+
+
+def ggml_config(**over):
+    """kcGgmlConfigFromEnv (host only) with the given switches overridden: a GgmlConfig."""
+    c = GgmlConfig()
+    lib().kcGgmlConfigFromEnv(C.byref(c))
+    for k, v in over.items():
+        if k in _MM_KEYS:
+            setattr(c.mul_mat, k, int(v))
+        else:
+            setattr(c, k, int(v))
+    return c
+
+
+def ggml_config_dict(c):
+    d = {k: getattr(c.mul_mat, k) for k in _MM_KEYS}
+    d.update({k: getattr(c, k) for k, _ in GgmlConfig._fields_[1:]})
+    return d
+
+
+def _node_array(nodes):
+    arr = (C.POINTER(GgmlTensor) * max(1, len(nodes)))(*[C.pointer(t) for t in nodes])
+    return arr
+
+
+def ggml_supports_op(t, **cfg):
+    """kcGgmlSupportsOp: whether the backend claims t (host logic only)."""
+    return bool(lib().kcGgmlSupportsOp(C.byref(ggml_config(**cfg)), C.byref(t)))
+
+
+def ggml_offers_kv_buffer(**cfg):
+    return bool(lib().kcGgmlOffersKvBuffer(C.byref(ggml_config(**cfg))))
+
+
+def ggml_graph_plan(nodes, **cfg):
+    """kcGgmlGraphPlan: the launch names graph_compute would make for nodes, and its scratch ints
+    (no device needed)."""
+    arr = _node_array(nodes)
+    need, ints = C.c_size_t(), C.c_size_t()
+    c = ggml_config(**cfg)
+    call("kcGgmlGraphPlan", C.byref(c), arr, len(nodes), None, 0, C.byref(need), C.byref(ints))
+    buf = C.create_string_buffer(need.value)
+    call("kcGgmlGraphPlan", C.byref(c), arr, len(nodes), buf, need.value, None, None)
+    return buf.value.decode().split(), ints.value
+
+
+class GgmlBackend:
+    """A kcGgmlBackend: graph_compute over descriptor lists on one stream."""
+
+    def __init__(self, stream=None, **cfg):
+        h = _p()
+        call("kcGgmlBackendCreate", C.byref(h), C.byref(ggml_config(**cfg)), stream)
+        self.h = h
+
+    def compute(self, nodes):
+        call("kcGgmlGraphCompute", self.h, _node_array(nodes), len(nodes))
+
+    def stats(self):
+        s = GgmlStats()
+        call("kcGgmlBackendGetStats", self.h, C.byref(s))
+        return {k: getattr(s, k) for k, _ in GgmlStats._fields_}
+
+    def close(self):
+        if self.h:
+            call("kcGgmlBackendDestroy", self.h)
             self.h = None
 
 

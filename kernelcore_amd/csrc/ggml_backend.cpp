@@ -1,0 +1,734 @@
+// ggml_backend.cpp -- the compute side of the reference's ggml backend over kcGgmlTensor
+// descriptors (integrations/llama.cpp/ggml/src/ggml-kernelcore/ggml-kernelcore.cpp):
+//   - kcGgmlSupportsOp restates dev_supports_op_impl (:902-957) with weight_shape_ok (:103-109),
+//     in_kv_buffer / f16_rows / flash_attn_ok (:865-891);
+//   - kcGgmlGraphCompute restates backend_graph_compute (:706-792) -- the node walk and its fusion
+//     patterns -- and the op launchers rms_norm / mul / add / rope / swiglu / set_rows / flash_attn
+//     (:597-699), over the MUL_MAT recording of mul_mat.cpp (mul_mat_impl, quantized_input,
+//     fused_norm, fused_swiglu), on a HIP stream.
+// The rules and the kernels each op launches are the reference's (they are the backend's
+// behaviour); the recording is this device's: a planning pass sizes the scratch and names the
+// launches first, then the launches are made eagerly or captured once into a HIP graph that later
+// calls with the same nodes launch again.
+//
+// ggml's own helpers that the reference calls (ggml_is_contiguous, ggml_nrows, ggml_nelements,
+// ggml_are_same_shape, ggml_is_empty, ggml_can_fuse) belong to ggml, which the reference tree does
+// not hold; they are restated below from their definitions in ggml (ggml.c: ggml_is_contiguous_n;
+// ggml-impl.h: ggml_can_fuse_ext, ggml_node_has_n_uses).
+#include <algorithm>
+#include <climits>
+#include <cmath>
+#include <cstdint>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <new>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "internal.hpp"
+#include "kernelcore/ggml_backend.h"
+#include "kernelcore/llm_kernels.h"
+#include "mul_mat_internal.hpp"
+
+using T = kcGgmlTensor;
+
+struct kcGgmlBackend_st {
+    kcGgmlConfig cfg{};
+    kcStream_t stream = nullptr;
+    kcMulMatRecording_st rec;
+    std::map<int, float*> ones;  // device float[n] of 1.0f: rms_norm without a weight, rope without factors
+    kcGraph_t graph = nullptr;   // the kept graph, the signature of its nodes, the scratch it points into
+    std::vector<uint64_t> sig;
+    unsigned graph_gen = 0;
+    long long graph_launches = 0;
+    kcGgmlStats stats{};
+};
+
+namespace {
+
+using E = kcError_t;
+constexpr E ok = kc::Error::Success;
+
+E bad(const char* why) {
+    kcamd::setDetail("ggml backend: %s", why);
+    return kc::Error::InvalidValue;
+}
+
+// ---- ggml's tensor predicates ----------------------------------------------------------------
+
+// Bytes per block and values per block of the types the rules meet; 0 bytes for any other type.
+size_t typeSize(int type, int64_t* blck) {
+    *blck = 1;
+    switch (type) {
+        case KC_GGML_TYPE_F32: return 4;
+        case KC_GGML_TYPE_F16: return 2;
+        case KC_GGML_TYPE_I32: return 4;
+        case KC_GGML_TYPE_I64: return 8;
+        case KC_GGML_TYPE_Q4_K: *blck = 256; return 144;
+        case KC_GGML_TYPE_Q6_K: *blck = 256; return 210;
+        default: return 0;
+    }
+}
+
+// ggml_is_contiguous: elements packed in each row, then every dimension of more than one element
+// packed after the previous ones (dimensions of one element take any stride).
+bool contiguous(const T* t) {
+    int64_t blck = 1;
+    size_t next = typeSize(t->type, &blck);
+    if (!next) return false;
+    if (t->ne[0] != blck && t->nb[0] != next) return false;
+    next *= size_t(t->ne[0] / blck);
+    for (int i = 1; i < 4; ++i)
+        if (t->ne[i] != 1) {
+            if (t->nb[i] != next) return false;
+            next *= size_t(t->ne[i]);
+        }
+    return true;
+}
+
+int64_t nrows(const T* t) { return t->ne[1] * t->ne[2] * t->ne[3]; }
+int64_t nelements(const T* t) { return t->ne[0] * nrows(t); }
+bool sameShape(const T* a, const T* b) {
+    for (int i = 0; i < 4; ++i)
+        if (a->ne[i] != b->ne[i]) return false;
+    return true;
+}
+bool empty(const T* t) {
+    for (int i = 0; i < 4; ++i)
+        if (t->ne[i] == 0) return true;
+    return false;
+}
+float paramF32(const T* t, int i) {
+    float v;
+    std::memcpy(&v, &t->op_params[i], sizeof v);
+    return v;
+}
+bool f32c(const T* t) { return t && t->type == KC_GGML_TYPE_F32 && contiguous(t); }
+// v is one contiguous f32 row as long as x's rows (a norm weight)
+bool rowVectorOf(const T* v, const T* x) {
+    return v && v->type == KC_GGML_TYPE_F32 && contiguous(v) && v->ne[0] == x->ne[0] && nrows(v) == 1;
+}
+
+// ggml_can_fuse: nodes[i..i+n) carry ops[0..n) in order; each but the last has exactly one use and
+// is neither a view nor a graph output; each after the first reads the one before it and has its
+// shape.
+bool canFuse(const T* const* nodes, int n_nodes, int i, const int* ops, int n) {
+    for (int j = 0; j < n; ++j) {
+        if (i + j >= n_nodes) return false;
+        const T* node = nodes[i + j];
+        if (node->op != ops[j]) return false;
+        if (j < n - 1 && (node->uses != 1 || node->view || node->output)) return false;
+        if (j > 0) {
+            const T* prev = nodes[i + j - 1];
+            if (node->src[0] != prev && node->src[1] != prev) return false;
+            if (!sameShape(node, prev)) return false;
+        }
+    }
+    return true;
+}
+
+// ---- supports_op -----------------------------------------------------------------------------
+
+bool weightShapeOk(const T* w) {  // K-quants (super-blocks of 256) and fp16, in 8-row groups
+    const bool kq = (w->type == KC_GGML_TYPE_Q4_K || w->type == KC_GGML_TYPE_Q6_K) && w->ne[0] % 256 == 0;
+    const bool f16 = w->type == KC_GGML_TYPE_F16 && w->ne[0] % 2 == 0;
+    return (kq || f16) && w->ne[2] == 1 && w->ne[3] == 1 && w->ne[1] % 8 == 0 && w->ne[0] <= INT32_MAX &&
+           w->ne[1] <= INT32_MAX && contiguous(w);
+}
+
+bool inKv(const T* t) { return t->buffer == KC_GGML_BUFFER_KV; }
+bool f16Rows(const T* t) {  // fp16, rows and heads at 32-bit word strides
+    return t->type == KC_GGML_TYPE_F16 && t->nb[0] == 2 && t->nb[1] % 4 == 0 && t->nb[2] % 4 == 0 && t->ne[3] == 1 &&
+           t->nb[1] / 4 <= INT32_MAX && t->nb[2] / 4 <= INT32_MAX;
+}
+
+// flash_attn_ok, and the size limits of the attention kernels (beyond them the reference's kernels
+// refuse the launch; here the op is not claimed, so the scheduler places it elsewhere).
+bool flashAttnOk(const kcGgmlConfig& c, const T* op) {
+    const T* q = op->src[0];
+    const T* k = op->src[1];
+    const T* v = op->src[2];
+    const T* mask = op->src[3];
+    if (!q || !k || !v) return false;
+    if (op->src[4] || q->ne[1] > c.attn_tokens) return false;  // no sinks
+    if (paramF32(op, 1) != 0.0f || paramF32(op, 2) != 0.0f) return false;  // no ALiBi, no softcap
+    if (!inKv(k) || !inKv(v) || !f16Rows(k) || !f16Rows(v)) return false;
+    const int64_t D = k->ne[0];
+    if (v->ne[0] != D || q->ne[0] != D || D % 8 || k->ne[1] != v->ne[1] || k->ne[2] != v->ne[2] || k->ne[2] <= 0 ||
+        q->ne[2] % k->ne[2] || q->ne[3] != 1 || k->ne[1] <= 0 || k->ne[1] > INT32_MAX)
+        return false;
+    if (q->type != KC_GGML_TYPE_F32 || q->nb[0] != 4 || q->nb[1] % 4 || q->nb[2] % 4) return false;
+    if (!f32c(op) || op->ne[0] != D || op->ne[1] != q->ne[2] || op->ne[2] != q->ne[1] || op->ne[3] != 1) return false;
+    if (mask && (mask->type != KC_GGML_TYPE_F16 || mask->nb[0] != 2 || mask->nb[1] % 4 || mask->ne[0] < k->ne[1] ||
+                 mask->ne[1] < q->ne[1] || mask->ne[2] != 1 || mask->ne[3] != 1))
+        return false;
+    const int64_t tp = (k->ne[1] + 7) / 8 * 8, rows = q->ne[2] * q->ne[1];
+    return rows * tp < (int64_t(1) << 24) && rows * D < (int64_t(1) << 24) && q->nb[2] / 4 >= uint64_t(D);
+}
+
+bool supports(const kcGgmlConfig& c, const T* op) {
+    if (!op || c.disabled) return false;
+    const T* s0 = op->src[0];
+    const T* s1 = op->src[1];
+    switch (op->op) {
+        case KC_GGML_OP_NONE:
+        case KC_GGML_OP_RESHAPE:
+        case KC_GGML_OP_VIEW:
+        case KC_GGML_OP_PERMUTE:
+        case KC_GGML_OP_TRANSPOSE:
+            return true;
+        case KC_GGML_OP_MUL_MAT:  // the weight in this backend's buffers (repacked), any batch size
+            return s0 && s1 && s0->buffer == KC_GGML_BUFFER_WEIGHTS && weightShapeOk(s0) && f32c(s1) &&
+                   s1->ne[0] == s0->ne[0] && f32c(op) && op->ne[0] == s0->ne[1] && nrows(op) == nrows(s1);
+        default:
+            break;
+    }
+    if (c.matmul_only) return false;
+    switch (op->op) {
+        case KC_GGML_OP_RMS_NORM:
+            return f32c(s0) && f32c(op) && sameShape(s0, op);
+        case KC_GGML_OP_ADD:
+            return f32c(s0) && f32c(s1) && f32c(op) && sameShape(s0, s1) && sameShape(s0, op);
+        case KC_GGML_OP_MUL:  // by a row vector (norm weight, n % 8 == 0) or elementwise
+            return f32c(s0) && f32c(s1) && f32c(op) && sameShape(s0, op) &&
+                   ((rowVectorOf(s1, s0) && s0->ne[0] % 8 == 0) || (sameShape(s0, s1) && nelements(s0) % 8 == 0));
+        case KC_GGML_OP_ROPE: {
+            const int32_t* p = op->op_params;
+            const T* ff = op->src[2];
+            return s0 && (p[2] == 0 /* NORM */ || p[2] == KC_GGML_ROPE_TYPE_NEOX) && p[1] == s0->ne[0] &&
+                   paramF32(op, 6) == 1.0f && paramF32(op, 7) == 0.0f && paramF32(op, 8) == 1.0f && p[15] == 0 &&
+                   f32c(s0) && f32c(op) && sameShape(s0, op) && s0->ne[0] % 16 == 0 && s0->ne[3] == 1 && s1 &&
+                   s1->type == KC_GGML_TYPE_I32 && contiguous(s1) && s1->ne[0] == s0->ne[2] &&
+                   (!ff || (f32c(ff) && ff->ne[0] >= s0->ne[0] / 2));
+        }
+        case KC_GGML_OP_SET_ROWS:  // into the fp16 KV cache
+            return c.attn && s0 && s1 && inKv(op) && op->type == KC_GGML_TYPE_F16 && op->nb[0] == 2 &&
+                   op->nb[1] % 4 == 0 && op->ne[2] == 1 && op->ne[3] == 1 && op->ne[1] <= INT32_MAX &&
+                   s0->type == KC_GGML_TYPE_F32 && s0->nb[0] == 4 && s0->nb[1] % 4 == 0 && s0->ne[0] == op->ne[0] &&
+                   s0->ne[0] % 16 == 0 && s0->ne[2] == 1 && s0->ne[3] == 1 && s1->type == KC_GGML_TYPE_I64 &&
+                   contiguous(s1) && s1->ne[0] == s0->ne[1] && s1->ne[1] == 1 && s1->ne[2] == 1 && s1->ne[3] == 1;
+        case KC_GGML_OP_FLASH_ATTN_EXT:
+            return c.attn && flashAttnOk(c, op);
+        case KC_GGML_OP_GLU:
+            return op->op_params[0] == KC_GGML_GLU_OP_SWIGLU && op->op_params[1] == 0 && f32c(s0) && f32c(s1) &&
+                   f32c(op) && sameShape(s0, s1) && sameShape(s0, op);
+        default:
+            return false;
+    }
+}
+
+// ---- the graph walk ---------------------------------------------------------------------------
+
+// One pass over a graph's nodes: a plan (dry recording, no backend) or the launches.
+struct Pass {
+    const kcGgmlConfig& cfg;
+    kcMulMatRecording_st& rec;
+    kcGgmlBackend_st* be;            // null in a plan
+    std::vector<int>* ones_wanted;   // a plan: the lengths of the 1.0f arrays the launches read
+    bool capturing;                  // launches recorded into a graph (MUL_MAT groups run concurrently)
+};
+
+const float* onesOf(Pass& p, int n) {
+    if (!p.be) {
+        p.ones_wanted->push_back(n);
+        return reinterpret_cast<const float*>(uintptr_t(256));  // a plan never dereferences it
+    }
+    const auto it = p.be->ones.find(n);
+    return it == p.be->ones.end() ? nullptr : it->second;
+}
+
+E launch(Pass& p, const char* kernel, const void* args) { return kcamd::mulmat::launch(p.rec, kernel, args); }
+
+E marker(Pass& p, const char* m) {
+    if (p.rec.trace) {
+        try {
+            p.rec.trace->push_back(m);
+        } catch (...) {
+            return kc::Error::OutOfMemory;
+        }
+    }
+    return ok;
+}
+
+const float* f32(const T* t) { return static_cast<const float*>(t->data); }
+float* f32w(const T* t) { return static_cast<float*>(t->data); }
+
+kcMulMatNode mulMatNode(const T* dst) {
+    const T* w = dst->src[0];
+    const T* x = dst->src[1];
+    return kcMulMatNode{w->type, w->data, int(w->ne[1]), int(w->ne[0]), f32(x), (long long)nrows(x), x->nb[1], f32w(dst)};
+}
+
+E mulMat(Pass& p, const T* dst) {
+    kcMulMatPlan plan{};
+    return kcamd::mulmat::mulMat(p.rec, mulMatNode(dst), plan);
+}
+
+E mulMatInput(Pass& p, const T* dst) {
+    kcMulMatPlan plan{};
+    return kcamd::mulmat::mulMatInput(p.rec, mulMatNode(dst), plan);
+}
+
+// RMS_NORM, with the weight of a following MUL when given (rms_norm, :597-606)
+E rmsNorm(Pass& p, const T* norm, const float* weight, const T* out) {
+    const T* x = norm->src[0];
+    const int n = int(x->ne[0]), rows = int(nrows(x));
+    const float* w = weight ? weight : onesOf(p, n);
+    if (!w) return kc::Error::InternalError;
+    const kcRmsNormArgs a{f32(x), w, f32w(out), n, rows, paramF32(norm, 0)};
+    return launch(p, "rms_norm", &a);
+}
+
+E mul(Pass& p, const T* dst) {  // by a row vector (broadcast) or elementwise (:612-619)
+    const T* a = dst->src[0];
+    const T* b = dst->src[1];
+    const int count = int(nelements(a));
+    const int n = rowVectorOf(b, a) ? int(a->ne[0]) : count;
+    const kcMulRowsArgs m{f32(a), f32(b), f32w(dst), n, count};
+    return launch(p, "mul_rows", &m);
+}
+
+E add(Pass& p, const T* dst) {  // :621-626
+    const kcVectorAddArgs a{f32(dst->src[0]), f32(dst->src[1]), f32w(dst), int(nelements(dst))};
+    return launch(p, "vector_add", &a);
+}
+
+E rope(Pass& p, const T* dst) {  // :628-639
+    const T* x = dst->src[0];
+    const int hd = int(x->ne[0]), nh = int(x->ne[1]), nt = int(x->ne[2]), pairs = hd / 2;
+    const float* ff = dst->src[2] ? f32(dst->src[2]) : onesOf(p, pairs);
+    if (!ff) return kc::Error::InternalError;
+    const bool neox = (dst->op_params[2] & KC_GGML_ROPE_TYPE_NEOX) != 0;
+    const kcRopeGgmlArgs a{f32(x), f32w(dst), static_cast<const int*>(dst->src[1]->data), ff, nullptr, hd, nh, nt,
+                           std::log2(paramF32(dst, 5)), neox};
+    return launch(p, "rope_ggml", &a);
+}
+
+E swiglu(Pass& p, const T* dst) {  // :641-646
+    const kcSiluMulArgs a{f32(dst->src[0]), f32(dst->src[1]), f32w(dst), int(nelements(dst))};
+    return launch(p, "silu_mul", &a);
+}
+
+// [ADD +] RMS_NORM + MUL, the result also quantized for the MUL_MATs that read it (:502-530).
+// Beyond the fused kernels' 2^24 values: the ADD and a weighted rms_norm.
+E fusedNorm(Pass& p, const T* addNode, const T* norm, const T* mulNode) {
+    const T* x = norm->src[0];
+    const int64_t n = x->ne[0], rows = nrows(x);
+    if (n * rows >= (int64_t(1) << 24)) {
+        if (addNode)
+            if (E e = add(p, addNode); e != ok) return e;
+        return rmsNorm(p, norm, f32(mulNode->src[1]), mulNode);
+    }
+    const kcMulMatNormNode nn{addNode ? f32(addNode->src[0]) : nullptr, addNode ? f32(addNode->src[1]) : nullptr,
+                              f32w(x), f32(mulNode->src[1]), f32w(mulNode), int(n), int(rows), paramF32(norm, 0)};
+    kcMulMatPlan plan{};
+    return kcamd::mulmat::fusedNorm(p.rec, nn, plan);
+}
+
+// SWIGLU with the result also quantized for the down projection (:533-545); n % 256 == 0.
+E fusedSwiglu(Pass& p, const T* dst) {
+    const int64_t n = dst->ne[0], cols = nrows(dst);
+    if (n * cols >= (int64_t(1) << 24)) return swiglu(p, dst);
+    const kcMulMatSwigluNode sn{f32(dst->src[0]), f32(dst->src[1]), f32w(dst), int(n), int(cols)};
+    kcMulMatPlan plan{};
+    return kcamd::mulmat::fusedSwiglu(p.rec, sn, plan);
+}
+
+E setRows(Pass& p, const T* dst) {  // dst rows src1[r] (int64) = fp16(src0 row r) (:650-661)
+    const T* src = dst->src[0];
+    const T* idx = dst->src[1];
+    const kcSetRowsF16Args a{f32(src), static_cast<const int*>(idx->data), static_cast<int*>(dst->data), nullptr,
+                             int(src->ne[0] / 2), int(src->ne[1]), int(src->nb[1] / 4), int(dst->nb[1] / 4),
+                             int(dst->ne[1])};
+    return launch(p, "set_rows_f16", &a);
+}
+
+// FLASH_ATTN_EXT (:663-699): the dimensions as the reference derives them; one flash_attn_f16
+// kernel, or for contexts beyond its 16384 the four fa_* kernels with their scores in the scratch.
+E flashAttn(Pass& p, const T* dst) {
+    const T* q = dst->src[0];
+    const T* k = dst->src[1];
+    const T* v = dst->src[2];
+    const T* mask = dst->src[3];
+    kcFaDims d{};
+    d.D = int(k->ne[0]);
+    d.T = int(k->ne[1]);
+    d.H_kv = int(k->ne[2]);
+    d.H = int(q->ne[2]);
+    d.N = int(q->ne[1]);
+    d.group = d.H / d.H_kv;
+    d.tp = (d.T + 7) / 8 * 8;
+    d.k_row = int(k->nb[1] / 4), d.k_head = int(k->nb[2] / 4);
+    d.v_row = int(v->nb[1] / 4), d.v_head = int(v->nb[2] / 4);
+    d.q_tok = int(q->nb[1] / 4), d.q_head = int(q->nb[2] / 4);
+    d.m_row = mask ? int(mask->nb[1] / 4) : 0;
+    d.has_mask = mask ? 1 : 0;
+    const float scale = paramF32(dst, 0);
+    const int* kd = static_cast<const int*>(k->data);
+    const int* vd = static_cast<const int*>(v->data);
+    const int* md = mask ? static_cast<const int*>(mask->data) : nullptr;
+    if (d.T <= 16384) {
+        const kcFlashAttnArgs a{f32(q), kd, vd, md, f32w(dst), nullptr, d, scale};
+        return launch(p, "flash_attn_f16", &a);
+    }
+    const size_t rows = size_t(d.H) * size_t(d.N);
+    int* sc = nullptr;
+    if (E e = kcamd::mulmat::take(p.rec, rows * size_t(d.tp) + rows, &sc); e != ok) return e;
+    float* s = reinterpret_cast<float*>(sc);
+    float* m = s + rows * size_t(d.tp);
+    const kcFaScoresArgs sa{f32(q), kd, md, s, nullptr, d, scale};
+    const kcFaMaxArgs ma{s, m, nullptr, d};
+    const kcFaExpArgs ea{s, m, nullptr, d};
+    const kcFaValuesArgs va{s, vd, f32w(dst), nullptr, d};
+    if (E e = launch(p, "fa_scores", &sa); e != ok) return e;
+    if (E e = launch(p, "fa_max", &ma); e != ok) return e;
+    if (E e = launch(p, "fa_exp", &ea); e != ok) return e;
+    return launch(p, "fa_values", &va);
+}
+
+E concurrent(Pass& p, bool begin) {
+    if (E e = marker(p, begin ? "[" : "]"); e != ok) return e;
+    if (p.rec.dry) return ok;
+    return begin ? kcStreamConcurrentBegin(p.rec.stream) : kcStreamConcurrentEnd(p.rec.stream);
+}
+
+bool computed(const T* t) { return t->compute && !empty(t); }
+
+// backend_graph_compute's walk (:712-788)
+E walk(Pass& p, const T* const* nodes, int n) {
+    static const int kNormMul[2] = {KC_GGML_OP_RMS_NORM, KC_GGML_OP_MUL};
+    for (int i = 0; i < n; ++i) {
+        const T* node = nodes[i];
+        // nothing to compute (e.g. a prompt's earlier batches select no output rows); fused
+        // partners of an empty node are empty too
+        if (!computed(node)) continue;
+        E e = ok;
+        switch (node->op) {
+            case KC_GGML_OP_MUL_MAT: {
+                // consecutive MUL_MATs of one input (q, k, v; gate, up) as one step
+                int g = 1;
+                while (p.cfg.concurrent && p.capturing && i + g < n && nodes[i + g]->op == KC_GGML_OP_MUL_MAT &&
+                       nodes[i + g]->src[1] == node->src[1] && computed(nodes[i + g]))
+                    ++g;
+                if (g == 1) {
+                    e = mulMat(p, node);
+                    break;
+                }
+                e = mulMatInput(p, node);  // the shared input quantized first (its own step)
+                if (e == ok) e = concurrent(p, true);
+                if (e != ok) break;
+                for (int j = 0; e == ok && j < g; ++j) e = mulMat(p, nodes[i + j]);
+                const E f = concurrent(p, false);
+                if (e == ok) e = f;
+                i += g - 1;
+                break;
+            }
+            case KC_GGML_OP_ADD:
+            case KC_GGML_OP_RMS_NORM: {
+                // [ADD +] RMS_NORM + MUL by a row vector (the norm weight): the fused producer
+                // (n % 256 == 0), else vector_add or a one-pass rms_norm
+                const int ni = node->op == KC_GGML_OP_ADD ? i + 1 : i;  // the RMS_NORM node
+                const T* norm = ni < n ? nodes[ni] : nullptr;
+                const T* mulNode = ni + 1 < n ? nodes[ni + 1] : nullptr;
+                const bool pattern = norm && mulNode && norm->op == KC_GGML_OP_RMS_NORM &&
+                                     canFuse(nodes, n, ni, kNormMul, 2) && mulNode->src[0] == norm &&
+                                     rowVectorOf(mulNode->src[1], norm) && norm->src[0]->ne[0] % 256 == 0 &&
+                                     contiguous(norm->src[0]) &&
+                                     (node->op == KC_GGML_OP_RMS_NORM || norm->src[0] == node);
+                if (pattern) {
+                    e = fusedNorm(p, node->op == KC_GGML_OP_ADD ? node : nullptr, norm, mulNode);
+                    i = ni + 1;
+                } else if (node->op == KC_GGML_OP_ADD) {
+                    e = add(p, node);
+                } else {
+                    const T* next = i + 1 < n ? nodes[i + 1] : nullptr;
+                    if (next && canFuse(nodes, n, i, kNormMul, 2) && next->src[0] == node &&
+                        rowVectorOf(next->src[1], node)) {
+                        e = rmsNorm(p, node, f32(next->src[1]), next);
+                        ++i;
+                    } else {
+                        e = rmsNorm(p, node, nullptr, node);
+                    }
+                }
+                break;
+            }
+            case KC_GGML_OP_MUL: e = mul(p, node); break;
+            case KC_GGML_OP_ROPE: e = rope(p, node); break;
+            case KC_GGML_OP_GLU: e = node->ne[0] % 256 == 0 ? fusedSwiglu(p, node) : swiglu(p, node); break;
+            case KC_GGML_OP_SET_ROWS: e = setRows(p, node); break;
+            case KC_GGML_OP_FLASH_ATTN_EXT: e = flashAttn(p, node); break;
+            case KC_GGML_OP_NONE:
+            case KC_GGML_OP_RESHAPE:
+            case KC_GGML_OP_VIEW:
+            case KC_GGML_OP_PERMUTE:
+            case KC_GGML_OP_TRANSPOSE:
+                break;
+            default:
+                kcamd::setDetail("ggml backend: node %d: op %d is not one this backend runs", i, node->op);
+                return kc::Error::UnsupportedOperation;
+        }
+        if (e != ok) return e;
+    }
+    return ok;
+}
+
+// Every node present, and every node with work one this backend claims (the scheduler only hands
+// it such nodes; anything else is refused before a launch).
+E checkNodes(const kcGgmlConfig& c, const T* const* nodes, int n) {
+    if (n < 0 || (n > 0 && !nodes)) return bad("null node list or negative count");
+    for (int i = 0; i < n; ++i) {
+        if (!nodes[i]) {
+            kcamd::setDetail("ggml backend: node %d is null", i);
+            return kc::Error::InvalidValue;
+        }
+        if (computed(nodes[i]) && !supports(c, nodes[i])) {
+            kcamd::setDetail("ggml backend: node %d (op %d) is not one this backend runs with these operands", i,
+                             nodes[i]->op);
+            return kc::Error::UnsupportedOperation;
+        }
+    }
+    return ok;
+}
+
+// A plan of the walk: its launch names, the scratch it takes and the 1.0f arrays it reads.
+struct Plan {
+    std::vector<const char*> trace;
+    std::vector<int> ones;
+    size_t scratch = 0;
+    long long launches = 0;
+};
+
+E plan(const kcGgmlConfig& c, const T* const* nodes, int n, Plan& out) {
+    if (E e = checkNodes(c, nodes, n); e != ok) return e;
+    kcMulMatRecording_st dry;
+    dry.cfg = c.mul_mat;
+    dry.dry = true;
+    dry.trace = &out.trace;
+    Pass p{c, dry, nullptr, &out.ones, c.graphs != 0};
+    if (E e = walk(p, nodes, n); e != ok) return e;
+    out.scratch = dry.peak;
+    for (const char* t : out.trace)
+        if (t[0] != '[' && t[0] != ']') ++out.launches;
+    return ok;
+}
+
+// The nodes as a graph would be recorded from them: every field a launch or a fusion decision reads,
+// src links as node indices (or, for tensors outside the list, their first-seen order and fields).
+void signature(const T* const* nodes, int n, std::vector<uint64_t>& s) {
+    std::unordered_map<const T*, int64_t> id;
+    for (int i = 0; i < n; ++i) id.emplace(nodes[i], i);
+    std::unordered_map<const T*, int64_t> leaf;
+    const auto put = [&s](const T* t) {
+        s.push_back(uint64_t(uint32_t(t->op)) | uint64_t(uint32_t(t->type)) << 32);
+        for (int d = 0; d < 4; ++d) s.push_back(uint64_t(t->ne[d]));
+        for (int d = 0; d < 4; ++d) s.push_back(uint64_t(t->nb[d]));
+        s.push_back(uint64_t(reinterpret_cast<uintptr_t>(t->data)));
+        for (int j = 0; j < 16; j += 2) s.push_back(uint64_t(uint32_t(t->op_params[j])) | uint64_t(uint32_t(t->op_params[j + 1])) << 32);
+        s.push_back(uint64_t(uint32_t(t->buffer)) | uint64_t(t->compute != 0) << 32 | uint64_t(t->output != 0) << 33 |
+                    uint64_t(t->view != 0) << 34);
+        s.push_back(uint64_t(uint32_t(t->uses)));
+    };
+    s.push_back(uint64_t(n));
+    for (int i = 0; i < n; ++i) {
+        put(nodes[i]);
+        for (const T* src : nodes[i]->src) {
+            if (!src) {
+                s.push_back(~uint64_t(0));
+                continue;
+            }
+            const auto it = id.find(src);
+            if (it != id.end()) {
+                s.push_back(uint64_t(it->second));
+                continue;
+            }
+            const auto [lt, fresh] = leaf.emplace(src, int64_t(leaf.size()));
+            s.push_back(uint64_t(1) << 62 | uint64_t(lt->second));
+            if (fresh) put(src);
+        }
+    }
+}
+
+E makeOnes(kcGgmlBackend_st& be, const std::vector<int>& lengths) {
+    for (const int n : lengths) {
+        if (n <= 0) return bad("a 1.0f array of no length");
+        if (be.ones.count(n)) continue;
+        void* d = nullptr;
+        if (E e = kcMalloc(&d, size_t(n) * sizeof(float)); e != ok) return e;
+        const std::vector<float> v(size_t(n), 1.0f);
+        if (E e = kcMemcpy(d, v.data(), v.size() * sizeof(float), kc::CopyKind::HostToDevice); e != ok) {
+            (void)kcFree(d);
+            return e;
+        }
+        be.ones.emplace(n, static_cast<float*>(d));
+    }
+    return ok;
+}
+
+void dropGraph(kcGgmlBackend_st& be) {
+    if (be.graph) (void)kcGraphDestroy(be.graph);
+    be.graph = nullptr;
+    be.sig.clear();
+}
+
+E compute(kcGgmlBackend_st& be, const T* const* nodes, int n) {
+    if (E e = checkNodes(be.cfg, nodes, n); e != ok) return e;
+    const bool graphs = be.cfg.graphs != 0;
+    std::vector<uint64_t> sig;
+    if (graphs) {
+        signature(nodes, n, sig);
+        if (be.graph && be.graph_gen == be.rec.gen && sig == be.sig) {  // the kept graph again
+            if (E e = kcGraphLaunch(be.graph, be.stream); e != ok) return e;
+            if (E e = kcStreamSynchronize(be.stream); e != ok) return e;
+            ++be.stats.computes;
+            ++be.stats.graphs_reused;
+            be.stats.launches += be.graph_launches;
+            return ok;
+        }
+    }
+    Plan pl;
+    if (E e = plan(be.cfg, nodes, n, pl); e != ok) return e;
+    if (E e = makeOnes(be, pl.ones); e != ok) return e;
+    kcamd::mulmat::reset(be.rec);
+    if (pl.scratch > be.rec.cap) {  // replaced before anything is recorded into it
+        dropGraph(be);
+        if (E e = kcamd::mulmat::reserve(be.rec, pl.scratch); e != ok) return e;
+    }
+    Pass p{be.cfg, be.rec, &be, nullptr, graphs};
+    if (!graphs) {
+        const E e = walk(p, nodes, n);
+        const E s = kcStreamSynchronize(be.stream);
+        if (e != ok) return e;
+        if (s != ok) return s;
+    } else {
+        dropGraph(be);
+        if (E e = kcStreamBeginCapture(be.stream); e != ok) return e;
+        const E e = walk(p, nodes, n);
+        kcGraph_t g = nullptr;
+        const E c = kcStreamEndCapture(be.stream, &g);
+        if (e != ok || c != ok) {
+            if (g) (void)kcGraphDestroy(g);
+            return e != ok ? e : c;
+        }
+        if (E l = kcGraphLaunch(g, be.stream); l != ok) {
+            (void)kcGraphDestroy(g);
+            return l;
+        }
+        be.graph = g;
+        be.sig = std::move(sig);
+        be.graph_gen = be.rec.gen;
+        be.graph_launches = pl.launches;
+        ++be.stats.graphs_recorded;
+        if (E s = kcStreamSynchronize(be.stream); s != ok) return s;
+    }
+    ++be.stats.computes;
+    be.stats.launches += pl.launches;
+    return ok;
+}
+
+kcGgmlConfig configOrEnv(const kcGgmlConfig* cfg) {
+    kcGgmlConfig c;
+    if (cfg) c = *cfg;
+    else kcGgmlConfigFromEnv(&c);
+    return c;
+}
+
+bool envIs(const char* name, const char* value) {
+    const char* v = std::getenv(name);
+    return v && std::strcmp(v, value) == 0;
+}
+
+}  // namespace
+
+KC_API void kcGgmlConfigFromEnv(kcGgmlConfig* cfg) noexcept {
+    if (!cfg) return;
+    kcMulMatConfigFromEnv(&cfg->mul_mat);
+    cfg->disabled = envIs("GGML_KERNELCORE_DISABLE", "1");
+    cfg->matmul_only = envIs("GGML_KERNELCORE_MATMUL_ONLY", "1");
+    cfg->attn = !envIs("GGML_KERNELCORE_ATTN", "0");
+    cfg->attn_tokens = 8;
+    if (const char* an = std::getenv("GGML_KERNELCORE_ATTN_TOKENS")) cfg->attn_tokens = std::max(0, std::atoi(an));
+    cfg->concurrent = !envIs("GGML_KERNELCORE_CONCURRENT", "0");
+    cfg->graphs = !envIs("GGML_KERNELCORE_GRAPHS", "0");
+}
+
+KC_API int kcGgmlSupportsOp(const kcGgmlConfig* cfg, const kcGgmlTensor* op) noexcept {
+    return supports(configOrEnv(cfg), op) ? 1 : 0;
+}
+
+KC_API int kcGgmlOffersKvBuffer(const kcGgmlConfig* cfg) noexcept {
+    const kcGgmlConfig c = configOrEnv(cfg);
+    return !c.disabled && !c.matmul_only && c.attn ? 1 : 0;
+}
+
+KC_API kcError_t kcGgmlGraphPlan(const kcGgmlConfig* cfg, const kcGgmlTensor* const* nodes, int n_nodes, char* names,
+                                 size_t size, size_t* needed, size_t* scratch_ints) noexcept {
+    try {
+        kcGgmlConfig c = configOrEnv(cfg);
+        if (E e = kcamd::mulmat::checkConfig(c.mul_mat); e != ok) return e;
+        Plan pl;
+        if (E e = plan(c, nodes, n_nodes, pl); e != ok) return e;
+        std::string s;
+        for (const char* t : pl.trace) {
+            if (!s.empty()) s += ' ';
+            s += t;
+        }
+        if (needed) *needed = s.size() + 1;
+        if (scratch_ints) *scratch_ints = pl.scratch;
+        if (names && size >= s.size() + 1) std::memcpy(names, s.c_str(), s.size() + 1);
+        else if (names && size) names[0] = '\0';
+        return ok;
+    } catch (...) {
+        return kc::Error::OutOfMemory;
+    }
+}
+
+KC_API kcError_t kcGgmlBackendCreate(kcGgmlBackend_t* backend, const kcGgmlConfig* cfg, kcStream_t stream) noexcept {
+    if (!backend) return bad("null backend pointer");
+    *backend = nullptr;
+    kcGgmlConfig c = configOrEnv(cfg);
+    if (E e = kcamd::mulmat::checkConfig(c.mul_mat); e != ok) return e;
+    if (c.disabled) {
+        kcamd::setDetail("ggml backend: disabled (GGML_KERNELCORE_DISABLE=1)");
+        return kc::Error::UnsupportedOperation;
+    }
+    int dev = 0;
+    if (E e = kcGetDevice(&dev); e != ok) return e;  // the runtime is up
+    auto* be = new (std::nothrow) kcGgmlBackend_st;
+    if (!be) return kc::Error::OutOfMemory;
+    be->cfg = c;
+    be->stream = stream;
+    be->rec.cfg = c.mul_mat;
+    be->rec.stream = stream;
+    *backend = be;
+    return ok;
+}
+
+KC_API kcError_t kcGgmlBackendDestroy(kcGgmlBackend_t backend) noexcept {
+    if (!backend) return ok;
+    E e = kcStreamSynchronize(backend->stream);  // nothing in flight reads what is freed below
+    dropGraph(*backend);
+    for (auto& [n, ptr] : backend->ones)
+        if (E f = kcFree(ptr); e == ok) e = f;
+    if (backend->rec.scratch)
+        if (E f = kcFree(backend->rec.scratch); e == ok) e = f;
+    delete backend;
+    return e;
+}
+
+KC_API kcError_t kcGgmlGraphCompute(kcGgmlBackend_t backend, const kcGgmlTensor* const* nodes, int n_nodes) noexcept {
+    if (!backend) return kc::Error::InvalidResourceHandle;
+    try {
+        return compute(*backend, nodes, n_nodes);
+    } catch (...) {
+        return kc::Error::OutOfMemory;
+    }
+}
+
+KC_API kcError_t kcGgmlBackendGetStats(kcGgmlBackend_t backend, kcGgmlStats* stats) noexcept {
+    if (!backend) return kc::Error::InvalidResourceHandle;
+    if (!stats) return bad("null stats pointer");
+    *stats = backend->stats;
+    return ok;
+}

@@ -7,6 +7,7 @@
 // scratch waits for the stream before the old buffer goes.
 #include <algorithm>
 #include <climits>
+#include <cstdint>
 #include <cstdlib>
 #include <cstring>
 #include <new>
@@ -16,22 +17,7 @@
 #include "kernelcore/llm_kernels.h"
 #include "kernelcore/model.h"
 #include "kernelcore/mul_mat.h"
-
-struct kcMulMatRecording_st {
-    kcMulMatConfig cfg{};
-    kcStream_t stream = nullptr;
-    int* scratch = nullptr;
-    size_t cap = 0;   // ints
-    size_t used = 0;  // ints taken by this recording
-    struct Input {
-        const float* x;
-        long long ncols;
-        int k;
-        bool k256;
-        int* q;
-    };
-    std::vector<Input> inputs;  // the recording's quantized inputs
-};
+#include "mul_mat_internal.hpp"
 
 namespace {
 
@@ -47,26 +33,21 @@ E bad(const char* why) {
 // per 256 values nsb * 85 (the reference's scratchInts / scratchKInts, llm/llm_kernels.hpp:84-89).
 size_t slotInts(int k, bool k256) { return k256 ? size_t(k / 256) * 85 : size_t(k / 32) * 11; }
 
-// `ints` ints of the recording's scratch (64-byte multiples). Growing it: the stream finishes
-// the launches that read the old buffer, which is freed, and the cached inputs (in it) are dropped.
-E take(kcMulMatRecording_st& r, size_t ints, int** out) {
-    ints = (ints + 15) / 16 * 16;
-    if (r.used + ints > r.cap) {
-        if (r.scratch) {
-            if (E e = kcStreamSynchronize(r.stream); e != ok) return e;
-            if (E e = kcFree(r.scratch); e != ok) return e;
-            r.scratch = nullptr;
-        }
-        const size_t want = std::max(ints * 4, r.cap * 2);
-        r.cap = r.used = 0;
-        r.inputs.clear();
-        void* p = nullptr;
-        if (E e = kcMalloc(&p, want * sizeof(int)); e != ok) return e;
-        r.scratch = static_cast<int*>(p);
-        r.cap = want;
+// Replaces the scratch by one of `ints` ints: the stream finishes the launches that read the old
+// buffer, which is freed, and the cached inputs (in it) are dropped.
+E regrow(kcMulMatRecording_st& r, size_t ints) {
+    if (r.scratch) {
+        if (E e = kcStreamSynchronize(r.stream); e != ok) return e;
+        if (E e = kcFree(r.scratch); e != ok) return e;
+        r.scratch = nullptr;
     }
-    *out = r.scratch + r.used;
-    r.used += ints;
+    r.cap = r.used = 0;
+    r.inputs.clear();
+    ++r.gen;
+    void* p = nullptr;
+    if (E e = kcMalloc(&p, ints * sizeof(int)); e != ok) return e;
+    r.scratch = static_cast<int*>(p);
+    r.cap = ints;
     return ok;
 }
 
@@ -75,8 +56,8 @@ void name(char (&dst)[24], const char* src) {
     dst[sizeof dst - 1] = '\0';
 }
 
-E launch(const kcMulMatRecording_st& r, const char* kernel, const void* args, kcMulMatPlan& plan) {
-    const E e = kcLaunchKernel(kernel, args, r.stream);
+E launch(kcMulMatRecording_st& r, const char* kernel, const void* args, kcMulMatPlan& plan) {
+    const E e = kcamd::mulmat::launch(r, kernel, args);
     if (e == ok) ++plan.launches;
     return e;
 }
@@ -92,7 +73,7 @@ E quantizedInput(kcMulMatRecording_st& r, const kcMulMatNode& n, bool k256, int*
     const int nb = n.k / 32;
     const size_t slot = slotInts(n.k, k256);
     int* base = nullptr;
-    if (E e = take(r, slot * size_t(n.ncols), &base); e != ok) return e;
+    if (E e = kcamd::mulmat::take(r, slot * size_t(n.ncols), &base); e != ok) return e;
     const bool contiguous = n.x_col_bytes == size_t(n.k) * sizeof(float);
     if (k256) {
         const kcQuantizeColsArgs a{n.x, base, nullptr, n.k, int(n.ncols)};
@@ -122,7 +103,7 @@ bool batchK256(const kcMulMatRecording_st& r, long long ncols) { return ncols > 
 // Slots for the 8-bit form of y (ncols columns of k values) plus `extra` ints, registered under y
 // so that the MUL_MATs reading y find them (quantized_slots, :451-467).
 E registeredSlots(kcMulMatRecording_st& r, const float* y, int k, long long ncols, bool k256, size_t extra, int** q) {
-    if (E e = take(r, slotInts(k, k256) * size_t(ncols) + extra, q); e != ok) return e;
+    if (E e = kcamd::mulmat::take(r, slotInts(k, k256) * size_t(ncols) + extra, q); e != ok) return e;
     for (auto it = r.inputs.begin(); it != r.inputs.end(); ++it)  // y rewritten: older slots of it are stale
         if (it->x == y && it->ncols == ncols && it->k == k && it->k256 == k256) {
             r.inputs.erase(it);
@@ -132,7 +113,7 @@ E registeredSlots(kcMulMatRecording_st& r, const float* y, int k, long long ncol
     return ok;
 }
 
-E fusedNorm(kcMulMatRecording_st& r, const kcMulMatNormNode& n, kcMulMatPlan& plan) {
+E fusedNormImpl(kcMulMatRecording_st& r, const kcMulMatNormNode& n, kcMulMatPlan& plan) {
     if (!n.x || !n.w || !n.y || (n.a != nullptr) != (n.b != nullptr)) return bad("norm: null x, w or y, or one of a / b");
     if (n.n <= 0 || n.n % 256 || n.rows <= 0 || (long long)n.n * n.rows >= (1 << 24))
         return bad("norm: n must be a positive multiple of 256, rows positive, n * rows < 2^24");
@@ -159,7 +140,7 @@ E fusedNorm(kcMulMatRecording_st& r, const kcMulMatNormNode& n, kcMulMatPlan& pl
     return launch(r, kernel, &a, plan);
 }
 
-E fusedSwiglu(kcMulMatRecording_st& r, const kcMulMatSwigluNode& n, kcMulMatPlan& plan) {
+E fusedSwigluImpl(kcMulMatRecording_st& r, const kcMulMatSwigluNode& n, kcMulMatPlan& plan) {
     if (!n.g || !n.u || !n.y) return bad("swiglu: null g, u or y");
     if (n.n <= 0 || n.n % 256 || n.cols <= 0 || (long long)n.n * n.cols >= (1 << 24))
         return bad("swiglu: n must be a positive multiple of 256, cols positive, n * cols < 2^24");
@@ -187,7 +168,7 @@ E validate(const kcMulMatNode& n) {
     return ok;
 }
 
-E mulMat(kcMulMatRecording_st& r, const kcMulMatNode& n, kcMulMatPlan& plan) {
+E mulMatImpl(kcMulMatRecording_st& r, const kcMulMatNode& n, kcMulMatPlan& plan) {
     if (E e = validate(n); e != ok) return e;
     const int ncols = int(n.ncols);
     if (n.wtype == KC_QTYPE_F16) {  // f32 activations as they are
@@ -226,6 +207,92 @@ E mulMat(kcMulMatRecording_st& r, const kcMulMatNode& n, kcMulMatPlan& plan) {
 
 }  // namespace
 
+namespace kcamd::mulmat {
+
+kcError_t checkConfig(kcMulMatConfig& c) noexcept {
+    if (c.tile != 4 && c.tile != 8) return bad("tile must be 4 or 8");
+    if (c.row_block < 1) return bad("row_block must be at least 1");
+    c.matvec_cols = c.matvec_cols != 0;
+    c.q8k = c.q8k != 0;
+    return ok;
+}
+
+void reset(kcMulMatRecording_st& r) noexcept {
+    r.inputs.clear();
+    r.used = r.peak = 0;  // same stream: the next recording's launches run after the last one's
+}
+
+kcError_t reserve(kcMulMatRecording_st& r, size_t ints) noexcept {
+    ints = (ints + 15) / 16 * 16;
+    if (r.dry || ints <= r.cap) return ok;
+    return regrow(r, ints);
+}
+
+kcError_t take(kcMulMatRecording_st& r, size_t ints, int** out) noexcept {
+    ints = (ints + 15) / 16 * 16;
+    if (r.dry) {  // an offset only, never dereferenced
+        *out = reinterpret_cast<int*>(uintptr_t(256) + r.used * sizeof(int));
+        r.used += ints;
+        r.peak = std::max(r.peak, r.used);
+        return ok;
+    }
+    if (r.used + ints > r.cap)
+        if (E e = regrow(r, std::max(ints * 4, r.cap * 2)); e != ok) return e;
+    *out = r.scratch + r.used;
+    r.used += ints;
+    r.peak = std::max(r.peak, r.used);
+    return ok;
+}
+
+kcError_t launch(kcMulMatRecording_st& r, const char* kernel, const void* args) noexcept {
+    if (r.trace) {
+        try {
+            r.trace->push_back(kernel);
+        } catch (...) {
+            return kc::Error::OutOfMemory;
+        }
+    }
+    return r.dry ? ok : kcLaunchKernel(kernel, args, r.stream);
+}
+
+kcError_t mulMat(kcMulMatRecording_st& r, const kcMulMatNode& n, kcMulMatPlan& plan) noexcept {
+    try {
+        return mulMatImpl(r, n, plan);
+    } catch (...) {
+        return kc::Error::OutOfMemory;
+    }
+}
+
+kcError_t mulMatInput(kcMulMatRecording_st& r, const kcMulMatNode& n, kcMulMatPlan& plan) noexcept {
+    if (E e = validate(n); e != ok) return e;
+    if (n.wtype == KC_QTYPE_F16) return ok;
+    const bool k256 = batchK256(r, n.ncols) && n.x_col_bytes == size_t(n.k) * sizeof(float);
+    int* q = nullptr;
+    try {
+        return quantizedInput(r, n, k256, &q, plan);
+    } catch (...) {
+        return kc::Error::OutOfMemory;
+    }
+}
+
+kcError_t fusedNorm(kcMulMatRecording_st& r, const kcMulMatNormNode& n, kcMulMatPlan& plan) noexcept {
+    try {
+        return fusedNormImpl(r, n, plan);
+    } catch (...) {
+        return kc::Error::OutOfMemory;
+    }
+}
+
+kcError_t fusedSwiglu(kcMulMatRecording_st& r, const kcMulMatSwigluNode& n, kcMulMatPlan& plan) noexcept {
+    try {
+        return fusedSwigluImpl(r, n, plan);
+    } catch (...) {
+        return kc::Error::OutOfMemory;
+    }
+}
+
+}  // namespace kcamd::mulmat
+
 KC_API void kcMulMatConfigFromEnv(kcMulMatConfig* cfg) noexcept {
     if (!cfg) return;
     *cfg = kcMulMatConfig{0, 1, 8, 8};
@@ -242,10 +309,7 @@ KC_API kcError_t kcMulMatRecordingCreate(kcMulMatRecording_t* rec, const kcMulMa
     kcMulMatConfig c;
     if (cfg) c = *cfg;
     else kcMulMatConfigFromEnv(&c);
-    if (c.tile != 4 && c.tile != 8) return bad("tile must be 4 or 8");
-    if (c.row_block < 1) return bad("row_block must be at least 1");
-    c.matvec_cols = c.matvec_cols != 0;
-    c.q8k = c.q8k != 0;
+    if (E e = kcamd::mulmat::checkConfig(c); e != ok) return e;
     auto* r = new (std::nothrow) kcMulMatRecording_st;
     if (!r) return kc::Error::OutOfMemory;
     r->cfg = c;
@@ -256,8 +320,7 @@ KC_API kcError_t kcMulMatRecordingCreate(kcMulMatRecording_t* rec, const kcMulMa
 
 KC_API kcError_t kcMulMatRecordingReset(kcMulMatRecording_t rec) noexcept {
     if (!rec) return kc::Error::InvalidResourceHandle;
-    rec->inputs.clear();
-    rec->used = 0;  // same stream: the next recording's launches run after the last one's
+    kcamd::mulmat::reset(*rec);
     return ok;
 }
 
@@ -277,7 +340,7 @@ KC_API kcError_t kcMulMat(kcMulMatRecording_t rec, const kcMulMatNode* node, kcM
     if (!rec) return kc::Error::InvalidResourceHandle;
     if (!node) return bad("null node");
     kcMulMatPlan p{};
-    const E e = mulMat(*rec, *node, p);
+    const E e = kcamd::mulmat::mulMat(*rec, *node, p);
     if (plan) *plan = p;
     return e;
 }
@@ -286,7 +349,7 @@ KC_API kcError_t kcMulMatFusedNorm(kcMulMatRecording_t rec, const kcMulMatNormNo
     if (!rec) return kc::Error::InvalidResourceHandle;
     if (!node) return bad("null node");
     kcMulMatPlan p{};
-    const E e = fusedNorm(*rec, *node, p);
+    const E e = kcamd::mulmat::fusedNorm(*rec, *node, p);
     if (plan) *plan = p;
     return e;
 }
@@ -296,7 +359,7 @@ KC_API kcError_t kcMulMatFusedSwiglu(kcMulMatRecording_t rec, const kcMulMatSwig
     if (!rec) return kc::Error::InvalidResourceHandle;
     if (!node) return bad("null node");
     kcMulMatPlan p{};
-    const E e = fusedSwiglu(*rec, *node, p);
+    const E e = kcamd::mulmat::fusedSwiglu(*rec, *node, p);
     if (plan) *plan = p;
     return e;
 }

@@ -1,0 +1,52 @@
+// mul_mat_internal.hpp -- the MUL_MAT recording shared by kcMulMat* (mul_mat.cpp) and the ggml
+// backend core (ggml_backend.cpp): its scratch, its cache of quantized inputs and the dispatch
+// functions behind the public calls.
+#pragma once
+
+#include <cstddef>
+#include <vector>
+
+#include "kernelcore/mul_mat.h"
+
+struct kcMulMatRecording_st {
+    kcMulMatConfig cfg{};
+    kcStream_t stream = nullptr;
+    int* scratch = nullptr;
+    size_t cap = 0;   // ints
+    size_t used = 0;  // ints taken by this recording
+    size_t peak = 0;  // the most ints taken since the last reset (a dry recording's requirement)
+    unsigned gen = 0; // bumped whenever the scratch buffer is replaced
+    // A dry recording plans: it takes scratch offsets and names its kernels without allocating or
+    // launching anything (no device is needed); pointers it hands out are never dereferenced.
+    bool dry = false;
+    std::vector<const char*>* trace = nullptr;  // when set: every kernel name, in launch order
+    struct Input {
+        const float* x;
+        long long ncols;
+        int k;
+        bool k256;
+        int* q;
+    };
+    std::vector<Input> inputs;  // the recording's quantized inputs
+};
+
+namespace kcamd::mulmat {
+
+// tile 4 or 8, row_block >= 1; the flags normalised to 0 / 1
+kcError_t checkConfig(kcMulMatConfig& c) noexcept;
+// a new recording: the cached inputs dropped, the scratch reused from its start
+void reset(kcMulMatRecording_st& r) noexcept;
+// the scratch holds at least `ints` ints (replacing it waits for the stream and drops the cache)
+kcError_t reserve(kcMulMatRecording_st& r, size_t ints) noexcept;
+// `ints` ints of the recording's scratch (64-byte multiples), growing it if needed
+kcError_t take(kcMulMatRecording_st& r, size_t ints, int** out) noexcept;
+// one launch on the recording's stream (dry: named only)
+kcError_t launch(kcMulMatRecording_st& r, const char* kernel, const void* args) noexcept;
+
+kcError_t mulMat(kcMulMatRecording_st& r, const kcMulMatNode& n, kcMulMatPlan& plan) noexcept;
+// the node's 8-bit input made now (the reference's mul_mat_input; nothing for F16 weights)
+kcError_t mulMatInput(kcMulMatRecording_st& r, const kcMulMatNode& n, kcMulMatPlan& plan) noexcept;
+kcError_t fusedNorm(kcMulMatRecording_st& r, const kcMulMatNormNode& n, kcMulMatPlan& plan) noexcept;
+kcError_t fusedSwiglu(kcMulMatRecording_st& r, const kcMulMatSwigluNode& n, kcMulMatPlan& plan) noexcept;
+
+}  // namespace kcamd::mulmat

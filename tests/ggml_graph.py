@@ -1,0 +1,200 @@
+"""ggml-shaped graphs of kcGgmlTensor descriptors (include/kernelcore/ggml_backend.h) for the
+backend-core tests: tensors follow ggml's conventions (ne[0] the fastest dimension, nb in bytes,
+views share their source's memory), ops get ggml's result shapes and op_params layout, and
+`finish` fills the use counts and output flags a ggml_cgraph would carry.
+
+`llama_layer` builds one transformer layer the way llama.cpp's graph does with flash attention
+on (the attention block: RMS_NORM + MUL, MUL_MAT q/k/v, RESHAPE, ROPE, SET_ROWS of k and v into
+the fp16 KV cache, VIEWs of the cache, PERMUTE of q, FLASH_ATTN_EXT, MUL_MAT o, ADD; the FFN:
+RMS_NORM + MUL, MUL_MAT gate/up, GLU SWIGLU, MUL_MAT down, ADD) -- the node order of
+/root/reference/docs/cuda_cpu_poc_plan.md:1156-1158 and llm/llm_model.cpp:287-360.
+
+With no allocator every tensor gets a distinct fake address (for plans, which never touch
+memory); with one (called with the ggml byte size, type and ne), every non-view tensor gets the
+memory it returns."""
+import ctypes as C
+import struct
+
+import kernelcore_amd as kc
+
+SIZE = {"f32": 4, "f16": 2, "i32": 4, "i64": 8}
+BLOCK = {"q4k": (256, 144), "q6k": (256, 210)}
+
+
+def f32bits(v):
+    return struct.unpack("<i", struct.pack("<f", float(v)))[0]
+
+
+def packed_nb(type_, ne):
+    blck, size = BLOCK.get(type_, (1, SIZE.get(type_, 4)))
+    nb = [size, size * (ne[0] // blck)]
+    for d in range(2, 4):
+        nb.append(nb[-1] * ne[d - 1])
+    return nb
+
+
+class Graph:
+    def __init__(self, alloc=None):
+        self.alloc = alloc
+        self.fake = 1 << 20
+        self.nodes = []
+        self.keep = []
+        self.srcs = {}  # id(tensor) -> [src tensors]
+
+    def _memory(self, nbytes, type_, ne):
+        if self.alloc is None:
+            p = self.fake
+            self.fake += (nbytes + 255) // 256 * 256 + 256
+            return p
+        return self.alloc(nbytes, type_, ne)
+
+    def tensor(self, op, type_, ne, srcs=(), params=(), nb=None, data=None, buffer="other", view=False,
+               compute=False):
+        ne = list(ne) + [1] * (4 - len(ne))
+        nb = list(nb) if nb is not None else packed_nb(type_, ne)
+        t = kc.GgmlTensor()
+        t.op, t.type = kc.GGML_OP[op], kc.GGML_TYPE[type_]
+        for d in range(4):
+            t.ne[d], t.nb[d] = ne[d], nb[d]
+        nbytes = nb[3] * ne[3]
+        t.data = data if data is not None else self._memory(max(nbytes, 4), type_, ne)
+        for i, s in enumerate(srcs):
+            if s is not None:
+                t.src[i] = C.pointer(s)
+        for i, p in enumerate(params):
+            t.op_params[i] = p
+        t.buffer, t.view, t.compute = kc.GGML_BUFFER[buffer], int(view), int(compute)
+        self.keep.append(t)
+        self.srcs[id(t)] = [s for s in srcs if s is not None]
+        return t
+
+    def leaf(self, type_, ne, buffer="other"):
+        return self.tensor("none", type_, ne, buffer=buffer)
+
+    def node(self, *a, **k):
+        t = self.tensor(*a, compute=True, **k)
+        self.nodes.append(t)
+        return t
+
+    # ---- ops (ggml result shapes and op_params) ----
+    def rms_norm(self, x, eps):
+        return self.node("rms_norm", "f32", x.ne, [x], [f32bits(eps)])
+
+    def mul(self, a, b):
+        return self.node("mul", "f32", a.ne, [a, b])
+
+    def add(self, a, b):
+        return self.node("add", "f32", a.ne, [a, b])
+
+    def mul_mat(self, w, x):
+        return self.node("mul_mat", "f32", [w.ne[1], x.ne[1], x.ne[2], x.ne[3]], [w, x])
+
+    def reshape(self, t, ne):
+        return self.node("reshape", _tname(t), ne, [t], data=t.data, buffer=_bname(t), view=True)
+
+    def view(self, t, ne, nb, offset=0):
+        return self.node("view", _tname(t), ne, [t], nb=list(nb), data=t.data + offset, buffer=_bname(t), view=True)
+
+    def permute(self, t, axes):
+        ne, nb = [0] * 4, [0] * 4
+        for i, a in enumerate(axes):
+            ne[a], nb[a] = t.ne[i], t.nb[i]
+        return self.node("permute", _tname(t), ne, [t], nb=nb, data=t.data, buffer=_bname(t), view=True)
+
+    def rope(self, x, pos, n_dims, neox, freq_base, ff=None, p15=0, freq_scale=1.0, ext_factor=0.0,
+             attn_factor=1.0):
+        params = [0, n_dims, 2 if neox else 0, 0, 0, f32bits(freq_base), f32bits(freq_scale), f32bits(ext_factor),
+                  f32bits(attn_factor), f32bits(32.0), f32bits(1.0)] + [0] * 4 + [p15]
+        return self.node("rope", "f32", x.ne, [x, pos, ff], params)
+
+    def set_rows(self, dst, src, idx):
+        return self.node("set_rows", _tname(dst), dst.ne, [src, idx], nb=list(dst.nb), data=dst.data,
+                         buffer=_bname(dst), view=True)
+
+    def flash_attn_ext(self, q, k, v, mask, scale, max_bias=0.0, softcap=0.0):
+        return self.node("flash_attn_ext", "f32", [v.ne[0], q.ne[2], q.ne[1], q.ne[3]], [q, k, v, mask],
+                         [f32bits(scale), f32bits(max_bias), f32bits(softcap)])
+
+    def swiglu(self, g, u, op=2, swapped=0):
+        return self.node("glu", "f32", g.ne, [g, u], [op, swapped])
+
+    def finish(self, outputs=()):
+        """Use counts (how many nodes read each node) and output flags, as ggml_cgraph keeps them."""
+        uses = {}
+        for t in self.nodes:
+            for s in self.srcs[id(t)]:
+                uses[id(s)] = uses.get(id(s), 0) + 1
+        for t in self.nodes:
+            t.uses = uses.get(id(t), 0)
+        for t in outputs:
+            t.output = 1
+        return self.nodes
+
+
+def _tname(t):
+    return {v: k for k, v in kc.GGML_TYPE.items()}[t.type]
+
+
+def _bname(t):
+    return {v: k for k, v in kc.GGML_BUFFER.items()}[t.buffer]
+
+
+class LayerShape:
+    def __init__(self, n_embd=512, n_head=8, n_head_kv=2, n_ff=1024, kv_size=512, eps=1e-5, base=500000.0,
+                 neox=False, wq="q4k", wk="q4k", wv="q6k", wo="q4k", wg="q4k", wu="q4k", wd="q6k", freq_factors=False):
+        self.n_embd, self.n_head, self.n_head_kv, self.n_ff = n_embd, n_head, n_head_kv, n_ff
+        self.hd = n_embd // n_head
+        self.kv_dim = self.hd * n_head_kv
+        self.kv_size, self.eps, self.base, self.neox = kv_size, eps, base, neox
+        self.types = dict(wq=wq, wk=wk, wv=wv, wo=wo, wg=wg, wu=wu, wd=wd)
+        self.freq_factors = freq_factors
+
+
+def llama_layer(g, s, n_tokens, n_kv):
+    """One layer over n_tokens new tokens whose keys go to cache rows given by `kv_idx`, attending over
+    the first n_kv rows of the cache. Returns the named tensors (leaves and nodes)."""
+    N, t = n_tokens, {}
+    t["x"] = g.leaf("f32", [s.n_embd, N])
+    t["pos"] = g.leaf("i32", [N])
+    t["kv_idx"] = g.leaf("i64", [N])
+    n_kv_pad = (n_kv + 1) // 2 * 2
+    t["mask"] = g.leaf("f16", [n_kv_pad, N])
+    t["ff"] = g.leaf("f32", [s.hd // 2]) if s.freq_factors else None
+    for name, (rows, k) in dict(wq=(s.n_embd, s.n_embd), wk=(s.kv_dim, s.n_embd), wv=(s.kv_dim, s.n_embd),
+                                wo=(s.n_embd, s.n_embd), wg=(s.n_ff, s.n_embd), wu=(s.n_ff, s.n_embd),
+                                wd=(s.n_embd, s.n_ff)).items():
+        t[name] = g.leaf(s.types[name], [k, rows], buffer="weights")
+    t["attn_norm"] = g.leaf("f32", [s.n_embd], buffer="weights")
+    t["ffn_norm"] = g.leaf("f32", [s.n_embd], buffer="weights")
+    t["k_cache"] = g.leaf("f16", [s.kv_dim, s.kv_size], buffer="kv")
+    t["v_cache"] = g.leaf("f16", [s.kv_dim, s.kv_size], buffer="kv")
+
+    t["norm"] = g.rms_norm(t["x"], s.eps)
+    t["cur"] = g.mul(t["norm"], t["attn_norm"])
+    t["q"] = g.mul_mat(t["wq"], t["cur"])
+    t["k"] = g.mul_mat(t["wk"], t["cur"])
+    t["v"] = g.mul_mat(t["wv"], t["cur"])
+    t["q3"] = g.reshape(t["q"], [s.hd, s.n_head, N])
+    t["qr"] = g.rope(t["q3"], t["pos"], s.hd, s.neox, s.base, t["ff"])
+    t["k3"] = g.reshape(t["k"], [s.hd, s.n_head_kv, N])
+    t["kr"] = g.rope(t["k3"], t["pos"], s.hd, s.neox, s.base, t["ff"])
+    t["kr2"] = g.reshape(t["kr"], [s.kv_dim, N])
+    t["k_set"] = g.set_rows(t["k_cache"], t["kr2"], t["kv_idx"])
+    t["v_set"] = g.set_rows(t["v_cache"], t["v"], t["kv_idx"])
+    row = s.kv_dim * 2
+    t["k_view"] = g.view(t["k_set"], [s.hd, n_kv, s.n_head_kv, 1], [2, row, s.hd * 2, row * n_kv])
+    t["v_view"] = g.view(t["v_set"], [s.hd, n_kv, s.n_head_kv, 1], [2, row, s.hd * 2, row * n_kv])
+    t["q_perm"] = g.permute(t["qr"], [0, 2, 1, 3])
+    t["attn"] = g.flash_attn_ext(t["q_perm"], t["k_view"], t["v_view"], t["mask"], 1.0 / s.hd ** 0.5)
+    t["attn2"] = g.reshape(t["attn"], [s.n_embd, N])
+    t["o"] = g.mul_mat(t["wo"], t["attn2"])
+    t["ffn_inp"] = g.add(t["o"], t["x"])
+    t["norm2"] = g.rms_norm(t["ffn_inp"], s.eps)
+    t["cur2"] = g.mul(t["norm2"], t["ffn_norm"])
+    t["gate"] = g.mul_mat(t["wg"], t["cur2"])
+    t["up"] = g.mul_mat(t["wu"], t["cur2"])
+    t["act"] = g.swiglu(t["gate"], t["up"])
+    t["down"] = g.mul_mat(t["wd"], t["act"])
+    t["out"] = g.add(t["down"], t["ffn_inp"])
+    g.finish(outputs=[t["out"]])
+    return t

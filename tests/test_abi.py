@@ -82,13 +82,14 @@ STRUCTS = ["VectorAddArgs", "QuantizeArgs", "MatvecQ4Q8Args", "MatmulKQ8Args", "
            "SiluMulQ8FArgs",
            "SiluMulArgs", "SetRowsF16Args", "FaDims", "FaScoresArgs", "FaMaxArgs", "FaExpArgs", "FaValuesArgs",
            "KquantRepackArgs", "GetRowsKquantArgs", "QuantizeKquantArgs", "FillNormalArgs", "FlashAttnArgs", "DeviceProperties",
-           "MulMatConfig", "MulMatNode", "MulMatPlan", "MulMatNormNode", "MulMatSwigluNode"]
+           "MulMatConfig", "MulMatNode", "MulMatPlan", "MulMatNormNode", "MulMatSwigluNode", "GgmlTensor",
+           "GgmlConfig", "GgmlStats"]
 
 
 def test_struct_layouts_match_the_c_header(tmp_path):
     """ctypes mirrors against what gcc makes of include/kernelcore/llm_kernels.h."""
     lines = ["#include <stdio.h>", "#include <stddef.h>", "#include <kernelcore/llm_kernels.h>",
-             "#include <kernelcore/mul_mat.h>", "int main(void) {"]
+             "#include <kernelcore/mul_mat.h>", "#include <kernelcore/ggml_backend.h>", "int main(void) {"]
     for s in STRUCTS:
         cls = getattr(kc, s)
         lines.append(f'printf("{s} %zu\\n", sizeof(kc{s}));')

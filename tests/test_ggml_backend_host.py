@@ -1,0 +1,329 @@
+"""Host-only checks of the ggml backend core (include/kernelcore/ggml_backend.h): its supports_op
+rules (integrations/llama.cpp/ggml/src/ggml-kernelcore/ggml-kernelcore.cpp:865-957, weight_shape_ok
+:103-109) and the launch sequence graph_compute makes (:706-792) -- which nodes fuse, which are
+skipped, which MUL_MATs share a quantized input and run as one concurrent step -- read from
+kcGgmlGraphPlan, which walks the nodes exactly as kcGgmlGraphCompute does without a device.
+
+Each fusion rule is checked both ways: the layer graph llama.cpp builds fuses, and a planted
+change that ggml_can_fuse or the reference's pattern must reject (a second use of the norm, a
+norm that is a graph output or a view, a MUL by a full matrix, rows not a multiple of 256, an
+ADD whose result the norm does not read) turns the fusion off."""
+import pytest
+
+import kernelcore_amd as kc
+from tests import ggml_graph as gg
+
+
+def layer(N=1, n_kv=None, shape=None, **kw):
+    g = gg.Graph()
+    t = gg.llama_layer(g, shape or gg.LayerShape(**kw), N, n_kv or 40 + N)
+    return g, t
+
+
+def plan(g, **cfg):
+    return kc.ggml_graph_plan(g.nodes, **cfg)[0]
+
+
+ATTN = ["rope_ggml", "rope_ggml", "set_rows_f16", "set_rows_f16", "flash_attn_f16"]
+
+
+# ---- graph_compute's walk --------------------------------------------------------------------------------------
+
+def test_decode_layer_plan():
+    g, _ = layer(N=1)
+    assert plan(g) == (["sumsq_part", "norm_mul_q8_f", "[", "matvec_q4k_q8", "matvec_q4k_q8", "matvec_q6k_q8", "]"]
+                       + ATTN + ["quantize_q8x4", "matvec_q4k_q8", "add_sumsq_f", "norm_mul_q8_f",
+                                 "[", "matvec_q4k_q8", "matvec_q4k_q8", "]", "silu_mul_q8x4f", "matvec_q6k_q8",
+                                 "vector_add"])
+
+
+def test_graphs_off_runs_no_concurrent_groups():
+    g, _ = layer(N=1)
+    names = plan(g, graphs=0)
+    assert "[" not in names and names[:5] == ["sumsq_part", "norm_mul_q8_f", "matvec_q4k_q8", "matvec_q4k_q8",
+                                              "matvec_q6k_q8"]
+    assert plan(g, concurrent=0) == names
+
+
+@pytest.mark.parametrize("N,cfg,mm,quant", [
+    (8, {}, "matmul_{}_q8kx8", "quantize_cols_k"),           # batch_k256: per-256 slots, x8 tiles
+    (4, {}, "matmul_{}_q8kx4", "quantize_cols_k"),           # four columns: x4
+    (8, dict(tile=4), "matmul_{}_q8kx4", "quantize_cols_k"),
+    (3, dict(q8k=0), "matmul_{}_q8x4", "quantize_cols"),      # Q8K=0: per-32 slots
+    (64, dict(attn_tokens=64), "matmul_{}_q8kx8", "quantize_cols_k"),
+])
+def test_batch_layer_plans(N, cfg, mm, quant):
+    g, _ = layer(N=N)
+    k = "q8k" if quant == "quantize_cols_k" else "q8"
+    norm = "norm_mul_q8k_f" if k == "q8k" else "norm_mul_q8_f"
+    silu = "silu_mul_q8kf" if k == "q8k" else "silu_mul_q8x4f"
+    want = (["sumsq_part", norm, "[", mm.format("q4k"), mm.format("q4k"), mm.format("q6k"), "]"] + ATTN +
+            [quant, mm.format("q4k"), "add_sumsq_f", norm, "[", mm.format("q4k"), mm.format("q4k"), "]", silu,
+             mm.format("q6k"), "vector_add"])
+    assert plan(g, **cfg) == want
+
+
+def test_matvec_cols_runs_one_matvec_per_column():
+    g, _ = layer(N=3)
+    names = plan(g, matvec_cols=1)
+    assert names[:2] == ["sumsq_part", "norm_mul_q8_f"]  # not batch_k256: per-32 slots
+    assert names[2:12] == ["["] + ["matvec_q4k_q8"] * 6 + ["matvec_q6k_q8"] * 3
+    assert "quantize_cols" in names  # the attention output: contiguous columns, one launch
+
+
+def test_residual_add_fuses_into_the_next_layers_norm():
+    g = gg.Graph()
+    s = gg.LayerShape()
+    t = gg.llama_layer(g, s, 1, 41)
+    t["out"].output = 0
+    norm = g.rms_norm(t["out"], s.eps)
+    cur = g.mul(norm, t["attn_norm"])
+    g.mul_mat(t["wq"], cur)
+    g.finish()
+    names = plan(g)
+    # the residual ADD fused with the next layer's norm, whose slots the MUL_MAT takes (no quantizer)
+    assert names[-3:] == ["add_sumsq_f", "norm_mul_q8_f", "matvec_q4k_q8"] and "vector_add" not in names
+
+
+def norm_mul_graph(n=512, rows=1, weight_rows=1, mm=True):
+    g = gg.Graph()
+    x = g.leaf("f32", [n, rows])
+    w = g.leaf("f32", [n, weight_rows], buffer="weights")
+    norm = g.rms_norm(x, 1e-5)
+    mul = g.mul(norm, w)
+    if mm:
+        g.mul_mat(g.leaf("q4k", [n, 64], buffer="weights"), mul)
+    return g, norm, mul
+
+
+def test_norm_mul_fuses():
+    g, _, _ = norm_mul_graph()
+    g.finish()
+    assert plan(g) == ["sumsq_part", "norm_mul_q8_f", "matvec_q4k_q8"]
+
+
+@pytest.mark.parametrize("plant", ["second_use", "output", "view"])
+def test_norm_that_cannot_fuse_runs_alone(plant):
+    g, norm, mul = norm_mul_graph()
+    if plant == "second_use":
+        g.add(norm, norm)
+    g.finish()
+    if plant == "output":
+        norm.output = 1
+    if plant == "view":
+        norm.view = 1
+    names = plan(g)
+    # one-pass rms_norm without a weight, the MUL on its own, the MUL_MAT quantizes its input
+    assert names[:4] == ["rms_norm", "mul_rows", "quantize_q8x4", "matvec_q4k_q8"]
+
+
+def test_mul_by_a_matrix_is_not_the_norm_weight():
+    g, _, _ = norm_mul_graph(rows=2, weight_rows=2)
+    g.finish()
+    assert plan(g) == ["rms_norm", "mul_rows", "quantize_cols_k", "matmul_q4k_q8kx4"]
+
+
+def test_rows_not_a_multiple_of_256_take_the_weighted_rms_norm():
+    g, _, _ = norm_mul_graph(n=384, mm=False)
+    g.finish()
+    assert plan(g) == ["rms_norm"]  # RMS_NORM + MUL as one rms_norm with the weight
+
+
+def test_add_whose_result_the_norm_does_not_read():
+    g = gg.Graph()
+    a, b, x = (g.leaf("f32", [512, 1]) for _ in range(3))
+    g.add(a, b)
+    norm = g.rms_norm(x, 1e-5)
+    g.mul(norm, g.leaf("f32", [512], buffer="weights"))
+    g.finish()
+    assert plan(g) == ["vector_add", "sumsq_part", "norm_mul_q8_f"]
+
+
+def test_nodes_without_work_are_skipped():
+    g, t = layer(N=1)
+    t["o"].compute = 0  # not computed by this backend (the scheduler's flag)
+    names = plan(g)
+    assert names.count("matvec_q4k_q8") == 4 and "quantize_q8x4" not in names
+    g = gg.Graph()
+    x = g.leaf("f32", [512, 0])
+    g.add(x, x)
+    g.finish()
+    assert plan(g) == []  # an empty node
+
+
+def test_swiglu_unfused_when_rows_are_not_a_multiple_of_256():
+    g = gg.Graph()
+    a, b = g.leaf("f32", [96, 3]), g.leaf("f32", [96, 3])
+    g.swiglu(a, b)
+    g.finish()
+    assert plan(g) == ["silu_mul"]
+
+
+def test_long_context_attention_takes_the_four_kernels():
+    g, _ = layer(N=1, n_kv=20000, kv_size=20480)
+    names, ints = kc.ggml_graph_plan(g.nodes)
+    assert names[9:15] == ["set_rows_f16", "set_rows_f16", "fa_scores", "fa_max", "fa_exp", "fa_values"]
+    assert ints >= 8 * 20000  # the scores of 8 heads in the scratch
+
+
+def test_fused_producers_beyond_their_limit_run_unfused():
+    g, _, _ = norm_mul_graph(n=4096, rows=4096, mm=False)
+    g.finish()
+    assert plan(g, attn_tokens=8) == ["rms_norm"]
+    g = gg.Graph()
+    a, b = g.leaf("f32", [8192, 2048]), g.leaf("f32", [8192, 2048])
+    g.swiglu(a, b)
+    g.finish()
+    assert plan(g) == ["silu_mul"]
+
+
+def test_unsupported_nodes_are_refused_before_any_launch():
+    g, t = layer(N=1)
+    t["wq"].buffer = kc.GGML_BUFFER["other"]  # a weight outside this backend's buffers
+    with pytest.raises(kc.KcError) as e:
+        plan(g)
+    assert e.value.name == "UnsupportedOperation" and "node 2" in str(e.value)
+    g = gg.Graph()
+    x = g.leaf("f32", [64])
+    g.node("other", "f32", [64], [x])
+    with pytest.raises(kc.KcError) as e:
+        plan(g)
+    assert e.value.name == "UnsupportedOperation"
+
+
+def test_disabled_claims_nothing_and_makes_no_backend():
+    g, t = layer(N=1)
+    assert not kc.ggml_supports_op(t["q"], disabled=1)
+    assert not kc.ggml_offers_kv_buffer(disabled=1)
+    with pytest.raises(kc.KcError) as e:
+        kc.GgmlBackend(disabled=1)
+    assert e.value.name == "UnsupportedOperation"
+
+
+def test_scratch_requirement():
+    g, _ = layer(N=1)
+    assert kc.ggml_graph_plan(g.nodes)[1] == 880  # four per-32 slots of 512 or 1024 values (11 ints per 32)
+
+
+# ---- supports_op ---------------------------------------------------------------------------------------------
+
+def test_layer_nodes_are_all_claimed():
+    for N, cfg in [(1, {}), (8, {}), (64, dict(attn_tokens=64))]:
+        g, _ = layer(N=N)
+        assert all(kc.ggml_supports_op(n, **cfg) for n in g.nodes)
+
+
+def test_attention_of_batches_beyond_attn_tokens_is_not_claimed():
+    g, t = layer(N=9)
+    assert not kc.ggml_supports_op(t["attn"])
+    assert kc.ggml_supports_op(t["attn"], attn_tokens=9)
+    assert kc.ggml_supports_op(t["q"])  # MUL_MAT: any batch
+
+
+def test_matmul_only_and_attn_switches():
+    g, t = layer(N=1)
+    assert kc.ggml_supports_op(t["q"], matmul_only=1) and not kc.ggml_supports_op(t["norm"], matmul_only=1)
+    assert not kc.ggml_supports_op(t["k_set"], attn=0) and not kc.ggml_supports_op(t["attn"], attn=0)
+    assert kc.ggml_supports_op(t["rope"] if "rope" in t else t["qr"], attn=0)
+    assert not kc.ggml_offers_kv_buffer(attn=0) and not kc.ggml_offers_kv_buffer(matmul_only=1)
+    assert kc.ggml_offers_kv_buffer()
+
+
+def mm_case(wtype="q4k", k=512, rows=64, ncols=3, buffer="weights", **plant):
+    g = gg.Graph()
+    w = g.leaf(wtype, [k, rows], buffer=buffer)
+    x = g.leaf("f32", [k, ncols])
+    for f, v in plant.items():
+        if f == "w_ne2":
+            w.ne[2] = v
+        elif f == "x_nb1":
+            x.nb[1] = v
+        elif f == "x_ne0":
+            x.ne[0] = v
+    return g.mul_mat(w, x)
+
+
+@pytest.mark.parametrize("case,want", [
+    (dict(), True), (dict(wtype="q6k"), True), (dict(wtype="f16", k=514), True),
+    (dict(buffer="other"), False),      # the weight must be in this backend's (repacked) buffers
+    (dict(k=300), False),               # K-quant k % 256
+    (dict(rows=60), False),             # rows % 8
+    (dict(wtype="f16", k=513), False),  # fp16 k even
+    (dict(w_ne2=2), False),             # 2-D weights only
+    (dict(x_nb1=4 * 600), False),       # the input contiguous
+    (dict(x_ne0=256), False),           # the input's rows as long as the weight's
+])
+def test_mul_mat_rules(case, want):
+    assert kc.ggml_supports_op(mm_case(**case)) == want
+
+
+def rope_case(**plant):
+    g = gg.Graph()
+    x = g.leaf("f32", [64, 8, 3])
+    pos = g.leaf("i32", [3])
+    ff = g.leaf("f32", [32]) if plant.pop("ff", False) else None
+    kw = dict(neox=plant.pop("neox", False), ff=ff)
+    for k in ("freq_scale", "ext_factor", "attn_factor", "p15"):
+        if k in plant:
+            kw[k] = plant.pop(k)
+    n_dims = plant.pop("n_dims", 64)
+    if plant.pop("pos_i64", False):
+        pos = g.leaf("i64", [3])
+    t = g.rope(x, pos, n_dims, freq_base=10000.0, **kw)
+    if plant.pop("mode", None) is not None:
+        t.op_params[2] = 8  # another rope mode (e.g. multi-section)
+    return t
+
+
+@pytest.mark.parametrize("case,want", [
+    (dict(), True), (dict(neox=True), True), (dict(ff=True), True),
+    (dict(n_dims=32), False),           # partial rotation
+    (dict(freq_scale=0.5), False), (dict(ext_factor=1.0), False), (dict(attn_factor=2.0), False),
+    (dict(p15=1), False), (dict(mode=8), False), (dict(pos_i64=True), False),
+])
+def test_rope_rules(case, want):
+    assert kc.ggml_supports_op(rope_case(**case)) == want
+
+
+def test_elementwise_rules():
+    g = gg.Graph()
+    a, b = g.leaf("f32", [512, 2]), g.leaf("f32", [512, 2])
+    row = g.leaf("f32", [512])
+    odd = g.leaf("f32", [12, 1])
+    assert kc.ggml_supports_op(g.add(a, b)) and kc.ggml_supports_op(g.mul(a, row)) and kc.ggml_supports_op(g.mul(a, b))
+    assert not kc.ggml_supports_op(g.add(a, row))  # ADD: same shapes only
+    assert not kc.ggml_supports_op(g.mul(odd, odd))  # 12 values: not a multiple of 8
+    assert kc.ggml_supports_op(g.rms_norm(a, 1e-6))
+    f16 = g.leaf("f16", [512, 2])
+    assert not kc.ggml_supports_op(g.rms_norm(f16, 1e-6))
+    assert kc.ggml_supports_op(g.swiglu(a, b)) and not kc.ggml_supports_op(g.swiglu(a, b, op=1))
+    assert not kc.ggml_supports_op(g.swiglu(a, b, swapped=1))
+
+
+def test_set_rows_and_attention_rules():
+    g, t = layer(N=2)
+    assert kc.ggml_supports_op(t["k_set"]) and kc.ggml_supports_op(t["attn"])
+    t["k_cache"].buffer = t["k_set"].buffer = kc.GGML_BUFFER["other"]
+    assert not kc.ggml_supports_op(t["k_set"])  # not a KV buffer of this backend
+    t["k_view"].buffer = kc.GGML_BUFFER["other"]
+    assert not kc.ggml_supports_op(t["attn"])
+    g, t = layer(N=2)
+    t["attn"].op_params[2] = gg.f32bits(30.0)  # logit softcap
+    assert not kc.ggml_supports_op(t["attn"])
+    g, t = layer(N=2)
+    t["mask"].type = kc.GGML_TYPE["f32"]
+    assert not kc.ggml_supports_op(t["attn"])
+
+
+def test_host_environment_switches(monkeypatch):
+    for v in ("DISABLE", "MATMUL_ONLY", "ATTN", "ATTN_TOKENS", "CONCURRENT", "GRAPHS", "MATVEC_COLS", "Q8K", "TILE",
+              "ROW_BLOCK"):
+        monkeypatch.delenv(f"GGML_KERNELCORE_{v}", raising=False)
+    assert kc.ggml_config_dict(kc.ggml_config()) == dict(matvec_cols=0, q8k=1, tile=8, row_block=8, disabled=0,
+                                                         matmul_only=0, attn=1, attn_tokens=8, concurrent=1, graphs=1)
+    monkeypatch.setenv("GGML_KERNELCORE_ATTN_TOKENS", "-3")
+    monkeypatch.setenv("GGML_KERNELCORE_GRAPHS", "0")
+    monkeypatch.setenv("GGML_KERNELCORE_DISABLE", "yes")  # only "1" disables
+    monkeypatch.setenv("GGML_KERNELCORE_TILE", "4")
+    d = kc.ggml_config_dict(kc.ggml_config())
+    assert (d["attn_tokens"], d["graphs"], d["disabled"], d["tile"]) == (0, 0, 0, 4)

@@ -1,0 +1,271 @@
+"""The ggml backend core (include/kernelcore/ggml_backend.h) on the GPU: graph_compute
+(integrations/llama.cpp/ggml/src/ggml-kernelcore/ggml-kernelcore.cpp:706-792) over the layer graph
+llama.cpp builds (tests/ggml_graph.py), every node's output checked against the oracle on the
+GPU's own inputs to that node, so that each op is held to its own bar and nothing compounds:
+  - [ADD +] RMS_NORM + MUL (fused): bit-exact against the oracle's fused restatement;
+  - MUL_MAT q/k/v, o, gate/up, down: the oracle's quantizer and product on the node's f32 input --
+    bit-exact (matvec per column, column-tiled matmul), 1e-3 on the MFMA matmul (64 columns);
+  - ROPE: 2e-5 of the largest value (the layer tests' bar); SET_ROWS: the whole fp16 cache
+    bit-exact (rows written, rows untouched); FLASH_ATTN_EXT: 2e-6 relative;
+  - SWIGLU: 2e-6 relative (exp2 ulps); the residual ADDs: bit-exact.
+Then the graph paths: a backend recording graphs and one launching eagerly give bit-identical
+layers, and the kept graph, launched again for new input values with eager work and
+synchronizations between, matches the eager backend on every call (and is not recorded again)."""
+import ctypes as C
+import sys
+
+import numpy as np
+import pytest
+
+import kernelcore_amd as kc
+import oracle
+from tests import ggml_graph as gg
+from tests import kq
+
+pytestmark = pytest.mark.gpu
+O = oracle.lib()
+
+
+def note(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def runtime():
+    kc.init()
+    yield
+    kc.synchronize()
+
+
+class Layer:
+    """A layer graph over device memory with seeded contents: weights (N(0, 0.02) quantized to K-quant
+    blocks, uploaded through kcWeightSetTensor), norm weights, the token inputs, and a cache holding p0
+    earlier rows."""
+
+    def __init__(self, shape, N, p0, seed):
+        self.s, self.N, self.p0, self.n_kv = shape, N, p0, p0 + N
+        self.bufs = {}
+        self.g = gg.Graph(self._alloc)
+        self.t = gg.llama_layer(self.g, shape, N, self.n_kv)
+        s, t = shape, self.t
+        self.blocks = {}
+        for i, name in enumerate(("wq", "wk", "wv", "wo", "wg", "wu", "wd")):
+            w = t[name]
+            qt, k, rows = s.types[name], w.ne[0], w.ne[1]
+            # N(0, 0.02) quantized as ggml does: activations and attention scores of a real model's size
+            # (random block bytes make scores of ~1e5, where the softmax is too sharp to compare)
+            self.blocks[name] = oracle.quantize_weights(O, qt, kq.randn(rows * k, seed + i, 0.02), rows, k)
+            kc.weight_set(qt, rows, k, w.data, self.blocks[name])
+        self.attn_norm = kq.uniform(s.n_embd, seed + 10, 0.5, 1.5)
+        self.ffn_norm = kq.uniform(s.n_embd, seed + 11, 0.5, 1.5)
+        self.put("attn_norm", self.attn_norm)
+        self.put("ffn_norm", self.ffn_norm)
+        pos = np.arange(p0, p0 + N, dtype=np.int32)
+        self.pos = pos
+        self.put("pos", pos)
+        self.put("kv_idx", pos.astype(np.int64))
+        n_pad = t["mask"].ne[0]
+        m = np.full((N, n_pad), -np.inf, np.float16)
+        for i in range(N):
+            m[i, :p0 + i + 1] = 0.0
+        self.mask = m.reshape(-1).view(np.uint16)
+        self.put("mask", self.mask)
+        if t["ff"] is not None:
+            self.ff = kq.uniform(s.hd // 2, seed + 12, 1.0, 4.0)
+            self.put("ff", self.ff)
+        else:
+            self.ff = np.ones(s.hd // 2, np.float32)
+        rng = np.random.default_rng(seed + 13)
+        for c in ("k_cache", "v_cache"):
+            cache = np.zeros((s.kv_size, s.kv_dim), np.float16)
+            cache[:p0] = rng.standard_normal((p0, s.kv_dim)).astype(np.float16)
+            self.put(c, cache.reshape(-1).view(np.uint16))
+        self.set_x(seed + 14)
+
+    def _alloc(self, nbytes, type_, ne):
+        if type_ in ("q4k", "q6k"):
+            nbytes = kc.weight_alloc_size(type_, ne[1], ne[0])
+        b = kc.Buffer(nbytes)
+        self.bufs[b.ptr] = b
+        return b.ptr
+
+    def put(self, name, arr):
+        a = np.ascontiguousarray(arr)
+        kc.call("kcMemcpy", self.t[name].data, a.ctypes.data, a.nbytes, kc.HOST_TO_DEVICE)
+
+    def get(self, name, dtype, count=None):
+        t = self.t[name]
+        n = count if count is not None else int(np.prod([t.ne[d] for d in range(4)]))
+        out = np.empty(n, dtype)
+        kc.call("kcMemcpy", out.ctypes.data, t.data, out.nbytes, kc.DEVICE_TO_HOST)
+        return out
+
+    def set_x(self, seed):
+        self.x = kq.randn(self.s.n_embd * self.N, seed, 1.0)
+        self.put("x", self.x)
+
+    def free(self):
+        for b in self.bufs.values():
+            b.free()
+
+
+def fused_norm_oracle(x, w, n, rows, eps, a=None, b=None):
+    """The oracle's add_sumsq_f / sumsq_part + norm_mul_q8[k] (its f32 output)."""
+    nb, nsb = n // 32, n // 256
+    sq = np.zeros(rows * nb * 11, np.int32)
+    if a is not None:
+        x = np.zeros(n * rows, np.float32)
+        O.kco_add_sumsq_f(a, b, x, sq, n, rows)
+    else:
+        x = x.copy()
+        O.kco_sumsq_part(x, sq, n, rows)
+    y = np.zeros(n * rows, np.float32)
+    if rows > 1:
+        O.kco_norm_mul_q8k(x, w, y, np.zeros(rows * nsb * 85, np.int32), sq, n, rows, eps)
+    else:
+        O.kco_norm_mul_q8(x, w, y, sq, n, rows, eps)
+    return x, y
+
+
+def mul_mat_oracle(qtype, blocks, xcols, rows, k):
+    """The launches the backend makes for a MUL_MAT with default switches: one column -> quantize_q8x4
+    + matvec; a batch -> per-256 slots (quantize_cols_k) + the per-256 matmul."""
+    ncols = xcols.shape[0]
+    if ncols == 1:
+        xq, xd = oracle.quantize_q8x4(O, xcols[0])
+        y = np.zeros(rows, np.float32)
+        getattr(O, f"kco_matvec_{qtype}_q8")(blocks, xq, xd, y, rows, k)
+        return y.reshape(1, rows)
+    q = np.zeros(ncols * (k // 256 * 85), np.int32)
+    O.kco_quantize_cols_k(np.ascontiguousarray(xcols).reshape(-1), q, k, ncols)
+    y = np.zeros(rows * ncols, np.float32)
+    getattr(O, f"kco_matmul_{qtype}_q8k")(blocks, q, y, rows, k, ncols)
+    return y.reshape(ncols, rows)
+
+
+def check_mm(L, name, wname, xname, tol):
+    s = L.s
+    w = L.t[wname]
+    rows, k = w.ne[1], w.ne[0]
+    xcols = L.get(xname, np.float32).reshape(L.N, k)
+    got = L.get(name, np.float32).reshape(L.N, rows)
+    want = mul_mat_oracle(s.types[wname], L.blocks[wname], xcols, rows, k)
+    if tol == 0:
+        assert np.array_equal(kq.bits(got), kq.bits(want)), name
+    else:
+        assert kq.rel_diff(got, want) < tol, name
+
+
+def check_layer(L):
+    s, N = L.s, L.N
+    mm_tol = 1e-3 if N >= 64 else 0
+    # attention norm (fused): y bit-exact
+    _, y = fused_norm_oracle(L.x, L.attn_norm, s.n_embd, N, s.eps)
+    assert np.array_equal(kq.bits(L.get("cur", np.float32)), kq.bits(y)), "attn norm"
+    for name, w in (("q", "wq"), ("k", "wk"), ("v", "wv")):
+        check_mm(L, name, w, "cur", mm_tol)
+    # rope of q and k from the GPU's q and k
+    for src, dst, nh in (("q", "qr", s.n_head), ("k", "kr", s.n_head_kv)):
+        x = L.get(src, np.float32)
+        want = np.zeros_like(x)
+        O.kco_rope_ggml(x, want, L.pos, L.ff, s.hd, nh, N, np.log2(s.base), int(s.neox))
+        got = L.get(dst, np.float32)
+        assert np.abs(got - want).max() <= 2e-5 * max(1.0, np.abs(want).max()), dst
+    # the caches: the new rows are fp16 of the GPU's k (roped) and v, every other row untouched
+    for src, cache, before in (("kr", "k_cache", L.k_before), ("v", "v_cache", L.v_before)):
+        want = before.copy()
+        pairs = s.kv_dim // 2
+        O.kco_set_rows_f16(L.get(src, np.float32), L.pos.astype(np.int64), want, pairs, N, s.kv_dim, pairs,
+                           s.kv_size)
+        assert np.array_equal(L.get(cache, np.uint16), want), cache
+    # attention over the GPU's caches and roped q
+    d = oracle.FaDims(H=s.n_head, T=L.n_kv, D=s.hd, group=s.n_head // s.n_head_kv, tp=(L.n_kv + 7) // 8 * 8,
+                      k_row=s.kv_dim // 2, k_head=s.hd // 2, v_row=s.kv_dim // 2, v_head=s.hd // 2, N=N,
+                      q_tok=s.hd * s.n_head, q_head=s.hd, m_row=L.t["mask"].ne[0] // 2, has_mask=1, H_kv=s.n_head_kv)
+    want = np.zeros(N * s.n_head * s.hd, np.float32)
+    O.kco_flash_attn_f16(L.get("qr", np.float32), L.get("k_cache", np.uint16), L.get("v_cache", np.uint16), L.mask,
+                         want, C.byref(d), np.float32(1.0 / s.hd ** 0.5))
+    assert kq.rel_diff(L.get("attn", np.float32), want) < 2e-6, "attention"
+    check_mm(L, "o", "wo", "attn", mm_tol)
+    # residual ADD fused with the FFN norm: x = o + x_in, y = norm(x) * w, both bit-exact
+    x, y = fused_norm_oracle(None, L.ffn_norm, s.n_embd, N, s.eps, a=L.get("o", np.float32), b=L.x)
+    assert np.array_equal(kq.bits(L.get("ffn_inp", np.float32)), kq.bits(x)), "ffn_inp"
+    assert np.array_equal(kq.bits(L.get("cur2", np.float32)), kq.bits(y)), "ffn norm"
+    check_mm(L, "gate", "wg", "cur2", mm_tol)
+    check_mm(L, "up", "wu", "cur2", mm_tol)
+    g, u = L.get("gate", np.float32), L.get("up", np.float32)
+    want = np.zeros_like(g)
+    O.kco_silu_mul(g, u, want, g.size)
+    assert np.allclose(L.get("act", np.float32), want, rtol=2e-6, atol=1e-30), "swiglu"
+    check_mm(L, "down", "wd", "act", mm_tol)
+    want = L.get("down", np.float32) + L.get("ffn_inp", np.float32)
+    assert np.array_equal(kq.bits(L.get("out", np.float32)), kq.bits(want)), "out"
+
+
+CASES = [
+    ("decode", gg.LayerShape(), 1, 40, {}),
+    ("decode, NEOX rope with frequency factors, head_dim 128", gg.LayerShape(n_embd=1024, neox=True, freq_factors=True),
+     1, 300, {}),
+    ("batch of 8", gg.LayerShape(), 8, 100, {}),
+    ("batch of 64 (MFMA matmuls)", gg.LayerShape(), 64, 64, dict(attn_tokens=64)),
+]
+
+
+@pytest.mark.parametrize("graphs", [1, 0])
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_layer_graph_matches_the_oracle_node_by_node(case, graphs):
+    name, shape, N, p0, cfg = case
+    note(f"ggml layer: {name}, N={N}, p0={p0}, graphs={graphs}")
+    L = Layer(shape, N, p0, seed=300 + N)
+    L.k_before, L.v_before = L.get("k_cache", np.uint16), L.get("v_cache", np.uint16)
+    be = kc.GgmlBackend(graphs=graphs, **cfg)
+    names, _ = kc.ggml_graph_plan(L.g.nodes, graphs=graphs, **cfg)
+    be.compute(L.g.nodes)
+    st = be.stats()
+    assert st["computes"] == 1 and st["graphs_recorded"] == graphs
+    assert st["launches"] == len([n for n in names if n not in "[]"])
+    check_layer(L)
+    be.close()
+    L.free()
+
+
+def test_kept_graph_is_launched_again_for_new_inputs():
+    shape, N, p0 = gg.LayerShape(), 8, 100
+    note(f"ggml graph reuse: N={N}, p0={p0}")
+    L = Layer(shape, N, p0, seed=500)
+    graph_be, eager_be = kc.GgmlBackend(graphs=1), kc.GgmlBackend(graphs=0)
+    for trial in range(3):
+        L.set_x(600 + trial)  # new values at the same addresses
+        graph_be.compute(L.g.nodes)
+        got = L.get("out", np.float32)
+        kc.synchronize()
+        eager_be.compute(L.g.nodes)
+        want = L.get("out", np.float32)
+        assert np.array_equal(kq.bits(got), kq.bits(want)), trial
+        if trial:
+            assert not np.array_equal(kq.bits(got), kq.bits(prev)), "the output follows the input"
+        prev = got
+    st = graph_be.stats()
+    assert (st["computes"], st["graphs_recorded"], st["graphs_reused"]) == (3, 1, 2)
+    # another node list (the attention of one more token): recorded again
+    L2 = Layer(shape, N, p0 + 1, seed=500)
+    graph_be.compute(L2.g.nodes)
+    assert graph_be.stats()["graphs_recorded"] == 2
+    for b in (graph_be, eager_be):
+        b.close()
+    L.free()
+    L2.free()
+
+
+def test_unclaimed_node_is_refused_before_any_launch():
+    L = Layer(gg.LayerShape(), 9, 10, seed=700)  # 9 tokens: attention beyond attn_tokens
+    be = kc.GgmlBackend()
+    out_before = L.get("out", np.float32)
+    with pytest.raises(kc.KcError) as e:
+        be.compute(L.g.nodes)
+    assert e.value.name == "UnsupportedOperation"
+    assert np.array_equal(kq.bits(L.get("out", np.float32)), kq.bits(out_before))
+    assert be.stats()["computes"] == 0
+    be.close()
+    L.free()
