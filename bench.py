@@ -435,6 +435,8 @@ def main():
                     help="time config 1 by eager launches only (no graph capture: for kernel traces)")
     ap.add_argument("--only-model", action="store_true",
                     help="run only the config-3 matmul and the model legs (profiling); prints their JSON")
+    ap.add_argument("--only-cfg3", action="store_true",
+                    help="run only the config-3 matmul leg (counter profiles); prints its JSON")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -446,6 +448,10 @@ def main():
     props = kc.device_properties()
     note(f"# device: {props.name.decode()} ({props.worker_count} CUs)")
     mm = mdl = mdl5 = None
+    if args.only_cfg3:
+        print(json.dumps({"prefill_matmul_cfg3": prefill_matmul_run(max(args.steps // 5, 5), seed=7000, reps=reps)}),
+              flush=True)
+        return
     if args.only_model or not args.skip_model:
         mm = prefill_matmul_run(max(args.steps // 5, 5), seed=7000, reps=reps)
         note(f"# cfg3 done: {mm['achieved_tops']} TOP/s")
