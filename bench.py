@@ -218,6 +218,82 @@ def decode_bytes(w, cfg, ctx):
     return wb + kv + cfg["n_vocab"] * 4
 
 
+def ggml_backend_decode_run(cfg, n_ctx, n_decode, seed, reps, modes=(1, 0)):
+    """The drop-in path: single-token decode steps of cfg through the ggml backend core
+    (kcGgmlGraphCompute) on the graph llama.cpp builds for them (kernelcore_amd/ggml_graph.py: the
+    reference op sequence, the backend's fusions, no driver-level fusion), at context n_ctx
+    onwards. The KV view spans n_ctx + n_decode rows rounded up to 256 (llama.cpp pads n_kv so),
+    so every step has the same nodes and the backend launches its kept graph again; per step the
+    host updates the position, cache row and mask inputs (three small copies) and calls
+    graph_compute, which returns once the step has run. Weights N(0, 0.02) quantized on the device
+    (the types of kcModelTensorInfo), norms N(1, 0.05), caches zero (the step time does not depend
+    on their values). Also timed: the same steps with graphs off (launches one by one)."""
+    from kernelcore_amd import ggml_graph as gg
+
+    s = gg.LayerShape.of_model(cfg, (n_ctx + n_decode + 255) // 256 * 256)
+    n_kv = s.kv_size
+    bufs, seeds = [], iter(range(seed, seed + 10000))
+
+    def alloc(nbytes, type_, ne):
+        if type_ in ("q4k", "q6k"):
+            b = synth.quantized_stream(type_, ne[1], ne[0], next(seeds))
+        else:
+            b = kc.Buffer(nbytes)
+            if type_ == "f32" and ne[1] == 1 and ne[0] in (s.n_embd, s.hd):  # norm weights
+                kc.launch("fill_normal_f32", kc.FillNormalArgs(b.ptr, ne[0], next(seeds), 1.0, 0.05))
+            else:
+                kc.call("kcMemset", b.ptr, 0, nbytes)
+        bufs.append(b)
+        return b.ptr
+
+    t0 = time.perf_counter()
+    g = gg.Graph(alloc)
+    io, _, _, logits = gg.decoder(g, s, cfg["n_layer"], 1, n_kv)
+    kc.synchronize()
+    setup_s = time.perf_counter() - t0
+    x = np.random.default_rng(seed).standard_normal(s.n_embd).astype(np.float32)
+    kc.call("kcMemcpy", io["x"].data, x.ctypes.data, x.nbytes, kc.HOST_TO_DEVICE)
+    mask = np.full(n_kv, -np.inf, np.float16)
+
+    def step(p):
+        pos = np.array([p], np.int32)
+        kc.call("kcMemcpy", io["pos"].data, pos.ctypes.data, 4, kc.HOST_TO_DEVICE)
+        idx = pos.astype(np.int64)
+        kc.call("kcMemcpy", io["kv_idx"].data, idx.ctypes.data, 8, kc.HOST_TO_DEVICE)
+        mask[:p + 1] = 0.0
+        kc.call("kcMemcpy", io["mask"].data, mask.ctypes.data, mask.nbytes, kc.HOST_TO_DEVICE)
+        be.compute(g.nodes)
+
+    out = {"workload": f"{cfg['n_layer']}-layer decode steps at context {n_ctx}..{n_ctx + n_decode} through "
+                       f"kcGgmlGraphCompute on llama.cpp's graph ({len(g.nodes)} nodes per step, KV view of {n_kv} rows)",
+           "setup_s": round(setup_s, 1)}
+    for graphs in modes:
+        be = kc.GgmlBackend(graphs=graphs)
+        mask[:] = -np.inf
+        for p in range(n_ctx - 4, n_ctx):  # warm-up (records the kept graph)
+            step(p)
+        times = []
+        for _ in range(reps):
+            mask[:] = -np.inf
+            w0 = time.perf_counter()
+            for p in range(n_ctx, n_ctx + n_decode):
+                step(p)
+            times.append(time.perf_counter() - w0)
+        st = be.stats()
+        be.close()
+        ms = med(times) / n_decode * 1e3
+        key = "kept_graph" if graphs else "eager"
+        out[key] = {"tok_s": round(1e3 / ms, 1), "ms_per_token": round(ms, 4),
+                    "launches_per_token": round(st["launches"] / st["computes"], 1),
+                    "graphs_recorded": st["graphs_recorded"], "graphs_reused": st["graphs_reused"]}
+    lg = np.empty(s.n_vocab, np.float32)
+    kc.call("kcMemcpy", lg.ctypes.data, logits.data, lg.nbytes, kc.DEVICE_TO_HOST)
+    out["finite"] = bool(np.all(np.isfinite(lg)))
+    for b in bufs:
+        b.free()
+    return out
+
+
 def model_run(cfg, n_prompt, n_decode, seed, reps, eager=False, name=CFG4_NAME):
     """A random n_prompt-token prompt (one batched forward), then n_decode greedy decode steps
     (graph-replayed, argmax on the device). A warm-up prompt + 4 steps first (builds the decode
@@ -432,11 +508,14 @@ def main():
     ap.add_argument("--eager-decode", action="store_true",
                     help="decode with one kcModelForward per token instead of the replayed graph")
     ap.add_argument("--no-graph", action="store_true",
-                    help="time config 1 by eager launches only (no graph capture: for kernel traces)")
+                    help="time config 1 and the ggml-backend leg by eager launches only (no graph capture: for "
+                         "kernel traces)")
     ap.add_argument("--only-model", action="store_true",
                     help="run only the config-3 matmul and the model legs (profiling); prints their JSON")
     ap.add_argument("--only-cfg3", action="store_true",
                     help="run only the config-3 matmul leg (counter profiles); prints its JSON")
+    ap.add_argument("--skip-ggml", action="store_true", help="skip the ggml-backend decode leg")
+    ap.add_argument("--only-ggml", action="store_true", help="run only the ggml-backend decode leg; prints its JSON")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -447,7 +526,12 @@ def main():
     kc.init()
     props = kc.device_properties()
     note(f"# device: {props.name.decode()} ({props.worker_count} CUs)")
-    mm = mdl = mdl5 = None
+    mm = mdl = mdl5 = ggml_leg = None
+    if args.only_ggml:
+        print(json.dumps({"ggml_backend_decode_cfg4": ggml_backend_decode_run(
+            LLAMA32_3B, 512, args.decode_steps, seed=9700, reps=reps, modes=(0,) if args.no_graph else (1, 0))}),
+            flush=True)
+        return
     if args.only_cfg3:
         print(json.dumps({"prefill_matmul_cfg3": prefill_matmul_run(max(args.steps // 5, 5), seed=7000, reps=reps)}),
               flush=True)
@@ -470,8 +554,13 @@ def main():
             del w5
         if cpu:
             mm["cpu_baseline"] = cpu_matmul_cfg3(7000, 10.0)
+        if not args.skip_ggml:
+            ggml_leg = ggml_backend_decode_run(LLAMA32_3B, 512, args.decode_steps, seed=9700, reps=reps)
+            note(f"# ggml backend decode done: {ggml_leg['kept_graph']['tok_s']} tok/s (kept graph)")
     if args.only_model:
         res = {"prefill_matmul_cfg3": mm, "model_cfg4": mdl}
+        if ggml_leg:
+            res["ggml_backend_decode_cfg4"] = ggml_leg
         if mdl5:
             res["model_cfg5"] = mdl5
         print(json.dumps(res), flush=True)
@@ -537,6 +626,8 @@ def main():
         out["model_cfg4"] = mdl
     if mdl5:
         out["model_cfg5"] = mdl5
+    if ggml_leg:
+        out["ggml_backend_decode_cfg4"] = ggml_leg
     if cal:
         out["calibration"] = cal
     if cpu:

@@ -14,9 +14,10 @@
  * row vector fused into add_sumsq_f / sumsq_part + norm_mul_q8[k]_f, whose 8-bit output the next
  * MUL_MATs take; RMS_NORM + MUL otherwise one rms_norm with the weight; SWIGLU with n % 256 == 0
  * fused into silu_mul_q8[k]f -- and launches the same kernels (kcLaunchKernel names) on the
- * backend's stream, except that FLASH_ATTN_EXT runs as one flash_attn_f16 kernel (the four fa_*
- * kernels for contexts over 16384), and that a fused norm or SwiGLU whose n * rows reaches 2^24
- * (beyond the fused kernels) runs unfused. It returns once the stream has run them.
+ * backend's stream, except that FLASH_ATTN_EXT runs split over the context for up to 8 query tokens
+ * (flash_decode_f16) and as one flash_attn_f16 kernel for larger batches (the four fa_* kernels
+ * beyond 16384 positions), and that a fused norm or SwiGLU whose n * rows reaches 2^24 (beyond the
+ * fused kernels) runs unfused. It returns once the stream has run them.
  *
  * Graphs (switch on): the launches of a call are captured into a HIP graph and launched; the graph
  * is kept, and a later call with the same nodes (ops, types, shapes, strides, data pointers,

@@ -253,6 +253,23 @@ typedef struct kcFlashAttnArgs {
     float scale;
 } kcFlashAttnArgs;
 
+/* flash_decode_f16 (no reference counterpart: the same FLASH_ATTN_EXT result for a few query tokens
+ * over a long context): split over 64-position chunks, each chunk's maximum, sum of exponentials
+ * and unnormalized output in part (N * H * ceil(T / 64) * (D + 2) floats), then merged in chunk
+ * order into out[N][H][D]. D is 64 or 128 and the group (query heads per KV head) at most 8;
+ * within 2e-6 of the four fa_* kernels (another summation order). */
+typedef struct kcFlashDecodeArgs {
+    const float* q;
+    const int* k;
+    const int* v;
+    const int* mask;
+    float* out;
+    float* part;
+    const int* dims;
+    kcFaDims d;
+    float scale;
+} kcFlashDecodeArgs;
+
 /* ---- K-quant weight streams (this device's layout; no reference counterpart beyond
  * llm::ref::repackQ4K/Q6K and the ggml backend's unpack_stream, ggml-kernelcore.cpp:124-154) ----
  * Rows are grouped in tiles of 16 and super-blocks in groups of 4 (padding rows and super-blocks

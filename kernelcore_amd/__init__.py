@@ -82,6 +82,8 @@ FaExpArgs = _struct("FaExpArgs", [("s", _p), ("m", _p), ("dims", _p), ("d", FaDi
 FaValuesArgs = _struct("FaValuesArgs", [("p", _p), ("v", _p), ("out", _p), ("dims", _p), ("d", FaDims)])
 FlashAttnArgs = _struct("FlashAttnArgs", [("q", _p), ("k", _p), ("v", _p), ("mask", _p), ("out", _p), ("dims", _p),
                                           ("d", FaDims), ("scale", _f)])
+FlashDecodeArgs = _struct("FlashDecodeArgs", [("q", _p), ("k", _p), ("v", _p), ("mask", _p), ("out", _p),
+                                             ("part", _p), ("dims", _p), ("d", FaDims), ("scale", _f)])
 GetRowsKquantArgs = _struct("GetRowsKquantArgs", [("qw", _p), ("ids", _p), ("y", _p), ("qtype", _i), ("rows", _i),
                                                   ("k", _i), ("n", _i)])
 QuantizeKquantArgs = _struct("QuantizeKquantArgs", [("x", _p), ("blocks", _p), ("qtype", _i), ("rows", _i), ("k", _i)])

@@ -28,6 +28,7 @@
 #include <vector>
 
 #include "internal.hpp"
+#include "kdecode.hpp"
 #include "kernelcore/ggml_backend.h"
 #include "kernelcore/llm_kernels.h"
 #include "mul_mat_internal.hpp"
@@ -345,8 +346,10 @@ E setRows(Pass& p, const T* dst) {  // dst rows src1[r] (int64) = fp16(src0 row 
     return launch(p, "set_rows_f16", &a);
 }
 
-// FLASH_ATTN_EXT (:663-699): the dimensions as the reference derives them; one flash_attn_f16
-// kernel, or for contexts beyond its 16384 the four fa_* kernels with their scores in the scratch.
+// FLASH_ATTN_EXT (:663-699): the dimensions as the reference derives them. Up to 8 query tokens
+// (decode) the context is split over 64-position chunks (flash_decode_f16, the chunk partials in the
+// scratch); larger batches take one flash_attn_f16 kernel, or beyond its 16384 positions the four
+// fa_* kernels with their scores in the scratch.
 E flashAttn(Pass& p, const T* dst) {
     const T* q = dst->src[0];
     const T* k = dst->src[1];
@@ -369,6 +372,12 @@ E flashAttn(Pass& p, const T* dst) {
     const int* kd = static_cast<const int*>(k->data);
     const int* vd = static_cast<const int*>(v->data);
     const int* md = mask ? static_cast<const int*>(mask->data) : nullptr;
+    if (d.N <= 8 && kcamd::flashDecodeSupports(d.D, d.group) && d.q_tok % 4 == 0 && d.q_head % 4 == 0) {
+        int* part = nullptr;
+        if (E e = kcamd::mulmat::take(p.rec, kcamd::flashDecodePartFloats(d), &part); e != ok) return e;
+        const kcFlashDecodeArgs a{f32(q), kd, vd, md, f32w(dst), reinterpret_cast<float*>(part), nullptr, d, scale};
+        return launch(p, "flash_decode_f16", &a);
+    }
     if (d.T <= 16384) {
         const kcFlashAttnArgs a{f32(q), kd, vd, md, f32w(dst), nullptr, d, scale};
         return launch(p, "flash_attn_f16", &a);

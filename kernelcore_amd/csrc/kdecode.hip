@@ -991,6 +991,154 @@ __global__ __launch_bounds__(64) void attn_merge_wave_kernel(AttnDecodeArgs a) {
     if ((lane & 31) == 0) *reinterpret_cast<float2*>(a.slot + a.nq * 8 + 2 * b) = make_float2(dq, (float)sq);
 }
 
+// ---------------------------------------------------------------- split-context FLASH_ATTN_EXT
+
+// flash_decode_f16: FLASH_ATTN_EXT (fa_scores / fa_max / fa_exp / fa_values: s = scale q.k + mask,
+// softmax over the context, sum p v) for a few query tokens over a long context, split over
+// 64-position chunks so that the whole GPU takes part (the one-kernel flash_attn_f16 runs one
+// workgroup per (token, head)). Workgroup (chunk c, KV head g, token i) of 256 threads computes the
+// G query heads of g against positions [64c, 64c + 64) with the layout of attn_decode_kernel (LP
+// lanes per position, 8 values each); it writes the chunk's maximum, sum of exponentials and
+// unnormalized output to part; flash_merge_kernel combines the chunks in order with a running
+// maximum. A chunk whose positions are all masked contributes nothing.
+template <int D, int G>
+__global__ __launch_bounds__(256) void flash_decode_kernel(const float* __restrict__ q, const int* __restrict__ k,
+                                                           const int* __restrict__ v, const int* __restrict__ mask,
+                                                           float* __restrict__ part, kcFaDims d, float scale, int nch) {
+    constexpr int LP = D / 8;      // lanes per position
+    constexpr int PPI = 64 / LP;   // positions per wave instruction
+    constexpr int NI = 16 / PPI;   // instructions per wave (16 positions per wave)
+    __shared__ float sc[G][kChunk];
+    __shared__ float red[16][G * D];
+    __shared__ float mg[G], lg[G];
+    const int c = blockIdx.x, kvh = blockIdx.y, i = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int sub = lane / LP, l = lane % LP;
+    const int t0 = c * kChunk + wave * 16, tmax = d.T - 1;
+    // every load first, unconditional (rows past the context are clamped and masked below)
+    u32x4 kp[NI], vp[NI];
+    float mk[NI];
+#pragma unroll
+    for (int n = 0; n < NI; ++n) {
+        const int t = min(t0 + n * PPI + sub, tmax);
+        kp[n] = *reinterpret_cast<const u32x4*>(k + (size_t)t * d.k_row + (size_t)kvh * d.k_head + l * 4);
+        vp[n] = *reinterpret_cast<const u32x4*>(v + (size_t)t * d.v_row + (size_t)kvh * d.v_head + l * 4);
+        const uint32_t w = d.has_mask ? (uint32_t)mask[(size_t)i * d.m_row + t / 2] : 0u;
+        mk[n] = h2f((w >> ((t & 1) * 16)) & 0xFFFFu);
+    }
+    float qv[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const float4* qh = reinterpret_cast<const float4*>(q + (size_t)i * d.q_tok + (size_t)(kvh * G + g) * d.q_head + l * 8);
+        const float4 a = qh[0], b = qh[1];
+        qv[g][0] = a.x, qv[g][1] = a.y, qv[g][2] = a.z, qv[g][3] = a.w;
+        qv[g][4] = b.x, qv[g][5] = b.y, qv[g][6] = b.z, qv[g][7] = b.w;
+    }
+#pragma unroll
+    for (int n = 0; n < NI; ++n) {
+        const int tl = wave * 16 + n * PPI + sub, t = c * kChunk + tl;
+        float kf[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            kf[2 * e] = h2f(kp[n][e] & 0xFFFFu);
+            kf[2 * e + 1] = h2f(kp[n][e] >> 16);
+        }
+        float sg[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float sv = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sv += qv[g][e] * kf[e];
+            sg[g] = dppSum<LP>(sv);
+        }
+        if (l == 0)
+#pragma unroll
+            for (int g = 0; g < G; ++g) sc[g][tl] = t < d.T ? scale * sg[g] + mk[n] : -INFINITY;
+    }
+    __syncthreads();
+    for (int g = wave; g < G; g += 4) {  // one wavefront per head: lane = position
+        const float sv = sc[g][lane];
+        const float m = waveMax64(sv);
+        const float pr = sv == -INFINITY ? 0.0f : exp2f((sv - m) * kLog2e);
+        const float sum = waveSum64(pr);
+        sc[g][lane] = pr;
+        if (lane == 0) {
+            mg[g] = m;
+            lg[g] = sum;
+        }
+    }
+    __syncthreads();
+    float acc[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
+#pragma unroll
+    for (int n = 0; n < NI; ++n) {
+        const int tl = wave * 16 + n * PPI + sub;
+        float vf[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            vf[2 * e] = h2f(vp[n][e] & 0xFFFFu);
+            vf[2 * e + 1] = h2f(vp[n][e] >> 16);
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float pr = sc[g][tl];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[g][e] += pr * vf[e];
+        }
+    }
+    // the position slots through LDS, one row of 16 lanes per LDS row (for D = 64 the two slots of
+    // a row are added first), summed in row order
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float a = acc[g][e];
+            if (LP == 8) a += dppMove<0x128>(a);  // row_ror:8
+            if (LP == 16 || (lane & 8) == 0) red[wave * 4 + (lane >> 4)][g * D + l * 8 + e] = a;
+        }
+    __syncthreads();
+    for (int x = tid; x < G * D; x += 256) {
+        float a = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) a += red[r][x];
+        const int g = x / D, h = kvh * G + g;
+        part[(((size_t)i * d.H + h) * nch + c) * (D + 2) + x % D] = a;
+    }
+    if (tid < G) {
+        float* pc = part + (((size_t)i * d.H + kvh * G + tid) * nch + c) * (D + 2);
+        pc[D] = mg[tid];
+        pc[D + 1] = lg[tid];
+    }
+}
+
+// out[i][h][:] of the chunk partials of (token i, head h) = blockIdx.x, in chunk order.
+template <int D>
+__global__ __launch_bounds__(128) void flash_merge_kernel(const float* __restrict__ part, float* __restrict__ out,
+                                                          int nch) {
+    const float* base = part + (size_t)blockIdx.x * nch * (D + 2);
+    for (int e = threadIdx.x; e < D; e += 128) {
+        float M = -INFINITY, L = 0.0f, O = 0.0f;
+        for (int c = 0; c < nch; ++c) {
+            const float* pc = base + (size_t)c * (D + 2);
+            const float m = pc[D];
+            if (m == -INFINITY) continue;  // every position of the chunk masked
+            if (m > M) {
+                const float f = exp2f((M - m) * kLog2e);
+                L *= f;
+                O *= f;
+                M = m;
+            }
+            const float f = exp2f((m - M) * kLog2e);
+            L += pc[D + 1] * f;
+            O += pc[e] * f;
+        }
+        out[(size_t)blockIdx.x * D + e] = O / L;
+    }
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------- launchers
@@ -1140,5 +1288,27 @@ int launchAttnDecode(AttnDecodeArgs a, int D, int Hkv, int max_ctx, hipStream_t 
     return fromHip(hipGetLastError(), "attn_decode");
 }
 
-}  // namespace kcamd
+bool flashDecodeSupports(int D, int G) { return (D == 64 || D == 128) && G >= 1 && G <= kMaxGroup; }
+size_t flashDecodePartFloats(const kcFaDims& d) {
+    return (size_t)d.N * d.H * ((d.T + kChunk - 1) / kChunk) * (d.D + 2);
+}
 
+int launchFlashDecode(const kcFlashDecodeArgs& a, hipStream_t s) {
+    const kcFaDims& d = a.d;
+    if (!flashDecodeSupports(d.D, d.group)) return fromHip(hipErrorInvalidValue, "flash_decode_f16: shape");
+    const int nch = (d.T + kChunk - 1) / kChunk;
+    const dim3 grid(nch, d.H_kv, d.N);
+#define KC_FD(DD, GG)                                                                                               \
+    if (d.D == DD && d.group == GG)                                                                                 \
+        hipLaunchKernelGGL((flash_decode_kernel<DD, GG>), grid, dim3(256), 0, s, a.q, a.k, a.v, a.mask, a.part, d, \
+                           a.scale, nch);
+    KC_FD(128, 1) KC_FD(128, 2) KC_FD(128, 3) KC_FD(128, 4) KC_FD(128, 5) KC_FD(128, 6) KC_FD(128, 7) KC_FD(128, 8)
+    KC_FD(64, 1) KC_FD(64, 2) KC_FD(64, 3) KC_FD(64, 4) KC_FD(64, 5) KC_FD(64, 6) KC_FD(64, 7) KC_FD(64, 8)
+#undef KC_FD
+    if (int e = fromHip(hipGetLastError(), "flash_decode_f16")) return e;
+    if (d.D == 128) hipLaunchKernelGGL(flash_merge_kernel<128>, dim3(d.N * d.H), dim3(128), 0, s, a.part, a.out, nch);
+    else hipLaunchKernelGGL(flash_merge_kernel<64>, dim3(d.N * d.H), dim3(128), 0, s, a.part, a.out, nch);
+    return fromHip(hipGetLastError(), "flash_decode_f16: merge");
+}
+
+}  // namespace kcamd

@@ -5,6 +5,8 @@
 
 #include <cstddef>
 
+#include "kernelcore/llm_kernels.h"
+
 namespace kcamd {
 
 // Prologue: where the matvec's activations come from.
@@ -79,5 +81,9 @@ size_t attnDecodePartFloats(int Hkv, int max_ctx, int D);
 // seq_merge: the merge in one workgroup per KV head with one thread per block quantizing (the
 // first form, kept as a diagnostic); else one wavefront per 64 outputs (same results, bit for bit).
 int launchAttnDecode(AttnDecodeArgs a, int D, int Hkv, int max_ctx, hipStream_t s, bool seq_merge = false);
+// flash_decode_f16 (kcFlashDecodeArgs): the split-context FLASH_ATTN_EXT for D 64 / 128, group <= 8.
+bool flashDecodeSupports(int D, int G);
+size_t flashDecodePartFloats(const kcFaDims& d);
+int launchFlashDecode(const kcFlashDecodeArgs& a, hipStream_t s);
 
 }  // namespace kcamd

@@ -15,6 +15,7 @@
 #include "kquant.hpp"
 #include "launch.hpp"
 #include "kquantize.hpp"
+#include "kdecode.hpp"
 #include "model_kernels.hpp"
 
 namespace {
@@ -377,6 +378,21 @@ int flashValidate(const void* p, const kcLaunchContext*) {
 }
 int flashLaunch(const void* p, void* s) { return kcamd::launchFlashAttn(*static_cast<const kcFlashAttnArgs*>(p), hs(s)); }
 
+int flashDecodeValidate(const void* p, const kcLaunchContext*) {
+    const auto& a = *static_cast<const kcFlashDecodeArgs*>(p);
+    KC_TRY(faShape(a.d, a.dims));
+    if (!kcamd::flashDecodeSupports(a.d.D, a.d.group)) return invalid("flash_decode_f16: D must be 64 or 128, group at most 8");
+    if (a.d.q_head % 4 || a.d.q_tok % 4) return invalid("flash_decode_f16: q rows and heads at 16-byte strides");
+    KC_TRY(faQMask(a.d, a.q, a.mask));
+    KC_TRY(checkRange(a.k, faCacheBytes(a.d, a.d.k_row, a.d.k_head), "k"));
+    KC_TRY(checkRange(a.v, faCacheBytes(a.d, a.d.v_row, a.d.v_head), "v"));
+    KC_TRY(checkRange(a.part, kcamd::flashDecodePartFloats(a.d) * sizeof(float), "part"));
+    return checkRange(a.out, f32Bytes(int64_t(a.d.N) * a.d.H * a.d.D), "out");
+}
+int flashDecodeLaunch(const void* p, void* s) {
+    return kcamd::launchFlashDecode(*static_cast<const kcFlashDecodeArgs*>(p), hs(s));
+}
+
 // ---- repack_kquant / unpack_kquant: ggml blocks <-> this device's weight stream
 
 template <bool Unpack>
@@ -471,6 +487,7 @@ const kcKernelEntry kTable[] = {
     {"fa_exp", faExpValidate, faExpLaunch, 1},
     {"fa_values", faValuesValidate, faValuesLaunch, 1},
     {"flash_attn_f16", flashValidate, flashLaunch, 0},
+    {"flash_decode_f16", flashDecodeValidate, flashDecodeLaunch, 0},
     {"repack_kquant", repackValidate<false>, repackLaunch<false>, 0},
     {"unpack_kquant", repackValidate<true>, repackLaunch<true>, 0},
     {"get_rows_kquant", getRowsValidate, getRowsLaunch, 0},

@@ -1,7 +1,7 @@
-"""ggml-shaped graphs of kcGgmlTensor descriptors (include/kernelcore/ggml_backend.h) for the
-backend-core tests: tensors follow ggml's conventions (ne[0] the fastest dimension, nb in bytes,
-views share their source's memory), ops get ggml's result shapes and op_params layout, and
-`finish` fills the use counts and output flags a ggml_cgraph would carry.
+"""ggml-shaped graphs of kcGgmlTensor descriptors (include/kernelcore/ggml_backend.h), to drive the
+backend core from Python (its tests and the bench): tensors follow ggml's conventions (ne[0] the
+fastest dimension, nb in bytes, views share their source's memory), ops get ggml's result shapes
+and op_params layout, and `finish` fills the use counts and output flags a ggml_cgraph would carry.
 
 `llama_layer` builds one transformer layer the way llama.cpp's graph does with flash attention
 on (the attention block: RMS_NORM + MUL, MUL_MAT q/k/v, RESHAPE, ROPE, SET_ROWS of k and v into
@@ -141,60 +141,126 @@ def _bname(t):
 
 class LayerShape:
     def __init__(self, n_embd=512, n_head=8, n_head_kv=2, n_ff=1024, kv_size=512, eps=1e-5, base=500000.0,
-                 neox=False, wq="q4k", wk="q4k", wv="q6k", wo="q4k", wg="q4k", wu="q4k", wd="q6k", freq_factors=False):
+                 neox=False, wq="q4k", wk="q4k", wv="q6k", wo="q4k", wg="q4k", wu="q4k", wd="q6k", freq_factors=False,
+                 head_dim=None, qk_norm=False, n_vocab=0):
         self.n_embd, self.n_head, self.n_head_kv, self.n_ff = n_embd, n_head, n_head_kv, n_ff
-        self.hd = n_embd // n_head
+        self.hd = head_dim or n_embd // n_head
+        self.q_dim = self.hd * n_head
         self.kv_dim = self.hd * n_head_kv
         self.kv_size, self.eps, self.base, self.neox = kv_size, eps, base, neox
         self.types = dict(wq=wq, wk=wk, wv=wv, wo=wo, wg=wg, wu=wu, wd=wd)
-        self.freq_factors = freq_factors
+        self.freq_factors, self.qk_norm, self.n_vocab = freq_factors, qk_norm, n_vocab
+
+    @classmethod
+    def of_model(cls, cfg, kv_size):
+        """The shape of a kc.Model config dict (n_layer, n_embd, n_head, ...)."""
+        return cls(n_embd=cfg["n_embd"], n_head=cfg["n_head"], n_head_kv=cfg["n_head_kv"], n_ff=cfg["n_ff"],
+                   kv_size=kv_size, eps=cfg["norm_eps"], base=cfg["rope_theta"], neox=bool(cfg["rope_neox"]),
+                   head_dim=cfg["head_dim"], qk_norm=bool(cfg["qk_norm"]), n_vocab=cfg["n_vocab"])
 
 
-def llama_layer(g, s, n_tokens, n_kv):
-    """One layer over n_tokens new tokens whose keys go to cache rows given by `kv_idx`, attending over
-    the first n_kv rows of the cache. Returns the named tensors (leaves and nodes)."""
-    N, t = n_tokens, {}
-    t["x"] = g.leaf("f32", [s.n_embd, N])
-    t["pos"] = g.leaf("i32", [N])
-    t["kv_idx"] = g.leaf("i64", [N])
-    n_kv_pad = (n_kv + 1) // 2 * 2
-    t["mask"] = g.leaf("f16", [n_kv_pad, N])
+def inputs(g, s, n_tokens, n_kv):
+    """The graph inputs of a step over n_tokens tokens attending over n_kv cache rows: the token
+    embeddings (GET_ROWS runs on the CPU backend, which hands its output over), the positions, the
+    cache rows the new keys go to, and the f16 causal mask (rows padded to an even count)."""
+    N = n_tokens
+    t = {"x": g.leaf("f32", [s.n_embd, N]), "pos": g.leaf("i32", [N]), "kv_idx": g.leaf("i64", [N]),
+         "mask": g.leaf("f16", [(n_kv + 1) // 2 * 2, N])}
     t["ff"] = g.leaf("f32", [s.hd // 2]) if s.freq_factors else None
-    for name, (rows, k) in dict(wq=(s.n_embd, s.n_embd), wk=(s.kv_dim, s.n_embd), wv=(s.kv_dim, s.n_embd),
-                                wo=(s.n_embd, s.n_embd), wg=(s.n_ff, s.n_embd), wu=(s.n_ff, s.n_embd),
+    return t
+
+
+def layer_weights(g, s):
+    """One layer's weights (the backend's weight buffers) and its fp16 K / V caches (its KV buffers)."""
+    t = {}
+    for name, (rows, k) in dict(wq=(s.q_dim, s.n_embd), wk=(s.kv_dim, s.n_embd), wv=(s.kv_dim, s.n_embd),
+                                wo=(s.n_embd, s.q_dim), wg=(s.n_ff, s.n_embd), wu=(s.n_ff, s.n_embd),
                                 wd=(s.n_embd, s.n_ff)).items():
         t[name] = g.leaf(s.types[name], [k, rows], buffer="weights")
     t["attn_norm"] = g.leaf("f32", [s.n_embd], buffer="weights")
     t["ffn_norm"] = g.leaf("f32", [s.n_embd], buffer="weights")
+    if s.qk_norm:
+        t["q_norm"] = g.leaf("f32", [s.hd], buffer="weights")
+        t["k_norm"] = g.leaf("f32", [s.hd], buffer="weights")
     t["k_cache"] = g.leaf("f16", [s.kv_dim, s.kv_size], buffer="kv")
     t["v_cache"] = g.leaf("f16", [s.kv_dim, s.kv_size], buffer="kv")
+    return t
 
-    t["norm"] = g.rms_norm(t["x"], s.eps)
-    t["cur"] = g.mul(t["norm"], t["attn_norm"])
-    t["q"] = g.mul_mat(t["wq"], t["cur"])
-    t["k"] = g.mul_mat(t["wk"], t["cur"])
-    t["v"] = g.mul_mat(t["wv"], t["cur"])
+
+def layer(g, s, x, io, w, n_tokens, n_kv, last_only=False):
+    """One transformer layer on x (a [n_embd, N] tensor) in llama.cpp's order; returns its nodes.
+    last_only: the output-row selection of the last layer (llama.cpp's GET_ROWS of the output rows,
+    which the CPU backend runs; here a view of the last row): after the attention projection only
+    the last token's row continues through the residual ADD and the FFN."""
+    N, t = n_tokens, dict(w)
+    t["norm"] = g.rms_norm(x, s.eps)
+    t["cur"] = g.mul(t["norm"], w["attn_norm"])
+    t["q"] = g.mul_mat(w["wq"], t["cur"])
+    t["k"] = g.mul_mat(w["wk"], t["cur"])
+    t["v"] = g.mul_mat(w["wv"], t["cur"])
     t["q3"] = g.reshape(t["q"], [s.hd, s.n_head, N])
-    t["qr"] = g.rope(t["q3"], t["pos"], s.hd, s.neox, s.base, t["ff"])
     t["k3"] = g.reshape(t["k"], [s.hd, s.n_head_kv, N])
-    t["kr"] = g.rope(t["k3"], t["pos"], s.hd, s.neox, s.base, t["ff"])
+    q3, k3 = t["q3"], t["k3"]
+    if s.qk_norm:  # Qwen3: RMS norm of each head's q and k with their own weights, before RoPE
+        t["qn"] = g.mul(g.rms_norm(q3, s.eps), w["q_norm"])
+        t["kn"] = g.mul(g.rms_norm(k3, s.eps), w["k_norm"])
+        q3, k3 = t["qn"], t["kn"]
+    t["qr"] = g.rope(q3, io["pos"], s.hd, s.neox, s.base, io["ff"])
+    t["kr"] = g.rope(k3, io["pos"], s.hd, s.neox, s.base, io["ff"])
     t["kr2"] = g.reshape(t["kr"], [s.kv_dim, N])
-    t["k_set"] = g.set_rows(t["k_cache"], t["kr2"], t["kv_idx"])
-    t["v_set"] = g.set_rows(t["v_cache"], t["v"], t["kv_idx"])
+    t["k_set"] = g.set_rows(w["k_cache"], t["kr2"], io["kv_idx"])
+    t["v_set"] = g.set_rows(w["v_cache"], t["v"], io["kv_idx"])
     row = s.kv_dim * 2
     t["k_view"] = g.view(t["k_set"], [s.hd, n_kv, s.n_head_kv, 1], [2, row, s.hd * 2, row * n_kv])
     t["v_view"] = g.view(t["v_set"], [s.hd, n_kv, s.n_head_kv, 1], [2, row, s.hd * 2, row * n_kv])
     t["q_perm"] = g.permute(t["qr"], [0, 2, 1, 3])
-    t["attn"] = g.flash_attn_ext(t["q_perm"], t["k_view"], t["v_view"], t["mask"], 1.0 / s.hd ** 0.5)
-    t["attn2"] = g.reshape(t["attn"], [s.n_embd, N])
-    t["o"] = g.mul_mat(t["wo"], t["attn2"])
-    t["ffn_inp"] = g.add(t["o"], t["x"])
+    t["attn"] = g.flash_attn_ext(t["q_perm"], t["k_view"], t["v_view"], io["mask"], 1.0 / s.hd ** 0.5)
+    t["attn2"] = g.reshape(t["attn"], [s.q_dim, N])
+    t["o"] = g.mul_mat(w["wo"], t["attn2"])
+    o, res = t["o"], x
+    if last_only and N > 1:
+        row = s.n_embd * 4
+        o = t["o_last"] = g.view(t["o"], [s.n_embd, 1], [4, row, row, row], (N - 1) * row)
+        res = t["x_last"] = g.view(x, [s.n_embd, 1], [4, row, row, row], (N - 1) * row)
+    t["ffn_inp"] = g.add(o, res)
     t["norm2"] = g.rms_norm(t["ffn_inp"], s.eps)
-    t["cur2"] = g.mul(t["norm2"], t["ffn_norm"])
-    t["gate"] = g.mul_mat(t["wg"], t["cur2"])
-    t["up"] = g.mul_mat(t["wu"], t["cur2"])
+    t["cur2"] = g.mul(t["norm2"], w["ffn_norm"])
+    t["gate"] = g.mul_mat(w["wg"], t["cur2"])
+    t["up"] = g.mul_mat(w["wu"], t["cur2"])
     t["act"] = g.swiglu(t["gate"], t["up"])
-    t["down"] = g.mul_mat(t["wd"], t["act"])
+    t["down"] = g.mul_mat(w["wd"], t["act"])
     t["out"] = g.add(t["down"], t["ffn_inp"])
+    return t
+
+
+def llama_layer(g, s, n_tokens, n_kv):
+    """One layer over n_tokens new tokens whose keys go to the cache rows given by `kv_idx`,
+    attending over the first n_kv rows of the cache. Returns the named tensors (leaves and nodes)."""
+    io = inputs(g, s, n_tokens, n_kv)
+    w = layer_weights(g, s)
+    t = layer(g, s, io["x"], io, w, n_tokens, n_kv)
+    t.update(io)
     g.finish(outputs=[t["out"]])
     return t
+
+
+def decoder(g, s, n_layer, n_tokens, n_kv, weights=None):
+    """n_layer layers, the output norm and the head (the last token's logits, [n_vocab, 1]: the last
+    layer keeps only the output row after its attention, as llama.cpp does); weights: an optional
+    dict of layer_weights ("layers") and the "output_norm" / "output" leaves to build the step over
+    existing weights and caches. Returns (io, weights, layers, logits)."""
+    io = inputs(g, s, n_tokens, n_kv)
+    if weights is None:
+        weights = {"layers": [layer_weights(g, s) for _ in range(n_layer)],
+                   "output_norm": g.leaf("f32", [s.n_embd], buffer="weights"),
+                   "output": g.leaf("q6k", [s.n_embd, s.n_vocab], buffer="weights")}
+    x, layers = io["x"], []
+    for l in range(n_layer):
+        t = layer(g, s, x, io, weights["layers"][l], n_tokens, n_kv, last_only=l == n_layer - 1)
+        layers.append(t)
+        x = t["out"]
+    norm = g.rms_norm(x, s.eps)
+    cur = g.mul(norm, weights["output_norm"])
+    logits = g.mul_mat(weights["output"], cur)
+    g.finish(outputs=[logits])
+    return io, weights, layers, logits

@@ -81,7 +81,8 @@ STRUCTS = ["VectorAddArgs", "QuantizeArgs", "MatvecQ4Q8Args", "MatmulKQ8Args", "
            "RmsNormArgs", "MulRowsArgs", "RopeGgmlArgs", "AddSumsqFArgs", "SumsqPartArgs", "NormMulQ8Args",
            "SiluMulQ8FArgs",
            "SiluMulArgs", "SetRowsF16Args", "FaDims", "FaScoresArgs", "FaMaxArgs", "FaExpArgs", "FaValuesArgs",
-           "KquantRepackArgs", "GetRowsKquantArgs", "QuantizeKquantArgs", "FillNormalArgs", "FlashAttnArgs", "DeviceProperties",
+           "KquantRepackArgs", "GetRowsKquantArgs", "QuantizeKquantArgs", "FillNormalArgs", "FlashAttnArgs", "FlashDecodeArgs",
+           "DeviceProperties",
            "MulMatConfig", "MulMatNode", "MulMatPlan", "MulMatNormNode", "MulMatSwigluNode", "GgmlTensor",
            "GgmlConfig", "GgmlStats"]
 

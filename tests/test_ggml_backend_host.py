@@ -11,7 +11,7 @@ ADD whose result the norm does not read) turns the fusion off."""
 import pytest
 
 import kernelcore_amd as kc
-from tests import ggml_graph as gg
+from kernelcore_amd import ggml_graph as gg
 
 
 def layer(N=1, n_kv=None, shape=None, **kw):
@@ -24,7 +24,7 @@ def plan(g, **cfg):
     return kc.ggml_graph_plan(g.nodes, **cfg)[0]
 
 
-ATTN = ["rope_ggml", "rope_ggml", "set_rows_f16", "set_rows_f16", "flash_attn_f16"]
+ATTN = ["rope_ggml", "rope_ggml", "set_rows_f16", "set_rows_f16", "flash_decode_f16"]
 
 
 # ---- graph_compute's walk --------------------------------------------------------------------------------------
@@ -57,7 +57,8 @@ def test_batch_layer_plans(N, cfg, mm, quant):
     k = "q8k" if quant == "quantize_cols_k" else "q8"
     norm = "norm_mul_q8k_f" if k == "q8k" else "norm_mul_q8_f"
     silu = "silu_mul_q8kf" if k == "q8k" else "silu_mul_q8x4f"
-    want = (["sumsq_part", norm, "[", mm.format("q4k"), mm.format("q4k"), mm.format("q6k"), "]"] + ATTN +
+    attn = ATTN if N <= 8 else ATTN[:4] + ["flash_attn_f16"]  # batches past 8 tokens: the one-kernel form
+    want = (["sumsq_part", norm, "[", mm.format("q4k"), mm.format("q4k"), mm.format("q6k"), "]"] + attn +
             [quant, mm.format("q4k"), "add_sumsq_f", norm, "[", mm.format("q4k"), mm.format("q4k"), "]", silu,
              mm.format("q6k"), "vector_add"])
     assert plan(g, **cfg) == want
@@ -159,11 +160,18 @@ def test_swiglu_unfused_when_rows_are_not_a_multiple_of_256():
     assert plan(g) == ["silu_mul"]
 
 
-def test_long_context_attention_takes_the_four_kernels():
+def test_decode_attention_is_split_over_the_context():
     g, _ = layer(N=1, n_kv=20000, kv_size=20480)
     names, ints = kc.ggml_graph_plan(g.nodes)
+    assert names[9:12] == ["set_rows_f16", "set_rows_f16", "flash_decode_f16"]
+    assert ints >= 8 * 313 * 66  # the partials of 8 heads x 313 chunks x (64 values + max + sum)
+
+
+def test_long_context_batch_attention_takes_the_four_kernels():
+    g, _ = layer(N=12, n_kv=20000, kv_size=20480)
+    names, ints = kc.ggml_graph_plan(g.nodes, attn_tokens=16)
     assert names[9:15] == ["set_rows_f16", "set_rows_f16", "fa_scores", "fa_max", "fa_exp", "fa_values"]
-    assert ints >= 8 * 20000  # the scores of 8 heads in the scratch
+    assert ints >= 8 * 12 * 20000  # the scores of 8 heads x 12 tokens in the scratch
 
 
 def test_fused_producers_beyond_their_limit_run_unfused():
@@ -202,7 +210,9 @@ def test_disabled_claims_nothing_and_makes_no_backend():
 
 def test_scratch_requirement():
     g, _ = layer(N=1)
-    assert kc.ggml_graph_plan(g.nodes)[1] == 880  # four per-32 slots of 512 or 1024 values (11 ints per 32)
+    # four per-32 slots of 512 or 1024 values (11 ints per 32: 880), the attention partials of 8 heads x
+    # 1 chunk x (64 values + max + sum) = 528
+    assert kc.ggml_graph_plan(g.nodes)[1] == 880 + 528
 
 
 # ---- supports_op ---------------------------------------------------------------------------------------------

@@ -1,6 +1,6 @@
 """The ggml backend core (include/kernelcore/ggml_backend.h) on the GPU: graph_compute
 (integrations/llama.cpp/ggml/src/ggml-kernelcore/ggml-kernelcore.cpp:706-792) over the layer graph
-llama.cpp builds (tests/ggml_graph.py), every node's output checked against the oracle on the
+llama.cpp builds (kernelcore_amd/ggml_graph.py), every node's output checked against the oracle on the
 GPU's own inputs to that node, so that each op is held to its own bar and nothing compounds:
   - [ADD +] RMS_NORM + MUL (fused): bit-exact against the oracle's fused restatement;
   - MUL_MAT q/k/v, o, gate/up, down: the oracle's quantizer and product on the node's f32 input --
@@ -19,7 +19,8 @@ import pytest
 
 import kernelcore_amd as kc
 import oracle
-from tests import ggml_graph as gg
+from kernelcore_amd import ggml_graph as gg
+from oracle.model import OracleModel
 from tests import kq
 
 pytestmark = pytest.mark.gpu
@@ -269,3 +270,132 @@ def test_unclaimed_node_is_refused_before_any_launch():
     assert be.stats()["computes"] == 0
     be.close()
     L.free()
+
+
+# ---- a whole decoder through the backend against the model driver ---------------------------------
+
+LLAMA = dict(n_layer=2, n_embd=512, n_head=8, n_head_kv=2, head_dim=64, n_ff=1024, n_vocab=1024, norm_eps=1e-5,
+             rope_theta=500000.0, rope_neox=0, qk_norm=0, max_ctx=256, max_batch=128)
+QWEN = dict(n_layer=2, n_embd=512, n_head=4, n_head_kv=2, head_dim=128, n_ff=768, n_vocab=1536, norm_eps=1e-6,
+            rope_theta=1000000.0, rope_neox=1, qk_norm=1, max_ctx=256, max_batch=128)
+LAYER_IDS = dict(attn_norm=3, wq=4, wk=5, wv=6, wo=7, ffn_norm=8, wg=9, wu=10, wd=11, q_norm=12, k_norm=13)
+
+
+class BackendDecoder:
+    """The model's weights in the backend's buffers (kcWeightSetTensor) and its KV caches; step(tokens)
+    builds llama.cpp's graph for those tokens at the current position and runs kcGgmlGraphCompute."""
+
+    def __init__(self, cfg, weights, be):
+        self.cfg, self.be = cfg, be
+        self.s = gg.LayerShape.of_model(cfg, cfg["max_ctx"])
+        self.bufs = []
+        wg = gg.Graph(self._alloc)
+        self.W = {"layers": [gg.layer_weights(wg, self.s) for _ in range(cfg["n_layer"])],
+                  "output_norm": wg.leaf("f32", [self.s.n_embd], buffer="weights"),
+                  "output": wg.leaf("q6k", [self.s.n_embd, self.s.n_vocab], buffer="weights")}
+        self.keep = wg
+        for l, lw in enumerate(self.W["layers"]):
+            for name, tid in LAYER_IDS.items():
+                if name in lw:
+                    self._set(lw[name], weights[(tid, l)])
+            for c in ("k_cache", "v_cache"):
+                kc.call("kcMemset", lw[c].data, 0, self.s.kv_dim * self.s.kv_size * 2)
+        self._set(self.W["output_norm"], weights[(1, -1)])
+        self._set(self.W["output"], weights[(2, -1)])
+        self.embd = oracle.dequant(O, "q4k", weights[(0, -1)], cfg["n_vocab"], cfg["n_embd"]).reshape(
+            cfg["n_vocab"], cfg["n_embd"])
+        self.pos = 0
+
+    def _alloc(self, nbytes, type_, ne):
+        if type_ in ("q4k", "q6k"):
+            nbytes = kc.weight_alloc_size(type_, ne[1], ne[0])
+        b = kc.Buffer(nbytes)
+        self.bufs.append(b)
+        return b.ptr
+
+    def _set(self, t, data):
+        names = {v: k for k, v in kc.GGML_TYPE.items()}
+        qt = names[t.type]
+        if qt in ("q4k", "q6k"):
+            kc.weight_set(qt, t.ne[1], t.ne[0], t.data, data)
+        else:
+            a = np.ascontiguousarray(data)
+            kc.call("kcMemcpy", t.data, a.ctypes.data, a.nbytes, kc.HOST_TO_DEVICE)
+
+    def step(self, tokens):
+        N, p0 = len(tokens), self.pos
+        n_kv = p0 + N
+        step_bufs = len(self.bufs)
+        g = gg.Graph(self._alloc)
+        io, _, _, logits = gg.decoder(g, self.s, self.cfg["n_layer"], N, n_kv, weights=self.W)
+        put = lambda t, a: kc.call("kcMemcpy", t.data, np.ascontiguousarray(a).ctypes.data, a.nbytes,
+                                   kc.HOST_TO_DEVICE)
+        put(io["x"], self.embd[np.asarray(tokens)].astype(np.float32))
+        pos = np.arange(p0, p0 + N, dtype=np.int32)
+        put(io["pos"], pos)
+        put(io["kv_idx"], pos.astype(np.int64))
+        m = np.full((N, io["mask"].ne[0]), -np.inf, np.float16)
+        for i in range(N):
+            m[i, :p0 + i + 1] = 0.0
+        put(io["mask"], m)
+        self.be.compute(g.nodes)
+        out = np.empty(self.s.n_vocab, np.float32)  # the last token's logits
+        kc.call("kcMemcpy", out.ctypes.data, logits.data, out.nbytes, kc.DEVICE_TO_HOST)
+        for b in self.bufs[step_bufs:]:
+            b.free()
+        del self.bufs[step_bufs:]
+        self.pos += N
+        return out
+
+    def free(self):
+        for b in self.bufs:
+            b.free()
+
+
+def rel_l2(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return np.linalg.norm(a - b) / np.linalg.norm(b)
+
+
+@pytest.mark.parametrize("name,cfg", [("llama", LLAMA), ("qwen3", QWEN)])
+def test_decoder_graph_matches_the_model_driver(name, cfg):
+    """Two layers, the output norm and the head as llama.cpp's graph through kcGgmlGraphCompute,
+    against kcModelForward and the oracle model on the same weights (N(0, 0.02) quantized as ggml
+    does): a 20-token prompt in steps of up to 8 tokens (the backend's attention batch), then 4
+    single tokens. The paths sum attention in different orders, and a per-32 activation that sits
+    on a rounding tie flips one 8-bit value on an ulp of difference: in the Qwen3 case the second
+    decode step is such a step (the oracle itself moves by 2.7e-3 when its attention output is
+    perturbed by one ulp; the driver lands there, the backend not). So the bar is the model tests'
+    -- 1e-2 relative L2 on the logits, the q8 activation noise -- and the same greedy token;
+    typical steps agree to 2e-7."""
+    from tests.model_weights import quantized_weights
+    note(f"ggml decoder vs model driver: {name}")
+    w = quantized_weights(cfg, 11)
+    m = kc.Model(**cfg)
+    for (tid, layer), data in w.items():
+        m.set_tensor(tid, layer, data)
+    be = kc.GgmlBackend()
+    d = BackendDecoder(cfg, w, be)
+    o = OracleModel(cfg, w)
+    rng = np.random.default_rng(5)
+    prompt = rng.integers(0, cfg["n_vocab"], 20).astype(np.int32)
+    want = m.forward(prompt)
+    ref = o.forward(prompt)
+    for i in range(0, 20, 8):
+        got = d.step(prompt[i:i + 8])
+    note(f"  prompt: rel L2 {rel_l2(got, want):.2e} (vs the oracle: backend {rel_l2(got, ref):.2e}, "
+         f"driver {rel_l2(want, ref):.2e})")
+    assert rel_l2(got, want) < 1e-2 and rel_l2(got, ref) < 1e-2 and int(np.argmax(got)) == int(np.argmax(want))
+    for step in range(4):
+        t = int(np.argmax(want))
+        want = m.forward([t])
+        ref = o.forward([t])
+        got = d.step([t])
+        note(f"  decode {step}: rel L2 {rel_l2(got, want):.2e} (vs the oracle: backend {rel_l2(got, ref):.2e}, "
+             f"driver {rel_l2(want, ref):.2e})")
+        assert rel_l2(got, want) < 1e-2 and rel_l2(got, ref) < 1e-2 and int(np.argmax(got)) == int(np.argmax(want))
+    st = be.stats()
+    assert st["computes"] == 7 and st["graphs_recorded"] == 7  # every step a new node list (n_kv grows)
+    be.close()
+    d.free()
+    m.close()

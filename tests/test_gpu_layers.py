@@ -238,3 +238,40 @@ def test_layer_argument_validation():
                   m_row=4, has_mask=0, H_kv=2)  # H != H_kv * group
     assert kc.launch_status("fa_max", kc.FaMaxArgs(x.ptr, q.ptr, None, d)) == "InvalidValue"
     B.free()
+
+
+@pytest.mark.parametrize("mask", ["causal", "none", "holes"])
+@pytest.mark.parametrize("shape", [dict(), dict(H=24, H_kv=8, T=700, N=1), dict(H=32, H_kv=8, T=1300, N=2),
+                                   dict(H=8, H_kv=8, T=65, D=64, N=8), dict(H=16, H_kv=2, T=1, D=64, N=1),
+                                   dict(H=16, H_kv=2, T=64, D=128, N=5), dict(H=8, H_kv=1, T=200, D=64, N=4)])
+def test_flash_decode_split_context(mask, shape):
+    """flash_decode_f16 (the context split over 64-position chunks, merged in chunk order) against the
+    oracle's FLASH_ATTN_EXT: every group size the kernels take shapes of 1-8, D 64 and 128, one to
+    eight query tokens, contexts of one position, one chunk, one more position than a chunk and
+    1300; masks causal, absent, or with every position of the second chunk masked (a chunk that
+    contributes nothing) and random holes."""
+    note(f"flash_decode {shape} mask={mask}")
+    q, k, v, m, d, od = _fa_case(14, mask=mask != "none", **shape)
+    if mask == "holes":
+        mm = m.view(np.float16).reshape(d.N, d.tp)
+        rng = np.random.default_rng(3)
+        mm[:, 64:128] = -np.inf
+        mm[rng.random(mm.shape) < 0.2] = -np.inf
+        mm[:, 0] = 0.0  # every query keeps one position
+        m = mm.reshape(-1).view(np.uint16)
+    want = np.zeros(d.N * d.H * d.D, np.float32)
+    O.kco_flash_attn_f16(q, k, v, m, want, C.byref(od), 0.0883883)
+    B = Bufs()
+    bq, bk, bv, bm = B.of(q), B.of(k), B.of(v), B.of(m if mask != "none" else np.zeros(8, np.uint16))
+    nch = (d.T + 63) // 64
+    bp, bo = B.new(d.N * d.H * nch * (d.D + 2) * 4), B.new(want.nbytes)
+    kc.launch("flash_decode_f16", kc.FlashDecodeArgs(bq.ptr, bk.ptr, bv.ptr, bm.ptr, bo.ptr, bp.ptr, None, d, 0.0883883))
+    got = bo.download(np.float32)
+    assert np.all(np.isfinite(got))
+    assert kq.rel_diff(got, want) < 2e-6, kq.rel_diff(got, want)
+    # a part buffer one float short is refused before any launch
+    small = B.new(d.N * d.H * nch * (d.D + 2) * 4 - 4)
+    with pytest.raises(kc.KcError):
+        kc.launch("flash_decode_f16", kc.FlashDecodeArgs(bq.ptr, bk.ptr, bv.ptr, bm.ptr, bo.ptr, small.ptr, None, d,
+                                                         0.0883883))
+    B.free()
