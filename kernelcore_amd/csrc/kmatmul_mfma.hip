@@ -669,14 +669,16 @@ __global__ void act_to_f16_kernel(const int* __restrict__ xq, uint2* __restrict_
 
 constexpr int kColB = 528;  // bytes per column in LDS: 32 chunks + 1 pad chunk
 
-// LDS geometry of the fp16-activation kernel with CB column blocks of 32 per wavefront (every
-// wavefront of a workgroup covers the same 32 CB columns, each its own 32 weight rows).
-template <int CB>
+// LDS geometry of the fp16-activation kernel with CB column blocks of 32 per wavefront and NW
+// wavefronts per workgroup (every wavefront of a workgroup covers the same 32 CB columns, each its
+// own 32 weight rows, so a workgroup stages each activation tile once for 32 NW rows).
+template <int CB, int NW>
 struct HGeo {
     static constexpr int kCols = 32 * CB;                   // activation columns per workgroup
+    static constexpr int kRows = 32 * NW;                   // weight rows per workgroup
     static constexpr int kActLoads = kCols * 33 / 64;       // direct loads of 1 KB per stage
     static constexpr int kActB = kActLoads * 1024;          // the stage's activation tile
-    static constexpr int kPerWave = (kActLoads + 3) / 4;    // loads per wavefront (the last ones repeat)
+    static constexpr int kPerWave = (kActLoads + NW - 1) / NW;  // loads per wavefront (the last ones repeat)
     static constexpr int kMinB = kCols * 32;                // Q4_K min operands
     static constexpr int kBuf = kActB + kMinB + 1024;       // + column scales (one 1 KB load)
     static constexpr int kLds = 2 * kBuf;
@@ -716,38 +718,44 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t bufRes(const void* p, uint32_t
 // They are buffer loads into LDS rather than global_load_lds: the compiler counts the latter as
 // possibly LDS-side operations and then waits for every LDS read in flight (lgkmcnt(0)) before
 // each use, which serializes the A-operand reads of the K loop with the matrix ops.
-template <bool Q6, int CB>
-__device__ __forceinline__ void stageH(char* buf, const HRes& rs, const uint32_t (&goff)[HGeo<CB>::kPerWave], int s,
-                                       int wave, int lane, int col0, int ncols, int nsb, int ncp) {
-    using G = HGeo<CB>;
+// (wave is wavefront-uniform: the loads past the activation tile are issued by single wavefronts.)
+template <bool Q6, int CB, int NW>
+__device__ __forceinline__ void stageH(char* buf, const HRes& rs, const uint32_t (&goff)[HGeo<CB, NW>::kPerWave],
+                                       int s, int wave, int lane, int col0, int ncols, int nsb, int ncp) {
+    using G = HGeo<CB, NW>;
 #pragma unroll
     for (int r = 0; r < G::kPerWave; ++r) {
-        const int g = min(r * 4 + wave, G::kActLoads - 1);
+        const int g = min(r * NW + wave, G::kActLoads - 1);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs.act, (LdsPtr)(buf + g * 1024), 16, goff[r], (uint32_t)s * 512u, 0,
                                                  0);
     }
-    if constexpr (!Q6) {  // 32 columns per load; wavefronts past CB repeat the loads of wavefront wave % CB
-        const int wq = wave % CB, p = wq * 64 + lane, c = p >> 1;
-        const int cc = col0 + c < ncols ? col0 + c : 0;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs.mins, (LdsPtr)(buf + G::kActB + wq * 1024), 16,
-                                                 (uint32_t)(((cc * nsb + s) * 16 + (p & 1) * 8) * 2), 0, 0, 0);
+    if constexpr (!Q6) {  // 32 columns per load, by wavefronts NW - CB .. NW - 1
+        const int wq = wave - (NW - CB);
+        if (wq >= 0) {
+            const int p = wq * 64 + lane, c = p >> 1;
+            const int cc = col0 + c < ncols ? col0 + c : 0;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs.mins, (LdsPtr)(buf + G::kActB + wq * 1024), 16,
+                                                     (uint32_t)(((cc * nsb + s) * 16 + (p & 1) * 8) * 2), 0, 0, 0);
+        }
     }
-    // the column scales: every wavefront writes the same 1 KB (lanes past the tile repeat)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs.xd, (LdsPtr)(buf + G::kActB + G::kMinB), 16,
-                                             (uint32_t)((s * ncp + col0 + ((lane & 31) % (8 * CB)) * 4) * 4), 0, 0, 0);
+    // the column scales: one wavefront writes the 1 KB (lanes past the tile repeat)
+    if (wave == 0)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs.xd, (LdsPtr)(buf + G::kActB + G::kMinB), 16,
+                                                 (uint32_t)((s * ncp + col0 + ((lane & 31) % (8 * CB)) * 4) * 4), 0, 0,
+                                                 0);
 }
 
-// One workgroup's tile: weight rows rowTile * 128 .., columns colTile * 32 CB .., super-blocks
+// One workgroup's tile: weight rows rowTile * 32 NW .., columns colTile * 32 CB .., super-blocks
 // [sb0, sb1) of the nsb (y = the partial sum over that range).
-template <bool Q6, int CB>
+template <bool Q6, int CB, int NW>
 __device__ __forceinline__ void hTile(char* lbase, const uint8_t* __restrict__ qw, const _Float16* __restrict__ act,
                                       const _Float16* __restrict__ mins, const float* __restrict__ xdT,
                                       float* __restrict__ y, int rows, int nsb, int ncols, int ncp, int rowTile,
                                       int colTile, int sb0, int sb1) {
-    using G = HGeo<CB>;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    using G = HGeo<CB, NW>;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5, l32 = lane & 31;
-    const int row = rowTile * kBM + wave * 32 + l32;
+    const int row = rowTile * G::kRows + wave * 32 + l32;
     const int col0 = colTile * G::kCols;
     const int ngroups = (nsb + kGroupSb - 1) / kGroupSb;
     const int rows_stream = ((rows + kTileRows - 1) / kTileRows) * kTileRows;
@@ -760,7 +768,7 @@ __device__ __forceinline__ void hTile(char* lbase, const uint8_t* __restrict__ q
     uint32_t goff[G::kPerWave];
 #pragma unroll
     for (int r = 0; r < G::kPerWave; ++r) {
-        const int g = min(r * 4 + wave, G::kActLoads - 1);
+        const int g = min(r * NW + wave, G::kActLoads - 1);
         const int slot = g * 64 + lane, c = slot / 33, kc = slot - 33 * c;
         const int cc = col0 + c < ncols ? col0 + c : 0;
         goff[r] = (uint32_t)cc * (uint32_t)k * 2u + (uint32_t)(kc == 32 ? 0 : kc) * 16u;
@@ -774,21 +782,26 @@ __device__ __forceinline__ void hTile(char* lbase, const uint8_t* __restrict__ q
     const f16v zero = acc[0];
     using Rows = typename std::conditional<Q6, Rows32Q6, Rows32>::type;
     Rows wcur, wnext;
-    stageH<Q6, CB>(lbase, rs, goff, sb0, wave, lane, col0, ncols, nsb, ncp);
+    stageH<Q6, CB, NW>(lbase, rs, goff, sb0, wave, lane, col0, ncols, nsb, ncp);
     wnext.load(qw, row, rows_stream, ngroups, sb0, h);
     // this lane's A-operand byte offset in a stage for column block cb (K-step t adds 32 t)
     int aoff[CB];
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) aoff[cb] = (cb * 32 + l32) * kColB + h * 16;
 
+    // A wavefront waits at each vector-memory instruction until the CU's memory unit takes it (about
+    // 20 cycles per instruction and CU, whatever its width), so a burst of loads stalls its issuer.
+    // With 8 wavefronts the two of a SIMD (w, w + 4) leave the barrier together: the second one
+    // issues its loads at K-step 8 instead, so one of them computes while the other waits.
+    const bool late = NW == 8 && wave >= NW / 2;
     for (int s = sb0; s < sb1; ++s) {
         const int b = (s - sb0) & 1;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wavefront's loads of stage s
         __syncthreads();  // everyone's: stage s is complete, stage b ^ 1 is no longer read
         wcur = wnext;
         wcur.decode();
-        if (s + 1 < sb1) {
-            stageH<Q6, CB>(lbase + (b ^ 1) * G::kBuf, rs, goff, s + 1, wave, lane, col0, ncols, nsb, ncp);
+        if (s + 1 < sb1 && !late) {
+            stageH<Q6, CB, NW>(lbase + (b ^ 1) * G::kBuf, rs, goff, s + 1, wave, lane, col0, ncols, nsb, ncp);
             wnext.load(qw, row, rows_stream, ngroups, s + 1, h);
         }
         const char* buf = lbase + b * G::kBuf;
@@ -834,6 +847,11 @@ __device__ __forceinline__ void hTile(char* lbase, const uint8_t* __restrict__ q
             for (int cb = 0; cb < CB; ++cb) {
                 is[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[cb], bq, t == 0 ? zero : is[cb], 0, 0, 0);
                 if constexpr (Q6) is[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[cb], bq2, is[cb], 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (late && t == 8 && s + 1 < sb1) {
+                stageH<Q6, CB, NW>(lbase + (b ^ 1) * G::kBuf, rs, goff, s + 1, wave, lane, col0, ncols, nsb, ncp);
+                wnext.load(qw, row, rows_stream, ngroups, s + 1, h);
             }
             __builtin_amdgcn_sched_barrier(0);
             if (t + 1 < 16) {
@@ -896,10 +914,11 @@ __device__ __forceinline__ void hTile(char* lbase, const uint8_t* __restrict__ q
 using HPart = MfmaPart;
 using HGroup = MfmaGroup;
 
-__global__ __launch_bounds__(256) void matmul_kq_mfma_h_kernel(HGroup g, const _Float16* __restrict__ act,
-                                                               const _Float16* __restrict__ mins,
-                                                               const float* __restrict__ xdT, int nsb, int ncols,
-                                                               int ncp) {
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void matmul_kq_mfma_h_kernel(HGroup g, const _Float16* __restrict__ act,
+                                                                   const _Float16* __restrict__ mins,
+                                                                   const float* __restrict__ xdT, int nsb, int ncols,
+                                                                   int ncp) {
     extern __shared__ int4 lds4[];
     char* lbase = reinterpret_cast<char*>(lds4);
     const int bx = blockIdx.x;
@@ -907,11 +926,11 @@ __global__ __launch_bounds__(256) void matmul_kq_mfma_h_kernel(HGroup g, const _
     const HPart& p = g.p[pi];
     const int z = blockIdx.z, sb0 = z * nsb / g.ks, sb1 = (z + 1) * nsb / g.ks;
     if (p.q6)
-        hTile<true, 2>(lbase, p.qw, act, mins, xdT, p.y[z], p.rows, nsb, ncols, ncp, bx - p.tile0, blockIdx.y, sb0,
-                       sb1);
+        hTile<true, 2, NW>(lbase, p.qw, act, mins, xdT, p.y[z], p.rows, nsb, ncols, ncp, bx - p.tile0, blockIdx.y, sb0,
+                           sb1);
     else
-        hTile<false, 2>(lbase, p.qw, act, mins, xdT, p.y[z], p.rows, nsb, ncols, ncp, bx - p.tile0, blockIdx.y, sb0,
-                        sb1);
+        hTile<false, 2, NW>(lbase, p.qw, act, mins, xdT, p.y[z], p.rows, nsb, ncols, ncp, bx - p.tile0, blockIdx.y, sb0,
+                            sb1);
 }
 
 // The fp16 activation buffer: ncols * k halves, then (Q4_K) ncols * nsb * 16 halves of mins, then
@@ -921,22 +940,40 @@ size_t actBytes(int ncols, int k) {
     return (size_t)ncols * k * 2 + (size_t)ncols * (k / 256) * 32 + (size_t)(k / 256) * actCols(ncols) * 4;
 }
 
+// Wavefronts per workgroup of the fp16-activation kernel for a grid of wgs8 workgroups of 8
+// (option matmul_waves: 4, 8, or 0 = by the grid). 8 wavefronts (256 weight rows, one workgroup
+// per CU) stage each activation tile once per CU instead of once per 128 rows and stagger their
+// loads; they are taken when their grid fills the CUs in whole rounds or fits in one.
+int cuCount();
+int hWaves(long long wgs8) {
+    const int o = option("matmul_waves");
+    if (option("matmul_path") == 7 || o == 4) return 4;
+    if (o == 8) return 8;
+    const long long cus = cuCount();
+    return wgs8 <= cus || wgs8 % cus == 0 ? 8 : 4;
+}
+
 // The fp16-activation kernel over parts[0..nparts) (one conversion of the activations), K split
 // into ks ranges.
 int runMfmaH(const MmPart* parts, int nparts, const int* xq, int k, int ncols, int ks, void* act, hipStream_t s,
              const ActF16* pre = nullptr) {
-    using G = HGeo<2>;
-    static const int attr = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(matmul_kq_mfma_h_kernel),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, G::kLds);
-    if (attr != 0) return fromHip(attr, "matmul (MFMA): LDS size");
+    using G = HGeo<2, 4>;  // (the LDS geometry does not depend on the wavefront count)
+    static const int attr4 = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(matmul_kq_mfma_h_kernel<4>),
+                                                      hipFuncAttributeMaxDynamicSharedMemorySize, G::kLds);
+    static const int attr8 = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(matmul_kq_mfma_h_kernel<8>),
+                                                      hipFuncAttributeMaxDynamicSharedMemorySize, G::kLds);
+    if (attr4 != 0 || attr8 != 0) return fromHip(attr4 ? attr4 : attr8, "matmul (MFMA): LDS size");
     const int nsb = k / 256;
+    long long tiles8 = 0;
+    for (int i = 0; i < nparts; ++i) tiles8 += (parts[i].rows + 255) / 256;
+    const int nw = hWaves(tiles8 * ((ncols + G::kCols - 1) / G::kCols) * ks), wg_rows = 32 * nw;
     HGroup g{};
     bool any_q4 = false;
     int tiles = 0;
     for (int i = 0; i < nparts; ++i) {
         g.p[i] = HPart{static_cast<const uint8_t*>(parts[i].qw), {parts[i].y[0], parts[i].y[1]}, parts[i].rows,
                        parts[i].q6, tiles};
-        tiles += (parts[i].rows + kBM - 1) / kBM;
+        tiles += (parts[i].rows + wg_rows - 1) / wg_rows;
         any_q4 |= !parts[i].q6;
     }
     g.nparts = nparts;
@@ -961,8 +998,12 @@ int runMfmaH(const MmPart* parts, int nparts, const int* xq, int k, int ncols, i
     if (option("matmul_path") == 7)  // the wide-tile kernel (every weight dequantized once per workgroup)
         return launchMfmaW(g, tiles, act, mins, xdT, nsb, ncols, ncp, s);
     const dim3 grid(tiles, (ncols + G::kCols - 1) / G::kCols, ks);
-    hipLaunchKernelGGL(matmul_kq_mfma_h_kernel, grid, dim3(256), G::kLds, s, g, static_cast<const _Float16*>(act),
-                       mins, xdT, nsb, ncols, ncp);
+    if (nw == 8)
+        hipLaunchKernelGGL(matmul_kq_mfma_h_kernel<8>, grid, dim3(512), G::kLds, s, g,
+                           static_cast<const _Float16*>(act), mins, xdT, nsb, ncols, ncp);
+    else
+        hipLaunchKernelGGL(matmul_kq_mfma_h_kernel<4>, grid, dim3(256), G::kLds, s, g,
+                           static_cast<const _Float16*>(act), mins, xdT, nsb, ncols, ncp);
     return fromHip(hipGetLastError(), "matmul_q4k/q6k_q8k (MFMA)");
 }
 
@@ -996,9 +1037,9 @@ __global__ void add_partial_kernel(float* __restrict__ y, const float* __restric
     if (i < n) y[i] += p[i];
 }
 
-// A by-name launch on the fp16-activation kernel: a grid under two workgroups per CU splits K in
-// two, the second half's partial sums staged after the activations and added into y by one more
-// kernel (fl(a + b): the same for either order).
+// A by-name launch on the fp16-activation kernel: a grid under two workgroups of 4 wavefronts per
+// CU splits K in two, the second half's partial sums staged after the activations and added into
+// y by one more kernel (fl(a + b): the same for either order).
 int stagedKs(const kcMatmulKQ8Args& a) {
     const long long wgs = (long long)((a.rows + kBM - 1) / kBM) * ((a.ncols + 63) / 64);
     return (a.k / 256 >= 2 && wgs < 2LL * cuCount()) ? 2 : 1;

@@ -152,6 +152,11 @@ def test_mfma_matmul_matches_oracle(qtype, rows, k, ncols):
     x = kq.randn(k * ncols, ncols + 5, 1.5)
     kc.set_option("matmul_path", 2)
     y, _ = run_matmul(qtype, True, w, x, rows, k, ncols)
+    ys = {}
+    for nw in (4, 8):  # workgroups of 4 wavefronts (128 rows) and of 8 (256 rows, staggered loads)
+        kc.set_option("matmul_waves", nw)
+        ys[nw], _ = run_matmul(qtype, True, w, x, rows, k, ncols)
+    kc.set_option("matmul_waves", 0)
     kc.set_option("matmul_path", 1)
     yc, _ = run_matmul(qtype, True, w, x, rows, k, ncols)
     kc.set_option("matmul_path", 7)  # the wide-tile kernel (kmatmul_mfmaw.hip)
@@ -159,9 +164,11 @@ def test_mfma_matmul_matches_oracle(qtype, rows, k, ncols):
     kc.set_option("matmul_path", 0)
     want = oracle_matmul(qtype, True, w, oracle_slots(x, k, ncols, True), rows, k, ncols)
     assert np.array_equal(kq.bits(yc), kq.bits(want))  # the column-tile path stays bit-exact
-    for got in (y, yw):
+    for got in (y, ys[4], ys[8], yw):
         assert kq.rel_diff(got, want) < TOL
         assert kq.rel_diff(got, want) < 1e-5  # exact integers; only the final float combine differs
+    # the workgroup shape changes no output's arithmetic
+    assert np.array_equal(kq.bits(ys[4]), kq.bits(ys[8]))
 
 
 def test_mfma_matmul_config3_shapes():
@@ -171,10 +178,16 @@ def test_mfma_matmul_config3_shapes():
         note(f"mfma cfg3 {rows}x{k}x{ncols}")
         w = kq.random_blocks("q4k", rows, k, seed=seed)
         x = kq.randn(k * ncols, seed + 1)
-        y, slots = run_matmul("q4k", True, w, x, rows, k, ncols)
         want = np.zeros(rows * ncols, np.float32)
+        got = {}
+        for nw in (4, 8, 0):
+            kc.set_option("matmul_waves", nw)
+            got[nw], slots = run_matmul("q4k", True, w, x, rows, k, ncols)
+        kc.set_option("matmul_waves", 0)
         O.kco_matmul_q4k_q8k_mt(w, slots, want, rows, k, ncols, O.kco_max_threads())
-        assert kq.rel_diff(y, want.reshape(ncols, rows)) < TOL
+        for nw, y in got.items():
+            assert kq.rel_diff(y, want.reshape(ncols, rows)) < TOL, nw
+        assert np.array_equal(kq.bits(got[4]), kq.bits(got[8]))
 
 
 def test_captured_matmul_keeps_its_scratch_after_an_eager_growth():
