@@ -669,6 +669,107 @@ __global__ void act_to_f16_kernel(const int* __restrict__ xq, uint2* __restrict_
 
 constexpr int kColB = 528;  // bytes per column in LDS: 32 chunks + 1 pad chunk
 
+// The fp16-activation kernel's view of 32 weight rows for one super-block, loaded in whole 16-byte
+// chunks: lane -> row lane % 32 and half h = lane / 32, which takes chunk h of every pair of slabs
+// (a wavefront waits about as long for the memory unit to take a 16-byte load as an 8-byte one).
+// K-step t then covers, in lane half h, the 8 values at k = 64 (t >> 2) + 32 ((t >> 1) & 1) + 16 h
+// + 8 (t & 1) (qs bytes 32 (t >> 2) + 16 h + 8 (t & 1) .., nibble (t >> 1) & 1, sub-block t >> 1):
+// the A operand reads the activation chunk at byte 64 (t >> 1) + 32 h + 16 (t & 1) of the column,
+// so both operands of a step pair the same k.
+struct Rows32W {
+    uint4 q16[4];  // [a]: qs bytes 32a + 16h .. +15
+    uint4 hdr;     // d, dmin (fp16) and the 12 packed scale / min bytes
+    float d, dmin;
+    int scw[2], mw[2];
+    __device__ __forceinline__ void load(const uint8_t* qw, int row, int rows_stream, int ngroups, int s, int h) {
+        const bool live = row < rows_stream;
+        const int rr = live ? row : 0;
+        const int tile = rr >> 4, r = rr & 15, g = s >> 2, kq = s & 3;
+        const uint8_t* piece = qw + ((size_t)tile * ngroups + g) * kQ4kSeg + (kq * 16 + r) * 16;
+        hdr = *reinterpret_cast<const uint4*>(piece);
+#pragma unroll
+        for (int a = 0; a < 4; ++a) q16[a] = *reinterpret_cast<const uint4*>(piece + (1 + 2 * a + h) * 1024);
+    }
+    __device__ __forceinline__ void decode() {
+        d = (float)__builtin_bit_cast(_Float16, (unsigned short)(hdr.x & 0xFFFFu));
+        dmin = (float)__builtin_bit_cast(_Float16, (unsigned short)(hdr.x >> 16));
+        const int s0 = (int)hdr.y, s1 = (int)hdr.z, s2 = (int)hdr.w;
+        scw[0] = s0 & 0x3F3F3F3F;
+        mw[0] = s1 & 0x3F3F3F3F;
+        scw[1] = (s2 & 0x0F0F0F0F) | ((s0 >> 2) & 0x30303030);
+        mw[1] = ((s2 >> 4) & 0x0F0F0F0F) | ((s1 >> 2) & 0x30303030);
+    }
+    __device__ __forceinline__ _Float16 sc(int j) const { return (_Float16)(float)((scw[j >> 2] >> (8 * (j & 3))) & 255); }
+    __device__ __forceinline__ _Float16 m(int j) const { return (_Float16)(float)((mw[j >> 2] >> (8 * (j & 3))) & 255); }
+    // the 8 bytes of K-step t
+    __device__ __forceinline__ uint2 bytes(int t) const {
+        const uint4 q = q16[t >> 2];
+        return (t & 1) ? make_uint2(q.z, q.w) : make_uint2(q.x, q.y);
+    }
+};
+
+// Q6_K rows loaded in whole chunks (see Rows32W): K-step t covers, in lane half h, the 8 values
+// k = 128 n + 32 quad + 16 h + 8 p (n = t >> 3, quad = (t >> 1) & 3, p = t & 1): ql bytes
+// 64 n + 32 (quad & 1) + 16 h + 8 p .. (nibble quad >> 1), qh bytes 32 n + 16 h + 8 p .. (bits
+// 2 quad), scale of sub-block 8 n + 2 quad + h (so the two lane halves of a step scale by different
+// sub-blocks); the activation chunk is again at byte 64 (t >> 1) + 32 h + 16 p of the column.
+struct Rows32Q6W {
+    uint4 ql16[2][2];  // [n][a]: ql bytes 64n + 32a + 16h .. +15
+    uint4 qh16[2];     // [n]: qh bytes 32n + 16h .. +15
+    int sw[4];         // the 16 int8 scales
+    uint32_t dbits;    // d (fp16)
+    float d;
+    __device__ __forceinline__ void load(const uint8_t* qw, int row, int rows_stream, int ngroups, int s, int h) {
+        const bool live = row < rows_stream;
+        const int rr = live ? row : 0;
+        const int tile = rr >> 4, r = rr & 15, g = s >> 2, kq = s & 3;
+        const uint8_t* seg = qw + ((size_t)tile * ngroups + g) * kQ6kSeg;
+        const uint8_t* piece = seg + (kq * 16 + r) * 16;
+#pragma unroll
+        for (int n = 0; n < 2; ++n)
+#pragma unroll
+            for (int a = 0; a < 2; ++a) ql16[n][a] = *reinterpret_cast<const uint4*>(piece + (4 * n + 2 * a + h) * 1024);
+#pragma unroll
+        for (int n = 0; n < 2; ++n) qh16[n] = *reinterpret_cast<const uint4*>(piece + (8 + 2 * n + h) * 1024);
+        const uint4 sc = *reinterpret_cast<const uint4*>(piece + 12 * 1024);
+        sw[0] = (int)sc.x;
+        sw[1] = (int)sc.y;
+        sw[2] = (int)sc.z;
+        sw[3] = (int)sc.w;
+        dbits = *reinterpret_cast<const uint16_t*>(seg + kQ6kSlabs * 1024 + (kq * 16 + r) * 2);
+    }
+    __device__ __forceinline__ void decode() { d = (float)__builtin_bit_cast(_Float16, (unsigned short)dbits); }
+    // K-step t for activations 16 x, as Rows32Q6::dequantA16: sh (q - 32) and sl (q - 32) / 16.
+    __device__ __forceinline__ void dequantA16(int t, int h, h8& b1, h8& b2) const {
+        const int n = t >> 3, quad = (t >> 1) & 3, p = t & 1;
+        const uint4 L = ql16[n][quad & 1], H = qh16[n];
+        const uint32_t lw[2] = {p ? L.z : L.x, p ? L.w : L.y}, hw[2] = {p ? H.z : H.x, p ? H.w : H.y};
+        const int w = sw[2 * n + (quad >> 1)];
+        const int bi = 2 * (quad & 1) + h;  // this lane half's sub-block within the scale word
+        const int sh = (w << (24 - 8 * bi)) >> 28, sl = (w >> (8 * bi)) & 15;
+        const _Float16 fh = (_Float16)(short)sh, fl = (_Float16)(short)sl;
+        const h2 mh = {fh, fh}, ml = {fl * (_Float16)0.0625f, fl * (_Float16)0.0625f};
+        const h2 ch = {fh * (_Float16)(-1056.0f), fh * (_Float16)(-1056.0f)};
+        const h2 cl = {fl * (_Float16)(-66.0f), fl * (_Float16)(-66.0f)};
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t q = ((lw[i] >> (4 * (quad >> 1))) & 0x0F0F0F0Fu) | (((hw[i] >> (2 * quad)) & 0x03030303u) << 4);
+            const h2 a = bits_h2(__builtin_amdgcn_perm(0x64646464u, q, 0x04010400u));  // 1024 + q
+            const h2 b = bits_h2(__builtin_amdgcn_perm(0x64646464u, q, 0x04030402u));
+            const h2 a1 = __builtin_elementwise_fma(a, mh, ch), b1v = __builtin_elementwise_fma(b, mh, ch);
+            const h2 a2 = __builtin_elementwise_fma(a, ml, cl), b2v = __builtin_elementwise_fma(b, ml, cl);
+            b1[4 * i + 0] = a1[0];
+            b1[4 * i + 1] = a1[1];
+            b1[4 * i + 2] = b1v[0];
+            b1[4 * i + 3] = b1v[1];
+            b2[4 * i + 0] = a2[0];
+            b2[4 * i + 1] = a2[1];
+            b2[4 * i + 2] = b2v[0];
+            b2[4 * i + 3] = b2v[1];
+        }
+    }
+};
+
 // LDS geometry of the fp16-activation kernel with CB column blocks of 32 per wavefront and NW
 // wavefronts per workgroup (every wavefront of a workgroup covers the same 32 CB columns, each its
 // own 32 weight rows, so a workgroup stages each activation tile once for 32 NW rows).
@@ -780,14 +881,15 @@ __device__ __forceinline__ void hTile(char* lbase, const uint8_t* __restrict__ q
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[cb][i] = 0.0f;
     const f16v zero = acc[0];
-    using Rows = typename std::conditional<Q6, Rows32Q6, Rows32>::type;
+    using Rows = typename std::conditional<Q6, Rows32Q6W, Rows32W>::type;
     Rows wcur, wnext;
     stageH<Q6, CB, NW>(lbase, rs, goff, sb0, wave, lane, col0, ncols, nsb, ncp);
     wnext.load(qw, row, rows_stream, ngroups, sb0, h);
-    // this lane's A-operand byte offset in a stage for column block cb (K-step t adds 32 t)
+    // this lane's A-operand byte offset in a stage for column block cb (K-step t adds
+    // 64 (t >> 1) + 16 (t & 1), the k-order of Rows32W / Rows32Q6W)
     int aoff[CB];
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb) aoff[cb] = (cb * 32 + l32) * kColB + h * 16;
+    for (int cb = 0; cb < CB; ++cb) aoff[cb] = (cb * 32 + l32) * kColB + h * 32;
 
     // A wavefront waits at each vector-memory instruction until the CU's memory unit takes it (about
     // 20 cycles per instruction and CU, whatever its width), so a burst of loads stalls its issuer.
@@ -828,19 +930,20 @@ __device__ __forceinline__ void hTile(char* lbase, const uint8_t* __restrict__ q
         for (int cb = 0; cb < CB; ++cb) av[cb] = *reinterpret_cast<const h8*>(buf + aoff[cb]);
         h8 bq, bq2, bn, bn2;  // B operands of steps t and t + 1 (Q6_K: two per step)
         if constexpr (Q6)
-            wcur.dequantA16(0, bq, bq2);
+            wcur.dequantA16(0, h, bq, bq2);
         else
-            bq = dequant8s(wcur.qs[0][0], false, m2[0], s2[0]);
+            bq = dequant8s(wcur.bytes(0), false, m2[0], s2[0]);
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
             if (t + 1 < 16) {
+                const int tn = t + 1, toff = 64 * (tn >> 1) + 16 * (tn & 1);
 #pragma unroll
-                for (int cb = 0; cb < CB; ++cb) an[cb] = *reinterpret_cast<const h8*>(buf + aoff[cb] + 32 * (t + 1));
+                for (int cb = 0; cb < CB; ++cb) an[cb] = *reinterpret_cast<const h8*>(buf + aoff[cb] + toff);
                 if constexpr (Q6) {
-                    wcur.dequantA16(t + 1, bn, bn2);
+                    wcur.dequantA16(tn, h, bn, bn2);
                 } else {
-                    const int j = (t + 1) >> 1, u = (t + 1) & 1;
-                    bn = dequant8s(wcur.qs[j >> 1][u], j & 1, m2[j], s2[j]);
+                    const int j = tn >> 1;  // sub-block (nibble j & 1 of the step's bytes)
+                    bn = dequant8s(wcur.bytes(tn), j & 1, m2[j], s2[j]);
                 }
             }
 #pragma unroll
