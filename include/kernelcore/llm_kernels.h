@@ -162,6 +162,22 @@ typedef struct kcNormMulQ8Args {
     int rows;
     float eps;
 } kcNormMulQ8Args;
+/* add_norm_q8_f (no reference counterpart: add_sumsq_f, or sumsq_part when a and b are null,
+ * followed by norm_mul_q8_f, in one launch with one workgroup per row, for rows of 256 .. 8192
+ * values): x = a + b (else x is read), the per-32 sums of squares into the slot tails, then
+ * y = x * r * w and the per-32 slot q -- the same bytes as the two launches. dims: [n / 32, n, rows]. */
+typedef struct kcAddNormQ8FArgs {
+    const float* a;
+    const float* b;
+    float* x;
+    const float* w;
+    float* y;
+    int* q;
+    const int* dims;
+    int n;
+    int rows;
+    float eps;
+} kcAddNormQ8FArgs;
 typedef struct kcSiluMulQ8FArgs {
     const float* g;
     const float* u;
@@ -354,6 +370,7 @@ typedef ::kcRopeGgmlArgs RopeGgmlArgs;
 typedef ::kcAddSumsqFArgs AddSumsqFArgs;
 typedef ::kcSumsqPartArgs SumsqPartArgs;
 typedef ::kcNormMulQ8Args NormMulQ8Args;
+typedef ::kcAddNormQ8FArgs AddNormQ8FArgs;
 typedef ::kcSiluMulQ8FArgs SiluMulQ8FArgs;
 typedef ::kcSiluMulArgs SiluMulArgs;
 typedef ::kcSetRowsF16Args SetRowsF16Args;

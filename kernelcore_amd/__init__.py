@@ -68,6 +68,8 @@ AddSumsqFArgs = _struct("AddSumsqFArgs", [("a", _p), ("b", _p), ("out", _p), ("q
 SumsqPartArgs = _struct("SumsqPartArgs", [("x", _p), ("q", _p), ("dims", _p), ("n", _i), ("rows", _i)])
 NormMulQ8Args = _struct("NormMulQ8Args", [("x", _p), ("w", _p), ("y", _p), ("q", _p), ("dims", _p), ("n", _i),
                                           ("rows", _i), ("eps", _f)])
+AddNormQ8FArgs = _struct("AddNormQ8FArgs", [("a", _p), ("b", _p), ("x", _p), ("w", _p), ("y", _p), ("q", _p),
+                                            ("dims", _p), ("n", _i), ("rows", _i), ("eps", _f)])
 SiluMulQ8FArgs = _struct("SiluMulQ8FArgs", [("g", _p), ("u", _p), ("y", _p), ("q", _p), ("dims", _p), ("n", _i),
                                             ("cols", _i)])
 SiluMulArgs = _struct("SiluMulArgs", [("g", _p), ("u", _p), ("out", _p), ("count", _i)])

@@ -1114,26 +1114,38 @@ __global__ __launch_bounds__(256) void flash_decode_kernel(const float* __restri
     }
 }
 
-// out[i][h][:] of the chunk partials of (token i, head h) = blockIdx.x, in chunk order.
+// out[i][h][:] of the chunk partials of (token i, head h) = blockIdx.x, in chunk order. The
+// partials of 16 chunks are loaded before they are merged (one memory round trip per 16 chunks).
 template <int D>
 __global__ __launch_bounds__(128) void flash_merge_kernel(const float* __restrict__ part, float* __restrict__ out,
                                                           int nch) {
     const float* base = part + (size_t)blockIdx.x * nch * (D + 2);
     for (int e = threadIdx.x; e < D; e += 128) {
         float M = -INFINITY, L = 0.0f, O = 0.0f;
-        for (int c = 0; c < nch; ++c) {
-            const float* pc = base + (size_t)c * (D + 2);
-            const float m = pc[D];
-            if (m == -INFINITY) continue;  // every position of the chunk masked
-            if (m > M) {
-                const float f = exp2f((M - m) * kLog2e);
-                L *= f;
-                O *= f;
-                M = m;
+        for (int c0 = 0; c0 < nch; c0 += 16) {
+            float mc[16], lc[16], oc[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const float* pc = base + (size_t)min(c0 + u, nch - 1) * (D + 2);
+                mc[u] = pc[D];
+                lc[u] = pc[D + 1];
+                oc[u] = pc[e];
             }
-            const float f = exp2f((m - M) * kLog2e);
-            L += pc[D + 1] * f;
-            O += pc[e] * f;
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                if (c0 + u >= nch) break;
+                const float m = mc[u];
+                if (m == -INFINITY) continue;  // every position of the chunk masked
+                if (m > M) {
+                    const float f = exp2f((M - m) * kLog2e);
+                    L *= f;
+                    O *= f;
+                    M = m;
+                }
+                const float f = exp2f((m - M) * kLog2e);
+                L += lc[u] * f;
+                O += oc[u] * f;
+            }
         }
         out[(size_t)blockIdx.x * D + e] = O / L;
     }

@@ -71,6 +71,9 @@ int launchVectorAdd(const float* a, const float* b, float* out, int count, hipSt
 int launchAddSumsq(const float* a, const float* b, float* out, int* q, int n, int rows, hipStream_t s,
                    const float* b2 = nullptr);
 int launchNormMulQ8(bool per256, const kcNormMulQ8Args& a, hipStream_t s);
+// add_sumsq_f (a, b given) or sumsq_part, then norm_mul_q8_f, in one workgroup per row (n <= 8192).
+int launchAddNormQ8(const float* a, const float* b, float* x, const float* w, float* y, int* q, int n, int rows,
+                    float eps, hipStream_t s);
 // Batch fusions of the model path: x = a + (b [+ b2]) into out (a null: x = b), RMS norm with w
 // and per-256 quantization into q (rows slots of n / 256 * 85 ints); RoPE of q into qr and of k,
 // with k and v stored as fp16 into cache rows pos[t] (dst_row 32-bit words per row).

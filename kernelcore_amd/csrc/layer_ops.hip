@@ -30,28 +30,6 @@ __device__ __forceinline__ int q8r(float t) {
     return q > 127 ? 127 : (q < -127 ? -127 : q);
 }
 
-// One block of 32 values of y quantized into a per-32 slot (quantize_q8x4.cu:15-40).
-__device__ __forceinline__ void quant32(const float* yb, int* qw, float* xd2) {
-    float amax = 0.0f;
-    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fmaxf(yb[i], 0.0f - yb[i]));
-    const float d = amax / 127.0f;
-    float id;
-    if (d > 0.0f) id = 1.0f / d;
-    else id = 0.0f;
-    int sum = 0;
-    for (int k = 0; k < 8; ++k) {
-        int word = 0;
-        for (int i = 0; i < 4; ++i) {
-            const int c = q8r(yb[4 * k + i] * id);
-            sum += c;
-            word |= (c & 255) << (8 * i);
-        }
-        qw[k] = word;
-    }
-    xd2[0] = d;
-    xd2[1] = (float)sum;
-}
-
 __device__ __forceinline__ float rmsScale(const float* ss, int nb, int n, float eps) {
     float tot = 0.0f;
     for (int j = 0; j < nb; ++j) tot += ss[j];
@@ -81,6 +59,65 @@ __device__ __forceinline__ float waveMax(float v) {
     v = fmaxf(v, dppF<0x141>(v));
     v = fmaxf(v, dppF<0x140>(v));
     return fmaxf(fmaxf(laneF(v, 0), laneF(v, 16)), fmaxf(laneF(v, 32), laneF(v, 48)));
+}
+
+// Block quantization by the 8 lanes of an aligned group (lane j holds values 4j .. 4j + 3 of the
+// block): quant32's arithmetic (the block maximum and the integer sum do not depend on the order
+// of their terms; every value takes the same rounding), the cross-lane steps as DPP moves inside a
+// row of 16 lanes. Returns this lane's word; every lane gets d and the block's sum.
+struct Q8L {
+    int w, sum;
+    float d;
+};
+__device__ __forceinline__ Q8L quant8(const float (&y)[4]) {
+    float m = fmaxf(fmaxf(fmaxf(y[0], 0.0f - y[0]), fmaxf(y[1], 0.0f - y[1])),
+                    fmaxf(fmaxf(y[2], 0.0f - y[2]), fmaxf(y[3], 0.0f - y[3])));
+    m = fmaxf(m, dppF<0xB1>(m));   // quad_perm [1,0,3,2]
+    m = fmaxf(m, dppF<0x4E>(m));   // quad_perm [2,3,0,1]
+    m = fmaxf(m, dppF<0x141>(m));  // row_half_mirror: the other quad of the 8
+    Q8L o;
+    o.d = fmaxf(0.0f, m) / 127.0f;
+    float id;
+    if (o.d > 0.0f) id = 1.0f / o.d;
+    else id = 0.0f;
+    const int c0 = q8r(y[0] * id), c1 = q8r(y[1] * id), c2 = q8r(y[2] * id), c3 = q8r(y[3] * id);
+    o.w = (c0 & 255) | ((c1 & 255) << 8) | ((c2 & 255) << 16) | ((c3 & 255) << 24);
+    int sm = (c0 + c1) + (c2 + c3);
+    sm += dppI<0xB1>(sm);
+    sm += dppI<0x4E>(sm);
+    sm += dppI<0x141>(sm);
+    o.sum = sm;
+    return o;
+}
+
+// The sum of squares of a block of 32 in element order, by the 8 lanes of an aligned group (lane
+// j holds values 4j .. 4j + 3): the running sum passes from lane j - 1 to lane j in eight steps
+// (step k completes lane k), the same additions as one thread over the 32 values. Lane 7 returns
+// the block's sum.
+__device__ __forceinline__ float sumsq8(const float (&v)[4], int j) {
+    float s = 0.0f, t = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        t = s;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t += v[e] * v[e];
+        const float left = dppF<0x111>(t);  // row_shr:1: lane i - 1's value
+        if (j == k + 1) s = left;
+    }
+    return t;
+}
+
+// The row's RMS scale from its nb per-32 sums of squares, summed in block order (rmsScale); every
+// lane of the wavefront gets it.
+__device__ __forceinline__ float rmsScaleWave(const float* ss, int nb, int n, float eps) {
+    const int lane = threadIdx.x & 63;
+    float tot = 0.0f;
+    for (int j0 = 0; j0 < nb; j0 += 64) {
+        const float v = ss[min(j0 + lane, nb - 1)];
+        const int cnt = min(64, nb - j0);
+        for (int L = 0; L < cnt; ++L) tot += laneF(v, L);
+    }
+    return 1.0f / sqrtf(tot / (float)n + eps);
 }
 
 // The MFMA layout of one quantized super-block (ActF16): lane L's four codes as fp16, lanes 8i
@@ -154,63 +191,110 @@ __device__ __forceinline__ void store4(float* p, float4 v) {
 
 // out = a + b and per-32 sums of out^2 into the row's slot tail (add_sumsq_f.cu). a may be null:
 // then x = b and only the sums are written (sumsq_part.cu). a and out may be the same buffer (the
-// residual stream updated in place). One thread per block of 32, whose values it loads at once
-// and sums of squares in order.
+// residual stream updated in place). Four values per lane, eight lanes per block of 32 (grid: the
+// rows, the row's quads by 256); the sums of squares in element order (sumsq8).
 template <bool A16>
-__global__ void add_sumsq_kernel(const float* a, const float* b, const float* b2, float* out, int* __restrict__ q, int n,
-                                 int rows) {
-    const int nb = n / 32;
-    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= nb * rows) return;
-    const int row = idx / nb, bl = idx - row * nb;
-    const size_t o = (size_t)row * n + bl * 32;
-    float v[32];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const float4 bv = load4<A16>(b + o + 4 * k);
-        v[4 * k] = bv.x, v[4 * k + 1] = bv.y, v[4 * k + 2] = bv.z, v[4 * k + 3] = bv.w;
-    }
+__global__ __launch_bounds__(256) void add_sumsq_kernel(const float* a, const float* b, const float* b2, float* out,
+                                                        int* __restrict__ q, int n, int rows) {
+    const int nb = n / 32, nq = n / 4, row = blockIdx.x;
+    const int qi = blockIdx.y * 256 + threadIdx.x, qc = min(qi, nq - 1), j = qi & 7;
+    const size_t o = (size_t)row * n + 4 * qc;
+    const float4 bv = load4<A16>(b + o);
+    float v[4] = {bv.x, bv.y, bv.z, bv.w};
     if (b2) {  // a product split in two partial sums
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const float4 bv = load4<A16>(b2 + o + 4 * k);
-            v[4 * k] += bv.x, v[4 * k + 1] += bv.y, v[4 * k + 2] += bv.z, v[4 * k + 3] += bv.w;
-        }
+        const float4 bw = load4<A16>(b2 + o);
+        v[0] += bw.x, v[1] += bw.y, v[2] += bw.z, v[3] += bw.w;
     }
     if (a) {
-        float av[32];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const float4 x = load4<A16>(a + o + 4 * k);
-            av[4 * k] = x.x, av[4 * k + 1] = x.y, av[4 * k + 2] = x.z, av[4 * k + 3] = x.w;
-        }
-#pragma unroll
-        for (int i = 0; i < 32; ++i) v[i] = av[i] + v[i];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) store4<A16>(out + o + 4 * k, make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]));
+        const float4 av = load4<A16>(a + o);
+        v[0] = av.x + v[0], v[1] = av.y + v[1], v[2] = av.z + v[2], v[3] = av.w + v[3];
+        if (qi < nq) store4<A16>(out + o, make_float4(v[0], v[1], v[2], v[3]));
     }
-    float sq = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) sq += v[i] * v[i];
-    reinterpret_cast<float*>(q + (size_t)row * nb * 11 + nb * 10)[bl] = sq;
+    const float sq = sumsq8(v, j);
+    if (j == 7 && qi < nq) reinterpret_cast<float*>(q + (size_t)row * nb * 11 + nb * 10)[qi >> 3] = sq;
 }
 
-// y = x * r * w, quantized per 32 into the row's slot (norm_mul_q8_f.cu).
-__global__ void norm_mul_q8_kernel(const float* __restrict__ x, const float* __restrict__ w, float* __restrict__ y,
-                                   int* __restrict__ q, int n, int rows, float eps) {
-    const int nb = n / 32;
-    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= nb * rows) return;
-    const int row = idx / nb, bl = idx - row * nb;
+// y = x * r * w, quantized per 32 into the row's slot (norm_mul_q8_f.cu). Four values per lane,
+// eight lanes per block (quant8); every wavefront takes the row total itself (rmsScaleWave).
+template <bool A16>
+__global__ __launch_bounds__(256) void norm_mul_q8_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                          float* __restrict__ y, int* __restrict__ q, int n, int rows,
+                                                          float eps) {
+    const int nb = n / 32, nq = n / 4, row = blockIdx.x;
+    const int qi = blockIdx.y * 256 + threadIdx.x, qc = min(qi, nq - 1);
     int* qr = q + (size_t)row * nb * 11;
-    const float r = rmsScale(reinterpret_cast<const float*>(qr + nb * 10), nb, n, eps);
-    const size_t o = (size_t)row * n + bl * 32;
-    float v[32];
-    for (int i = 0; i < 32; ++i) {
-        v[i] = x[o + i] * r * w[bl * 32 + i];
-        y[o + i] = v[i];
+    const size_t o = (size_t)row * n + 4 * qc;
+    const float4 xv = load4<A16>(x + o), wv = load4<A16>(w + 4 * qc);  // in flight while r is summed
+    const float r = rmsScaleWave(reinterpret_cast<const float*>(qr + nb * 10), nb, n, eps);
+    const float v[4] = {xv.x * r * wv.x, xv.y * r * wv.y, xv.z * r * wv.z, xv.w * r * wv.w};
+    const Q8L b = quant8(v);
+    if (qi < nq) {
+        store4<A16>(y + o, make_float4(v[0], v[1], v[2], v[3]));
+        qr[qi] = b.w;  // block qi / 8, word qi % 8
+        if ((qi & 7) == 0) {
+            float* xd2 = reinterpret_cast<float*>(qr + nb * 8) + (qi >> 3) * 2;
+            xd2[0] = b.d;
+            xd2[1] = (float)b.sum;
+        }
     }
-    quant32(v, qr + bl * 8, reinterpret_cast<float*>(qr + nb * 8) + bl * 2);
+}
+
+// add_sumsq_f / sumsq_part and norm_mul_q8_f in one workgroup per row (NP passes of the block's
+// threads over the row's quads): x = a + b (a null: x is read), the per-32 sums of squares
+// (sumsq8) into LDS and the slot tail, the row total in block order by the first wavefront, then
+// y = x * r * w and quant8 -- the values and bytes of the two kernels.
+template <bool A16, int NP>
+__global__ __launch_bounds__(1024) void add_norm_q8_kernel(const float* a, const float* b, float* x,
+                                                           const float* __restrict__ w, float* y, int* __restrict__ q,
+                                                           int n, float eps) {
+    __shared__ float ss[8192 / 32 + 1];
+    const int nb = n / 32, nq = n / 4, row = blockIdx.x, nth = blockDim.x;
+    int* qr = q + (size_t)row * nb * 11;
+    float v[NP][4];
+    float4 wv[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        const int qi = threadIdx.x + p * nth, qc = min(qi, nq - 1);
+        const size_t o = (size_t)row * n + 4 * qc;
+        float4 xv;
+        if (a) {
+            const float4 bv = load4<A16>(b + o), av = load4<A16>(a + o);
+            xv = make_float4(av.x + bv.x, av.y + bv.y, av.z + bv.z, av.w + bv.w);
+            if (qi < nq) store4<A16>(x + o, xv);
+        } else {
+            xv = load4<A16>(x + o);
+        }
+        v[p][0] = xv.x, v[p][1] = xv.y, v[p][2] = xv.z, v[p][3] = xv.w;
+        wv[p] = load4<A16>(w + 4 * qc);
+        const float sq = sumsq8(v[p], qi & 7);
+        if ((qi & 7) == 7 && qi < nq) {
+            ss[qi >> 3] = sq;
+            reinterpret_cast<float*>(qr + nb * 10)[qi >> 3] = sq;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        const float r = rmsScaleWave(ss, nb, n, eps);
+        if (threadIdx.x == 0) ss[nb] = r;
+    }
+    __syncthreads();
+    const float r = ss[nb];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        const int qi = threadIdx.x + p * nth;
+        const size_t o = (size_t)row * n + 4 * min(qi, nq - 1);
+        const float yv[4] = {v[p][0] * r * wv[p].x, v[p][1] * r * wv[p].y, v[p][2] * r * wv[p].z, v[p][3] * r * wv[p].w};
+        const Q8L bq = quant8(yv);
+        if (qi < nq) {
+            store4<A16>(y + o, make_float4(yv[0], yv[1], yv[2], yv[3]));
+            qr[qi] = bq.w;
+            if ((qi & 7) == 0) {
+                float* xd2 = reinterpret_cast<float*>(qr + nb * 8) + (qi >> 3) * 2;
+                xd2[0] = bq.d;
+                xd2[1] = (float)bq.sum;
+            }
+        }
+    }
 }
 
 // The same with per-256 slots (norm_mul_q8k_f.cu): q holds rows slots of nsb*85 ints, then the
@@ -245,21 +329,27 @@ __global__ __launch_bounds__(256) void norm_mul_q8k_kernel(const float* __restri
     }
 }
 
-// SwiGLU, quantized per 32 (silu_mul_q8x4f.cu) or per 256 (silu_mul_q8kf.cu); columns of n.
-__global__ void silu_mul_q8_kernel(const float* __restrict__ g, const float* __restrict__ u, float* __restrict__ y,
-                                   int* __restrict__ q, int n, int cols) {
-    const int nb = n / 32;
-    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= nb * cols) return;
-    const int c = idx / nb, b = idx - c * nb;
-    const size_t o = (size_t)c * n + b * 32;
-    float v[32];
-    for (int i = 0; i < 32; ++i) {
-        v[i] = silu(g[o + i]) * u[o + i];
-        y[o + i] = v[i];
+// SwiGLU, quantized per 32 (silu_mul_q8x4f.cu) or per 256 (silu_mul_q8kf.cu); columns of n. The
+// per-32 form: four values per lane, eight lanes per block (quant8).
+template <bool A16>
+__global__ __launch_bounds__(256) void silu_mul_q8_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                          float* __restrict__ y, int* __restrict__ q, int n, int cols) {
+    const int nb = n / 32, nq = n / 4, c = blockIdx.x;
+    const int qi = blockIdx.y * 256 + threadIdx.x, qc = min(qi, nq - 1);
+    const size_t o = (size_t)c * n + 4 * qc;
+    const float4 gv = load4<A16>(g + o), uv = load4<A16>(u + o);
+    const float v[4] = {silu(gv.x) * uv.x, silu(gv.y) * uv.y, silu(gv.z) * uv.z, silu(gv.w) * uv.w};
+    const Q8L b = quant8(v);
+    if (qi < nq) {
+        store4<A16>(y + o, make_float4(v[0], v[1], v[2], v[3]));
+        int* qcol = q + (size_t)c * nb * 11;
+        qcol[qi] = b.w;
+        if ((qi & 7) == 0) {
+            float* xd2 = reinterpret_cast<float*>(qcol + nb * 8) + (qi >> 3) * 2;
+            xd2[0] = b.d;
+            xd2[1] = (float)b.sum;
+        }
     }
-    int* qc = q + (size_t)c * nb * 11;
-    quant32(v, qc + b * 8, reinterpret_cast<float*>(qc + nb * 8) + b * 2);
 }
 
 template <bool A16>
@@ -312,21 +402,20 @@ __global__ void rms_norm_kernel(const float* __restrict__ x, const float* __rest
     for (int j = 0; j < n; ++j) yr[j] = xr[j] * r * w[j];
 }
 
-// ggml ROPE (rope_ggml.cu): one thread per (token, pair), applied to the pair of every head.
+// ggml ROPE (rope_ggml.cu): one thread per (token, head, pair); each thread takes the pair's
+// angle itself (the reference's per-(token, pair) value, recomputed per head).
 __global__ void rope_kernel(const float* __restrict__ x, float* __restrict__ y, const int* __restrict__ pos,
                             const float* __restrict__ ff, int pairs, int nh, int count, float log2_base, int m1,
                             int m2) {
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= count) return;
-    const int t = idx / pairs, i = idx - t * pairs;
+    const int th = idx / pairs, i = idx - th * pairs, t = th / nh;
     const float theta = (float)pos[t] * exp2f(-(float)i / (float)pairs * log2_base) / ff[i];
     const float c = cosf(theta), s = sinf(theta);
-    for (int h = 0; h < nh; ++h) {
-        const size_t a = 2 * ((size_t)t * nh + h) * pairs + (size_t)i * m1;
-        const float x0 = x[a], x1 = x[a + m2];
-        y[a] = x0 * c - x1 * s;
-        y[a + m2] = x0 * s + x1 * c;
-    }
+    const size_t a = 2 * (size_t)th * pairs + (size_t)i * m1;
+    const float x0 = x[a], x1 = x[a + m2];
+    y[a] = x0 * c - x1 * s;
+    y[a + m2] = x0 * s + x1 * c;
 }
 
 // fp32 -> fp16 bits as set_rows_f16.cu: nearest even, |x| >= 65520 -> +-0x7bff, -0 -> +0.
@@ -613,7 +702,8 @@ static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) =
 
 int launchAddSumsq(const float* a, const float* b, float* out, int* q, int n, int rows, hipStream_t s,
                    const float* b2) {
-    const dim3 grid(blocksFor((long long)(n / 32) * rows));
+    if (rows <= 0 || n <= 0) return 0;
+    const dim3 grid(rows, blocksFor(n / 4));
     if (al16(b) && (!b2 || al16(b2)) && (!a || (al16(a) && al16(out))))
         hipLaunchKernelGGL(add_sumsq_kernel<true>, grid, dim3(256), 0, s, a, b, b2, out, q, n, rows);
     else
@@ -629,10 +719,30 @@ int launchNormMulQ8(bool per256, const kcNormMulQ8Args& a, hipStream_t s) {
         else
             hipLaunchKernelGGL(norm_mul_q8k_kernel<false>, dim3(a.rows), dim3(256), 0, s, a.x, a.w, a.y, a.q, a.n,
                                a.rows, a.eps);
-    } else if (!per256)
-        hipLaunchKernelGGL(norm_mul_q8_kernel, dim3(blocksFor((long long)(a.n / 32) * a.rows)), dim3(256), 0, s, a.x,
-                           a.w, a.y, a.q, a.n, a.rows, a.eps);
+    } else if (!per256 && a.rows > 0 && a.n > 0) {
+        const dim3 grid(a.rows, blocksFor(a.n / 4));
+        if (al16(a.x) && al16(a.w) && al16(a.y))
+            hipLaunchKernelGGL(norm_mul_q8_kernel<true>, grid, dim3(256), 0, s, a.x, a.w, a.y, a.q, a.n, a.rows, a.eps);
+        else
+            hipLaunchKernelGGL(norm_mul_q8_kernel<false>, grid, dim3(256), 0, s, a.x, a.w, a.y, a.q, a.n, a.rows, a.eps);
+    }
     return fromHip(hipGetLastError(), per256 ? "norm_mul_q8k_f" : "norm_mul_q8_f");
+}
+
+int launchAddNormQ8(const float* a, const float* b, float* x, const float* w, float* y, int* q, int n, int rows,
+                    float eps, hipStream_t s) {
+    if (rows <= 0) return 0;
+    if (n <= 0 || n % 256 || n > 8192) return fromHip(hipErrorInvalidValue, "add_norm_q8: row length");
+    const int nq = n / 4, nth = std::min(1024, nq);
+    const bool a16 = (!a || (al16(a) && al16(b))) && al16(x) && al16(w) && al16(y);
+    if (nq <= 1024) {
+        if (a16) hipLaunchKernelGGL((add_norm_q8_kernel<true, 1>), dim3(rows), dim3(nth), 0, s, a, b, x, w, y, q, n, eps);
+        else hipLaunchKernelGGL((add_norm_q8_kernel<false, 1>), dim3(rows), dim3(nth), 0, s, a, b, x, w, y, q, n, eps);
+    } else {
+        if (a16) hipLaunchKernelGGL((add_norm_q8_kernel<true, 2>), dim3(rows), dim3(nth), 0, s, a, b, x, w, y, q, n, eps);
+        else hipLaunchKernelGGL((add_norm_q8_kernel<false, 2>), dim3(rows), dim3(nth), 0, s, a, b, x, w, y, q, n, eps);
+    }
+    return fromHip(hipGetLastError(), "add_norm_q8_f");
 }
 
 int launchSiluMulQ8(bool per256, const kcSiluMulQ8FArgs& a, hipStream_t s) {
@@ -643,9 +753,13 @@ int launchSiluMulQ8(bool per256, const kcSiluMulQ8FArgs& a, hipStream_t s) {
         else
             hipLaunchKernelGGL(silu_mul_q8k_kernel<false>, dim3(a.cols), dim3(256), 0, s, a.g, a.u, a.y, a.q, a.n, a.cols,
                                ActF16{}, 0);
-    } else if (!per256)
-        hipLaunchKernelGGL(silu_mul_q8_kernel, dim3(blocksFor((long long)(a.n / 32) * a.cols)), dim3(256), 0, s, a.g,
-                           a.u, a.y, a.q, a.n, a.cols);
+    } else if (!per256 && a.cols > 0 && a.n > 0) {
+        const dim3 grid(a.cols, blocksFor(a.n / 4));
+        if (al16(a.g) && al16(a.u) && al16(a.y))
+            hipLaunchKernelGGL(silu_mul_q8_kernel<true>, grid, dim3(256), 0, s, a.g, a.u, a.y, a.q, a.n, a.cols);
+        else
+            hipLaunchKernelGGL(silu_mul_q8_kernel<false>, grid, dim3(256), 0, s, a.g, a.u, a.y, a.q, a.n, a.cols);
+    }
     return fromHip(hipGetLastError(), per256 ? "silu_mul_q8kf" : "silu_mul_q8x4f");
 }
 
@@ -680,10 +794,11 @@ int launchRmsNorm(const kcRmsNormArgs& a, hipStream_t s) {
 
 int launchRope(const kcRopeGgmlArgs& a, hipStream_t s) {
     const int pairs = a.head_dim / 2;
-    const int count = pairs * a.n_tokens;
-    if (count == 0) return 0;
+    const long long count = (long long)pairs * a.n_head * a.n_tokens;
+    if (count <= 0) return 0;
+    if (count > INT32_MAX) return fromHip(hipErrorInvalidValue, "rope_ggml: more than 2^31 pairs");
     hipLaunchKernelGGL(rope_kernel, dim3(blocksFor(count)), dim3(256), 0, s, a.x, a.y, a.pos, a.ff, pairs, a.n_head,
-                       count, a.log2_base, a.neox ? 1 : 2, a.neox ? pairs : 1);
+                       (int)count, a.log2_base, a.neox ? 1 : 2, a.neox ? pairs : 1);
     return fromHip(hipGetLastError(), "rope_ggml");
 }
 

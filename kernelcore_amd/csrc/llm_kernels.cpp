@@ -229,6 +229,27 @@ int normMulLaunch(const void* p, void* s) {
     return kcamd::launchNormMulQ8(K8, *static_cast<const kcNormMulQ8Args*>(p), hs(s));
 }
 
+int addNormValidate(const void* p, const kcLaunchContext*) {
+    const auto& a = *static_cast<const kcAddNormQ8FArgs*>(p);
+    KC_TRY(checkRowsQ(a.n, a.rows, a.q));
+    if (a.n > 8192) return invalid("add_norm_q8_f: rows of at most 8192 values");
+    if ((a.a != nullptr) != (a.b != nullptr)) return invalid("a and b are both given or both null");
+    const size_t bytes = f32Bytes(int64_t(a.n) * a.rows);
+    if (a.a) {
+        KC_TRY(checkRange(a.a, bytes, "a"));
+        KC_TRY(checkRange(a.b, bytes, "b"));
+    }
+    KC_TRY(checkRange(a.x, bytes, "x"));
+    KC_TRY(checkRange(a.w, f32Bytes(a.n), "w"));
+    KC_TRY(checkRange(a.y, bytes, "y"));
+    const int want[3] = {a.n / 32, a.n, a.rows};
+    return checkDims(a.dims, want, 3);
+}
+int addNormLaunch(const void* p, void* s) {
+    const auto& a = *static_cast<const kcAddNormQ8FArgs*>(p);
+    return kcamd::launchAddNormQ8(a.a, a.b, a.x, a.w, a.y, a.q, a.n, a.rows, a.eps, hs(s));
+}
+
 template <bool K8>
 int siluQValidate(const void* p, const kcLaunchContext*) {
     const auto& a = *static_cast<const kcSiluMulQ8FArgs*>(p);
@@ -475,6 +496,7 @@ const kcKernelEntry kTable[] = {
     {"sumsq_part", sumsqValidate, sumsqLaunch, 1},
     {"norm_mul_q8_f", normMulValidate<false>, normMulLaunch<false>, 1},
     {"norm_mul_q8k_f", normMulValidate<true>, normMulLaunch<true>, 1},
+    {"add_norm_q8_f", addNormValidate, addNormLaunch, 1},
     {"silu_mul_q8x4f", siluQValidate<false>, siluQLaunch<false>, 1},
     {"silu_mul_q8kf", siluQValidate<true>, siluQLaunch<true>, 1},
     {"rms_norm", rmsValidate, rmsLaunch, 1},

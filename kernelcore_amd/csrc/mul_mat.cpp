@@ -125,6 +125,11 @@ E fusedNormImpl(kcMulMatRecording_st& r, const kcMulMatNormNode& n, kcMulMatPlan
     if (E e = registeredSlots(r, n.y, n.n, n.rows, k256, k256 ? size_t(n.rows) * slotInts(n.n, false) : 0, &qk); e != ok)
         return e;
     int* q = qk + off;
+    if (!k256 && n.n <= 8192) {  // both steps in one workgroup per row (the same bytes)
+        const kcAddNormQ8FArgs a{n.a, n.b, n.x, n.w, n.y, q, nullptr, n.n, n.rows, n.eps};
+        name(plan.kernel, "add_norm_q8_f");
+        return launch(r, "add_norm_q8_f", &a, plan);
+    }
     if (n.a) {
         const kcAddSumsqFArgs a{n.a, n.b, n.x, q, nullptr, n.n, n.rows};
         name(plan.quantizer, "add_sumsq_f");

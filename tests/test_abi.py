@@ -79,7 +79,7 @@ def test_codegen_cpu_paths_are_unsupported():
 
 STRUCTS = ["VectorAddArgs", "QuantizeArgs", "MatvecQ4Q8Args", "MatmulKQ8Args", "MatmulF16Args", "QuantizeColsArgs",
            "RmsNormArgs", "MulRowsArgs", "RopeGgmlArgs", "AddSumsqFArgs", "SumsqPartArgs", "NormMulQ8Args",
-           "SiluMulQ8FArgs",
+           "AddNormQ8FArgs", "SiluMulQ8FArgs",
            "SiluMulArgs", "SetRowsF16Args", "FaDims", "FaScoresArgs", "FaMaxArgs", "FaExpArgs", "FaValuesArgs",
            "KquantRepackArgs", "GetRowsKquantArgs", "QuantizeKquantArgs", "FillNormalArgs", "FlashAttnArgs", "FlashDecodeArgs",
            "DeviceProperties",

@@ -31,8 +31,9 @@ ATTN = ["rope_ggml", "rope_ggml", "set_rows_f16", "set_rows_f16", "flash_decode_
 
 def test_decode_layer_plan():
     g, _ = layer(N=1)
-    assert plan(g) == (["sumsq_part", "norm_mul_q8_f", "[", "matvec_q4k_q8", "matvec_q4k_q8", "matvec_q6k_q8", "]"]
-                       + ATTN + ["quantize_q8x4", "matvec_q4k_q8", "add_sumsq_f", "norm_mul_q8_f",
+    # the per-32 norms: add_sumsq_f / sumsq_part and norm_mul_q8_f in one add_norm_q8_f launch
+    assert plan(g) == (["add_norm_q8_f", "[", "matvec_q4k_q8", "matvec_q4k_q8", "matvec_q6k_q8", "]"]
+                       + ATTN + ["quantize_q8x4", "matvec_q4k_q8", "add_norm_q8_f",
                                  "[", "matvec_q4k_q8", "matvec_q4k_q8", "]", "silu_mul_q8x4f", "matvec_q6k_q8",
                                  "vector_add"])
 
@@ -40,8 +41,7 @@ def test_decode_layer_plan():
 def test_graphs_off_runs_no_concurrent_groups():
     g, _ = layer(N=1)
     names = plan(g, graphs=0)
-    assert "[" not in names and names[:5] == ["sumsq_part", "norm_mul_q8_f", "matvec_q4k_q8", "matvec_q4k_q8",
-                                              "matvec_q6k_q8"]
+    assert "[" not in names and names[:4] == ["add_norm_q8_f", "matvec_q4k_q8", "matvec_q4k_q8", "matvec_q6k_q8"]
     assert plan(g, concurrent=0) == names
 
 
@@ -55,11 +55,13 @@ def test_graphs_off_runs_no_concurrent_groups():
 def test_batch_layer_plans(N, cfg, mm, quant):
     g, _ = layer(N=N)
     k = "q8k" if quant == "quantize_cols_k" else "q8"
-    norm = "norm_mul_q8k_f" if k == "q8k" else "norm_mul_q8_f"
+    # per-256 slots: the sums then norm_mul_q8k_f; per-32: both in add_norm_q8_f
+    norm0 = ["sumsq_part", "norm_mul_q8k_f"] if k == "q8k" else ["add_norm_q8_f"]
+    norm1 = ["add_sumsq_f", "norm_mul_q8k_f"] if k == "q8k" else ["add_norm_q8_f"]
     silu = "silu_mul_q8kf" if k == "q8k" else "silu_mul_q8x4f"
     attn = ATTN if N <= 8 else ATTN[:4] + ["flash_attn_f16"]  # batches past 8 tokens: the one-kernel form
-    want = (["sumsq_part", norm, "[", mm.format("q4k"), mm.format("q4k"), mm.format("q6k"), "]"] + attn +
-            [quant, mm.format("q4k"), "add_sumsq_f", norm, "[", mm.format("q4k"), mm.format("q4k"), "]", silu,
+    want = (norm0 + ["[", mm.format("q4k"), mm.format("q4k"), mm.format("q6k"), "]"] + attn +
+            [quant, mm.format("q4k")] + norm1 + ["[", mm.format("q4k"), mm.format("q4k"), "]", silu,
              mm.format("q6k"), "vector_add"])
     assert plan(g, **cfg) == want
 
@@ -67,8 +69,8 @@ def test_batch_layer_plans(N, cfg, mm, quant):
 def test_matvec_cols_runs_one_matvec_per_column():
     g, _ = layer(N=3)
     names = plan(g, matvec_cols=1)
-    assert names[:2] == ["sumsq_part", "norm_mul_q8_f"]  # not batch_k256: per-32 slots
-    assert names[2:12] == ["["] + ["matvec_q4k_q8"] * 6 + ["matvec_q6k_q8"] * 3
+    assert names[:1] == ["add_norm_q8_f"]  # not batch_k256: per-32 slots
+    assert names[1:11] == ["["] + ["matvec_q4k_q8"] * 6 + ["matvec_q6k_q8"] * 3
     assert "quantize_cols" in names  # the attention output: contiguous columns, one launch
 
 
@@ -83,7 +85,7 @@ def test_residual_add_fuses_into_the_next_layers_norm():
     g.finish()
     names = plan(g)
     # the residual ADD fused with the next layer's norm, whose slots the MUL_MAT takes (no quantizer)
-    assert names[-3:] == ["add_sumsq_f", "norm_mul_q8_f", "matvec_q4k_q8"] and "vector_add" not in names
+    assert names[-2:] == ["add_norm_q8_f", "matvec_q4k_q8"] and "vector_add" not in names
 
 
 def norm_mul_graph(n=512, rows=1, weight_rows=1, mm=True):
@@ -99,6 +101,9 @@ def norm_mul_graph(n=512, rows=1, weight_rows=1, mm=True):
 
 def test_norm_mul_fuses():
     g, _, _ = norm_mul_graph()
+    g.finish()
+    assert plan(g) == ["add_norm_q8_f", "matvec_q4k_q8"]
+    g, _, _ = norm_mul_graph(n=8448)  # rows past 8192 values: the reference's two kernels
     g.finish()
     assert plan(g) == ["sumsq_part", "norm_mul_q8_f", "matvec_q4k_q8"]
 
@@ -137,7 +142,7 @@ def test_add_whose_result_the_norm_does_not_read():
     norm = g.rms_norm(x, 1e-5)
     g.mul(norm, g.leaf("f32", [512], buffer="weights"))
     g.finish()
-    assert plan(g) == ["vector_add", "sumsq_part", "norm_mul_q8_f"]
+    assert plan(g) == ["vector_add", "add_norm_q8_f"]
 
 
 def test_nodes_without_work_are_skipped():
@@ -163,7 +168,7 @@ def test_swiglu_unfused_when_rows_are_not_a_multiple_of_256():
 def test_decode_attention_is_split_over_the_context():
     g, _ = layer(N=1, n_kv=20000, kv_size=20480)
     names, ints = kc.ggml_graph_plan(g.nodes)
-    assert names[9:12] == ["set_rows_f16", "set_rows_f16", "flash_decode_f16"]
+    assert names[8:11] == ["set_rows_f16", "set_rows_f16", "flash_decode_f16"]
     assert ints >= 8 * 313 * 66  # the partials of 8 heads x 313 chunks x (64 values + max + sum)
 
 

@@ -85,6 +85,51 @@ def test_add_sumsq_norm_mul_q8_bit_exact():
     B.free()
 
 
+@pytest.mark.parametrize("n,rows", [(256, 1), (3072, 1), (3072, 3), (4096, 2), (8192, 1), (5120, 2)])
+@pytest.mark.parametrize("mode", ["add", "in_place", "norm_only"])
+def test_add_norm_q8_one_launch_bit_exact(n, rows, mode):
+    """add_norm_q8_f: add_sumsq_f (or sumsq_part) + norm_mul_q8_f in one launch -- x, y and every
+    slot word (codes, scale / sum pairs, the per-32 sums of squares in the tails) as the oracle's
+    two steps; in place: x is a's buffer (the residual stream)."""
+    note(f"add_norm_q8_f n={n} rows={rows} {mode}")
+    nb = n // 32
+    a, b, w = kq.randn(n * rows, n + rows), kq.randn(n * rows, n + 7), kq.uniform(n, 3, 0.5, 1.5)
+    B = Bufs()
+    ba, bb, bw = B.of(a), B.of(b), B.of(w)
+    bx = ba if mode == "in_place" else B.of(a if mode == "norm_only" else np.zeros(n * rows, np.float32))
+    by, bq = B.new(n * rows * 4), B.new(rows * nb * 11 * 4)
+    has_add = mode != "norm_only"
+    kc.launch("add_norm_q8_f", kc.AddNormQ8FArgs(ba.ptr if has_add else None, bb.ptr if has_add else None, bx.ptr,
+                                                 bw.ptr, by.ptr, bq.ptr, None, n, rows, 1e-5))
+    x = np.zeros(n * rows, np.float32)
+    q = np.zeros(rows * nb * 11, np.int32)
+    if has_add:
+        O.kco_add_sumsq_f(a, b, x, q, n, rows)
+    else:
+        x = a.copy()
+        O.kco_sumsq_part(x, q, n, rows)
+    y = np.zeros(n * rows, np.float32)
+    O.kco_norm_mul_q8(x, w, y, q, n, rows, 1e-5)
+    assert np.array_equal(kq.bits(bx.download(np.float32)), kq.bits(x))
+    assert np.array_equal(kq.bits(by.download(np.float32)), kq.bits(y))
+    assert np.array_equal(bq.download(np.int32), q)
+    B.free()
+
+
+def test_add_norm_q8_refuses_what_it_does_not_cover():
+    B = Bufs()
+    big = B.new(8448 * 4 * 2)
+    q = B.new(8448 // 32 * 11 * 4 * 2)
+    A = kc.AddNormQ8FArgs
+    assert kc.launch_status("add_norm_q8_f", A(None, None, big.ptr, big.ptr, big.ptr, q.ptr, None, 8448, 1, 1e-5)) \
+        == "InvalidValue"  # rows past 8192 values: the two kernels
+    assert kc.launch_status("add_norm_q8_f", A(big.ptr, None, big.ptr, big.ptr, big.ptr, q.ptr, None, 256, 1, 1e-5)) \
+        == "InvalidValue"  # a without b
+    assert kc.launch_status("add_norm_q8_f", A(None, None, big.ptr, big.ptr, big.ptr, q.ptr, None, 300, 1, 1e-5)) \
+        == "InvalidValue"
+    B.free()
+
+
 def test_norm_golden_fixture():
     g = np.load(os.path.join(GOLDEN, "norm_mul_q8.npz"))
     n, rows = int(g["n"]), int(g["rows"])
@@ -95,6 +140,11 @@ def test_norm_golden_fixture():
     kc.launch("norm_mul_q8_f", kc.NormMulQ8Args(bout.ptr, bw.ptr, by.ptr, bq.ptr, None, n, rows, 1e-5))
     assert np.array_equal(bq.download(np.int32), g["q"])
     assert np.array_equal(kq.bits(by.download(np.float32)), kq.bits(g["y"]))
+    # the same in one add_norm_q8_f launch
+    bx2, by2, bq2 = B.new(n * rows * 4), B.new(n * rows * 4), B.new(rows * (n // 32) * 11 * 4)
+    kc.launch("add_norm_q8_f", kc.AddNormQ8FArgs(ba.ptr, bb.ptr, bx2.ptr, bw.ptr, by2.ptr, bq2.ptr, None, n, rows, 1e-5))
+    assert np.array_equal(bq2.download(np.int32), g["q"])
+    assert np.array_equal(kq.bits(by2.download(np.float32)), kq.bits(g["y"]))
     B.free()
 
 
