@@ -337,6 +337,97 @@ E fusedSwiglu(Pass& p, const T* dst) {
     return kcamd::mulmat::fusedSwiglu(p.rec, sn, plan);
 }
 
+// ---- one input column through the fused decode matvec (kdecode.hip) ------------------------------
+// No reference counterpart: where the reference launches one matvec per MUL_MAT, 2-3 MUL_MATs of
+// one input column run as one launch whose rows each take the reference matvec's sum, from the same
+// per-32 slot; gate and up followed by SWIGLU also apply silu(gate) * up and quantize it per 32 into
+// the slot the down MUL_MAT reads. Option ggml_decode_matvec = 1 keeps one launch per node.
+
+// A launch of this build's own kernels (no by-name entry), named in the trace like the others.
+template <class F>
+E direct(Pass& p, const char* name, F&& fn) {
+    if (E e = marker(p, name); e != ok) return e;
+    if (p.rec.dry) return ok;
+    void* hs = nullptr;
+    if (E e = kcStreamGetNative(p.rec.stream, &hs); e != ok) return e;
+    return static_cast<E>(fn(static_cast<hipStream_t>(hs)));
+}
+
+bool kquant(const T* w) { return w->type == KC_GGML_TYPE_Q4_K || w->type == KC_GGML_TYPE_Q6_K; }
+bool computed(const T* t) { return t->compute && !empty(t); }
+
+// MUL_MATs mm[0..g) of the one-column input x through one decode matvec with epilogue epi
+bool decodeMatvecOk(const T* x, const T* const* mm, int g, int epi, int tpw) {
+    if (g < 1 || g > 3 || !f32c(x) || nrows(x) != 1 || x->ne[0] % 256 || x->ne[0] > INT_MAX) return false;
+    for (int j = 0; j < g; ++j)
+        if (!kquant(mm[j]->src[0]) || mm[j]->src[0]->ne[0] != x->ne[0] || !f32c(mm[j])) return false;
+    return kcamd::planDecodeMatvec(kcamd::kProSlot, epi, int(x->ne[0]), tpw).nw > 0;
+}
+
+// The per-32 slot of the group's input (the fused norm's, or quantized now) as DmvArgs.
+E slotArgs(Pass& p, const T* mm0, kcamd::DmvArgs& a) {
+    const T* x = mm0->src[1];
+    const int k = int(x->ne[0]);
+    if (E e = mulMatInput(p, mm0); e != ok) return e;
+    int* q = kcamd::mulmat::inputSlot(p.rec, f32(x), 1, k, false);
+    if (!q) return kc::Error::InternalError;
+    a.k = k;
+    a.xq = q;
+    a.xd = reinterpret_cast<const float*>(q + k / 32 * 8);
+    return ok;
+}
+
+kcamd::DmvPart dmvPart(const T* mm, float* y) {
+    const T* w = mm->src[0];
+    return kcamd::DmvPart{w->data, y, int(w->ne[1]), w->type == KC_GGML_TYPE_Q6_K ? 1 : 0, 0, 0};
+}
+
+E decodeGroup(Pass& p, const T* const* mm, int g) {
+    kcamd::DmvArgs a{};
+    if (E e = slotArgs(p, mm[0], a); e != ok) return e;
+    kcamd::DmvPart* ps[3] = {&a.p0, &a.p1, &a.p2};
+    for (int j = 0; j < g; ++j) *ps[j] = dmvPart(mm[j], f32w(mm[j]));
+    a.nparts = g;
+    a.tpw = 1;
+    return direct(p, "decode_matvec", [&](hipStream_t s) {
+        return kcamd::launchDecodeMatvec(kcamd::kProSlot, kcamd::kEpiStore, a, s);
+    });
+}
+
+// nodes[i], nodes[i + 1] = gate, up of one input column and nodes[i + 2] their SWIGLU, whose one
+// use is a K-quant MUL_MAT (which reads the slot, not the f32 result); gate's and up's one use is
+// the GLU. None of the three is a view or a graph output.
+bool decodeSwigluOk(const T* const* nodes, int n, int i) {
+    if (i + 2 >= n) return false;
+    const T *ga = nodes[i], *up = nodes[i + 1], *glu = nodes[i + 2];
+    if (glu->op != KC_GGML_OP_GLU || glu->src[0] != ga || glu->src[1] != up || !computed(glu) ||
+        glu->op_params[0] != KC_GGML_GLU_OP_SWIGLU || glu->op_params[1] != 0 || !f32c(glu))
+        return false;
+    for (const T* t : {ga, up, glu})
+        if (t->uses != 1 || t->view || t->output) return false;
+    if (ga->src[0]->ne[1] != up->src[0]->ne[1] || glu->ne[0] != ga->ne[0]) return false;
+    const T* user = nullptr;
+    for (int j = i + 3; j < n && !user; ++j)
+        for (int s = 0; s < 5; ++s)
+            if (nodes[j]->src[s] == glu) user = nodes[j];
+    if (!user || user->op != KC_GGML_OP_MUL_MAT || user->src[1] != glu || !kquant(user->src[0])) return false;
+    const T* mm[2] = {ga, up};
+    return decodeMatvecOk(ga->src[1], mm, 2, kcamd::kEpiSwiglu, 2);
+}
+
+E decodeSwiglu(Pass& p, const T* ga, const T* up, const T* glu) {
+    kcamd::DmvArgs a{};
+    if (E e = slotArgs(p, ga, a); e != ok) return e;
+    a.p0 = dmvPart(ga, nullptr);
+    a.p1 = dmvPart(up, nullptr);
+    a.nparts = 2;
+    a.tpw = 2;
+    if (E e = kcamd::mulmat::outputSlot(p.rec, f32(glu), a.p0.rows, 1, false, &a.qout); e != ok) return e;
+    return direct(p, "decode_swiglu", [&](hipStream_t s) {
+        return kcamd::launchDecodeMatvec(kcamd::kProSlot, kcamd::kEpiSwiglu, a, s);
+    });
+}
+
 E setRows(Pass& p, const T* dst) {  // dst rows src1[r] (int64) = fp16(src0 row r) (:650-661)
     const T* src = dst->src[0];
     const T* idx = dst->src[1];
@@ -403,8 +494,6 @@ E concurrent(Pass& p, bool begin) {
     return begin ? kcStreamConcurrentBegin(p.rec.stream) : kcStreamConcurrentEnd(p.rec.stream);
 }
 
-bool computed(const T* t) { return t->compute && !empty(t); }
-
 // backend_graph_compute's walk (:712-788)
 E walk(Pass& p, const T* const* nodes, int n) {
     static const int kNormMul[2] = {KC_GGML_OP_RMS_NORM, KC_GGML_OP_MUL};
@@ -416,6 +505,22 @@ E walk(Pass& p, const T* const* nodes, int n) {
         E e = ok;
         switch (node->op) {
             case KC_GGML_OP_MUL_MAT: {
+                if (kcamd::option("ggml_decode_matvec") != 1) {  // one input column: the fused decode matvec
+                    int ga = 1;
+                    while (i + ga < n && ga < 3 && nodes[i + ga]->op == KC_GGML_OP_MUL_MAT &&
+                           nodes[i + ga]->src[1] == node->src[1] && computed(nodes[i + ga]))
+                        ++ga;
+                    if (ga == 2 && decodeSwigluOk(nodes, n, i)) {
+                        e = decodeSwiglu(p, nodes[i], nodes[i + 1], nodes[i + 2]);
+                        i += 2;
+                        break;
+                    }
+                    if (ga >= 2 && decodeMatvecOk(node->src[1], nodes + i, ga, kcamd::kEpiStore, 1)) {
+                        e = decodeGroup(p, nodes + i, ga);
+                        i += ga - 1;
+                        break;
+                    }
+                }
                 // consecutive MUL_MATs of one input (q, k, v; gate, up) as one step
                 int g = 1;
                 while (p.cfg.concurrent && p.capturing && i + g < n && nodes[i + g]->op == KC_GGML_OP_MUL_MAT &&

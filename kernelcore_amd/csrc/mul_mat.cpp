@@ -249,6 +249,20 @@ kcError_t take(kcMulMatRecording_st& r, size_t ints, int** out) noexcept {
     return ok;
 }
 
+int* inputSlot(const kcMulMatRecording_st& r, const float* x, long long ncols, int k, bool k256) noexcept {
+    for (const auto& in : r.inputs)
+        if (in.x == x && in.ncols == ncols && in.k == k && in.k256 == k256) return in.q;
+    return nullptr;
+}
+
+kcError_t outputSlot(kcMulMatRecording_st& r, const float* y, int k, long long ncols, bool k256, int** q) noexcept {
+    try {
+        return registeredSlots(r, y, k, ncols, k256, 0, q);
+    } catch (...) {
+        return kc::Error::OutOfMemory;
+    }
+}
+
 kcError_t launch(kcMulMatRecording_st& r, const char* kernel, const void* args) noexcept {
     if (r.trace) {
         try {

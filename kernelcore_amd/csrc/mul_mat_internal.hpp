@@ -42,6 +42,11 @@ kcError_t reserve(kcMulMatRecording_st& r, size_t ints) noexcept;
 kcError_t take(kcMulMatRecording_st& r, size_t ints, int** out) noexcept;
 // one launch on the recording's stream (dry: named only)
 kcError_t launch(kcMulMatRecording_st& r, const char* kernel, const void* args) noexcept;
+// the recording's 8-bit slots of input x (nullptr when it made none)
+int* inputSlot(const kcMulMatRecording_st& r, const float* x, long long ncols, int k, bool k256) noexcept;
+// slots for the 8-bit form of y registered under y, for a producer that writes them itself (the
+// MUL_MATs that read y then take them)
+kcError_t outputSlot(kcMulMatRecording_st& r, const float* y, int k, long long ncols, bool k256, int** q) noexcept;
 
 kcError_t mulMat(kcMulMatRecording_st& r, const kcMulMatNode& n, kcMulMatPlan& plan) noexcept;
 // the node's 8-bit input made now (the reference's mul_mat_input; nothing for F16 weights)

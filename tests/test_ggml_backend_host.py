@@ -29,16 +29,49 @@ ATTN = ["rope_ggml", "rope_ggml", "set_rows_f16", "set_rows_f16", "flash_decode_
 
 # ---- graph_compute's walk --------------------------------------------------------------------------------------
 
+@pytest.fixture
+def reference_matvecs():
+    """The reference's one launch per MUL_MAT node (no fused decode matvec)."""
+    kc.set_option("ggml_decode_matvec", 1)
+    yield
+    kc.set_option("ggml_decode_matvec", 0)
+
+
 def test_decode_layer_plan():
     g, _ = layer(N=1)
-    # the per-32 norms: add_sumsq_f / sumsq_part and norm_mul_q8_f in one add_norm_q8_f launch
+    # the per-32 norms: add_sumsq_f / sumsq_part and norm_mul_q8_f in one add_norm_q8_f launch; one
+    # input column: q / k / v in one fused decode matvec, gate / up and the SWIGLU in another
+    assert plan(g) == (["add_norm_q8_f", "decode_matvec"] + ATTN +
+                       ["quantize_q8x4", "matvec_q4k_q8", "add_norm_q8_f", "decode_swiglu", "matvec_q6k_q8",
+                        "vector_add"])
+
+
+def test_decode_layer_plan_with_one_launch_per_node(reference_matvecs):
+    g, _ = layer(N=1)
     assert plan(g) == (["add_norm_q8_f", "[", "matvec_q4k_q8", "matvec_q4k_q8", "matvec_q6k_q8", "]"]
                        + ATTN + ["quantize_q8x4", "matvec_q4k_q8", "add_norm_q8_f",
                                  "[", "matvec_q4k_q8", "matvec_q4k_q8", "]", "silu_mul_q8x4f", "matvec_q6k_q8",
                                  "vector_add"])
 
 
-def test_graphs_off_runs_no_concurrent_groups():
+@pytest.mark.parametrize("plant", ["glu_output", "glu_second_use", "gate_second_use", "up_view"])
+def test_decode_swiglu_fuses_only_when_nothing_else_reads_its_parts(plant):
+    """The fused gate / up / SWIGLU writes neither the f32 products nor the GLU's f32 result."""
+    g, _ = layer(N=1)
+    glu = next(x for x in g.nodes if x.op == kc.GGML_OP["glu"])
+    if plant == "glu_output":
+        glu.output = 1
+    elif plant == "glu_second_use":
+        glu.uses = 2
+    elif plant == "gate_second_use":
+        glu.src[0].contents.uses = 2
+    else:
+        glu.src[1].contents.view = 1
+    names = plan(g)
+    assert "decode_swiglu" not in names and "silu_mul_q8x4f" in names
+
+
+def test_graphs_off_runs_no_concurrent_groups(reference_matvecs):
     g, _ = layer(N=1)
     names = plan(g, graphs=0)
     assert "[" not in names and names[:4] == ["add_norm_q8_f", "matvec_q4k_q8", "matvec_q4k_q8", "matvec_q6k_q8"]
@@ -149,6 +182,12 @@ def test_nodes_without_work_are_skipped():
     g, t = layer(N=1)
     t["o"].compute = 0  # not computed by this backend (the scheduler's flag)
     names = plan(g)
+    assert "matvec_q4k_q8" not in names and "quantize_q8x4" not in names  # q / k / v fused, o skipped
+    kc.set_option("ggml_decode_matvec", 1)
+    try:
+        names = plan(g)
+    finally:
+        kc.set_option("ggml_decode_matvec", 0)
     assert names.count("matvec_q4k_q8") == 4 and "quantize_q8x4" not in names
     g = gg.Graph()
     x = g.leaf("f32", [512, 0])
@@ -168,7 +207,8 @@ def test_swiglu_unfused_when_rows_are_not_a_multiple_of_256():
 def test_decode_attention_is_split_over_the_context():
     g, _ = layer(N=1, n_kv=20000, kv_size=20480)
     names, ints = kc.ggml_graph_plan(g.nodes)
-    assert names[8:11] == ["set_rows_f16", "set_rows_f16", "flash_decode_f16"]
+    i = names.index("flash_decode_f16")
+    assert names[i - 2:i] == ["set_rows_f16", "set_rows_f16"]
     assert ints >= 8 * 313 * 66  # the partials of 8 heads x 313 chunks x (64 values + max + sum)
 
 

@@ -158,7 +158,7 @@ def check_mm(L, name, wname, xname, tol):
         assert kq.rel_diff(got, want) < tol, name
 
 
-def check_layer(L):
+def check_layer(L, fused_swiglu=False):
     s, N = L.s, L.N
     mm_tol = 1e-3 if N >= 64 else 0
     # attention norm (fused): y bit-exact
@@ -193,13 +193,25 @@ def check_layer(L):
     x, y = fused_norm_oracle(None, L.ffn_norm, s.n_embd, N, s.eps, a=L.get("o", np.float32), b=L.x)
     assert np.array_equal(kq.bits(L.get("ffn_inp", np.float32)), kq.bits(x)), "ffn_inp"
     assert np.array_equal(kq.bits(L.get("cur2", np.float32)), kq.bits(y)), "ffn norm"
-    check_mm(L, "gate", "wg", "cur2", mm_tol)
-    check_mm(L, "up", "wu", "cur2", mm_tol)
-    g, u = L.get("gate", np.float32), L.get("up", np.float32)
-    want = np.zeros_like(g)
-    O.kco_silu_mul(g, u, want, g.size)
-    assert np.allclose(L.get("act", np.float32), want, rtol=2e-6, atol=1e-30), "swiglu"
-    check_mm(L, "down", "wd", "act", mm_tol)
+    if fused_swiglu:
+        # gate, up and the GLU's f32 results are not written (one fused launch): the down projection
+        # against the oracle's chain from the GPU's normed input (a value within an ulp of a rounding
+        # tie may quantize one step apart: exp2 ulps of the two silu)
+        cur2 = L.get("cur2", np.float32).reshape(N, s.n_embd)
+        g = mul_mat_oracle(s.types["wg"], L.blocks["wg"], cur2, s.n_ff, s.n_embd)
+        u = mul_mat_oracle(s.types["wu"], L.blocks["wu"], cur2, s.n_ff, s.n_embd)
+        act = np.zeros(g.size, np.float32)
+        O.kco_silu_mul(g.reshape(-1), u.reshape(-1), act, g.size)
+        want = mul_mat_oracle(s.types["wd"], L.blocks["wd"], act.reshape(N, s.n_ff), s.n_embd, s.n_ff)
+        assert kq.rel_diff(L.get("down", np.float32).reshape(N, s.n_embd), want) < 1e-4, "down (fused swiglu)"
+    else:
+        check_mm(L, "gate", "wg", "cur2", mm_tol)
+        check_mm(L, "up", "wu", "cur2", mm_tol)
+        g, u = L.get("gate", np.float32), L.get("up", np.float32)
+        want = np.zeros_like(g)
+        O.kco_silu_mul(g, u, want, g.size)
+        assert np.allclose(L.get("act", np.float32), want, rtol=2e-6, atol=1e-30), "swiglu"
+        check_mm(L, "down", "wd", "act", mm_tol)
     want = L.get("down", np.float32) + L.get("ffn_inp", np.float32)
     assert np.array_equal(kq.bits(L.get("out", np.float32)), kq.bits(want)), "out"
 
@@ -226,8 +238,37 @@ def test_layer_graph_matches_the_oracle_node_by_node(case, graphs):
     st = be.stats()
     assert st["computes"] == 1 and st["graphs_recorded"] == graphs
     assert st["launches"] == len([n for n in names if n not in "[]"])
-    check_layer(L)
+    check_layer(L, fused_swiglu="decode_swiglu" in names)
     be.close()
+    L.free()
+
+
+@pytest.mark.parametrize("shape", [gg.LayerShape(), gg.LayerShape(n_embd=1024, neox=True, freq_factors=True)],
+                         ids=["llama", "neox-ff"])
+def test_fused_decode_matvecs_equal_one_launch_per_node(shape):
+    """One input column: q / k / v in one decode_matvec, gate / up / SWIGLU in one decode_swiglu --
+    every output the layer keeps (q, k, v, the caches, attention, o, the residuals, down) equals the
+    reference's one launch per node bit for bit."""
+    L = Layer(shape, 1, 90, seed=808)
+    names, _ = kc.ggml_graph_plan(L.g.nodes)
+    assert "decode_matvec" in names and "decode_swiglu" in names
+    kept = ("q", "k", "v", "qr", "kr", "attn", "o", "ffn_inp", "cur2", "down", "out")
+    got = {}
+    for opt in (1, 0):
+        kc.set_option("ggml_decode_matvec", opt)
+        try:
+            be = kc.GgmlBackend(graphs=1)
+            be.compute(L.g.nodes)
+            kc.synchronize()
+            got[opt] = {n: L.get(n, np.float32) for n in kept}
+            got[opt]["k_cache"], got[opt]["v_cache"] = L.get("k_cache", np.uint16), L.get("v_cache", np.uint16)
+            be.close()
+        finally:
+            kc.set_option("ggml_decode_matvec", 0)
+    for n in got[0]:
+        a, b = got[0][n], got[1][n]
+        assert np.array_equal(a.view(np.uint32) if a.dtype == np.float32 else a,
+                              b.view(np.uint32) if b.dtype == np.float32 else b), n
     L.free()
 
 
