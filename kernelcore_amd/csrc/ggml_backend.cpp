@@ -31,6 +31,7 @@
 #include "kdecode.hpp"
 #include "kernelcore/ggml_backend.h"
 #include "kernelcore/llm_kernels.h"
+#include "launch.hpp"
 #include "mul_mat_internal.hpp"
 
 using T = kcGgmlTensor;
@@ -337,11 +338,12 @@ E fusedSwiglu(Pass& p, const T* dst) {
     return kcamd::mulmat::fusedSwiglu(p.rec, sn, plan);
 }
 
-// ---- one input column through the fused decode matvec (kdecode.hip) ------------------------------
-// No reference counterpart: where the reference launches one matvec per MUL_MAT, 2-3 MUL_MATs of
-// one input column run as one launch whose rows each take the reference matvec's sum, from the same
-// per-32 slot; gate and up followed by SWIGLU also apply silu(gate) * up and quantize it per 32 into
-// the slot the down MUL_MAT reads. Option ggml_decode_matvec = 1 keeps one launch per node.
+// ---- fusions beyond the reference's --------------------------------------------------------------
+// No reference counterpart (option ggml_extra_fusions = 1 keeps the reference's launches): where the
+// reference launches one matvec per MUL_MAT, 2-3 MUL_MATs of one input column run as one launch
+// whose rows each take the reference matvec's sum, from the same per-32 slot; gate and up followed
+// by SWIGLU also apply silu(gate) * up and quantize it per 32 into the slot the down MUL_MAT reads;
+// ROPE of q and k and the two SET_ROWS into the caches run as one launch.
 
 // A launch of this build's own kernels (no by-name entry), named in the trace like the others.
 template <class F>
@@ -428,6 +430,52 @@ E decodeSwiglu(Pass& p, const T* ga, const T* up, const T* glu) {
     });
 }
 
+bool noop(const T* t) {
+    return t->op == KC_GGML_OP_NONE || t->op == KC_GGML_OP_RESHAPE || t->op == KC_GGML_OP_VIEW ||
+           t->op == KC_GGML_OP_PERMUTE || t->op == KC_GGML_OP_TRANSPOSE;
+}
+int nextWork(const T* const* nodes, int n, int j) {  // the next node with work after no-op nodes
+    while (j < n && noop(nodes[j])) ++j;
+    return j;
+}
+
+// nodes[i] = ROPE(q), then (past no-op nodes) ROPE(k) of the same positions, factors and
+// parameters, SET_ROWS(k cache, the roped k) and SET_ROWS(v cache, v) of the same row indices:
+// at[0..3) their indices.
+bool ropeKvOk(const T* const* nodes, int n, int i, int (&at)[3]) {
+    const T* rq = nodes[i];
+    const int a = nextWork(nodes, n, i + 1), b = a < n ? nextWork(nodes, n, a + 1) : n,
+              c = b < n ? nextWork(nodes, n, b + 1) : n;
+    if (c >= n) return false;
+    const T *rk = nodes[a], *sk = nodes[b], *sv = nodes[c];
+    if (rk->op != KC_GGML_OP_ROPE || sk->op != KC_GGML_OP_SET_ROWS || sv->op != KC_GGML_OP_SET_ROWS) return false;
+    if (!computed(rk) || !computed(sk) || !computed(sv)) return false;
+    if (rk->src[1] != rq->src[1] || rk->src[2] != rq->src[2] ||
+        std::memcmp(rk->op_params, rq->op_params, sizeof rq->op_params) != 0)
+        return false;
+    const int64_t hd = rq->ne[0], nt = rq->ne[2], kv = rk->ne[1] * hd;
+    if (rk->ne[0] != hd || rk->ne[2] != nt) return false;
+    const T *ks = sk->src[0], *vs = sv->src[0];
+    if (ks->data != rk->data || ks->ne[0] != kv || ks->ne[1] != nt || ks->nb[1] != size_t(kv) * 4) return false;
+    if (sv->src[1] != sk->src[1] || vs->ne[0] != kv || vs->ne[1] != nt || vs->nb[1] / 4 > INT32_MAX) return false;
+    if (vs->data == rq->data || vs->data == rk->data || sk->ne[1] != sv->ne[1]) return false;
+    at[0] = a, at[1] = b, at[2] = c;
+    return true;
+}
+
+E ropeKv(Pass& p, const T* rq, const T* rk, const T* sk, const T* sv) {
+    const int hd = int(rq->ne[0]);
+    const float* ff = rq->src[2] ? f32(rq->src[2]) : onesOf(p, hd / 2);
+    if (!ff) return kc::Error::InternalError;
+    const kcamd::RopeKvRows r{f32(rq->src[0]), f32w(rq), f32(rk->src[0]), f32w(rk), f32(sv->src[0]),
+                              static_cast<int*>(sk->data), static_cast<int*>(sv->data),
+                              static_cast<const int*>(rq->src[1]->data), static_cast<const int*>(sk->src[1]->data), ff,
+                              hd, int(rq->ne[1]), int(rk->ne[1]), int(rq->ne[2]), std::log2(paramF32(rq, 5)),
+                              (rq->op_params[2] & KC_GGML_ROPE_TYPE_NEOX) != 0, int(sv->src[0]->nb[1] / 4),
+                              int(sk->nb[1] / 4), int(sv->nb[1] / 4), int(sk->ne[1])};
+    return direct(p, "rope_set_rows", [&](hipStream_t s) { return kcamd::launchRopeKvRows(r, s); });
+}
+
 E setRows(Pass& p, const T* dst) {  // dst rows src1[r] (int64) = fp16(src0 row r) (:650-661)
     const T* src = dst->src[0];
     const T* idx = dst->src[1];
@@ -467,6 +515,12 @@ E flashAttn(Pass& p, const T* dst) {
         int* part = nullptr;
         if (E e = kcamd::mulmat::take(p.rec, kcamd::flashDecodePartFloats(d), &part); e != ok) return e;
         const kcFlashDecodeArgs a{f32(q), kd, vd, md, f32w(dst), reinterpret_cast<float*>(part), nullptr, d, scale};
+        if (d.N == 1 && (d.H * d.D) % 256 == 0 && kcamd::option("ggml_extra_fusions") != 1) {
+            // one token: the output's per-32 slot too, for the MUL_MAT that reads it (the o projection)
+            int* slot = nullptr;
+            if (E e = kcamd::mulmat::outputSlot(p.rec, f32(dst), d.H * d.D, 1, false, &slot); e != ok) return e;
+            return direct(p, "flash_decode_q8", [&](hipStream_t s) { return kcamd::launchFlashDecode(a, s, slot); });
+        }
         return launch(p, "flash_decode_f16", &a);
     }
     if (d.T <= 16384) {
@@ -505,7 +559,7 @@ E walk(Pass& p, const T* const* nodes, int n) {
         E e = ok;
         switch (node->op) {
             case KC_GGML_OP_MUL_MAT: {
-                if (kcamd::option("ggml_decode_matvec") != 1) {  // one input column: the fused decode matvec
+                if (kcamd::option("ggml_extra_fusions") != 1) {  // one input column: the fused decode matvec
                     int ga = 1;
                     while (i + ga < n && ga < 3 && nodes[i + ga]->op == KC_GGML_OP_MUL_MAT &&
                            nodes[i + ga]->src[1] == node->src[1] && computed(nodes[i + ga]))
@@ -569,7 +623,16 @@ E walk(Pass& p, const T* const* nodes, int n) {
                 break;
             }
             case KC_GGML_OP_MUL: e = mul(p, node); break;
-            case KC_GGML_OP_ROPE: e = rope(p, node); break;
+            case KC_GGML_OP_ROPE: {
+                int at[3];
+                if (kcamd::option("ggml_extra_fusions") != 1 && ropeKvOk(nodes, n, i, at)) {
+                    e = ropeKv(p, node, nodes[at[0]], nodes[at[1]], nodes[at[2]]);
+                    i = at[2];
+                } else {
+                    e = rope(p, node);
+                }
+                break;
+            }
             case KC_GGML_OP_GLU: e = node->ne[0] % 256 == 0 ? fusedSwiglu(p, node) : swiglu(p, node); break;
             case KC_GGML_OP_SET_ROWS: e = setRows(p, node); break;
             case KC_GGML_OP_FLASH_ATTN_EXT: e = flashAttn(p, node); break;

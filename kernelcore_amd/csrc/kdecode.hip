@@ -1116,9 +1116,12 @@ __global__ __launch_bounds__(256) void flash_decode_kernel(const float* __restri
 
 // out[i][h][:] of the chunk partials of (token i, head h) = blockIdx.x, in chunk order. The
 // partials of 16 chunks are loaded before they are merged (one memory round trip per 16 chunks).
+// slot (optional, one token): the head's D outputs also quantized per 32 into the per-32 slot of
+// the token's nb = H * D / 32 blocks (quantize_q8x4.cu: codes and d / sum pairs; quant8).
 template <int D>
 __global__ __launch_bounds__(128) void flash_merge_kernel(const float* __restrict__ part, float* __restrict__ out,
-                                                          int nch) {
+                                                          int nch, int* __restrict__ slot, int nb) {
+    __shared__ float ov[D];
     const float* base = part + (size_t)blockIdx.x * nch * (D + 2);
     for (int e = threadIdx.x; e < D; e += 128) {
         float M = -INFINITY, L = 0.0f, O = 0.0f;
@@ -1148,6 +1151,18 @@ __global__ __launch_bounds__(128) void flash_merge_kernel(const float* __restric
             }
         }
         out[(size_t)blockIdx.x * D + e] = O / L;
+        ov[e] = O / L;
+    }
+    if (slot) {
+        __syncthreads();
+        const int t = threadIdx.x;
+        if (t < D / 4) {  // eight lanes per block of 32, four values each
+            const float y[4] = {ov[4 * t], ov[4 * t + 1], ov[4 * t + 2], ov[4 * t + 3]};
+            const Q8L o = quant8(y);
+            const int b = blockIdx.x * (D / 32) + (t >> 3), j = t & 7;
+            slot[b * 8 + j] = o.w;
+            if (j == 0) *reinterpret_cast<float2*>(slot + nb * 8 + 2 * b) = make_float2(o.d, (float)o.sum);
+        }
     }
 }
 
@@ -1305,7 +1320,7 @@ size_t flashDecodePartFloats(const kcFaDims& d) {
     return (size_t)d.N * d.H * ((d.T + kChunk - 1) / kChunk) * (d.D + 2);
 }
 
-int launchFlashDecode(const kcFlashDecodeArgs& a, hipStream_t s) {
+int launchFlashDecode(const kcFlashDecodeArgs& a, hipStream_t s, int* slot) {
     const kcFaDims& d = a.d;
     if (!flashDecodeSupports(d.D, d.group)) return fromHip(hipErrorInvalidValue, "flash_decode_f16: shape");
     const int nch = (d.T + kChunk - 1) / kChunk;
@@ -1318,8 +1333,12 @@ int launchFlashDecode(const kcFlashDecodeArgs& a, hipStream_t s) {
     KC_FD(64, 1) KC_FD(64, 2) KC_FD(64, 3) KC_FD(64, 4) KC_FD(64, 5) KC_FD(64, 6) KC_FD(64, 7) KC_FD(64, 8)
 #undef KC_FD
     if (int e = fromHip(hipGetLastError(), "flash_decode_f16")) return e;
-    if (d.D == 128) hipLaunchKernelGGL(flash_merge_kernel<128>, dim3(d.N * d.H), dim3(128), 0, s, a.part, a.out, nch);
-    else hipLaunchKernelGGL(flash_merge_kernel<64>, dim3(d.N * d.H), dim3(128), 0, s, a.part, a.out, nch);
+    if (slot && (d.N != 1 || (d.H * d.D) % 32)) return fromHip(hipErrorInvalidValue, "flash_decode_f16: slot of one token");
+    const int nb = d.H * d.D / 32;
+    if (d.D == 128)
+        hipLaunchKernelGGL(flash_merge_kernel<128>, dim3(d.N * d.H), dim3(128), 0, s, a.part, a.out, nch, slot, nb);
+    else
+        hipLaunchKernelGGL(flash_merge_kernel<64>, dim3(d.N * d.H), dim3(128), 0, s, a.part, a.out, nch, slot, nb);
     return fromHip(hipGetLastError(), "flash_decode_f16: merge");
 }
 

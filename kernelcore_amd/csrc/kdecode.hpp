@@ -84,6 +84,7 @@ int launchAttnDecode(AttnDecodeArgs a, int D, int Hkv, int max_ctx, hipStream_t 
 // flash_decode_f16 (kcFlashDecodeArgs): the split-context FLASH_ATTN_EXT for D 64 / 128, group <= 8.
 bool flashDecodeSupports(int D, int G);
 size_t flashDecodePartFloats(const kcFaDims& d);
-int launchFlashDecode(const kcFlashDecodeArgs& a, hipStream_t s);
+// slot (optional, one query token): the output also quantized into a per-32 slot of H * D values.
+int launchFlashDecode(const kcFlashDecodeArgs& a, hipStream_t s, int* slot = nullptr);
 
 }  // namespace kcamd

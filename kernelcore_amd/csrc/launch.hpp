@@ -90,6 +90,24 @@ int launchMulRows(const kcMulRowsArgs& a, hipStream_t s);
 int launchSiluMul(const kcSiluMulArgs& a, hipStream_t s);
 int launchRmsNorm(const kcRmsNormArgs& a, hipStream_t s);
 int launchRope(const kcRopeGgmlArgs& a, hipStream_t s);
+// ROPE of q and k, and the fp16 rows of the roped k and of v into the caches at rows idx (int64),
+// in one launch; the roped k also kept in kr (layer_ops.hip rope_kv_rows_kernel).
+struct RopeKvRows {
+    const float* q;
+    float* qr;
+    const float* k;
+    float* kr;
+    const float* v;
+    int *kcache, *vcache;
+    const int* pos;
+    const int* idx;
+    const float* ff;
+    int head_dim, nh, nkv, n;
+    float log2_base;
+    bool neox;
+    int src_v, k_row, v_row, dst_rows;  // v row stride (floats), cache row strides (32-bit words), cache rows
+};
+int launchRopeKvRows(const RopeKvRows& r, hipStream_t s);
 int launchSetRows(const kcSetRowsF16Args& a, hipStream_t s);
 int launchFaScores(const kcFaScoresArgs& a, hipStream_t s);
 int launchFaMax(const kcFaMaxArgs& a, hipStream_t s);

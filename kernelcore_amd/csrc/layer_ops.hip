@@ -480,6 +480,55 @@ __global__ void rope_qk_store_kernel(const float* __restrict__ q, float* __restr
     }
 }
 
+// The ggml graph's ROPE(q), ROPE(k), SET_ROWS(k cache, roped k, idx) and SET_ROWS(v cache, v, idx)
+// in one launch (rope_ggml.cu, set_rows_f16.cu): one thread per (token, group of 4 heads, pair) as
+// rope_qk_store_kernel, which also keeps the roped k in kr and takes the cache rows from idx (int64,
+// low words; rows outside [0, dst_rows) are not stored). Sources: q, k contiguous [n][heads][hd];
+// v rows src_v floats apart; cache rows k_row / v_row 32-bit words apart.
+__global__ void rope_kv_rows_kernel(const float* __restrict__ q, float* __restrict__ qr, const float* __restrict__ k,
+                                    float* __restrict__ kr, const float* __restrict__ v, unsigned short* __restrict__ kc,
+                                    unsigned short* __restrict__ vc, const int* __restrict__ pos,
+                                    const int* __restrict__ idx, const float* __restrict__ ff, int pairs, int nh,
+                                    int nkv, int n, float log2_base, int m1, int m2, int src_v, int k_row, int v_row,
+                                    int dst_rows) {
+    const int ng = (nh + nkv + 3) / 4;
+    const long long id = blockIdx.x * (long long)blockDim.x + threadIdx.x;
+    if (id >= (long long)n * ng * pairs) return;
+    const int i = (int)(id % pairs);
+    const long long tg = id / pairs;
+    const int hg = (int)(tg % ng), t = (int)(tg / ng);
+    const float theta = (float)pos[t] * exp2f(-(float)i / (float)pairs * log2_base) / ff[i];
+    const float c = cosf(theta), sn = sinf(theta);
+    const int row = idx[2 * t];
+    const bool store = row >= 0 && row < dst_rows;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int h = hg * 4 + u;
+        if (h < nh) {
+            const size_t a = 2 * ((size_t)t * nh + h) * pairs + (size_t)i * m1;
+            const float x0 = q[a], x1 = q[a + m2];
+            qr[a] = x0 * c - x1 * sn;
+            qr[a + m2] = x0 * sn + x1 * c;
+        } else if (h < nh + nkv) {
+            const int hk = h - nh;
+            const size_t a = 2 * ((size_t)t * nkv + hk) * pairs + (size_t)i * m1;
+            const float x0 = k[a], x1 = k[a + m2];
+            const float y0 = x0 * c - x1 * sn, y1 = x0 * sn + x1 * c;
+            kr[a] = y0;
+            kr[a + m2] = y1;
+            if (store) {
+                const size_t o = 2 * (size_t)hk * pairs + (size_t)i * m1;
+                const size_t e = (size_t)row * k_row * 2 + o, f = (size_t)row * v_row * 2 + o;
+                const size_t av = (size_t)t * src_v + o;
+                kc[e] = (unsigned short)f2h(y0);
+                kc[e + m2] = (unsigned short)f2h(y1);
+                vc[f] = (unsigned short)f2h(v[av]);
+                vc[f + m2] = (unsigned short)f2h(v[av + m2]);
+            }
+        }
+    }
+}
+
 // Residual add + RMS norm + per-256 quantization of a batch (add_sumsq_f.cu then norm_mul_q8k_f.cu
 // in one workgroup per row): x = a + (b [+ b2]) (a null: x = b, not stored), the per-32 sums of
 // squares in order, their total in block order, y = x r w quantized per 256 into the row's slot.
@@ -811,6 +860,17 @@ int launchRopeQKStore(const float* q, float* qr, const float* k, const float* v,
                        reinterpret_cast<unsigned short*>(kcache), reinterpret_cast<unsigned short*>(vcache), pos, ff,
                        pairs, nh, nkv, n, log2_base, neox ? 1 : 2, neox ? pairs : 1, dst_row, dst_rows);
     return fromHip(hipGetLastError(), "rope + kv store");
+}
+
+int launchRopeKvRows(const RopeKvRows& r, hipStream_t s) {
+    const int pairs = r.head_dim / 2;
+    const long long threads = (long long)r.n * ((r.nh + r.nkv + 3) / 4) * pairs;
+    if (threads <= 0) return 0;
+    hipLaunchKernelGGL(rope_kv_rows_kernel, dim3(blocksFor(threads)), dim3(256), 0, s, r.q, r.qr, r.k, r.kr, r.v,
+                       reinterpret_cast<unsigned short*>(r.kcache), reinterpret_cast<unsigned short*>(r.vcache), r.pos,
+                       r.idx, r.ff, pairs, r.nh, r.nkv, r.n, r.log2_base, r.neox ? 1 : 2, r.neox ? pairs : 1, r.src_v,
+                       r.k_row, r.v_row, r.dst_rows);
+    return fromHip(hipGetLastError(), "rope + set_rows");
 }
 
 int launchAddNormQ8K(const float* a, const float* b, const float* b2, float* out, const float* w, int* q, int n,

@@ -8,6 +8,8 @@ Each fusion rule is checked both ways: the layer graph llama.cpp builds fuses, a
 change that ggml_can_fuse or the reference's pattern must reject (a second use of the norm, a
 norm that is a graph output or a view, a MUL by a full matrix, rows not a multiple of 256, an
 ADD whose result the norm does not read) turns the fusion off."""
+import ctypes as C
+
 import pytest
 
 import kernelcore_amd as kc
@@ -24,7 +26,9 @@ def plan(g, **cfg):
     return kc.ggml_graph_plan(g.nodes, **cfg)[0]
 
 
-ATTN = ["rope_ggml", "rope_ggml", "set_rows_f16", "set_rows_f16", "flash_decode_f16"]
+ATTN = ["rope_ggml", "rope_ggml", "set_rows_f16", "set_rows_f16", "flash_decode_f16"]  # the reference's launches
+# ROPE of q and k and the two SET_ROWS in one launch; one token's attention also quantizes its output
+ATTN1 = ["rope_set_rows", "flash_decode_q8"]
 
 
 # ---- graph_compute's walk --------------------------------------------------------------------------------------
@@ -32,18 +36,17 @@ ATTN = ["rope_ggml", "rope_ggml", "set_rows_f16", "set_rows_f16", "flash_decode_
 @pytest.fixture
 def reference_matvecs():
     """The reference's one launch per MUL_MAT node (no fused decode matvec)."""
-    kc.set_option("ggml_decode_matvec", 1)
+    kc.set_option("ggml_extra_fusions", 1)
     yield
-    kc.set_option("ggml_decode_matvec", 0)
+    kc.set_option("ggml_extra_fusions", 0)
 
 
 def test_decode_layer_plan():
     g, _ = layer(N=1)
     # the per-32 norms: add_sumsq_f / sumsq_part and norm_mul_q8_f in one add_norm_q8_f launch; one
     # input column: q / k / v in one fused decode matvec, gate / up and the SWIGLU in another
-    assert plan(g) == (["add_norm_q8_f", "decode_matvec"] + ATTN +
-                       ["quantize_q8x4", "matvec_q4k_q8", "add_norm_q8_f", "decode_swiglu", "matvec_q6k_q8",
-                        "vector_add"])
+    assert plan(g) == (["add_norm_q8_f", "decode_matvec"] + ATTN1 +
+                       ["matvec_q4k_q8", "add_norm_q8_f", "decode_swiglu", "matvec_q6k_q8", "vector_add"])
 
 
 def test_decode_layer_plan_with_one_launch_per_node(reference_matvecs):
@@ -52,6 +55,21 @@ def test_decode_layer_plan_with_one_launch_per_node(reference_matvecs):
                        + ATTN + ["quantize_q8x4", "matvec_q4k_q8", "add_norm_q8_f",
                                  "[", "matvec_q4k_q8", "matvec_q4k_q8", "]", "silu_mul_q8x4f", "matvec_q6k_q8",
                                  "vector_add"])
+
+
+@pytest.mark.parametrize("plant", ["positions", "row_indices", "params"])
+def test_rope_and_cache_rows_fuse_only_with_shared_positions_rows_and_parameters(plant):
+    g, _ = layer(N=2)
+    ropes = [x for x in g.nodes if x.op == kc.GGML_OP["rope"]]
+    rows = [x for x in g.nodes if x.op == kc.GGML_OP["set_rows"]]
+    if plant == "positions":
+        ropes[1].src[1] = C.pointer(g.leaf("i32", [2]))
+    elif plant == "row_indices":
+        rows[1].src[1] = C.pointer(g.leaf("i64", [2]))
+    else:
+        ropes[1].op_params[5] = ropes[1].op_params[5] + 1  # another frequency base
+    names = plan(g)
+    assert "rope_set_rows" not in names and names.count("rope_ggml") == 2 and names.count("set_rows_f16") == 2
 
 
 @pytest.mark.parametrize("plant", ["glu_output", "glu_second_use", "gate_second_use", "up_view"])
@@ -92,7 +110,7 @@ def test_batch_layer_plans(N, cfg, mm, quant):
     norm0 = ["sumsq_part", "norm_mul_q8k_f"] if k == "q8k" else ["add_norm_q8_f"]
     norm1 = ["add_sumsq_f", "norm_mul_q8k_f"] if k == "q8k" else ["add_norm_q8_f"]
     silu = "silu_mul_q8kf" if k == "q8k" else "silu_mul_q8x4f"
-    attn = ATTN if N <= 8 else ATTN[:4] + ["flash_attn_f16"]  # batches past 8 tokens: the one-kernel form
+    attn = ["rope_set_rows", "flash_decode_f16" if N <= 8 else "flash_attn_f16"]  # past 8 tokens: one kernel
     want = (norm0 + ["[", mm.format("q4k"), mm.format("q4k"), mm.format("q6k"), "]"] + attn +
             [quant, mm.format("q4k")] + norm1 + ["[", mm.format("q4k"), mm.format("q4k"), "]", silu,
              mm.format("q6k"), "vector_add"])
@@ -183,11 +201,11 @@ def test_nodes_without_work_are_skipped():
     t["o"].compute = 0  # not computed by this backend (the scheduler's flag)
     names = plan(g)
     assert "matvec_q4k_q8" not in names and "quantize_q8x4" not in names  # q / k / v fused, o skipped
-    kc.set_option("ggml_decode_matvec", 1)
+    kc.set_option("ggml_extra_fusions", 1)
     try:
         names = plan(g)
     finally:
-        kc.set_option("ggml_decode_matvec", 0)
+        kc.set_option("ggml_extra_fusions", 0)
     assert names.count("matvec_q4k_q8") == 4 and "quantize_q8x4" not in names
     g = gg.Graph()
     x = g.leaf("f32", [512, 0])
@@ -207,15 +225,16 @@ def test_swiglu_unfused_when_rows_are_not_a_multiple_of_256():
 def test_decode_attention_is_split_over_the_context():
     g, _ = layer(N=1, n_kv=20000, kv_size=20480)
     names, ints = kc.ggml_graph_plan(g.nodes)
-    i = names.index("flash_decode_f16")
-    assert names[i - 2:i] == ["set_rows_f16", "set_rows_f16"]
+    i = names.index("flash_decode_q8")
+    assert names[i - 1] == "rope_set_rows"
     assert ints >= 8 * 313 * 66  # the partials of 8 heads x 313 chunks x (64 values + max + sum)
 
 
 def test_long_context_batch_attention_takes_the_four_kernels():
     g, _ = layer(N=12, n_kv=20000, kv_size=20480)
     names, ints = kc.ggml_graph_plan(g.nodes, attn_tokens=16)
-    assert names[9:15] == ["set_rows_f16", "set_rows_f16", "fa_scores", "fa_max", "fa_exp", "fa_values"]
+    i = names.index("rope_set_rows")
+    assert names[i:i + 5] == ["rope_set_rows", "fa_scores", "fa_max", "fa_exp", "fa_values"]
     assert ints >= 8 * 12 * 20000  # the scores of 8 heads x 12 tokens in the scratch
 
 

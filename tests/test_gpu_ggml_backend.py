@@ -255,7 +255,7 @@ def test_fused_decode_matvecs_equal_one_launch_per_node(shape):
     kept = ("q", "k", "v", "qr", "kr", "attn", "o", "ffn_inp", "cur2", "down", "out")
     got = {}
     for opt in (1, 0):
-        kc.set_option("ggml_decode_matvec", opt)
+        kc.set_option("ggml_extra_fusions", opt)
         try:
             be = kc.GgmlBackend(graphs=1)
             be.compute(L.g.nodes)
@@ -264,7 +264,7 @@ def test_fused_decode_matvecs_equal_one_launch_per_node(shape):
             got[opt]["k_cache"], got[opt]["v_cache"] = L.get("k_cache", np.uint16), L.get("v_cache", np.uint16)
             be.close()
         finally:
-            kc.set_option("ggml_decode_matvec", 0)
+            kc.set_option("ggml_extra_fusions", 0)
     for n in got[0]:
         a, b = got[0][n], got[1][n]
         assert np.array_equal(a.view(np.uint32) if a.dtype == np.float32 else a,
