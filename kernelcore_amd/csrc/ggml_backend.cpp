@@ -343,7 +343,10 @@ E fusedSwiglu(Pass& p, const T* dst) {
 // reference launches one matvec per MUL_MAT, 2-3 MUL_MATs of one input column run as one launch
 // whose rows each take the reference matvec's sum, from the same per-32 slot; gate and up followed
 // by SWIGLU also apply silu(gate) * up and quantize it per 32 into the slot the down MUL_MAT reads;
-// ROPE of q and k and the two SET_ROWS into the caches run as one launch.
+// ROPE of q and k and the two SET_ROWS into the caches run as one launch; a MUL_MAT whose one use is
+// an ADD writes the ADD's result (residual + each row's sum); RMS_NORM + MUL whose one use is a
+// group of MUL_MATs (q / k / v, gate / up + SWIGLU) is computed in the group's launch (the norm as
+// add_norm_q8_f's, per workgroup).
 
 // A launch of this build's own kernels (no by-name entry), named in the trace like the others.
 template <class F>
@@ -357,13 +360,22 @@ E direct(Pass& p, const char* name, F&& fn) {
 
 bool kquant(const T* w) { return w->type == KC_GGML_TYPE_Q4_K || w->type == KC_GGML_TYPE_Q6_K; }
 bool computed(const T* t) { return t->compute && !empty(t); }
+bool noop(const T* t) {
+    return t->op == KC_GGML_OP_NONE || t->op == KC_GGML_OP_RESHAPE || t->op == KC_GGML_OP_VIEW ||
+           t->op == KC_GGML_OP_PERMUTE || t->op == KC_GGML_OP_TRANSPOSE;
+}
+int nextWork(const T* const* nodes, int n, int j) {  // the next node with work after no-op nodes
+    while (j < n && noop(nodes[j])) ++j;
+    return j;
+}
 
 // MUL_MATs mm[0..g) of the one-column input x through one decode matvec with epilogue epi
-bool decodeMatvecOk(const T* x, const T* const* mm, int g, int epi, int tpw) {
+// (prologue pro: the input's per-32 slot, or the norm of the row the input is the norm of)
+bool decodeMatvecOk(const T* x, const T* const* mm, int g, int epi, int tpw, int pro = kcamd::kProSlot) {
     if (g < 1 || g > 3 || !f32c(x) || nrows(x) != 1 || x->ne[0] % 256 || x->ne[0] > INT_MAX) return false;
     for (int j = 0; j < g; ++j)
         if (!kquant(mm[j]->src[0]) || mm[j]->src[0]->ne[0] != x->ne[0] || !f32c(mm[j])) return false;
-    return kcamd::planDecodeMatvec(kcamd::kProSlot, epi, int(x->ne[0]), tpw).nw > 0;
+    return kcamd::planDecodeMatvec(pro, epi, int(x->ne[0]), tpw).nw > 0;
 }
 
 // The per-32 slot of the group's input (the fused norm's, or quantized now) as DmvArgs.
@@ -384,6 +396,33 @@ kcamd::DmvPart dmvPart(const T* mm, float* y) {
     return kcamd::DmvPart{w->data, y, int(w->ne[1]), w->type == KC_GGML_TYPE_Q6_K ? 1 : 0, 0, 0};
 }
 
+// nodes[i] = a one-column K-quant MUL_MAT (one use, not a view or an output) and the next node with
+// work the ADD of it and a residual of its shape: *add = that ADD's index.
+bool matvecAddOk(const T* const* nodes, int n, int i, int* add) {
+    const T* mm = nodes[i];
+    if (mm->uses != 1 || mm->view || mm->output) return false;
+    const int j = nextWork(nodes, n, i + 1);
+    if (j >= n || nodes[j]->op != KC_GGML_OP_ADD || !computed(nodes[j])) return false;
+    const T* ad = nodes[j];
+    const T* r = ad->src[0] == mm ? ad->src[1] : (ad->src[1] == mm ? ad->src[0] : nullptr);
+    if (!r || r == mm || !f32c(r) || !sameShape(r, mm) || !f32c(ad)) return false;
+    if (!decodeMatvecOk(mm->src[1], &mm, 1, kcamd::kEpiResid, 1)) return false;
+    *add = j;
+    return true;
+}
+
+E decodeMatvecAdd(Pass& p, const T* mm, const T* ad) {
+    kcamd::DmvArgs a{};
+    if (E e = slotArgs(p, mm, a); e != ok) return e;
+    a.p0 = dmvPart(mm, f32w(ad));
+    a.nparts = 1;
+    a.tpw = 1;
+    a.r = f32(ad->src[0] == mm ? ad->src[1] : ad->src[0]);
+    return direct(p, "decode_matvec_add", [&](hipStream_t s) {
+        return kcamd::launchDecodeMatvec(kcamd::kProSlot, kcamd::kEpiResid, a, s);
+    });
+}
+
 E decodeGroup(Pass& p, const T* const* mm, int g) {
     kcamd::DmvArgs a{};
     if (E e = slotArgs(p, mm[0], a); e != ok) return e;
@@ -399,7 +438,7 @@ E decodeGroup(Pass& p, const T* const* mm, int g) {
 // nodes[i], nodes[i + 1] = gate, up of one input column and nodes[i + 2] their SWIGLU, whose one
 // use is a K-quant MUL_MAT (which reads the slot, not the f32 result); gate's and up's one use is
 // the GLU. None of the three is a view or a graph output.
-bool decodeSwigluOk(const T* const* nodes, int n, int i) {
+bool decodeSwigluOk(const T* const* nodes, int n, int i, int pro = kcamd::kProSlot) {
     if (i + 2 >= n) return false;
     const T *ga = nodes[i], *up = nodes[i + 1], *glu = nodes[i + 2];
     if (glu->op != KC_GGML_OP_GLU || glu->src[0] != ga || glu->src[1] != up || !computed(glu) ||
@@ -414,7 +453,54 @@ bool decodeSwigluOk(const T* const* nodes, int n, int i) {
             if (nodes[j]->src[s] == glu) user = nodes[j];
     if (!user || user->op != KC_GGML_OP_MUL_MAT || user->src[1] != glu || !kquant(user->src[0])) return false;
     const T* mm[2] = {ga, up};
-    return decodeMatvecOk(ga->src[1], mm, 2, kcamd::kEpiSwiglu, 2);
+    return decodeMatvecOk(ga->src[1], mm, 2, kcamd::kEpiSwiglu, 2, pro);
+}
+
+// nodes[i] = RMS_NORM of one row and nodes[i + 1] its MUL by the norm weight (ggml_can_fuse), whose
+// only uses are 2-3 MUL_MATs after it (not a view or an output): g.first, g.n = that group;
+// g.glu: the group is gate / up followed by their SWIGLU (decodeSwigluOk).
+struct NormGroup {
+    int first = 0, n = 0;
+    bool glu = false;
+};
+bool normGroupOk(const T* const* nodes, int n, int i, NormGroup& g) {
+    static const int kNormMul[2] = {KC_GGML_OP_RMS_NORM, KC_GGML_OP_MUL};
+    if (i + 1 >= n || !canFuse(nodes, n, i, kNormMul, 2)) return false;
+    const T *norm = nodes[i], *mul = nodes[i + 1];
+    if (mul->src[0] != norm || !rowVectorOf(mul->src[1], norm) || mul->view || mul->output) return false;
+    const int j = nextWork(nodes, n, i + 2);
+    int c = 0;
+    while (j + c < n && c < 3 && nodes[j + c]->op == KC_GGML_OP_MUL_MAT && nodes[j + c]->src[1] == mul &&
+           computed(nodes[j + c]))
+        ++c;
+    if (c < 2 || mul->uses != c) return false;
+    g.first = j, g.n = c;
+    g.glu = c == 2 && decodeSwigluOk(nodes, n, j, kcamd::kProNorm);
+    return g.glu || decodeMatvecOk(mul, nodes + j, c, kcamd::kEpiStore, 2, kcamd::kProNorm);
+}
+
+E decodeNormGroup(Pass& p, const T* norm, const T* mul, const T* const* mm, const NormGroup& g) {
+    kcamd::DmvArgs a{};
+    a.k = int(norm->src[0]->ne[0]);
+    a.x = f32(norm->src[0]);
+    a.nw = f32(mul->src[1]);
+    a.eps = paramF32(norm, 0);
+    a.tpw = 2;
+    if (g.glu) {
+        a.p0 = dmvPart(mm[0], nullptr);
+        a.p1 = dmvPart(mm[1], nullptr);
+        a.nparts = 2;
+        if (E e = kcamd::mulmat::outputSlot(p.rec, f32(mm[2]), a.p0.rows, 1, false, &a.qout); e != ok) return e;
+        return direct(p, "decode_norm_swiglu", [&](hipStream_t s) {
+            return kcamd::launchDecodeMatvec(kcamd::kProNorm, kcamd::kEpiSwiglu, a, s);
+        });
+    }
+    kcamd::DmvPart* ps[3] = {&a.p0, &a.p1, &a.p2};
+    for (int j = 0; j < g.n; ++j) *ps[j] = dmvPart(mm[j], f32w(mm[j]));
+    a.nparts = g.n;
+    return direct(p, "decode_norm_matvec", [&](hipStream_t s) {
+        return kcamd::launchDecodeMatvec(kcamd::kProNorm, kcamd::kEpiStore, a, s);
+    });
 }
 
 E decodeSwiglu(Pass& p, const T* ga, const T* up, const T* glu) {
@@ -430,14 +516,6 @@ E decodeSwiglu(Pass& p, const T* ga, const T* up, const T* glu) {
     });
 }
 
-bool noop(const T* t) {
-    return t->op == KC_GGML_OP_NONE || t->op == KC_GGML_OP_RESHAPE || t->op == KC_GGML_OP_VIEW ||
-           t->op == KC_GGML_OP_PERMUTE || t->op == KC_GGML_OP_TRANSPOSE;
-}
-int nextWork(const T* const* nodes, int n, int j) {  // the next node with work after no-op nodes
-    while (j < n && noop(nodes[j])) ++j;
-    return j;
-}
 
 // nodes[i] = ROPE(q), then (past no-op nodes) ROPE(k) of the same positions, factors and
 // parameters, SET_ROWS(k cache, the roped k) and SET_ROWS(v cache, v) of the same row indices:
@@ -574,6 +652,12 @@ E walk(Pass& p, const T* const* nodes, int n) {
                         i += ga - 1;
                         break;
                     }
+                    int add = 0;
+                    if (ga == 1 && matvecAddOk(nodes, n, i, &add)) {
+                        e = decodeMatvecAdd(p, node, nodes[add]);
+                        i = add;
+                        break;
+                    }
                 }
                 // consecutive MUL_MATs of one input (q, k, v; gate, up) as one step
                 int g = 1;
@@ -595,6 +679,13 @@ E walk(Pass& p, const T* const* nodes, int n) {
             }
             case KC_GGML_OP_ADD:
             case KC_GGML_OP_RMS_NORM: {
+                NormGroup ng;
+                if (node->op == KC_GGML_OP_RMS_NORM && kcamd::option("ggml_extra_fusions") != 1 &&
+                    normGroupOk(nodes, n, i, ng)) {  // the norm in the group's launch
+                    e = decodeNormGroup(p, node, nodes[i + 1], nodes + ng.first, ng);
+                    i = ng.first + ng.n - 1 + (ng.glu ? 1 : 0);
+                    break;
+                }
                 // [ADD +] RMS_NORM + MUL by a row vector (the norm weight): the fused producer
                 // (n % 256 == 0), else vector_add or a one-pass rms_norm
                 const int ni = node->op == KC_GGML_OP_ADD ? i + 1 : i;  // the RMS_NORM node

@@ -504,7 +504,7 @@ __global__ __launch_bounds__(EPI == kEpiSwiglu ? 768 : 512) void dmv_kernel(DmvA
         const Slot s = slotOf<EPI>(a, part, tid >> 4);
         row = s.tile * kTileRows + (tid & 15);
         row_ok = s.live && row < P.rows;
-        if (EPI == kEpiResid) y_old = P.y[row_ok ? row : 0];
+        if (EPI == kEpiResid) y_old = (a.r ? a.r : P.y)[row_ok ? row : 0];
     }
     // The norm prologue: with 8 lanes per block in the wide SwiGLU workgroups (at most two passes:
     // the launcher checks n / 4 <= 2 * threads), one thread per block in the others (where 8 lanes

@@ -39,6 +39,7 @@ struct DmvArgs {
     const int* xq;    // kProSlot
     const float* xd;  // kProSlot
     int* qout;        // kEpiSwiglu: per-32 slot of p0.rows values
+    const float* r;   // kEpiResid: the residual read (y = r + acc); null: y itself, updated in place
 };
 
 struct QkPostArgs {

@@ -43,10 +43,10 @@ def reference_matvecs():
 
 def test_decode_layer_plan():
     g, _ = layer(N=1)
-    # the per-32 norms: add_sumsq_f / sumsq_part and norm_mul_q8_f in one add_norm_q8_f launch; one
-    # input column: q / k / v in one fused decode matvec, gate / up and the SWIGLU in another
-    assert plan(g) == (["add_norm_q8_f", "decode_matvec"] + ATTN1 +
-                       ["matvec_q4k_q8", "add_norm_q8_f", "decode_swiglu", "matvec_q6k_q8", "vector_add"])
+    # one input column: the attention norm inside the q / k / v launch, the FFN norm inside the gate /
+    # up / SWIGLU launch, the o and down products each with their residual ADD
+    assert plan(g) == (["decode_norm_matvec"] + ATTN1 + ["decode_matvec_add", "decode_norm_swiglu",
+                                                         "decode_matvec_add"])
 
 
 def test_decode_layer_plan_with_one_launch_per_node(reference_matvecs):
@@ -55,6 +55,25 @@ def test_decode_layer_plan_with_one_launch_per_node(reference_matvecs):
                        + ATTN + ["quantize_q8x4", "matvec_q4k_q8", "add_norm_q8_f",
                                  "[", "matvec_q4k_q8", "matvec_q4k_q8", "]", "silu_mul_q8x4f", "matvec_q6k_q8",
                                  "vector_add"])
+
+
+def test_matvec_add_fuses_only_when_the_add_is_its_one_use():
+    g, t = layer(N=1)
+    t["o"].uses = 2  # the o product read again elsewhere: written, then added by the FFN norm
+    names = plan(g)
+    assert names.count("decode_matvec_add") == 1 and "add_norm_q8_f" in names and "matvec_q4k_q8" in names
+
+
+@pytest.mark.parametrize("plant", ["output", "second_use"])
+def test_norm_inside_the_matvecs_only_when_they_are_its_only_uses(plant):
+    g, _ = layer(N=1)
+    mul = next(x for x in g.nodes if x.op == kc.GGML_OP["mul"])  # the attention norm's weight
+    if plant == "output":
+        mul.output = 1
+    else:
+        mul.uses = 4
+    names = plan(g)
+    assert names[:2] == ["add_norm_q8_f", "decode_matvec"] and names.count("decode_norm_matvec") == 0
 
 
 @pytest.mark.parametrize("plant", ["positions", "row_indices", "params"])
@@ -272,11 +291,18 @@ def test_disabled_claims_nothing_and_makes_no_backend():
     assert e.value.name == "UnsupportedOperation"
 
 
-def test_scratch_requirement():
+def test_scratch_requirement(reference_matvecs):
     g, _ = layer(N=1)
     # four per-32 slots of 512 or 1024 values (11 ints per 32: 880), the attention partials of 8 heads x
     # 1 chunk x (64 values + max + sum) = 528
     assert kc.ggml_graph_plan(g.nodes)[1] == 880 + 528
+
+
+def test_scratch_requirement_of_the_fused_decode_layer():
+    g, _ = layer(N=1)
+    # the norms run inside the matvec launches: the slots of the attention output (512 values: 176) and
+    # of the SWIGLU result (1024: 352), and the attention partials (528)
+    assert kc.ggml_graph_plan(g.nodes)[1] == 176 + 352 + 528
 
 
 # ---- supports_op ---------------------------------------------------------------------------------------------

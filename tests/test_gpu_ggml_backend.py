@@ -145,11 +145,12 @@ def mul_mat_oracle(qtype, blocks, xcols, rows, k):
     return y.reshape(ncols, rows)
 
 
-def check_mm(L, name, wname, xname, tol):
+def check_mm(L, name, wname, xname, tol, xcols=None):
     s = L.s
     w = L.t[wname]
     rows, k = w.ne[1], w.ne[0]
-    xcols = L.get(xname, np.float32).reshape(L.N, k)
+    if xcols is None:
+        xcols = L.get(xname, np.float32).reshape(L.N, k)
     got = L.get(name, np.float32).reshape(L.N, rows)
     want = mul_mat_oracle(s.types[wname], L.blocks[wname], xcols, rows, k)
     if tol == 0:
@@ -158,14 +159,22 @@ def check_mm(L, name, wname, xname, tol):
         assert kq.rel_diff(got, want) < tol, name
 
 
-def check_layer(L, fused_swiglu=False):
+def check_layer(L, names=()):
+    """names: the plan's launches. The fused decode launches leave some intermediates unwritten
+    (decode_norm_*: the normed rows; decode_matvec_add: the o / down products; decode_*swiglu: gate,
+    up and their SWIGLU); they are then taken from the oracle's chain on the GPU's written tensors."""
     s, N = L.s, L.N
     mm_tol = 1e-3 if N >= 64 else 0
+    norm_fused = "decode_norm_matvec" in names
+    ffn_norm_fused = "decode_norm_swiglu" in names
+    swiglu_fused = ffn_norm_fused or "decode_swiglu" in names
+    add_fused = "decode_matvec_add" in names
     # attention norm (fused): y bit-exact
     _, y = fused_norm_oracle(L.x, L.attn_norm, s.n_embd, N, s.eps)
-    assert np.array_equal(kq.bits(L.get("cur", np.float32)), kq.bits(y)), "attn norm"
+    if not norm_fused:
+        assert np.array_equal(kq.bits(L.get("cur", np.float32)), kq.bits(y)), "attn norm"
     for name, w in (("q", "wq"), ("k", "wk"), ("v", "wv")):
-        check_mm(L, name, w, "cur", mm_tol)
+        check_mm(L, name, w, "cur", mm_tol, xcols=y.reshape(N, s.n_embd) if norm_fused else None)
     # rope of q and k from the GPU's q and k
     for src, dst, nh in (("q", "qr", s.n_head), ("k", "kr", s.n_head_kv)):
         x = L.get(src, np.float32)
@@ -188,22 +197,34 @@ def check_layer(L, fused_swiglu=False):
     O.kco_flash_attn_f16(L.get("qr", np.float32), L.get("k_cache", np.uint16), L.get("v_cache", np.uint16), L.mask,
                          want, C.byref(d), np.float32(1.0 / s.hd ** 0.5))
     assert kq.rel_diff(L.get("attn", np.float32), want) < 2e-6, "attention"
-    check_mm(L, "o", "wo", "attn", mm_tol)
+    attn = L.get("attn", np.float32).reshape(N, s.n_head * s.hd)
+    if add_fused:
+        o = mul_mat_oracle(s.types["wo"], L.blocks["wo"], attn, s.n_embd, s.n_head * s.hd).reshape(-1)
+    else:
+        check_mm(L, "o", "wo", "attn", mm_tol)
+        o = L.get("o", np.float32)
     # residual ADD fused with the FFN norm: x = o + x_in, y = norm(x) * w, both bit-exact
-    x, y = fused_norm_oracle(None, L.ffn_norm, s.n_embd, N, s.eps, a=L.get("o", np.float32), b=L.x)
+    x, y = fused_norm_oracle(None, L.ffn_norm, s.n_embd, N, s.eps, a=o, b=L.x)
     assert np.array_equal(kq.bits(L.get("ffn_inp", np.float32)), kq.bits(x)), "ffn_inp"
-    assert np.array_equal(kq.bits(L.get("cur2", np.float32)), kq.bits(y)), "ffn norm"
-    if fused_swiglu:
-        # gate, up and the GLU's f32 results are not written (one fused launch): the down projection
-        # against the oracle's chain from the GPU's normed input (a value within an ulp of a rounding
-        # tie may quantize one step apart: exp2 ulps of the two silu)
-        cur2 = L.get("cur2", np.float32).reshape(N, s.n_embd)
+    if not ffn_norm_fused:
+        assert np.array_equal(kq.bits(L.get("cur2", np.float32)), kq.bits(y)), "ffn norm"
+    cur2 = y.reshape(N, s.n_embd)
+    if swiglu_fused:
+        # gate, up and the GLU's f32 results are not written: the down projection (or the layer output)
+        # against the oracle's chain (a value within an ulp of a rounding tie may quantize one step
+        # apart: exp2 ulps of the two silu)
         g = mul_mat_oracle(s.types["wg"], L.blocks["wg"], cur2, s.n_ff, s.n_embd)
         u = mul_mat_oracle(s.types["wu"], L.blocks["wu"], cur2, s.n_ff, s.n_embd)
         act = np.zeros(g.size, np.float32)
         O.kco_silu_mul(g.reshape(-1), u.reshape(-1), act, g.size)
-        want = mul_mat_oracle(s.types["wd"], L.blocks["wd"], act.reshape(N, s.n_ff), s.n_embd, s.n_ff)
-        assert kq.rel_diff(L.get("down", np.float32).reshape(N, s.n_embd), want) < 1e-4, "down (fused swiglu)"
+        down = mul_mat_oracle(s.types["wd"], L.blocks["wd"], act.reshape(N, s.n_ff), s.n_embd, s.n_ff).reshape(-1)
+        if not add_fused:
+            assert kq.rel_diff(L.get("down", np.float32), down) < 1e-4, "down (fused swiglu)"
+            down = L.get("down", np.float32)
+        want = down + L.get("ffn_inp", np.float32)
+        assert kq.rel_diff(L.get("out", np.float32), want) < 1e-4, "out"
+        if not add_fused:
+            assert np.array_equal(kq.bits(L.get("out", np.float32)), kq.bits(want)), "out"
     else:
         check_mm(L, "gate", "wg", "cur2", mm_tol)
         check_mm(L, "up", "wu", "cur2", mm_tol)
@@ -212,8 +233,8 @@ def check_layer(L, fused_swiglu=False):
         O.kco_silu_mul(g, u, want, g.size)
         assert np.allclose(L.get("act", np.float32), want, rtol=2e-6, atol=1e-30), "swiglu"
         check_mm(L, "down", "wd", "act", mm_tol)
-    want = L.get("down", np.float32) + L.get("ffn_inp", np.float32)
-    assert np.array_equal(kq.bits(L.get("out", np.float32)), kq.bits(want)), "out"
+        want = L.get("down", np.float32) + L.get("ffn_inp", np.float32)
+        assert np.array_equal(kq.bits(L.get("out", np.float32)), kq.bits(want)), "out"
 
 
 CASES = [
@@ -238,7 +259,7 @@ def test_layer_graph_matches_the_oracle_node_by_node(case, graphs):
     st = be.stats()
     assert st["computes"] == 1 and st["graphs_recorded"] == graphs
     assert st["launches"] == len([n for n in names if n not in "[]"])
-    check_layer(L, fused_swiglu="decode_swiglu" in names)
+    check_layer(L, names)
     be.close()
     L.free()
 
@@ -246,13 +267,15 @@ def test_layer_graph_matches_the_oracle_node_by_node(case, graphs):
 @pytest.mark.parametrize("shape", [gg.LayerShape(), gg.LayerShape(n_embd=1024, neox=True, freq_factors=True)],
                          ids=["llama", "neox-ff"])
 def test_fused_decode_matvecs_equal_one_launch_per_node(shape):
-    """One input column: q / k / v in one decode_matvec, gate / up / SWIGLU in one decode_swiglu --
-    every output the layer keeps (q, k, v, the caches, attention, o, the residuals, down) equals the
-    reference's one launch per node bit for bit."""
+    """One input column: the norms inside the q / k / v and gate / up / SWIGLU launches, the o and
+    down products with their residual ADDs, ROPE with the cache rows, the attention output
+    quantized in its merge -- every output both write (q, k, v, the roped q and k, the caches, the
+    attention, the two residual sums) equals the reference's one launch per node bit for bit."""
     L = Layer(shape, 1, 90, seed=808)
     names, _ = kc.ggml_graph_plan(L.g.nodes)
-    assert "decode_matvec" in names and "decode_swiglu" in names
-    kept = ("q", "k", "v", "qr", "kr", "attn", "o", "ffn_inp", "cur2", "down", "out")
+    assert names == ["decode_norm_matvec", "rope_set_rows", "flash_decode_q8", "decode_matvec_add",
+                     "decode_norm_swiglu", "decode_matvec_add"]
+    kept = ("q", "k", "v", "qr", "kr", "attn", "ffn_inp", "out")  # what both write
     got = {}
     for opt in (1, 0):
         kc.set_option("ggml_extra_fusions", opt)
