@@ -469,6 +469,16 @@ def _node_array(nodes):
     return arr
 
 
+class GgmlNodes:
+    """A node list converted once to the array kcGgmlGraphCompute reads (a caller that computes the
+    same graph every step passes this instead of rebuilding the array each time, as ggml's own
+    cgraph node array is passed)."""
+
+    def __init__(self, nodes):
+        self.n = len(nodes)
+        self.arr = _node_array(nodes)
+
+
 def ggml_supports_op(t, **cfg):
     """kcGgmlSupportsOp: whether the backend claims t (host logic only)."""
     return bool(lib().kcGgmlSupportsOp(C.byref(ggml_config(**cfg)), C.byref(t)))
@@ -499,7 +509,10 @@ class GgmlBackend:
         self.h = h
 
     def compute(self, nodes):
-        call("kcGgmlGraphCompute", self.h, _node_array(nodes), len(nodes))
+        if isinstance(nodes, GgmlNodes):
+            call("kcGgmlGraphCompute", self.h, nodes.arr, nodes.n)
+        else:
+            call("kcGgmlGraphCompute", self.h, _node_array(nodes), len(nodes))
 
     def stats(self):
         s = GgmlStats()

@@ -300,9 +300,10 @@ def test_kept_graph_is_launched_again_for_new_inputs():
     note(f"ggml graph reuse: N={N}, p0={p0}")
     L = Layer(shape, N, p0, seed=500)
     graph_be, eager_be = kc.GgmlBackend(graphs=1), kc.GgmlBackend(graphs=0)
+    nodes = kc.GgmlNodes(L.g.nodes)  # the node array built once
     for trial in range(3):
         L.set_x(600 + trial)  # new values at the same addresses
-        graph_be.compute(L.g.nodes)
+        graph_be.compute(nodes)
         got = L.get("out", np.float32)
         kc.synchronize()
         eager_be.compute(L.g.nodes)
