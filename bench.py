@@ -295,6 +295,62 @@ def ggml_backend_decode_run(cfg, n_ctx, n_decode, seed, reps, modes=(1, 0)):
     return out
 
 
+def ggml_backend_prefill_run(cfg, n_prompt, seed, reps):
+    """The drop-in path for a prompt: one n_prompt-token step of cfg (positions 0 .., the causal
+    mask, the KV view of n_prompt rows rounded up to 256) through kcGgmlGraphCompute on the graph
+    llama.cpp builds (the last layer keeps only the last row after its attention; the head gives
+    that row's logits), with the backend claiming attention over the whole prompt (attn_tokens =
+    n_prompt: one flash_attn_f16 kernel). The same step is computed reps times (the kept graph after
+    the first); weights as the decode leg's."""
+    from kernelcore_amd import ggml_graph as gg
+
+    n_kv = (n_prompt + 255) // 256 * 256
+    s = gg.LayerShape.of_model(cfg, n_kv)
+    bufs, seeds = [], iter(range(seed, seed + 10000))
+
+    def alloc(nbytes, type_, ne):
+        if type_ in ("q4k", "q6k"):
+            b = synth.quantized_stream(type_, ne[1], ne[0], next(seeds))
+        else:
+            b = kc.Buffer(nbytes)
+            if type_ == "f32" and ne[1] == 1 and ne[0] in (s.n_embd, s.hd):  # norm weights
+                kc.launch("fill_normal_f32", kc.FillNormalArgs(b.ptr, ne[0], next(seeds), 1.0, 0.05))
+            else:
+                kc.call("kcMemset", b.ptr, 0, nbytes)
+        bufs.append(b)
+        return b.ptr
+
+    g = gg.Graph(alloc)
+    io, _, _, logits = gg.decoder(g, s, cfg["n_layer"], n_prompt, n_kv)
+    x = np.random.default_rng(seed).standard_normal(n_prompt * s.n_embd).astype(np.float32)
+    pos = np.arange(n_prompt, dtype=np.int32)
+    mrow = io["mask"].ne[0]
+    mask = np.where(np.arange(mrow)[None, :] <= pos[:, None], 0.0, -np.inf).astype(np.float16)
+    for name, a in (("x", x), ("pos", pos), ("kv_idx", pos.astype(np.int64)), ("mask", mask)):
+        kc.call("kcMemcpy", io[name].data, a.ctypes.data, a.nbytes, kc.HOST_TO_DEVICE)
+    kc.synchronize()
+    nodes = kc.GgmlNodes(g.nodes)
+    be = kc.GgmlBackend(graphs=1, attn_tokens=n_prompt)
+    be.compute(nodes)  # records the kept graph
+    times = []
+    for _ in range(reps):
+        w0 = time.perf_counter()
+        be.compute(nodes)
+        times.append(time.perf_counter() - w0)
+    st = be.stats()
+    be.close()
+    lg = np.empty(s.n_vocab, np.float32)
+    kc.call("kcMemcpy", lg.ctypes.data, logits.data, lg.nbytes, kc.DEVICE_TO_HOST)
+    for b in bufs:
+        b.free()
+    ms = med(times) * 1e3
+    return {"workload": f"{cfg['n_layer']}-layer {n_prompt}-token prompt through kcGgmlGraphCompute on llama.cpp's "
+                        f"graph ({len(g.nodes)} nodes, KV view of {n_kv} rows)",
+            "prefill_tok_s": round(n_prompt / ms * 1e3, 1), "prefill_ms": round(ms, 3),
+            "launches": round(st["launches"] / st["computes"], 1), "reps": reps,
+            "finite": bool(np.all(np.isfinite(lg)))}
+
+
 def model_run(cfg, n_prompt, n_decode, seed, reps, eager=False, name=CFG4_NAME):
     """A random n_prompt-token prompt (one batched forward), then n_decode greedy decode steps
     (graph-replayed, argmax on the device). A warm-up prompt + 4 steps first (builds the decode
@@ -527,10 +583,11 @@ def main():
     kc.init()
     props = kc.device_properties()
     note(f"# device: {props.name.decode()} ({props.worker_count} CUs)")
-    mm = mdl = mdl5 = ggml_leg = None
+    mm = mdl = mdl5 = ggml_leg = ggml_pre = None
     if args.only_ggml:
         print(json.dumps({"ggml_backend_decode_cfg4": ggml_backend_decode_run(
-            LLAMA32_3B, 512, args.decode_steps, seed=9700, reps=reps, modes=(0,) if args.no_graph else (1, 0))}),
+            LLAMA32_3B, 512, args.decode_steps, seed=9700, reps=reps, modes=(0,) if args.no_graph else (1, 0)),
+            "ggml_backend_prefill_cfg4": ggml_backend_prefill_run(LLAMA32_3B, 512, seed=9800, reps=reps)}),
             flush=True)
         return
     if args.only_cfg3:
@@ -558,10 +615,13 @@ def main():
         if not args.skip_ggml:
             ggml_leg = ggml_backend_decode_run(LLAMA32_3B, 512, args.decode_steps, seed=9700, reps=reps)
             note(f"# ggml backend decode done: {ggml_leg['kept_graph']['tok_s']} tok/s (kept graph)")
+            ggml_pre = ggml_backend_prefill_run(LLAMA32_3B, 512, seed=9800, reps=reps)
+            note(f"# ggml backend prefill done: {ggml_pre['prefill_tok_s']} tok/s")
     if args.only_model:
         res = {"prefill_matmul_cfg3": mm, "model_cfg4": mdl}
         if ggml_leg:
             res["ggml_backend_decode_cfg4"] = ggml_leg
+            res["ggml_backend_prefill_cfg4"] = ggml_pre
         if mdl5:
             res["model_cfg5"] = mdl5
         print(json.dumps(res), flush=True)
@@ -629,6 +689,7 @@ def main():
         out["model_cfg5"] = mdl5
     if ggml_leg:
         out["ggml_backend_decode_cfg4"] = ggml_leg
+        out["ggml_backend_prefill_cfg4"] = ggml_pre
     if cal:
         out["calibration"] = cal
     if cpu:

@@ -32,6 +32,7 @@
 #include "kernelcore/ggml_backend.h"
 #include "kernelcore/llm_kernels.h"
 #include "launch.hpp"
+#include "model_kernels.hpp"
 #include "mul_mat_internal.hpp"
 
 using T = kcGgmlTensor;
@@ -601,6 +602,16 @@ E flashAttn(Pass& p, const T* dst) {
         }
         return launch(p, "flash_decode_f16", &a);
     }
+    // a batch with a mask, in the layout of the decoder's caches (heads D / 2 words apart in K and V
+    // rows of one stride, q and out [N][H][D]): on the matrix cores, masked key blocks skipped
+    const kcamd::AttnShape as{d.N, d.H, d.H_kv, d.D, d.q_tok, d.k_row, d.T, 0, scale};
+    if (md && kcamd::attnMaskedSupports(as) && d.q_head == d.D && d.q_tok == d.H * d.D && d.k_head == d.D / 2 &&
+        d.v_head == d.D / 2 && d.v_row == d.k_row && d.m_row > 0) {
+        const auto* mh = static_cast<const unsigned short*>(mask->data);
+        return direct(p, "attn_masked", [&](hipStream_t s) {
+            return kcamd::launchAttnMasked(f32(q), kd, vd, mh, 2 * d.m_row, d.T, f32w(dst), as, s);
+        });
+    }
     if (d.T <= 16384) {
         const kcFlashAttnArgs a{f32(q), kd, vd, md, f32w(dst), nullptr, d, scale};
         return launch(p, "flash_attn_f16", &a);
@@ -765,6 +776,7 @@ struct Plan {
     std::vector<const char*> trace;
     std::vector<int> ones;
     size_t scratch = 0;
+    size_t staging = 0;  // the largest per-stream fp16 staging of a by-name MFMA matmul
     long long launches = 0;
 };
 
@@ -779,6 +791,12 @@ E plan(const kcGgmlConfig& c, const T* const* nodes, int n, Plan& out) {
     out.scratch = dry.peak;
     for (const char* t : out.trace)
         if (t[0] != '[' && t[0] != ']') ++out.launches;
+    for (int i = 0; i < n; ++i) {  // the MFMA matmuls' staging (a graph records the buffer it finds)
+        const T* t = nodes[i];
+        if (t->op == KC_GGML_OP_MUL_MAT && computed(t) && kquant(t->src[0]))
+            out.staging = std::max(out.staging, kcamd::matmulStagingBytes(int(t->src[0]->ne[1]), int(t->src[0]->ne[0]),
+                                                                          int(nrows(t->src[1]))));
+    }
     return ok;
 }
 
@@ -871,6 +889,12 @@ E compute(kcGgmlBackend_st& be, const T* const* nodes, int n) {
         if (s != ok) return s;
     } else {
         dropGraph(be);
+        if (pl.staging) {  // grown now: inside the capture it could not grow, and the MFMA matmuls would
+                           // take their unstaged kernels
+            void* hs = nullptr;
+            if (E e = kcStreamGetNative(be.stream, &hs); e != ok) return e;
+            if (!kcamd::streamScratch(hs, pl.staging)) return kc::Error::OutOfMemory;
+        }
         if (E e = kcStreamBeginCapture(be.stream); e != ok) return e;
         const E e = walk(p, nodes, n);
         kcGraph_t g = nullptr;

@@ -1235,6 +1235,14 @@ int launchMatmulMfma(bool q6k, const kcMatmulKQ8Args& a, hipStream_t s) {
     return q6k ? runMfma8<true, 1>(a, s) : runMfma8<false, 1>(a, s);
 }
 
+size_t matmulStagingBytes(int rows, int k, int ncols) {
+    const int path = option("matmul_path");
+    if (!(path == 0 && ncols >= 64) && !(path >= 2 && path != 3 && path != 4 && path != 5)) return 0;
+    if ((size_t)ncols * k * 2 >= (1ull << 32)) return 0;
+    const kcMatmulKQ8Args a{nullptr, nullptr, nullptr, nullptr, rows, k, ncols, 8};
+    return stagedBytes(a, stagedKs(a));
+}
+
 int launchMatmulGroup(const MmPart* parts, int nparts, const int* xq, int k, int ncols, int ks, int* used_ks,
                       hipStream_t s, const ActF16* pre) {
     *used_ks = 1;

@@ -41,6 +41,9 @@ int launchMatvecKq(bool q6k, const kcMatvecQ4Q8Args& a, hipStream_t s);
 int launchMatmulCols(bool q6k, bool per256, const kcMatmulKQ8Args& a, hipStream_t s);
 // kmatmul_mfma.hip: K-quant x per-256 activations on MFMA (large batches).
 int launchMatmulMfma(bool q6k, const kcMatmulKQ8Args& a, hipStream_t s);
+// The per-stream scratch a by-name per-256 matmul of these sizes stages its fp16 activations (and
+// K-split partial sums) in; 0 when it takes a path without it.
+size_t matmulStagingBytes(int rows, int k, int ncols);
 // The matmul names: column tiles for small batches and per-32 slots, MFMA for large per-256 batches.
 int launchMatmulKq(bool q6k, bool per256, const kcMatmulKQ8Args& a, hipStream_t s);
 // The same kernels with the MFMA activations staged in the fixed device array (kcLaunchMatmulNoAlloc):

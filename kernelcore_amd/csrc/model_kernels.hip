@@ -231,10 +231,16 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // V[keys kappa(k)][d], from there. Query tiles are dispatched longest first.
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 
-template <int D, int W>
+// MASKED: FLASH_ATTN_EXT's form for the ggml backend -- the N queries attend over T = t_host keys
+// with ggml's f16 mask (row i of m_row2 halves: dot * scale + mask[i][key], the oracle's order)
+// instead of the causal positions; a key block whose mask is -inf for every query of the tile is
+// skipped (it would add nothing).
+template <int D, int W, bool MASKED = false>
 __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(const float* __restrict__ q, const int* __restrict__ kc,
                                                                const int* __restrict__ vc, float* __restrict__ out,
-                                                               const int* __restrict__ n_ctx, AttnShape a) {
+                                                               const int* __restrict__ n_ctx, AttnShape a,
+                                                               const unsigned short* __restrict__ mask = nullptr,
+                                                               int m_row2 = 0, int t_host = 0) {
     constexpr int KS = D / 16, DB = D / 32;
     constexpr int VR = D + 8;        // halves per V row in LDS
     constexpr int CPR = D / 8;       // 16-byte chunks per V row
@@ -244,7 +250,7 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(const float* __res
     constexpr int kLdsHalves = W * 32 * VR > (W - 1) * 32 * D * 2 ? W * 32 * VR : (W - 1) * 32 * D * 2;
     __shared__ __attribute__((aligned(16))) _Float16 vsall[kLdsHalves];
     __shared__ __attribute__((aligned(16))) float qx[W][4][32];
-    const int T = *n_ctx, N = a.N, p0 = T - N;
+    const int T = MASKED ? t_host : *n_ctx, N = a.N, p0 = T - N;
     const int tiles = (N + 31) / 32;
     const int i0 = (tiles - 1 - (int)blockIdx.x) * 32;
     const int head = blockIdx.y, kvh = head / (a.H / a.H_kv);
@@ -272,7 +278,20 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(const float* __res
         }
     }
     const int qpos = p0 + i0 + j;
-    const int nkb = min(p0 + i0 + 31, T - 1) / 32 + 1;
+    const int nkb = MASKED ? (T + 31) / 32 : min(p0 + i0 + 31, T - 1) / 32 + 1;
+    // MASKED: this lane's 16 mask values of a key block (keys 32 kb + 8 g + 4 h + 0..3) as 8 words,
+    // read inside the query's row (keys past it are dropped by key < T)
+    const unsigned short* mrow = MASKED ? mask + (size_t)min(i0 + j, N - 1) * m_row2 : nullptr;
+    uint32_t mk[8], mkn[8];
+    auto loadM = [&](int kb, uint32_t* dst) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int w2 = 0; w2 < 2; ++w2) {
+                const int key = min(kb * 32 + 8 * g + 4 * h + 2 * w2, m_row2 - 2);
+                dst[2 * g + w2] = *reinterpret_cast<const uint32_t*>(mrow + key);
+            }
+    };
     f32x16 zero;
 #pragma unroll
     for (int v = 0; v < 16; ++v) zero[v] = 0.0f;
@@ -299,6 +318,7 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(const float* __res
     if (wave < nkb) {
         loadK(wave, ka);
         loadV(wave);
+        if constexpr (MASKED) loadM(wave, mk);
     }
     f32x16 o[DB];
 #pragma unroll
@@ -312,6 +332,27 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(const float* __res
         if (kb + W < nkb) {
             loadK(kb + W, kn);
             loadV(kb + W);
+            if constexpr (MASKED) loadM(kb + W, mkn);
+        }
+        float mval[16];
+        if constexpr (MASKED) {
+            bool any = false;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const uint32_t w2 = mk[v >> 1];
+                mval[v] = (float)__builtin_bit_cast(_Float16, (unsigned short)((v & 1) ? (w2 >> 16) : (w2 & 0xFFFFu)));
+                const int key_abs = kb * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                any |= key_abs < T && mval[v] != -INFINITY;
+            }
+            if (__ballot(any) == 0) {  // every score of the block masked: nothing to add
+                if (kb + W < nkb) {
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks) ka[ks] = kn[ks];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) mk[e] = mkn[e];
+                }
+                continue;
+            }
         }
         f32x16 sh = zero, sl = zero;  // two independent chains (q hi, q lo)
 #pragma unroll
@@ -324,7 +365,10 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(const float* __res
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
             const int key_abs = kb * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-            sacc[v] = key_abs <= qpos && key_abs < T ? a.scale * (sh[v] + sl[v]) : -INFINITY;
+            if constexpr (MASKED)
+                sacc[v] = key_abs < T ? a.scale * (sh[v] + sl[v]) + mval[v] : -INFINITY;
+            else
+                sacc[v] = key_abs <= qpos && key_abs < T ? a.scale * (sh[v] + sl[v]) : -INFINITY;
             bm = fmaxf(bm, sacc[v]);
         }
         bm = fmaxf(bm, __shfl_xor(bm, 32));
@@ -369,9 +413,13 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(const float* __res
                 o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[mm], vbv, o[db], 0, 0, 0);
                 o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pl[mm], vbv, o[db], 0, 0, 0);
             }
-        if (kb + W < nkb)
+        if (kb + W < nkb) {
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) ka[ks] = kn[ks];
+            if constexpr (MASKED)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) mk[e] = mkn[e];
+        }
     }
     // ---- merge: wavefronts 1.. hand (m, l, o) to wavefront 0 through LDS
     l += __shfl_xor(l, 32);
@@ -445,6 +493,22 @@ static int runPrefill(const float* q, const int* k, const int* v, float* out, co
     else
         hipLaunchKernelGGL((attn_prefill_kernel<D, 4>), grid, dim3(256), 0, s, q, k, v, out, n_ctx, a);
     return fromHip(hipGetLastError(), "attn (prefill)");
+}
+
+bool attnMaskedSupports(const AttnShape& a) { return a.D == 64 || a.D == 128; }
+
+int launchAttnMasked(const float* q, const int* k, const int* v, const unsigned short* mask, int m_row2, int T,
+                     float* out, const AttnShape& a, hipStream_t s) {
+    if (!attnMaskedSupports(a) || m_row2 < 2 || m_row2 % 2 || T <= 0 || a.N <= 0)
+        return fromHip(hipErrorInvalidValue, "attn (masked): shape");
+    const dim3 grid((a.N + 31) / 32, a.H);
+    if (a.D == 128)
+        hipLaunchKernelGGL((attn_prefill_kernel<128, 2, true>), grid, dim3(128), 0, s, q, k, v, out, nullptr, a, mask,
+                           m_row2, T);
+    else
+        hipLaunchKernelGGL((attn_prefill_kernel<64, 4, true>), grid, dim3(256), 0, s, q, k, v, out, nullptr, a, mask,
+                           m_row2, T);
+    return fromHip(hipGetLastError(), "attn (masked)");
 }
 
 int launchAttn(const float* q, const int* k, const int* v, float* out, const int* n_ctx, const AttnShape& a,

@@ -15,6 +15,12 @@ struct AttnShape {
 int launchGetRows(bool q6k, const void* qw, const int* tok, float* y, int n, int k, int rows, hipStream_t s);
 int launchAttn(const float* q, const int* k, const int* v, float* out, const int* n_ctx, const AttnShape& a,
                hipStream_t s);
+// FLASH_ATTN_EXT on the matrix cores with ggml's f16 mask (rows of m_row2 halves) over T keys: q
+// rows a.q_tok floats apart (heads D apart), K / V rows a.kv_row words apart (heads D / 2 words
+// apart), out[N][H][D] rows a.q_tok apart; D 64 or 128.
+bool attnMaskedSupports(const AttnShape& a);
+int launchAttnMasked(const float* q, const int* k, const int* v, const unsigned short* mask, int m_row2, int T,
+                     float* out, const AttnShape& a, hipStream_t s);
 int launchArgmaxStep(const float* logits, int n, int* tokens, int* gen, int* step, int* n_past, int max_gen,
                      hipStream_t s);
 int launchPositions(const int* n_past, int n, int* pos, long long* idx, int* n_ctx, hipStream_t s);

@@ -129,7 +129,7 @@ def test_batch_layer_plans(N, cfg, mm, quant):
     norm0 = ["sumsq_part", "norm_mul_q8k_f"] if k == "q8k" else ["add_norm_q8_f"]
     norm1 = ["add_sumsq_f", "norm_mul_q8k_f"] if k == "q8k" else ["add_norm_q8_f"]
     silu = "silu_mul_q8kf" if k == "q8k" else "silu_mul_q8x4f"
-    attn = ["rope_set_rows", "flash_decode_f16" if N <= 8 else "flash_attn_f16"]  # past 8 tokens: one kernel
+    attn = ["rope_set_rows", "flash_decode_f16" if N <= 8 else "attn_masked"]  # past 8 tokens: the matrix cores
     want = (norm0 + ["[", mm.format("q4k"), mm.format("q4k"), mm.format("q6k"), "]"] + attn +
             [quant, mm.format("q4k")] + norm1 + ["[", mm.format("q4k"), mm.format("q4k"), "]", silu,
              mm.format("q6k"), "vector_add"])
@@ -249,8 +249,17 @@ def test_decode_attention_is_split_over_the_context():
     assert ints >= 8 * 313 * 66  # the partials of 8 heads x 313 chunks x (64 values + max + sum)
 
 
-def test_long_context_batch_attention_takes_the_four_kernels():
+def test_batch_attention_runs_masked_on_the_matrix_cores():
     g, _ = layer(N=12, n_kv=20000, kv_size=20480)
+    names, ints = kc.ggml_graph_plan(g.nodes, attn_tokens=16)
+    i = names.index("rope_set_rows")
+    assert names[i + 1] == "attn_masked" and "fa_scores" not in names
+    assert ints < 8 * 12 * 20000  # no score matrix in the scratch
+
+
+def test_long_context_batch_attention_takes_the_four_kernels():
+    # head_dim 96: not one the masked matrix-core kernel takes; past 16384 keys: the reference's four
+    g, _ = layer(N=12, n_kv=20000, kv_size=20480, n_embd=768, head_dim=96)
     names, ints = kc.ggml_graph_plan(g.nodes, attn_tokens=16)
     i = names.index("rope_set_rows")
     assert names[i:i + 5] == ["rope_set_rows", "fa_scores", "fa_max", "fa_exp", "fa_values"]

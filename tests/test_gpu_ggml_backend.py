@@ -295,6 +295,41 @@ def test_fused_decode_matvecs_equal_one_launch_per_node(shape):
     L.free()
 
 
+@pytest.mark.parametrize("shape", [gg.LayerShape(), gg.LayerShape(n_embd=1024, neox=True)], ids=["D64", "D128"])
+def test_batch_attention_with_an_irregular_mask(shape):
+    """The matrix-core FLASH_ATTN_EXT of a batch with ggml's mask as given, not causal: random holes,
+    keys 64-127 masked for every query (two whole key blocks skipped), a query with a single key,
+    keys past the prompt open to the first queries; against the oracle on the GPU's own inputs."""
+    N, p0 = 40, 150
+    L = Layer(shape, N, p0, seed=919)
+    names, _ = kc.ggml_graph_plan(L.g.nodes, attn_tokens=N)
+    assert "attn_masked" in names
+    rng = np.random.default_rng(5)
+    n_pad = L.t["mask"].ne[0]
+    m = np.where(rng.random((N, n_pad)) < 0.3, -np.inf, 0.0).astype(np.float16)
+    m[:, L.n_kv:] = -np.inf
+    m[:, 64:128] = -np.inf
+    m[3, :] = -np.inf
+    m[3, 5] = 0.0
+    m[:4, p0 + N - 1] = 0.0  # the last key, ahead of these queries' positions
+    m[7, 130:140] = np.float16(-2.5)  # finite penalties, not only 0 / -inf
+    L.mask = m.reshape(-1).view(np.uint16)
+    L.put("mask", L.mask)
+    be = kc.GgmlBackend(graphs=1, attn_tokens=N)
+    be.compute(L.g.nodes)
+    kc.synchronize()
+    s = L.s
+    d = oracle.FaDims(H=s.n_head, T=L.n_kv, D=s.hd, group=s.n_head // s.n_head_kv, tp=(L.n_kv + 7) // 8 * 8,
+                      k_row=s.kv_dim // 2, k_head=s.hd // 2, v_row=s.kv_dim // 2, v_head=s.hd // 2, N=N,
+                      q_tok=s.hd * s.n_head, q_head=s.hd, m_row=n_pad // 2, has_mask=1, H_kv=s.n_head_kv)
+    want = np.zeros(N * s.n_head * s.hd, np.float32)
+    O.kco_flash_attn_f16(L.get("qr", np.float32), L.get("k_cache", np.uint16), L.get("v_cache", np.uint16), L.mask,
+                         want, C.byref(d), np.float32(1.0 / s.hd ** 0.5))
+    assert kq.rel_diff(L.get("attn", np.float32), want) < 2e-6
+    be.close()
+    L.free()
+
+
 def test_kept_graph_is_launched_again_for_new_inputs():
     shape, N, p0 = gg.LayerShape(), 8, 100
     note(f"ggml graph reuse: N={N}, p0={p0}")
