@@ -555,6 +555,79 @@ E ropeKv(Pass& p, const T* rq, const T* rk, const T* sk, const T* sv) {
     return direct(p, "rope_set_rows", [&](hipStream_t s) { return kcamd::launchRopeKvRows(r, s); });
 }
 
+// (No reference counterpart.) After ropeKvOk's four nodes, the next node with work: the
+// FLASH_ATTN_EXT of one token on the roped q, whose K and V are views of the two caches the
+// SET_ROWS write (rows as the caches' rows from one common row, heads D halves apart), taken by the
+// split-context kernel with its per-32 slot: then the four nodes run as that kernel's prologue.
+// fa: the attention node's index.
+bool ropeFaOk(const T* const* nodes, int n, int i, const int (&at)[3], int* fa) {
+    const T *rq = nodes[i], *rk = nodes[at[0]], *sk = nodes[at[1]], *sv = nodes[at[2]];
+    const int f = nextWork(nodes, n, at[2] + 1);
+    if (f >= n) return false;
+    const T* node = nodes[f];
+    if (node->op != KC_GGML_OP_FLASH_ATTN_EXT || !computed(node)) return false;
+    const T *q = node->src[0], *k = node->src[1], *v = node->src[2];
+    const int64_t hd = rq->ne[0], nh = rq->ne[1], nkv = rk->ne[1];
+    if (!q || !k || !v || q->data != rq->data || rq->ne[2] != 1 || q->ne[1] != 1 || q->ne[2] != nh) return false;
+    if (k->ne[0] != hd || k->ne[2] != nkv || v->ne[0] != hd || v->ne[2] != nkv || nh % nkv) return false;
+    if (q->nb[2] != size_t(hd) * 4 || k->nb[2] != size_t(hd) * 2 || v->nb[2] != size_t(hd) * 2) return false;
+    // the raw sources: contiguous heads
+    const T *q0 = rq->src[0], *k0 = rk->src[0], *v0 = sv->src[0];
+    if (q0->nb[0] != 4 || q0->nb[1] != size_t(hd) * 4 || k0->nb[0] != 4 || k0->nb[1] != size_t(hd) * 4 ||
+        v0->nb[0] != 4)
+        return false;
+    // K and V: views of the caches from the same row, with the caches' row strides
+    if (k->nb[1] != sk->nb[1] || v->nb[1] != sv->nb[1] || sk->nb[1] % 4 || sv->nb[1] % 4) return false;
+    const auto off = [](const T* view, const T* base) {
+        return static_cast<const char*>(view->data) - static_cast<const char*>(base->data);
+    };
+    const ptrdiff_t ok_ = off(k, sk), ov = off(v, sv);
+    if (ok_ < 0 || ov < 0 || ok_ % ptrdiff_t(sk->nb[1]) || ov % ptrdiff_t(sv->nb[1])) return false;
+    if (ok_ / ptrdiff_t(sk->nb[1]) != ov / ptrdiff_t(sv->nb[1]) || ok_ / ptrdiff_t(sk->nb[1]) > INT32_MAX) return false;
+    // what flashAttn takes for one token with its slot
+    const int D = int(hd), G = int(nh / nkv);
+    if (!kcamd::flashDecodeSupports(D, G) || (nh * hd) % 256 || q->nb[1] % 16) return false;
+    *fa = f;
+    return true;
+}
+
+E ropeFlashAttn(Pass& p, const T* rq, const T* rk, const T* sk, const T* sv, const T* dst) {
+    const T* q = dst->src[0];
+    const T* k = dst->src[1];
+    const T* v = dst->src[2];
+    const T* mask = dst->src[3];
+    kcFaDims d{};
+    d.D = int(k->ne[0]);
+    d.T = int(k->ne[1]);
+    d.H_kv = int(k->ne[2]);
+    d.H = int(q->ne[2]);
+    d.N = 1;
+    d.group = d.H / d.H_kv;
+    d.tp = (d.T + 7) / 8 * 8;
+    d.k_row = int(k->nb[1] / 4), d.k_head = int(k->nb[2] / 4);
+    d.v_row = int(v->nb[1] / 4), d.v_head = int(v->nb[2] / 4);
+    d.q_tok = int(q->nb[1] / 4), d.q_head = int(q->nb[2] / 4);
+    d.m_row = mask ? int(mask->nb[1] / 4) : 0;
+    d.has_mask = mask ? 1 : 0;
+    const int hd = int(rq->ne[0]);
+    const float* ff = rq->src[2] ? f32(rq->src[2]) : onesOf(p, hd / 2);
+    if (!ff) return kc::Error::InternalError;
+    int* part = nullptr;
+    if (E e = kcamd::mulmat::take(p.rec, kcamd::flashDecodePartFloats(d), &part); e != ok) return e;
+    int* slot = nullptr;
+    if (E e = kcamd::mulmat::outputSlot(p.rec, f32(dst), d.H * d.D, 1, false, &slot); e != ok) return e;
+    const kcFlashDecodeArgs a{f32(q), static_cast<const int*>(k->data), static_cast<const int*>(v->data),
+                              mask ? static_cast<const int*>(mask->data) : nullptr, f32w(dst),
+                              reinterpret_cast<float*>(part), nullptr, d, paramF32(dst, 0)};
+    const ptrdiff_t row0 = (static_cast<const char*>(k->data) - static_cast<const char*>(sk->data)) / ptrdiff_t(sk->nb[1]);
+    const kcamd::FdRope r{f32(rq->src[0]), f32(rk->src[0]), f32(sv->src[0]), f32w(rq), f32w(rk),
+                          static_cast<int*>(sk->data), static_cast<int*>(sv->data),
+                          static_cast<const int*>(rq->src[1]->data), static_cast<const int*>(sk->src[1]->data), ff,
+                          std::log2(paramF32(rq, 5)), (rq->op_params[2] & KC_GGML_ROPE_TYPE_NEOX) != 0,
+                          int(sk->nb[1] / 4), int(sv->nb[1] / 4), int(sk->ne[1]), int(row0)};
+    return direct(p, "rope_flash_decode_q8", [&](hipStream_t s) { return kcamd::launchFlashDecode(a, s, slot, &r); });
+}
+
 E setRows(Pass& p, const T* dst) {  // dst rows src1[r] (int64) = fp16(src0 row r) (:650-661)
     const T* src = dst->src[0];
     const T* idx = dst->src[1];
@@ -727,9 +800,15 @@ E walk(Pass& p, const T* const* nodes, int n) {
             case KC_GGML_OP_MUL: e = mul(p, node); break;
             case KC_GGML_OP_ROPE: {
                 int at[3];
+                int fa = 0;
                 if (kcamd::option("ggml_extra_fusions") != 1 && ropeKvOk(nodes, n, i, at)) {
-                    e = ropeKv(p, node, nodes[at[0]], nodes[at[1]], nodes[at[2]]);
-                    i = at[2];
+                    if (ropeFaOk(nodes, n, i, at, &fa)) {  // and the attention they feed: one launch
+                        e = ropeFlashAttn(p, node, nodes[at[0]], nodes[at[1]], nodes[at[2]], nodes[fa]);
+                        i = fa;
+                    } else {
+                        e = ropeKv(p, node, nodes[at[0]], nodes[at[1]], nodes[at[2]]);
+                        i = at[2];
+                    }
                 } else {
                     e = rope(p, node);
                 }

@@ -1001,13 +1001,21 @@ __global__ __launch_bounds__(64) void attn_merge_wave_kernel(AttnDecodeArgs a) {
 // lanes per position, 8 values each); it writes the chunk's maximum, sum of exponentials and
 // unnormalized output to part; flash_merge_kernel combines the chunks in order with a running
 // maximum. A chunk whose positions are all masked contributes nothing.
-template <int D, int G>
+// RP: the ROPE / SET_ROWS prologue (FdRope; one query token): the raw q of the G heads and k, v of
+// KV head g into LDS, RoPE as rope_kv_rows_kernel computes it (the same expressions, so the same
+// bits), the roped q and k written by the workgroups of chunk 0, the fp16 cache row of head g
+// stored by the workgroup whose chunk holds it (chunk 0's when the view does not hold it), and
+// that row read from registers by the workgroup that holds it: no workgroup reads a row another
+// one writes.
+template <int D, int G, bool RP>
 __global__ __launch_bounds__(256) void flash_decode_kernel(const float* __restrict__ q, const int* __restrict__ k,
                                                            const int* __restrict__ v, const int* __restrict__ mask,
-                                                           float* __restrict__ part, kcFaDims d, float scale, int nch) {
+                                                           float* __restrict__ part, kcFaDims d, float scale, int nch,
+                                                           FdRope rp) {
     constexpr int LP = D / 8;      // lanes per position
     constexpr int PPI = 64 / LP;   // positions per wave instruction
     constexpr int NI = 16 / PPI;   // instructions per wave (16 positions per wave)
+    constexpr int pairs = D / 2;
     __shared__ float sc[G][kChunk];
     __shared__ float red[16][G * D];
     __shared__ float mg[G], lg[G];
@@ -1027,21 +1035,96 @@ __global__ __launch_bounds__(256) void flash_decode_kernel(const float* __restri
         mk[n] = h2f((w >> ((t & 1) * 16)) & 0xFFFFu);
     }
     float qv[G][8];
+    int tnew = -1;     // RP: the view row of the new cache row (-1: none)
+    u32x4 knw, vnw;    // RP: this lane's 8 values of that row, as the fp16 words the cache holds
+    if constexpr (RP) {
+        __shared__ float raw[(G + 2) * D];
+        __shared__ float qs[G * D];
+        __shared__ float kn[D];
+        __shared__ float ffl[pairs];
+        constexpr int NR = ((G + 2) * D + 255) / 256;
+        float rv[NR];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const float4* qh = reinterpret_cast<const float4*>(q + (size_t)i * d.q_tok + (size_t)(kvh * G + g) * d.q_head + l * 8);
-        const float4 a = qh[0], b = qh[1];
-        qv[g][0] = a.x, qv[g][1] = a.y, qv[g][2] = a.z, qv[g][3] = a.w;
-        qv[g][4] = b.x, qv[g][5] = b.y, qv[g][6] = b.z, qv[g][7] = b.w;
+        for (int r = 0; r < NR; ++r) {
+            const int x = min(tid + r * 256, (G + 2) * D - 1);
+            rv[r] = x < G * D ? rp.q[(size_t)kvh * G * D + x]
+                              : (x < (G + 1) * D ? rp.k[(size_t)kvh * D + (x - G * D)]
+                                                 : rp.v[(size_t)kvh * D + (x - (G + 1) * D)]);
+        }
+        const float ffv = rp.ff[tid % pairs];
+        const int p = rp.pos[0], row = rp.idx[0];
+        const bool stored = row >= 0 && row < rp.dst_rows;
+        const int tv = row - rp.row0;
+        tnew = stored && tv >= 0 && tv < d.T ? tv : -1;
+        const int cstore = tnew >= 0 ? tnew / kChunk : 0;
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+            if (tid + r * 256 < (G + 2) * D) raw[tid + r * 256] = rv[r];
+        if (tid < pairs) ffl[tid] = ffv;
+        __syncthreads();
+        const int m1 = rp.neox ? 1 : 2, m2 = rp.neox ? pairs : 1;
+        for (int x = tid; x < (G + 1) * pairs; x += 256) {
+            const int h = x / pairs, j = x % pairs;
+            const float theta = (float)p * exp2f(-(float)j / (float)pairs * rp.log2_base) / ffl[j];
+            const float cs = cosf(theta), sn = sinf(theta);
+            const int o = j * m1;
+            const float x0 = raw[h * D + o], x1 = raw[h * D + o + m2];
+            const float y0 = x0 * cs - x1 * sn, y1 = x0 * sn + x1 * cs;
+            if (h < G) {
+                qs[h * D + o] = y0;
+                qs[h * D + o + m2] = y1;
+                if (c == 0) {
+                    rp.qr[(size_t)(kvh * G + h) * D + o] = y0;
+                    rp.qr[(size_t)(kvh * G + h) * D + o + m2] = y1;
+                }
+            } else {
+                kn[o] = y0;
+                kn[o + m2] = y1;
+                if (c == 0) {
+                    rp.kr[(size_t)kvh * D + o] = y0;
+                    rp.kr[(size_t)kvh * D + o + m2] = y1;
+                }
+                if (stored && c == cstore) {
+                    unsigned short* kc = reinterpret_cast<unsigned short*>(rp.kc);
+                    unsigned short* vc = reinterpret_cast<unsigned short*>(rp.vc);
+                    const size_t e = (size_t)row * rp.k_row * 2 + (size_t)kvh * D + o;
+                    const size_t f = (size_t)row * rp.v_row * 2 + (size_t)kvh * D + o;
+                    kc[e] = (unsigned short)f2h(y0);
+                    kc[e + m2] = (unsigned short)f2h(y1);
+                    vc[f] = (unsigned short)f2h(raw[(G + 1) * D + o]);
+                    vc[f + m2] = (unsigned short)f2h(raw[(G + 1) * D + o + m2]);
+                }
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qv[g][e] = qs[g * D + l * 8 + e];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            knw[e] = f2h(kn[l * 8 + 2 * e]) | (f2h(kn[l * 8 + 2 * e + 1]) << 16);
+            vnw[e] = f2h(raw[(G + 1) * D + l * 8 + 2 * e]) | (f2h(raw[(G + 1) * D + l * 8 + 2 * e + 1]) << 16);
+        }
+    } else {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float4* qh =
+                reinterpret_cast<const float4*>(q + (size_t)i * d.q_tok + (size_t)(kvh * G + g) * d.q_head + l * 8);
+            const float4 a = qh[0], b = qh[1];
+            qv[g][0] = a.x, qv[g][1] = a.y, qv[g][2] = a.z, qv[g][3] = a.w;
+            qv[g][4] = b.x, qv[g][5] = b.y, qv[g][6] = b.z, qv[g][7] = b.w;
+        }
     }
 #pragma unroll
     for (int n = 0; n < NI; ++n) {
         const int tl = wave * 16 + n * PPI + sub, t = c * kChunk + tl;
+        const u32x4 kw = RP && t == tnew ? knw : kp[n];
         float kf[8];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            kf[2 * e] = h2f(kp[n][e] & 0xFFFFu);
-            kf[2 * e + 1] = h2f(kp[n][e] >> 16);
+            kf[2 * e] = h2f(kw[e] & 0xFFFFu);
+            kf[2 * e + 1] = h2f(kw[e] >> 16);
         }
         float sg[G];
 #pragma unroll
@@ -1076,11 +1159,12 @@ __global__ __launch_bounds__(256) void flash_decode_kernel(const float* __restri
 #pragma unroll
     for (int n = 0; n < NI; ++n) {
         const int tl = wave * 16 + n * PPI + sub;
+        const u32x4 vw = RP && c * kChunk + tl == tnew ? vnw : vp[n];
         float vf[8];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            vf[2 * e] = h2f(vp[n][e] & 0xFFFFu);
-            vf[2 * e + 1] = h2f(vp[n][e] >> 16);
+            vf[2 * e] = h2f(vw[e] & 0xFFFFu);
+            vf[2 * e + 1] = h2f(vw[e] >> 16);
         }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
@@ -1320,15 +1404,23 @@ size_t flashDecodePartFloats(const kcFaDims& d) {
     return (size_t)d.N * d.H * ((d.T + kChunk - 1) / kChunk) * (d.D + 2);
 }
 
-int launchFlashDecode(const kcFlashDecodeArgs& a, hipStream_t s, int* slot) {
+int launchFlashDecode(const kcFlashDecodeArgs& a, hipStream_t s, int* slot, const FdRope* rope) {
     const kcFaDims& d = a.d;
     if (!flashDecodeSupports(d.D, d.group)) return fromHip(hipErrorInvalidValue, "flash_decode_f16: shape");
+    if (rope && (d.N != 1 || d.H != d.H_kv * d.group))
+        return fromHip(hipErrorInvalidValue, "flash_decode_f16: the RoPE prologue takes one query token");
     const int nch = (d.T + kChunk - 1) / kChunk;
     const dim3 grid(nch, d.H_kv, d.N);
-#define KC_FD(DD, GG)                                                                                               \
-    if (d.D == DD && d.group == GG)                                                                                 \
-        hipLaunchKernelGGL((flash_decode_kernel<DD, GG>), grid, dim3(256), 0, s, a.q, a.k, a.v, a.mask, a.part, d, \
-                           a.scale, nch);
+    const FdRope rp = rope ? *rope : FdRope{};
+#define KC_FD(DD, GG)                                                                                              \
+    if (d.D == DD && d.group == GG) {                                                                              \
+        if (rope)                                                                                                  \
+            hipLaunchKernelGGL((flash_decode_kernel<DD, GG, true>), grid, dim3(256), 0, s, a.q, a.k, a.v, a.mask,  \
+                               a.part, d, a.scale, nch, rp);                                                      \
+        else                                                                                                       \
+            hipLaunchKernelGGL((flash_decode_kernel<DD, GG, false>), grid, dim3(256), 0, s, a.q, a.k, a.v, a.mask, \
+                               a.part, d, a.scale, nch, rp);                                                      \
+    }
     KC_FD(128, 1) KC_FD(128, 2) KC_FD(128, 3) KC_FD(128, 4) KC_FD(128, 5) KC_FD(128, 6) KC_FD(128, 7) KC_FD(128, 8)
     KC_FD(64, 1) KC_FD(64, 2) KC_FD(64, 3) KC_FD(64, 4) KC_FD(64, 5) KC_FD(64, 6) KC_FD(64, 7) KC_FD(64, 8)
 #undef KC_FD

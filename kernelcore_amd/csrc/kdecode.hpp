@@ -82,10 +82,28 @@ size_t attnDecodePartFloats(int Hkv, int max_ctx, int D);
 // seq_merge: the merge in one workgroup per KV head with one thread per block quantizing (the
 // first form, kept as a diagnostic); else one wavefront per 64 outputs (same results, bit for bit).
 int launchAttnDecode(AttnDecodeArgs a, int D, int Hkv, int max_ctx, hipStream_t s, bool seq_merge = false);
+// The ROPE / SET_ROWS prologue of a one-token flash_decode (the ggml graph's ROPE(q), ROPE(k),
+// SET_ROWS(k cache), SET_ROWS(v cache) before FLASH_ATTN_EXT): every workgroup ropes its heads'
+// q and k itself, the new cache row is stored by one workgroup and taken from registers by the one
+// whose chunk holds it, and the roped q and k are written as the ROPE nodes' outputs.
+struct FdRope {
+    const float *q, *k, *v;  // one token, before RoPE: q [H][D], k [Hkv][D] contiguous; v [Hkv][D]
+    float *qr, *kr;          // the ROPE outputs (same layouts as q, k)
+    int *kc, *vc;            // the caches (SET_ROWS destinations): fp16 rows k_row / v_row words apart
+    const int* pos;          // ROPE positions (int32; pos[0])
+    const int* idx;          // SET_ROWS row (int64; its low word)
+    const float* ff;         // RoPE frequency factors [D / 2]
+    float log2_base;
+    int neox;
+    int k_row, v_row;  // cache row strides (32-bit words)
+    int dst_rows;      // cache rows: a row index outside [0, dst_rows) is not stored
+    int row0;          // the cache row of the attention's K / V view row 0 (the same for both)
+};
 // flash_decode_f16 (kcFlashDecodeArgs): the split-context FLASH_ATTN_EXT for D 64 / 128, group <= 8.
 bool flashDecodeSupports(int D, int G);
 size_t flashDecodePartFloats(const kcFaDims& d);
 // slot (optional, one query token): the output also quantized into a per-32 slot of H * D values.
-int launchFlashDecode(const kcFlashDecodeArgs& a, hipStream_t s, int* slot = nullptr);
+// rope (optional, one query token): the ROPE / SET_ROWS prologue above (a.q is then unused).
+int launchFlashDecode(const kcFlashDecodeArgs& a, hipStream_t s, int* slot = nullptr, const FdRope* rope = nullptr);
 
 }  // namespace kcamd

@@ -27,8 +27,9 @@ def plan(g, **cfg):
 
 
 ATTN = ["rope_ggml", "rope_ggml", "set_rows_f16", "set_rows_f16", "flash_decode_f16"]  # the reference's launches
-# ROPE of q and k and the two SET_ROWS in one launch; one token's attention also quantizes its output
-ATTN1 = ["rope_set_rows", "flash_decode_q8"]
+# one token: ROPE of q and k and the two SET_ROWS run inside the attention's launch, which also
+# quantizes its output (batches: ROPE and SET_ROWS in one launch, then the attention)
+ATTN1 = ["rope_flash_decode_q8"]
 
 
 # ---- graph_compute's walk --------------------------------------------------------------------------------------
@@ -89,6 +90,25 @@ def test_rope_and_cache_rows_fuse_only_with_shared_positions_rows_and_parameters
         ropes[1].op_params[5] = ropes[1].op_params[5] + 1  # another frequency base
     names = plan(g)
     assert "rope_set_rows" not in names and names.count("rope_ggml") == 2 and names.count("set_rows_f16") == 2
+
+
+@pytest.mark.parametrize("plant", ["q_source", "k_rows", "v_rows", "k_heads"])
+def test_rope_enters_the_attention_only_on_the_roped_q_and_cache_views(plant):
+    """The ROPE / SET_ROWS nodes run inside one token's attention launch only when the attention reads
+    the roped q and views of the two caches from one common row with the caches' row strides and heads
+    D halves apart; otherwise ROPE + SET_ROWS stay one launch and the attention another."""
+    g, t = layer(N=1)
+    fa = next(x for x in g.nodes if x.op == kc.GGML_OP["flash_attn_ext"])
+    if plant == "q_source":
+        fa.src[0] = C.pointer(g.leaf("f32", [64, 1, 8]))
+    elif plant == "k_rows":
+        fa.src[1].contents.data = fa.src[1].contents.data + fa.src[1].contents.nb[1]  # a view from row 1
+    elif plant == "v_rows":
+        fa.src[2].contents.nb[1] = fa.src[2].contents.nb[1] * 2
+    else:
+        fa.src[1].contents.nb[2] = fa.src[1].contents.nb[2] * 2
+    names = plan(g)
+    assert "rope_flash_decode_q8" not in names and names[1:3] == ["rope_set_rows", "flash_decode_q8"], names
 
 
 @pytest.mark.parametrize("plant", ["glu_output", "glu_second_use", "gate_second_use", "up_view"])
@@ -244,8 +264,7 @@ def test_swiglu_unfused_when_rows_are_not_a_multiple_of_256():
 def test_decode_attention_is_split_over_the_context():
     g, _ = layer(N=1, n_kv=20000, kv_size=20480)
     names, ints = kc.ggml_graph_plan(g.nodes)
-    i = names.index("flash_decode_q8")
-    assert names[i - 1] == "rope_set_rows"
+    assert "rope_flash_decode_q8" in names
     assert ints >= 8 * 313 * 66  # the partials of 8 heads x 313 chunks x (64 values + max + sum)
 
 

@@ -273,7 +273,7 @@ def test_fused_decode_matvecs_equal_one_launch_per_node(shape):
     attention, the two residual sums) equals the reference's one launch per node bit for bit."""
     L = Layer(shape, 1, 90, seed=808)
     names, _ = kc.ggml_graph_plan(L.g.nodes)
-    assert names == ["decode_norm_matvec", "rope_set_rows", "flash_decode_q8", "decode_matvec_add",
+    assert names == ["decode_norm_matvec", "rope_flash_decode_q8", "decode_matvec_add",
                      "decode_norm_swiglu", "decode_matvec_add"]
     kept = ("q", "k", "v", "qr", "kr", "attn", "ffn_inp", "out")  # what both write
     got = {}
