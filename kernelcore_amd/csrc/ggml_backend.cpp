@@ -704,6 +704,43 @@ E flashAttn(Pass& p, const T* dst) {
     return launch(p, "fa_values", &va);
 }
 
+// (No reference counterpart.) mm[0..g) = 2-3 batch MUL_MATs of one input (q / k / v; gate / up)
+// that all run on the per-256 MFMA matmul: K-quant weights of one k, contiguous f32 input columns
+// and outputs, at least 64 columns. They run as one grouped launch over their rows, the input
+// converted to fp16 once (the decode driver's prefill does the same), instead of one matmul each.
+bool batchGroupOk(const Pass& p, const T* const* mm, int g) {
+    if (g < 2 || g > 3 || !p.rec.cfg.q8k || p.rec.cfg.matvec_cols) return false;
+    const T* x = mm[0]->src[1];
+    const int64_t k = mm[0]->src[0]->ne[0], ncols = nrows(x);
+    if (ncols < 64 || ncols > INT32_MAX || k % 256 || k > INT32_MAX || !f32c(x) || x->nb[1] != size_t(k) * 4)
+        return false;
+    if (!kcamd::mfmaHUsable(int(ncols), int(k))) return false;
+    for (int j = 0; j < g; ++j) {
+        const T* w = mm[j]->src[0];
+        if (mm[j]->src[1] != x || !kquant(w) || w->ne[0] != k || w->ne[1] % 8 || w->ne[1] > INT32_MAX ||
+            !f32c(mm[j]) || mm[j]->ne[0] != w->ne[1] || nrows(mm[j]) != ncols)
+            return false;
+    }
+    return true;
+}
+
+E batchGroup(Pass& p, const T* const* mm, int g) {
+    if (E e = mulMatInput(p, mm[0]); e != ok) return e;  // quantize_cols_k, once per input
+    const T* x = mm[0]->src[1];
+    const int k = int(mm[0]->src[0]->ne[0]), ncols = int(nrows(x));
+    const int* q = p.rec.dry ? nullptr : kcamd::mulmat::inputSlot(p.rec, f32(x), ncols, k, true);
+    if (!p.rec.dry && !q) return kc::Error::InternalError;
+    kcamd::MmPart parts[3];
+    for (int j = 0; j < g; ++j) {
+        const T* w = mm[j]->src[0];
+        parts[j] = kcamd::MmPart{w->data, {f32w(mm[j]), nullptr}, int(w->ne[1]), w->type == KC_GGML_TYPE_Q6_K ? 1 : 0};
+    }
+    return direct(p, "matmul_group", [&](hipStream_t s) {
+        int ks = 1;
+        return kcamd::launchMatmulGroup(parts, g, q, k, ncols, 1, &ks, s);
+    });
+}
+
 E concurrent(Pass& p, bool begin) {
     if (E e = marker(p, begin ? "[" : "]"); e != ok) return e;
     if (p.rec.dry) return ok;
@@ -740,6 +777,17 @@ E walk(Pass& p, const T* const* nodes, int n) {
                     if (ga == 1 && matvecAddOk(nodes, n, i, &add)) {
                         e = decodeMatvecAdd(p, node, nodes[add]);
                         i = add;
+                        break;
+                    }
+                }
+                if (kcamd::option("ggml_extra_fusions") != 1) {  // a batch group on the matrix cores: one launch
+                    int gb = 1;
+                    while (i + gb < n && gb < 3 && nodes[i + gb]->op == KC_GGML_OP_MUL_MAT &&
+                           nodes[i + gb]->src[1] == node->src[1] && computed(nodes[i + gb]))
+                        ++gb;
+                    if (batchGroupOk(p, nodes + i, gb)) {
+                        e = batchGroup(p, nodes + i, gb);
+                        i += gb - 1;
                         break;
                     }
                 }

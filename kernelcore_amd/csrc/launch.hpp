@@ -65,6 +65,8 @@ struct MmPart {
 // pre (may be null): the activations already in the MFMA layout (then no conversion is launched).
 int launchMatmulGroup(const MmPart* parts, int nparts, const int* xq, int k, int ncols, int ks, int* used_ks,
                       hipStream_t s, const ActF16* pre = nullptr);
+// Whether a group of ncols >= 64 columns of k values runs on the fp16-activation MFMA kernel.
+bool mfmaHUsable(int ncols, int k);
 // kmatmul_f16.hip: Y [ncols][rows] = W X, W row-major fp16 [rows][k], x ncols columns of k floats;
 // rows % 8 == 0, k even.
 int launchMatmulF16(const void* w, const float* x, float* y, int rows, int k, int ncols, hipStream_t s);

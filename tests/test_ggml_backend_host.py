@@ -150,10 +150,24 @@ def test_batch_layer_plans(N, cfg, mm, quant):
     norm1 = ["add_sumsq_f", "norm_mul_q8k_f"] if k == "q8k" else ["add_norm_q8_f"]
     silu = "silu_mul_q8kf" if k == "q8k" else "silu_mul_q8x4f"
     attn = ["rope_set_rows", "flash_decode_f16" if N <= 8 else "attn_masked"]  # past 8 tokens: the matrix cores
-    want = (norm0 + ["[", mm.format("q4k"), mm.format("q4k"), mm.format("q6k"), "]"] + attn +
-            [quant, mm.format("q4k")] + norm1 + ["[", mm.format("q4k"), mm.format("q4k"), "]", silu,
-             mm.format("q6k"), "vector_add"])
+    # from 64 columns (the MFMA matmul) the q / k / v and gate / up groups are one grouped launch each
+    qkv = ["matmul_group"] if N >= 64 else ["[", mm.format("q4k"), mm.format("q4k"), mm.format("q6k"), "]"]
+    gu = ["matmul_group"] if N >= 64 else ["[", mm.format("q4k"), mm.format("q4k"), "]"]
+    want = (norm0 + qkv + attn + [quant, mm.format("q4k")] + norm1 + gu + [silu, mm.format("q6k"), "vector_add"])
     assert plan(g, **cfg) == want
+
+
+def test_batch_groups_on_the_matrix_cores_take_one_grouped_launch(reference_matvecs):
+    """The grouped launch is a fusion beyond the reference's (ggml_extra_fusions = 1 restores its
+    concurrent group of one matmul per MUL_MAT); below 64 columns, or with per-32 slots, the group
+    stays one matmul each."""
+    g, _ = layer(N=64)
+    names = plan(g, attn_tokens=64)
+    assert "matmul_group" not in names and names.count("[") == 2
+    kc.set_option("ggml_extra_fusions", 0)
+    assert plan(g, attn_tokens=64, q8k=0).count("matmul_group") == 0
+    assert plan(layer(N=63)[0], attn_tokens=64).count("matmul_group") == 0
+    assert plan(g, attn_tokens=64).count("matmul_group") == 2
 
 
 def test_matvec_cols_runs_one_matvec_per_column():
