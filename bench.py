@@ -295,7 +295,7 @@ def ggml_backend_decode_run(cfg, n_ctx, n_decode, seed, reps, modes=(1, 0)):
     return out
 
 
-def ggml_backend_prefill_run(cfg, n_prompt, seed, reps):
+def ggml_backend_prefill_run(cfg, n_prompt, seed, reps, graphs=1):
     """The drop-in path for a prompt: one n_prompt-token step of cfg (positions 0 .., the causal
     mask, the KV view of n_prompt rows rounded up to 256) through kcGgmlGraphCompute on the graph
     llama.cpp builds (the last layer keeps only the last row after its attention; the head gives
@@ -330,7 +330,7 @@ def ggml_backend_prefill_run(cfg, n_prompt, seed, reps):
         kc.call("kcMemcpy", io[name].data, a.ctypes.data, a.nbytes, kc.HOST_TO_DEVICE)
     kc.synchronize()
     nodes = kc.GgmlNodes(g.nodes)
-    be = kc.GgmlBackend(graphs=1, attn_tokens=n_prompt)
+    be = kc.GgmlBackend(graphs=graphs, attn_tokens=n_prompt)
     be.compute(nodes)  # records the kept graph
     times = []
     for _ in range(reps):
@@ -565,7 +565,7 @@ def main():
     ap.add_argument("--eager-decode", action="store_true",
                     help="decode with one kcModelForward per token instead of the replayed graph")
     ap.add_argument("--no-graph", action="store_true",
-                    help="time config 1 and the ggml-backend leg by eager launches only (no graph capture: for "
+                    help="time config 1 and the ggml-backend legs by eager launches only (no graph capture: for "
                          "kernel traces)")
     ap.add_argument("--only-model", action="store_true",
                     help="run only the config-3 matmul and the model legs (profiling); prints their JSON")
@@ -587,7 +587,8 @@ def main():
     if args.only_ggml:
         print(json.dumps({"ggml_backend_decode_cfg4": ggml_backend_decode_run(
             LLAMA32_3B, 512, args.decode_steps, seed=9700, reps=reps, modes=(0,) if args.no_graph else (1, 0)),
-            "ggml_backend_prefill_cfg4": ggml_backend_prefill_run(LLAMA32_3B, 512, seed=9800, reps=reps)}),
+            "ggml_backend_prefill_cfg4": ggml_backend_prefill_run(LLAMA32_3B, 512, seed=9800, reps=reps,
+                                                                 graphs=0 if args.no_graph else 1)}),
             flush=True)
         return
     if args.only_cfg3:
@@ -615,7 +616,7 @@ def main():
         if not args.skip_ggml:
             ggml_leg = ggml_backend_decode_run(LLAMA32_3B, 512, args.decode_steps, seed=9700, reps=reps)
             note(f"# ggml backend decode done: {ggml_leg['kept_graph']['tok_s']} tok/s (kept graph)")
-            ggml_pre = ggml_backend_prefill_run(LLAMA32_3B, 512, seed=9800, reps=reps)
+            ggml_pre = ggml_backend_prefill_run(LLAMA32_3B, 512, seed=9800, reps=reps, graphs=0 if args.no_graph else 1)
             note(f"# ggml backend prefill done: {ggml_pre['prefill_tok_s']} tok/s")
     if args.only_model:
         res = {"prefill_matmul_cfg3": mm, "model_cfg4": mdl}
