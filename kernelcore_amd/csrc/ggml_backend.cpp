@@ -704,12 +704,14 @@ E flashAttn(Pass& p, const T* dst) {
     return launch(p, "fa_values", &va);
 }
 
-// (No reference counterpart.) mm[0..g) = 2-3 batch MUL_MATs of one input (q / k / v; gate / up)
-// that all run on the per-256 MFMA matmul: K-quant weights of one k, contiguous f32 input columns
-// and outputs, at least 64 columns. They run as one grouped launch over their rows, the input
-// converted to fp16 once (the decode driver's prefill does the same), instead of one matmul each.
+// (No reference counterpart.) mm[0..g) = 1-3 batch MUL_MATs of one input (q / k / v; gate / up; o;
+// down) that all run on the per-256 MFMA matmul: K-quant weights of one k, contiguous f32 input
+// columns and outputs, at least 64 columns. They run as one grouped launch over their rows (the
+// decode driver's prefill does the same), from the fp16 form the input's producer wrote with its
+// slots (else converted once), instead of one by-name matmul each that converts its input itself.
+// One MUL_MAT takes the by-name launch's K split (matmulKs), its second half added afterwards.
 bool batchGroupOk(const Pass& p, const T* const* mm, int g) {
-    if (g < 2 || g > 3 || !p.rec.cfg.q8k || p.rec.cfg.matvec_cols) return false;
+    if (g < 1 || g > 3 || !p.rec.cfg.q8k || p.rec.cfg.matvec_cols) return false;
     const T* x = mm[0]->src[1];
     const int64_t k = mm[0]->src[0]->ne[0], ncols = nrows(x);
     if (ncols < 64 || ncols > INT32_MAX || k % 256 || k > INT32_MAX || !f32c(x) || x->nb[1] != size_t(k) * 4)
@@ -717,7 +719,7 @@ bool batchGroupOk(const Pass& p, const T* const* mm, int g) {
     if (!kcamd::mfmaHUsable(int(ncols), int(k))) return false;
     for (int j = 0; j < g; ++j) {
         const T* w = mm[j]->src[0];
-        if (mm[j]->src[1] != x || !kquant(w) || w->ne[0] != k || w->ne[1] % 8 || w->ne[1] > INT32_MAX ||
+        if (mm[j]->src[1] != x || !kquant(w) || w->ne[0] != k || w->ne[1] % 8 || w->ne[1] * ncols > INT32_MAX ||
             !f32c(mm[j]) || mm[j]->ne[0] != w->ne[1] || nrows(mm[j]) != ncols)
             return false;
     }
@@ -730,14 +732,25 @@ E batchGroup(Pass& p, const T* const* mm, int g) {
     const int k = int(mm[0]->src[0]->ne[0]), ncols = int(nrows(x));
     const int* q = p.rec.dry ? nullptr : kcamd::mulmat::inputSlot(p.rec, f32(x), ncols, k, true);
     if (!p.rec.dry && !q) return kc::Error::InternalError;
+    const kcamd::ActF16* pre = kcamd::mulmat::inputAct(p.rec, f32(x), ncols, k);
     kcamd::MmPart parts[3];
     for (int j = 0; j < g; ++j) {
         const T* w = mm[j]->src[0];
         parts[j] = kcamd::MmPart{w->data, {f32w(mm[j]), nullptr}, int(w->ne[1]), w->type == KC_GGML_TYPE_Q6_K ? 1 : 0};
     }
-    return direct(p, "matmul_group", [&](hipStream_t s) {
-        int ks = 1;
-        return kcamd::launchMatmulGroup(parts, g, q, k, ncols, 1, &ks, s);
+    const int rows0 = parts[0].rows;
+    const int ks = g == 1 ? kcamd::matmulKs(rows0, k, ncols) : 1;
+    if (ks == 2) {  // the second K half's partial sums, added into the product after the launch
+        int* part = nullptr;
+        if (E e = kcamd::mulmat::take(p.rec, size_t(rows0) * size_t(ncols), &part); e != ok) return e;
+        parts[0].y[1] = reinterpret_cast<float*>(part);
+    }
+    return direct(p, ks == 2 ? "matmul_group+add" : "matmul_group", [&](hipStream_t s) {
+        int used = 1;
+        if (int e = kcamd::launchMatmulGroup(parts, g, q, k, ncols, ks, &used, s, pre)) return e;
+        if (used != 2) return 0;
+        const kcVectorAddArgs a{parts[0].y[0], parts[0].y[1], parts[0].y[0], rows0 * ncols};
+        return int(kcLaunchKernel("vector_add", &a, p.rec.stream));
     });
 }
 
@@ -911,6 +924,7 @@ E plan(const kcGgmlConfig& c, const T* const* nodes, int n, Plan& out) {
     if (E e = checkNodes(c, nodes, n); e != ok) return e;
     kcMulMatRecording_st dry;
     dry.cfg = c.mul_mat;
+    dry.act_f16 = true;
     dry.dry = true;
     dry.trace = &out.trace;
     Pass p{c, dry, nullptr, &out.ones, c.graphs != 0};
@@ -1119,6 +1133,7 @@ KC_API kcError_t kcGgmlBackendCreate(kcGgmlBackend_t* backend, const kcGgmlConfi
     be->cfg = c;
     be->stream = stream;
     be->rec.cfg = c.mul_mat;
+    be->rec.act_f16 = true;  // the batch producers write the MFMA matmul's fp16 form (batchGroup reads it)
     be->rec.stream = stream;
     *backend = be;
     return ok;

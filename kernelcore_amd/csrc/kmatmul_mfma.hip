@@ -1143,10 +1143,7 @@ __global__ void add_partial_kernel(float* __restrict__ y, const float* __restric
 // A by-name launch on the fp16-activation kernel: a grid under two workgroups of 4 wavefronts per
 // CU splits K in two, the second half's partial sums staged after the activations and added into
 // y by one more kernel (fl(a + b): the same for either order).
-int stagedKs(const kcMatmulKQ8Args& a) {
-    const long long wgs = (long long)((a.rows + kBM - 1) / kBM) * ((a.ncols + 63) / 64);
-    return (a.k / 256 >= 2 && wgs < 2LL * cuCount()) ? 2 : 1;
-}
+int stagedKs(const kcMatmulKQ8Args& a) { return matmulKs(a.rows, a.k, a.ncols); }
 size_t stagedActBytes(const kcMatmulKQ8Args& a) { return (actBytes(a.ncols, a.k) + 255) & ~size_t(255); }
 size_t stagedBytes(const kcMatmulKQ8Args& a, int ks) {
     return stagedActBytes(a) + (ks == 2 ? (size_t)a.rows * a.ncols * 4 : 0);
@@ -1215,6 +1212,11 @@ int launchMatmulKqNoAlloc(bool q6k, bool per256, const kcMatmulKQ8Args& a, hipSt
         return KC_ERROR_NOT_INITIALIZED;
     }
     return runStaged(q6k, a, ks, p, s);
+}
+
+int matmulKs(int rows, int k, int ncols) {
+    const long long wgs = (long long)((rows + kBM - 1) / kBM) * ((ncols + 63) / 64);
+    return (k / 256 >= 2 && wgs < 2LL * cuCount()) ? 2 : 1;
 }
 
 bool mfmaHUsable(int ncols, int k) {

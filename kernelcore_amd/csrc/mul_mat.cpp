@@ -62,6 +62,31 @@ E launch(kcMulMatRecording_st& r, const char* kernel, const void* args, kcMulMat
     return e;
 }
 
+// A launch of one of this build's launchers (no by-name entry) on the recording's stream, named and
+// counted like launch().
+template <class F>
+E direct(kcMulMatRecording_st& r, const char* kernel, F&& fn, kcMulMatPlan& plan) {
+    if (r.trace) r.trace->push_back(kernel);
+    ++plan.launches;
+    if (r.dry) return ok;
+    void* hs = nullptr;
+    if (E e = kcStreamGetNative(r.stream, &hs); e != ok) return e;
+    return static_cast<E>(fn(static_cast<hipStream_t>(hs)));
+}
+
+// Whether a per-256 producer of ncols columns of k values also writes the fp16 MFMA form (act_f16),
+// and that form's buffer in the recording's scratch.
+// Both are the ggml backend's own (act_f16 recordings; kernel option ggml_extra_fusions = 1 keeps the
+// reference's launches), as is the per-256 norm in one workgroup per row.
+bool ownFusions(const kcMulMatRecording_st& r) { return r.act_f16 && kcamd::option("ggml_extra_fusions") != 1; }
+bool wantAct(const kcMulMatRecording_st& r, long long ncols, int k, bool k256) {
+    return ownFusions(r) && k256 && ncols >= 64 && ncols <= INT_MAX && kcamd::mfmaHUsable(int(ncols), k);
+}
+// The fp16 form sits in the same take as the slots it mirrors (a later take may replace the scratch):
+// `ints` of slots, padded to 64 bytes, then the form.
+size_t actOffset(size_t ints) { return (ints + 15) / 16 * 16; }
+size_t actInts(int ncols, int k) { return (kcamd::actF16Bytes(ncols, k) + 3) / 4; }
+
 // The 8-bit form of the node's input, made once per recording.
 E quantizedInput(kcMulMatRecording_st& r, const kcMulMatNode& n, bool k256, int** q, kcMulMatPlan& plan) {
     for (const auto& in : r.inputs)
@@ -72,9 +97,23 @@ E quantizedInput(kcMulMatRecording_st& r, const kcMulMatNode& n, bool k256, int*
         }
     const int nb = n.k / 32;
     const size_t slot = slotInts(n.k, k256);
+    const bool act = wantAct(r, n.ncols, n.k, k256);
+    const size_t ints = slot * size_t(n.ncols);
     int* base = nullptr;
-    if (E e = kcamd::mulmat::take(r, slot * size_t(n.ncols), &base); e != ok) return e;
+    if (E e = kcamd::mulmat::take(r, act ? actOffset(ints) + actInts(int(n.ncols), n.k) : ints, &base); e != ok)
+        return e;
     const bool contiguous = n.x_col_bytes == size_t(n.k) * sizeof(float);
+    if (act) {  // the slots and their fp16 form in one launch
+        const kcamd::ActF16 ao = kcamd::actF16View(base + actOffset(ints), int(n.ncols), n.k, int(n.ncols));
+        name(plan.quantizer, "quantize_cols_k");
+        if (E e = direct(r, "quantize_cols_k", [&](hipStream_t s) {
+                return kcamd::launchQuantizeColsK(n.x, base, n.k, int(n.ncols), s, &ao);
+            }, plan); e != ok)
+            return e;
+        r.inputs.push_back({n.x, n.ncols, n.k, k256, base, ao, true});
+        *q = base;
+        return ok;
+    }
     if (k256) {
         const kcQuantizeColsArgs a{n.x, base, nullptr, n.k, int(n.ncols)};
         name(plan.quantizer, "quantize_cols_k");
@@ -121,10 +160,29 @@ E fusedNormImpl(kcMulMatRecording_st& r, const kcMulMatNormNode& n, kcMulMatPlan
     plan.k256 = k256;
     // per 256: the rows' slots, then the per-32 partial sums of squares; per 32: in the slots' tails
     const size_t off = k256 ? size_t(n.rows) * slotInts(n.n, true) : 0;
+    const size_t sums = k256 ? size_t(n.rows) * slotInts(n.n, false) : 0;
+    const bool one = k256 && n.n <= 8192 && ownFusions(r);  // add_norm_q8k_f
+    const bool act = one && wantAct(r, n.rows, n.n, k256);
     int* qk = nullptr;
-    if (E e = registeredSlots(r, n.y, n.n, n.rows, k256, k256 ? size_t(n.rows) * slotInts(n.n, false) : 0, &qk); e != ok)
+    if (E e = registeredSlots(r, n.y, n.n, n.rows, k256, act ? actOffset(off + sums) - off + actInts(n.rows, n.n) : sums,
+                              &qk);
+        e != ok)
         return e;
     int* q = qk + off;
+    if (one) {  // per 256: both steps in one workgroup per row (the same bytes)
+        kcamd::ActF16 ao{};
+        if (act) {
+            ao = kcamd::actF16View(qk + actOffset(off + sums), n.rows, n.n, n.rows);
+            auto& in = r.inputs.back();  // registeredSlots' entry for y
+            in.act = ao;
+            in.has_act = true;
+        }
+        name(plan.kernel, "add_norm_q8k_f");
+        return direct(r, "add_norm_q8k_f", [&](hipStream_t s) {
+            return kcamd::launchAddNormQ8K(n.a, n.a ? n.b : n.x, nullptr, n.a ? n.x : nullptr, n.w, qk, n.n, n.rows, n.eps,
+                                           s, act ? &ao : nullptr, n.y);
+        }, plan);
+    }
     if (!k256 && n.n <= 8192) {  // both steps in one workgroup per row (the same bytes)
         const kcAddNormQ8FArgs a{n.a, n.b, n.x, n.w, n.y, q, nullptr, n.n, n.rows, n.eps};
         name(plan.kernel, "add_norm_q8_f");
@@ -152,8 +210,20 @@ E fusedSwigluImpl(kcMulMatRecording_st& r, const kcMulMatSwigluNode& n, kcMulMat
     const bool k256 = batchK256(r, n.cols);
     plan.k256 = k256;
     int* q = nullptr;
-    if (E e = registeredSlots(r, n.y, n.n, n.cols, k256, 0, &q); e != ok) return e;
+    const bool act = wantAct(r, n.cols, n.n, k256);
+    const size_t ints = slotInts(n.n, k256) * size_t(n.cols);
+    if (E e = registeredSlots(r, n.y, n.n, n.cols, k256, act ? actOffset(ints) - ints + actInts(n.cols, n.n) : 0, &q);
+        e != ok)
+        return e;
     const kcSiluMulQ8FArgs a{n.g, n.u, n.y, q, nullptr, n.n, n.cols};
+    if (act) {  // the slots and their fp16 form in one launch
+        const kcamd::ActF16 ao = kcamd::actF16View(q + actOffset(ints), n.cols, n.n, n.cols);
+        auto& in = r.inputs.back();
+        in.act = ao;
+        in.has_act = true;
+        name(plan.kernel, "silu_mul_q8kf");
+        return direct(r, "silu_mul_q8kf", [&](hipStream_t s) { return kcamd::launchSiluMulQ8KAct(a, &ao, s); }, plan);
+    }
     const char* kernel = k256 ? "silu_mul_q8kf" : "silu_mul_q8x4f";
     name(plan.kernel, kernel);
     return launch(r, kernel, &a, plan);
@@ -252,6 +322,12 @@ kcError_t take(kcMulMatRecording_st& r, size_t ints, int** out) noexcept {
 int* inputSlot(const kcMulMatRecording_st& r, const float* x, long long ncols, int k, bool k256) noexcept {
     for (const auto& in : r.inputs)
         if (in.x == x && in.ncols == ncols && in.k == k && in.k256 == k256) return in.q;
+    return nullptr;
+}
+
+const kcamd::ActF16* inputAct(const kcMulMatRecording_st& r, const float* x, long long ncols, int k) noexcept {
+    for (const auto& in : r.inputs)
+        if (in.x == x && in.ncols == ncols && in.k == k && in.k256) return in.has_act ? &in.act : nullptr;
     return nullptr;
 }
 

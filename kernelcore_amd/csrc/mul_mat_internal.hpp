@@ -7,6 +7,7 @@
 #include <vector>
 
 #include "kernelcore/mul_mat.h"
+#include "launch.hpp"
 
 struct kcMulMatRecording_st {
     kcMulMatConfig cfg{};
@@ -26,8 +27,13 @@ struct kcMulMatRecording_st {
         int k;
         bool k256;
         int* q;
+        kcamd::ActF16 act{};  // the fp16 MFMA form of the slots, when has_act
+        bool has_act = false;
     };
     std::vector<Input> inputs;  // the recording's quantized inputs
+    // The ggml backend's recordings: per-256 producers of at least 64 columns that the MFMA matmul
+    // takes also write the fp16 form it reads, so the matmuls convert nothing (kcMulMat* leave it off).
+    bool act_f16 = false;
 };
 
 namespace kcamd::mulmat {
@@ -44,6 +50,8 @@ kcError_t take(kcMulMatRecording_st& r, size_t ints, int** out) noexcept;
 kcError_t launch(kcMulMatRecording_st& r, const char* kernel, const void* args) noexcept;
 // the recording's 8-bit slots of input x (nullptr when it made none)
 int* inputSlot(const kcMulMatRecording_st& r, const float* x, long long ncols, int k, bool k256) noexcept;
+// the fp16 MFMA form of x's per-256 slots (nullptr when no producer wrote it)
+const kcamd::ActF16* inputAct(const kcMulMatRecording_st& r, const float* x, long long ncols, int k) noexcept;
 // slots for the 8-bit form of y registered under y, for a producer that writes them itself (the
 // MUL_MATs that read y then take them)
 kcError_t outputSlot(kcMulMatRecording_st& r, const float* y, int k, long long ncols, bool k256, int** q) noexcept;

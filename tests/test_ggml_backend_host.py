@@ -145,15 +145,16 @@ def test_graphs_off_runs_no_concurrent_groups(reference_matvecs):
 def test_batch_layer_plans(N, cfg, mm, quant):
     g, _ = layer(N=N)
     k = "q8k" if quant == "quantize_cols_k" else "q8"
-    # per-256 slots: the sums then norm_mul_q8k_f; per-32: both in add_norm_q8_f
-    norm0 = ["sumsq_part", "norm_mul_q8k_f"] if k == "q8k" else ["add_norm_q8_f"]
-    norm1 = ["add_sumsq_f", "norm_mul_q8k_f"] if k == "q8k" else ["add_norm_q8_f"]
+    # [ADD +] RMS_NORM + MUL in one workgroup per row: add_norm_q8k_f (per 256) or add_norm_q8_f (per 32)
+    norm = ["add_norm_q8k_f"] if k == "q8k" else ["add_norm_q8_f"]
     silu = "silu_mul_q8kf" if k == "q8k" else "silu_mul_q8x4f"
     attn = ["rope_set_rows", "flash_decode_f16" if N <= 8 else "attn_masked"]  # past 8 tokens: the matrix cores
-    # from 64 columns (the MFMA matmul) the q / k / v and gate / up groups are one grouped launch each
+    # from 64 columns (the MFMA matmul) every MUL_MAT runs grouped from its input's fp16 form: q / k / v and
+    # gate / up one launch each, o and down with the K split and its add
     qkv = ["matmul_group"] if N >= 64 else ["[", mm.format("q4k"), mm.format("q4k"), mm.format("q6k"), "]"]
     gu = ["matmul_group"] if N >= 64 else ["[", mm.format("q4k"), mm.format("q4k"), "]"]
-    want = (norm0 + qkv + attn + [quant, mm.format("q4k")] + norm1 + gu + [silu, mm.format("q6k"), "vector_add"])
+    o, down = (["matmul_group+add"], ["matmul_group+add"]) if N >= 64 else ([mm.format("q4k")], [mm.format("q6k")])
+    want = (norm + qkv + attn + [quant] + o + norm + gu + [silu] + down + ["vector_add"])
     assert plan(g, **cfg) == want
 
 
