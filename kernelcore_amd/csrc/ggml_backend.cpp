@@ -231,6 +231,9 @@ struct Pass {
     kcGgmlBackend_st* be;            // null in a plan
     std::vector<int>* ones_wanted;   // a plan: the lengths of the 1.0f arrays the launches read
     bool capturing;                  // launches recorded into a graph (MUL_MAT groups run concurrently)
+    // Batch products whose second K half (partial sums) is not yet added: the ADD that reads one adds
+    // it inside its fused norm; any other reader, and the end of the walk, adds it first.
+    std::vector<std::pair<const T*, const float*>> pending{};
 };
 
 const float* onesOf(Pass& p, int n) {
@@ -314,20 +317,59 @@ E swiglu(Pass& p, const T* dst) {  // :641-646
     return launch(p, "silu_mul", &a);
 }
 
+// The pending second K half of product t (null if none), now the caller's to add.
+const float* takePending(Pass& p, const T* t) {
+    for (auto it = p.pending.begin(); it != p.pending.end(); ++it)
+        if (it->first == t) {
+            const float* h = it->second;
+            p.pending.erase(it);
+            return h;
+        }
+    return nullptr;
+}
+// t += h (the product's two K halves, fl(y1 + y2) as the by-name launch's add)
+E addHalf(Pass& p, const T* t, const float* h) {
+    const kcVectorAddArgs a{f32(t), h, f32w(t), int(nelements(t))};
+    return launch(p, "vector_add", &a);
+}
+// Adds the pending half of t, if any, before something reads t.
+E settle(Pass& p, const T* t) {
+    if (!t || p.pending.empty()) return ok;
+    if (const float* h = takePending(p, t)) return addHalf(p, t, h);
+    return ok;
+}
+
 // [ADD +] RMS_NORM + MUL, the result also quantized for the MUL_MATs that read it (:502-530).
 // Beyond the fused kernels' 2^24 values: the ADD and a weighted rms_norm.
 E fusedNorm(Pass& p, const T* addNode, const T* norm, const T* mulNode) {
     const T* x = norm->src[0];
     const int64_t n = x->ne[0], rows = nrows(x);
+    // an ADD operand with a pending second K half: it becomes b, its half b2 (x = a + (b + b2))
+    const T* a = addNode ? addNode->src[0] : nullptr;
+    const T* b = addNode ? addNode->src[1] : nullptr;
+    const float* b2 = nullptr;
+    if (addNode) {
+        if (const float* h = takePending(p, a)) {
+            std::swap(a, b);
+            b2 = h;
+        } else {
+            b2 = takePending(p, b);
+        }
+        if (E e = settle(p, a); e != ok) return e;  // (both operands pending: one is added first)
+        if (b2 && (n * rows >= (int64_t(1) << 24) || !kcamd::mulmat::fusesHalf(p.rec, int(n)))) {
+            if (E e = addHalf(p, b, b2); e != ok) return e;
+            b2 = nullptr;
+        }
+    }
     if (n * rows >= (int64_t(1) << 24)) {
         if (addNode)
             if (E e = add(p, addNode); e != ok) return e;
         return rmsNorm(p, norm, f32(mulNode->src[1]), mulNode);
     }
-    const kcMulMatNormNode nn{addNode ? f32(addNode->src[0]) : nullptr, addNode ? f32(addNode->src[1]) : nullptr,
-                              f32w(x), f32(mulNode->src[1]), f32w(mulNode), int(n), int(rows), paramF32(norm, 0)};
+    const kcMulMatNormNode nn{addNode ? f32(a) : nullptr, addNode ? f32(b) : nullptr, f32w(x), f32(mulNode->src[1]),
+                              f32w(mulNode), int(n), int(rows), paramF32(norm, 0)};
     kcMulMatPlan plan{};
-    return kcamd::mulmat::fusedNorm(p.rec, nn, plan);
+    return kcamd::mulmat::fusedNorm(p.rec, nn, plan, b2);
 }
 
 // SWIGLU with the result also quantized for the down projection (:533-545); n % 256 == 0.
@@ -740,18 +782,29 @@ E batchGroup(Pass& p, const T* const* mm, int g) {
     }
     const int rows0 = parts[0].rows;
     const int ks = g == 1 ? kcamd::matmulKs(rows0, k, ncols) : 1;
-    if (ks == 2) {  // the second K half's partial sums, added into the product after the launch
+    if (ks == 2) {  // the second K half's partial sums
         int* part = nullptr;
         if (E e = kcamd::mulmat::take(p.rec, size_t(rows0) * size_t(ncols), &part); e != ok) return e;
         parts[0].y[1] = reinterpret_cast<float*>(part);
     }
-    return direct(p, ks == 2 ? "matmul_group+add" : "matmul_group", [&](hipStream_t s) {
+    const E e = direct(p, "matmul_group", [&](hipStream_t s) {
         int used = 1;
-        if (int e = kcamd::launchMatmulGroup(parts, g, q, k, ncols, ks, &used, s, pre)) return e;
-        if (used != 2) return 0;
-        const kcVectorAddArgs a{parts[0].y[0], parts[0].y[1], parts[0].y[0], rows0 * ncols};
-        return int(kcLaunchKernel("vector_add", &a, p.rec.stream));
+        if (int st = kcamd::launchMatmulGroup(parts, g, q, k, ncols, ks, &used, s, pre)) return st;
+        if (used != ks) {  // (the launcher runs the MFMA kernel whenever batchGroupOk holds)
+            kcamd::setDetail("ggml backend: the grouped matmul took another K split than planned");
+            return int(kc::Error::InternalError);
+        }
+        return 0;
     });
+    if (e != ok || ks != 2) return e;
+    // the half is added by whatever reads the product next (the ADD's fused norm takes it along)
+    // unless the product is a view, an output or read twice: then now
+    const T* y = mm[0];
+    if (y->uses == 1 && !y->view && !y->output) {
+        p.pending.emplace_back(y, parts[0].y[1]);
+        return ok;
+    }
+    return addHalf(p, y, parts[0].y[1]);
 }
 
 E concurrent(Pass& p, bool begin) {
@@ -765,6 +818,11 @@ E walk(Pass& p, const T* const* nodes, int n) {
     static const int kNormMul[2] = {KC_GGML_OP_RMS_NORM, KC_GGML_OP_MUL};
     for (int i = 0; i < n; ++i) {
         const T* node = nodes[i];
+        // a reader of a product with a pending K half (views included) adds it first; an ADD decides
+        // below (its fused norm takes it along)
+        if (!p.pending.empty() && node->op != KC_GGML_OP_ADD)
+            for (int s = 0; s < 5; ++s)
+                if (E e = settle(p, node->src[s]); e != ok) return e;
         // nothing to compute (e.g. a prompt's earlier batches select no output rows); fused
         // partners of an empty node are empty too
         if (!computed(node)) continue;
@@ -845,7 +903,9 @@ E walk(Pass& p, const T* const* nodes, int n) {
                     e = fusedNorm(p, node->op == KC_GGML_OP_ADD ? node : nullptr, norm, mulNode);
                     i = ni + 1;
                 } else if (node->op == KC_GGML_OP_ADD) {
-                    e = add(p, node);
+                    e = settle(p, node->src[0]);
+                    if (e == ok) e = settle(p, node->src[1]);
+                    if (e == ok) e = add(p, node);
                 } else {
                     const T* next = i + 1 < n ? nodes[i + 1] : nullptr;
                     if (next && canFuse(nodes, n, i, kNormMul, 2) && next->src[0] == node &&
@@ -889,6 +949,10 @@ E walk(Pass& p, const T* const* nodes, int n) {
                 return kc::Error::UnsupportedOperation;
         }
         if (e != ok) return e;
+    }
+    while (!p.pending.empty()) {  // products nothing in the list read: whole for the caller
+        const T* t = p.pending.front().first;
+        if (E e = settle(p, t); e != ok) return e;
     }
     return ok;
 }

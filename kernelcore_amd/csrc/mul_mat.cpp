@@ -152,7 +152,7 @@ E registeredSlots(kcMulMatRecording_st& r, const float* y, int k, long long ncol
     return ok;
 }
 
-E fusedNormImpl(kcMulMatRecording_st& r, const kcMulMatNormNode& n, kcMulMatPlan& plan) {
+E fusedNormImpl(kcMulMatRecording_st& r, const kcMulMatNormNode& n, kcMulMatPlan& plan, const float* b2) {
     if (!n.x || !n.w || !n.y || (n.a != nullptr) != (n.b != nullptr)) return bad("norm: null x, w or y, or one of a / b");
     if (n.n <= 0 || n.n % 256 || n.rows <= 0 || (long long)n.n * n.rows >= (1 << 24))
         return bad("norm: n must be a positive multiple of 256, rows positive, n * rows < 2^24");
@@ -162,6 +162,7 @@ E fusedNormImpl(kcMulMatRecording_st& r, const kcMulMatNormNode& n, kcMulMatPlan
     const size_t off = k256 ? size_t(n.rows) * slotInts(n.n, true) : 0;
     const size_t sums = k256 ? size_t(n.rows) * slotInts(n.n, false) : 0;
     const bool one = k256 && n.n <= 8192 && ownFusions(r);  // add_norm_q8k_f
+    if (b2 && (!one || !n.a)) return bad("norm: a second K half needs an ADD and the one-kernel per-256 norm");
     const bool act = one && wantAct(r, n.rows, n.n, k256);
     int* qk = nullptr;
     if (E e = registeredSlots(r, n.y, n.n, n.rows, k256, act ? actOffset(off + sums) - off + actInts(n.rows, n.n) : sums,
@@ -179,8 +180,8 @@ E fusedNormImpl(kcMulMatRecording_st& r, const kcMulMatNormNode& n, kcMulMatPlan
         }
         name(plan.kernel, "add_norm_q8k_f");
         return direct(r, "add_norm_q8k_f", [&](hipStream_t s) {
-            return kcamd::launchAddNormQ8K(n.a, n.a ? n.b : n.x, nullptr, n.a ? n.x : nullptr, n.w, qk, n.n, n.rows, n.eps,
-                                           s, act ? &ao : nullptr, n.y);
+            return kcamd::launchAddNormQ8K(n.a, n.a ? n.b : n.x, n.a ? b2 : nullptr, n.a ? n.x : nullptr, n.w, qk, n.n,
+                                           n.rows, n.eps, s, act ? &ao : nullptr, n.y);
         }, plan);
     }
     if (!k256 && n.n <= 8192) {  // both steps in one workgroup per row (the same bytes)
@@ -370,9 +371,13 @@ kcError_t mulMatInput(kcMulMatRecording_st& r, const kcMulMatNode& n, kcMulMatPl
     }
 }
 
-kcError_t fusedNorm(kcMulMatRecording_st& r, const kcMulMatNormNode& n, kcMulMatPlan& plan) noexcept {
+bool fusesHalf(const kcMulMatRecording_st& r, int n) noexcept {
+    return n > 0 && n % 256 == 0 && n <= 8192 && batchK256(r, 2) && ownFusions(r);
+}
+
+kcError_t fusedNorm(kcMulMatRecording_st& r, const kcMulMatNormNode& n, kcMulMatPlan& plan, const float* b2) noexcept {
     try {
-        return fusedNormImpl(r, n, plan);
+        return fusedNormImpl(r, n, plan, b2);
     } catch (...) {
         return kc::Error::OutOfMemory;
     }

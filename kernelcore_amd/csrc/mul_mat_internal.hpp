@@ -59,7 +59,11 @@ kcError_t outputSlot(kcMulMatRecording_st& r, const float* y, int k, long long n
 kcError_t mulMat(kcMulMatRecording_st& r, const kcMulMatNode& n, kcMulMatPlan& plan) noexcept;
 // the node's 8-bit input made now (the reference's mul_mat_input; nothing for F16 weights)
 kcError_t mulMatInput(kcMulMatRecording_st& r, const kcMulMatNode& n, kcMulMatPlan& plan) noexcept;
-kcError_t fusedNorm(kcMulMatRecording_st& r, const kcMulMatNormNode& n, kcMulMatPlan& plan) noexcept;
+// b2 (with an ADD, only where fusesHalf): x = a + (b + b2), the second K half of the product b
+kcError_t fusedNorm(kcMulMatRecording_st& r, const kcMulMatNormNode& n, kcMulMatPlan& plan,
+                    const float* b2 = nullptr) noexcept;
+// whether fusedNorm of rows of n values takes a b2 (the per-256 norm in one workgroup per row)
+bool fusesHalf(const kcMulMatRecording_st& r, int n) noexcept;
 kcError_t fusedSwiglu(kcMulMatRecording_st& r, const kcMulMatSwigluNode& n, kcMulMatPlan& plan) noexcept;
 
 }  // namespace kcamd::mulmat

@@ -150,25 +150,44 @@ def test_batch_layer_plans(N, cfg, mm, quant):
     silu = "silu_mul_q8kf" if k == "q8k" else "silu_mul_q8x4f"
     attn = ["rope_set_rows", "flash_decode_f16" if N <= 8 else "attn_masked"]  # past 8 tokens: the matrix cores
     # from 64 columns (the MFMA matmul) every MUL_MAT runs grouped from its input's fp16 form: q / k / v and
-    # gate / up one launch each, o and down with the K split and its add
+    # gate / up one launch each, o and down with the K split whose second half the next reader adds: the
+    # FFN norm takes o's along, the layer's last ADD (no norm follows in this one-layer graph) adds down's
+    # with one more vector_add first
     qkv = ["matmul_group"] if N >= 64 else ["[", mm.format("q4k"), mm.format("q4k"), mm.format("q6k"), "]"]
     gu = ["matmul_group"] if N >= 64 else ["[", mm.format("q4k"), mm.format("q4k"), "]"]
-    o, down = (["matmul_group+add"], ["matmul_group+add"]) if N >= 64 else ([mm.format("q4k")], [mm.format("q6k")])
+    o, down = (["matmul_group"], ["matmul_group", "vector_add"]) if N >= 64 else ([mm.format("q4k")], [mm.format("q6k")])
     want = (norm + qkv + attn + [quant] + o + norm + gu + [silu] + down + ["vector_add"])
     assert plan(g, **cfg) == want
 
 
 def test_batch_groups_on_the_matrix_cores_take_one_grouped_launch(reference_matvecs):
     """The grouped launch is a fusion beyond the reference's (ggml_extra_fusions = 1 restores its
-    concurrent group of one matmul per MUL_MAT); below 64 columns, or with per-32 slots, the group
-    stays one matmul each."""
+    concurrent group of one by-name matmul per MUL_MAT); below 64 columns, or with per-32 slots, the
+    MUL_MATs stay by-name matmuls."""
     g, _ = layer(N=64)
     names = plan(g, attn_tokens=64)
     assert "matmul_group" not in names and names.count("[") == 2
     kc.set_option("ggml_extra_fusions", 0)
     assert plan(g, attn_tokens=64, q8k=0).count("matmul_group") == 0
     assert plan(layer(N=63)[0], attn_tokens=64).count("matmul_group") == 0
-    assert plan(g, attn_tokens=64).count("matmul_group") == 2
+    assert plan(g, attn_tokens=64).count("matmul_group") == 4  # q / k / v, o, gate / up, down
+
+
+@pytest.mark.parametrize("plant", ["second_use", "output", "view"])
+def test_second_k_half_is_added_at_once_unless_the_add_alone_reads_the_product(plant):
+    """A batch product whose K is split leaves its second half for its one reader, the ADD, whose
+    fused norm adds it; a product read twice, a graph output or a view is completed right after its
+    matmul."""
+    g, t = layer(N=64)
+    if plant == "second_use":
+        t["o"].uses = 2
+    elif plant == "output":
+        t["o"].output = 1
+    else:
+        t["o"].view = 1
+    names = plan(g, attn_tokens=64)
+    i = names.index("attn_masked")
+    assert names[i + 1:i + 5] == ["quantize_cols_k", "matmul_group", "vector_add", "add_norm_q8k_f"], names
 
 
 def test_matvec_cols_runs_one_matvec_per_column():
