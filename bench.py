@@ -583,13 +583,25 @@ def main():
     kc.init()
     props = kc.device_properties()
     note(f"# device: {props.name.decode()} ({props.worker_count} CUs)")
-    mm = mdl = mdl5 = ggml_leg = ggml_pre = None
+    mm = mdl = mdl5 = ggml_leg = ggml_pre = ggml_leg5 = ggml_pre5 = None
+    modes, gr = ((0,), 0) if args.no_graph else ((1, 0), 1)
+
+    def ggml_cfg5():
+        # config 5 (Qwen3-8B shape: the per-head q / k norms, NEOX RoPE) through the backend: decode at
+        # context 1024 onwards (a quarter of the model leg's steps), then the 1024-token prompt
+        d = ggml_backend_decode_run(QWEN3_8B, 1024, max(args.decode_steps5 // 4, 8), seed=9900, reps=reps, modes=modes)
+        note(f"# ggml backend cfg5 decode done: {d[('kept_graph' if gr else 'eager')]['tok_s']} tok/s")
+        p = ggml_backend_prefill_run(QWEN3_8B, 1024, seed=9950, reps=reps, graphs=gr)
+        note(f"# ggml backend cfg5 prefill done: {p['prefill_tok_s']} tok/s")
+        return d, p
+
     if args.only_ggml:
-        print(json.dumps({"ggml_backend_decode_cfg4": ggml_backend_decode_run(
-            LLAMA32_3B, 512, args.decode_steps, seed=9700, reps=reps, modes=(0,) if args.no_graph else (1, 0)),
-            "ggml_backend_prefill_cfg4": ggml_backend_prefill_run(LLAMA32_3B, 512, seed=9800, reps=reps,
-                                                                 graphs=0 if args.no_graph else 1)}),
-            flush=True)
+        res = {"ggml_backend_decode_cfg4": ggml_backend_decode_run(LLAMA32_3B, 512, args.decode_steps, seed=9700,
+                                                                   reps=reps, modes=modes),
+               "ggml_backend_prefill_cfg4": ggml_backend_prefill_run(LLAMA32_3B, 512, seed=9800, reps=reps, graphs=gr)}
+        if not args.skip_cfg5:
+            res["ggml_backend_decode_cfg5"], res["ggml_backend_prefill_cfg5"] = ggml_cfg5()
+        print(json.dumps(res), flush=True)
         return
     if args.only_cfg3:
         print(json.dumps({"prefill_matmul_cfg3": prefill_matmul_run(max(args.steps // 5, 5), seed=7000, reps=reps)}),
@@ -616,13 +628,18 @@ def main():
         if not args.skip_ggml:
             ggml_leg = ggml_backend_decode_run(LLAMA32_3B, 512, args.decode_steps, seed=9700, reps=reps)
             note(f"# ggml backend decode done: {ggml_leg['kept_graph']['tok_s']} tok/s (kept graph)")
-            ggml_pre = ggml_backend_prefill_run(LLAMA32_3B, 512, seed=9800, reps=reps, graphs=0 if args.no_graph else 1)
+            ggml_pre = ggml_backend_prefill_run(LLAMA32_3B, 512, seed=9800, reps=reps, graphs=gr)
             note(f"# ggml backend prefill done: {ggml_pre['prefill_tok_s']} tok/s")
+            if not args.skip_cfg5:
+                ggml_leg5, ggml_pre5 = ggml_cfg5()
     if args.only_model:
         res = {"prefill_matmul_cfg3": mm, "model_cfg4": mdl}
         if ggml_leg:
             res["ggml_backend_decode_cfg4"] = ggml_leg
             res["ggml_backend_prefill_cfg4"] = ggml_pre
+        if ggml_leg5:
+            res["ggml_backend_decode_cfg5"] = ggml_leg5
+            res["ggml_backend_prefill_cfg5"] = ggml_pre5
         if mdl5:
             res["model_cfg5"] = mdl5
         print(json.dumps(res), flush=True)
@@ -691,6 +708,9 @@ def main():
     if ggml_leg:
         out["ggml_backend_decode_cfg4"] = ggml_leg
         out["ggml_backend_prefill_cfg4"] = ggml_pre
+    if ggml_leg5:
+        out["ggml_backend_decode_cfg5"] = ggml_leg5
+        out["ggml_backend_prefill_cfg5"] = ggml_pre5
     if cal:
         out["calibration"] = cal
     if cpu:

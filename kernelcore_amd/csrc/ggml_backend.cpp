@@ -149,6 +149,20 @@ bool f16Rows(const T* t) {  // fp16, rows and heads at 32-bit word strides
 
 // flash_attn_ok, and the size limits of the attention kernels (beyond them the reference's kernels
 // refuse the launch; here the op is not claimed, so the scheduler places it elsewhere).
+// A batch attention flashAttn runs on the matrix cores, reading ggml's mask (no score matrix in
+// scratch, so the 2^24-value limit below does not apply): a mask, more than 8 query tokens, the
+// decoder caches' layout (heads D / 2 words apart in K and V rows of one stride, q and out
+// [N][H][D]) and a shape the kernel takes.
+bool maskedAttn(const T* op) {
+    const T *q = op->src[0], *k = op->src[1], *v = op->src[2], *mask = op->src[3];
+    if (!mask || q->ne[1] <= 8 || k->ne[0] > INT32_MAX || k->ne[1] > INT32_MAX || q->ne[1] > INT32_MAX) return false;
+    const int D = int(k->ne[0]), H = int(q->ne[2]), Hkv = int(k->ne[2]), N = int(q->ne[1]), T = int(k->ne[1]);
+    const kcamd::AttnShape as{N, H, Hkv, D, int(q->nb[1] / 4), int(k->nb[1] / 4), T, 0, paramF32(op, 0)};
+    return kcamd::attnMaskedSupports(as) && q->nb[2] / 4 == uint64_t(D) && q->nb[1] / 4 == uint64_t(H) * D &&
+           k->nb[2] / 4 == uint64_t(D / 2) && v->nb[2] / 4 == uint64_t(D / 2) && v->nb[1] == k->nb[1] &&
+           mask->nb[1] / 4 > 0;
+}
+
 bool flashAttnOk(const kcGgmlConfig& c, const T* op) {
     const T* q = op->src[0];
     const T* k = op->src[1];
@@ -168,7 +182,8 @@ bool flashAttnOk(const kcGgmlConfig& c, const T* op) {
                  mask->ne[1] < q->ne[1] || mask->ne[2] != 1 || mask->ne[3] != 1))
         return false;
     const int64_t tp = (k->ne[1] + 7) / 8 * 8, rows = q->ne[2] * q->ne[1];
-    return rows * tp < (int64_t(1) << 24) && rows * D < (int64_t(1) << 24) && q->nb[2] / 4 >= uint64_t(D);
+    if (rows * D >= (int64_t(1) << 24) || q->nb[2] / 4 < uint64_t(D)) return false;
+    return rows * tp < (int64_t(1) << 24) || maskedAttn(op);
 }
 
 bool supports(const kcGgmlConfig& c, const T* op) {
@@ -720,8 +735,7 @@ E flashAttn(Pass& p, const T* dst) {
     // a batch with a mask, in the layout of the decoder's caches (heads D / 2 words apart in K and V
     // rows of one stride, q and out [N][H][D]): on the matrix cores, masked key blocks skipped
     const kcamd::AttnShape as{d.N, d.H, d.H_kv, d.D, d.q_tok, d.k_row, d.T, 0, scale};
-    if (md && kcamd::attnMaskedSupports(as) && d.q_head == d.D && d.q_tok == d.H * d.D && d.k_head == d.D / 2 &&
-        d.v_head == d.D / 2 && d.v_row == d.k_row && d.m_row > 0) {
+    if (maskedAttn(dst)) {
         const auto* mh = static_cast<const unsigned short*>(mask->data);
         return direct(p, "attn_masked", [&](hipStream_t s) {
             return kcamd::launchAttnMasked(f32(q), kd, vd, mh, 2 * d.m_row, d.T, f32w(dst), as, s);

@@ -402,6 +402,30 @@ __global__ void rms_norm_kernel(const float* __restrict__ x, const float* __rest
     for (int j = 0; j < n; ++j) yr[j] = xr[j] * r * w[j];
 }
 
+// The same per row with one workgroup of 64 lanes (rows up to 16384 values): the row staged in LDS
+// by coalesced loads, its sum of squares in element order by one lane (the same additions, so the
+// same bits), then y = x r w by every lane. A thread per row leaves the GPU nearly idle and waits
+// for each of its row's loads in turn (a Qwen3 layer's per-head q / k norms, 32 and 8 rows of 128).
+__global__ __launch_bounds__(64) void rms_norm_row_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                          float* __restrict__ y, int n, float eps) {
+    extern __shared__ float xs[];
+    __shared__ float rr;
+    const int lane = threadIdx.x;
+    const float* xr = x + (size_t)blockIdx.x * n;
+    for (int j = lane; j < n; j += 64) xs[j] = xr[j];
+    __syncthreads();
+    if (lane == 0) {
+        float ss = 0.0f;
+#pragma unroll 8
+        for (int j = 0; j < n; ++j) ss += xs[j] * xs[j];
+        rr = 1.0f / sqrtf(ss / (float)n + eps);
+    }
+    __syncthreads();
+    const float r = rr;
+    float* yr = y + (size_t)blockIdx.x * n;
+    for (int j = lane; j < n; j += 64) yr[j] = xs[j] * r * w[j];
+}
+
 // ggml ROPE (rope_ggml.cu): one thread per (token, head, pair); each thread takes the pair's
 // angle itself (the reference's per-(token, pair) value, recomputed per head).
 __global__ void rope_kernel(const float* __restrict__ x, float* __restrict__ y, const int* __restrict__ pos,
@@ -837,7 +861,11 @@ int launchSiluMul(const kcSiluMulArgs& a, hipStream_t s) {
 
 int launchRmsNorm(const kcRmsNormArgs& a, hipStream_t s) {
     if (a.rows == 0) return 0;
-    hipLaunchKernelGGL(rms_norm_kernel, dim3(blocksFor(a.rows)), dim3(256), 0, s, a.x, a.w, a.y, a.n, a.rows, a.eps);
+    if (a.n > 0 && a.n <= 16384)
+        hipLaunchKernelGGL(rms_norm_row_kernel, dim3(a.rows), dim3(64), (size_t)a.n * 4, s, a.x, a.w, a.y, a.n, a.eps);
+    else
+        hipLaunchKernelGGL(rms_norm_kernel, dim3(blocksFor(a.rows)), dim3(256), 0, s, a.x, a.w, a.y, a.n, a.rows,
+                           a.eps);
     return fromHip(hipGetLastError(), "rms_norm");
 }
 

@@ -190,6 +190,22 @@ def test_second_k_half_is_added_at_once_unless_the_add_alone_reads_the_product(p
     assert names[i + 1:i + 5] == ["quantize_cols_k", "matmul_group", "vector_add", "add_norm_q8k_f"], names
 
 
+def test_masked_batch_attention_is_claimed_past_the_score_limit():
+    """A prompt whose score matrix would pass 2^24 values (32 heads x 1024 tokens x 1024 keys: BASELINE
+    config 5's prompt) is claimed when it runs on the masked matrix-core kernel, which keeps no scores;
+    without a mask (the four fa_* kernels and their score scratch) it is not."""
+    s = gg.LayerShape(n_embd=4096, n_head=32, n_head_kv=8, n_ff=1024, head_dim=128, kv_size=1024, neox=True,
+                      qk_norm=True)
+    g = gg.Graph()
+    gg.llama_layer(g, s, 1024, 1024)
+    names = kc.ggml_graph_plan(g.nodes, attn_tokens=1024)[0]
+    assert "attn_masked" in names
+    fa = next(x for x in g.nodes if x.op == kc.GGML_OP["flash_attn_ext"])
+    assert kc.ggml_supports_op(fa, attn_tokens=1024)
+    fa.src[3] = None
+    assert not kc.ggml_supports_op(fa, attn_tokens=1024)
+
+
 def test_matvec_cols_runs_one_matvec_per_column():
     g, _ = layer(N=3)
     names = plan(g, matvec_cols=1)

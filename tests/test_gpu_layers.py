@@ -173,6 +173,23 @@ def test_silu_mul_q8(per256):
     B.free()
 
 
+@pytest.mark.parametrize("n,rows", [(128, 40), (100, 3), (4096, 2), (20000, 2)])
+def test_rms_norm_rows_bit_exact(n, rows):
+    """rms_norm with one workgroup per row (rows up to 16384 values: a Qwen3 layer's per-head q / k norms),
+    past that one thread per row: both the reference's sequential sums, bit for bit; also in place."""
+    note(f"rms_norm n={n} rows={rows}")
+    x, w = kq.randn(n * rows, 60 + rows), kq.uniform(n, 61, 0.5, 1.5)
+    B = Bufs()
+    bx, bw, by = B.of(x), B.of(w), B.new(n * rows * 4)
+    want = np.zeros_like(x)
+    O.kco_rms_norm(x, w, want, n, rows, 1e-6)
+    kc.launch("rms_norm", kc.RmsNormArgs(bx.ptr, bw.ptr, by.ptr, n, rows, 1e-6))
+    assert np.array_equal(kq.bits(by.download(np.float32)), kq.bits(want))
+    kc.launch("rms_norm", kc.RmsNormArgs(bx.ptr, bw.ptr, bx.ptr, n, rows, 1e-6))  # y = x
+    assert np.array_equal(kq.bits(bx.download(np.float32)), kq.bits(want))
+    B.free()
+
+
 def test_elementwise_ops():
     n, rows = 256, 5
     x, w, u = kq.randn(n * rows, 6), kq.uniform(n, 7, 0.5, 1.5), kq.randn(n * rows, 8)
