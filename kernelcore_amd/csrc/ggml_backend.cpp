@@ -648,7 +648,27 @@ bool ropeFaOk(const T* const* nodes, int n, int i, const int (&at)[3], int* fa) 
     return true;
 }
 
-E ropeFlashAttn(Pass& p, const T* rq, const T* rk, const T* sk, const T* sv, const T* dst) {
+// (No reference counterpart.) nodes[i] = RMS_NORM of q's heads and its MUL by a D-value weight, the
+// same for k (Qwen3), each norm read by its MUL alone, then ROPE of those two MUL results, the cache
+// SET_ROWS and the one-token FLASH_ATTN_EXT as ropeFaOk takes them: the norms run in the attention's
+// prologue too (the MUL results still written). jr: the ROPE(q) index.
+bool normRopeFaOk(const T* const* nodes, int n, int i, int* jr, int (&at)[3], int* fa) {
+    static const int kNormMul[2] = {KC_GGML_OP_RMS_NORM, KC_GGML_OP_MUL};
+    if (i + 3 >= n || !canFuse(nodes, n, i, kNormMul, 2) || !canFuse(nodes, n, i + 2, kNormMul, 2)) return false;
+    const T *nq = nodes[i], *mq = nodes[i + 1], *nk = nodes[i + 2], *mk = nodes[i + 3];
+    if (mq->src[0] != nq || mk->src[0] != nk || !rowVectorOf(mq->src[1], nq) || !rowVectorOf(mk->src[1], nk)) return false;
+    const T *q0 = nq->src[0], *k0 = nk->src[0];
+    if (nk->ne[0] != nq->ne[0] || paramF32(nq, 0) != paramF32(nk, 0) || !f32c(q0) || !f32c(k0) || !f32c(mq) || !f32c(mk))
+        return false;
+    const int j = nextWork(nodes, n, i + 4);
+    if (j >= n || nodes[j]->op != KC_GGML_OP_ROPE || !computed(nodes[j]) || nodes[j]->src[0] != mq) return false;
+    if (!ropeKvOk(nodes, n, j, at) || nodes[at[0]]->src[0] != mk || !ropeFaOk(nodes, n, j, at, fa)) return false;
+    *jr = j;
+    return true;
+}
+
+E ropeFlashAttn(Pass& p, const T* rq, const T* rk, const T* sk, const T* sv, const T* dst,
+                const T* const* norms = nullptr) {
     const T* q = dst->src[0];
     const T* k = dst->src[1];
     const T* v = dst->src[2];
@@ -682,6 +702,19 @@ E ropeFlashAttn(Pass& p, const T* rq, const T* rk, const T* sk, const T* sv, con
                           static_cast<const int*>(rq->src[1]->data), static_cast<const int*>(sk->src[1]->data), ff,
                           std::log2(paramF32(rq, 5)), (rq->op_params[2] & KC_GGML_ROPE_TYPE_NEOX) != 0,
                           int(sk->nb[1] / 4), int(sv->nb[1] / 4), int(sk->ne[1]), int(row0)};
+    if (norms) {  // nodes: RMS_NORM q, MUL q, RMS_NORM k, MUL k
+        kcamd::FdRope rn = r;
+        rn.q = f32(norms[0]->src[0]);
+        rn.k = f32(norms[2]->src[0]);
+        rn.q_norm = f32(norms[1]->src[1]);
+        rn.k_norm = f32(norms[3]->src[1]);
+        rn.qn = f32w(norms[1]);
+        rn.kn = f32w(norms[3]);
+        rn.eps = paramF32(norms[0], 0);
+        rn.qk_norm = 1;
+        return direct(p, "norm_rope_flash_decode_q8",
+                      [&](hipStream_t s) { return kcamd::launchFlashDecode(a, s, slot, &rn); });
+    }
     return direct(p, "rope_flash_decode_q8", [&](hipStream_t s) { return kcamd::launchFlashDecode(a, s, slot, &r); });
 }
 
@@ -896,6 +929,13 @@ E walk(Pass& p, const T* const* nodes, int n) {
             }
             case KC_GGML_OP_ADD:
             case KC_GGML_OP_RMS_NORM: {
+                int jr = 0, at4[3], fa4 = 0;
+                if (node->op == KC_GGML_OP_RMS_NORM && kcamd::option("ggml_extra_fusions") != 1 &&
+                    normRopeFaOk(nodes, n, i, &jr, at4, &fa4)) {  // per-head norms into the attention's launch
+                    e = ropeFlashAttn(p, nodes[jr], nodes[at4[0]], nodes[at4[1]], nodes[at4[2]], nodes[fa4], nodes + i);
+                    i = fa4;
+                    break;
+                }
                 NormGroup ng;
                 if (node->op == KC_GGML_OP_RMS_NORM && kcamd::option("ggml_extra_fusions") != 1 &&
                     normGroupOk(nodes, n, i, ng)) {  // the norm in the group's launch

@@ -1042,6 +1042,7 @@ __global__ __launch_bounds__(256) void flash_decode_kernel(const float* __restri
         __shared__ float qs[G * D];
         __shared__ float kn[D];
         __shared__ float ffl[pairs];
+        __shared__ float nwl[2 * D], rn[G + 1];
         constexpr int NR = ((G + 2) * D + 255) / 256;
         float rv[NR];
 #pragma unroll
@@ -1052,6 +1053,8 @@ __global__ __launch_bounds__(256) void flash_decode_kernel(const float* __restri
                                                  : rp.v[(size_t)kvh * D + (x - (G + 1) * D)]);
         }
         const float ffv = rp.ff[tid % pairs];
+        const int tn = tid % (2 * D);
+        const float nwv = rp.qk_norm ? (tn < D ? rp.q_norm[tn] : rp.k_norm[tn - D]) : 0.0f;
         const int p = rp.pos[0], row = rp.idx[0];
         const bool stored = row >= 0 && row < rp.dst_rows;
         const int tv = row - rp.row0;
@@ -1061,7 +1064,26 @@ __global__ __launch_bounds__(256) void flash_decode_kernel(const float* __restri
         for (int r = 0; r < NR; ++r)
             if (tid + r * 256 < (G + 2) * D) raw[tid + r * 256] = rv[r];
         if (tid < pairs) ffl[tid] = ffv;
+        if (tid < 2 * D) nwl[tid] = nwv;
         __syncthreads();
+        if (rp.qk_norm) {  // rms_norm + MUL of each head (q heads 0 .. G - 1, k head G): sequential sums
+            if (tid <= G) {
+                float ss = 0.0f;
+                for (int j = 0; j < D; ++j) ss += raw[tid * D + j] * raw[tid * D + j];
+                rn[tid] = 1.0f / sqrtf(ss / (float)D + rp.eps);
+            }
+            __syncthreads();
+            for (int x = tid; x < (G + 1) * D; x += 256) {
+                const int h = x / D, e = x % D;
+                const float y = raw[x] * rn[h] * nwl[(h < G ? 0 : D) + e];
+                raw[x] = y;
+                if (c == 0) {
+                    if (h < G) rp.qn[(size_t)(kvh * G + h) * D + e] = y;
+                    else rp.kn[(size_t)kvh * D + e] = y;
+                }
+            }
+            __syncthreads();
+        }
         const int m1 = rp.neox ? 1 : 2, m2 = rp.neox ? pairs : 1;
         for (int x = tid; x < (G + 1) * pairs; x += 256) {
             const int h = x / pairs, j = x % pairs;

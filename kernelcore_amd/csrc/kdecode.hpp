@@ -98,6 +98,12 @@ struct FdRope {
     int k_row, v_row;  // cache row strides (32-bit words)
     int dst_rows;      // cache rows: a row index outside [0, dst_rows) is not stored
     int row0;          // the cache row of the attention's K / V view row 0 (the same for both)
+    // Qwen3's per-head RMS norms of q and k before RoPE (q, k above are then their inputs): weights
+    // [D], the normed q and k written as the MUL nodes' outputs (qn, kn; same layouts as q, k)
+    const float *q_norm, *k_norm;
+    float *qn, *kn;
+    float eps;
+    int qk_norm;
 };
 // flash_decode_f16 (kcFlashDecodeArgs): the split-context FLASH_ATTN_EXT for D 64 / 128, group <= 8.
 bool flashDecodeSupports(int D, int G);

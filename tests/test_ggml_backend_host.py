@@ -206,6 +206,28 @@ def test_masked_batch_attention_is_claimed_past_the_score_limit():
     assert not kc.ggml_supports_op(fa, attn_tokens=1024)
 
 
+@pytest.mark.parametrize("plant", [None, "norm_second_use", "other_eps", "rope_source"])
+def test_per_head_norms_enter_the_attention_only_when_they_feed_its_ropes(plant):
+    """Qwen3's per-head q / k RMS_NORM + MUL run in the one-token attention's prologue only when each
+    norm is read by its MUL alone, both take one eps, and the ROPEs read those MUL results."""
+    s = gg.LayerShape(n_embd=1024, n_head=8, n_head_kv=2, head_dim=128, neox=True, qk_norm=True)
+    g, t = gg.Graph(), None
+    t = gg.llama_layer(g, s, 1, 90)
+    norms = [x for x in g.nodes if x.op == kc.GGML_OP["rms_norm"] and x.ne[0] == 128]
+    if plant == "norm_second_use":
+        norms[0].uses = 2
+    elif plant == "other_eps":
+        norms[1].op_params[0] = norms[1].op_params[0] + 1
+    elif plant == "rope_source":
+        rope = next(x for x in g.nodes if x.op == kc.GGML_OP["rope"])
+        rope.src[0] = C.pointer(g.leaf("f32", [128, 8, 1]))
+    names = plan(g)
+    if plant is None:
+        assert names[:2] == ["decode_norm_matvec", "norm_rope_flash_decode_q8"], names
+    else:
+        assert "norm_rope_flash_decode_q8" not in names and "rms_norm" in names, names
+
+
 def test_matvec_cols_runs_one_matvec_per_column():
     g, _ = layer(N=3)
     names = plan(g, matvec_cols=1)

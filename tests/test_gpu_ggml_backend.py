@@ -62,6 +62,9 @@ class Layer:
         self.ffn_norm = kq.uniform(s.n_embd, seed + 11, 0.5, 1.5)
         self.put("attn_norm", self.attn_norm)
         self.put("ffn_norm", self.ffn_norm)
+        if s.qk_norm:  # Qwen3's per-head q / k norm weights
+            self.put("q_norm", kq.uniform(s.hd, seed + 15, 0.5, 1.5))
+            self.put("k_norm", kq.uniform(s.hd, seed + 16, 0.5, 1.5))
         pos = np.arange(p0, p0 + N, dtype=np.int32)
         self.pos = pos
         self.put("pos", pos)
@@ -271,8 +274,10 @@ def test_layer_graph_matches_the_oracle_node_by_node(case, graphs):
     L.free()
 
 
-@pytest.mark.parametrize("shape", [gg.LayerShape(), gg.LayerShape(n_embd=1024, neox=True, freq_factors=True)],
-                         ids=["llama", "neox-ff"])
+@pytest.mark.parametrize("shape", [gg.LayerShape(), gg.LayerShape(n_embd=1024, neox=True, freq_factors=True),
+                                   gg.LayerShape(n_embd=1024, n_head=8, n_head_kv=2, head_dim=128, neox=True,
+                                                 qk_norm=True)],
+                         ids=["llama", "neox-ff", "qwen3-qk-norm"])
 def test_fused_decode_matvecs_equal_one_launch_per_node(shape):
     """One input column: the norms inside the q / k / v and gate / up / SWIGLU launches, the o and
     down products with their residual ADDs, ROPE with the cache rows, the attention output
@@ -280,9 +285,12 @@ def test_fused_decode_matvecs_equal_one_launch_per_node(shape):
     attention, the two residual sums) equals the reference's one launch per node bit for bit."""
     L = Layer(shape, 1, 90, seed=808)
     names, _ = kc.ggml_graph_plan(L.g.nodes)
-    assert names == ["decode_norm_matvec", "rope_flash_decode_q8", "decode_matvec_add",
+    attn = "norm_rope_flash_decode_q8" if shape.qk_norm else "rope_flash_decode_q8"
+    assert names == ["decode_norm_matvec", attn, "decode_matvec_add",
                      "decode_norm_swiglu", "decode_matvec_add"]
     kept = ("q", "k", "v", "qr", "kr", "attn", "ffn_inp", "out")  # what both write
+    if shape.qk_norm:
+        kept += ("qn", "kn")  # the per-head norms' MUL results
     got = {}
     for opt in (1, 0):
         kc.set_option("ggml_extra_fusions", opt)
