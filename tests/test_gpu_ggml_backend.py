@@ -345,6 +345,37 @@ def test_batch_attention_with_an_irregular_mask(shape):
     L.free()
 
 
+def test_batch_attention_past_the_score_limit():
+    """A prompt whose score matrix passes 2^24 values (32 heads x 1024 tokens x 1024 keys, as BASELINE
+    config 5's prompt): claimed because it runs on the masked matrix-core kernel, which keeps no score
+    matrix; against the oracle on the GPU's own inputs (causal mask with a block of holes)."""
+    shape = gg.LayerShape(n_embd=2048, n_head=32, n_head_kv=8, head_dim=64, n_ff=1024, kv_size=1024)
+    N, p0 = 1024, 0
+    note("ggml attention past the score limit: 32 heads, 1024 tokens")
+    L = Layer(shape, N, p0, seed=929)
+    names, _ = kc.ggml_graph_plan(L.g.nodes, attn_tokens=N)
+    assert "attn_masked" in names
+    n_pad = L.t["mask"].ne[0]
+    m = L.mask.view(np.float16).reshape(N, n_pad).copy()
+    m[600:700, 100:164] = -np.inf
+    L.mask = m.reshape(-1).view(np.uint16)
+    L.put("mask", L.mask)
+    be = kc.GgmlBackend(graphs=0, attn_tokens=N)
+    be.compute(L.g.nodes)
+    kc.synchronize()
+    s = L.s
+    d = oracle.FaDims(H=s.n_head, T=L.n_kv, D=s.hd, group=s.n_head // s.n_head_kv, tp=(L.n_kv + 7) // 8 * 8,
+                      k_row=s.kv_dim // 2, k_head=s.hd // 2, v_row=s.kv_dim // 2, v_head=s.hd // 2, N=N,
+                      q_tok=s.hd * s.n_head, q_head=s.hd, m_row=n_pad // 2, has_mask=1, H_kv=s.n_head_kv)
+    assert s.n_head * N * d.tp >= 1 << 24
+    want = np.zeros(N * s.n_head * s.hd, np.float32)
+    O.kco_flash_attn_f16(L.get("qr", np.float32), L.get("k_cache", np.uint16), L.get("v_cache", np.uint16), L.mask,
+                         want, C.byref(d), np.float32(1.0 / s.hd ** 0.5))
+    assert kq.rel_diff(L.get("attn", np.float32), want) < 2e-6
+    be.close()
+    L.free()
+
+
 def test_kept_graph_is_launched_again_for_new_inputs():
     shape, N, p0 = gg.LayerShape(), 8, 100
     note(f"ggml graph reuse: N={N}, p0={p0}")
