@@ -363,7 +363,9 @@ E fusedNorm(Pass& p, const T* addNode, const T* norm, const T* mulNode) {
     const T* a = addNode ? addNode->src[0] : nullptr;
     const T* b = addNode ? addNode->src[1] : nullptr;
     const float* b2 = nullptr;
-    if (addNode) {
+    if (addNode && a == b) {  // x + x: both operands need the half, so it is added first
+        if (E e = settle(p, a); e != ok) return e;
+    } else if (addNode) {
         if (const float* h = takePending(p, a)) {
             std::swap(a, b);
             b2 = h;
