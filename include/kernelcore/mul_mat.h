@@ -13,8 +13,11 @@
  *     without matvec_cols, one matmul_{q4k,q6k}_q8[k]x{4,8} (x8 when tile == 8 and ncols > 4), else
  *     one matvec_{q4k,q6k}_q8 per column into dst + c * rows (mul_mat_impl, :555-589).
  * A recording keeps the quantized inputs it made (keyed by input pointer, ncols, k and slot kind),
- * so matrices that read the same input (q, k, v; gate, up) quantize it once, as the reference's
- * per-recording cache does; kcMulMatRecordingReset starts a new recording.
+ * so matrices that read the same input (q, k, v; gate, up) quantize it once; kcMulMatRecordingReset
+ * starts a new recording. The reference keys its per-recording cache by ggml tensor (:323); a caller
+ * here names an input by its pointer, so one that writes new values to an input within a recording
+ * (or reuses an input's memory for another tensor) resets the recording first. The ggml backend
+ * (ggml_backend.h) keys the same cache by tensor.
  *
  * Weights are what a backend buffer holds after its set_tensor: K-quant as the repacked stream
  * (repack_kquant, kcKquantStreamBytes bytes), F16 as ggml's row-major halves. Launches go to the

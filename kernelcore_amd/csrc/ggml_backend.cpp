@@ -21,10 +21,12 @@
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
+#include <iterator>
 #include <map>
 #include <new>
 #include <string>
 #include <unordered_map>
+#include <utility>
 #include <vector>
 
 #include "internal.hpp"
@@ -45,6 +47,7 @@ struct kcGgmlBackend_st {
     kcGraph_t graph = nullptr;   // the kept graph, the signature of its nodes, the scratch it points into
     std::vector<uint64_t> sig;
     unsigned graph_gen = 0;
+    unsigned graph_options = 0;  // the kernel options' generation the graph was recorded under
     long long graph_launches = 0;
     kcGgmlStats stats{};
 };
@@ -276,6 +279,18 @@ E marker(Pass& p, const char* m) {
 const float* f32(const T* t) { return static_cast<const float*>(t->data); }
 float* f32w(const T* t) { return static_cast<float*>(t->data); }
 
+// The tensor whose values t holds as a MUL_MAT reads them: t, or through RESHAPE / VIEW nodes that
+// keep its memory and its elements packed, the tensor they view. The quantized inputs are cached by
+// this key, as the reference caches them by tensor (:323): ggml's allocator gives a tensor's memory to
+// a later tensor once the first is dead, so a data pointer does not name one tensor's values.
+const T* keyOf(const T* t) {
+    while (t && (t->op == KC_GGML_OP_RESHAPE || t->op == KC_GGML_OP_VIEW) && t->src[0] &&
+           t->data == t->src[0]->data && nelements(t) == nelements(t->src[0]) && contiguous(t) &&
+           contiguous(t->src[0]))
+        t = t->src[0];
+    return t;
+}
+
 kcMulMatNode mulMatNode(const T* dst) {
     const T* w = dst->src[0];
     const T* x = dst->src[1];
@@ -284,12 +299,12 @@ kcMulMatNode mulMatNode(const T* dst) {
 
 E mulMat(Pass& p, const T* dst) {
     kcMulMatPlan plan{};
-    return kcamd::mulmat::mulMat(p.rec, mulMatNode(dst), plan);
+    return kcamd::mulmat::mulMat(p.rec, mulMatNode(dst), plan, keyOf(dst->src[1]));
 }
 
 E mulMatInput(Pass& p, const T* dst) {
     kcMulMatPlan plan{};
-    return kcamd::mulmat::mulMatInput(p.rec, mulMatNode(dst), plan);
+    return kcamd::mulmat::mulMatInput(p.rec, mulMatNode(dst), plan, keyOf(dst->src[1]));
 }
 
 // RMS_NORM, with the weight of a following MUL when given (rms_norm, :597-606)
@@ -386,7 +401,7 @@ E fusedNorm(Pass& p, const T* addNode, const T* norm, const T* mulNode) {
     const kcMulMatNormNode nn{addNode ? f32(a) : nullptr, addNode ? f32(b) : nullptr, f32w(x), f32(mulNode->src[1]),
                               f32w(mulNode), int(n), int(rows), paramF32(norm, 0)};
     kcMulMatPlan plan{};
-    return kcamd::mulmat::fusedNorm(p.rec, nn, plan, b2);
+    return kcamd::mulmat::fusedNorm(p.rec, nn, plan, b2, mulNode);
 }
 
 // SWIGLU with the result also quantized for the down projection (:533-545); n % 256 == 0.
@@ -395,7 +410,7 @@ E fusedSwiglu(Pass& p, const T* dst) {
     if (n * cols >= (int64_t(1) << 24)) return swiglu(p, dst);
     const kcMulMatSwigluNode sn{f32(dst->src[0]), f32(dst->src[1]), f32w(dst), int(n), int(cols)};
     kcMulMatPlan plan{};
-    return kcamd::mulmat::fusedSwiglu(p.rec, sn, plan);
+    return kcamd::mulmat::fusedSwiglu(p.rec, sn, plan, dst);
 }
 
 // ---- fusions beyond the reference's --------------------------------------------------------------
@@ -429,6 +444,36 @@ int nextWork(const T* const* nodes, int n, int j) {  // the next node with work 
     return j;
 }
 
+// The bytes from t's data pointer to the end of its last element (0 when it has none).
+size_t spanBytes(const T* t) {
+    int64_t blck = 1;
+    const size_t es = typeSize(t->type, &blck);
+    if (!es || empty(t)) return 0;
+    size_t end = es + size_t(t->ne[0] / blck - 1) * t->nb[0];
+    for (int d = 1; d < 4; ++d) end += size_t(t->ne[d] - 1) * t->nb[d];
+    return end;
+}
+bool overlaps(const T* a, const T* b) {
+    if (!a || !b) return false;
+    const char* pa = static_cast<const char*>(a->data);
+    const char* pb = static_cast<const char*>(b->data);
+    const size_t na = spanBytes(a), nb = spanBytes(b);
+    return na && nb && pa < pb + nb && pb < pa + na;
+}
+// Whether anything outside fused[0..nf) needs t's values: t is a graph output, or a node reads it
+// (itself or through no-op views of t) that is not one of them.
+bool readBeyond(const T* t, const T* const* nodes, int n, const T* const* fused, int nf) {
+    if (t->output) return true;
+    for (int j = 0; j < n; ++j) {
+        const T* r = nodes[j];
+        if (std::find(std::begin(r->src), std::end(r->src), t) == std::end(r->src)) continue;
+        if (std::find(fused, fused + nf, r) != fused + nf) continue;
+        if (noop(r) && !readBeyond(r, nodes, n, fused, nf)) continue;
+        return true;
+    }
+    return false;
+}
+
 // MUL_MATs mm[0..g) of the one-column input x through one decode matvec with epilogue epi
 // (prologue pro: the input's per-32 slot, or the norm of the row the input is the norm of)
 bool decodeMatvecOk(const T* x, const T* const* mm, int g, int epi, int tpw, int pro = kcamd::kProSlot) {
@@ -443,7 +488,7 @@ E slotArgs(Pass& p, const T* mm0, kcamd::DmvArgs& a) {
     const T* x = mm0->src[1];
     const int k = int(x->ne[0]);
     if (E e = mulMatInput(p, mm0); e != ok) return e;
-    int* q = kcamd::mulmat::inputSlot(p.rec, f32(x), 1, k, false);
+    int* q = kcamd::mulmat::inputSlot(p.rec, keyOf(x), 1, k, false);
     if (!q) return kc::Error::InternalError;
     a.k = k;
     a.xq = q;
@@ -550,7 +595,7 @@ E decodeNormGroup(Pass& p, const T* norm, const T* mul, const T* const* mm, cons
         a.p0 = dmvPart(mm[0], nullptr);
         a.p1 = dmvPart(mm[1], nullptr);
         a.nparts = 2;
-        if (E e = kcamd::mulmat::outputSlot(p.rec, f32(mm[2]), a.p0.rows, 1, false, &a.qout); e != ok) return e;
+        if (E e = kcamd::mulmat::outputSlot(p.rec, mm[2], a.p0.rows, 1, false, &a.qout); e != ok) return e;
         return direct(p, "decode_norm_swiglu", [&](hipStream_t s) {
             return kcamd::launchDecodeMatvec(kcamd::kProNorm, kcamd::kEpiSwiglu, a, s);
         });
@@ -570,7 +615,7 @@ E decodeSwiglu(Pass& p, const T* ga, const T* up, const T* glu) {
     a.p1 = dmvPart(up, nullptr);
     a.nparts = 2;
     a.tpw = 2;
-    if (E e = kcamd::mulmat::outputSlot(p.rec, f32(glu), a.p0.rows, 1, false, &a.qout); e != ok) return e;
+    if (E e = kcamd::mulmat::outputSlot(p.rec, glu, a.p0.rows, 1, false, &a.qout); e != ok) return e;
     return direct(p, "decode_swiglu", [&](hipStream_t s) {
         return kcamd::launchDecodeMatvec(kcamd::kProSlot, kcamd::kEpiSwiglu, a, s);
     });
@@ -619,7 +664,17 @@ E ropeKv(Pass& p, const T* rq, const T* rk, const T* sk, const T* sv) {
 // SET_ROWS write (rows as the caches' rows from one common row, heads D halves apart), taken by the
 // split-context kernel with its per-32 slot: then the four nodes run as that kernel's prologue.
 // fa: the attention node's index.
-bool ropeFaOk(const T* const* nodes, int n, int i, const int (&at)[3], int* fa) {
+// The fused attention's intermediate outputs that it writes (the ROPE results; Qwen3's per-head
+// norm MUL results): those something outside the fused nodes reads.
+struct FaWrites {
+    bool qr = false, kr = false, qn = false, kn = false;
+};
+// norms (Qwen3): RMS_NORM q, MUL q, RMS_NORM k, MUL k before the ROPEs (their MUL results are what
+// the ROPEs read). The kernel's chunk-0 workgroups write the outputs of *w while the others still
+// read the raw q, k and v; ggml's allocator runs ROPE, RMS_NORM and MUL in place, so a written output
+// that overlaps one of those sources refuses the fusion.
+bool ropeFaOk(const T* const* nodes, int n, int i, const int (&at)[3], int* fa, FaWrites* w,
+              const T* const* norms = nullptr) {
     const T *rq = nodes[i], *rk = nodes[at[0]], *sk = nodes[at[1]], *sv = nodes[at[2]];
     const int f = nextWork(nodes, n, at[2] + 1);
     if (f >= n) return false;
@@ -646,7 +701,26 @@ bool ropeFaOk(const T* const* nodes, int n, int i, const int (&at)[3], int* fa) 
     // what flashAttn takes for one token with its slot
     const int D = int(hd), G = int(nh / nkv);
     if (!kcamd::flashDecodeSupports(D, G) || (nh * hd) % 256 || q->nb[1] % 16) return false;
+    const T* fused[9] = {rq, rk, sk, sv, node};
+    int nf = 5;
+    if (norms)
+        for (int j = 0; j < 4; ++j) fused[nf++] = norms[j];
+    const T* srcs[3] = {norms ? norms[0]->src[0] : q0, norms ? norms[2]->src[0] : k0, v0};
+    FaWrites wr;
+    wr.qr = readBeyond(rq, nodes, n, fused, nf);
+    wr.kr = readBeyond(rk, nodes, n, fused, nf);
+    if (norms) {
+        wr.qn = readBeyond(norms[1], nodes, n, fused, nf);
+        wr.kn = readBeyond(norms[3], nodes, n, fused, nf);
+    }
+    const std::pair<bool, const T*> outs[4] = {{wr.qr, rq}, {wr.kr, rk}, {wr.qn, norms ? norms[1] : nullptr},
+                                               {wr.kn, norms ? norms[3] : nullptr}};
+    for (const auto& [written, o] : outs)
+        if (written)
+            for (const T* src : srcs)
+                if (overlaps(o, src)) return false;
     *fa = f;
+    *w = wr;
     return true;
 }
 
@@ -654,7 +728,7 @@ bool ropeFaOk(const T* const* nodes, int n, int i, const int (&at)[3], int* fa) 
 // same for k (Qwen3), each norm read by its MUL alone, then ROPE of those two MUL results, the cache
 // SET_ROWS and the one-token FLASH_ATTN_EXT as ropeFaOk takes them: the norms run in the attention's
 // prologue too (the MUL results still written). jr: the ROPE(q) index.
-bool normRopeFaOk(const T* const* nodes, int n, int i, int* jr, int (&at)[3], int* fa) {
+bool normRopeFaOk(const T* const* nodes, int n, int i, int* jr, int (&at)[3], int* fa, FaWrites* w) {
     static const int kNormMul[2] = {KC_GGML_OP_RMS_NORM, KC_GGML_OP_MUL};
     if (i + 3 >= n || !canFuse(nodes, n, i, kNormMul, 2) || !canFuse(nodes, n, i + 2, kNormMul, 2)) return false;
     const T *nq = nodes[i], *mq = nodes[i + 1], *nk = nodes[i + 2], *mk = nodes[i + 3];
@@ -664,12 +738,13 @@ bool normRopeFaOk(const T* const* nodes, int n, int i, int* jr, int (&at)[3], in
         return false;
     const int j = nextWork(nodes, n, i + 4);
     if (j >= n || nodes[j]->op != KC_GGML_OP_ROPE || !computed(nodes[j]) || nodes[j]->src[0] != mq) return false;
-    if (!ropeKvOk(nodes, n, j, at) || nodes[at[0]]->src[0] != mk || !ropeFaOk(nodes, n, j, at, fa)) return false;
+    if (!ropeKvOk(nodes, n, j, at) || nodes[at[0]]->src[0] != mk || !ropeFaOk(nodes, n, j, at, fa, w, nodes + i))
+        return false;
     *jr = j;
     return true;
 }
 
-E ropeFlashAttn(Pass& p, const T* rq, const T* rk, const T* sk, const T* sv, const T* dst,
+E ropeFlashAttn(Pass& p, const T* rq, const T* rk, const T* sk, const T* sv, const T* dst, const FaWrites& w,
                 const T* const* norms = nullptr) {
     const T* q = dst->src[0];
     const T* k = dst->src[1];
@@ -694,12 +769,13 @@ E ropeFlashAttn(Pass& p, const T* rq, const T* rk, const T* sk, const T* sv, con
     int* part = nullptr;
     if (E e = kcamd::mulmat::take(p.rec, kcamd::flashDecodePartFloats(d), &part); e != ok) return e;
     int* slot = nullptr;
-    if (E e = kcamd::mulmat::outputSlot(p.rec, f32(dst), d.H * d.D, 1, false, &slot); e != ok) return e;
+    if (E e = kcamd::mulmat::outputSlot(p.rec, dst, d.H * d.D, 1, false, &slot); e != ok) return e;
     const kcFlashDecodeArgs a{f32(q), static_cast<const int*>(k->data), static_cast<const int*>(v->data),
                               mask ? static_cast<const int*>(mask->data) : nullptr, f32w(dst),
                               reinterpret_cast<float*>(part), nullptr, d, paramF32(dst, 0)};
     const ptrdiff_t row0 = (static_cast<const char*>(k->data) - static_cast<const char*>(sk->data)) / ptrdiff_t(sk->nb[1]);
-    const kcamd::FdRope r{f32(rq->src[0]), f32(rk->src[0]), f32(sv->src[0]), f32w(rq), f32w(rk),
+    const kcamd::FdRope r{f32(rq->src[0]), f32(rk->src[0]), f32(sv->src[0]), w.qr ? f32w(rq) : nullptr,
+                          w.kr ? f32w(rk) : nullptr,
                           static_cast<int*>(sk->data), static_cast<int*>(sv->data),
                           static_cast<const int*>(rq->src[1]->data), static_cast<const int*>(sk->src[1]->data), ff,
                           std::log2(paramF32(rq, 5)), (rq->op_params[2] & KC_GGML_ROPE_TYPE_NEOX) != 0,
@@ -710,8 +786,8 @@ E ropeFlashAttn(Pass& p, const T* rq, const T* rk, const T* sk, const T* sv, con
         rn.k = f32(norms[2]->src[0]);
         rn.q_norm = f32(norms[1]->src[1]);
         rn.k_norm = f32(norms[3]->src[1]);
-        rn.qn = f32w(norms[1]);
-        rn.kn = f32w(norms[3]);
+        rn.qn = w.qn ? f32w(norms[1]) : nullptr;
+        rn.kn = w.kn ? f32w(norms[3]) : nullptr;
         rn.eps = paramF32(norms[0], 0);
         rn.qk_norm = 1;
         return direct(p, "norm_rope_flash_decode_q8",
@@ -762,7 +838,7 @@ E flashAttn(Pass& p, const T* dst) {
         if (d.N == 1 && (d.H * d.D) % 256 == 0 && kcamd::option("ggml_extra_fusions") != 1) {
             // one token: the output's per-32 slot too, for the MUL_MAT that reads it (the o projection)
             int* slot = nullptr;
-            if (E e = kcamd::mulmat::outputSlot(p.rec, f32(dst), d.H * d.D, 1, false, &slot); e != ok) return e;
+            if (E e = kcamd::mulmat::outputSlot(p.rec, dst, d.H * d.D, 1, false, &slot); e != ok) return e;
             return direct(p, "flash_decode_q8", [&](hipStream_t s) { return kcamd::launchFlashDecode(a, s, slot); });
         }
         return launch(p, "flash_decode_f16", &a);
@@ -821,9 +897,9 @@ E batchGroup(Pass& p, const T* const* mm, int g) {
     if (E e = mulMatInput(p, mm[0]); e != ok) return e;  // quantize_cols_k, once per input
     const T* x = mm[0]->src[1];
     const int k = int(mm[0]->src[0]->ne[0]), ncols = int(nrows(x));
-    const int* q = p.rec.dry ? nullptr : kcamd::mulmat::inputSlot(p.rec, f32(x), ncols, k, true);
+    const int* q = p.rec.dry ? nullptr : kcamd::mulmat::inputSlot(p.rec, keyOf(x), ncols, k, true);
     if (!p.rec.dry && !q) return kc::Error::InternalError;
-    const kcamd::ActF16* pre = kcamd::mulmat::inputAct(p.rec, f32(x), ncols, k);
+    const kcamd::ActF16* pre = kcamd::mulmat::inputAct(p.rec, keyOf(x), ncols, k);
     kcamd::MmPart parts[3];
     for (int j = 0; j < g; ++j) {
         const T* w = mm[j]->src[0];
@@ -932,9 +1008,11 @@ E walk(Pass& p, const T* const* nodes, int n) {
             case KC_GGML_OP_ADD:
             case KC_GGML_OP_RMS_NORM: {
                 int jr = 0, at4[3], fa4 = 0;
+                FaWrites w4;
                 if (node->op == KC_GGML_OP_RMS_NORM && kcamd::option("ggml_extra_fusions") != 1 &&
-                    normRopeFaOk(nodes, n, i, &jr, at4, &fa4)) {  // per-head norms into the attention's launch
-                    e = ropeFlashAttn(p, nodes[jr], nodes[at4[0]], nodes[at4[1]], nodes[at4[2]], nodes[fa4], nodes + i);
+                    normRopeFaOk(nodes, n, i, &jr, at4, &fa4, &w4)) {  // per-head norms into the attention's launch
+                    e = ropeFlashAttn(p, nodes[jr], nodes[at4[0]], nodes[at4[1]], nodes[at4[2]], nodes[fa4], w4,
+                                      nodes + i);
                     i = fa4;
                     break;
                 }
@@ -978,9 +1056,10 @@ E walk(Pass& p, const T* const* nodes, int n) {
             case KC_GGML_OP_ROPE: {
                 int at[3];
                 int fa = 0;
+                FaWrites w;
                 if (kcamd::option("ggml_extra_fusions") != 1 && ropeKvOk(nodes, n, i, at)) {
-                    if (ropeFaOk(nodes, n, i, at, &fa)) {  // and the attention they feed: one launch
-                        e = ropeFlashAttn(p, node, nodes[at[0]], nodes[at[1]], nodes[at[2]], nodes[fa]);
+                    if (ropeFaOk(nodes, n, i, at, &fa, &w)) {  // and the attention they feed: one launch
+                        e = ropeFlashAttn(p, node, nodes[at[0]], nodes[at[1]], nodes[at[2]], nodes[fa], w);
                         i = fa;
                     } else {
                         e = ropeKv(p, node, nodes[at[0]], nodes[at[1]], nodes[at[2]]);
@@ -1122,10 +1201,11 @@ void dropGraph(kcGgmlBackend_st& be) {
 E compute(kcGgmlBackend_st& be, const T* const* nodes, int n) {
     if (E e = checkNodes(be.cfg, nodes, n); e != ok) return e;
     const bool graphs = be.cfg.graphs != 0;
+    const unsigned options = kcamd::optionsGeneration();  // read before the walk reads any option
     std::vector<uint64_t> sig;
     if (graphs) {
         signature(nodes, n, sig);
-        if (be.graph && be.graph_gen == be.rec.gen && sig == be.sig) {  // the kept graph again
+        if (be.graph && be.graph_gen == be.rec.gen && be.graph_options == options && sig == be.sig) {  // the kept graph again
             if (E e = kcGraphLaunch(be.graph, be.stream); e != ok) return e;
             if (E e = kcStreamSynchronize(be.stream); e != ok) return e;
             ++be.stats.computes;
@@ -1171,6 +1251,7 @@ E compute(kcGgmlBackend_st& be, const T* const* nodes, int n) {
         be.graph = g;
         be.sig = std::move(sig);
         be.graph_gen = be.rec.gen;
+        be.graph_options = options;
         be.graph_launches = pl.launches;
         ++be.stats.graphs_recorded;
         if (E s = kcStreamSynchronize(be.stream); s != ok) return s;

@@ -32,6 +32,8 @@ void* streamScratch(void* stream, size_t bytes);
 
 // Launch options (kcSetKernelOption).
 int option(const char* name);
+// Changes with every kcSetKernelOption call: work recorded under other options (a kept graph) is stale.
+unsigned optionsGeneration();
 
 // The built-in kernels, registered by kcInit.
 const kcKernelEntry* builtinKernels(size_t* count);

@@ -1003,7 +1003,9 @@ __global__ __launch_bounds__(64) void attn_merge_wave_kernel(AttnDecodeArgs a) {
 // maximum. A chunk whose positions are all masked contributes nothing.
 // RP: the ROPE / SET_ROWS prologue (FdRope; one query token): the raw q of the G heads and k, v of
 // KV head g into LDS, RoPE as rope_kv_rows_kernel computes it (the same expressions, so the same
-// bits), the roped q and k written by the workgroups of chunk 0, the fp16 cache row of head g
+// bits), the roped q and k written by the workgroups of chunk 0 (where rp.qr / rp.kr are given:
+// the other chunks read the raw q and k meanwhile, so these outputs must not overlap them), the fp16
+// cache row of head g
 // stored by the workgroup whose chunk holds it (chunk 0's when the view does not hold it), and
 // that row read from registers by the workgroup that holds it: no workgroup reads a row another
 // one writes.
@@ -1078,8 +1080,11 @@ __global__ __launch_bounds__(256) void flash_decode_kernel(const float* __restri
                 const float y = raw[x] * rn[h] * nwl[(h < G ? 0 : D) + e];
                 raw[x] = y;
                 if (c == 0) {
-                    if (h < G) rp.qn[(size_t)(kvh * G + h) * D + e] = y;
-                    else rp.kn[(size_t)kvh * D + e] = y;
+                    if (h < G) {
+                        if (rp.qn) rp.qn[(size_t)(kvh * G + h) * D + e] = y;
+                    } else if (rp.kn) {
+                        rp.kn[(size_t)kvh * D + e] = y;
+                    }
                 }
             }
             __syncthreads();
@@ -1095,14 +1100,14 @@ __global__ __launch_bounds__(256) void flash_decode_kernel(const float* __restri
             if (h < G) {
                 qs[h * D + o] = y0;
                 qs[h * D + o + m2] = y1;
-                if (c == 0) {
+                if (c == 0 && rp.qr) {
                     rp.qr[(size_t)(kvh * G + h) * D + o] = y0;
                     rp.qr[(size_t)(kvh * G + h) * D + o + m2] = y1;
                 }
             } else {
                 kn[o] = y0;
                 kn[o + m2] = y1;
-                if (c == 0) {
+                if (c == 0 && rp.kr) {
                     rp.kr[(size_t)kvh * D + o] = y0;
                     rp.kr[(size_t)kvh * D + o + m2] = y1;
                 }

@@ -88,7 +88,9 @@ int launchAttnDecode(AttnDecodeArgs a, int D, int Hkv, int max_ctx, hipStream_t 
 // whose chunk holds it, and the roped q and k are written as the ROPE nodes' outputs.
 struct FdRope {
     const float *q, *k, *v;  // one token, before RoPE: q [H][D], k [Hkv][D] contiguous; v [Hkv][D]
-    float *qr, *kr;          // the ROPE outputs (same layouts as q, k)
+    float *qr, *kr;          // the ROPE outputs (same layouts as q, k); null: not written. The
+                             // workgroups of chunk 0 write them while others still read q, k, v,
+                             // so they must not overlap those (qn, kn below likewise)
     int *kc, *vc;            // the caches (SET_ROWS destinations): fp16 rows k_row / v_row words apart
     const int* pos;          // ROPE positions (int32; pos[0])
     const int* idx;          // SET_ROWS row (int64; its low word)
@@ -99,7 +101,8 @@ struct FdRope {
     int dst_rows;      // cache rows: a row index outside [0, dst_rows) is not stored
     int row0;          // the cache row of the attention's K / V view row 0 (the same for both)
     // Qwen3's per-head RMS norms of q and k before RoPE (q, k above are then their inputs): weights
-    // [D], the normed q and k written as the MUL nodes' outputs (qn, kn; same layouts as q, k)
+    // [D], the normed q and k written as the MUL nodes' outputs (qn, kn; same layouts as q, k; null:
+    // not written)
     const float *q_norm, *k_norm;
     float *qn, *kn;
     float eps;

@@ -87,10 +87,11 @@ bool wantAct(const kcMulMatRecording_st& r, long long ncols, int k, bool k256) {
 size_t actOffset(size_t ints) { return (ints + 15) / 16 * 16; }
 size_t actInts(int ncols, int k) { return (kcamd::actF16Bytes(ncols, k) + 3) / 4; }
 
-// The 8-bit form of the node's input, made once per recording.
-E quantizedInput(kcMulMatRecording_st& r, const kcMulMatNode& n, bool k256, int** q, kcMulMatPlan& plan) {
+// The 8-bit form of the node's input, made once per recording (found again by key).
+E quantizedInput(kcMulMatRecording_st& r, const kcMulMatNode& n, bool k256, int** q, kcMulMatPlan& plan,
+                 const void* key) {
     for (const auto& in : r.inputs)
-        if (in.x == n.x && in.ncols == n.ncols && in.k == n.k && in.k256 == k256) {
+        if (in.key == key && in.ncols == n.ncols && in.k == n.k && in.k256 == k256) {
             *q = in.q;
             plan.input_reused = 1;
             return ok;
@@ -110,7 +111,7 @@ E quantizedInput(kcMulMatRecording_st& r, const kcMulMatNode& n, bool k256, int*
                 return kcamd::launchQuantizeColsK(n.x, base, n.k, int(n.ncols), s, &ao);
             }, plan); e != ok)
             return e;
-        r.inputs.push_back({n.x, n.ncols, n.k, k256, base, ao, true});
+        r.inputs.push_back({key, n.ncols, n.k, k256, base, ao, true});
         *q = base;
         return ok;
     }
@@ -131,7 +132,7 @@ E quantizedInput(kcMulMatRecording_st& r, const kcMulMatNode& n, bool k256, int*
             if (E e = launch(r, "quantize_q8x4", &a, plan); e != ok) return e;
         }
     }
-    r.inputs.push_back({n.x, n.ncols, n.k, k256, base});
+    r.inputs.push_back({key, n.ncols, n.k, k256, base});
     *q = base;
     return ok;
 }
@@ -139,20 +140,22 @@ E quantizedInput(kcMulMatRecording_st& r, const kcMulMatNode& n, bool k256, int*
 // batch_k256: batches read activations scaled per 256 values unless matvec_cols or q8k = 0
 bool batchK256(const kcMulMatRecording_st& r, long long ncols) { return ncols > 1 && !r.cfg.matvec_cols && r.cfg.q8k; }
 
-// Slots for the 8-bit form of y (ncols columns of k values) plus `extra` ints, registered under y
-// so that the MUL_MATs reading y find them (quantized_slots, :451-467).
-E registeredSlots(kcMulMatRecording_st& r, const float* y, int k, long long ncols, bool k256, size_t extra, int** q) {
+// Slots for the 8-bit form of an output (ncols columns of k values) plus `extra` ints, registered
+// under its key so that the MUL_MATs reading it find them (quantized_slots, :451-467).
+E registeredSlots(kcMulMatRecording_st& r, const void* key, int k, long long ncols, bool k256, size_t extra,
+                  int** q) {
     if (E e = kcamd::mulmat::take(r, slotInts(k, k256) * size_t(ncols) + extra, q); e != ok) return e;
-    for (auto it = r.inputs.begin(); it != r.inputs.end(); ++it)  // y rewritten: older slots of it are stale
-        if (it->x == y && it->ncols == ncols && it->k == k && it->k256 == k256) {
+    for (auto it = r.inputs.begin(); it != r.inputs.end(); ++it)  // rewritten: older slots of it are stale
+        if (it->key == key && it->ncols == ncols && it->k == k && it->k256 == k256) {
             r.inputs.erase(it);
             break;
         }
-    r.inputs.push_back({y, ncols, k, k256, *q});
+    r.inputs.push_back({key, ncols, k, k256, *q});
     return ok;
 }
 
-E fusedNormImpl(kcMulMatRecording_st& r, const kcMulMatNormNode& n, kcMulMatPlan& plan, const float* b2) {
+E fusedNormImpl(kcMulMatRecording_st& r, const kcMulMatNormNode& n, kcMulMatPlan& plan, const float* b2,
+                const void* key) {
     if (!n.x || !n.w || !n.y || (n.a != nullptr) != (n.b != nullptr)) return bad("norm: null x, w or y, or one of a / b");
     if (n.n <= 0 || n.n % 256 || n.rows <= 0 || (long long)n.n * n.rows >= (1 << 24))
         return bad("norm: n must be a positive multiple of 256, rows positive, n * rows < 2^24");
@@ -165,8 +168,8 @@ E fusedNormImpl(kcMulMatRecording_st& r, const kcMulMatNormNode& n, kcMulMatPlan
     if (b2 && (!one || !n.a)) return bad("norm: a second K half needs an ADD and the one-kernel per-256 norm");
     const bool act = one && wantAct(r, n.rows, n.n, k256);
     int* qk = nullptr;
-    if (E e = registeredSlots(r, n.y, n.n, n.rows, k256, act ? actOffset(off + sums) - off + actInts(n.rows, n.n) : sums,
-                              &qk);
+    if (E e = registeredSlots(r, key ? key : n.y, n.n, n.rows, k256,
+                              act ? actOffset(off + sums) - off + actInts(n.rows, n.n) : sums, &qk);
         e != ok)
         return e;
     int* q = qk + off;
@@ -204,7 +207,7 @@ E fusedNormImpl(kcMulMatRecording_st& r, const kcMulMatNormNode& n, kcMulMatPlan
     return launch(r, kernel, &a, plan);
 }
 
-E fusedSwigluImpl(kcMulMatRecording_st& r, const kcMulMatSwigluNode& n, kcMulMatPlan& plan) {
+E fusedSwigluImpl(kcMulMatRecording_st& r, const kcMulMatSwigluNode& n, kcMulMatPlan& plan, const void* key) {
     if (!n.g || !n.u || !n.y) return bad("swiglu: null g, u or y");
     if (n.n <= 0 || n.n % 256 || n.cols <= 0 || (long long)n.n * n.cols >= (1 << 24))
         return bad("swiglu: n must be a positive multiple of 256, cols positive, n * cols < 2^24");
@@ -213,7 +216,8 @@ E fusedSwigluImpl(kcMulMatRecording_st& r, const kcMulMatSwigluNode& n, kcMulMat
     int* q = nullptr;
     const bool act = wantAct(r, n.cols, n.n, k256);
     const size_t ints = slotInts(n.n, k256) * size_t(n.cols);
-    if (E e = registeredSlots(r, n.y, n.n, n.cols, k256, act ? actOffset(ints) - ints + actInts(n.cols, n.n) : 0, &q);
+    if (E e = registeredSlots(r, key ? key : n.y, n.n, n.cols, k256,
+                              act ? actOffset(ints) - ints + actInts(n.cols, n.n) : 0, &q);
         e != ok)
         return e;
     const kcSiluMulQ8FArgs a{n.g, n.u, n.y, q, nullptr, n.n, n.cols};
@@ -244,7 +248,7 @@ E validate(const kcMulMatNode& n) {
     return ok;
 }
 
-E mulMatImpl(kcMulMatRecording_st& r, const kcMulMatNode& n, kcMulMatPlan& plan) {
+E mulMatImpl(kcMulMatRecording_st& r, const kcMulMatNode& n, kcMulMatPlan& plan, const void* key) {
     if (E e = validate(n); e != ok) return e;
     const int ncols = int(n.ncols);
     if (n.wtype == KC_QTYPE_F16) {  // f32 activations as they are
@@ -257,7 +261,7 @@ E mulMatImpl(kcMulMatRecording_st& r, const kcMulMatNode& n, kcMulMatPlan& plan)
     const bool k256 = batchK256(r, n.ncols) && contiguous;
     plan.k256 = k256;
     int* base = nullptr;
-    if (E e = quantizedInput(r, n, k256, &base, plan); e != ok) return e;
+    if (E e = quantizedInput(r, n, k256, &base, plan, key ? key : n.x); e != ok) return e;
     if (n.ncols > 1 && !r.cfg.matvec_cols) {  // a batch: one matmul (weights read once per 4 or 8 columns)
         const bool x8 = r.cfg.tile == 8 && n.ncols > 4;
         const char* kernel = k256 ? (x8 ? (q4 ? "matmul_q4k_q8kx8" : "matmul_q6k_q8kx8")
@@ -320,21 +324,21 @@ kcError_t take(kcMulMatRecording_st& r, size_t ints, int** out) noexcept {
     return ok;
 }
 
-int* inputSlot(const kcMulMatRecording_st& r, const float* x, long long ncols, int k, bool k256) noexcept {
+int* inputSlot(const kcMulMatRecording_st& r, const void* key, long long ncols, int k, bool k256) noexcept {
     for (const auto& in : r.inputs)
-        if (in.x == x && in.ncols == ncols && in.k == k && in.k256 == k256) return in.q;
+        if (in.key == key && in.ncols == ncols && in.k == k && in.k256 == k256) return in.q;
     return nullptr;
 }
 
-const kcamd::ActF16* inputAct(const kcMulMatRecording_st& r, const float* x, long long ncols, int k) noexcept {
+const kcamd::ActF16* inputAct(const kcMulMatRecording_st& r, const void* key, long long ncols, int k) noexcept {
     for (const auto& in : r.inputs)
-        if (in.x == x && in.ncols == ncols && in.k == k && in.k256) return in.has_act ? &in.act : nullptr;
+        if (in.key == key && in.ncols == ncols && in.k == k && in.k256) return in.has_act ? &in.act : nullptr;
     return nullptr;
 }
 
-kcError_t outputSlot(kcMulMatRecording_st& r, const float* y, int k, long long ncols, bool k256, int** q) noexcept {
+kcError_t outputSlot(kcMulMatRecording_st& r, const void* key, int k, long long ncols, bool k256, int** q) noexcept {
     try {
-        return registeredSlots(r, y, k, ncols, k256, 0, q);
+        return registeredSlots(r, key, k, ncols, k256, 0, q);
     } catch (...) {
         return kc::Error::OutOfMemory;
     }
@@ -351,21 +355,21 @@ kcError_t launch(kcMulMatRecording_st& r, const char* kernel, const void* args) 
     return r.dry ? ok : kcLaunchKernel(kernel, args, r.stream);
 }
 
-kcError_t mulMat(kcMulMatRecording_st& r, const kcMulMatNode& n, kcMulMatPlan& plan) noexcept {
+kcError_t mulMat(kcMulMatRecording_st& r, const kcMulMatNode& n, kcMulMatPlan& plan, const void* key) noexcept {
     try {
-        return mulMatImpl(r, n, plan);
+        return mulMatImpl(r, n, plan, key);
     } catch (...) {
         return kc::Error::OutOfMemory;
     }
 }
 
-kcError_t mulMatInput(kcMulMatRecording_st& r, const kcMulMatNode& n, kcMulMatPlan& plan) noexcept {
+kcError_t mulMatInput(kcMulMatRecording_st& r, const kcMulMatNode& n, kcMulMatPlan& plan, const void* key) noexcept {
     if (E e = validate(n); e != ok) return e;
     if (n.wtype == KC_QTYPE_F16) return ok;
     const bool k256 = batchK256(r, n.ncols) && n.x_col_bytes == size_t(n.k) * sizeof(float);
     int* q = nullptr;
     try {
-        return quantizedInput(r, n, k256, &q, plan);
+        return quantizedInput(r, n, k256, &q, plan, key ? key : n.x);
     } catch (...) {
         return kc::Error::OutOfMemory;
     }
@@ -375,17 +379,19 @@ bool fusesHalf(const kcMulMatRecording_st& r, int n) noexcept {
     return n > 0 && n % 256 == 0 && n <= 8192 && batchK256(r, 2) && ownFusions(r);
 }
 
-kcError_t fusedNorm(kcMulMatRecording_st& r, const kcMulMatNormNode& n, kcMulMatPlan& plan, const float* b2) noexcept {
+kcError_t fusedNorm(kcMulMatRecording_st& r, const kcMulMatNormNode& n, kcMulMatPlan& plan, const float* b2,
+                    const void* key) noexcept {
     try {
-        return fusedNormImpl(r, n, plan, b2);
+        return fusedNormImpl(r, n, plan, b2, key);
     } catch (...) {
         return kc::Error::OutOfMemory;
     }
 }
 
-kcError_t fusedSwiglu(kcMulMatRecording_st& r, const kcMulMatSwigluNode& n, kcMulMatPlan& plan) noexcept {
+kcError_t fusedSwiglu(kcMulMatRecording_st& r, const kcMulMatSwigluNode& n, kcMulMatPlan& plan,
+                      const void* key) noexcept {
     try {
-        return fusedSwigluImpl(r, n, plan);
+        return fusedSwigluImpl(r, n, plan, key);
     } catch (...) {
         return kc::Error::OutOfMemory;
     }

@@ -21,8 +21,10 @@ struct kcMulMatRecording_st {
     // launching anything (no device is needed); pointers it hands out are never dereferenced.
     bool dry = false;
     std::vector<const char*>* trace = nullptr;  // when set: every kernel name, in launch order
+    // A cached input is found by its key: the input's data pointer for kcMulMat* callers, the tensor's
+    // identity for the ggml backend (whose allocator hands a freed tensor's memory to a later one).
     struct Input {
-        const float* x;
+        const void* key;
         long long ncols;
         int k;
         bool k256;
@@ -48,22 +50,27 @@ kcError_t reserve(kcMulMatRecording_st& r, size_t ints) noexcept;
 kcError_t take(kcMulMatRecording_st& r, size_t ints, int** out) noexcept;
 // one launch on the recording's stream (dry: named only)
 kcError_t launch(kcMulMatRecording_st& r, const char* kernel, const void* args) noexcept;
-// the recording's 8-bit slots of input x (nullptr when it made none)
-int* inputSlot(const kcMulMatRecording_st& r, const float* x, long long ncols, int k, bool k256) noexcept;
-// the fp16 MFMA form of x's per-256 slots (nullptr when no producer wrote it)
-const kcamd::ActF16* inputAct(const kcMulMatRecording_st& r, const float* x, long long ncols, int k) noexcept;
-// slots for the 8-bit form of y registered under y, for a producer that writes them itself (the
-// MUL_MATs that read y then take them)
-kcError_t outputSlot(kcMulMatRecording_st& r, const float* y, int k, long long ncols, bool k256, int** q) noexcept;
+// Keys: where a function takes `key`, nullptr means the data pointer (the input's x, the output's y).
+// the recording's 8-bit slots of the input with this key (nullptr when it made none)
+int* inputSlot(const kcMulMatRecording_st& r, const void* key, long long ncols, int k, bool k256) noexcept;
+// the fp16 MFMA form of that input's per-256 slots (nullptr when no producer wrote it)
+const kcamd::ActF16* inputAct(const kcMulMatRecording_st& r, const void* key, long long ncols, int k) noexcept;
+// slots for the 8-bit form of an output registered under key, for a producer that writes them itself
+// (the MUL_MATs that read that output then take them)
+kcError_t outputSlot(kcMulMatRecording_st& r, const void* key, int k, long long ncols, bool k256, int** q) noexcept;
 
-kcError_t mulMat(kcMulMatRecording_st& r, const kcMulMatNode& n, kcMulMatPlan& plan) noexcept;
+kcError_t mulMat(kcMulMatRecording_st& r, const kcMulMatNode& n, kcMulMatPlan& plan,
+                 const void* key = nullptr) noexcept;
 // the node's 8-bit input made now (the reference's mul_mat_input; nothing for F16 weights)
-kcError_t mulMatInput(kcMulMatRecording_st& r, const kcMulMatNode& n, kcMulMatPlan& plan) noexcept;
-// b2 (with an ADD, only where fusesHalf): x = a + (b + b2), the second K half of the product b
+kcError_t mulMatInput(kcMulMatRecording_st& r, const kcMulMatNode& n, kcMulMatPlan& plan,
+                      const void* key = nullptr) noexcept;
+// b2 (with an ADD, only where fusesHalf): x = a + (b + b2), the second K half of the product b;
+// the slots are registered under key (nullptr: n.y)
 kcError_t fusedNorm(kcMulMatRecording_st& r, const kcMulMatNormNode& n, kcMulMatPlan& plan,
-                    const float* b2 = nullptr) noexcept;
+                    const float* b2 = nullptr, const void* key = nullptr) noexcept;
 // whether fusedNorm of rows of n values takes a b2 (the per-256 norm in one workgroup per row)
 bool fusesHalf(const kcMulMatRecording_st& r, int n) noexcept;
-kcError_t fusedSwiglu(kcMulMatRecording_st& r, const kcMulMatSwigluNode& n, kcMulMatPlan& plan) noexcept;
+kcError_t fusedSwiglu(kcMulMatRecording_st& r, const kcMulMatSwigluNode& n, kcMulMatPlan& plan,
+                      const void* key = nullptr) noexcept;
 
 }  // namespace kcamd::mulmat

@@ -87,6 +87,7 @@ struct Runtime {
     std::atomic<int> codegen{KC_CODEGEN_AUTO};
     std::mutex options_mutex;
     std::map<std::string, int> options;
+    std::atomic<unsigned> options_gen{0};  // bumped by every kcSetKernelOption
 
     // Device scratch of kernels that stage operands (kcamd::streamScratch), one buffer per HIP
     // stream. A buffer handed out while its stream was capturing may be baked into a graph, so it
@@ -545,6 +546,8 @@ int option(const char* name) {
     auto it = r.options.find(name);
     return it == r.options.end() ? 0 : it->second;
 }
+
+unsigned optionsGeneration() { return R().options_gen.load(); }
 
 int fromHip(int hip_status, const char* what) {
     const hipError_t s = static_cast<hipError_t>(hip_status);
@@ -1253,6 +1256,7 @@ kcError_t kcSetKernelOption(const char* option, int value) noexcept {
         if (value < 0) return kc::Error::InvalidValue;
         std::lock_guard lk(r.options_mutex);
         r.options[option] = value;
+        r.options_gen.fetch_add(1);
         return ok;
     });
 }

@@ -11,7 +11,9 @@ RMS_NORM + MUL, MUL_MAT gate/up, GLU SWIGLU, MUL_MAT down, ADD) -- the node orde
 
 With no allocator every tensor gets a distinct fake address (for plans, which never touch
 memory); with one (called with the ggml byte size, type and ne), every non-view tensor gets the
-memory it returns."""
+memory it returns. `Graph.share_memory` then places the computed nodes as ggml's graph allocator
+does (ggml-alloc.c: freed tensors' memory reused best-fit, elementwise ops run in place over a parent
+whose last use they are), so that tests see the aliasing a llama.cpp build hands the backend."""
 import ctypes as C
 import struct
 
@@ -40,6 +42,7 @@ class Graph:
         self.nodes = []
         self.keep = []
         self.srcs = {}  # id(tensor) -> [src tensors]
+        self.view_of = {}  # id(view) -> (base tensor, byte offset): ggml's view_src and view_offs
 
     def _memory(self, nbytes, type_, ne):
         if self.alloc is None:
@@ -49,7 +52,7 @@ class Graph:
         return self.alloc(nbytes, type_, ne)
 
     def tensor(self, op, type_, ne, srcs=(), params=(), nb=None, data=None, buffer="other", view=False,
-               compute=False):
+               compute=False, view_src=None):
         ne = list(ne) + [1] * (4 - len(ne))
         nb = list(nb) if nb is not None else packed_nb(type_, ne)
         t = kc.GgmlTensor()
@@ -66,6 +69,9 @@ class Graph:
         t.buffer, t.view, t.compute = kc.GGML_BUFFER[buffer], int(view), int(compute)
         self.keep.append(t)
         self.srcs[id(t)] = [s for s in srcs if s is not None]
+        if view:  # the base is never itself a view (ggml folds view chains into view_src)
+            base = self.view_of.get(id(view_src or srcs[0]), (view_src or srcs[0], 0))[0]
+            self.view_of[id(t)] = (base, t.data - base.data)
         return t
 
     def leaf(self, type_, ne, buffer="other"):
@@ -109,7 +115,7 @@ class Graph:
 
     def set_rows(self, dst, src, idx):
         return self.node("set_rows", _tname(dst), dst.ne, [src, idx], nb=list(dst.nb), data=dst.data,
-                         buffer=_bname(dst), view=True)
+                         buffer=_bname(dst), view=True, view_src=dst)
 
     def flash_attn_ext(self, q, k, v, mask, scale, max_bias=0.0, softcap=0.0):
         return self.node("flash_attn_ext", "f32", [v.ne[0], q.ne[2], q.ne[1], q.ne[3]], [q, k, v, mask],
@@ -129,6 +135,106 @@ class Graph:
         for t in outputs:
             t.output = 1
         return self.nodes
+
+
+INPLACE_OPS = ("add", "mul", "rms_norm", "rope")  # ggml_op_can_inplace, for the ops built here
+
+
+def share_memory(g, alloc, align=64, inplace_views=True):
+    """Places g's computed non-view nodes (g.finish first) in one arena as ggml_gallocr does: nodes in
+    order; a node of an op that can run in place takes the memory of a parent whose last remaining
+    use it is (not an output, the same layout, no view of it left); else the best-fitting freed
+    block, else new memory at the end; a tensor's memory is freed after its last reader (and the last
+    reader of its views) ran, outputs never. inplace_views: a parent that is a view of offset 0 (a
+    RESHAPE of a MUL_MAT output) is taken over too, with its base (the variant that shares the most
+    memory). alloc(nbytes) gives the arena; views then follow their bases. Leaves keep their memory.
+    Returns the arena size."""
+    base_of = lambda t: g.view_of.get(id(t), (t, 0))[0]
+    children, views = {}, {}
+    for t in g.nodes:
+        if t.view:
+            b = base_of(t)
+            views[id(b)] = views.get(id(b), 0) + 1
+        for s in g.srcs[id(t)]:
+            children[id(s)] = children.get(id(s), 0) + 1
+    addr, live, free, top = {}, set(), [], 0  # free: [offset, size] blocks, merged when adjacent
+    nbytes = lambda t: (max(t.nb[3] * t.ne[3], 4) + align - 1) // align * align
+    layout = lambda t: (t.type, tuple(t.ne), tuple(t.nb))
+    owner = {}  # id(node) -> the node whose block it holds (itself, or an in-place parent's)
+
+    def release(t):
+        if t.output or id(t) not in live:
+            return
+        live.discard(id(t))
+        free.append([addr[id(t)], nbytes(owner[id(t)])])
+        free.sort()
+        merged = []
+        for b in free:
+            if merged and merged[-1][0] + merged[-1][1] == b[0]:
+                merged[-1][1] += b[1]
+            else:
+                merged.append(b)
+        free[:] = merged
+
+    def in_place(t):
+        if kc_op_name(t) not in INPLACE_OPS:
+            return None
+        for p in g.srcs[id(t)]:
+            q = base_of(p)
+            if id(q) not in live or q.output or layout(p) != layout(t) or children.get(id(p), 0) != 1:
+                continue
+            if not p.view and not views.get(id(p), 0):
+                return p
+            if p.view and inplace_views and views.get(id(q), 0) == 1 and not children.get(id(q), 0) and \
+                    p.data == q.data:
+                return q
+        return None
+
+    for t in g.nodes:
+        if not t.view:
+            q = in_place(t)
+            if q is not None:  # t takes over q's block; q is never freed
+                live.discard(id(q))
+                addr[id(t)], owner[id(t)] = addr[id(q)], owner[id(q)]
+            else:
+                n = nbytes(t)
+                fits = [b for b in free if b[1] >= n]
+                if fits:
+                    b = min(fits, key=lambda b: b[1])
+                    addr[id(t)] = b[0]
+                    b[0] += n
+                    b[1] -= n
+                    if not b[1]:
+                        free.remove(b)
+                else:
+                    addr[id(t)] = top
+                    top += n
+                owner[id(t)] = t
+            live.add(id(t))
+        for s in g.srcs[id(t)]:
+            children[id(s)] -= 1
+            if children[id(s)]:
+                continue
+            if s.view:
+                b = base_of(s)
+                views[id(b)] -= 1
+                if not views[id(b)] and not children.get(id(b), 0):
+                    release(b)
+            elif not views.get(id(s), 0):
+                release(s)
+    arena = alloc(max(top, 4))
+    for t in g.nodes:
+        if not t.view:
+            t.data = arena + addr[id(t)]
+    for t in g.nodes:  # views follow their bases (in node order: a base comes before its views)
+        if t.view:
+            b, o = g.view_of[id(t)]
+            t.data = b.data + o
+    return top
+
+
+def kc_op_name(t):
+    return {v: k for k, v in kc.GGML_OP.items()}[t.op]
 
 
 def _tname(t):

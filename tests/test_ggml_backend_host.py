@@ -527,3 +527,109 @@ def test_host_environment_switches(monkeypatch):
     monkeypatch.setenv("GGML_KERNELCORE_TILE", "4")
     d = kc.ggml_config_dict(kc.ggml_config())
     assert (d["attn_tokens"], d["graphs"], d["disabled"], d["tile"]) == (0, 0, 0, 4)
+
+
+# ---- graphs whose tensors share memory as ggml's allocator places them --------------------------------------
+
+def shared_layer(N=1, outputs=(), inplace_views=True, **kw):
+    """The layer graph with its computed nodes placed by gg.share_memory (one fake arena); names in
+    `outputs` are marked graph outputs before the placement (as llama.cpp flags them)."""
+    g = gg.Graph()
+    t = gg.llama_layer(g, gg.LayerShape(**kw), N, 40 + N)
+    for name in outputs:
+        t[name].output = 1
+    gg.share_memory(g, lambda n: 1 << 24, inplace_views=inplace_views)
+    return g, t
+
+
+def spans(t):
+    end = 4 + sum((t.ne[d] - 1) * t.nb[d] for d in range(4))
+    return t.data, t.data + end
+
+
+@pytest.mark.parametrize("inplace_views", [True, False])
+@pytest.mark.parametrize("N", [1, 8, 64])
+def test_shared_memory_never_overlaps_two_live_tensors(N, inplace_views):
+    """The placement itself: a computed node's memory is not overlapped by any other computed
+    non-view node between the first's definition and its last reader (views counted as readers of
+    their base), unless the second is the first's in-place successor (same address, defined by an
+    op that reads it last); in-place placement happens (RMS_NORM + MUL, the residual ADD) and memory
+    is reused (the arena is smaller than the nodes' sum)."""
+    g, t = shared_layer(N=N, inplace_views=inplace_views)
+    base = lambda x: g.view_of.get(id(x), (x, 0))[0]
+    nodes = [x for x in g.nodes]
+    last = {}
+    for i, x in enumerate(nodes):
+        for s in g.srcs[id(x)]:
+            last[id(base(s))] = i
+    own = [(i, x) for i, x in enumerate(nodes) if not x.view]
+    for a_i, a in own:
+        end = max(last.get(id(a), a_i), a_i) if not a.output else len(nodes)
+        for b_i, b in own:
+            if b_i <= a_i or b_i > end:
+                continue
+            lo_a, hi_a = spans(a)
+            lo_b, hi_b = spans(b)
+            if lo_a < hi_b and lo_b < hi_a:  # only an in-place successor reading a last
+                assert b.data == a.data and kc_name(b) in gg.INPLACE_OPS and b_i == last[id(a)], (a_i, b_i)
+    assert t["cur"].data == t["norm"].data  # MUL in place over RMS_NORM
+    assert t["out"].data == t["down"].data  # the residual ADD in place over the down product
+    assert (t["qr"].data == t["q"].data) == inplace_views  # ROPE over the reshaped q
+
+
+def kc_name(x):
+    return gg.kc_op_name(x)
+
+
+def test_shared_memory_puts_the_attention_output_on_the_dead_norm_output():
+    """ggml's best fit: a prompt's FLASH_ATTN_EXT output ([D, H, N] f32, the size of the normed
+    activations the q / k / v products read) takes the block the attention norm's output left: the
+    aliasing under which a MUL_MAT input cache keyed by address hands the o projection the normed
+    activations' 8-bit slots. The plan keys the cache by tensor: o quantizes its own input."""
+    g, t = shared_layer(N=64)
+    assert t["attn"].data == t["cur"].data
+    names = plan(g, attn_tokens=64)
+    # cur (per 256, MFMA form) for q / k / v, then the attention output quantized for o
+    assert names.count("quantize_cols_k") == 1 and names.index("quantize_cols_k") > names.index("attn_masked")
+
+
+def test_fused_attention_writes_no_dead_intermediates_and_refuses_live_aliased_ones():
+    """One token with in-place ROPE (qr on q's memory, kr on k's): nothing outside the fused launch reads
+    qr or kr, so the fusion stands (it writes neither). Marked graph outputs, qr / kr must be written,
+    and their chunk-0 writes would race with the other chunks' reads of q / k: the fusion is refused
+    and the nodes run as rope_set_rows + flash_decode_q8 (both element by element in place)."""
+    g, t = shared_layer(N=1)
+    assert t["qr"].data == t["q"].data and t["kr"].data == t["k"].data
+    assert "rope_flash_decode_q8" in plan(g)
+    g, t = shared_layer(N=1, outputs=("qr",))
+    names = plan(g)
+    assert "rope_flash_decode_q8" not in names and "rope_set_rows" in names and "flash_decode_q8" in names
+    g, t = shared_layer(N=1, outputs=("qr",), inplace_views=False)  # written, not aliased: fused
+    assert t["qr"].data != t["q"].data and "rope_flash_decode_q8" in plan(g)
+
+
+def test_fused_qk_norm_attention_refuses_live_aliased_norm_outputs():
+    kw = dict(n_embd=1024, n_head=8, n_head_kv=2, head_dim=128, neox=True, qk_norm=True)
+    g, t = shared_layer(N=1, **kw)
+    assert t["qn"].data == t["q"].data  # RMS_NORM over the reshaped q, MUL over that, ROPE over that
+    assert "norm_rope_flash_decode_q8" in plan(g)
+    g, t = shared_layer(N=1, outputs=("qn",), **kw)
+    assert "norm_rope_flash_decode_q8" not in plan(g)
+
+
+def test_add_of_a_pending_product_with_itself_completes_the_product_first():
+    """ADD(y, y) of a K-split batch product y: both operands need y's second K half, so it is added to
+    y (vector_add) before the fused ADD + norm reads y twice. ggml counts one use per src slot (y has
+    two), which keeps y from being left pending; forced to one use, the walk still completes y first."""
+    g = gg.Graph()
+    x = g.leaf("f32", [512, 64])
+    y = g.mul_mat(g.leaf("q4k", [512, 512], buffer="weights"), x)
+    a = g.add(y, y)
+    cur = g.mul(g.rms_norm(a, 1e-5), g.leaf("f32", [512], buffer="weights"))
+    g.mul_mat(g.leaf("q4k", [512, 256], buffer="weights"), cur)
+    g.finish()
+    # (the last product's K is split too; nothing reads it, so the walk's end completes it)
+    want = ["quantize_cols_k", "matmul_group", "vector_add", "add_norm_q8k_f", "matmul_group", "vector_add"]
+    assert y.uses == 2 and plan(g) == want
+    y.uses = 1
+    assert plan(g) == want

@@ -44,11 +44,17 @@ class Layer:
     blocks, uploaded through kcWeightSetTensor), norm weights, the token inputs, and a cache holding p0
     earlier rows."""
 
-    def __init__(self, shape, N, p0, seed):
+    def __init__(self, shape, N, p0, seed, share=False, outputs=()):
+        """share: the computed nodes placed as ggml's allocator places them (gg.share_memory: freed
+        memory reused, in-place ops), after marking the tensors named in `outputs` graph outputs."""
         self.s, self.N, self.p0, self.n_kv = shape, N, p0, p0 + N
         self.bufs = {}
         self.g = gg.Graph(self._alloc)
         self.t = gg.llama_layer(self.g, shape, N, self.n_kv)
+        for name in outputs:
+            self.t[name].output = 1
+        if share:
+            gg.share_memory(self.g, lambda n: self._alloc(n, "f32", [n // 4]))
         s, t = shape, self.t
         self.blocks = {}
         for i, name in enumerate(("wq", "wk", "wv", "wo", "wg", "wu", "wd")):
@@ -261,7 +267,9 @@ CASES = [
 def test_layer_graph_matches_the_oracle_node_by_node(case, graphs):
     name, shape, N, p0, cfg = case
     note(f"ggml layer: {name}, N={N}, p0={p0}, graphs={graphs}")
-    L = Layer(shape, N, p0, seed=300 + N)
+    # the roped q and k as graph outputs: one token's fused attention writes them only when something
+    # outside it reads them, and this test checks every node
+    L = Layer(shape, N, p0, seed=300 + N, outputs=("qr", "kr"))
     L.k_before, L.v_before = L.get("k_cache", np.uint16), L.get("v_cache", np.uint16)
     be = kc.GgmlBackend(graphs=graphs, **cfg)
     names, _ = kc.ggml_graph_plan(L.g.nodes, graphs=graphs, **cfg)
@@ -274,23 +282,25 @@ def test_layer_graph_matches_the_oracle_node_by_node(case, graphs):
     L.free()
 
 
+@pytest.mark.parametrize("live", [False, True], ids=["dead-intermediates", "live-intermediates"])
 @pytest.mark.parametrize("shape", [gg.LayerShape(), gg.LayerShape(n_embd=1024, neox=True, freq_factors=True),
                                    gg.LayerShape(n_embd=1024, n_head=8, n_head_kv=2, head_dim=128, neox=True,
                                                  qk_norm=True)],
                          ids=["llama", "neox-ff", "qwen3-qk-norm"])
-def test_fused_decode_matvecs_equal_one_launch_per_node(shape):
+def test_fused_decode_matvecs_equal_one_launch_per_node(shape, live):
     """One input column: the norms inside the q / k / v and gate / up / SWIGLU launches, the o and
     down products with their residual ADDs, ROPE with the cache rows, the attention output
-    quantized in its merge -- every output both write (q, k, v, the roped q and k, the caches, the
-    attention, the two residual sums) equals the reference's one launch per node bit for bit."""
-    L = Layer(shape, 1, 90, seed=808)
+    quantized in its merge -- every output both write (q, k, v, the caches, the attention, the two
+    residual sums) equals the reference's one launch per node bit for bit. The roped q and k (and
+    Qwen3's normed q and k) are written by the fused attention only when something outside it reads
+    them: live, they are graph outputs and compared as well."""
+    qk = ("qr", "kr") + (("qn", "kn") if shape.qk_norm else ())
+    L = Layer(shape, 1, 90, seed=808, outputs=qk if live else ())
     names, _ = kc.ggml_graph_plan(L.g.nodes)
     attn = "norm_rope_flash_decode_q8" if shape.qk_norm else "rope_flash_decode_q8"
     assert names == ["decode_norm_matvec", attn, "decode_matvec_add",
                      "decode_norm_swiglu", "decode_matvec_add"]
-    kept = ("q", "k", "v", "qr", "kr", "attn", "ffn_inp", "out")  # what both write
-    if shape.qk_norm:
-        kept += ("qn", "kn")  # the per-head norms' MUL results
+    kept = ("q", "k", "v", "attn", "ffn_inp", "out") + (qk if live else ())  # what both write
     got = {}
     for opt in (1, 0):
         kc.set_option("ggml_extra_fusions", opt)
@@ -405,6 +415,48 @@ def test_kept_graph_is_launched_again_for_new_inputs():
     L2.free()
 
 
+SHARED = [
+    ("decode", gg.LayerShape(), 1, 40, {}, ()),
+    ("decode, roped q and k graph outputs", gg.LayerShape(), 1, 40, {}, ("qr", "kr")),
+    ("decode, qwen3 q / k norm", gg.LayerShape(n_embd=1024, n_head=8, n_head_kv=2, head_dim=128, neox=True,
+                                              qk_norm=True), 1, 70, {}, ()),
+    ("decode, qwen3, normed q graph output", gg.LayerShape(n_embd=1024, n_head=8, n_head_kv=2, head_dim=128, neox=True,
+                                                           qk_norm=True), 1, 70, {}, ("qn",)),
+    ("batch of 8", gg.LayerShape(), 8, 100, {}, ()),
+    ("batch of 64 (MFMA matmuls, masked attention)", gg.LayerShape(), 64, 64, dict(attn_tokens=64), ()),
+]
+
+
+@pytest.mark.parametrize("graphs", [1, 0])
+@pytest.mark.parametrize("case", SHARED, ids=[c[0] for c in SHARED])
+def test_layer_with_shared_memory_equals_distinct_memory(case, graphs):
+    """The layer with its nodes placed as ggml's allocator places them (freed memory reused best
+    fit, ROPE / RMS_NORM / MUL / ADD in place over the parent they read last) against the same layer
+    with a block of its own per tensor: the layer output and both caches bit-identical. With the
+    memory shared, a cache of quantized inputs keyed by data pointer hands the o projection another
+    tensor's slots, and fused launches whose workgroups write one tensor while others read its
+    in-place parent race; both are what this checks."""
+    name, shape, N, p0, cfg, outs = case
+    note(f"ggml layer, shared memory: {name}, graphs={graphs}")
+    got = {}
+    for share in (True, False):
+        L = Layer(shape, N, p0, seed=1300 + N, share=share, outputs=outs)
+        if share:
+            assert L.t["cur"].data == L.t["norm"].data
+            assert (L.t["qr"].data == L.t["q"].data) == (shape.qk_norm == 0 or "qn" not in outs)
+            if N == 64:
+                assert L.t["attn"].data == L.t["cur"].data  # the attention output on the normed rows
+        be = kc.GgmlBackend(graphs=graphs, **cfg)
+        be.compute(L.g.nodes)
+        kc.synchronize()
+        got[share] = [L.get("out", np.float32).view(np.uint32), L.get("k_cache", np.uint16),
+                      L.get("v_cache", np.uint16)] + [L.get(n, np.float32).view(np.uint32) for n in outs]
+        be.close()
+        L.free()
+    for a, b, what in zip(got[True], got[False], ("out", "k_cache", "v_cache") + outs):
+        assert np.array_equal(a, b), what
+
+
 def test_unclaimed_node_is_refused_before_any_launch():
     L = Layer(gg.LayerShape(), 9, 10, seed=700)  # 9 tokens: attention beyond attn_tokens
     be = kc.GgmlBackend()
@@ -431,8 +483,8 @@ class BackendDecoder:
     """The model's weights in the backend's buffers (kcWeightSetTensor) and its KV caches; step(tokens)
     builds llama.cpp's graph for those tokens at the current position and runs kcGgmlGraphCompute."""
 
-    def __init__(self, cfg, weights, be):
-        self.cfg, self.be = cfg, be
+    def __init__(self, cfg, weights, be, share=False):
+        self.cfg, self.be, self.share = cfg, be, share
         self.s = gg.LayerShape.of_model(cfg, cfg["max_ctx"])
         self.bufs = []
         wg = gg.Graph(self._alloc)
@@ -474,6 +526,8 @@ class BackendDecoder:
         step_bufs = len(self.bufs)
         g = gg.Graph(self._alloc)
         io, _, _, logits = gg.decoder(g, self.s, self.cfg["n_layer"], N, n_kv, weights=self.W)
+        if self.share:  # the step's nodes placed as ggml's allocator places them
+            gg.share_memory(g, lambda n: self._alloc(n, "f32", [n // 4]))
         put = lambda t, a: kc.call("kcMemcpy", t.data, np.ascontiguousarray(a).ctypes.data, a.nbytes,
                                    kc.HOST_TO_DEVICE)
         put(io["x"], self.embd[np.asarray(tokens)].astype(np.float32))
@@ -503,8 +557,9 @@ def rel_l2(a, b):
     return np.linalg.norm(a - b) / np.linalg.norm(b)
 
 
+@pytest.mark.parametrize("share", [False, True], ids=["distinct-memory", "shared-memory"])
 @pytest.mark.parametrize("name,cfg", [("llama", LLAMA), ("qwen3", QWEN)])
-def test_decoder_graph_matches_the_model_driver(name, cfg):
+def test_decoder_graph_matches_the_model_driver(name, cfg, share):
     """Two layers, the output norm and the head as llama.cpp's graph through kcGgmlGraphCompute,
     against kcModelForward and the oracle model on the same weights (N(0, 0.02) quantized as ggml
     does): a 20-token prompt in steps of up to 8 tokens (the backend's attention batch), then 4
@@ -513,7 +568,8 @@ def test_decoder_graph_matches_the_model_driver(name, cfg):
     decode step is such a step (the oracle itself moves by 2.7e-3 when its attention output is
     perturbed by one ulp; the driver lands there, the backend not). So the bar is the model tests'
     -- 1e-2 relative L2 on the logits, the q8 activation noise -- and the same greedy token;
-    typical steps agree to 2e-7."""
+    typical steps agree to 2e-7. shared-memory: each step's nodes placed as ggml's allocator
+    places them (gg.share_memory)."""
     from tests.model_weights import quantized_weights
     note(f"ggml decoder vs model driver: {name}")
     w = quantized_weights(cfg, 11)
@@ -521,7 +577,7 @@ def test_decoder_graph_matches_the_model_driver(name, cfg):
     for (tid, layer), data in w.items():
         m.set_tensor(tid, layer, data)
     be = kc.GgmlBackend()
-    d = BackendDecoder(cfg, w, be)
+    d = BackendDecoder(cfg, w, be, share=share)
     o = OracleModel(cfg, w)
     rng = np.random.default_rng(5)
     prompt = rng.integers(0, cfg["n_vocab"], 20).astype(np.int32)
