@@ -90,14 +90,34 @@ typedef struct kcGgmlConfig {
     int attn_tokens;        /* GGML_KERNELCORE_ATTN_TOKENS=n: largest batch whose attention runs here (default 8) */
     int concurrent;         /* GGML_KERNELCORE_CONCURRENT=0: MUL_MATs of one input not grouped (default 1) */
     int graphs;             /* GGML_KERNELCORE_GRAPHS=0: no graph recording (default 1) */
+    int profile;            /* GGML_KERNELCORE_PROFILE=1: time each call's recording and run; =2: also
+                               every launch (default 0; ggml-kernelcore.cpp:331-346, 1033-1035) */
 } kcGgmlConfig;
 
+/* The times are host wall clock over the calls that succeeded, kept only with profile >= 1
+ * (BackendCtx t_compute / t_record / t_run, ggml-kernelcore.cpp:331-346): compute_ms the whole
+ * kcGgmlGraphCompute call; record_ms the planning pass and the walk that records the graph (or,
+ * graphs off, issues the launches); run_ms the graph launch (a kept graph's too) and the wait for
+ * the stream (graphs off: the wait). */
 typedef struct kcGgmlStats {
     long long computes;       /* kcGgmlGraphCompute calls that succeeded */
     long long graphs_recorded; /* calls that recorded (and launched) a new graph */
     long long graphs_reused;   /* calls that launched the kept graph again */
     long long launches;        /* kernel launches recorded or made (a reused graph's count again) */
+    double compute_ms;
+    double record_ms;
+    double run_ms;
 } kcGgmlStats;
+
+/* profile = 2: every launch timed on the device (HIP events on the backend's stream around it; the
+ * call's launches are then made one by one, as the reference times them only with graphs off,
+ * :400-415), summed per kernel name; launches made for a MUL_MAT node or a group of them carry the
+ * first weight's shape ("matvec_q4k_q8 3072x3072": rows x k), as GGML_KERNELCORE_PROFILE=2 does. */
+typedef struct kcGgmlProfileEntry {
+    char name[64];
+    long long launches;
+    double ms;
+} kcGgmlProfileEntry;
 
 typedef struct kcGgmlBackend_st* kcGgmlBackend_t;
 
@@ -128,5 +148,9 @@ KC_API kcError_t kcGgmlBackendDestroy(kcGgmlBackend_t backend) KC_NOEXCEPT;
 KC_API kcError_t kcGgmlGraphCompute(kcGgmlBackend_t backend, const kcGgmlTensor* const* nodes,
                                     int n_nodes) KC_NOEXCEPT;
 KC_API kcError_t kcGgmlBackendGetStats(kcGgmlBackend_t backend, kcGgmlStats* stats) KC_NOEXCEPT;
+/* The per-launch times of profile = 2, in name order: the first min(capacity, *count) entries are
+ * written; *count is how many there are. */
+KC_API kcError_t kcGgmlBackendGetProfile(kcGgmlBackend_t backend, kcGgmlProfileEntry* entries, int capacity,
+                                         int* count) KC_NOEXCEPT;
 
 #endif /* KERNELCORE_GGML_BACKEND_H */

@@ -225,5 +225,8 @@ KC_API kcError_t kcEventElapsedTime(float* ms, kcEvent_t start, kcEvent_t end) K
  * default. Unknown names: InvalidValue. */
 KC_API kcError_t kcSetKernelOption(const char* option, int value) KC_NOEXCEPT;
 KC_API kcError_t kcGetKernelOption(const char* option, int* value) KC_NOEXCEPT;
+/* Free and total HBM bytes of the device (hipMemGetInfo): what the ggml backend's get_memory
+ * reports (the reference's dev_get_memory returns 0 / 0, ggml-kernelcore.cpp:823-826). */
+KC_API kcError_t kcDeviceGetMemoryInfo(size_t* free_bytes, size_t* total_bytes) KC_NOEXCEPT;
 
 #endif /* KERNELCORE_KC_H */

@@ -28,5 +28,12 @@ KC_API kcError_t kcWeightSetTensor(int qtype, int rows, int k, void* dst, const 
 /* get_tensor: bytes [offset, offset + size) of the tensor's ggml form, read from src, into host. */
 KC_API kcError_t kcWeightGetTensor(int qtype, int rows, int k, const void* src, void* host, size_t offset,
                                    size_t size, kcStream_t stream KC_DEF(nullptr)) KC_NOEXCEPT;
+/* memset_tensor: bytes [offset, offset + size) of the tensor's ggml form set to value (its low
+ * byte), so that a later get_tensor reads value there (buffer_memset_tensor,
+ * ggml-kernelcore.cpp:171-173, which sets the repacked memory itself). A K-quant weight is
+ * unpacked, set and repacked on the device (its stream holds exactly the ggml bytes, rearranged);
+ * any other tensor is a plain device memset of the range. */
+KC_API kcError_t kcWeightMemsetTensor(int qtype, int rows, int k, void* dst, int value, size_t offset, size_t size,
+                                      kcStream_t stream KC_DEF(nullptr)) KC_NOEXCEPT;
 
 #endif /* KERNELCORE_WEIGHTS_H */

@@ -179,6 +179,9 @@ def lib():
         L.kcWeightAllocSize.argtypes = [_i, _i, _i, C.POINTER(C.c_size_t)]
         L.kcWeightSetTensor.argtypes = [_i, _i, _i, _p, _p, C.c_size_t, C.c_size_t, _p]
         L.kcWeightGetTensor.argtypes = [_i, _i, _i, _p, _p, C.c_size_t, C.c_size_t, _p]
+        L.kcWeightMemsetTensor.argtypes = [_i, _i, _i, _p, _i, C.c_size_t, C.c_size_t, _p]
+        L.kcDeviceGetMemoryInfo.argtypes = [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
+        L.kcGgmlBackendGetProfile.argtypes = [_p, _p, _i, C.POINTER(_i)]
         L.kcMulMatFusedNorm.argtypes = [_p, C.POINTER(MulMatNormNode), C.POINTER(MulMatPlan)]
         L.kcMulMatFusedSwiglu.argtypes = [_p, C.POINTER(MulMatSwigluNode), C.POINTER(MulMatPlan)]
         L.kcGgmlConfigFromEnv.argtypes = [C.POINTER(GgmlConfig)]
@@ -326,6 +329,18 @@ def weight_set(qtype, rows, k, dst, data, offset=0, stream=None):
     call("kcWeightSetTensor", WEIGHT_TYPES.get(qtype, qtype), rows, k, dst, a.ctypes.data, offset, a.nbytes, stream)
 
 
+def weight_memset(qtype, rows, k, dst, value, offset, size, stream=None):
+    """kcWeightMemsetTensor: bytes [offset, offset + size) of the tensor's ggml form set to value."""
+    call("kcWeightMemsetTensor", WEIGHT_TYPES.get(qtype, qtype), rows, k, dst, value, offset, size, stream)
+
+
+def device_memory():
+    """kcDeviceGetMemoryInfo: (free, total) HBM bytes."""
+    f, t = C.c_size_t(), C.c_size_t()
+    call("kcDeviceGetMemoryInfo", C.byref(f), C.byref(t))
+    return f.value, t.value
+
+
 def weight_get(qtype, rows, k, src, offset, size, stream=None):
     """kcWeightGetTensor: bytes [offset, offset + size) of the tensor's ggml form (uint8 array)."""
     out = np.zeros(size, np.uint8)
@@ -434,13 +449,18 @@ GgmlTensor._fields_ = [("op", _i), ("type", _i), ("ne", C.c_int64 * 4), ("nb", C
 class GgmlConfig(C.Structure):
     """kcGgmlConfig: the backend's switches."""
     _fields_ = [("mul_mat", MulMatConfig), ("disabled", _i), ("matmul_only", _i), ("attn", _i), ("attn_tokens", _i),
-                ("concurrent", _i), ("graphs", _i)]
+                ("concurrent", _i), ("graphs", _i), ("profile", _i)]
 
 
 class GgmlStats(C.Structure):
     """kcGgmlStats: what a backend's graph_compute calls did."""
     _fields_ = [("computes", C.c_longlong), ("graphs_recorded", C.c_longlong), ("graphs_reused", C.c_longlong),
-                ("launches", C.c_longlong)]
+                ("launches", C.c_longlong), ("compute_ms", C.c_double), ("record_ms", C.c_double), ("run_ms", C.c_double)]
+
+
+class GgmlProfileEntry(C.Structure):
+    """kcGgmlProfileEntry: one launch name's device time (profile = 2)."""
+    _fields_ = [("name", C.c_char * 64), ("launches", C.c_longlong), ("ms", C.c_double)]
 
 
 _MM_KEYS = ("matvec_cols", "q8k", "tile", "row_block")
@@ -518,6 +538,14 @@ class GgmlBackend:
         s = GgmlStats()
         call("kcGgmlBackendGetStats", self.h, C.byref(s))
         return {k: getattr(s, k) for k, _ in GgmlStats._fields_}
+
+    def profile(self):
+        """kcGgmlBackendGetProfile: {launch name: (launches, ms)} of profile = 2."""
+        n = _i()
+        call("kcGgmlBackendGetProfile", self.h, None, 0, C.byref(n))
+        arr = (GgmlProfileEntry * max(1, n.value))()
+        call("kcGgmlBackendGetProfile", self.h, arr, n.value, C.byref(n))
+        return {arr[i].name.decode(): (arr[i].launches, arr[i].ms) for i in range(n.value)}
 
     def close(self):
         if self.h:

@@ -16,9 +16,11 @@
 // not hold; they are restated below from their definitions in ggml (ggml.c: ggml_is_contiguous_n;
 // ggml-impl.h: ggml_can_fuse_ext, ggml_node_has_n_uses).
 #include <algorithm>
+#include <chrono>
 #include <climits>
 #include <cmath>
 #include <cstdint>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <iterator>
@@ -50,6 +52,9 @@ struct kcGgmlBackend_st {
     unsigned graph_options = 0;  // the kernel options' generation the graph was recorded under
     long long graph_launches = 0;
     kcGgmlStats stats{};
+    // profile = 2: the launch timer of the calls and the device times summed per launch name
+    kcamd::LaunchTimer timer;
+    std::map<std::string, std::pair<long long, double>> per_kernel;
 };
 
 namespace {
@@ -428,10 +433,20 @@ template <class F>
 E direct(Pass& p, const char* name, F&& fn) {
     if (E e = marker(p, name); e != ok) return e;
     if (p.rec.dry) return ok;
-    void* hs = nullptr;
-    if (E e = kcStreamGetNative(p.rec.stream, &hs); e != ok) return e;
-    return static_cast<E>(fn(static_cast<hipStream_t>(hs)));
+    return kcamd::mulmat::timed(p.rec, name, fn);
 }
+
+// While it lives, launches are timed under the weight shape of MUL_MAT mm ("rows x k"), as
+// GGML_KERNELCORE_PROFILE=2 names them (ggml-kernelcore.cpp:549-553).
+struct ShapeTag {
+    kcamd::LaunchTimer* t;
+    ShapeTag(const Pass& p, const T* mm) : t(p.rec.timer) {
+        if (t) t->tag = std::to_string(mm->src[0]->ne[1]) + "x" + std::to_string(mm->src[0]->ne[0]);
+    }
+    ~ShapeTag() {
+        if (t) t->tag.clear();
+    }
+};
 
 bool kquant(const T* w) { return w->type == KC_GGML_TYPE_Q4_K || w->type == KC_GGML_TYPE_Q6_K; }
 bool computed(const T* t) { return t->compute && !empty(t); }
@@ -954,6 +969,7 @@ E walk(Pass& p, const T* const* nodes, int n) {
         E e = ok;
         switch (node->op) {
             case KC_GGML_OP_MUL_MAT: {
+                const ShapeTag tag(p, node);
                 if (kcamd::option("ggml_extra_fusions") != 1) {  // one input column: the fused decode matvec
                     int ga = 1;
                     while (i + ga < n && ga < 3 && nodes[i + ga]->op == KC_GGML_OP_MUL_MAT &&
@@ -1019,6 +1035,7 @@ E walk(Pass& p, const T* const* nodes, int n) {
                 NormGroup ng;
                 if (node->op == KC_GGML_OP_RMS_NORM && kcamd::option("ggml_extra_fusions") != 1 &&
                     normGroupOk(nodes, n, i, ng)) {  // the norm in the group's launch
+                    const ShapeTag tag(p, nodes[ng.first]);
                     e = decodeNormGroup(p, node, nodes[i + 1], nodes + ng.first, ng);
                     i = ng.first + ng.n - 1 + (ng.glu ? 1 : 0);
                     break;
@@ -1198,19 +1215,44 @@ void dropGraph(kcGgmlBackend_st& be) {
     be.sig.clear();
 }
 
+double msSince(std::chrono::steady_clock::time_point t0) {
+    return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+}
+
+// profile = 2: the device time of every timed launch of the call, summed per name (the stream has run them)
+E collectTimes(kcGgmlBackend_st& be) {
+    for (const auto& m : be.timer.marks) {
+        float ms = 0.0f;
+        if (int e = kcamd::fromHip(hipEventElapsedTime(&ms, m.a, m.b), "hipEventElapsedTime")) return E(e);
+        auto& [count, total] = be.per_kernel[m.name];
+        ++count;
+        total += ms;
+    }
+    be.timer.marks.clear();
+    be.timer.used = 0;
+    return ok;
+}
+
 E compute(kcGgmlBackend_st& be, const T* const* nodes, int n) {
     if (E e = checkNodes(be.cfg, nodes, n); e != ok) return e;
-    const bool graphs = be.cfg.graphs != 0;
+    const auto t0 = std::chrono::steady_clock::now();
+    const bool prof = be.cfg.profile >= 1, each = be.cfg.profile >= 2;
+    const bool graphs = be.cfg.graphs != 0 && !each;  // launches timed one by one: no graph
     const unsigned options = kcamd::optionsGeneration();  // read before the walk reads any option
     std::vector<uint64_t> sig;
     if (graphs) {
         signature(nodes, n, sig);
         if (be.graph && be.graph_gen == be.rec.gen && be.graph_options == options && sig == be.sig) {  // the kept graph again
+            const auto tr = std::chrono::steady_clock::now();
             if (E e = kcGraphLaunch(be.graph, be.stream); e != ok) return e;
             if (E e = kcStreamSynchronize(be.stream); e != ok) return e;
             ++be.stats.computes;
             ++be.stats.graphs_reused;
             be.stats.launches += be.graph_launches;
+            if (prof) {
+                be.stats.run_ms += msSince(tr);
+                be.stats.compute_ms += msSince(t0);
+            }
             return ok;
         }
     }
@@ -1223,9 +1265,21 @@ E compute(kcGgmlBackend_st& be, const T* const* nodes, int n) {
         if (E e = kcamd::mulmat::reserve(be.rec, pl.scratch); e != ok) return e;
     }
     Pass p{be.cfg, be.rec, &be, nullptr, graphs};
+    double record = 0, run = 0;
     if (!graphs) {
+        be.rec.timer = each ? &be.timer : nullptr;
         const E e = walk(p, nodes, n);
+        be.rec.timer = nullptr;
+        record = msSince(t0);
+        const auto tr = std::chrono::steady_clock::now();
         const E s = kcStreamSynchronize(be.stream);
+        run = msSince(tr);
+        if (each) {
+            const E c = e == ok && s == ok ? collectTimes(be) : ok;
+            be.timer.marks.clear();
+            be.timer.used = 0;
+            if (c != ok) return c;
+        }
         if (e != ok) return e;
         if (s != ok) return s;
     } else {
@@ -1244,6 +1298,8 @@ E compute(kcGgmlBackend_st& be, const T* const* nodes, int n) {
             if (g) (void)kcGraphDestroy(g);
             return e != ok ? e : c;
         }
+        record = msSince(t0);
+        const auto tr = std::chrono::steady_clock::now();
         if (E l = kcGraphLaunch(g, be.stream); l != ok) {
             (void)kcGraphDestroy(g);
             return l;
@@ -1255,9 +1311,15 @@ E compute(kcGgmlBackend_st& be, const T* const* nodes, int n) {
         be.graph_launches = pl.launches;
         ++be.stats.graphs_recorded;
         if (E s = kcStreamSynchronize(be.stream); s != ok) return s;
+        run = msSince(tr);
     }
     ++be.stats.computes;
     be.stats.launches += pl.launches;
+    if (prof) {
+        be.stats.record_ms += record;
+        be.stats.run_ms += run;
+        be.stats.compute_ms += msSince(t0);
+    }
     return ok;
 }
 
@@ -1285,6 +1347,7 @@ KC_API void kcGgmlConfigFromEnv(kcGgmlConfig* cfg) noexcept {
     if (const char* an = std::getenv("GGML_KERNELCORE_ATTN_TOKENS")) cfg->attn_tokens = std::max(0, std::atoi(an));
     cfg->concurrent = !envIs("GGML_KERNELCORE_CONCURRENT", "0");
     cfg->graphs = !envIs("GGML_KERNELCORE_GRAPHS", "0");
+    cfg->profile = envIs("GGML_KERNELCORE_PROFILE", "1") ? 1 : envIs("GGML_KERNELCORE_PROFILE", "2") ? 2 : 0;
 }
 
 KC_API int kcGgmlSupportsOp(const kcGgmlConfig* cfg, const kcGgmlTensor* op) noexcept {
@@ -1344,6 +1407,7 @@ KC_API kcError_t kcGgmlBackendDestroy(kcGgmlBackend_t backend) noexcept {
     if (!backend) return ok;
     E e = kcStreamSynchronize(backend->stream);  // nothing in flight reads what is freed below
     dropGraph(*backend);
+    for (hipEvent_t ev : backend->timer.pool) (void)hipEventDestroy(ev);
     for (auto& [n, ptr] : backend->ones)
         if (E f = kcFree(ptr); e == ok) e = f;
     if (backend->rec.scratch)
@@ -1365,5 +1429,21 @@ KC_API kcError_t kcGgmlBackendGetStats(kcGgmlBackend_t backend, kcGgmlStats* sta
     if (!backend) return kc::Error::InvalidResourceHandle;
     if (!stats) return bad("null stats pointer");
     *stats = backend->stats;
+    return ok;
+}
+
+KC_API kcError_t kcGgmlBackendGetProfile(kcGgmlBackend_t backend, kcGgmlProfileEntry* entries, int capacity,
+                                         int* count) noexcept {
+    if (!backend) return kc::Error::InvalidResourceHandle;
+    if (!count || capacity < 0 || (capacity > 0 && !entries)) return bad("null count, or capacity without entries");
+    *count = int(backend->per_kernel.size());
+    int i = 0;
+    for (const auto& [name, tc] : backend->per_kernel) {
+        if (i == capacity) break;
+        kcGgmlProfileEntry& e = entries[i++];
+        std::snprintf(e.name, sizeof e.name, "%s", name.c_str());
+        e.launches = tc.first;
+        e.ms = tc.second;
+    }
     return ok;
 }

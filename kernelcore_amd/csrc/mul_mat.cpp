@@ -69,9 +69,7 @@ E direct(kcMulMatRecording_st& r, const char* kernel, F&& fn, kcMulMatPlan& plan
     if (r.trace) r.trace->push_back(kernel);
     ++plan.launches;
     if (r.dry) return ok;
-    void* hs = nullptr;
-    if (E e = kcStreamGetNative(r.stream, &hs); e != ok) return e;
-    return static_cast<E>(fn(static_cast<hipStream_t>(hs)));
+    return kcamd::mulmat::timed(r, kernel, fn);
 }
 
 // Whether a per-256 producer of ncols columns of k values also writes the fp16 MFMA form (act_f16),
@@ -287,6 +285,20 @@ E mulMatImpl(kcMulMatRecording_st& r, const kcMulMatNode& n, kcMulMatPlan& plan,
 
 }  // namespace
 
+hipEvent_t kcamd::LaunchTimer::next() {
+    if (used == pool.size()) {
+        hipEvent_t e = nullptr;
+        if (hipEventCreate(&e) != hipSuccess) return nullptr;
+        try {
+            pool.push_back(e);
+        } catch (...) {
+            (void)hipEventDestroy(e);
+            return nullptr;
+        }
+    }
+    return pool[used++];
+}
+
 namespace kcamd::mulmat {
 
 kcError_t checkConfig(kcMulMatConfig& c) noexcept {
@@ -352,7 +364,9 @@ kcError_t launch(kcMulMatRecording_st& r, const char* kernel, const void* args) 
             return kc::Error::OutOfMemory;
         }
     }
-    return r.dry ? ok : kcLaunchKernel(kernel, args, r.stream);
+    if (r.dry) return ok;
+    if (!r.timer) return kcLaunchKernel(kernel, args, r.stream);
+    return timed(r, kernel, [&](hipStream_t) { return int(kcLaunchKernel(kernel, args, r.stream)); });
 }
 
 kcError_t mulMat(kcMulMatRecording_st& r, const kcMulMatNode& n, kcMulMatPlan& plan, const void* key) noexcept {

@@ -4,10 +4,27 @@
 #pragma once
 
 #include <cstddef>
+#include <string>
 #include <vector>
 
 #include "kernelcore/mul_mat.h"
 #include "launch.hpp"
+
+namespace kcamd {
+// Device times of launches (the ggml backend's profile = 2): an event pair on the recording's stream
+// around each launch, named by its kernel and the weight shape of the MUL_MAT it serves.
+struct LaunchTimer {
+    std::string tag;  // "rows x k" of the MUL_MAT (group) being launched, else empty
+    struct Mark {
+        std::string name;
+        hipEvent_t a, b;
+    };
+    std::vector<Mark> marks;
+    std::vector<hipEvent_t> pool;  // created once, reused by every call
+    size_t used = 0;
+    hipEvent_t next();  // nullptr when HIP cannot create one
+};
+}  // namespace kcamd
 
 struct kcMulMatRecording_st {
     kcMulMatConfig cfg{};
@@ -36,6 +53,7 @@ struct kcMulMatRecording_st {
     // The ggml backend's recordings: per-256 producers of at least 64 columns that the MFMA matmul
     // takes also write the fp16 form it reads, so the matmuls convert nothing (kcMulMat* leave it off).
     bool act_f16 = false;
+    kcamd::LaunchTimer* timer = nullptr;  // when set (never with a dry or capturing recording): each launch timed
 };
 
 namespace kcamd::mulmat {
@@ -50,6 +68,27 @@ kcError_t reserve(kcMulMatRecording_st& r, size_t ints) noexcept;
 kcError_t take(kcMulMatRecording_st& r, size_t ints, int** out) noexcept;
 // one launch on the recording's stream (dry: named only)
 kcError_t launch(kcMulMatRecording_st& r, const char* kernel, const void* args) noexcept;
+// fn(hip stream) -> kc code: one launch of a launcher of this build, on the recording's stream,
+// timed when the recording has a timer
+template <class F>
+kcError_t timed(kcMulMatRecording_st& r, const char* kernel, F&& fn) noexcept {
+    void* hs = nullptr;
+    if (kcError_t e = kcStreamGetNative(r.stream, &hs); e != kc::Error::Success) return e;
+    const auto s = static_cast<hipStream_t>(hs);
+    hipEvent_t a = r.timer ? r.timer->next() : nullptr, b = r.timer ? r.timer->next() : nullptr;
+    if (a && b) (void)hipEventRecord(a, s);
+    const auto e = static_cast<kcError_t>(fn(s));
+    if (a && b) {
+        (void)hipEventRecord(b, s);
+        try {
+            r.timer->marks.push_back({r.timer->tag.empty() ? std::string(kernel) : std::string(kernel) + " " + r.timer->tag,
+                                      a, b});
+        } catch (...) {
+            return kc::Error::OutOfMemory;
+        }
+    }
+    return e;
+}
 // Keys: where a function takes `key`, nullptr means the data pointer (the input's x, the output's y).
 // the recording's 8-bit slots of the input with this key (nullptr when it made none)
 int* inputSlot(const kcMulMatRecording_st& r, const void* key, long long ncols, int k, bool k256) noexcept;

@@ -647,6 +647,17 @@ kcError_t kcGetDeviceProperties(kcDeviceProperties* props, int device) noexcept 
     });
 }
 
+kcError_t kcDeviceGetMemoryInfo(size_t* free_bytes, size_t* total_bytes) noexcept {
+    return gated<Need::Live>("kcDeviceGetMemoryInfo", [&](Runtime& r) {
+        if (!free_bytes || !total_bytes) return kc::Error::InvalidValue;
+        size_t f = 0, t = 0;
+        if (int e = kcamd::fromHip(hipMemGetInfo(&f, &t), "hipMemGetInfo")) return err(e);
+        *free_bytes = f;
+        *total_bytes = t;
+        return ok;
+    });
+}
+
 kcError_t kcSetDevice(int device) noexcept {
     return gated<Need::Init>("kcSetDevice", [&](Runtime& r) {
         if (device != 0) {

@@ -81,6 +81,24 @@ KC_API kcError_t kcWeightSetTensor(int qtype, int rows, int k, void* dst, const 
     return kcStreamSynchronize(stream);
 }
 
+KC_API kcError_t kcWeightMemsetTensor(int qtype, int rows, int k, void* dst, int value, size_t offset, size_t size,
+                                      kcStream_t stream) noexcept {
+    size_t total = 0;
+    if (E e = range(qtype, rows, k, dst, dst, offset, size, &total); e != ok) return e;
+    if (E e = kcStreamSynchronize(stream); e != ok) return e;  // after the stream's earlier use of dst
+    if (!size) return ok;
+    if (!kquant(qtype)) return kcMemset(static_cast<char*>(dst) + offset, value, size);
+    Staging st;  // the ggml blocks: unpacked, the range set, repacked
+    if (E e = kcMalloc(&st.p, total); e != ok) return e;
+    const kcKquantRepackArgs un{dst, st.p, qtype, rows, k};
+    if (E e = kcLaunchKernel("unpack_kquant", &un, stream); e != ok) return e;
+    if (E e = kcStreamSynchronize(stream); e != ok) return e;
+    if (E e = kcMemset(static_cast<char*>(st.p) + offset, value, size); e != ok) return e;
+    const kcKquantRepackArgs re{st.p, dst, qtype, rows, k};
+    if (E e = kcLaunchKernel("repack_kquant", &re, stream); e != ok) return e;
+    return kcStreamSynchronize(stream);
+}
+
 KC_API kcError_t kcWeightGetTensor(int qtype, int rows, int k, const void* src, void* host, size_t offset, size_t size,
                                    kcStream_t stream) noexcept {
     size_t total = 0;

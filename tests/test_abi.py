@@ -84,7 +84,7 @@ STRUCTS = ["VectorAddArgs", "QuantizeArgs", "MatvecQ4Q8Args", "MatmulKQ8Args", "
            "KquantRepackArgs", "GetRowsKquantArgs", "QuantizeKquantArgs", "FillNormalArgs", "FlashAttnArgs", "FlashDecodeArgs",
            "DeviceProperties",
            "MulMatConfig", "MulMatNode", "MulMatPlan", "MulMatNormNode", "MulMatSwigluNode", "GgmlTensor",
-           "GgmlConfig", "GgmlStats"]
+           "GgmlConfig", "GgmlStats", "GgmlProfileEntry"]
 
 
 def test_struct_layouts_match_the_c_header(tmp_path):

@@ -517,16 +517,20 @@ def test_set_rows_and_attention_rules():
 
 def test_host_environment_switches(monkeypatch):
     for v in ("DISABLE", "MATMUL_ONLY", "ATTN", "ATTN_TOKENS", "CONCURRENT", "GRAPHS", "MATVEC_COLS", "Q8K", "TILE",
-              "ROW_BLOCK"):
+              "ROW_BLOCK", "PROFILE"):
         monkeypatch.delenv(f"GGML_KERNELCORE_{v}", raising=False)
     assert kc.ggml_config_dict(kc.ggml_config()) == dict(matvec_cols=0, q8k=1, tile=8, row_block=8, disabled=0,
-                                                         matmul_only=0, attn=1, attn_tokens=8, concurrent=1, graphs=1)
+                                                         matmul_only=0, attn=1, attn_tokens=8, concurrent=1, graphs=1,
+                                                         profile=0)
     monkeypatch.setenv("GGML_KERNELCORE_ATTN_TOKENS", "-3")
     monkeypatch.setenv("GGML_KERNELCORE_GRAPHS", "0")
     monkeypatch.setenv("GGML_KERNELCORE_DISABLE", "yes")  # only "1" disables
     monkeypatch.setenv("GGML_KERNELCORE_TILE", "4")
+    monkeypatch.setenv("GGML_KERNELCORE_PROFILE", "2")  # "1" or "2" (ggml-kernelcore.cpp:1033-1035)
     d = kc.ggml_config_dict(kc.ggml_config())
-    assert (d["attn_tokens"], d["graphs"], d["disabled"], d["tile"]) == (0, 0, 0, 4)
+    assert (d["attn_tokens"], d["graphs"], d["disabled"], d["tile"], d["profile"]) == (0, 0, 0, 4, 2)
+    monkeypatch.setenv("GGML_KERNELCORE_PROFILE", "3")
+    assert kc.ggml_config_dict(kc.ggml_config())["profile"] == 0
 
 
 # ---- graphs whose tensors share memory as ggml's allocator places them --------------------------------------

@@ -457,6 +457,42 @@ def test_layer_with_shared_memory_equals_distinct_memory(case, graphs):
         assert np.array_equal(a, b), what
 
 
+def test_profile_times_calls_and_launches():
+    """GGML_KERNELCORE_PROFILE (ggml-kernelcore.cpp:331-346, 400-415, 1033-1035): with 1 each call's
+    compute, recording and run times add up in the stats; with 2 every launch is also timed on the
+    device (one by one), per kernel name and MUL_MAT weight shape, and the results are those of the
+    untimed backend bit for bit."""
+    L = Layer(gg.LayerShape(), 1, 40, seed=1700)
+    plain = kc.GgmlBackend(graphs=1)
+    plain.compute(L.g.nodes)
+    want = L.get("out", np.float32)
+    assert plain.stats()["compute_ms"] == 0.0  # profile off: nothing timed
+    plain.close()
+    be1 = kc.GgmlBackend(graphs=1, profile=1)
+    for _ in range(3):
+        be1.compute(L.g.nodes)
+    st = be1.stats()
+    assert st["graphs_recorded"] == 1 and st["graphs_reused"] == 2
+    assert st["compute_ms"] > 0 and st["run_ms"] > 0 and st["record_ms"] > 0
+    assert st["record_ms"] + st["run_ms"] <= st["compute_ms"] * 1.001 + 1e-3
+    assert be1.profile() == {}
+    be1.close()
+    be2 = kc.GgmlBackend(graphs=1, profile=2)
+    for _ in range(2):
+        be2.compute(L.g.nodes)
+    assert np.array_equal(kq.bits(L.get("out", np.float32)), kq.bits(want))
+    st, prof = be2.stats(), be2.profile()
+    assert st["graphs_recorded"] == 0 and st["computes"] == 2
+    names, _ = kc.ggml_graph_plan(L.g.nodes)
+    s = L.s
+    assert sum(n for n, _ in prof.values()) == 2 * len([n for n in names if n not in "[]"])
+    assert prof[f"decode_norm_matvec {s.q_dim}x{s.n_embd}"][0] == 2
+    assert prof[f"decode_norm_swiglu {s.n_ff}x{s.n_embd}"][0] == 2
+    assert all(ms > 0 for _, ms in prof.values())
+    be2.close()
+    L.free()
+
+
 def test_unclaimed_node_is_refused_before_any_launch():
     L = Layer(gg.LayerShape(), 9, 10, seed=700)  # 9 tokens: attention beyond attn_tokens
     be = kc.GgmlBackend()
