@@ -203,7 +203,11 @@ __global__ void quantize_k_kernel(const float* __restrict__ x, int* __restrict__
 
 // ---------------------------------------------------------------- decode matvecs
 
-template <bool Q6, int WT, bool PIPE, bool NT>
+// AF (k <= 4096: at most four activation words and one (d, sum) pair per thread): the activations
+// are loaded into registers before the first segment's weights, so the staging waits for them alone
+// (a wave's vector loads complete in issue order); else the weights go out first and the staging's
+// loads after them.
+template <bool Q6, int WT, bool PIPE, bool NT, bool AF>
 __global__ __launch_bounds__(256) void matvec_kq_kernel(const uint8_t* __restrict__ qw, const int* __restrict__ xq,
                                                         const float* __restrict__ xd, float* __restrict__ y, int rows,
                                                         int nsb, int ntiles) {
@@ -229,30 +233,59 @@ __global__ __launch_bounds__(256) void matvec_kq_kernel(const uint8_t* __restric
     const bool live = tile < ntiles;
     const uint8_t* seg0 = qw + (size_t)(live ? tile : 0) * ngroups * kSeg;
 
-    // The first segment's loads go out before the activations are staged, so both latencies overlap.
     Pieces<Q6, NT> cur;
     int g = wk;
-    if (live && g < ngroups) cur.load(seg0 + (size_t)g * kSeg, lane);
-
-    for (int i = tid; i < nsbp * 64; i += 256) {  // 4-byte loads: xq needs no 16-byte alignment
-        const int s = i >> 6, w = i & 63;
-        xs[s * kXsStride + w] = s < nsb ? xq[i] : 0;
-    }
-    for (int b = tid; b < nsbp * 8; b += 256) {
-        float d = 0.0f, sm = 0.0f;
-        if (b < nsb * 8) {
-            d = xd[2 * b];
-            sm = xd[2 * b + 1];
+    if constexpr (AF) {
+        // unconditional, clamped 4-byte loads (xq needs no 16-byte alignment), then the weights
+        const int nw = nsb * 64, nbk = nsb * 8;
+        int xw[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) xw[u] = xq[min(u * 256 + tid, nw - 1)];
+        const float d0 = xd[2 * min(tid, nbk - 1)], s0 = xd[2 * min(tid, nbk - 1) + 1];
+        if (live && g < ngroups) cur.load(seg0 + (size_t)g * kSeg, lane);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = u * 256 + tid;
+            if (i < nsbp * 64) xs[(i >> 6) * kXsStride + (i & 63)] = i < nw ? xw[u] : 0;
         }
-        dx[b] = d;
-        if (Q6) {
-            reinterpret_cast<int*>(aux)[b] = (int)sm;
-            int a = 0;
-            if (b < nsb * 8)
-                for (int w = 0; w < 4; ++w) a = dot4(0x01010101, xq[b * 8 + w], a);
-            s16[b] = a;
-        } else {
-            aux[b] = d * sm;
+        if (tid < nsbp * 8) {
+            const float d = tid < nbk ? d0 : 0.0f, sm = tid < nbk ? s0 : 0.0f;
+            dx[tid] = d;
+            if (Q6) reinterpret_cast<int*>(aux)[tid] = (int)sm;
+            else aux[tid] = d * sm;
+        }
+        if (Q6) {  // the sums of the blocks' first 16 values, from the staged words
+            __syncthreads();
+            if (tid < nsbp * 8) {
+                int a = 0;
+                if (tid < nbk)
+                    for (int w = 0; w < 4; ++w) a = dot4(0x01010101, xs[(tid >> 3) * kXsStride + (tid & 7) * 8 + w], a);
+                s16[tid] = a;
+            }
+        }
+    } else {
+        // The first segment's loads go out before the activations are staged, so both latencies overlap.
+        if (live && g < ngroups) cur.load(seg0 + (size_t)g * kSeg, lane);
+        for (int i = tid; i < nsbp * 64; i += 256) {  // 4-byte loads: xq needs no 16-byte alignment
+            const int s = i >> 6, w = i & 63;
+            xs[s * kXsStride + w] = s < nsb ? xq[i] : 0;
+        }
+        for (int b = tid; b < nsbp * 8; b += 256) {
+            float d = 0.0f, sm = 0.0f;
+            if (b < nsb * 8) {
+                d = xd[2 * b];
+                sm = xd[2 * b + 1];
+            }
+            dx[b] = d;
+            if (Q6) {
+                reinterpret_cast<int*>(aux)[b] = (int)sm;
+                int a = 0;
+                if (b < nsb * 8)
+                    for (int w = 0; w < 4; ++w) a = dot4(0x01010101, xq[b * 8 + w], a);
+                s16[b] = a;
+            } else {
+                aux[b] = d * sm;
+            }
         }
     }
     __syncthreads();
@@ -303,8 +336,18 @@ int runMatvec(const kcMatvecQ4Q8Args& a, hipStream_t s) {
     const int ntiles = tilesOf(a.rows);
     const size_t lds = matvecLds(Q6, nsb, WT);
     const int blocks = (ntiles + WT - 1) / WT;
-    hipLaunchKernelGGL((matvec_kq_kernel<Q6, WT, PIPE, NT>), dim3(blocks), dim3(256), lds, s,
-                       reinterpret_cast<const uint8_t*>(a.qw), a.xq, a.xd, a.y, a.rows, nsb, ntiles);
+    const auto* qw = reinterpret_cast<const uint8_t*>(a.qw);
+    // Activations first for a small matrix (one tile per workgroup), where they fit four words per
+    // thread: config 1 (3072 x 3072) 3.97 -> 3.74 us per matvec in a replayed graph. A large one
+    // starts its weight stream first (config 2: 48.2 against 49.5 us). Option matvec_af = 1: weights
+    // first always, 2: activations first wherever they fit.
+    const int af = option("matvec_af");
+    if (groupsOf(nsb) * kGroupSb * 64 <= 4 * 256 && af != 1 && (WT == 1 || af == 2))
+        hipLaunchKernelGGL((matvec_kq_kernel<Q6, WT, PIPE, NT, true>), dim3(blocks), dim3(256), lds, s, qw, a.xq, a.xd,
+                           a.y, a.rows, nsb, ntiles);
+    else
+        hipLaunchKernelGGL((matvec_kq_kernel<Q6, WT, PIPE, NT, false>), dim3(blocks), dim3(256), lds, s, qw, a.xq, a.xd,
+                           a.y, a.rows, nsb, ntiles);
     return fromHip(hipGetLastError(), Q6 ? "matvec_q6k_q8" : "matvec_q4k_q8");
 }
 
