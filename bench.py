@@ -674,6 +674,8 @@ def main():
                    "region_reps_ms": r2["region_reps_ms"]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic_from_profile(),
+                     "traffic_source": "not measured in this run: the committed rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE "
+                                       "figure of the same kernel and launch (profiles/traffic_matvec_q6k_cfg2.json)",
                      "kernel": "matvec_q6k_q8", "kernel_us": round(r2["kernel_ms"] * 1e3, 2)},
     }
     if r1:

@@ -186,6 +186,54 @@ static void unpack_q6k(const uint8_t* b, wblock* o) {
     }
 }
 
+/* The same bytes as unpack_q4k / unpack_q6k, 32 at a time (AVX2: the level-1 and level-2 paths). */
+__attribute__((target("avx2"))) static void unpack_q4k_avx2(const uint8_t* b, wblock* o) {
+    o->d = kco_f16_to_f32(rd16s(b));
+    o->dmin = kco_f16_to_f32(rd16s(b + 2));
+    const uint8_t* s = b + 4;
+    for (int j = 0; j < 8; ++j) {
+        if (j < 4) {
+            o->sc[j] = s[j] & 63;
+            o->sc[8 + j] = s[j + 4] & 63;
+        } else {
+            o->sc[j] = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4);
+            o->sc[8 + j] = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+        }
+    }
+    const __m256i m4 = _mm256_set1_epi8(0x0F);
+    for (int p = 0; p < 4; ++p) {
+        const __m256i v = _mm256_loadu_si256((const __m256i*)(b + 16 + 32 * p));
+        _mm256_storeu_si256((__m256i*)(o->q + 64 * p), _mm256_and_si256(v, m4));
+        _mm256_storeu_si256((__m256i*)(o->q + 64 * p + 32), _mm256_and_si256(_mm256_srli_epi16(v, 4), m4));
+    }
+}
+
+__attribute__((target("avx2"))) static void unpack_q6k_avx2(const uint8_t* b, wblock* o) {
+    o->d = kco_f16_to_f32(rd16s(b + 208));
+    o->dmin = 0.0f;
+    for (int g = 0; g < 16; ++g) o->sc[g] = (int8_t)b[192 + g];
+    const __m256i m4 = _mm256_set1_epi8(0x0F), m2 = _mm256_set1_epi8(0x03);
+    for (int n = 0; n < 2; ++n) {
+        const __m256i l0 = _mm256_loadu_si256((const __m256i*)(b + 64 * n));
+        const __m256i l1 = _mm256_loadu_si256((const __m256i*)(b + 64 * n + 32));
+        const __m256i h = _mm256_loadu_si256((const __m256i*)(b + 128 + 32 * n));
+        uint8_t* q = o->q + 128 * n;
+        /* (qh >> 2t) & 3, moved up to bits 4-5: shifts on 16-bit lanes, then the byte mask */
+        const __m256i h0 = _mm256_slli_epi16(_mm256_and_si256(h, m2), 4);
+        const __m256i h1 = _mm256_slli_epi16(_mm256_and_si256(_mm256_srli_epi16(h, 2), m2), 4);
+        const __m256i h2 = _mm256_slli_epi16(_mm256_and_si256(_mm256_srli_epi16(h, 4), m2), 4);
+        const __m256i h3 = _mm256_slli_epi16(_mm256_and_si256(_mm256_srli_epi16(h, 6), m2), 4);
+        _mm256_storeu_si256((__m256i*)(q), _mm256_or_si256(_mm256_and_si256(l0, m4), h0));
+        _mm256_storeu_si256((__m256i*)(q + 32), _mm256_or_si256(_mm256_and_si256(l1, m4), h1));
+        _mm256_storeu_si256((__m256i*)(q + 64), _mm256_or_si256(_mm256_and_si256(_mm256_srli_epi16(l0, 4), m4), h2));
+        _mm256_storeu_si256((__m256i*)(q + 96), _mm256_or_si256(_mm256_and_si256(_mm256_srli_epi16(l1, 4), m4), h3));
+    }
+}
+
+typedef void (*unpack_fn)(const uint8_t*, wblock*);
+static unpack_fn unpack4(void) { return kco_simd_level() >= 1 ? unpack_q4k_avx2 : unpack_q4k; }
+static unpack_fn unpack6(void) { return kco_simd_level() >= 1 ? unpack_q6k_avx2 : unpack_q6k; }
+
 static int threads_of(int n) {
 #ifdef _OPENMP
     return n > 0 ? n : omp_get_max_threads();
@@ -296,7 +344,7 @@ void kco_matmul_q4k_q8k_simd(const uint8_t* w, const int32_t* q, float* y, int r
             const int r0 = rb * kRB, nr = rows - r0 < kRB ? rows - r0 : kRB;
             for (size_t i = 0; i < (size_t)ncols * kRB; ++i) acc[i] = 0.0f;
             for (int s = 0; s < nsb; ++s) {
-                for (int rr = 0; rr < nr; ++rr) unpack_q4k(w + ((size_t)(r0 + rr) * nsb + s) * 144, &b[rr]);
+                for (int rr = 0; rr < nr; ++rr) unpack4()(w + ((size_t)(r0 + rr) * nsb + s) * 144, &b[rr]);
                 if (kco_simd_level() == 2) {
                     q4k_sb_vnni(b, nr, q, slot, nsb, s, ncols, ncols, acc);
                     continue;
@@ -340,7 +388,7 @@ void kco_matmul_q6k_q8k_simd(const uint8_t* w, const int32_t* q, float* y, int r
             const int r0 = rb * kRB, nr = rows - r0 < kRB ? rows - r0 : kRB;
             for (size_t i = 0; i < (size_t)ncols * kRB; ++i) acc[i] = 0.0f;
             for (int s = 0; s < nsb; ++s) {
-                for (int rr = 0; rr < nr; ++rr) unpack_q6k(w + ((size_t)(r0 + rr) * nsb + s) * 210, &b[rr]);
+                for (int rr = 0; rr < nr; ++rr) unpack6()(w + ((size_t)(r0 + rr) * nsb + s) * 210, &b[rr]);
                 if (kco_simd_level() == 2) {
                     q6k_sb_vnni(b, nr, q, slot, nsb, s, ncols, ncols, acc);
                     continue;
@@ -372,12 +420,13 @@ void kco_matvec_q4k_q8_simd(const uint8_t* w, const int32_t* xq, const float* xd
                             int nthreads) {
     const int nsb = k / 256;
     const dots_fn dot = dots32();
+    const unpack_fn unpack = unpack4();
 #pragma omp parallel for num_threads(threads_of(nthreads)) schedule(static)
     for (int r = 0; r < rows; ++r) {
         float acc = 0.0f;
         for (int s = 0; s < nsb; ++s) {
             wblock b;
-            unpack_q4k(w + ((size_t)r * nsb + s) * 144, &b);
+            unpack(w + ((size_t)r * nsb + s) * 144, &b);
             int32_t S[8];
             dot(b.q, (const int8_t*)(xq + (size_t)s * 64), S);
             float fd = 0.0f, fm = 0.0f;
@@ -397,6 +446,7 @@ void kco_matvec_q6k_q8_simd(const uint8_t* w, const int32_t* xq, const float* xd
                             int nthreads) {
     const int nsb = k / 256, nb = k / 32;
     const dots_fn dot = dots16();
+    const unpack_fn unpack = unpack6();
     /* the sums of the first 16 values of every block of 32 (the activation side, once per call) */
     int32_t* sa = (int32_t*)malloc(sizeof(int32_t) * (size_t)nb);
     const int8_t* x8 = (const int8_t*)xq;
@@ -410,7 +460,7 @@ void kco_matvec_q6k_q8_simd(const uint8_t* w, const int32_t* xq, const float* xd
         float acc = 0.0f;
         for (int s = 0; s < nsb; ++s) {
             wblock b;
-            unpack_q6k(w + ((size_t)r * nsb + s) * 210, &b);
+            unpack(w + ((size_t)r * nsb + s) * 210, &b);
             int32_t S[16];
             dot(b.q, (const int8_t*)(xq + (size_t)s * 64), S);
             for (int n = 0; n < 2; ++n) {
