@@ -217,7 +217,7 @@ bool supports(const kcGgmlConfig& c, const T* op) {
             return f32c(s0) && f32c(op) && sameShape(s0, op);
         case KC_GGML_OP_ADD:
             return f32c(s0) && f32c(s1) && f32c(op) && sameShape(s0, s1) && sameShape(s0, op);
-        case KC_GGML_OP_MUL:  // by a row vector (norm weight, n % 8 == 0) or elementwise
+        case KC_GGML_OP_MUL:  // s1 broadcast over the rows of s0 (rows a multiple of 8 wide), or same-shape
             return f32c(s0) && f32c(s1) && f32c(op) && sameShape(s0, op) &&
                    ((rowVectorOf(s1, s0) && s0->ne[0] % 8 == 0) || (sameShape(s0, s1) && nelements(s0) % 8 == 0));
         case KC_GGML_OP_ROPE: {
@@ -229,7 +229,7 @@ bool supports(const kcGgmlConfig& c, const T* op) {
                    s1->type == KC_GGML_TYPE_I32 && contiguous(s1) && s1->ne[0] == s0->ne[2] &&
                    (!ff || (f32c(ff) && ff->ne[0] >= s0->ne[0] / 2));
         }
-        case KC_GGML_OP_SET_ROWS:  // into the fp16 KV cache
+        case KC_GGML_OP_SET_ROWS:  // f32 rows stored as fp16 at i64 row indices of a KV-buffer tensor
             return c.attn && s0 && s1 && inKv(op) && op->type == KC_GGML_TYPE_F16 && op->nb[0] == 2 &&
                    op->nb[1] % 4 == 0 && op->ne[2] == 1 && op->ne[3] == 1 && op->ne[1] <= INT32_MAX &&
                    s0->type == KC_GGML_TYPE_F32 && s0->nb[0] == 4 && s0->nb[1] % 4 == 0 && s0->ne[0] == op->ne[0] &&
