@@ -36,6 +36,7 @@
 // so stores of y (column-major, y + c * rows) are contiguous 128-byte runs.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <type_traits>
 #include <vector>
@@ -638,21 +639,27 @@ int runMfma8(const kcMatmulKQ8Args& a, hipStream_t s) {
 // mins[c][s][16] = [64 (B_j >> 6) for j < 8 | B_j & 63 for j < 8] (B_j = sum of the 32 values of
 // sub-block j, the reference's byte split); xdT[s][c] = the scale of column c's super-block s
 // (0 for the padding columns ncols <= c < ncp).
-__global__ void act_to_f16_kernel(const int* __restrict__ xq, uint2* __restrict__ act, h8* __restrict__ mins,
-                                  float* __restrict__ xdT, int nsb, long long words, int ncols, int ncp) {
-    const long long i = blockIdx.x * 256LL + threadIdx.x;
-    const long long per = (long long)nsb * 64;
-    if (i < words) {
-        const long long c = i / per, w = i - c * per;
-        act[i] = i8x4_to_h4x16((uint32_t)xq[c * nsb * 85 + w]);
+// One thread per 16 activations of a column (four slot words in, 32 bytes out), and per entry of
+// xdT and of the min operands; 32-bit indices (the launcher keeps ncols * k * 2 below 2^32).
+__global__ void act_to_f16_kernel(const int* __restrict__ xq, uint4* __restrict__ act, h8* __restrict__ mins,
+                                  float* __restrict__ xdT, int nsb, unsigned quads, int ncols, int ncp) {
+    const unsigned i = blockIdx.x * 256u + threadIdx.x;
+    const unsigned per = (unsigned)nsb * 16u;  // 16-value groups per column
+    if (i < quads) {
+        const unsigned c = i / per, w = (i - c * per) * 4u;
+        const int* src = xq + (size_t)c * nsb * 85 + w;
+        const uint2 a0 = i8x4_to_h4x16((uint32_t)src[0]), a1 = i8x4_to_h4x16((uint32_t)src[1]);
+        const uint2 a2 = i8x4_to_h4x16((uint32_t)src[2]), a3 = i8x4_to_h4x16((uint32_t)src[3]);
+        act[2 * (size_t)i] = make_uint4(a0.x, a0.y, a1.x, a1.y);
+        act[2 * (size_t)i + 1] = make_uint4(a2.x, a2.y, a3.x, a3.y);
     }
-    if (i < (long long)nsb * ncp) {
-        const long long sx = i / ncp, c = i - sx * ncp;
-        xdT[i] = c < ncols ? reinterpret_cast<const float*>(xq + c * nsb * 85 + nsb * 64)[sx] : 0.0f;
+    if (i < (unsigned)nsb * (unsigned)ncp) {
+        const unsigned sx = i / (unsigned)ncp, c = i - sx * (unsigned)ncp;
+        xdT[i] = (int)c < ncols ? reinterpret_cast<const float*>(xq + (size_t)c * nsb * 85 + nsb * 64)[sx] : 0.0f;
     }
-    if (mins && i < (long long)ncols * nsb) {
-        const long long c = i / nsb, sx = i - c * nsb;
-        const int* pw = xq + c * nsb * 85 + nsb * 81 + sx * 4;
+    if (mins && i < (unsigned)ncols * (unsigned)nsb) {
+        const unsigned c = i / (unsigned)nsb, sx = i - c * (unsigned)nsb;
+        const int* pw = xq + (size_t)c * nsb * 85 + nsb * 81 + sx * 4;
         const int w0 = pw[0], w1 = pw[1], w2 = pw[2], w3 = pw[3];
         h8 lo, hi;
 #pragma unroll
@@ -662,8 +669,8 @@ __global__ void act_to_f16_kernel(const int* __restrict__ xq, uint2* __restrict_
             lo[j] = (_Float16)(float)(64 * hb);
             hi[j] = (_Float16)(float)lb;
         }
-        mins[2 * i] = lo;
-        mins[2 * i + 1] = hi;
+        mins[2 * (size_t)i] = lo;
+        mins[2 * (size_t)i + 1] = hi;
     }
 }
 
@@ -1069,7 +1076,11 @@ int runMfmaH(const MmPart* parts, int nparts, const int* xq, int k, int ncols, i
     const int nsb = k / 256;
     long long tiles8 = 0;
     for (int i = 0; i < nparts; ++i) tiles8 += (parts[i].rows + 255) / 256;
-    const int nw = hWaves(tiles8 * ((ncols + G::kCols - 1) / G::kCols) * ks), wg_rows = 32 * nw;
+    // Q4_K parts only: the producer-wavefront kernel (256-row tiles) unless option matmul_ws = 1
+    bool ws = option("matmul_ws") != 1 && (option("matmul_path") == 0 || option("matmul_path") == 2);
+    for (int i = 0; i < nparts; ++i) ws = ws && !parts[i].q6;
+    const int nw = ws ? 8 : hWaves(tiles8 * ((ncols + G::kCols - 1) / G::kCols) * ks);
+    const int wg_rows = ws ? mfmaWsRows() : 32 * nw;
     HGroup g{};
     bool any_q4 = false;
     int tiles = 0;
@@ -1094,12 +1105,20 @@ int runMfmaH(const MmPart* parts, int nparts, const int* xq, int k, int ncols, i
         mins = static_cast<_Float16*>(act) + (size_t)ncols * k;
         xdT = reinterpret_cast<float*>(mins + (size_t)ncols * nsb * 16);
         ncp = actCols(ncols);
-        hipLaunchKernelGGL(act_to_f16_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, s, xq,
-                           static_cast<uint2*>(act), any_q4 ? reinterpret_cast<h8*>(mins) : nullptr, xdT, nsb, words,
-                           ncols, ncp);
+        const long long quads = words / 4, threads = std::max(quads, (long long)nsb * ncp);
+        hipLaunchKernelGGL(act_to_f16_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, xq,
+                           static_cast<uint4*>(act), any_q4 ? reinterpret_cast<h8*>(mins) : nullptr, xdT, nsb,
+                           (unsigned)quads, ncols, ncp);
     }
     if (option("matmul_path") == 7)  // the wide-tile kernel (every weight dequantized once per workgroup)
         return launchMfmaW(g, tiles, act, mins, xdT, nsb, ncols, ncp, s);
+    if (ws && mfmaWsFits(g, nsb, ncols)) return launchMfmaWs(g, tiles, act, mins, xdT, nsb, ncols, ncp, s);
+    if (ws) {  // beyond the 32-bit offsets: the 8-wavefront kernel over the same 256-row tiles
+        const dim3 grid(tiles, (ncols + G::kCols - 1) / G::kCols, ks);
+        hipLaunchKernelGGL(matmul_kq_mfma_h_kernel<8>, grid, dim3(512), G::kLds, s, g,
+                           static_cast<const _Float16*>(act), mins, xdT, nsb, ncols, ncp);
+        return fromHip(hipGetLastError(), "matmul_q4k/q6k_q8k (MFMA)");
+    }
     const dim3 grid(tiles, (ncols + G::kCols - 1) / G::kCols, ks);
     if (nw == 8)
         hipLaunchKernelGGL(matmul_kq_mfma_h_kernel<8>, grid, dim3(512), G::kLds, s, g,
@@ -1134,8 +1153,24 @@ int cuCount() {
     return cus[dev];
 }
 
-// y += p over n floats (the second K half of a split launch).
+// y += p over n floats (the second K half of a split launch): four per thread (both arrays 16-byte
+// aligned, as the launcher checks), the last n % 4 one each.
 __global__ void add_partial_kernel(float* __restrict__ y, const float* __restrict__ p, long long n) {
+    const long long i = blockIdx.x * 256LL + threadIdx.x, i4 = 4 * i;
+    if (i4 + 3 < n) {
+        float4 a = reinterpret_cast<const float4*>(y)[i];
+        const float4 b = reinterpret_cast<const float4*>(p)[i];
+        a.x += b.x;
+        a.y += b.y;
+        a.z += b.z;
+        a.w += b.w;
+        reinterpret_cast<float4*>(y)[i] = a;
+    } else {
+        for (long long j = i4; j < n; ++j) y[j] += p[j];
+    }
+}
+// The same one float per thread (y not 16-byte aligned).
+__global__ void add_partial1_kernel(float* __restrict__ y, const float* __restrict__ p, long long n) {
     const long long i = blockIdx.x * 256LL + threadIdx.x;
     if (i < n) y[i] += p[i];
 }
@@ -1154,7 +1189,11 @@ int runStaged(bool q6k, const kcMatmulKQ8Args& a, int ks, void* buf, hipStream_t
     if (int st = runMfmaH(&part, 1, a.xq, a.k, a.ncols, ks, buf, s)) return st;
     if (ks == 1) return 0;
     const long long n = (long long)a.rows * a.ncols;
-    hipLaunchKernelGGL(add_partial_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a.y, partial, n);
+    if (reinterpret_cast<uintptr_t>(a.y) % 16 == 0)  // (the partial sums are 256-byte aligned)
+        hipLaunchKernelGGL(add_partial_kernel, dim3((unsigned)((n / 4 + 1 + 255) / 256)), dim3(256), 0, s, a.y, partial,
+                           n);
+    else
+        hipLaunchKernelGGL(add_partial1_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a.y, partial, n);
     return fromHip(hipGetLastError(), "matmul (MFMA, K split): partial sum");
 }
 

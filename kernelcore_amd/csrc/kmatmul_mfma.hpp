@@ -30,4 +30,12 @@ struct MfmaGroup {
 int launchMfmaW(const MfmaGroup& g, int tiles, const void* act, const void* mins, const float* xdT, int nsb, int ncols,
                 int ncp, hipStream_t s);
 
+// The producer-wavefront kernel (kmatmul_mfmaws.hip): Q4_K parts only, 256-row tiles (tile0 in
+// units of mfmaWsRows()); mfmaWsFits says whether g's parts and the activations fit its 32-bit
+// buffer offsets.
+int mfmaWsRows();
+bool mfmaWsFits(const MfmaGroup& g, int nsb, int ncols);
+int launchMfmaWs(const MfmaGroup& g, int tiles, const void* act, const void* mins, const float* xdT, int nsb, int ncols,
+                 int ncp, hipStream_t s);
+
 }  // namespace kcamd

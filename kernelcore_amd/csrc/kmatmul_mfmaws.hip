@@ -1,0 +1,307 @@
+// kmatmul_mfmaws.hip -- the prefill matmul for Q4_K weights with producer and consumer wavefronts
+// (gfx950): Y = W X for per-256 8-bit activations, the arithmetic of kmatmul_mfma.hip (exact integer
+// sums per super-block on v_mfma_f32_32x32x16_f16, the reference's combine per super-block;
+// reference kernels/llm/matmul_q4k_q8kx8.cu, mirror llm/llm_reference.cpp:529-596).
+//
+// A wavefront stalls at each vector-memory instruction until the CU's memory unit takes it (about
+// 20 cycles per instruction), and a wavefront that stalls issues neither matrix ops nor the VALU
+// dequantization that feeds them. So the loads get wavefronts of their own: a workgroup of 12
+// wavefronts owns 256 weight rows x 64 activation columns,
+//   - 8 consumer wavefronts (two per SIMD), each 32 weight rows x 64 columns as two 32 x 32 blocks:
+//     they only read LDS, dequantize and issue matrix ops (the K-step pipeline of
+//     kmatmul_mfma.hip's hTile, with the weights read from LDS instead of memory);
+//   - 4 producer wavefronts (one per SIMD) issue every load of a super-block, straight into LDS
+//     with buffer-to-LDS loads: the activation tile (fp16, 16 x, as act_to_f16 or the quantizers
+//     write it), the min operands, the column scales, and the weights of the 256 rows (the
+//     super-block's header slab and eight qs slabs of each 16-row tile).
+// Two LDS stages (72 KiB each): while the consumers compute super-block s from one, the producers
+// fill the other with s + 1 and wait for their loads; one barrier per super-block hands it over.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "internal.hpp"
+#include "kmatmul_mfma.hpp"
+#include "kquant.hpp"
+
+namespace kcamd {
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef uint32_t u32v4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void* LdsPtr;
+
+constexpr int kCons = 8;                       // consumer wavefronts
+constexpr int kProd = 4;                       // producer wavefronts
+constexpr int kThreads = 64 * (kCons + kProd);
+constexpr int kRows = 32 * kCons;              // weight rows per workgroup
+constexpr int kCols = 64;                      // activation columns per workgroup
+constexpr int kColB = 528;                     // LDS bytes per column: 32 chunks of 16 B + 1 pad chunk
+constexpr int kActLoads = kCols * 33 / 64;     // 1 KiB direct loads of the activation tile
+constexpr int kMinOff = kActLoads * 1024;      // Q4_K min operands: 32 B per column
+constexpr int kXdOff = kMinOff + kCols * 32;   // column scales (one 1 KiB load, 256 B used)
+constexpr int kWOff = kXdOff + 1024;           // weights: [tile][slab][16 rows x 16 B]
+constexpr int kTiles = kRows / kTileRows;      // 16-row tiles per workgroup
+constexpr int kWLoads = kTiles * kQ4kSlabs / 4;  // each load: four (tile, slab) chunks of 256 B
+constexpr int kStage = kWOff + kTiles * kQ4kSlabs * 256;
+constexpr int kLdsBytes = 2 * kStage;
+constexpr int kLoads = kActLoads + 2 + 1 + kWLoads;  // per super-block
+constexpr int kPerProd = kLoads / kProd;
+static_assert(kLoads % kProd == 0 && kWLoads * 4 == kTiles * kQ4kSlabs, "load split");
+static_assert(kLdsBytes <= 160 * 1024, "LDS");
+
+__device__ __forceinline__ h2 bits_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t bufRes(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+// Eight 4-bit weights (nibble hiNib of 8 bytes) times a sub-block scale, as exact fp16 (the
+// operand of kmatmul_mfma.hip's dequant8s: (1024 + q) m2 + s2).
+__device__ __forceinline__ h8 nib8(uint2 q, bool hiNib, h2 m2, h2 s2) {
+    const uint32_t mask = hiNib ? 0xFFF0FFF0u : 0xFF0FFF0Fu;
+    h8 r;
+    const uint32_t w[2] = {q.x, q.y};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const h2 a = bits_h2(__builtin_amdgcn_perm(0x64646464u, w[i], 0x04010400u) & mask);
+        const h2 b = bits_h2(__builtin_amdgcn_perm(0x64646464u, w[i], 0x04030402u) & mask);
+        const h2 ra = __builtin_elementwise_fma(a, m2, s2);
+        const h2 rb = __builtin_elementwise_fma(b, m2, s2);
+        r[4 * i + 0] = ra[0];
+        r[4 * i + 1] = ra[1];
+        r[4 * i + 2] = rb[0];
+        r[4 * i + 3] = rb[1];
+    }
+    return r;
+}
+
+struct WsArgs {
+    const _Float16* act;
+    const _Float16* mins;
+    const float* xdT;
+    int nsb, ncols, ncp;
+};
+
+// The producers' loads of super-block s into stage buf. Load L = kProd r + p of the kLoads:
+// activation chunks, then the min operands, the column scales, the weight chunks; voff[r] is this
+// lane's byte offset of load r at super-block 0 of the array it reads (the super-block's part is
+// the uniform soffset).
+__device__ __forceinline__ void produce(char* buf, int p, int lane, const uint32_t (&voff)[kPerProd],
+                                        __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rm,
+                                        __amdgpu_buffer_rsrc_t rx, __amdgpu_buffer_rsrc_t rw, int s, int ncp) {
+    (void)lane;
+#pragma unroll
+    for (int r = 0; r < kPerProd; ++r) {
+        const int L = kProd * r + p;
+        if (L < kActLoads) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (LdsPtr)(buf + L * 1024), 16, voff[r], (uint32_t)s * 512u, 0, 0);
+        } else if (L < kActLoads + 2) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (LdsPtr)(buf + kMinOff + (L - kActLoads) * 1024), 16, voff[r],
+                                                     (uint32_t)s * 32u, 0, 0);
+        } else if (L == kActLoads + 2) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (LdsPtr)(buf + kXdOff), 16, voff[r], (uint32_t)(s * ncp) * 4u, 0,
+                                                     0);
+        } else {
+            const int wl = L - (kActLoads + 3);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (LdsPtr)(buf + kWOff + wl * 1024), 16, voff[r],
+                                                     (uint32_t)((s >> 2) * kQ4kSeg + (s & 3) * 256), 0, 0);
+        }
+    }
+}
+
+// One workgroup: rows rowTile * 256 .., columns colTile * 64 .., super-blocks [sb0, sb1).
+__device__ __forceinline__ void wsTile(char* lbase, const uint8_t* __restrict__ qw, const WsArgs& a,
+                                       float* __restrict__ y, int rows, int rowTile, int colTile, int sb0, int sb1) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nsb = a.nsb, ncols = a.ncols, k = nsb * 256;
+    const int col0 = colTile * kCols;
+    const int ngroups = (nsb + kGroupSb - 1) / kGroupSb;
+    const int tiles_stream = (rows + kTileRows - 1) / kTileRows;
+    const bool prod = wave >= kCons;
+
+    if (prod) {
+        const int p = wave - kCons;
+        const __amdgpu_buffer_rsrc_t ra = bufRes(a.act, (uint32_t)ncols * (uint32_t)k * 2u);
+        const __amdgpu_buffer_rsrc_t rm = bufRes(a.mins, (uint32_t)ncols * (uint32_t)nsb * 32u);
+        const __amdgpu_buffer_rsrc_t rx = bufRes(a.xdT, (uint32_t)nsb * (uint32_t)a.ncp * 4u);
+        const __amdgpu_buffer_rsrc_t rw = bufRes(qw, (uint32_t)tiles_stream * (uint32_t)ngroups * (uint32_t)kQ4kSeg);
+        uint32_t voff[kPerProd];
+#pragma unroll
+        for (int r = 0; r < kPerProd; ++r) {
+            const int L = kProd * r + p;
+            if (L < kActLoads) {  // columns past ncols read column 0 (never stored)
+                const int slot = L * 64 + lane, c = slot / 33, kc = slot - 33 * c;
+                const int cc = col0 + c < ncols ? col0 + c : 0;
+                voff[r] = (uint32_t)cc * (uint32_t)k * 2u + (uint32_t)(kc == 32 ? 0 : kc) * 16u;
+            } else if (L < kActLoads + 2) {
+                const int p2 = (L - kActLoads) * 64 + lane, c = p2 >> 1;
+                const int cc = col0 + c < ncols ? col0 + c : 0;
+                voff[r] = (uint32_t)((cc * nsb * 16 + (p2 & 1) * 8) * 2);
+            } else if (L == kActLoads + 2) {
+                voff[r] = (uint32_t)((col0 + (lane & 15) * 4) * 4);
+            } else {  // tiles past the stream read tile 0 (their rows are never stored)
+                const int q = (L - (kActLoads + 3)) * 4 + (lane >> 4), t = q / kQ4kSlabs, j = q - kQ4kSlabs * t;
+                int tg = rowTile * kTiles + t;
+                if (tg >= tiles_stream) tg = 0;
+                voff[r] = (uint32_t)tg * (uint32_t)ngroups * (uint32_t)kQ4kSeg + (uint32_t)(j * 1024 + (lane & 15) * 16);
+            }
+        }
+        produce(lbase, p, lane, voff, ra, rm, rx, rw, sb0, a.ncp);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        for (int s = sb0; s < sb1; ++s) {
+            const int b = (s - sb0) & 1;
+            if (s + 1 < sb1) produce(lbase + (b ^ 1) * kStage, p, lane, voff, ra, rm, rx, rw, s + 1, a.ncp);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+        }
+        return;
+    }
+
+    // consumer wavefront: rows rowTile * 256 + wave * 32 + lane % 32, lane half h
+    const int h = lane >> 5, l32 = lane & 31;
+    const int row = rowTile * kRows + wave * 32 + l32;
+    const int woff = kWOff + (wave * 2 + (l32 >> 4)) * kQ4kSlabs * 256 + (l32 & 15) * 16;
+    int aoff[2];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) aoff[cb] = (cb * 32 + l32) * kColB + h * 32;
+    f16v acc[2];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[cb][i] = 0.0f;
+    const f16v zero = acc[0];
+    __syncthreads();  // stage 0 loaded
+    for (int s = sb0; s < sb1; ++s) {
+        const char* buf = lbase + ((s - sb0) & 1) * kStage;
+        // the row's super-block: header (d, dmin, 12 scale / min bytes) and the qs chunks of this half
+        const uint4 hdr = *reinterpret_cast<const uint4*>(buf + woff);
+        uint4 q16[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) q16[j] = *reinterpret_cast<const uint4*>(buf + woff + (1 + 2 * j + h) * 256);
+        h8 av[2], an[2];
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) av[cb] = *reinterpret_cast<const h8*>(buf + aoff[cb]);
+        const float d = (float)__builtin_bit_cast(_Float16, (unsigned short)(hdr.x & 0xFFFFu));
+        const float dmin = (float)__builtin_bit_cast(_Float16, (unsigned short)(hdr.x >> 16));
+        const int s0 = (int)hdr.y, s1 = (int)hdr.z, s2 = (int)hdr.w;
+        const int scw[2] = {s0 & 0x3F3F3F3F, (s2 & 0x0F0F0F0F) | ((s0 >> 2) & 0x30303030)};
+        const int mw[2] = {s1 & 0x3F3F3F3F, ((s2 >> 4) & 0x0F0F0F0F) | ((s1 >> 2) & 0x30303030)};
+        h2 m2[8], c2[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            // sc q / 16 (the activations are 16 x): (1024 + q) sc / 16 - 64 sc for a low nibble,
+            // (1024 + 16 q) sc / 256 - 4 sc for a high one; exact (sc / 256 >= 2^-8, q sc <= 945)
+            const _Float16 sc = (_Float16)(float)((scw[j >> 2] >> (8 * (j & 3))) & 255);
+            const _Float16 mul = (j & 1) ? sc * (_Float16)0.00390625f : sc * (_Float16)0.0625f;
+            const _Float16 sub = (j & 1) ? sc * (_Float16)(-4.0f) : sc * (_Float16)(-64.0f);
+            m2[j] = h2{mul, mul};
+            c2[j] = h2{sub, sub};
+        }
+        // K-step t covers, in lane half h, k = 64 (t >> 2) + 32 ((t >> 1) & 1) + 16 h + 8 (t & 1):
+        // qs bytes 32 (t >> 2) + 16 h + 8 (t & 1) (chunk t >> 2, nibble (t >> 1) & 1), activation
+        // chunk at byte 64 (t >> 1) + 32 h + 16 (t & 1) of the column; step t + 1's operands are
+        // read and dequantized while step t runs its matrix ops
+        auto bytes = [&](int t) {
+            const uint4 q = q16[t >> 2];
+            return (t & 1) ? make_uint2(q.z, q.w) : make_uint2(q.x, q.y);
+        };
+        f16v is[2];
+        h8 bq = nib8(bytes(0), false, m2[0], c2[0]), bn;
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            if (t + 1 < 16) {
+                const int tn = t + 1, toff = 64 * (tn >> 1) + 16 * (tn & 1), j = tn >> 1;
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb) an[cb] = *reinterpret_cast<const h8*>(buf + aoff[cb] + toff);
+                bn = nib8(bytes(tn), j & 1, m2[j], c2[j]);
+            }
+            // (scheduling fences: the next step's reads and dequantization stay ahead of this
+            // step's matrix ops instead of being sunk to just before their use)
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb)
+                is[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[cb], bq, t == 0 ? zero : is[cb], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (t + 1 < 16) {
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb) av[cb] = an[cb];
+                bq = bn;
+            }
+        }
+        // the min term (one matrix op per block against [64 (B >> 6) | B & 63]) and the combine
+        h8 bm;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) bm[e] = (_Float16)(float)((mw[e >> 2] >> (8 * (e & 3))) & 255);
+        const _Float16* xm = reinterpret_cast<const _Float16*>(buf + kMinOff);
+        const char* xdl = buf + kXdOff;
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+            const h8 am = *reinterpret_cast<const h8*>(xm + (cb * 32 + l32) * 16 + 8 * h);
+            const f16v im = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, zero, 0, 0, 0);
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                // (each element copied to a scalar before its bit cast: a bit cast of the vector
+                // element itself compiles to element 0 for all four)
+                const u32v4 xdw = *reinterpret_cast<const u32v4*>(xdl + (cb * 32 + q4 * 8 + h * 4) * 4);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int i = 4 * q4 + e;
+                    const uint32_t wv = xdw[e];
+                    const float t2 = __builtin_fmaf(-dmin, im[i], d * is[cb][i]);
+                    acc[cb][i] = __builtin_fmaf(__builtin_bit_cast(float, wv), t2, acc[cb][i]);
+                }
+            }
+        }
+        __syncthreads();  // stage read: the producers may refill it; the next stage is loaded
+    }
+    if (row < rows) {
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int c = col0 + cb * 32 + (i >> 2) * 8 + h * 4 + (i & 3);
+                if (c < ncols) y[(size_t)c * rows + row] = acc[cb][i];
+            }
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void matmul_q4k_mfma_ws_kernel(MfmaGroup g, WsArgs a) {
+    extern __shared__ int4 lds4[];
+    char* lbase = reinterpret_cast<char*>(lds4);
+    const int bx = blockIdx.x;
+    const int pi = (g.nparts > 2 && bx >= g.p[2].tile0) ? 2 : (g.nparts > 1 && bx >= g.p[1].tile0) ? 1 : 0;
+    const MfmaPart& p = g.p[pi];
+    const int z = blockIdx.z, sb0 = z * a.nsb / g.ks, sb1 = (z + 1) * a.nsb / g.ks;
+    wsTile(lbase, p.qw, a, p.y[z], p.rows, bx - p.tile0, blockIdx.y, sb0, sb1);
+}
+
+}  // namespace
+
+int mfmaWsRows() { return kRows; }
+
+bool mfmaWsFits(const MfmaGroup& g, int nsb, int ncols) {
+    for (int i = 0; i < g.nparts; ++i) {
+        if (g.p[i].q6) return false;
+        const unsigned long long wbytes =
+            (unsigned long long)tilesOf(g.p[i].rows) * (unsigned long long)groupsOf(nsb) * kQ4kSeg;
+        if (wbytes >= (1ull << 32)) return false;
+    }
+    return (unsigned long long)ncols * nsb * 512ull < (1ull << 32);
+}
+
+int launchMfmaWs(const MfmaGroup& g, int tiles, const void* act, const void* mins, const float* xdT, int nsb, int ncols,
+                 int ncp, hipStream_t s) {
+    static const int attr = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(matmul_q4k_mfma_ws_kernel),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+    if (attr != 0) return fromHip(attr, "matmul (MFMA, producer wavefronts): LDS size");
+    const WsArgs a{static_cast<const _Float16*>(act), static_cast<const _Float16*>(mins), xdT, nsb, ncols, ncp};
+    const dim3 grid(tiles, (ncols + kCols - 1) / kCols, g.ks);
+    hipLaunchKernelGGL(matmul_q4k_mfma_ws_kernel, grid, dim3(kThreads), kLdsBytes, s, g, a);
+    return fromHip(hipGetLastError(), "matmul_q4k_q8k (MFMA, producer wavefronts)");
+}
+
+}  // namespace kcamd

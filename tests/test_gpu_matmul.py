@@ -150,13 +150,15 @@ def test_mfma_matmul_matches_oracle(qtype, rows, k, ncols):
     note(f"mfma {qtype} {rows}x{k} ncols={ncols}")
     w = kq.random_blocks(qtype, rows, k, seed=rows + 3 * k + ncols)
     x = kq.randn(k * ncols, ncols + 5, 1.5)
-    kc.set_option("matmul_path", 2)
+    kc.set_option("matmul_path", 2)  # Q4_K: the producer-wavefront kernel (kmatmul_mfmaws.hip)
     y, _ = run_matmul(qtype, True, w, x, rows, k, ncols)
     ys = {}
+    kc.set_option("matmul_ws", 1)
     for nw in (4, 8):  # workgroups of 4 wavefronts (128 rows) and of 8 (256 rows, staggered loads)
         kc.set_option("matmul_waves", nw)
         ys[nw], _ = run_matmul(qtype, True, w, x, rows, k, ncols)
     kc.set_option("matmul_waves", 0)
+    kc.set_option("matmul_ws", 0)
     kc.set_option("matmul_path", 1)
     yc, _ = run_matmul(qtype, True, w, x, rows, k, ncols)
     kc.set_option("matmul_path", 7)  # the wide-tile kernel (kmatmul_mfmaw.hip)
@@ -167,8 +169,9 @@ def test_mfma_matmul_matches_oracle(qtype, rows, k, ncols):
     for got in (y, ys[4], ys[8], yw):
         assert kq.rel_diff(got, want) < TOL
         assert kq.rel_diff(got, want) < 1e-5  # exact integers; only the final float combine differs
-    # the workgroup shape changes no output's arithmetic
+    # the workgroup shape, and loads issued by wavefronts of their own, change no output's arithmetic
     assert np.array_equal(kq.bits(ys[4]), kq.bits(ys[8]))
+    assert np.array_equal(kq.bits(y), kq.bits(ys[8]))
 
 
 def test_mfma_matmul_config3_shapes():
@@ -180,14 +183,18 @@ def test_mfma_matmul_config3_shapes():
         x = kq.randn(k * ncols, seed + 1)
         want = np.zeros(rows * ncols, np.float32)
         got = {}
-        for nw in (4, 8, 0):
+        kc.set_option("matmul_ws", 1)  # the 4- and 8-wavefront kernels
+        for nw in (4, 8):
             kc.set_option("matmul_waves", nw)
             got[nw], slots = run_matmul("q4k", True, w, x, rows, k, ncols)
         kc.set_option("matmul_waves", 0)
+        kc.set_option("matmul_ws", 0)
+        got[0], slots = run_matmul("q4k", True, w, x, rows, k, ncols)  # the default: producer wavefronts
         O.kco_matmul_q4k_q8k_mt(w, slots, want, rows, k, ncols, O.kco_max_threads())
         for nw, y in got.items():
             assert kq.rel_diff(y, want.reshape(ncols, rows)) < TOL, nw
         assert np.array_equal(kq.bits(got[4]), kq.bits(got[8]))
+        assert np.array_equal(kq.bits(got[0]), kq.bits(got[8]))
 
 
 def test_captured_matmul_keeps_its_scratch_after_an_eager_growth():
