@@ -38,6 +38,7 @@ from kernelcore_amd import synth  # noqa: E402
 
 PEAK_HBM_GBS = 8000.0
 PEAK_F16_TFLOPS = 2500.0  # dense fp16 MFMA
+PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA (the bound the config-3 workload names: 8-bit products)
 METRIC = "Q4_K matvec HBM GB/s (% of peak); decode tok/s, 3B-shape Q4_K_M, 1 GPU"
 
 
@@ -194,7 +195,8 @@ def prefill_matmul_run(steps, seed, reps):
     return {"workload": "BASELINE config 3: gate + up (8192x3072) + down (3072x8192) Q4_K matmuls, 512 tokens, "
                         "weights N(0, 0.02) quantized as ggml does",
             "ms_per_step": round(ms, 4), "ops_per_step": ops, "achieved_tops": round(tops, 1),
-            "peak_tops": PEAK_F16_TFLOPS, "mfma_util": round(tops / PEAK_F16_TFLOPS, 4), "reps": reps,
+            "peak_tops": PEAK_F16_TFLOPS, "mfma_util": round(tops / PEAK_F16_TFLOPS, 4),
+            "peak_int8_tops": PEAK_INT8_TOPS, "mfma_util_int8": round(tops / PEAK_INT8_TOPS, 4), "reps": reps,
             "mfma": "v_mfma_f32_32x32x16_f16 on exact small-integer operands", "finite": bool(finite)}
 
 
