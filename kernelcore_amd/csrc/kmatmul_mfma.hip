@@ -1092,6 +1092,11 @@ int runMfmaH(const MmPart* parts, int nparts, const int* xq, int k, int ncols, i
     }
     g.nparts = nparts;
     g.ks = ks;
+    // slots handed over (no quantizer-written fp16 operands): the producer wavefronts convert them
+    // themselves, unless option matmul_ws = 2 (a conversion launch first, as for the other kernels)
+    if (ws && !pre && option("matmul_ws") != 2 && option("matmul_path") != 7 && mfmaWsSlotsFits(nsb) &&
+        mfmaWsFits(g, nsb, ncols))
+        return launchMfmaWsSlots(g, tiles, xq, nsb, ncols, s);
     const long long words = (long long)ncols * nsb * 64;
     _Float16* mins;
     float* xdT;

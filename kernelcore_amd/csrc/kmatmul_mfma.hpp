@@ -37,5 +37,9 @@ int mfmaWsRows();
 bool mfmaWsFits(const MfmaGroup& g, int nsb, int ncols);
 int launchMfmaWs(const MfmaGroup& g, int tiles, const void* act, const void* mins, const float* xdT, int nsb, int ncols,
                  int ncp, hipStream_t s);
+// The same kernel reading the per-256 int8 slots (xq) itself: no fp16 conversion launch before it
+// (k a multiple of 1024: mfmaWsSlotsFits).
+bool mfmaWsSlotsFits(int nsb);
+int launchMfmaWsSlots(const MfmaGroup& g, int tiles, const int* xq, int nsb, int ncols, hipStream_t s);
 
 }  // namespace kcamd

@@ -16,6 +16,9 @@
 //     super-block's header slab and eight qs slabs of each 16-row tile).
 // Two LDS stages (72 KiB each): while the consumers compute super-block s from one, the producers
 // fill the other with s + 1 and wait for their loads; one barrier per super-block hands it over.
+// Slot mode (matvec-style callers that hand over int8 slots, kcLaunchKernel's matmul_q4k_q8k*): the
+// producers read the per-256 slots themselves, convert them to the same fp16 operands in registers
+// and write them to the stage, in place of a conversion launch before the matmul.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -53,6 +56,18 @@ static_assert(kLoads % kProd == 0 && kWLoads * 4 == kTiles * kQ4kSlabs, "load sp
 static_assert(kLdsBytes <= 160 * 1024, "LDS");
 
 __device__ __forceinline__ h2 bits_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
+__device__ __forceinline__ uint32_t h2_bits(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Four int8 activations -> four fp16 values 16 x (exact): (x ^ 0x80) | 0x6400 is 1024 + x + 128,
+// and (1152 + x) * 16 - 18432 = 16 x in one fused multiply-add (act_to_f16's conversion).
+__device__ __forceinline__ uint2 i8x4_to_h4x16(uint32_t w) {
+    const uint32_t u = w ^ 0x80808080u;
+    const h2 m = {(_Float16)16.0f, (_Float16)16.0f}, c = {(_Float16)(-18432.0f), (_Float16)(-18432.0f)};
+    const h2 lo = __builtin_elementwise_fma(bits_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)), m, c);
+    const h2 hi = __builtin_elementwise_fma(bits_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)), m, c);
+    return make_uint2(h2_bits(lo), h2_bits(hi));
+}
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t bufRes(const void* p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
@@ -79,11 +94,66 @@ __device__ __forceinline__ h8 nib8(uint2 q, bool hiNib, h2 m2, h2 s2) {
 }
 
 struct WsArgs {
-    const _Float16* act;
+    const _Float16* act;  // fp16 mode: act_to_f16's (or a quantizer's) operands
     const _Float16* mins;
     const float* xdT;
+    const int* xq;        // slot mode: the per-256 slots (nsb * 85 ints per column)
     int nsb, ncols, ncp;
 };
+
+constexpr int kWPerProd = kWLoads / kProd;  // slot mode: each producer's weight loads
+static_assert(kWLoads % kProd == 0, "weight load split");
+
+// Slot mode: this producer lane's part of super-block s. Lane L = 64 p + lane of the 256 takes
+// column L / 4's activation words 16 (L % 4) .. +15 (64 int8); producer 0's lanes also the column
+// scale of column col0 + lane, producer 1's the four words of its min bytes. Columns past ncols read
+// column 0 (never stored). The launcher keeps nsb % 4 == 0: every read is 16-byte aligned.
+struct SlotRegs {
+    i32x4 a[4];
+    i32x4 m;
+    float d;
+};
+__device__ __forceinline__ void loadSlots(SlotRegs& r, const int* __restrict__ xq, int p, int lane, int col0,
+                                          int ncols, int nsb, int s) {
+    const int L = p * 64 + lane, c = L >> 2, qq = L & 3;
+    const int cc = col0 + c < ncols ? col0 + c : 0;
+    const i32x4* src = reinterpret_cast<const i32x4*>(xq + (size_t)cc * nsb * 85 + s * 64 + qq * 16);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) r.a[u] = src[u];
+    const int cl = col0 + lane < ncols ? col0 + lane : 0;
+    const int* colp = xq + (size_t)cl * nsb * 85;
+    if (p == 0) r.d = reinterpret_cast<const float*>(colp + nsb * 64)[s];
+    if (p == 1) r.m = *reinterpret_cast<const i32x4*>(colp + nsb * 81 + s * 4);
+}
+// ... converted and written to the stage: the activation chunks, the scales, the min operands
+// [64 (B_j >> 6) for j < 8 | B_j & 63 for j < 8] (the reference's byte split of the sub-block sums).
+__device__ __forceinline__ void writeSlots(char* buf, const SlotRegs& r, int p, int lane) {
+    const int L = p * 64 + lane, c = L >> 2, qq = L & 3;
+    char* dst = buf + c * kColB + qq * 128;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const i32x4 w = r.a[u];
+        const int w0 = w[0], w1 = w[1], w2 = w[2], w3 = w[3];  // (scalar copies before use)
+        const uint2 h0 = i8x4_to_h4x16((uint32_t)w0), h1 = i8x4_to_h4x16((uint32_t)w1);
+        const uint2 h2v = i8x4_to_h4x16((uint32_t)w2), h3 = i8x4_to_h4x16((uint32_t)w3);
+        *reinterpret_cast<uint4*>(dst + u * 32) = make_uint4(h0.x, h0.y, h1.x, h1.y);
+        *reinterpret_cast<uint4*>(dst + u * 32 + 16) = make_uint4(h2v.x, h2v.y, h3.x, h3.y);
+    }
+    if (p == 0) reinterpret_cast<float*>(buf + kXdOff)[lane] = r.d;
+    if (p == 1) {
+        const int m0 = r.m[0], m1 = r.m[1], m2 = r.m[2], m3 = r.m[3];
+        h8 lo, hi;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int hb = ((j < 4 ? m0 : m1) << (24 - 8 * (j & 3))) >> 24;
+            const int lb = ((j < 4 ? m2 : m3) >> (8 * (j & 3))) & 255;
+            lo[j] = (_Float16)(float)(64 * hb);
+            hi[j] = (_Float16)(float)lb;
+        }
+        *reinterpret_cast<h8*>(buf + kMinOff + lane * 32) = lo;
+        *reinterpret_cast<h8*>(buf + kMinOff + lane * 32 + 16) = hi;
+    }
+}
 
 // The producers' loads of super-block s into stage buf. Load L = kProd r + p of the kLoads:
 // activation chunks, then the min operands, the column scales, the weight chunks; voff[r] is this
@@ -113,6 +183,7 @@ __device__ __forceinline__ void produce(char* buf, int p, int lane, const uint32
 }
 
 // One workgroup: rows rowTile * 256 .., columns colTile * 64 .., super-blocks [sb0, sb1).
+template <bool SLOTS>
 __device__ __forceinline__ void wsTile(char* lbase, const uint8_t* __restrict__ qw, const WsArgs& a,
                                        float* __restrict__ y, int rows, int rowTile, int colTile, int sb0, int sb1) {
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -122,7 +193,42 @@ __device__ __forceinline__ void wsTile(char* lbase, const uint8_t* __restrict__ 
     const int tiles_stream = (rows + kTileRows - 1) / kTileRows;
     const bool prod = wave >= kCons;
 
-    if (prod) {
+    if (SLOTS && prod) {
+        const int p = wave - kCons;
+        const __amdgpu_buffer_rsrc_t rw = bufRes(qw, (uint32_t)tiles_stream * (uint32_t)ngroups * (uint32_t)kQ4kSeg);
+        uint32_t voff[kWPerProd];
+#pragma unroll
+        for (int r = 0; r < kWPerProd; ++r) {  // tiles past the stream read tile 0 (their rows are never stored)
+            const int q = (kProd * r + p) * 4 + (lane >> 4), t = q / kQ4kSlabs, j = q - kQ4kSlabs * t;
+            int tg = rowTile * kTiles + t;
+            if (tg >= tiles_stream) tg = 0;
+            voff[r] = (uint32_t)tg * (uint32_t)ngroups * (uint32_t)kQ4kSeg + (uint32_t)(j * 1024 + (lane & 15) * 16);
+        }
+        auto weights = [&](char* buf, int s) {
+#pragma unroll
+            for (int r = 0; r < kWPerProd; ++r)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (LdsPtr)(buf + kWOff + (kProd * r + p) * 1024), 16, voff[r],
+                                                         (uint32_t)((s >> 2) * kQ4kSeg + (s & 3) * 256), 0, 0);
+        };
+        SlotRegs sr;
+        weights(lbase, sb0);
+        loadSlots(sr, a.xq, p, lane, col0, ncols, nsb, sb0);
+        writeSlots(lbase, sr, p, lane);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        for (int s = sb0; s < sb1; ++s) {
+            const int b = (s - sb0) & 1;
+            if (s + 1 < sb1) {
+                weights(lbase + (b ^ 1) * kStage, s + 1);
+                loadSlots(sr, a.xq, p, lane, col0, ncols, nsb, s + 1);
+                writeSlots(lbase + (b ^ 1) * kStage, sr, p, lane);
+            }
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+        }
+        return;
+    }
+    if (!SLOTS && prod) {
         const int p = wave - kCons;
         const __amdgpu_buffer_rsrc_t ra = bufRes(a.act, (uint32_t)ncols * (uint32_t)k * 2u);
         const __amdgpu_buffer_rsrc_t rm = bufRes(a.mins, (uint32_t)ncols * (uint32_t)nsb * 32u);
@@ -269,6 +375,7 @@ __device__ __forceinline__ void wsTile(char* lbase, const uint8_t* __restrict__ 
     }
 }
 
+template <bool SLOTS>
 __global__ __launch_bounds__(kThreads) void matmul_q4k_mfma_ws_kernel(MfmaGroup g, WsArgs a) {
     extern __shared__ int4 lds4[];
     char* lbase = reinterpret_cast<char*>(lds4);
@@ -276,7 +383,7 @@ __global__ __launch_bounds__(kThreads) void matmul_q4k_mfma_ws_kernel(MfmaGroup 
     const int pi = (g.nparts > 2 && bx >= g.p[2].tile0) ? 2 : (g.nparts > 1 && bx >= g.p[1].tile0) ? 1 : 0;
     const MfmaPart& p = g.p[pi];
     const int z = blockIdx.z, sb0 = z * a.nsb / g.ks, sb1 = (z + 1) * a.nsb / g.ks;
-    wsTile(lbase, p.qw, a, p.y[z], p.rows, bx - p.tile0, blockIdx.y, sb0, sb1);
+    wsTile<SLOTS>(lbase, p.qw, a, p.y[z], p.rows, bx - p.tile0, blockIdx.y, sb0, sb1);
 }
 
 }  // namespace
@@ -295,13 +402,26 @@ bool mfmaWsFits(const MfmaGroup& g, int nsb, int ncols) {
 
 int launchMfmaWs(const MfmaGroup& g, int tiles, const void* act, const void* mins, const float* xdT, int nsb, int ncols,
                  int ncp, hipStream_t s) {
-    static const int attr = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(matmul_q4k_mfma_ws_kernel),
+    static const int attr = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(matmul_q4k_mfma_ws_kernel<false>),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
     if (attr != 0) return fromHip(attr, "matmul (MFMA, producer wavefronts): LDS size");
-    const WsArgs a{static_cast<const _Float16*>(act), static_cast<const _Float16*>(mins), xdT, nsb, ncols, ncp};
+    const WsArgs a{static_cast<const _Float16*>(act), static_cast<const _Float16*>(mins), xdT, nullptr, nsb, ncols, ncp};
     const dim3 grid(tiles, (ncols + kCols - 1) / kCols, g.ks);
-    hipLaunchKernelGGL(matmul_q4k_mfma_ws_kernel, grid, dim3(kThreads), kLdsBytes, s, g, a);
+    hipLaunchKernelGGL(matmul_q4k_mfma_ws_kernel<false>, grid, dim3(kThreads), kLdsBytes, s, g, a);
     return fromHip(hipGetLastError(), "matmul_q4k_q8k (MFMA, producer wavefronts)");
+}
+
+bool mfmaWsSlotsFits(int nsb) { return nsb % 4 == 0; }
+
+int launchMfmaWsSlots(const MfmaGroup& g, int tiles, const int* xq, int nsb, int ncols, hipStream_t s) {
+    static const int attr = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(matmul_q4k_mfma_ws_kernel<true>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+    if (attr != 0) return fromHip(attr, "matmul (MFMA, producer wavefronts, slots): LDS size");
+    if (!mfmaWsSlotsFits(nsb)) return fromHip(hipErrorInvalidValue, "matmul (MFMA, slots): k not a multiple of 1024");
+    const WsArgs a{nullptr, nullptr, nullptr, xq, nsb, ncols, 0};
+    const dim3 grid(tiles, (ncols + kCols - 1) / kCols, g.ks);
+    hipLaunchKernelGGL(matmul_q4k_mfma_ws_kernel<true>, grid, dim3(kThreads), kLdsBytes, s, g, a);
+    return fromHip(hipGetLastError(), "matmul_q4k_q8k (MFMA, producer wavefronts, slots)");
 }
 
 }  // namespace kcamd
