@@ -255,8 +255,15 @@ struct Pass {
     std::vector<int>* ones_wanted;   // a plan: the lengths of the 1.0f arrays the launches read
     bool capturing;                  // launches recorded into a graph (MUL_MAT groups run concurrently)
     // Batch products whose second K half (partial sums) is not yet added: the ADD that reads one adds
-    // it inside its fused norm; any other reader, and the end of the walk, adds it first.
-    std::vector<std::pair<const T*, const float*>> pending{};
+    // it inside its fused norm; any other reader, and the end of the walk, adds it first. A product
+    // marked views (a Q6_K matrix split beside Q4_K ones) keeps its half past the views of it: the
+    // fused RoPE / cache store takes v's along, any other reader adds it to the whole product.
+    struct Pending {
+        const T* t;
+        const float* h;
+        bool views;
+    };
+    std::vector<Pending> pending{};
 };
 
 const float* onesOf(Pass& p, int n) {
@@ -355,8 +362,30 @@ E swiglu(Pass& p, const T* dst) {  // :641-646
 // The pending second K half of product t (null if none), now the caller's to add.
 const float* takePending(Pass& p, const T* t) {
     for (auto it = p.pending.begin(); it != p.pending.end(); ++it)
-        if (it->first == t) {
-            const float* h = it->second;
+        if (it->t == t) {
+            const float* h = it->h;
+            p.pending.erase(it);
+            return h;
+        }
+    return nullptr;
+}
+bool viewOp(int op) {
+    return op == KC_GGML_OP_RESHAPE || op == KC_GGML_OP_VIEW || op == KC_GGML_OP_PERMUTE ||
+           op == KC_GGML_OP_TRANSPOSE;
+}
+// The tensor a chain of views of t looks into (t itself when t is no view).
+const T* viewBase(const T* t) {
+    while (t && t->view && viewOp(t->op) && t->src[0]) t = t->src[0];
+    return t;
+}
+// The pending half of the product a view t (or t itself) looks into, when that product keeps its
+// half past views; *base = the product.
+const float* takeViewPending(Pass& p, const T* t, const T** base) {
+    const T* b = viewBase(t);
+    for (auto it = p.pending.begin(); it != p.pending.end(); ++it)
+        if (it->t == t || (it->views && it->t == b)) {
+            const float* h = it->h;
+            *base = it->t;
             p.pending.erase(it);
             return h;
         }
@@ -367,10 +396,20 @@ E addHalf(Pass& p, const T* t, const float* h) {
     const kcVectorAddArgs a{f32(t), h, f32w(t), int(nelements(t))};
     return launch(p, "vector_add", &a);
 }
-// Adds the pending half of t, if any, before something reads t.
-E settle(Pass& p, const T* t) {
+// Adds the pending half of t, if any, before something reads t (a view node, which reads no data,
+// leaves the halves that are kept past views; another reader of a view of such a product adds the
+// half to the whole product).
+E settle(Pass& p, const T* t, bool view_node = false) {
     if (!t || p.pending.empty()) return ok;
-    if (const float* h = takePending(p, t)) return addHalf(p, t, h);
+    for (auto it = p.pending.begin(); it != p.pending.end(); ++it)
+        if (it->t == t && !(view_node && it->views)) {
+            const float* h = it->h;
+            p.pending.erase(it);
+            return addHalf(p, t, h);
+        }
+    if (view_node) return ok;
+    const T* base = nullptr;
+    if (const float* h = takeViewPending(p, t, &base)) return addHalf(p, base, h);
     return ok;
 }
 
@@ -665,12 +704,16 @@ E ropeKv(Pass& p, const T* rq, const T* rk, const T* sk, const T* sv) {
     const int hd = int(rq->ne[0]);
     const float* ff = rq->src[2] ? f32(rq->src[2]) : onesOf(p, hd / 2);
     if (!ff) return kc::Error::InternalError;
+    // v's product split over K: its pending half, at the view's offset, stored with it
+    const T* vbase = nullptr;
+    const float* v2 = takeViewPending(p, sv->src[0], &vbase);
+    if (v2) v2 += (static_cast<const char*>(sv->src[0]->data) - static_cast<const char*>(vbase->data)) / 4;
     const kcamd::RopeKvRows r{f32(rq->src[0]), f32w(rq), f32(rk->src[0]), f32w(rk), f32(sv->src[0]),
                               static_cast<int*>(sk->data), static_cast<int*>(sv->data),
                               static_cast<const int*>(rq->src[1]->data), static_cast<const int*>(sk->src[1]->data), ff,
                               hd, int(rq->ne[1]), int(rk->ne[1]), int(rq->ne[2]), std::log2(paramF32(rq, 5)),
                               (rq->op_params[2] & KC_GGML_ROPE_TYPE_NEOX) != 0, int(sv->src[0]->nb[1] / 4),
-                              int(sk->nb[1] / 4), int(sv->nb[1] / 4), int(sk->ne[1])};
+                              int(sk->nb[1] / 4), int(sv->nb[1] / 4), int(sk->ne[1]), v2};
     return direct(p, "rope_set_rows", [&](hipStream_t s) { return kcamd::launchRopeKvRows(r, s); });
 }
 
@@ -927,21 +970,48 @@ E batchGroup(Pass& p, const T* const* mm, int g) {
         if (E e = kcamd::mulmat::take(p.rec, size_t(rows0) * size_t(ncols), &part); e != ok) return e;
         parts[0].y[1] = reinterpret_cast<float*>(part);
     }
+    // a Q6_K matrix beside Q4_K ones (a Q6_K v in q / k / v) may run in two K ranges of its own
+    // (matmulGroupSplitsQ6): its second half goes to scratch and stays pending past the views of it
+    bool split6 = false;
+    if (g > 1) {
+        kcamd::MmPart probe[3];
+        for (int j = 0; j < g; ++j) {
+            probe[j] = parts[j];
+            if (probe[j].q6) probe[j].y[1] = reinterpret_cast<float*>(uintptr_t(256));  // (not dereferenced)
+        }
+        split6 = kcamd::matmulGroupSplitsQ6(probe, g, k, ncols);
+        for (int j = 0; split6 && j < g; ++j)
+            if (parts[j].q6) {
+                int* part = nullptr;
+                if (E e = kcamd::mulmat::take(p.rec, size_t(parts[j].rows) * size_t(ncols), &part); e != ok) return e;
+                parts[j].y[1] = reinterpret_cast<float*>(part);
+            }
+    }
     const E e = direct(p, "matmul_group", [&](hipStream_t s) {
-        int used = 1;
-        if (int st = kcamd::launchMatmulGroup(parts, g, q, k, ncols, ks, &used, s, pre)) return st;
-        if (used != ks) {  // (the launcher runs the MFMA kernel whenever batchGroupOk holds)
+        int used = 1, pks[3] = {1, 1, 1};
+        if (int st = kcamd::launchMatmulGroup(parts, g, q, k, ncols, ks, &used, s, pre, split6 ? pks : nullptr))
+            return st;
+        bool as_planned = used == ks;  // (the launcher runs the MFMA kernel whenever batchGroupOk holds)
+        for (int j = 0; split6 && j < g; ++j) as_planned = as_planned && pks[j] == (parts[j].q6 ? 2 : 1);
+        if (!as_planned) {
             kcamd::setDetail("ggml backend: the grouped matmul took another K split than planned");
             return int(kc::Error::InternalError);
         }
         return 0;
     });
-    if (e != ok || ks != 2) return e;
+    if (e != ok) return e;
+    for (int j = 0; split6 && j < g; ++j) {
+        if (!parts[j].q6) continue;
+        const T* y = mm[j];
+        if (y->uses == 1 && !y->view && !y->output) p.pending.push_back({y, parts[j].y[1], true});
+        else if (E e2 = addHalf(p, y, parts[j].y[1]); e2 != ok) return e2;
+    }
+    if (ks != 2) return ok;
     // the half is added by whatever reads the product next (the ADD's fused norm takes it along)
     // unless the product is a view, an output or read twice: then now
     const T* y = mm[0];
     if (y->uses == 1 && !y->view && !y->output) {
-        p.pending.emplace_back(y, parts[0].y[1]);
+        p.pending.push_back({y, parts[0].y[1], false});
         return ok;
     }
     return addHalf(p, y, parts[0].y[1]);
@@ -962,7 +1032,7 @@ E walk(Pass& p, const T* const* nodes, int n) {
         // below (its fused norm takes it along)
         if (!p.pending.empty() && node->op != KC_GGML_OP_ADD)
             for (int s = 0; s < 5; ++s)
-                if (E e = settle(p, node->src[s]); e != ok) return e;
+                if (E e = settle(p, node->src[s], viewOp(node->op)); e != ok) return e;
         // nothing to compute (e.g. a prompt's earlier batches select no output rows); fused
         // partners of an empty node are empty too
         if (!computed(node)) continue;
@@ -1103,7 +1173,7 @@ E walk(Pass& p, const T* const* nodes, int n) {
         if (e != ok) return e;
     }
     while (!p.pending.empty()) {  // products nothing in the list read: whole for the caller
-        const T* t = p.pending.front().first;
+        const T* t = p.pending.front().t;
         if (E e = settle(p, t); e != ok) return e;
     }
     return ok;

@@ -1063,10 +1063,24 @@ int hWaves(long long wgs8) {
     return wgs8 <= cus || wgs8 % cus == 0 ? 8 : 4;
 }
 
+// Whether the producer-wavefront kernel splits the Q6_K parts of group g over K (on top of a group
+// split of one): a Q4_K part beside a Q6_K one given a second output, at least two super-blocks,
+// option matmul_split6 not 1.
+bool splitsQ6(const MfmaGroup& g, int nparts, int nsb) {
+    bool q4 = false, q6 = false;
+    for (int i = 0; i < nparts; ++i) {
+        q4 |= !g.p[i].q6;
+        q6 |= g.p[i].q6 && g.p[i].y[1];
+    }
+    return q4 && q6 && nsb >= 2 && option("matmul_split6") != 1;
+}
+
 // The fp16-activation kernel over parts[0..nparts) (one conversion of the activations), K split
 // into ks ranges.
 int runMfmaH(const MmPart* parts, int nparts, const int* xq, int k, int ncols, int ks, void* act, hipStream_t s,
-             const ActF16* pre = nullptr) {
+             const ActF16* pre = nullptr, int* part_ks = nullptr) {
+    if (part_ks)
+        for (int i = 0; i < nparts; ++i) part_ks[i] = ks;
     using G = HGeo<2, 4>;  // (the LDS geometry does not depend on the wavefront count)
     static const int attr4 = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(matmul_kq_mfma_h_kernel<4>),
                                                       hipFuncAttributeMaxDynamicSharedMemorySize, G::kLds);
@@ -1076,9 +1090,10 @@ int runMfmaH(const MmPart* parts, int nparts, const int* xq, int k, int ncols, i
     const int nsb = k / 256;
     long long tiles8 = 0;
     for (int i = 0; i < nparts; ++i) tiles8 += (parts[i].rows + 255) / 256;
-    // Q4_K parts only: the producer-wavefront kernel (256-row tiles) unless option matmul_ws = 1
+    // the producer-wavefront kernel (256-row tiles) unless option matmul_ws = 1 (3: for Q4_K-only
+    // groups, a group with a Q6_K matrix on the kernel above)
     bool ws = option("matmul_ws") != 1 && (option("matmul_path") == 0 || option("matmul_path") == 2);
-    for (int i = 0; i < nparts; ++i) ws = ws && !parts[i].q6;
+    for (int i = 0; i < nparts; ++i) ws = ws && !(option("matmul_ws") == 3 && parts[i].q6);
     const int nw = ws ? 8 : hWaves(tiles8 * ((ncols + G::kCols - 1) / G::kCols) * ks);
     const int wg_rows = ws ? mfmaWsRows() : 32 * nw;
     HGroup g{};
@@ -1092,9 +1107,12 @@ int runMfmaH(const MmPart* parts, int nparts, const int* xq, int k, int ncols, i
     }
     g.nparts = nparts;
     g.ks = ks;
-    // slots handed over (no quantizer-written fp16 operands): the producer wavefronts convert them
-    // themselves, unless option matmul_ws = 2 (a conversion launch first, as for the other kernels)
-    if (ws && !pre && option("matmul_ws") != 2 && option("matmul_path") != 7 && mfmaWsSlotsFits(nsb) &&
+    // slots handed over (no quantizer-written fp16 operands) to Q4_K matrices: the producer
+    // wavefronts convert them themselves, unless option matmul_ws = 2 (a conversion launch first,
+    // as for the other kernels and for Q6_K)
+    bool all_q4 = true;
+    for (int i = 0; i < nparts; ++i) all_q4 = all_q4 && !parts[i].q6;
+    if (ws && all_q4 && !pre && option("matmul_ws") != 2 && option("matmul_path") != 7 && mfmaWsSlotsFits(nsb) &&
         mfmaWsFits(g, nsb, ncols))
         return launchMfmaWsSlots(g, tiles, xq, nsb, ncols, s);
     const long long words = (long long)ncols * nsb * 64;
@@ -1117,7 +1135,24 @@ int runMfmaH(const MmPart* parts, int nparts, const int* xq, int k, int ncols, i
     }
     if (option("matmul_path") == 7)  // the wide-tile kernel (every weight dequantized once per workgroup)
         return launchMfmaW(g, tiles, act, mins, xdT, nsb, ncols, ncp, s);
-    if (ws && mfmaWsFits(g, nsb, ncols)) return launchMfmaWs(g, tiles, act, mins, xdT, nsb, ncols, ncp, s);
+    if (ws && mfmaWsFits(g, nsb, ncols)) {
+        // A Q6_K part among Q4_K ones runs twice the matrix ops per super-block (its split scale), so
+        // its workgroups would end long after the others': given a second output (y[1]) and a caller
+        // that takes per-part splits (part_ks), it runs in two K ranges when the group has one
+        // (option matmul_split6 = 1: never).
+        // Each part then owns ks x its row tiles of blockIdx.x (no idle workgroups).
+        if (part_ks && ks == 1 && splitsQ6(g, nparts, nsb)) {
+            tiles = 0;
+            for (int i = 0; i < nparts; ++i) {
+                g.p[i].ntiles = (parts[i].rows + wg_rows - 1) / wg_rows;
+                g.p[i].ks = parts[i].q6 && parts[i].y[1] ? 2 : 1;
+                g.p[i].tile0 = tiles;
+                tiles += g.p[i].ks * g.p[i].ntiles;
+                part_ks[i] = g.p[i].ks;
+            }
+        }
+        return launchMfmaWs(g, tiles, act, mins, xdT, nsb, ncols, ncp, s);
+    }
     if (ws) {  // beyond the 32-bit offsets: the 8-wavefront kernel over the same 256-row tiles
         const dim3 grid(tiles, (ncols + G::kCols - 1) / G::kCols, ks);
         hipLaunchKernelGGL(matmul_kq_mfma_h_kernel<8>, grid, dim3(512), G::kLds, s, g,
@@ -1289,19 +1324,34 @@ size_t matmulStagingBytes(int rows, int k, int ncols) {
     return stagedBytes(a, stagedKs(a));
 }
 
+bool matmulGroupSplitsQ6(const MmPart* parts, int nparts, int k, int ncols) {
+    if (nparts < 1 || nparts > 3 || k % 256 != 0 || ncols < 64 || !mfmaHUsable(ncols, k)) return false;
+    if (option("matmul_ws") == 1 || option("matmul_ws") == 3 || (option("matmul_path") != 0 && option("matmul_path") != 2))
+        return false;
+    MfmaGroup g{};
+    for (int i = 0; i < nparts; ++i)
+        g.p[i] = MfmaPart{static_cast<const uint8_t*>(parts[i].qw), {parts[i].y[0], parts[i].y[1]}, parts[i].rows,
+                          parts[i].q6, 0};
+    g.nparts = nparts;
+    g.ks = 1;
+    return mfmaWsFits(g, k / 256, ncols) && splitsQ6(g, nparts, k / 256);
+}
+
 int launchMatmulGroup(const MmPart* parts, int nparts, const int* xq, int k, int ncols, int ks, int* used_ks,
-                      hipStream_t s, const ActF16* pre) {
+                      hipStream_t s, const ActF16* pre, int* part_ks) {
     *used_ks = 1;
+    if (part_ks)
+        for (int i = 0; i < nparts && i < 3; ++i) part_ks[i] = 1;
     if (nparts < 1 || nparts > 3 || ks < 1 || ks > 2 || k % 256 != 0) return fromHip(hipErrorInvalidValue, "matmul group");
     if (ncols >= 64 && mfmaHUsable(ncols, k)) {
         if (ks > k / 256) ks = 1;
         if (pre) {
             *used_ks = ks;
-            return runMfmaH(parts, nparts, xq, k, ncols, ks, nullptr, s, pre);
+            return runMfmaH(parts, nparts, xq, k, ncols, ks, nullptr, s, pre, part_ks);
         }
         if (void* act = streamScratch(s, actBytes(ncols, k))) {
             *used_ks = ks;
-            return runMfmaH(parts, nparts, xq, k, ncols, ks, act, s);
+            return runMfmaH(parts, nparts, xq, k, ncols, ks, act, s, nullptr, part_ks);
         }
     }
     for (int i = 0; i < nparts; ++i) {  // one matmul per part, no K split

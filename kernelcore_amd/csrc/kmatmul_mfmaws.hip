@@ -1,7 +1,8 @@
-// kmatmul_mfmaws.hip -- the prefill matmul for Q4_K weights with producer and consumer wavefronts
-// (gfx950): Y = W X for per-256 8-bit activations, the arithmetic of kmatmul_mfma.hip (exact integer
-// sums per super-block on v_mfma_f32_32x32x16_f16, the reference's combine per super-block;
-// reference kernels/llm/matmul_q4k_q8kx8.cu, mirror llm/llm_reference.cpp:529-596).
+// kmatmul_mfmaws.hip -- the prefill matmul with producer and consumer wavefronts (gfx950): Y = W X
+// for Q4_K / Q6_K weights and per-256 8-bit activations, the arithmetic of kmatmul_mfma.hip (exact
+// integer sums per super-block on v_mfma_f32_32x32x16_f16, the reference's combine per super-block;
+// reference kernels/llm/matmul_q4k_q8kx8.cu, matmul_q6k_q8kx8.cu, mirror
+// llm/llm_reference.cpp:529-596).
 //
 // A wavefront stalls at each vector-memory instruction until the CU's memory unit takes it (about
 // 20 cycles per instruction), and a wavefront that stalls issues neither matrix ops nor the VALU
@@ -10,13 +11,14 @@
 //   - 8 consumer wavefronts (two per SIMD), each 32 weight rows x 64 columns as two 32 x 32 blocks:
 //     they only read LDS, dequantize and issue matrix ops (the K-step pipeline of
 //     kmatmul_mfma.hip's hTile, with the weights read from LDS instead of memory);
-//   - 4 producer wavefronts (one per SIMD) issue every load of a super-block, straight into LDS
-//     with buffer-to-LDS loads: the activation tile (fp16, 16 x, as act_to_f16 or the quantizers
-//     write it), the min operands, the column scales, and the weights of the 256 rows (the
-//     super-block's header slab and eight qs slabs of each 16-row tile).
-// Two LDS stages (72 KiB each): while the consumers compute super-block s from one, the producers
-// fill the other with s + 1 and wait for their loads; one barrier per super-block hands it over.
-// Slot mode (matvec-style callers that hand over int8 slots, kcLaunchKernel's matmul_q4k_q8k*): the
+//   - 4 producer wavefronts (one per SIMD) issue every load of a stage, straight into LDS with
+//     buffer-to-LDS loads: the activation tile (fp16, 16 x, as act_to_f16 or the quantizers write
+//     it), the column scales, and the weights of the 256 rows; for Q4_K also the min operands.
+// Two LDS stages: while the consumers compute one, the producers fill the other and wait for their
+// loads; one barrier per stage hands it over. A Q4_K stage is a super-block (72 KiB: each 16-row
+// tile's header slab and eight qs slabs), a Q6_K stage half of one (47 KiB, below). One launch may
+// mix Q4_K and Q6_K matrices (q / k / v with a Q6_K v); each workgroup takes its matrix's path.
+// Slot mode (Q4_K callers that hand over int8 slots, kcLaunchKernel's matmul_q4k_q8k*): the
 // producers read the per-256 slots themselves, convert them to the same fp16 operands in registers
 // and write them to the stage, in place of a conversion launch before the matmul.
 #include <hip/hip_runtime.h>
@@ -103,6 +105,23 @@ struct WsArgs {
 
 constexpr int kWPerProd = kWLoads / kProd;  // slot mode: each producer's weight loads
 static_assert(kWLoads % kProd == 0, "weight load split");
+
+// Q6_K: a stage holds half a super-block (128 values): per 16-row tile the row pieces ql 4n ..
+// 4n + 3, qh 8 + 2n, 9 + 2n and the scales (piece 12) of half n, the activation half (16 chunks of
+// 16 B per column + 1 pad chunk), the tiles' d values and the column scales. Two stages of 47 KiB;
+// each holds the same matrix-op work as a Q4_K stage (two ops per K-step, Q6_K's split scale).
+constexpr int kQ6Pieces = 7;
+constexpr int kQ6ColB = 272;                              // LDS bytes per column and half
+constexpr int kQ6ActLoads = kCols * 17 / 64;              // 1 KiB direct loads of the activation half
+constexpr int kQ6WOff = kQ6ActLoads * 1024;               // weights: [tile][piece][16 rows x 16 B]
+constexpr int kQ6WLoads = kTiles * kQ6Pieces / 4;         // each load: four (tile, piece) chunks of 256 B
+constexpr int kQ6DOff = kQ6WOff + kQ6WLoads * 1024;       // d: [tile][16 rows] fp16 (512 B used)
+constexpr int kQ6XdOff = kQ6DOff + 1024;                  // column scales (256 B used)
+constexpr int kQ6Stage = kQ6XdOff + 1024;
+constexpr int kQ6Loads = kQ6ActLoads + kQ6WLoads + 2;     // per half super-block
+constexpr int kQ6PerProd = (kQ6Loads + kProd - 1) / kProd;
+static_assert(kCols * 17 % 64 == 0 && kTiles * kQ6Pieces % 4 == 0, "Q6_K load split");
+static_assert(2 * kQ6Stage <= kLdsBytes, "Q6_K LDS");
 
 // Slot mode: this producer lane's part of super-block s. Lane L = 64 p + lane of the 256 takes
 // column L / 4's activation words 16 (L % 4) .. +15 (64 int8); producer 0's lanes also the column
@@ -375,15 +394,221 @@ __device__ __forceinline__ void wsTile(char* lbase, const uint8_t* __restrict__ 
     }
 }
 
+// Q6_K K-step t (0..7) of a half super-block n for activations 16 x: in lane half h the 8 values
+// k = 128 n + 32 quad + 16 h + 8 p (quad = t >> 1, p = t & 1): ql bytes 64 n + 32 (quad & 1) + 16 h
+// + 8 p (nibble quad >> 1; ql[a] holds bytes 64 n + 32 a + 16 h ..), qh bytes 32 n + 16 h + 8 p
+// (bits 2 quad), the int8 scale of sub-block 8 n + 2 quad + h (byte 2 (quad & 1) + h of word
+// quad >> 1 of sw, the half's eight scales) split as sc = 16 sh + sl: b1 = sh (q - 32) and
+// b2 = sl (q - 32) / 16, exact fp16 values (kmatmul_mfma.hip's Q6_K operands, in its K-step order).
+__device__ __forceinline__ void dq6(const uint4 (&ql)[2], uint4 qh, uint2 sw, int t, int h, h8& b1, h8& b2) {
+    const int quad = t >> 1, p = t & 1;
+    const uint4 L = ql[quad & 1];
+    const uint32_t lw[2] = {p ? L.z : L.x, p ? L.w : L.y}, hw[2] = {p ? qh.z : qh.x, p ? qh.w : qh.y};
+    const int w = (quad >> 1) ? (int)sw.y : (int)sw.x;
+    const int bi = 2 * (quad & 1) + h;
+    const int sh = (w << (24 - 8 * bi)) >> 28, sl = (w >> (8 * bi)) & 15;
+    const _Float16 fh = (_Float16)(short)sh, fl = (_Float16)(short)sl;
+    const h2 mh = {fh, fh}, ml = {fl * (_Float16)0.0625f, fl * (_Float16)0.0625f};
+    const h2 ch = {fh * (_Float16)(-1056.0f), fh * (_Float16)(-1056.0f)};
+    const h2 cl = {fl * (_Float16)(-66.0f), fl * (_Float16)(-66.0f)};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        // q (0..63) per byte, then 1024 + q as fp16 (high byte 0x64)
+        const uint32_t q = ((lw[i] >> (4 * (quad >> 1))) & 0x0F0F0F0Fu) | (((hw[i] >> (2 * quad)) & 0x03030303u) << 4);
+        const h2 x0 = bits_h2(__builtin_amdgcn_perm(0x64646464u, q, 0x04010400u));
+        const h2 x1 = bits_h2(__builtin_amdgcn_perm(0x64646464u, q, 0x04030402u));
+        const h2 a1 = __builtin_elementwise_fma(x0, mh, ch), c1 = __builtin_elementwise_fma(x1, mh, ch);
+        const h2 a2 = __builtin_elementwise_fma(x0, ml, cl), c2 = __builtin_elementwise_fma(x1, ml, cl);
+        b1[4 * i + 0] = a1[0];
+        b1[4 * i + 1] = a1[1];
+        b1[4 * i + 2] = c1[0];
+        b1[4 * i + 3] = c1[1];
+        b2[4 * i + 0] = a2[0];
+        b2[4 * i + 1] = a2[1];
+        b2[4 * i + 2] = c2[0];
+        b2[4 * i + 3] = c2[1];
+    }
+}
+
+// One Q6_K workgroup: rows rowTile * 256 .., columns colTile * 64 .., super-blocks [sb0, sb1), in
+// stages of half a super-block (stage 2 (s - sb0) + n in buffer n), fp16 activations as act_to_f16
+// or the quantizers write them. The consumers run kmatmul_mfma.hip's Q6_K K-steps in its order
+// (bit-identical sums) and combine once per super-block: acc += (d xd) is.
+__device__ __forceinline__ void wsTileQ6(char* lbase, const uint8_t* __restrict__ qw, const WsArgs& a,
+                                         float* __restrict__ y, int rows, int rowTile, int colTile, int sb0, int sb1) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nsb = a.nsb, ncols = a.ncols, k = nsb * 256;
+    const int col0 = colTile * kCols;
+    const int ngroups = (nsb + kGroupSb - 1) / kGroupSb;
+    const int tiles_stream = (rows + kTileRows - 1) / kTileRows;
+    const int nst = 2 * (sb1 - sb0);
+
+    if (wave >= kCons) {
+        const int p = wave - kCons;
+        const __amdgpu_buffer_rsrc_t ra = bufRes(a.act, (uint32_t)ncols * (uint32_t)k * 2u);
+        const __amdgpu_buffer_rsrc_t rx = bufRes(a.xdT, (uint32_t)nsb * (uint32_t)a.ncp * 4u);
+        const __amdgpu_buffer_rsrc_t rw = bufRes(qw, (uint32_t)tiles_stream * (uint32_t)ngroups * (uint32_t)kQ6kSeg);
+        // this lane's byte offset of each of its loads at super-block 0, half 0; a weight piece of
+        // half 1 lies dn further (ql pieces 4 on, qh pieces 2 on, the scales the same)
+        uint32_t voff[kQ6PerProd], dn[kQ6PerProd];
+#pragma unroll
+        for (int r = 0; r < kQ6PerProd; ++r) {
+            const int L = kProd * r + p;
+            dn[r] = 0;
+            if (L < kQ6ActLoads) {  // columns past ncols read column 0 (never stored)
+                const int slot = L * 64 + lane, c = slot / 17, kc = slot - 17 * c;
+                const int cc = col0 + c < ncols ? col0 + c : 0;
+                voff[r] = (uint32_t)cc * (uint32_t)k * 2u + (uint32_t)(kc == 16 ? 0 : kc) * 16u;
+            } else if (L < kQ6ActLoads + kQ6WLoads) {  // tiles past the stream read tile 0
+                const int q = (L - kQ6ActLoads) * 4 + (lane >> 4), t = q / kQ6Pieces, jj = q - kQ6Pieces * t;
+                int tg = rowTile * kTiles + t;
+                if (tg >= tiles_stream) tg = 0;
+                const int piece = jj < 4 ? jj : (jj < 6 ? 4 + jj : 12);
+                dn[r] = jj < 4 ? 4096u : (jj < 6 ? 2048u : 0u);
+                voff[r] = (uint32_t)tg * (uint32_t)ngroups * (uint32_t)kQ6kSeg + (uint32_t)(piece * 1024 + (lane & 15) * 16);
+            } else if (L == kQ6ActLoads + kQ6WLoads) {  // d: lane (tile, 8-row half); lanes 32.. repeat
+                int tg = rowTile * kTiles + ((lane >> 1) & 15);
+                if (tg >= tiles_stream) tg = 0;
+                voff[r] = (uint32_t)tg * (uint32_t)ngroups * (uint32_t)kQ6kSeg + (uint32_t)(kQ6kSlabs * 1024 + (lane & 1) * 16);
+            } else {  // the column scales
+                voff[r] = (uint32_t)((col0 + (lane & 15) * 4) * 4);
+            }
+        }
+        auto produce = [&](char* buf, int st) {
+            const int s = sb0 + (st >> 1), n = st & 1;
+            const uint32_t sw = (uint32_t)((s >> 2) * kQ6kSeg);
+#pragma unroll
+            for (int r = 0; r < kQ6PerProd; ++r) {
+                const int L = kProd * r + p;
+                if (L < kQ6ActLoads)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (LdsPtr)(buf + L * 1024), 16, voff[r],
+                                                             (uint32_t)(s * 512 + n * 256), 0, 0);
+                else if (L < kQ6ActLoads + kQ6WLoads)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (LdsPtr)(buf + kQ6WOff + (L - kQ6ActLoads) * 1024), 16,
+                                                             voff[r] + (n ? dn[r] : 0u), sw + (uint32_t)((s & 3) * 256),
+                                                             0, 0);
+                else if (L == kQ6ActLoads + kQ6WLoads)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (LdsPtr)(buf + kQ6DOff), 16, voff[r],
+                                                             sw + (uint32_t)((s & 3) * 32), 0, 0);
+                else if (L < kQ6Loads)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (LdsPtr)(buf + kQ6XdOff), 16, voff[r],
+                                                             (uint32_t)(s * a.ncp) * 4u, 0, 0);
+            }
+        };
+        produce(lbase, 0);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        for (int st = 0; st < nst; ++st) {
+            if (st + 1 < nst) produce(lbase + ((st + 1) & 1) * kQ6Stage, st + 1);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+        }
+        return;
+    }
+
+    // consumer wavefront: rows rowTile * 256 + wave * 32 + lane % 32, lane half h
+    const int h = lane >> 5, l32 = lane & 31;
+    const int row = rowTile * kRows + wave * 32 + l32;
+    const int t16 = wave * 2 + (l32 >> 4);
+    const int woff = kQ6WOff + t16 * kQ6Pieces * 256 + (l32 & 15) * 16;
+    const int doff = kQ6DOff + t16 * 32 + (l32 & 15) * 2;
+    int aoff[2];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) aoff[cb] = (cb * 32 + l32) * kQ6ColB + h * 32;
+    f16v acc[2];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[cb][i] = 0.0f;
+    const f16v zero = acc[0];
+    f16v is[2];
+    __syncthreads();  // stage 0 loaded
+    for (int s = sb0; s < sb1; ++s) {
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+            const char* buf = lbase + n * kQ6Stage;
+            uint4 ql[2];
+#pragma unroll
+            for (int a2 = 0; a2 < 2; ++a2) ql[a2] = *reinterpret_cast<const uint4*>(buf + woff + (2 * a2 + h) * 256);
+            const uint4 qh = *reinterpret_cast<const uint4*>(buf + woff + (4 + h) * 256);
+            const uint2 sw = *reinterpret_cast<const uint2*>(buf + woff + 6 * 256 + 8 * n);
+            h8 av[2], an[2];
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) av[cb] = *reinterpret_cast<const h8*>(buf + aoff[cb]);
+            h8 bq, bq2, bn, bn2;
+            dq6(ql, qh, sw, 0, h, bq, bq2);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                if (t + 1 < 8) {
+                    const int tn = t + 1, toff = 64 * (tn >> 1) + 16 * (tn & 1);
+#pragma unroll
+                    for (int cb = 0; cb < 2; ++cb) an[cb] = *reinterpret_cast<const h8*>(buf + aoff[cb] + toff);
+                    dq6(ql, qh, sw, tn, h, bn, bn2);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb) {
+                    is[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[cb], bq, n == 0 && t == 0 ? zero : is[cb], 0, 0, 0);
+                    is[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[cb], bq2, is[cb], 0, 0, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                if (t + 1 < 8) {
+#pragma unroll
+                    for (int cb = 0; cb < 2; ++cb) av[cb] = an[cb];
+                    bq = bn;
+                    bq2 = bn2;
+                }
+            }
+            if (n == 1) {  // the super-block's combine: acc += (d xd) is
+                const float d = (float)__builtin_bit_cast(_Float16, *reinterpret_cast<const unsigned short*>(buf + doff));
+                const char* xdl = buf + kQ6XdOff;
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; ++q4) {
+                        const u32v4 xdw = *reinterpret_cast<const u32v4*>(xdl + (cb * 32 + q4 * 8 + h * 4) * 4);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int i = 4 * q4 + e;
+                            const uint32_t wv = xdw[e];  // (a scalar copy before the bit cast)
+                            acc[cb][i] = __builtin_fmaf(d * __builtin_bit_cast(float, wv), is[cb][i], acc[cb][i]);
+                        }
+                    }
+            }
+            __syncthreads();  // stage read: the producers may refill it; the next stage is loaded
+        }
+    }
+    if (row < rows) {
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int c = col0 + cb * 32 + (i >> 2) * 8 + h * 4 + (i & 3);
+                if (c < ncols) y[(size_t)c * rows + row] = acc[cb][i];
+            }
+    }
+}
+
+// A workgroup finds its part from its row tile and its K range from blockIdx.z and the part's split;
+// Q6_K parts (never in slot mode) take wsTileQ6 on a uniform branch.
 template <bool SLOTS>
-__global__ __launch_bounds__(kThreads) void matmul_q4k_mfma_ws_kernel(MfmaGroup g, WsArgs a) {
+__global__ __launch_bounds__(kThreads) void matmul_kq_mfma_ws_kernel(MfmaGroup g, WsArgs a) {
     extern __shared__ int4 lds4[];
     char* lbase = reinterpret_cast<char*>(lds4);
     const int bx = blockIdx.x;
     const int pi = (g.nparts > 2 && bx >= g.p[2].tile0) ? 2 : (g.nparts > 1 && bx >= g.p[1].tile0) ? 1 : 0;
     const MfmaPart& p = g.p[pi];
-    const int z = blockIdx.z, sb0 = z * a.nsb / g.ks, sb1 = (z + 1) * a.nsb / g.ks;
-    wsTile<SLOTS>(lbase, p.qw, a, p.y[z], p.rows, bx - p.tile0, blockIdx.y, sb0, sb1);
+    int z = blockIdx.z, ks = g.ks, rt = bx - p.tile0;
+    if (p.ks) {  // the part's own split over its workgroups
+        ks = p.ks;
+        z = rt / p.ntiles;
+        rt -= z * p.ntiles;
+    }
+    const int sb0 = z * a.nsb / ks, sb1 = (z + 1) * a.nsb / ks;
+    if (!SLOTS && p.q6)
+        wsTileQ6(lbase, p.qw, a, p.y[z], p.rows, rt, blockIdx.y, sb0, sb1);
+    else
+        wsTile<SLOTS>(lbase, p.qw, a, p.y[z], p.rows, rt, blockIdx.y, sb0, sb1);
 }
 
 }  // namespace
@@ -392,9 +617,8 @@ int mfmaWsRows() { return kRows; }
 
 bool mfmaWsFits(const MfmaGroup& g, int nsb, int ncols) {
     for (int i = 0; i < g.nparts; ++i) {
-        if (g.p[i].q6) return false;
-        const unsigned long long wbytes =
-            (unsigned long long)tilesOf(g.p[i].rows) * (unsigned long long)groupsOf(nsb) * kQ4kSeg;
+        const unsigned long long wbytes = (unsigned long long)tilesOf(g.p[i].rows) * (unsigned long long)groupsOf(nsb) *
+                                          (g.p[i].q6 ? kQ6kSeg : kQ4kSeg);
         if (wbytes >= (1ull << 32)) return false;
     }
     return (unsigned long long)ncols * nsb * 512ull < (1ull << 32);
@@ -402,25 +626,30 @@ bool mfmaWsFits(const MfmaGroup& g, int nsb, int ncols) {
 
 int launchMfmaWs(const MfmaGroup& g, int tiles, const void* act, const void* mins, const float* xdT, int nsb, int ncols,
                  int ncp, hipStream_t s) {
-    static const int attr = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(matmul_q4k_mfma_ws_kernel<false>),
+    static const int attr = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(matmul_kq_mfma_ws_kernel<false>),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
     if (attr != 0) return fromHip(attr, "matmul (MFMA, producer wavefronts): LDS size");
+    bool any_q4 = false;
+    for (int i = 0; i < g.nparts; ++i) any_q4 |= !g.p[i].q6;
     const WsArgs a{static_cast<const _Float16*>(act), static_cast<const _Float16*>(mins), xdT, nullptr, nsb, ncols, ncp};
     const dim3 grid(tiles, (ncols + kCols - 1) / kCols, g.ks);
-    hipLaunchKernelGGL(matmul_q4k_mfma_ws_kernel<false>, grid, dim3(kThreads), kLdsBytes, s, g, a);
-    return fromHip(hipGetLastError(), "matmul_q4k_q8k (MFMA, producer wavefronts)");
+    hipLaunchKernelGGL(matmul_kq_mfma_ws_kernel<false>, grid, dim3(kThreads), any_q4 ? kLdsBytes : 2 * kQ6Stage, s, g,
+                       a);
+    return fromHip(hipGetLastError(), "matmul_q4k/q6k_q8k (MFMA, producer wavefronts)");
 }
 
 bool mfmaWsSlotsFits(int nsb) { return nsb % 4 == 0; }
 
 int launchMfmaWsSlots(const MfmaGroup& g, int tiles, const int* xq, int nsb, int ncols, hipStream_t s) {
-    static const int attr = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(matmul_q4k_mfma_ws_kernel<true>),
+    static const int attr = (int)hipFuncSetAttribute(reinterpret_cast<const void*>(matmul_kq_mfma_ws_kernel<true>),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
     if (attr != 0) return fromHip(attr, "matmul (MFMA, producer wavefronts, slots): LDS size");
     if (!mfmaWsSlotsFits(nsb)) return fromHip(hipErrorInvalidValue, "matmul (MFMA, slots): k not a multiple of 1024");
     const WsArgs a{nullptr, nullptr, nullptr, xq, nsb, ncols, 0};
     const dim3 grid(tiles, (ncols + kCols - 1) / kCols, g.ks);
-    hipLaunchKernelGGL(matmul_q4k_mfma_ws_kernel<true>, grid, dim3(kThreads), kLdsBytes, s, g, a);
+    for (int i = 0; i < g.nparts; ++i)
+        if (g.p[i].q6) return fromHip(hipErrorInvalidValue, "matmul (MFMA, slots): Q6_K part");
+    hipLaunchKernelGGL(matmul_kq_mfma_ws_kernel<true>, grid, dim3(kThreads), kLdsBytes, s, g, a);
     return fromHip(hipGetLastError(), "matmul_q4k_q8k (MFMA, producer wavefronts, slots)");
 }
 

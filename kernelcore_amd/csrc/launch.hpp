@@ -59,12 +59,17 @@ struct MmPart {
     int rows;
     int q6;  // Q6_K (else Q4_K)
 };
+// Whether launchMatmulGroup with part_ks splits the Q6_K parts (those given a y[1]) of this group of
+// parts over K (their workgroups then end with the Q4_K parts').
+bool matmulGroupSplitsQ6(const MmPart* parts, int nparts, int k, int ncols);
 // parts[0..nparts) (at most 3) times the same per-256 activations (ncols columns of length k) in
 // one launch where the MFMA kernel applies, K split into ks <= 2 ranges: *used_ks = the split
 // taken (1: each y[0] holds the whole product; 2: y[0] + y[1] is the product).
 // pre (may be null): the activations already in the MFMA layout (then no conversion is launched).
+// part_ks (may be null): each part's own split, reported per part; with it, a Q6_K part that has a
+// y[1] may take two K ranges in a group of one (its partial sums y[0] + y[1]), the others one.
 int launchMatmulGroup(const MmPart* parts, int nparts, const int* xq, int k, int ncols, int ks, int* used_ks,
-                      hipStream_t s, const ActF16* pre = nullptr);
+                      hipStream_t s, const ActF16* pre = nullptr, int* part_ks = nullptr);
 // Whether a group of ncols >= 64 columns of k values runs on the fp16-activation MFMA kernel.
 bool mfmaHUsable(int ncols, int k);
 // The K ranges a by-name launch of this shape takes (2 when its grid is under two workgroups per CU).
@@ -83,7 +88,8 @@ int launchAddNormQ8(const float* a, const float* b, float* x, const float* w, fl
                     float eps, hipStream_t s);
 // Batch fusions of the model path: x = a + (b [+ b2]) into out (a null: x = b), RMS norm with w
 // and per-256 quantization into q (rows slots of n / 256 * 85 ints); RoPE of q into qr and of k,
-// with k and v stored as fp16 into cache rows pos[t] (dst_row 32-bit words per row).
+// with k and v (+ v2, when given) stored as fp16 into cache rows pos[t] (dst_row 32-bit words per
+// row).
 // (ao, when given, also receives the MFMA layout of the quantized rows; y, when given, the normed
 // rows x r w in f32, the values that are quantized.)
 int launchAddNormQ8K(const float* a, const float* b, const float* b2, float* out, const float* w, int* q, int n,
@@ -91,7 +97,7 @@ int launchAddNormQ8K(const float* a, const float* b, const float* b2, float* out
 int launchSiluMulQ8KAct(const kcSiluMulQ8FArgs& a, const ActF16* ao, hipStream_t s);
 int launchRopeQKStore(const float* q, float* qr, const float* k, const float* v, int* kcache, int* vcache,
                       const int* pos, const float* ff, int head_dim, int nh, int nkv, int n, float log2_base, int neox,
-                      int dst_row, int dst_rows, hipStream_t s);
+                      int dst_row, int dst_rows, hipStream_t s, const float* v2 = nullptr);
 int launchSiluMulQ8(bool per256, const kcSiluMulQ8FArgs& a, hipStream_t s);
 int launchMulRows(const kcMulRowsArgs& a, hipStream_t s);
 int launchSiluMul(const kcSiluMulArgs& a, hipStream_t s);
@@ -113,6 +119,7 @@ struct RopeKvRows {
     float log2_base;
     bool neox;
     int src_v, k_row, v_row, dst_rows;  // v row stride (floats), cache row strides (32-bit words), cache rows
+    const float* v2;                    // may be null: v's product in two K ranges, v + v2 stored (and into v)
 };
 int launchRopeKvRows(const RopeKvRows& r, hipStream_t s);
 int launchSetRows(const kcSetRowsF16Args& a, hipStream_t s);

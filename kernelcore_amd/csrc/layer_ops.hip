@@ -467,9 +467,11 @@ __global__ void set_rows_kernel(const float* __restrict__ src, const int* __rest
 // RoPE of q (nh heads) and k (nkv heads) of a batch, and the fp16 stores of the roped k and of v
 // into the cache rows pos[t] (rope_ggml.cu, set_rows_f16.cu): one thread per (token, group of 4
 // heads, pair), which takes theta, its cosine and sine once for its heads (q heads first, then the
-// k heads with their v). Rows outside [0, dst_rows) are not stored.
+// k heads with their v). Rows outside [0, dst_rows) are not stored. v2 (may be null): v's product
+// in two K ranges, stored as v + v2.
 __global__ void rope_qk_store_kernel(const float* __restrict__ q, float* __restrict__ qr, const float* __restrict__ k,
-                                     const float* __restrict__ v, unsigned short* __restrict__ kc,
+                                     const float* __restrict__ v, const float* __restrict__ v2,
+                                     unsigned short* __restrict__ kc,
                                      unsigned short* __restrict__ vc, const int* __restrict__ pos,
                                      const float* __restrict__ ff, int pairs, int nh, int nkv, int n, float log2_base,
                                      int m1, int m2, int dst_row, int dst_rows) {
@@ -498,8 +500,9 @@ __global__ void rope_qk_store_kernel(const float* __restrict__ q, float* __restr
             const float x0 = k[a], x1 = k[a + m2];
             kc[e] = (unsigned short)f2h(x0 * c - x1 * sn);
             kc[e + m2] = (unsigned short)f2h(x0 * sn + x1 * c);
-            vc[e] = (unsigned short)f2h(v[a]);
-            vc[e + m2] = (unsigned short)f2h(v[a + m2]);
+            const float v0 = v2 ? v[a] + v2[a] : v[a], v1 = v2 ? v[a + m2] + v2[a + m2] : v[a + m2];
+            vc[e] = (unsigned short)f2h(v0);
+            vc[e + m2] = (unsigned short)f2h(v1);
         }
     }
 }
@@ -508,13 +511,14 @@ __global__ void rope_qk_store_kernel(const float* __restrict__ q, float* __restr
 // in one launch (rope_ggml.cu, set_rows_f16.cu): one thread per (token, group of 4 heads, pair) as
 // rope_qk_store_kernel, which also keeps the roped k in kr and takes the cache rows from idx (int64,
 // low words; rows outside [0, dst_rows) are not stored). Sources: q, k contiguous [n][heads][hd];
-// v rows src_v floats apart; cache rows k_row / v_row 32-bit words apart.
+// v rows src_v floats apart (v2, when given, the second K range of v's product, the same layout:
+// v + v2 is stored, and written back into v); cache rows k_row / v_row 32-bit words apart.
 __global__ void rope_kv_rows_kernel(const float* __restrict__ q, float* __restrict__ qr, const float* __restrict__ k,
-                                    float* __restrict__ kr, const float* __restrict__ v, unsigned short* __restrict__ kc,
+                                    float* __restrict__ kr, float* __restrict__ v, unsigned short* __restrict__ kc,
                                     unsigned short* __restrict__ vc, const int* __restrict__ pos,
                                     const int* __restrict__ idx, const float* __restrict__ ff, int pairs, int nh,
                                     int nkv, int n, float log2_base, int m1, int m2, int src_v, int k_row, int v_row,
-                                    int dst_rows) {
+                                    int dst_rows, const float* __restrict__ v2) {
     const int ng = (nh + nkv + 3) / 4;
     const long long id = blockIdx.x * (long long)blockDim.x + threadIdx.x;
     if (id >= (long long)n * ng * pairs) return;
@@ -540,14 +544,24 @@ __global__ void rope_kv_rows_kernel(const float* __restrict__ q, float* __restri
             const float y0 = x0 * c - x1 * sn, y1 = x0 * sn + x1 * c;
             kr[a] = y0;
             kr[a + m2] = y1;
+            const size_t o = 2 * (size_t)hk * pairs + (size_t)i * m1;
+            const size_t av = (size_t)t * src_v + o;
+            float v0 = 0.0f, v1 = 0.0f;
+            if (v2) {  // the whole product, also back into v (stored or not)
+                v0 = v[av] + v2[av];
+                v1 = v[av + m2] + v2[av + m2];
+                v[av] = v0;
+                v[av + m2] = v1;
+            } else if (store) {
+                v0 = v[av];
+                v1 = v[av + m2];
+            }
             if (store) {
-                const size_t o = 2 * (size_t)hk * pairs + (size_t)i * m1;
                 const size_t e = (size_t)row * k_row * 2 + o, f = (size_t)row * v_row * 2 + o;
-                const size_t av = (size_t)t * src_v + o;
                 kc[e] = (unsigned short)f2h(y0);
                 kc[e + m2] = (unsigned short)f2h(y1);
-                vc[f] = (unsigned short)f2h(v[av]);
-                vc[f + m2] = (unsigned short)f2h(v[av + m2]);
+                vc[f] = (unsigned short)f2h(v0);
+                vc[f + m2] = (unsigned short)f2h(v1);
             }
         }
     }
@@ -881,10 +895,10 @@ int launchRope(const kcRopeGgmlArgs& a, hipStream_t s) {
 
 int launchRopeQKStore(const float* q, float* qr, const float* k, const float* v, int* kcache, int* vcache,
                       const int* pos, const float* ff, int head_dim, int nh, int nkv, int n, float log2_base, int neox,
-                      int dst_row, int dst_rows, hipStream_t s) {
+                      int dst_row, int dst_rows, hipStream_t s, const float* v2) {
     const int pairs = head_dim / 2;
     const long long threads = (long long)n * ((nh + nkv + 3) / 4) * pairs;
-    hipLaunchKernelGGL(rope_qk_store_kernel, dim3(blocksFor(threads)), dim3(256), 0, s, q, qr, k, v,
+    hipLaunchKernelGGL(rope_qk_store_kernel, dim3(blocksFor(threads)), dim3(256), 0, s, q, qr, k, v, v2,
                        reinterpret_cast<unsigned short*>(kcache), reinterpret_cast<unsigned short*>(vcache), pos, ff,
                        pairs, nh, nkv, n, log2_base, neox ? 1 : 2, neox ? pairs : 1, dst_row, dst_rows);
     return fromHip(hipGetLastError(), "rope + kv store");
@@ -894,10 +908,11 @@ int launchRopeKvRows(const RopeKvRows& r, hipStream_t s) {
     const int pairs = r.head_dim / 2;
     const long long threads = (long long)r.n * ((r.nh + r.nkv + 3) / 4) * pairs;
     if (threads <= 0) return 0;
-    hipLaunchKernelGGL(rope_kv_rows_kernel, dim3(blocksFor(threads)), dim3(256), 0, s, r.q, r.qr, r.k, r.kr, r.v,
+    hipLaunchKernelGGL(rope_kv_rows_kernel, dim3(blocksFor(threads)), dim3(256), 0, s, r.q, r.qr, r.k, r.kr,
+                       const_cast<float*>(r.v),
                        reinterpret_cast<unsigned short*>(r.kcache), reinterpret_cast<unsigned short*>(r.vcache), r.pos,
                        r.idx, r.ff, pairs, r.nh, r.nkv, r.n, r.log2_base, r.neox ? 1 : 2, r.neox ? pairs : 1, r.src_v,
-                       r.k_row, r.v_row, r.dst_rows);
+                       r.k_row, r.v_row, r.dst_rows, r.v2);
     return fromHip(hipGetLastError(), "rope + set_rows");
 }
 

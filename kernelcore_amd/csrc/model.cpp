@@ -67,7 +67,9 @@ struct kcModel_st {
     // activations, sized for max_batch tokens
     float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *qr = nullptr, *kr = nullptr;
     float *att = nullptr, *o = nullptr, *gate = nullptr, *up = nullptr, *sw = nullptr, *down = nullptr;
-    float *o2 = nullptr, *down2 = nullptr;  // second K-range partial sums of the batch's o / down products
+    // second K-range partial sums of the batch's o / down products, and of v's (a Q6_K v among Q4_K
+    // q and k: the grouped launch may split it alone)
+    float *o2 = nullptr, *down2 = nullptr, *v2 = nullptr;
     // the batch's quantized activations in the MFMA matmul's layout (kcamd::ActF16), for inputs of
     // n_embd, n_head * head_dim and n_ff values
     char *actE = nullptr, *actQ = nullptr, *actF = nullptr;
@@ -354,18 +356,29 @@ int decodeStepFused(kcModel_st* m, hipStream_t s) {
 int decodeAny(kcModel_st* m, hipStream_t s) { return fusedDecode(m) ? decodeStepFused(m, s) : decodeStep(m, s); }
 
 // The matrices t[0..nm) of a layer that read the same batch activations: the K-quant ones in one
-// grouped MFMA launch on the per-256 slots, each F16 one as matmul_f16 of the f32 rows xf.
+// grouped MFMA launch on the per-256 slots, each F16 one as matmul_f16 of the f32 rows xf. A matrix
+// with a second output y2[i] may be split over K (*split)[i]: its product is then y[i] + y2[i].
 int batchProj(const Layer& l, std::array<int, 3> t, std::array<const void*, 3> w,
               std::array<float*, 3> y, std::array<int, 3> rows, int nm, const int* slot, const float* xf, int k, int n,
-              hipStream_t s, const kcamd::ActF16* act) {
+              hipStream_t s, const kcamd::ActF16* act, std::array<float*, 3> y2 = {},
+              std::array<bool, 3>* split = nullptr) {
     kcamd::MmPart parts[3];
-    int np = 0;
+    int at[3], np = 0;
     for (int i = 0; i < nm; ++i) {
-        if (l.f16[t[i]]) KI_TRY(kcamd::launchMatmulF16(w[i], xf, y[i], rows[i], k, n, s));
-        else parts[np++] = kcamd::MmPart{w[i], {y[i], nullptr}, rows[i], l.q6[t[i]]};
+        if (split) (*split)[i] = false;
+        if (l.f16[t[i]]) {
+            KI_TRY(kcamd::launchMatmulF16(w[i], xf, y[i], rows[i], k, n, s));
+        } else {
+            at[np] = i;
+            parts[np++] = kcamd::MmPart{w[i], {y[i], split ? y2[i] : nullptr}, rows[i], l.q6[t[i]]};
+        }
     }
-    int ks = 1;
-    return np ? kcamd::launchMatmulGroup(parts, np, slot, k, n, 1, &ks, s, act) : 0;
+    if (!np) return 0;
+    int ks = 1, pks[3] = {1, 1, 1};
+    KI_TRY(kcamd::launchMatmulGroup(parts, np, slot, k, n, 1, &ks, s, act, split ? pks : nullptr));
+    if (split)
+        for (int j = 0; j < np; ++j) (*split)[at[j]] = pks[j] == 2;
+    return 0;
 }
 
 // n > 1 tokens (m->tokens[0..n)) at positions *n_past ..: per-256 slots and the matmuls.
@@ -396,13 +409,15 @@ int batchStep(kcModel_st* m, int n, hipStream_t s) {
                                                     c.norm_eps, s, aE, yq));
         else KI_TRY(kcamd::launchAddNormQ8K(m->x, m->down, down2, m->x, l.attn_norm, m->slotEK, E_, n, c.norm_eps, s,
                                             aE, yq));
+        std::array<bool, 3> split{};  // (v may run in two K ranges: stored as v + v2)
         KI_TRY(batchProj(l, {KC_TENSOR_WQ, KC_TENSOR_WK, KC_TENSOR_WV}, {l.wq, l.wk, l.wv}, {m->q, m->k, m->v},
-                         {Q, KV, KV}, 3, m->slotEK, m->xn, E_, n, s, aE));
+                         {Q, KV, KV}, 3, m->slotEK, m->xn, E_, n, s, aE, {nullptr, nullptr, m->v2}, &split));
         KI_TRY(qkNorm(m, l, n, s));
         // RoPE of q and k with the fp16 cache stores of k and v in one kernel
         KI_TRY(kcamd::launchRopeQKStore(c.qk_norm ? m->att : m->q, m->qr, c.qk_norm ? m->kr : m->k, m->v, l.kcache,
                                         l.vcache, m->pos, m->ones, c.head_dim, c.n_head, c.n_head_kv, n,
-                                        std::log2(c.rope_theta), c.rope_neox, KV / 2, c.max_ctx, s));
+                                        std::log2(c.rope_theta), c.rope_neox, KV / 2, c.max_ctx, s,
+                                        split[2] ? m->v2 : nullptr));
         KI_TRY(attention(m, l, n, s));
         const float* o2 = nullptr;
         if (l.f16[KC_TENSOR_WO]) {
@@ -501,6 +516,7 @@ kcError_t kcModelCreate(const kcModelConfig* cfg, kcModel_t* out) noexcept {
     KM_A(m->k, (size_t)B * KV);
     KM_A(m->kr, (size_t)B * KV);
     KM_A(m->v, (size_t)B * KV);
+    KM_A(m->v2, (size_t)B * KV);
     KM_A(m->att, (size_t)B * Q);
     KM_A(m->o, (size_t)B * E_);
     KM_A(m->o2, (size_t)B * E_);

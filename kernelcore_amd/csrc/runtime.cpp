@@ -1256,7 +1256,8 @@ const char* kcCodegenName(kcCodegen_t codegen) noexcept {
 kcError_t kcSetKernelOption(const char* option, int value) noexcept {
     return gated<Need::Nothing>("kcSetKernelOption", [&](Runtime& r) {
         static const char* known[] = {"matvec_waves", "matvec_pipe", "matvec_nt", "matmul_path", "decode_path", "attn_path", "prefill_act", "swiglu_pre",
-                                      "qkv_tiles", "matmul_waves", "ggml_extra_fusions", "matvec_af", "matmul_ws"};
+                                      "qkv_tiles", "matmul_waves", "ggml_extra_fusions", "matvec_af", "matmul_ws",
+                                      "matmul_split6"};
         if (!option) return kc::Error::InvalidValue;
         bool found = false;
         for (const char* k : known) found |= std::strcmp(k, option) == 0;
