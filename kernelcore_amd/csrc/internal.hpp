@@ -32,6 +32,8 @@ void* streamScratch(void* stream, size_t bytes);
 
 // Launch options (kcSetKernelOption).
 int option(const char* name);
+// The current device's compute units (cached per device).
+int cuCount();
 // Changes with every kcSetKernelOption call: work recorded under other options (a kept graph) is stale.
 unsigned optionsGeneration();
 

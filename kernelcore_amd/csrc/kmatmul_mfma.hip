@@ -1054,7 +1054,6 @@ size_t actBytes(int ncols, int k) {
 // (option matmul_waves: 4, 8, or 0 = by the grid). 8 wavefronts (256 weight rows, one workgroup
 // per CU) stage each activation tile once per CU instead of once per 128 rows and stagger their
 // loads; they are taken when their grid fills the CUs in whole rounds or fits in one.
-int cuCount();
 int hWaves(long long wgs8) {
     const int o = option("matmul_waves");
     if (option("matmul_path") == 7 || o == 4) return 4;
@@ -1180,19 +1179,6 @@ int runMfma(const kcMatmulKQ8Args& a, hipStream_t s) {
     return fromHip(hipGetLastError(), Q6 ? "matmul_q6k_q8k (MFMA)" : "matmul_q4k_q8k (MFMA)");
 }
 
-// The device's compute units (cached per device).
-int cuCount() {
-    static int cus[16] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return 256;
-    if (!cus[dev]) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cus[dev] = n;
-    }
-    return cus[dev];
-}
-
 // y += p over n floats (the second K half of a split launch): four per thread (both arrays 16-byte
 // aligned, as the launcher checks), the last n % 4 one each.
 __global__ void add_partial_kernel(float* __restrict__ y, const float* __restrict__ p, long long n) {
@@ -1251,6 +1237,19 @@ static __device__ __align__(256) unsigned char scratch[kFixedScratchBytes];
 void* g_fixed_scratch[kMaxDevices] = {};
 
 }  // namespace
+
+// The device's compute units (cached per device).
+int cuCount() {
+    static int cus[16] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
 
 int fixedScratchInit(int device) {
     if (device < 0 || device >= kMaxDevices) return fromHip(hipErrorInvalidDevice, "fixed scratch: device index");

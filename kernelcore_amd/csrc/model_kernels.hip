@@ -482,9 +482,19 @@ int launchGetRows(bool q6k, const void* qw, const int* tok, float* y, int n, int
     return fromHip(hipGetLastError(), "get_rows");
 }
 
+// The query heads of a KV head in one workgroup (kattn_prefill.hip) when its grid of (query tile, KV
+// head) workgroups fills the GPU; else one query head per workgroup, whose grid is G times larger
+// (option attn_path = 3: always the former, 2: always the latter).
+static bool useGqa(const AttnShape& a) {
+    const int ap = option("attn_path");
+    if (ap == 2 || !attnGqaSupports(a)) return false;
+    return ap == 3 || (long long)((a.N + 31) / 32) * a.H_kv >= cuCount();
+}
+
 template <int D>
 static int runPrefill(const float* q, const int* k, const int* v, float* out, const int* n_ctx, const AttnShape& a,
                        hipStream_t s) {
+    if (useGqa(a)) return launchAttnGqa(q, k, v, out, n_ctx, a, nullptr, 0, 0, a.max_t, s);
     const dim3 grid((a.N + 31) / 32, a.H);
     // key blocks split over 2 wavefronts for D = 128 (registers: one wavefront per SIMD), over 4
     // for D = 64 (two per SIMD)
@@ -501,6 +511,7 @@ int launchAttnMasked(const float* q, const int* k, const int* v, const unsigned 
                      float* out, const AttnShape& a, hipStream_t s) {
     if (!attnMaskedSupports(a) || m_row2 < 2 || m_row2 % 2 || T <= 0 || a.N <= 0)
         return fromHip(hipErrorInvalidValue, "attn (masked): shape");
+    if (useGqa(a)) return launchAttnGqa(q, k, v, out, nullptr, a, mask, m_row2, T, T, s);
     const dim3 grid((a.N + 31) / 32, a.H);
     if (a.D == 128)
         hipLaunchKernelGGL((attn_prefill_kernel<128, 2, true>), grid, dim3(128), 0, s, q, k, v, out, nullptr, a, mask,
@@ -514,7 +525,7 @@ int launchAttnMasked(const float* q, const int* k, const int* v, const unsigned 
 int launchAttn(const float* q, const int* k, const int* v, float* out, const int* n_ctx, const AttnShape& a,
                hipStream_t s) {
     const int ap = option("attn_path");
-    if (a.N > 1 && a.causal && ap == 0 && (a.D == 64 || a.D == 128)) {  // matrix cores, one pass
+    if (a.N > 1 && a.causal && ap != 1 && (a.D == 64 || a.D == 128)) {  // matrix cores, one pass
         return a.D == 128 ? runPrefill<128>(q, k, v, out, n_ctx, a, s) : runPrefill<64>(q, k, v, out, n_ctx, a, s);
     }
     const size_t lds = sizeof(float) * ((size_t)a.max_t + 256 + 64);

@@ -21,6 +21,12 @@ int launchAttn(const float* q, const int* k, const int* v, float* out, const int
 bool attnMaskedSupports(const AttnShape& a);
 int launchAttnMasked(const float* q, const int* k, const int* v, const unsigned short* mask, int m_row2, int T,
                      float* out, const AttnShape& a, hipStream_t s);
+// The same attention with the G = H / H_kv query heads of a KV head in one workgroup (kattn_prefill.hip,
+// G <= 4, D 64 or 128): mask null = causal over T = *n_ctx, else ggml's mask (m_row2 halves per
+// row) over t_host keys; cache_rows = the rows K and V hold.
+bool attnGqaSupports(const AttnShape& a);
+int launchAttnGqa(const float* q, const int* k, const int* v, float* out, const int* n_ctx, const AttnShape& a,
+                  const unsigned short* mask, int m_row2, int t_host, int cache_rows, hipStream_t s);
 int launchArgmaxStep(const float* logits, int n, int* tokens, int* gen, int* step, int* n_past, int max_gen,
                      hipStream_t s);
 int launchPositions(const int* n_past, int n, int* pos, long long* idx, int* n_ctx, hipStream_t s);

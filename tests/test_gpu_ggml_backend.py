@@ -320,11 +320,22 @@ def test_fused_decode_matvecs_equal_one_launch_per_node(shape, live):
     L.free()
 
 
+@pytest.mark.parametrize("attn_path", [2, 3], ids=["one-head", "gqa"])
 @pytest.mark.parametrize("shape", [gg.LayerShape(), gg.LayerShape(n_embd=1024, neox=True)], ids=["D64", "D128"])
-def test_batch_attention_with_an_irregular_mask(shape):
+def test_batch_attention_with_an_irregular_mask(shape, attn_path):
     """The matrix-core FLASH_ATTN_EXT of a batch with ggml's mask as given, not causal: random holes,
     keys 64-127 masked for every query (two whole key blocks skipped), a query with a single key,
-    keys past the prompt open to the first queries; against the oracle on the GPU's own inputs."""
+    keys past the prompt open to the first queries; against the oracle on the GPU's own inputs. Both
+    kernels: one query head per workgroup (attn_path 2) and the query heads of a KV head in one
+    workgroup (3), each the default for some grid size."""
+    kc.set_option("attn_path", attn_path)
+    try:
+        _irregular_mask_case(shape)
+    finally:
+        kc.set_option("attn_path", 0)
+
+
+def _irregular_mask_case(shape):
     N, p0 = 40, 150
     L = Layer(shape, N, p0, seed=919)
     names, _ = kc.ggml_graph_plan(L.g.nodes, attn_tokens=N)
@@ -340,6 +351,12 @@ def test_batch_attention_with_an_irregular_mask(shape):
     m[7, 130:140] = np.float16(-2.5)  # finite penalties, not only 0 / -inf
     L.mask = m.reshape(-1).view(np.uint16)
     L.put("mask", L.mask)
+    # cache rows past the view (the last key block reaches rows 190, 191) hold Inf: keys past T must
+    # not reach the products (p = 0 times Inf is NaN)
+    for c in ("k_cache", "v_cache"):
+        cache = L.get(c, np.uint16).reshape(L.s.kv_size, L.s.kv_dim)
+        cache[L.n_kv:] = 0x7C00
+        L.put(c, cache.reshape(-1))
     be = kc.GgmlBackend(graphs=1, attn_tokens=N)
     be.compute(L.g.nodes)
     kc.synchronize()

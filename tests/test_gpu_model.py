@@ -121,6 +121,35 @@ def test_model_argument_validation():
     m.close()
 
 
+@pytest.mark.parametrize("name,cfg,n_prompt,n_chunk", [("llama", LLAMA, 100, 24), ("qwen3", QWEN, 90, 64),
+                                                       ("llama", LLAMA, 65, 32)])
+def test_model_prompt_attention_kernels_agree(name, cfg, n_prompt, n_chunk):
+    """The prompt's attention with the query heads of a KV head in one workgroup (attn_path 3, the
+    default when its grid fills the GPU) against one query head per workgroup (2) and the oracle:
+    prompts and a continuing chunk whose last query tile holds a single query (65: a key block
+    reaching past the context, whose cache rows were never written)."""
+    w = random_weights(cfg, 7)
+    prompt = np.random.default_rng(3).integers(0, cfg["n_vocab"], n_prompt + n_chunk).astype(np.int32)
+    got = {}
+    for ap in (2, 3):
+        kc.set_option("attn_path", ap)
+        try:
+            m = kc.Model(**cfg)
+            for (tid, layer), data in w.items():
+                m.set_tensor(tid, layer, data)
+            got[ap] = [m.forward(prompt[:n_prompt]), m.forward(prompt[n_prompt:])]
+            m.close()
+        finally:
+            kc.set_option("attn_path", 0)
+    o = OracleModel(cfg, w)
+    for i, part in enumerate((prompt[:n_prompt], prompt[n_prompt:])):
+        lo = o.forward(part)
+        note(f"attention kernels {name} {n_prompt}+{n_chunk} part {i}: rel L2 {rel_l2(got[3][i], lo):.2e}, "
+             f"kernels {rel_l2(got[3][i], got[2][i]):.2e}")
+        assert rel_l2(got[3][i], lo) < 1e-2
+        assert rel_l2(got[3][i], got[2][i]) < 1e-6  # (the same products and sums: equal in practice)
+
+
 def test_model_3b_shape_two_layers():
     """Two layers at the full Llama-3.2-3B widths (3072 / 24 heads / 8 KV heads / 8192 FFN / 128256
     vocab): an 8-token prompt and two decode steps against the oracle."""
