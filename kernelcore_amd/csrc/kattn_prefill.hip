@@ -36,6 +36,8 @@ namespace kcamd {
 namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef short s4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s4* LdsS4;
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void* LdsPtr;
 
@@ -181,6 +183,9 @@ __global__ __launch_bounds__(512) void attn_prefill_gqa_kernel(const float* __re
     __syncthreads();
     const int koff = j * Geo::kKRow + 16 * h;  // this lane's K row (A operand), half h
     const _Float16* vcol = nullptr;
+    // this lane's row for the transposed V reads: group g = lane / 16 (lane half h = g / 2, d 16 (g % 2)
+    // on), lane L = lane % 16 of it: key 4 h + L / 4, d 16 (g % 2) + 4 (L % 4)
+    const int vlane = (4 * (lane >> 5) + ((lane & 15) >> 2)) * (Geo::kKRow / 2) + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
     int rc = 0, rn = 2;  // ring slots of block it and of block it + 2
     for (int it = 0; it < nit; ++it) {
         const int kb = kSplits * it + sp, kbn = kb + 2 * kSplits;
@@ -258,17 +263,20 @@ __global__ __launch_bounds__(512) void attn_prefill_gqa_kernel(const float* __re
             for (int t = 0; t < DB; ++t)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) o[t][v] *= alpha;
-            // O^T += V^T P^T: for half mm of the block's keys in kappa order, lane (j, h) gathers
-            // V[16 mm + 8 (e / 4) + 4 h + e % 4][32 t + j] for e = 0..7
-            vcol = reinterpret_cast<const _Float16*>(cur + Geo::kKBytes) + j;
+            // O^T += V^T P^T: for half mm of the block's keys in kappa order, lane (j, h) needs
+            // V[16 mm + 8 (e / 4) + 4 h + e % 4][32 t + j] for e = 0..7: two transposed reads
+            // (ds_read_b64_tr_b16: in each group of 16 lanes, lane i receives element i % 4 of the
+            // rows lanes 4 e + i / 4 address, e = 0..3; lane L here addresses V[key + L / 4][d0 +
+            // 4 (L % 4)], so lane i receives V[key + e][d0 + i])
+            vcol = reinterpret_cast<const _Float16*>(cur + Geo::kKBytes) + vlane;
 #pragma unroll
             for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
                 for (int t = 0; t < DB; ++t) {
-                    h8 va;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        va[e] = vcol[(16 * mm + 8 * (e >> 2) + 4 * h + (e & 3)) * (Geo::kKRow / 2) + 32 * t];
+                    const _Float16* vp = vcol + 16 * mm * (Geo::kKRow / 2) + 32 * t;
+                    const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LdsS4)vp);
+                    const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LdsS4)(vp + 8 * (Geo::kKRow / 2)));
+                    const h8 va = __builtin_bit_cast(h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
                     o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pa[mm], o[t], 0, 0, 0);
                     o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pl[mm], o[t], 0, 0, 0);
                 }
