@@ -209,6 +209,8 @@ __global__ void positions_kernel(const int* __restrict__ n_past, int n, int* pos
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short s4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s4* LdsS4;
 
 // Causal attention of a batch of N queries (positions p0 .. p0 + N - 1, p0 = T - N, T = *n_ctx)
 // on the matrix cores, v_mfma_f32_32x32x16_f16, in one pass over the keys per (query tile of 32,
@@ -256,6 +258,9 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(const float* __res
     const int head = blockIdx.y, kvh = head / (a.H / a.H_kv);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5;
     _Float16* vs = vsall + wave * 32 * VR;
+    // this lane's row for the transposed V reads: group g = lane / 16 (lane half h = g / 2, d 16 (g % 2)
+    // on), lane L = lane % 16 of it: key 4 h + L / 4, d 16 (g % 2) + 4 (L % 4)
+    const int vlane = (4 * h + ((lane & 15) >> 2)) * VR + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
     float* qw = qx[wave][0];
     const int* kb0 = kc + (size_t)kvh * (D / 2);
     const int* vb0 = vc + (size_t)kvh * (D / 2);
@@ -403,13 +408,13 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(const float* __res
         for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
-                const _Float16* vp = vs + (16 * mm + 4 * h) * VR + 32 * db + j;
-                h8 vbv;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    vbv[e] = vp[e * VR];
-                    vbv[4 + e] = vp[(8 + e) * VR];
-                }
+                // V[16 mm + 8 (e / 4) + 4 h + e % 4][32 db + j], e = 0..7, by two transposed reads
+                // (ds_read_b64_tr_b16: in each group of 16 lanes, lane i receives element i % 4 of the
+                // four halves lanes 4 e + i / 4 address; lane L addresses V[key + L / 4][d0 + 4 (L % 4)])
+                const _Float16* vp = vs + vlane + 16 * mm * VR + 32 * db;
+                const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LdsS4)vp);
+                const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LdsS4)(vp + 8 * VR));
+                const h8 vbv = __builtin_bit_cast(h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
                 o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[mm], vbv, o[db], 0, 0, 0);
                 o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pl[mm], vbv, o[db], 0, 0, 0);
             }
