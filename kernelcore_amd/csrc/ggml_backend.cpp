@@ -964,7 +964,7 @@ E batchGroup(Pass& p, const T* const* mm, int g) {
         parts[j] = kcamd::MmPart{w->data, {f32w(mm[j]), nullptr}, int(w->ne[1]), w->type == KC_GGML_TYPE_Q6_K ? 1 : 0};
     }
     const int rows0 = parts[0].rows;
-    const int ks = g == 1 ? kcamd::matmulKs(rows0, k, ncols) : 1;
+    const int ks = g == 1 ? kcamd::matmulKs(rows0, k, ncols, parts[0].q6 != 0) : 1;
     if (ks == 2) {  // the second K half's partial sums
         int* part = nullptr;
         if (E e = kcamd::mulmat::take(p.rec, size_t(rows0) * size_t(ncols), &part); e != ok) return e;

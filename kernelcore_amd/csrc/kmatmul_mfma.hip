@@ -1054,6 +1054,12 @@ size_t actBytes(int ncols, int k) {
 // (option matmul_waves: 4, 8, or 0 = by the grid). 8 wavefronts (256 weight rows, one workgroup
 // per CU) stage each activation tile once per CU instead of once per 128 rows and stagger their
 // loads; they are taken when their grid fills the CUs in whole rounds or fits in one.
+// Whether runMfmaH runs a matrix of this type on the producer-wavefront kernel.
+bool wsRuns(bool q6) {
+    const int ws = option("matmul_ws"), path = option("matmul_path");
+    return ws != 1 && !(ws == 3 && q6) && (path == 0 || path == 2);
+}
+
 int hWaves(long long wgs8) {
     const int o = option("matmul_waves");
     if (option("matmul_path") == 7 || o == 4) return 4;
@@ -1091,8 +1097,8 @@ int runMfmaH(const MmPart* parts, int nparts, const int* xq, int k, int ncols, i
     for (int i = 0; i < nparts; ++i) tiles8 += (parts[i].rows + 255) / 256;
     // the producer-wavefront kernel (256-row tiles) unless option matmul_ws = 1 (3: for Q4_K-only
     // groups, a group with a Q6_K matrix on the kernel above)
-    bool ws = option("matmul_ws") != 1 && (option("matmul_path") == 0 || option("matmul_path") == 2);
-    for (int i = 0; i < nparts; ++i) ws = ws && !(option("matmul_ws") == 3 && parts[i].q6);
+    bool ws = true;
+    for (int i = 0; i < nparts; ++i) ws = ws && wsRuns(parts[i].q6 != 0);
     const int nw = ws ? 8 : hWaves(tiles8 * ((ncols + G::kCols - 1) / G::kCols) * ks);
     const int wg_rows = ws ? mfmaWsRows() : 32 * nw;
     HGroup g{};
@@ -1204,7 +1210,7 @@ __global__ void add_partial1_kernel(float* __restrict__ y, const float* __restri
 // A by-name launch on the fp16-activation kernel: a grid under two workgroups of 4 wavefronts per
 // CU splits K in two, the second half's partial sums staged after the activations and added into
 // y by one more kernel (fl(a + b): the same for either order).
-int stagedKs(const kcMatmulKQ8Args& a) { return matmulKs(a.rows, a.k, a.ncols); }
+int stagedKs(bool q6k, const kcMatmulKQ8Args& a) { return matmulKs(a.rows, a.k, a.ncols, q6k); }
 size_t stagedActBytes(const kcMatmulKQ8Args& a) { return (actBytes(a.ncols, a.k) + 255) & ~size_t(255); }
 size_t stagedBytes(const kcMatmulKQ8Args& a, int ks) {
     return stagedActBytes(a) + (ks == 2 ? (size_t)a.rows * a.ncols * 4 : 0);
@@ -1273,7 +1279,7 @@ int launchMatmulKqNoAlloc(bool q6k, bool per256, const kcMatmulKQ8Args& a, hipSt
     if (path == 4) return q6k ? runMfma8<true, 2>(a, s) : runMfma8<false, 2>(a, s);
     if (path == 5) return q6k ? runMfma8<true, 1>(a, s) : runMfma8<false, 1>(a, s);
     // the K split of launchMatmulMfma when its partial sums fit too, else one K range
-    int ks = stagedKs(a);
+    int ks = stagedKs(q6k, a);
     if (ks == 2 && stagedBytes(a, 2) > kFixedScratchBytes) ks = 1;
     const size_t need = stagedBytes(a, ks);
     if (need > kFixedScratchBytes) {
@@ -1292,9 +1298,15 @@ int launchMatmulKqNoAlloc(bool q6k, bool per256, const kcMatmulKQ8Args& a, hipSt
     return runStaged(q6k, a, ks, p, s);
 }
 
-int matmulKs(int rows, int k, int ncols) {
-    const long long wgs = (long long)((rows + kBM - 1) / kBM) * ((ncols + 63) / 64);
-    return (k / 256 >= 2 && wgs < 2LL * cuCount()) ? 2 : 1;
+// K split in two where one K range leaves compute units idle. The producer-wavefront kernel holds
+// one workgroup per CU, so it splits only when twice its workgroups still run at once (a 4096-row
+// matrix over 1024 columns, 256 workgroups: 45.7 us in one K range, 51.5 us in two, the partial
+// sums' extra pass included); the other kernels split below two 128-row workgroups per CU.
+int matmulKs(int rows, int k, int ncols, bool q6) {
+    if (k / 256 < 2) return 1;
+    const long long ct = (ncols + 63) / 64;
+    if (wsRuns(q6)) return 2LL * ((rows + mfmaWsRows() - 1) / mfmaWsRows()) * ct <= cuCount() ? 2 : 1;
+    return (long long)((rows + kBM - 1) / kBM) * ct < 2LL * cuCount() ? 2 : 1;
 }
 
 bool mfmaHUsable(int ncols, int k) {
@@ -1309,7 +1321,7 @@ int launchMatmulMfma(bool q6k, const kcMatmulKQ8Args& a, hipStream_t s) {
     if (path == 4) return q6k ? runMfma8<true, 2>(a, s) : runMfma8<false, 2>(a, s);
     // fp16 activations staged by direct loads (a per-stream buffer, addressed with 32-bit offsets)
     if (path != 5 && (size_t)a.ncols * a.k * 2 < (1ull << 32)) {
-        const int ks = stagedKs(a);
+        const int ks = stagedKs(q6k, a);
         if (void* buf = streamScratch(s, stagedBytes(a, ks))) return runStaged(q6k, a, ks, buf, s);
     }
     return q6k ? runMfma8<true, 1>(a, s) : runMfma8<false, 1>(a, s);
@@ -1320,7 +1332,7 @@ size_t matmulStagingBytes(int rows, int k, int ncols) {
     if (!(path == 0 && ncols >= 64) && !(path >= 2 && path != 3 && path != 4 && path != 5)) return 0;
     if ((size_t)ncols * k * 2 >= (1ull << 32)) return 0;
     const kcMatmulKQ8Args a{nullptr, nullptr, nullptr, nullptr, rows, k, ncols, 8};
-    return stagedBytes(a, stagedKs(a));
+    return stagedBytes(a, std::max(stagedKs(false, a), stagedKs(true, a)));  // (either type)
 }
 
 bool matmulGroupSplitsQ6(const MmPart* parts, int nparts, int k, int ncols) {

@@ -72,8 +72,9 @@ int launchMatmulGroup(const MmPart* parts, int nparts, const int* xq, int k, int
                       hipStream_t s, const ActF16* pre = nullptr, int* part_ks = nullptr);
 // Whether a group of ncols >= 64 columns of k values runs on the fp16-activation MFMA kernel.
 bool mfmaHUsable(int ncols, int k);
-// The K ranges a by-name launch of this shape takes (2 when its grid is under two workgroups per CU).
-int matmulKs(int rows, int k, int ncols);
+// The K ranges a launch of this shape and weight type takes (2 where one K range would leave compute
+// units idle).
+int matmulKs(int rows, int k, int ncols, bool q6);
 // kmatmul_f16.hip: Y [ncols][rows] = W X, W row-major fp16 [rows][k], x ncols columns of k floats;
 // rows % 8 == 0, k even.
 int launchMatmulF16(const void* w, const float* x, float* y, int rows, int k, int ncols, hipStream_t s);

@@ -389,8 +389,9 @@ int batchStep(kcModel_st* m, int n, hipStream_t s) {
     KI_TRY(kcamd::launchPositions(m->n_past, n, m->pos, m->idx, m->n_ctx, s));
     KI_TRY(kcamd::launchGetRows(m->q6_tok, m->tok_embd, m->tokens, m->x, n, E_, c.n_vocab, s));
     float* x_last = m->x + (size_t)(n - 1) * E_;
-    // the products that read the same activations share one launch; o and down split K in two
-    // (the two partial sums are added in the residual add that consumes them)
+    // the products that read the same activations share one launch; o and down split K in two where
+    // one K range would leave CUs idle (the two partial sums are added in the residual add that
+    // consumes them)
     const float* down2 = nullptr;
     int ks = 1;
     // the quantizers also write the MFMA layout, so the matmuls launch no conversion
@@ -425,7 +426,8 @@ int batchStep(kcModel_st* m, int n, hipStream_t s) {
         } else {
             KI_TRY(kcamd::launchQuantizeColsK(m->att, m->slotQK, Q, n, s, aQ));
             const kcamd::MmPart op{l.wo, {m->o, m->o2}, E_, l.q6[KC_TENSOR_WO]};
-            KI_TRY(kcamd::launchMatmulGroup(&op, 1, m->slotQK, Q, n, 2, &ks, s, aQ));
+            KI_TRY(kcamd::launchMatmulGroup(&op, 1, m->slotQK, Q, n, kcamd::matmulKs(E_, Q, n, op.q6 != 0), &ks, s,
+                                            aQ));
             o2 = ks == 2 ? m->o2 : nullptr;
         }
         if (li + 1 < c.n_layer) {
@@ -443,7 +445,8 @@ int batchStep(kcModel_st* m, int n, hipStream_t s) {
                 down2 = nullptr;
             } else {
                 const kcamd::MmPart dp{l.wd, {m->down, m->down2}, E_, l.q6[KC_TENSOR_W_DOWN]};
-                KI_TRY(kcamd::launchMatmulGroup(&dp, 1, m->slotFK, c.n_ff, n, 2, &ks, s, aF));
+                KI_TRY(kcamd::launchMatmulGroup(&dp, 1, m->slotFK, c.n_ff, n, kcamd::matmulKs(E_, c.n_ff, n, dp.q6 != 0),
+                                                &ks, s, aF));
                 down2 = ks == 2 ? m->down2 : nullptr;
             }
         } else {  // the last layer continues with the last token only
