@@ -264,6 +264,17 @@ struct Pass {
         bool views;
     };
     std::vector<Pending> pending{};
+    // The summaries the pass's masked attention launches read (mask_summary_kernel), one per mask
+    // tensor: every layer's attention reads the same mask, whose values stay as they are while a
+    // later node still reads it (ggml reuses a tensor's memory only after its last reader). An entry
+    // holds while the scratch it lies in does (gen).
+    struct MaskSum {
+        const T* mask;
+        int N, T_keys;
+        unsigned gen;
+        int* sum;
+    };
+    std::vector<MaskSum> masks{};
 };
 
 const float* onesOf(Pass& p, int n) {
@@ -906,8 +917,26 @@ E flashAttn(Pass& p, const T* dst) {
     const kcamd::AttnShape as{d.N, d.H, d.H_kv, d.D, d.q_tok, d.k_row, d.T, 0, scale};
     if (maskedAttn(dst)) {
         const auto* mh = static_cast<const unsigned short*>(mask->data);
+        // the mask's summary per query tile: computed by the first masked attention that reads it
+        int* sum = nullptr;
+        bool fresh = true;
+        for (const auto& m : p.masks)
+            if (m.mask == mask && m.N == d.N && m.T_keys == d.T && m.gen == p.rec.gen) {
+                sum = m.sum;
+                fresh = false;
+            }
+        if (fresh) {
+            if (E e = kcamd::mulmat::take(p.rec, size_t(kcamd::maskSummaryInts(d.N)), &sum); e != ok) return e;
+            try {
+                p.masks.push_back({mask, d.N, d.T, p.rec.gen, sum});
+            } catch (...) {
+                return kc::Error::OutOfMemory;
+            }
+        }
         return direct(p, "attn_masked", [&](hipStream_t s) {
-            return kcamd::launchAttnMasked(f32(q), kd, vd, mh, 2 * d.m_row, d.T, f32w(dst), as, s);
+            if (fresh)
+                if (int st = kcamd::launchMaskSummary(mh, 2 * d.m_row, d.N, d.T, sum, s)) return st;
+            return kcamd::launchAttnMasked(f32(q), kd, vd, mh, 2 * d.m_row, d.T, f32w(dst), as, sum, s);
         });
     }
     if (d.T <= 16384) {

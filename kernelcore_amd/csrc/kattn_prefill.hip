@@ -9,6 +9,9 @@
 // (and ggml's mask for the tile's 32 queries) arrive by buffer-to-LDS loads (rows padded by 16 B:
 // the lanes of a read hit different banks) into a ring of three blocks, so two blocks' loads are in
 // flight while one is computed (a memory round trip under this load outlasts a block's work).
+// A causal prompt's tile reads the key blocks up to its last query. A masked one reads those its
+// mask summary (mask_summary_kernel) names, lo .. hi, and loads the mask's values only for blocks
+// mlo .. mhi (the others hold 0 for all 32 queries: the causal mask's blocks below the diagonal).
 //
 // Per wavefront (32 queries of one head, lane (j, h) = query j, lane half h):
 //   S^T = K Q^T: v_mfma_f32_32x32x16_f16 with A = K rows (LDS), B = q split into fp16 hi = fp16(x)
@@ -64,13 +67,15 @@ struct AttnGeo {
     static constexpr int kMerge(int G) { return G * 64 * kORow * 4; }
 };
 
-// MASKED: ggml's mask rows (m_row2 halves each) over t_host keys instead of the causal positions.
+// MASKED: ggml's mask rows (m_row2 halves each) over t_host keys instead of the causal positions,
+// msum the mask's summary per query tile ({lo, hi, mlo, mhi}).
 template <int D, bool MASKED>
 __global__ __launch_bounds__(512) void attn_prefill_gqa_kernel(const float* __restrict__ q, const int* __restrict__ kc,
                                                                const int* __restrict__ vc, float* __restrict__ out,
                                                                const int* __restrict__ n_ctx, AttnShape a,
                                                                const unsigned short* __restrict__ mask, int m_row2,
-                                                               int t_host, int cache_rows) {
+                                                               int t_host, int cache_rows,
+                                                               const int* __restrict__ msum) {
     using Geo = AttnGeo<D>;
     constexpr int KS = D / 16, DB = D / 32;
     extern __shared__ int4 lds4[];
@@ -85,8 +90,19 @@ __global__ __launch_bounds__(512) void attn_prefill_gqa_kernel(const float* __re
     const int head = kvh * G + gw;
     const int j = lane & 31, h = lane >> 5;
     const int qpos = p0 + i0 + j;
-    const int nkb = MASKED ? (T + 31) / 32 : min(p0 + i0 + 31, T - 1) / 32 + 1;
-    const int nit = (nkb + kSplits - 1) / kSplits;
+    // key blocks kb0 .. kend - 1 (causal: up to the tile's last query), those of mlo .. mhi with the
+    // mask's values
+    int kb0 = 0, kend = min(p0 + i0 + 31, T - 1) / 32 + 1, mlo = 0, mhi = -1;
+    if constexpr (MASKED) {
+        const int* ms = msum + 4 * (i0 / 32);
+        const int lo = ms[0], hi = ms[1];
+        kb0 = lo <= hi ? lo : 0;
+        kend = lo <= hi ? hi + 1 : 0;
+        mlo = ms[2];
+        mhi = ms[3];
+    }
+    auto mixed = [&](int kb) { return MASKED && kb >= mlo && kb <= mhi; };
+    const int nit = (kend - kb0 + kSplits - 1) / kSplits;
     char* sbuf = lds + sp * kRing * Geo::kBuf;  // this split's ring
 
     // q of this lane's query as the B operand: hi / lo fp16 of values 16 ks + 8 h .. + 8
@@ -122,11 +138,12 @@ __global__ __launch_bounds__(512) void attn_prefill_gqa_kernel(const float* __re
     const __amdgpu_buffer_rsrc_t rk = bufRes(kc + (size_t)kvh * (D / 2), span);
     const __amdgpu_buffer_rsrc_t rv = bufRes(vc + (size_t)kvh * (D / 2), span);
     const __amdgpu_buffer_rsrc_t rm = bufRes(mask, MASKED ? (uint32_t)((size_t)N * m_row2 * 2) : 0u);
-    constexpr int kNL = 2 * Geo::kKLoads + (MASKED ? Geo::kMLoads : 0);
-    const int per = (kNL + G - 1) / G;  // loads per wavefront and block
+    // loads per wavefront of block kb (with the mask's values or without)
+    auto loadsOf = [&](int kb) { return (2 * Geo::kKLoads + (mixed(kb) ? Geo::kMLoads : 0) + G - 1) / G; };
     auto issue = [&](int kb, char* buf) {
+        const int nl = 2 * Geo::kKLoads + (mixed(kb) ? Geo::kMLoads : 0), per = (nl + G - 1) / G;
         for (int i = 0; i < per; ++i) {
-            const int L = min(gw + G * i, kNL - 1);
+            const int L = min(gw + G * i, nl - 1);
             if (L < 2 * Geo::kKLoads) {
                 const int LL = L < Geo::kKLoads ? L : L - Geo::kKLoads;
                 const int slot = LL * 64 + lane, key = min(slot / (Geo::kCpr + 1), 31), c = slot % (Geo::kCpr + 1);
@@ -146,9 +163,8 @@ __global__ __launch_bounds__(512) void attn_prefill_gqa_kernel(const float* __re
             }
         }
     };
-    // wait for all but this wavefront's loads of the last `ahead` blocks issued
-    auto waitBut = [&](int ahead) {
-        const int n = ahead * per;
+    // wait for all but this wavefront's last n loads
+    auto waitBut = [&](int n) {
         switch (n) {
 #define KC_VMCNT(x) \
     case x: asm volatile("s_waitcnt vmcnt(" #x ")" ::: "memory"); break;
@@ -173,10 +189,10 @@ __global__ __launch_bounds__(512) void attn_prefill_gqa_kernel(const float* __re
     float m = -INFINITY, l = 0.0f;
 
     // block it of this split: kb = kSplits it + sp, in ring slot it % kRing
-    if (sp < nkb) issue(sp, sbuf);
-    if (sp + kSplits < nkb) {
-        issue(sp + kSplits, sbuf + Geo::kBuf);
-        waitBut(1);
+    if (kb0 + sp < kend) issue(kb0 + sp, sbuf);
+    if (kb0 + sp + kSplits < kend) {
+        issue(kb0 + sp + kSplits, sbuf + Geo::kBuf);
+        waitBut(loadsOf(kb0 + sp + kSplits));
     } else {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
@@ -188,12 +204,15 @@ __global__ __launch_bounds__(512) void attn_prefill_gqa_kernel(const float* __re
     const int vlane = (4 * (lane >> 5) + ((lane & 15) >> 2)) * (Geo::kKRow / 2) + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
     int rc = 0, rn = 2;  // ring slots of block it and of block it + 2
     for (int it = 0; it < nit; ++it) {
-        const int kb = kSplits * it + sp, kbn = kb + 2 * kSplits;
+        const int kb = kb0 + kSplits * it + sp, kbn = kb + 2 * kSplits;
         char* cur = sbuf + rc * Geo::kBuf;
-        if (kbn < nkb) issue(kbn, sbuf + rn * Geo::kBuf);  // (its slot held block it - 1)
-        bool work = kb < nkb;
+        if (kbn < kend) issue(kbn, sbuf + rn * Geo::kBuf);  // (its slot held block it - 1)
+        bool work = kb < kend;
         float mval[16];
-        if constexpr (MASKED) {  // a block whose mask is -inf for every query of the tile adds nothing
+        if (!mixed(kb)) {  // (the block's mask is 0 for every query of the tile)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) mval[v] = 0.0f;
+        } else {  // a block whose mask is -inf for every query of the tile adds nothing
             uint32_t mk[8];
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
@@ -221,10 +240,10 @@ __global__ __launch_bounds__(512) void attn_prefill_gqa_kernel(const float* __re
                 sh = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qb[ks], sh, 0, 0, 0);
                 sl = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, ql[ks], sl, 0, 0, 0);
             }
-            // scores of the lane's 16 keys; the causal limit and the end of the context only in the
-            // blocks that reach them (a uniform branch)
+            // scores of the lane's 16 keys; the causal limit (MASKED: the mask's values) and the end of
+            // the context only in the blocks that reach them (a uniform branch)
             float sc[16];
-            if (MASKED || kb * 32 + 31 > p0 + i0 || kb * 32 + 31 >= T) {
+            if ((MASKED ? mixed(kb) : kb * 32 + 31 > p0 + i0) || kb * 32 + 31 >= T) {
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
                     const int key = kb * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
@@ -281,7 +300,7 @@ __global__ __launch_bounds__(512) void attn_prefill_gqa_kernel(const float* __re
                     o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pl[mm], o[t], 0, 0, 0);
                 }
         }
-        if (kbn < nkb) waitBut(1);  // block it + 1 landed (block it + 2 may still be in flight)
+        if (kbn < kend) waitBut(loadsOf(kbn));  // block it + 1 landed (block it + 2 may still be in flight)
         else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();  // block it read by every wavefront; block it + 1 staged
         rc = rc == kRing - 1 ? 0 : rc + 1;
@@ -325,7 +344,7 @@ __global__ __launch_bounds__(512) void attn_prefill_gqa_kernel(const float* __re
 
 template <int D, bool MASKED>
 int launchGqa(const float* q, const int* k, const int* v, float* out, const int* n_ctx, const AttnShape& a,
-              const unsigned short* mask, int m_row2, int t_host, int cache_rows, hipStream_t s) {
+              const unsigned short* mask, int m_row2, int t_host, int cache_rows, const int* msum, hipStream_t s) {
     using Geo = AttnGeo<D>;
     const int G = a.H / a.H_kv;
     const int lds = std::max(Geo::kLoop, Geo::kMerge(G));
@@ -334,7 +353,7 @@ int launchGqa(const float* q, const int* k, const int* v, float* out, const int*
     if (attr != 0) return fromHip(attr, "attn (prefill, GQA): LDS size");
     const dim3 grid((a.N + 31) / 32, a.H_kv);
     hipLaunchKernelGGL((attn_prefill_gqa_kernel<D, MASKED>), grid, dim3(64 * G * kSplits), lds, s, q, k, v, out,
-                       n_ctx, a, mask, m_row2, t_host, cache_rows);
+                       n_ctx, a, mask, m_row2, t_host, cache_rows, msum);
     return fromHip(hipGetLastError(), MASKED ? "attn (masked, GQA)" : "attn (prefill, GQA)");
 }
 
@@ -347,14 +366,15 @@ bool attnGqaSupports(const AttnShape& a) {
 }
 
 int launchAttnGqa(const float* q, const int* k, const int* v, float* out, const int* n_ctx, const AttnShape& a,
-                  const unsigned short* mask, int m_row2, int t_host, int cache_rows, hipStream_t s) {
-    if (!attnGqaSupports(a) || cache_rows <= 0) return fromHip(hipErrorInvalidValue, "attn (GQA): shape");
+                  const unsigned short* mask, int m_row2, int t_host, int cache_rows, const int* msum, hipStream_t s) {
+    if (!attnGqaSupports(a) || cache_rows <= 0 || (mask && !msum))
+        return fromHip(hipErrorInvalidValue, "attn (GQA): shape");
     const bool masked = mask != nullptr;
     if (a.D == 128)
-        return masked ? launchGqa<128, true>(q, k, v, out, n_ctx, a, mask, m_row2, t_host, cache_rows, s)
-                      : launchGqa<128, false>(q, k, v, out, n_ctx, a, mask, m_row2, t_host, cache_rows, s);
-    return masked ? launchGqa<64, true>(q, k, v, out, n_ctx, a, mask, m_row2, t_host, cache_rows, s)
-                  : launchGqa<64, false>(q, k, v, out, n_ctx, a, mask, m_row2, t_host, cache_rows, s);
+        return masked ? launchGqa<128, true>(q, k, v, out, n_ctx, a, mask, m_row2, t_host, cache_rows, msum, s)
+                      : launchGqa<128, false>(q, k, v, out, n_ctx, a, mask, m_row2, t_host, cache_rows, msum, s);
+    return masked ? launchGqa<64, true>(q, k, v, out, n_ctx, a, mask, m_row2, t_host, cache_rows, msum, s)
+                  : launchGqa<64, false>(q, k, v, out, n_ctx, a, mask, m_row2, t_host, cache_rows, msum, s);
 }
 
 }  // namespace kcamd

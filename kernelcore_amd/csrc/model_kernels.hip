@@ -4,6 +4,7 @@
 // with its bookkeeping, and the per-step position update.
 #include <hip/hip_runtime.h>
 
+#include <climits>
 #include <cstdint>
 
 #include "internal.hpp"
@@ -235,14 +236,17 @@ typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 
 // MASKED: FLASH_ATTN_EXT's form for the ggml backend -- the N queries attend over T = t_host keys
 // with ggml's f16 mask (row i of m_row2 halves: dot * scale + mask[i][key], the oracle's order)
-// instead of the causal positions; a key block whose mask is -inf for every query of the tile is
-// skipped (it would add nothing).
+// instead of the causal positions. msum holds the tile's mask summary (mask_summary_kernel): only
+// its key blocks lo .. hi are read, and only blocks mlo .. mhi load and add the mask's values (the
+// others hold 0 for every query of the tile); a block among those whose mask is -inf for every query
+// of the tile is skipped (it would add nothing).
 template <int D, int W, bool MASKED = false>
 __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(const float* __restrict__ q, const int* __restrict__ kc,
                                                                const int* __restrict__ vc, float* __restrict__ out,
                                                                const int* __restrict__ n_ctx, AttnShape a,
                                                                const unsigned short* __restrict__ mask = nullptr,
-                                                               int m_row2 = 0, int t_host = 0) {
+                                                               int m_row2 = 0, int t_host = 0,
+                                                               const int* __restrict__ msum = nullptr) {
     constexpr int KS = D / 16, DB = D / 32;
     constexpr int VR = D + 8;        // halves per V row in LDS
     constexpr int CPR = D / 8;       // 16-byte chunks per V row
@@ -283,7 +287,18 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(const float* __res
         }
     }
     const int qpos = p0 + i0 + j;
-    const int nkb = MASKED ? (T + 31) / 32 : min(p0 + i0 + 31, T - 1) / 32 + 1;
+    // key blocks bk0 .. bkend - 1 (causal: up to the tile's last query), those of mlo .. mhi with the
+    // mask's values
+    int bk0 = 0, bkend = min(p0 + i0 + 31, T - 1) / 32 + 1, mlo = 0, mhi = -1;
+    if constexpr (MASKED) {
+        const int* ms = msum + 4 * (i0 / 32);
+        const int lo = ms[0], hi = ms[1];
+        bk0 = lo <= hi ? lo : 0;
+        bkend = lo <= hi ? hi + 1 : 0;
+        mlo = ms[2];
+        mhi = ms[3];
+    }
+    auto mixed = [&](int kb) { return MASKED && kb >= mlo && kb <= mhi; };
     // MASKED: this lane's 16 mask values of a key block (keys 32 kb + 8 g + 4 h + 0..3) as 8 words,
     // read inside the query's row (keys past it are dropped by key < T)
     const unsigned short* mrow = MASKED ? mask + (size_t)min(i0 + j, N - 1) * m_row2 : nullptr;
@@ -320,27 +335,31 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(const float* __res
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
-    if (wave < nkb) {
-        loadK(wave, ka);
-        loadV(wave);
-        if constexpr (MASKED) loadM(wave, mk);
+    if (bk0 + wave < bkend) {
+        loadK(bk0 + wave, ka);
+        loadV(bk0 + wave);
+        if (mixed(bk0 + wave)) loadM(bk0 + wave, mk);
     }
     f32x16 o[DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db) o[db] = zero;
     float m = -INFINITY, l = 0.0f;
-    for (int kb = wave; kb < nkb; kb += W) {
+    for (int kb = bk0 + wave; kb < bkend; kb += W) {
         waveSync();  // the previous block's LDS reads are done
 #pragma unroll
         for (int r = 0; r < VL; ++r)
             *reinterpret_cast<u32x4v*>(vs + (r * RPL + lane / CPR) * VR + (lane % CPR) * 8) = vr[r];
-        if (kb + W < nkb) {
+        const bool mx = mixed(kb), mxn = kb + W < bkend && mixed(kb + W);
+        if (kb + W < bkend) {
             loadK(kb + W, kn);
             loadV(kb + W);
-            if constexpr (MASKED) loadM(kb + W, mkn);
+            if (mxn) loadM(kb + W, mkn);
         }
         float mval[16];
-        if constexpr (MASKED) {
+        if (!mx) {  // (the block's mask is 0 for every query of the tile)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) mval[v] = 0.0f;
+        } else {
             bool any = false;
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
@@ -350,11 +369,12 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(const float* __res
                 any |= key_abs < T && mval[v] != -INFINITY;
             }
             if (__ballot(any) == 0) {  // every score of the block masked: nothing to add
-                if (kb + W < nkb) {
+                if (kb + W < bkend) {
 #pragma unroll
                     for (int ks = 0; ks < KS; ++ks) ka[ks] = kn[ks];
+                    if (mxn)
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) mk[e] = mkn[e];
+                        for (int e = 0; e < 8; ++e) mk[e] = mkn[e];
                 }
                 continue;
             }
@@ -365,16 +385,26 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(const float* __res
             sh = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks], qb[ks], sh, 0, 0, 0);
             sl = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks], ql[ks], sl, 0, 0, 0);
         }
+        // the causal limit (MASKED: the mask's values) and the end of the context only in the blocks
+        // that reach them (a uniform branch)
         f32x16 sacc;
         float bm = -INFINITY;
+        if ((MASKED ? mx : kb * 32 + 31 > p0 + i0) || kb * 32 + 31 >= T) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int key_abs = kb * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-            if constexpr (MASKED)
-                sacc[v] = key_abs < T ? a.scale * (sh[v] + sl[v]) + mval[v] : -INFINITY;
-            else
-                sacc[v] = key_abs <= qpos && key_abs < T ? a.scale * (sh[v] + sl[v]) : -INFINITY;
-            bm = fmaxf(bm, sacc[v]);
+            for (int v = 0; v < 16; ++v) {
+                const int key_abs = kb * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                if constexpr (MASKED)
+                    sacc[v] = key_abs < T ? a.scale * (sh[v] + sl[v]) + mval[v] : -INFINITY;
+                else
+                    sacc[v] = key_abs <= qpos && key_abs < T ? a.scale * (sh[v] + sl[v]) : -INFINITY;
+                bm = fmaxf(bm, sacc[v]);
+            }
+        } else {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                sacc[v] = a.scale * (sh[v] + sl[v]);
+                bm = fmaxf(bm, sacc[v]);
+            }
         }
         bm = fmaxf(bm, __shfl_xor(bm, 32));
         const float mn = fmaxf(m, bm);
@@ -418,10 +448,10 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(const float* __res
                 o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[mm], vbv, o[db], 0, 0, 0);
                 o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pl[mm], vbv, o[db], 0, 0, 0);
             }
-        if (kb + W < nkb) {
+        if (kb + W < bkend) {
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) ka[ks] = kn[ks];
-            if constexpr (MASKED)
+            if (mxn)
 #pragma unroll
                 for (int e = 0; e < 8; ++e) mk[e] = mkn[e];
         }
@@ -478,6 +508,96 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(const float* __res
 
 }  // namespace
 
+// ggml's f16 mask summarised per tile of 32 query rows (rows from N on read row N - 1) for the
+// masked attention kernels: {lo, hi, mlo, mhi} = the first and last 32-key block holding a value
+// other than -inf (keys below T; lo > hi when there is none), and the first and last block of lo ..
+// hi holding a value other than +-0 (-inf included; mlo > mhi when there is none), so that blocks of
+// lo .. hi outside mlo .. mhi hold 0 for every query of the tile: adding their values changes no
+// score. A causal mask gives lo = 0 and mlo = mhi = hi, the diagonal block. One workgroup of 16
+// wavefronts per tile, a wavefront per key block at a time: lane l reads row l / 2, keys 16 (l % 2) ..
+// + 15, in 4-byte pairs inside the row (rows of m_row2 >= T halves, 4-byte aligned). Past
+// kMaskBlocks blocks the flags do not fit in LDS and mlo .. mhi = lo .. hi (every block with values).
+constexpr int kMaskBlocks = 8192;
+constexpr int kMaskWaves = 16;
+
+__global__ __launch_bounds__(64 * kMaskWaves) void mask_summary_kernel(const unsigned short* __restrict__ mask,
+                                                                       int m_row2, int N, int T,
+                                                                       int* __restrict__ sum) {
+    __shared__ uint8_t nz[kMaskBlocks];  // per block: a value other than +-0
+    __shared__ int red[2 * kMaskWaves];
+    const int tile = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nkb = (T + 31) / 32;
+    const unsigned short* mr = mask + (size_t)min(tile * 32 + lane / 2, N - 1) * m_row2;
+    int lo = INT_MAX, hi = -1;
+    for (int b = wave; b < nkb; b += kMaskWaves) {
+        bool live = false, nonzero = false;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int k = b * 32 + 16 * (lane & 1) + 2 * e;  // keys k, k + 1
+            if (k >= T) break;
+            const int k0 = min(k, m_row2 - 2);  // (T = m_row2 odd: the row's last pair, key k at its end)
+            const uint32_t w = *reinterpret_cast<const uint32_t*>(mr + k0);
+#pragma unroll
+            for (int x = 0; x < 2; ++x) {
+                const int key = k0 + x;
+                const uint32_t hv = x ? w >> 16 : w & 0xFFFFu;
+                if (key >= k && key < T) {
+                    live |= hv != 0xFC00u;
+                    nonzero |= (hv & 0x7FFFu) != 0;
+                }
+            }
+        }
+        const bool bl = __ballot(live) != 0, bn = __ballot(nonzero) != 0;
+        if (bl) {
+            lo = min(lo, b);
+            hi = max(hi, b);
+        }
+        if (lane == 0 && b < kMaskBlocks) nz[b] = bn ? 1 : 0;
+    }
+    if (lane == 0) {
+        red[2 * wave] = lo;
+        red[2 * wave + 1] = hi;
+    }
+    __syncthreads();
+    for (int w = 0; w < kMaskWaves; ++w) {
+        lo = min(lo, red[2 * w]);
+        hi = max(hi, red[2 * w + 1]);
+    }
+    int ml = INT_MAX, mh = -1;
+    if (nkb > kMaskBlocks) {
+        ml = lo;
+        mh = hi;
+    } else {
+        for (int b = max(lo, 0) + (int)threadIdx.x; b <= hi; b += 64 * kMaskWaves)
+            if (nz[b]) {
+                ml = min(ml, b);
+                mh = max(mh, b);
+            }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        ml = min(ml, __shfl_xor(ml, o));
+        mh = max(mh, __shfl_xor(mh, o));
+    }
+    __syncthreads();  // red read by every thread
+    if (lane == 0) {
+        red[2 * wave] = ml;
+        red[2 * wave + 1] = mh;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 0; w < kMaskWaves; ++w) {
+            ml = min(ml, red[2 * w]);
+            mh = max(mh, red[2 * w + 1]);
+        }
+        int* o = sum + 4 * tile;
+        o[0] = lo;
+        o[1] = hi;
+        o[2] = ml;
+        o[3] = mh;
+    }
+}
+
 int launchGetRows(bool q6k, const void* qw, const int* tok, float* y, int n, int k, int rows, hipStream_t s) {
     const long long threads = (long long)n * (k / 16);
     if (threads == 0) return 0;
@@ -499,7 +619,7 @@ static bool useGqa(const AttnShape& a) {
 template <int D>
 static int runPrefill(const float* q, const int* k, const int* v, float* out, const int* n_ctx, const AttnShape& a,
                        hipStream_t s) {
-    if (useGqa(a)) return launchAttnGqa(q, k, v, out, n_ctx, a, nullptr, 0, 0, a.max_t, s);
+    if (useGqa(a)) return launchAttnGqa(q, k, v, out, n_ctx, a, nullptr, 0, 0, a.max_t, nullptr, s);
     const dim3 grid((a.N + 31) / 32, a.H);
     // key blocks split over 2 wavefronts for D = 128 (registers: one wavefront per SIMD), over 4
     // for D = 64 (two per SIMD)
@@ -513,18 +633,27 @@ static int runPrefill(const float* q, const int* k, const int* v, float* out, co
 bool attnMaskedSupports(const AttnShape& a) { return a.D == 64 || a.D == 128; }
 
 int launchAttnMasked(const float* q, const int* k, const int* v, const unsigned short* mask, int m_row2, int T,
-                     float* out, const AttnShape& a, hipStream_t s) {
-    if (!attnMaskedSupports(a) || m_row2 < 2 || m_row2 % 2 || T <= 0 || a.N <= 0)
+                     float* out, const AttnShape& a, const int* msum, hipStream_t s) {
+    if (!attnMaskedSupports(a) || m_row2 < 2 || m_row2 % 2 || T <= 0 || T > m_row2 || a.N <= 0 || !msum)
         return fromHip(hipErrorInvalidValue, "attn (masked): shape");
-    if (useGqa(a)) return launchAttnGqa(q, k, v, out, nullptr, a, mask, m_row2, T, T, s);
+    if (useGqa(a)) return launchAttnGqa(q, k, v, out, nullptr, a, mask, m_row2, T, T, msum, s);
     const dim3 grid((a.N + 31) / 32, a.H);
     if (a.D == 128)
         hipLaunchKernelGGL((attn_prefill_kernel<128, 2, true>), grid, dim3(128), 0, s, q, k, v, out, nullptr, a, mask,
-                           m_row2, T);
+                           m_row2, T, msum);
     else
         hipLaunchKernelGGL((attn_prefill_kernel<64, 4, true>), grid, dim3(256), 0, s, q, k, v, out, nullptr, a, mask,
-                           m_row2, T);
+                           m_row2, T, msum);
     return fromHip(hipGetLastError(), "attn (masked)");
+}
+
+int maskSummaryInts(int N) { return 4 * ((N + 31) / 32); }
+
+int launchMaskSummary(const unsigned short* mask, int m_row2, int N, int T, int* sum, hipStream_t s) {
+    if (m_row2 < 2 || m_row2 % 2 || T <= 0 || T > m_row2 || N <= 0 || !mask || !sum)
+        return fromHip(hipErrorInvalidValue, "mask summary: shape");
+    hipLaunchKernelGGL(mask_summary_kernel, dim3((N + 31) / 32), dim3(64 * kMaskWaves), 0, s, mask, m_row2, N, T, sum);
+    return fromHip(hipGetLastError(), "mask summary");
 }
 
 int launchAttn(const float* q, const int* k, const int* v, float* out, const int* n_ctx, const AttnShape& a,

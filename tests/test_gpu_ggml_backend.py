@@ -338,8 +338,6 @@ def test_batch_attention_with_an_irregular_mask(shape, attn_path):
 def _irregular_mask_case(shape):
     N, p0 = 40, 150
     L = Layer(shape, N, p0, seed=919)
-    names, _ = kc.ggml_graph_plan(L.g.nodes, attn_tokens=N)
-    assert "attn_masked" in names
     rng = np.random.default_rng(5)
     n_pad = L.t["mask"].ne[0]
     m = np.where(rng.random((N, n_pad)) < 0.3, -np.inf, 0.0).astype(np.float16)
@@ -349,9 +347,18 @@ def _irregular_mask_case(shape):
     m[3, 5] = 0.0
     m[:4, p0 + N - 1] = 0.0  # the last key, ahead of these queries' positions
     m[7, 130:140] = np.float16(-2.5)  # finite penalties, not only 0 / -inf
+    _masked_case(L, N, m)
+
+
+def _masked_case(L, N, m):
+    """L's layer with mask m through the backend (the masked matrix-core attention), against the
+    oracle on the GPU's own inputs."""
+    names, _ = kc.ggml_graph_plan(L.g.nodes, attn_tokens=N)
+    assert "attn_masked" in names
     L.mask = m.reshape(-1).view(np.uint16)
     L.put("mask", L.mask)
-    # cache rows past the view (the last key block reaches rows 190, 191) hold Inf: keys past T must
+    n_pad = L.t["mask"].ne[0]
+    # cache rows past the view (the last key block may reach past n_kv) hold Inf: keys past T must
     # not reach the products (p = 0 times Inf is NaN)
     for c in ("k_cache", "v_cache"):
         cache = L.get(c, np.uint16).reshape(L.s.kv_size, L.s.kv_dim)
@@ -370,6 +377,31 @@ def _irregular_mask_case(shape):
     assert kq.rel_diff(L.get("attn", np.float32), want) < 2e-6
     be.close()
     L.free()
+
+
+@pytest.mark.parametrize("attn_path", [2, 3], ids=["one-head", "gqa"])
+@pytest.mark.parametrize("p0", [64, 62], ids=["rows16B", "rows4B"])
+def test_batch_attention_with_a_window_mask(p0, attn_path):
+    """A sliding-window mask (each query sees its last 70 positions) over 192 queries: the later
+    query tiles see none of the first key blocks, which the kernels then do not load; one query of a
+    later tile also sees key 3 (its tile keeps every block from 0 on), and one row holds a finite
+    penalty. Mask rows of 256 halves (16-byte loads in the kernels' scan of the mask) and of 254
+    (4-byte loads); both kernels; against the oracle on the GPU's own inputs."""
+    shape = gg.LayerShape(n_embd=1024, neox=True, kv_size=256)
+    N = 192
+    kc.set_option("attn_path", attn_path)
+    try:
+        L = Layer(shape, N, p0, seed=931)
+        n_pad = L.t["mask"].ne[0]
+        assert n_pad == p0 + N and (n_pad % 8 == 0) == (p0 == 64)
+        key = np.arange(n_pad)[None, :]
+        pos = p0 + np.arange(N)[:, None]
+        m = np.where((key <= pos) & (key > pos - 70), 0.0, -np.inf).astype(np.float16)
+        m[150, 3] = 0.0
+        m[120, pos[120, 0] - 10] = np.float16(-1.5)
+        _masked_case(L, N, m)
+    finally:
+        kc.set_option("attn_path", 0)
 
 
 def test_batch_attention_past_the_score_limit():
