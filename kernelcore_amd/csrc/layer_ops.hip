@@ -426,6 +426,51 @@ __global__ __launch_bounds__(64) void rms_norm_row_kernel(const float* __restric
     for (int j = lane; j < n; j += 64) yr[j] = xs[j] * r * w[j];
 }
 
+// The same for short rows (n = 4, 8, .. 128: float4s per row dividing 64; rows 16-byte aligned)
+// with one lane per row: a workgroup's 64 rows (contiguous in memory) come into LDS by coalesced
+// 16-byte loads (rows padded by 4 floats, so the lanes' row reads hit different banks), each lane
+// takes its row's sum of squares in element order (the same additions as the kernels above, so the
+// same bits), and the outputs y = x r w leave by coalesced stores (in place is safe: every load
+// precedes every store). A Qwen3 prompt's per-head q / k norms are 32768 + 8192 rows of 128 per
+// layer at 1024 tokens: a workgroup per row left one lane per 64 working through the row's serial
+// sum.
+constexpr int kNormLaneMax = 128;
+__global__ __launch_bounds__(64) void rms_norm_lane_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                           float* __restrict__ y, int n, int rows, float eps) {
+    __shared__ float4 xs[64 * (kNormLaneMax / 4 + 1)];
+    __shared__ float rr[64];
+    const int lane = threadIdx.x, row0 = blockIdx.x * 64;
+    const int q = n / 4, stride = q + 1, rstep = 64 / q;  // float4s per row in memory and in LDS
+    const int nq = min(64, rows - row0) * q;
+    const int r0 = lane / q, c0 = lane - r0 * q;  // this lane's loads: rows r0 + i rstep, float4 c0
+    const float4* xb = reinterpret_cast<const float4*>(x + (size_t)row0 * n);
+#pragma unroll 8
+    for (int i = 0; lane + 64 * i < nq; ++i) xs[(r0 + i * rstep) * stride + c0] = xb[lane + 64 * i];
+    __syncthreads();
+    if (row0 + lane < rows) {
+        const float4* xr = xs + lane * stride;
+        float ss = 0.0f;
+        for (int i = 0; i < q; ++i) {
+            const float4 u = xr[i];
+            ss += u.x * u.x;
+            ss += u.y * u.y;
+            ss += u.z * u.z;
+            ss += u.w * u.w;
+        }
+        rr[lane] = 1.0f / sqrtf(ss / (float)n + eps);
+    }
+    __syncthreads();
+    float4* yb = reinterpret_cast<float4*>(y + (size_t)row0 * n);
+    const float4 wv = reinterpret_cast<const float4*>(w)[c0];
+#pragma unroll 8
+    for (int i = 0; lane + 64 * i < nq; ++i) {
+        const int r = r0 + i * rstep;
+        const float4 u = xs[r * stride + c0];
+        const float rv = rr[r];
+        yb[lane + 64 * i] = make_float4(u.x * rv * wv.x, u.y * rv * wv.y, u.z * rv * wv.z, u.w * rv * wv.w);
+    }
+}
+
 // ggml ROPE (rope_ggml.cu): one thread per (token, head, pair); each thread takes the pair's
 // angle itself (the reference's per-(token, pair) value, recomputed per head).
 __global__ void rope_kernel(const float* __restrict__ x, float* __restrict__ y, const int* __restrict__ pos,
@@ -875,7 +920,12 @@ int launchSiluMul(const kcSiluMulArgs& a, hipStream_t s) {
 
 int launchRmsNorm(const kcRmsNormArgs& a, hipStream_t s) {
     if (a.rows == 0) return 0;
-    if (a.n > 0 && a.n <= 16384)
+    const bool a16 = (reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.y) |
+                      reinterpret_cast<uintptr_t>(a.w)) % 16 == 0;
+    if (a.n > 0 && a.n <= kNormLaneMax && a.n % 4 == 0 && 64 % (a.n / 4) == 0 && a16)
+        hipLaunchKernelGGL(rms_norm_lane_kernel, dim3((unsigned)((a.rows + 63) / 64)), dim3(64), 0, s, a.x, a.w, a.y,
+                           a.n, a.rows, a.eps);
+    else if (a.n > 0 && a.n <= 16384)
         hipLaunchKernelGGL(rms_norm_row_kernel, dim3(a.rows), dim3(64), (size_t)a.n * 4, s, a.x, a.w, a.y, a.n, a.eps);
     else
         hipLaunchKernelGGL(rms_norm_kernel, dim3(blocksFor(a.rows)), dim3(256), 0, s, a.x, a.w, a.y, a.n, a.rows,

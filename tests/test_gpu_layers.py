@@ -173,10 +173,12 @@ def test_silu_mul_q8(per256):
     B.free()
 
 
-@pytest.mark.parametrize("n,rows", [(128, 40), (100, 3), (4096, 2), (20000, 2)])
+@pytest.mark.parametrize("n,rows", [(128, 40), (128, 4133), (64, 70), (8, 3), (100, 3), (130, 5), (4096, 2),
+                                    (20000, 2)])
 def test_rms_norm_rows_bit_exact(n, rows):
-    """rms_norm with one workgroup per row (rows up to 16384 values: a Qwen3 layer's per-head q / k norms),
-    past that one thread per row: both the reference's sequential sums, bit for bit; also in place."""
+    """rms_norm with one lane per row (rows of up to 128 values, a multiple of 4: a Qwen3 layer's per-head
+    q / k norms; 4133 rows end inside a workgroup), one workgroup per row (up to 16384 values), past that
+    one thread per row: all the reference's sequential sums, bit for bit; also in place."""
     note(f"rms_norm n={n} rows={rows}")
     x, w = kq.randn(n * rows, 60 + rows), kq.uniform(n, 61, 0.5, 1.5)
     B = Bufs()
