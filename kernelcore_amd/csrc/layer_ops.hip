@@ -30,9 +30,24 @@ __device__ __forceinline__ int q8r(float t) {
     return q > 127 ? 127 : (q < -127 ? -127 : q);
 }
 
+// (ss in LDS, 16-byte aligned: the sums in block order, sixteen read ahead of their adds)
 __device__ __forceinline__ float rmsScale(const float* ss, int nb, int n, float eps) {
     float tot = 0.0f;
-    for (int j = 0; j < nb; ++j) tot += ss[j];
+    const float4* s4 = reinterpret_cast<const float4*>(ss);
+    int j = 0;
+    for (; j + 16 <= nb; j += 16) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = s4[j / 4 + u];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            tot += v[u].x;
+            tot += v[u].y;
+            tot += v[u].z;
+            tot += v[u].w;
+        }
+    }
+    for (; j < nb; ++j) tot += ss[j];
     return 1.0f / sqrtf(tot / (float)n + eps);
 }
 
