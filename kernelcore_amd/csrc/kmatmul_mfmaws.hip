@@ -319,12 +319,14 @@ __device__ __forceinline__ void wsTile(char* lbase, const uint8_t* __restrict__ 
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             // sc q / 16 (the activations are 16 x): (1024 + q) sc / 16 - 64 sc for a low nibble,
-            // (1024 + 16 q) sc / 256 - 4 sc for a high one; exact (sc / 256 >= 2^-8, q sc <= 945)
-            const _Float16 sc = (_Float16)(float)((scw[j >> 2] >> (8 * (j & 3))) & 255);
-            const _Float16 mul = (j & 1) ? sc * (_Float16)0.00390625f : sc * (_Float16)0.0625f;
-            const _Float16 sub = (j & 1) ? sc * (_Float16)(-4.0f) : sc * (_Float16)(-64.0f);
-            m2[j] = h2{mul, mul};
-            c2[j] = h2{sub, sub};
+            // (1024 + 16 q) sc / 256 - 4 sc for a high one; exact (sc / 256 >= 2^-8, q sc <= 945).
+            // sc splat as {1024 + sc, 1024 + sc} by a byte permute, then m = (1024 + sc) f - 1024 f
+            // = sc f in one fused op (both products exact) and c = -1024 m (-64 sc, -4 sc)
+            const int b = j & 3;
+            const h2 t = bits_h2(__builtin_amdgcn_perm(0x64646464u, (uint32_t)scw[j >> 2], 0x04000400u | (b << 16) | b));
+            const _Float16 f = (j & 1) ? (_Float16)0.00390625f : (_Float16)0.0625f;
+            m2[j] = __builtin_elementwise_fma(t, h2{f, f}, h2{(_Float16)-1024.0f * f, (_Float16)-1024.0f * f});
+            c2[j] = m2[j] * h2{(_Float16)-1024.0f, (_Float16)-1024.0f};
         }
         // K-step t covers, in lane half h, k = 64 (t >> 2) + 32 ((t >> 1) & 1) + 16 h + 8 (t & 1):
         // qs bytes 32 (t >> 2) + 16 h + 8 (t & 1) (chunk t >> 2, nibble (t >> 1) & 1), activation
@@ -358,9 +360,15 @@ __device__ __forceinline__ void wsTile(char* lbase, const uint8_t* __restrict__ 
             }
         }
         // the min term (one matrix op per block against [64 (B >> 6) | B & 63]) and the combine
-        h8 bm;
+        h8 bm;  // the eight min bytes as fp16: {1024 + m, 1024 + m'} by byte permutes, less 1024
 #pragma unroll
-        for (int e = 0; e < 8; ++e) bm[e] = (_Float16)(float)((mw[e >> 2] >> (8 * (e & 3))) & 255);
+        for (int e2 = 0; e2 < 4; ++e2) {
+            const uint32_t w = (uint32_t)mw[e2 >> 1];
+            const h2 t = bits_h2(__builtin_amdgcn_perm(0x64646464u, w, (e2 & 1) ? 0x04030402u : 0x04010400u)) -
+                         h2{(_Float16)1024.0f, (_Float16)1024.0f};
+            bm[2 * e2] = t[0];
+            bm[2 * e2 + 1] = t[1];
+        }
         const _Float16* xm = reinterpret_cast<const _Float16*>(buf + kMinOff);
         const char* xdl = buf + kXdOff;
 #pragma unroll
