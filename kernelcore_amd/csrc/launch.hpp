@@ -99,6 +99,13 @@ int launchSiluMulQ8KAct(const kcSiluMulQ8FArgs& a, const ActF16* ao, hipStream_t
 int launchRopeQKStore(const float* q, float* qr, const float* k, const float* v, int* kcache, int* vcache,
                       const int* pos, const float* ff, int head_dim, int nh, int nkv, int n, float log2_base, int neox,
                       int dst_row, int dst_rows, hipStream_t s, const float* v2 = nullptr);
+// The same with the per-head q / k norms first (x r w with the weights qw / kw, eps): RMS_NORM +
+// MUL of each head row of q and of k in the same launch (head_dim 64 or 128, q and k 16-byte
+// aligned), the same floats as launchRmsNorm before launchRopeQKStore.
+int launchNormRopeQKStore(const float* q, float* qr, const float* k, const float* v, const float* qw, const float* kw,
+                          int* kcache, int* vcache, const int* pos, const float* ff, int head_dim, int nh, int nkv,
+                          int n, float log2_base, int neox, int dst_row, int dst_rows, float eps, hipStream_t s,
+                          const float* v2 = nullptr);
 int launchSiluMulQ8(bool per256, const kcSiluMulQ8FArgs& a, hipStream_t s);
 int launchMulRows(const kcMulRowsArgs& a, hipStream_t s);
 int launchSiluMul(const kcSiluMulArgs& a, hipStream_t s);

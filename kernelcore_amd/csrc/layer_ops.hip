@@ -567,6 +567,91 @@ __global__ void rope_qk_store_kernel(const float* __restrict__ q, float* __restr
     }
 }
 
+// The same for a model with per-head q / k norms (Qwen3), the norms included: RMS_NORM(q) * q_norm
+// and RMS_NORM(k) * k_norm per head row of hd = 2 pairs values, then the RoPE and stores above, in
+// one launch instead of three. A workgroup of 256 threads takes 64 consecutive head rows (q rows
+// [n][nh] in workgroups 0 .. nq_blocks - 1, then the k rows [n][nkv] with their v rows): the rows
+// come into LDS by coalesced 16-byte loads (padded by 4 floats), the first wavefront's lanes sum a
+// row's squares each in element order and take r (rms_norm_lane_kernel's arithmetic), theta, its
+// cosine and sine are taken once per (token, pair) of the workgroup's tokens into LDS
+// (rope_qk_store_kernel's arithmetic), and every thread rotates pairs of the normed values x r w:
+// thread t always pair t % pairs, of rows 256 / pairs apart. The same floats as the three launches,
+// bit for bit. hd 64 or 128 (lp = log2(pairs)), ff (the frequency factors) hd / 2 values.
+constexpr int kNormRopeThreads = 256;
+__global__ __launch_bounds__(kNormRopeThreads) void norm_rope_qk_store_kernel(
+    const float* __restrict__ q, float* __restrict__ qr, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ v2, const float* __restrict__ qw, const float* __restrict__ kw,
+    unsigned short* __restrict__ kc, unsigned short* __restrict__ vc, const int* __restrict__ pos,
+    const float* __restrict__ ff, int lp, int nh, int nkv, int n, float log2_base, int m1, int m2, int dst_row,
+    int dst_rows, float eps, int nq_blocks) {
+    extern __shared__ float4 nr_lds[];
+    const int pairs = 1 << lp, hd = 2 * pairs, lq4 = lp - 1, q4 = hd / 4, stride = q4 + 1;
+    float4* xs = nr_lds;                                       // 64 rows, padded
+    float* rr = reinterpret_cast<float*>(xs + 64 * stride);    // per row: the norm's scale
+    int* tl = reinterpret_cast<int*>(rr + 64);                 // per row: its token - t0
+    long long* dst = reinterpret_cast<long long*>(tl + 64);    // per row: q row / cache offset, -1: no store
+    float2* cs = reinterpret_cast<float2*>(dst + 64);          // [token - t0][pairs] (cos, sin)
+    const int tid = threadIdx.x;
+    const bool isq = (int)blockIdx.x < nq_blocks;
+    const int nhd = isq ? nh : nkv, rows = n * nhd;
+    const int row0 = (isq ? (int)blockIdx.x : (int)blockIdx.x - nq_blocks) * 64;
+    const int nr = min(64, rows - row0), nqw = nr * q4;
+    const float4* xb = reinterpret_cast<const float4*>((isq ? q : k) + (size_t)row0 * hd);
+#pragma unroll 4
+    for (int jj = tid; jj < nqw; jj += kNormRopeThreads) xs[(jj >> lq4) * stride + (jj & (q4 - 1))] = xb[jj];
+    // theta per (token, pair) of this workgroup's tokens t0 .. t0 + ntok - 1
+    const int t0 = row0 / nhd, ntok = (row0 + nr - 1) / nhd - t0 + 1;
+    for (int u = tid; u < ntok * pairs; u += kNormRopeThreads) {
+        const int tt = u >> lp, i = u & (pairs - 1);
+        const float theta = (float)pos[t0 + tt] * exp2f(-(float)i / (float)pairs * log2_base) / ff[i];
+        cs[u] = make_float2(cosf(theta), sinf(theta));
+    }
+    __syncthreads();
+    if (tid < nr) {
+        const float4* xr = xs + tid * stride;
+        float ss = 0.0f;
+        for (int i = 0; i < q4; ++i) {
+            const float4 x4 = xr[i];
+            ss += x4.x * x4.x;
+            ss += x4.y * x4.y;
+            ss += x4.z * x4.z;
+            ss += x4.w * x4.w;
+        }
+        rr[tid] = 1.0f / sqrtf(ss / (float)hd + eps);
+        const int row = row0 + tid, t = row / nhd, hh = row - t * nhd;
+        tl[tid] = t - t0;
+        if (isq) {
+            dst[tid] = (long long)row * hd;
+        } else {
+            const int p = pos[t];
+            dst[tid] = p >= 0 && p < dst_rows ? (long long)p * dst_row * 2 + (long long)hh * hd : -1;
+        }
+    }
+    __syncthreads();
+    const float* xf = reinterpret_cast<const float*>(xs);
+    const int i = tid & (pairs - 1), a = i * m1;  // this thread's pair: values a, a + m2 of a head row
+    const float* w = isq ? qw : kw;
+    const float wa = w[a], wb = w[a + m2];
+    for (int r = tid >> lp; r < nr; r += kNormRopeThreads >> lp) {
+        const float rv = rr[r];
+        const float x0 = xf[r * 4 * stride + a] * rv * wa, x1 = xf[r * 4 * stride + a + m2] * rv * wb;
+        const float2 csv = cs[(tl[r] << lp) + i];
+        const float y0 = x0 * csv.x - x1 * csv.y, y1 = x0 * csv.y + x1 * csv.x;
+        const long long d = dst[r];
+        if (isq) {
+            qr[d + a] = y0;
+            qr[d + a + m2] = y1;
+        } else if (d >= 0) {
+            const size_t e = (size_t)d + a, av = (size_t)(row0 + r) * hd + a;
+            kc[e] = (unsigned short)f2h(y0);
+            kc[e + m2] = (unsigned short)f2h(y1);
+            const float v0 = v2 ? v[av] + v2[av] : v[av], v1 = v2 ? v[av + m2] + v2[av + m2] : v[av + m2];
+            vc[e] = (unsigned short)f2h(v0);
+            vc[e + m2] = (unsigned short)f2h(v1);
+        }
+    }
+}
+
 // The ggml graph's ROPE(q), ROPE(k), SET_ROWS(k cache, roped k, idx) and SET_ROWS(v cache, v, idx)
 // in one launch (rope_ggml.cu, set_rows_f16.cu): one thread per (token, group of 4 heads, pair) as
 // rope_qk_store_kernel, which also keeps the roped k in kr and takes the cache rows from idx (int64,
@@ -956,6 +1041,25 @@ int launchRope(const kcRopeGgmlArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(rope_kernel, dim3(blocksFor(count)), dim3(256), 0, s, a.x, a.y, a.pos, a.ff, pairs, a.n_head,
                        (int)count, a.log2_base, a.neox ? 1 : 2, a.neox ? pairs : 1);
     return fromHip(hipGetLastError(), "rope_ggml");
+}
+
+int launchNormRopeQKStore(const float* q, float* qr, const float* k, const float* v, const float* qw, const float* kw,
+                          int* kcache, int* vcache, const int* pos, const float* ff, int head_dim, int nh, int nkv,
+                          int n, float log2_base, int neox, int dst_row, int dst_rows, float eps, hipStream_t s,
+                          const float* v2) {
+    const int pairs = head_dim / 2;
+    if (n <= 0) return 0;
+    if ((head_dim != 64 && head_dim != 128) || nh <= 0 || nkv <= 0 || !al16(q) || !al16(k))
+        return fromHip(hipErrorInvalidValue, "q / k norm + rope + kv store: shape");
+    const long long nqb = ((long long)n * nh + 63) / 64, nkb = ((long long)n * nkv + 63) / 64;
+    if (nqb + nkb > INT32_MAX) return fromHip(hipErrorInvalidValue, "q / k norm + rope + kv store: rows");
+    const int max_tok = 64 / std::min(nh, nkv) + 2;  // tokens one workgroup's 64 rows can span
+    const size_t lds = sizeof(float) * (64 * (head_dim + 4) + 64 + 64 + 128) + sizeof(float) * 2 * (size_t)max_tok * pairs;
+    hipLaunchKernelGGL(norm_rope_qk_store_kernel, dim3((unsigned)(nqb + nkb)), dim3(kNormRopeThreads), lds, s, q, qr, k,
+                       v, v2, qw, kw, reinterpret_cast<unsigned short*>(kcache), reinterpret_cast<unsigned short*>(vcache),
+                       pos, ff, pairs == 64 ? 6 : 5, nh, nkv, n, log2_base, neox ? 1 : 2, neox ? pairs : 1, dst_row,
+                       dst_rows, eps, (int)nqb);
+    return fromHip(hipGetLastError(), "q / k norm + rope + kv store");
 }
 
 int launchRopeQKStore(const float* q, float* qr, const float* k, const float* v, int* kcache, int* vcache,

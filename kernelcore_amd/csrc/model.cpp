@@ -413,12 +413,21 @@ int batchStep(kcModel_st* m, int n, hipStream_t s) {
         std::array<bool, 3> split{};  // (v may run in two K ranges: stored as v + v2)
         KI_TRY(batchProj(l, {KC_TENSOR_WQ, KC_TENSOR_WK, KC_TENSOR_WV}, {l.wq, l.wk, l.wv}, {m->q, m->k, m->v},
                          {Q, KV, KV}, 3, m->slotEK, m->xn, E_, n, s, aE, {nullptr, nullptr, m->v2}, &split));
-        KI_TRY(qkNorm(m, l, n, s));
-        // RoPE of q and k with the fp16 cache stores of k and v in one kernel
-        KI_TRY(kcamd::launchRopeQKStore(c.qk_norm ? m->att : m->q, m->qr, c.qk_norm ? m->kr : m->k, m->v, l.kcache,
-                                        l.vcache, m->pos, m->ones, c.head_dim, c.n_head, c.n_head_kv, n,
-                                        std::log2(c.rope_theta), c.rope_neox, KV / 2, c.max_ctx, s,
-                                        split[2] ? m->v2 : nullptr));
+        // RoPE of q and k with the fp16 cache stores of k and v in one kernel, Qwen3's per-head q / k
+        // norms in the same launch (option qk_fuse = 1: the norms as launches of their own)
+        const bool fuse = c.qk_norm && kcamd::option("qk_fuse") != 1 && (c.head_dim == 64 || c.head_dim == 128);
+        if (fuse) {
+            KI_TRY(kcamd::launchNormRopeQKStore(m->q, m->qr, m->k, m->v, l.q_norm, l.k_norm, l.kcache, l.vcache, m->pos,
+                                                m->ones, c.head_dim, c.n_head, c.n_head_kv, n, std::log2(c.rope_theta),
+                                                c.rope_neox, KV / 2, c.max_ctx, c.norm_eps, s,
+                                                split[2] ? m->v2 : nullptr));
+        } else {
+            KI_TRY(qkNorm(m, l, n, s));
+            KI_TRY(kcamd::launchRopeQKStore(c.qk_norm ? m->att : m->q, m->qr, c.qk_norm ? m->kr : m->k, m->v, l.kcache,
+                                            l.vcache, m->pos, m->ones, c.head_dim, c.n_head, c.n_head_kv, n,
+                                            std::log2(c.rope_theta), c.rope_neox, KV / 2, c.max_ctx, s,
+                                            split[2] ? m->v2 : nullptr));
+        }
         KI_TRY(attention(m, l, n, s));
         const float* o2 = nullptr;
         if (l.f16[KC_TENSOR_WO]) {

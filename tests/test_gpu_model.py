@@ -150,6 +150,36 @@ def test_model_prompt_attention_kernels_agree(name, cfg, n_prompt, n_chunk):
         assert rel_l2(got[3][i], got[2][i]) < 1e-6  # (the same products and sums: equal in practice)
 
 
+@pytest.mark.parametrize("head_dim,n_head,n_head_kv", [(128, 4, 2), (64, 8, 1), (128, 2, 2)])
+def test_qwen3_prompt_norms_fused_bit_identical(head_dim, n_head, n_head_kv):
+    """A Qwen3 prompt's per-head q / k norms inside the RoPE + cache-store launch (the default)
+    against the three launches (option qk_fuse = 1): the same logits and the same cache bits, for a
+    prompt and a continuing chunk (70 tokens: the last workgroups hold part of 64 head rows; one KV
+    head: a workgroup's 64 k rows span 64 tokens)."""
+    cfg = dict(QWEN, head_dim=head_dim, n_head=n_head, n_head_kv=n_head_kv)
+    w = random_weights(cfg, 17)
+    prompt = np.random.default_rng(4).integers(0, cfg["n_vocab"], 70 + 33).astype(np.int32)
+    got = {}
+    for fuse in (1, 0):
+        kc.set_option("qk_fuse", fuse)
+        try:
+            m = kc.Model(**cfg)
+            for (tid, layer), data in w.items():
+                m.set_tensor(tid, layer, data)
+            lg = [m.forward(prompt[:70]), m.forward(prompt[70:])]
+            caches = [m.read_cache(li, which, 0, len(prompt)) for li in range(cfg["n_layer"]) for which in (0, 1)]
+            got[fuse] = (lg, caches)
+            m.close()
+        finally:
+            kc.set_option("qk_fuse", 0)
+    for a, b in zip(got[0][0], got[1][0]):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    for a, b in zip(got[0][1], got[1][1]):
+        assert np.array_equal(a, b)
+    lo = OracleModel(cfg, w).forward(prompt[:70])
+    assert rel_l2(got[0][0][0], lo) < 1e-2
+
+
 def test_model_3b_shape_two_layers():
     """Two layers at the full Llama-3.2-3B widths (3072 / 24 heads / 8 KV heads / 8192 FFN / 128256
     vocab): an 8-token prompt and two decode steps against the oracle."""
