@@ -57,8 +57,12 @@ template <int D>
 struct AttnGeo {
     static constexpr int kCpr = D / 8;                  // 16-byte chunks per K / V row
     static constexpr int kKRow = 2 * D + 16;            // LDS bytes per K row (one pad chunk)
+    // LDS bytes per V row (two pad chunks: 8 dwords mod 32 banks, so the four rows of a transposed
+    // read's 16 lanes fall on different banks; K's one pad chunk keeps its 16-byte row reads apart)
+    static constexpr int kVRow = 2 * D + 32;
     static constexpr int kKLoads = (32 * (kCpr + 1) + 63) / 64;  // 1 KiB direct loads per K or V block
     static constexpr int kKBytes = kKLoads * 1024;
+    static_assert(32 * (kCpr + 2) <= kKLoads * 64, "V rows with two pad chunks in K's load count");
     static constexpr int kMRow = 20;                    // mask tile: dwords per row (16 + 4 pad)
     static constexpr int kMLoads = 32 * kMRow / 64;     // 256-byte direct loads of the mask tile
     static constexpr int kBuf = 2 * kKBytes + kMLoads * 256;  // one block of one split: K, V, mask
@@ -126,8 +130,8 @@ __global__ __launch_bounds__(512) void attn_prefill_gqa_kernel(const float* __re
     }
 
     // K and V rows by direct loads: slot L 64 + lane of a block's kKLoads loads holds key slot /
-    // (kCpr + 1), chunk slot % (kCpr + 1) (the pad chunk and slots past 32 keys reread chunk 0 / key
-    // 31). Keys from T on read row T - 1: cache rows past the context are not written yet and may
+    // cpr, chunk slot % cpr, cpr = kCpr + 1 for K and kCpr + 2 for V (pad chunks and slots past 32
+    // keys reread chunk 0 / key 31). Keys from T on read row T - 1: cache rows past the context are not written yet and may
     // hold any bits, and an Inf there times p = 0 would still make NaN (their scores are replaced
     // by -inf anyway). MASKED: the tile's 32 mask rows (queries past N read row N - 1), 32 keys each,
     // in dword loads (mask rows need only 4-byte alignment), kMRow dwords per LDS row; keys past the
@@ -145,10 +149,10 @@ __global__ __launch_bounds__(512) void attn_prefill_gqa_kernel(const float* __re
         for (int i = 0; i < per; ++i) {
             const int L = min(gw + G * i, nl - 1);
             if (L < 2 * Geo::kKLoads) {
-                const int LL = L < Geo::kKLoads ? L : L - Geo::kKLoads;
-                const int slot = LL * 64 + lane, key = min(slot / (Geo::kCpr + 1), 31), c = slot % (Geo::kCpr + 1);
+                const int LL = L < Geo::kKLoads ? L : L - Geo::kKLoads, cpr = L < Geo::kKLoads ? Geo::kCpr + 1 : Geo::kCpr + 2;
+                const int slot = LL * 64 + lane, key = min(slot / cpr, 31), c = slot % cpr;
                 const int row = min(kb * 32 + key, T - 1);
-                const uint32_t voff = (uint32_t)row * (uint32_t)a.kv_row * 4u + (uint32_t)(c == Geo::kCpr ? 0 : c) * 16u;
+                const uint32_t voff = (uint32_t)row * (uint32_t)a.kv_row * 4u + (uint32_t)(c >= Geo::kCpr ? 0 : c) * 16u;
                 if (L < Geo::kKLoads)
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (LdsPtr)(buf + L * 1024), 16, voff, 0, 0, 0);
                 else
@@ -201,7 +205,7 @@ __global__ __launch_bounds__(512) void attn_prefill_gqa_kernel(const float* __re
     const _Float16* vcol = nullptr;
     // this lane's row for the transposed V reads: group g = lane / 16 (lane half h = g / 2, d 16 (g % 2)
     // on), lane L = lane % 16 of it: key 4 h + L / 4, d 16 (g % 2) + 4 (L % 4)
-    const int vlane = (4 * (lane >> 5) + ((lane & 15) >> 2)) * (Geo::kKRow / 2) + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    const int vlane = (4 * (lane >> 5) + ((lane & 15) >> 2)) * (Geo::kVRow / 2) + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
     int rc = 0, rn = 2;  // ring slots of block it and of block it + 2
     for (int it = 0; it < nit; ++it) {
         const int kb = kb0 + kSplits * it + sp, kbn = kb + 2 * kSplits;
@@ -292,9 +296,9 @@ __global__ __launch_bounds__(512) void attn_prefill_gqa_kernel(const float* __re
             for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
                 for (int t = 0; t < DB; ++t) {
-                    const _Float16* vp = vcol + 16 * mm * (Geo::kKRow / 2) + 32 * t;
+                    const _Float16* vp = vcol + 16 * mm * (Geo::kVRow / 2) + 32 * t;
                     const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LdsS4)vp);
-                    const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LdsS4)(vp + 8 * (Geo::kKRow / 2)));
+                    const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LdsS4)(vp + 8 * (Geo::kVRow / 2)));
                     const h8 va = __builtin_bit_cast(h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
                     o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pa[mm], o[t], 0, 0, 0);
                     o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pl[mm], o[t], 0, 0, 0);

@@ -229,9 +229,9 @@ typedef __attribute__((address_space(3))) s4* LdsS4;
 // output accumulators rescaled by exp(m_old - m_new) before each block's P V; at the end the
 // partial results are merged, o = sum_w o_w exp(m_w - M) over l = sum_w l_w exp(m_w - M). Each
 // wavefront loads the K fragments and V rows of its next block into registers while it computes
-// the current one; V goes to the wavefront's own LDS buffer row-major (rows padded by 8 halves, so
-// the two halves of the wavefront read different banks) and each lane gathers its B operand,
-// V[keys kappa(k)][d], from there. Query tiles are dispatched longest first.
+// the current one; V goes to the wavefront's own LDS buffer row-major (rows padded by 16 halves)
+// and each lane takes its B operand, V[keys kappa(k)][d], from there by transposed reads. Query
+// tiles are dispatched longest first.
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 
 // MASKED: FLASH_ATTN_EXT's form for the ggml backend -- the N queries attend over T = t_host keys
@@ -248,7 +248,8 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(const float* __res
                                                                int m_row2 = 0, int t_host = 0,
                                                                const int* __restrict__ msum = nullptr) {
     constexpr int KS = D / 16, DB = D / 32;
-    constexpr int VR = D + 8;        // halves per V row in LDS
+    constexpr int VR = D + 16;       // halves per V row in LDS (8 dwords mod 32 banks: the four rows of a
+                                     // transposed read's 16 lanes on different banks)
     constexpr int CPR = D / 8;       // 16-byte chunks per V row
     constexpr int RPL = 64 / CPR;    // V rows per wavefront load
     constexpr int VL = 32 / RPL;     // loads per V block
