@@ -409,13 +409,18 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(const float* __res
         }
         bm = fmaxf(bm, __shfl_xor(bm, 32));
         const float mn = fmaxf(m, bm);
-        const float alpha = m == -INFINITY ? 0.0f : exp2f((m - mn) * kLog2e);
+        // exp2 on the transcendental unit (v_exp_f32: exp2f's result for arguments from -126 up, 0
+        // below, where p and alpha are absorbed by the sums they join); masked scores (-inf) give 0
+        // without a branch, and so does alpha for a first block (m = -inf); a query with every score
+        // so far masked (mn = -inf) subtracts 0 instead
+        const float msafe = mn == -INFINITY ? 0.0f : mn;
+        const float alpha = __builtin_amdgcn_exp2f((m - msafe) * kLog2e);
         m = mn;
         h8 pa[2], pl[2];
         float ls = 0.0f;
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-            const float pv = sacc[v] == -INFINITY ? 0.0f : exp2f((sacc[v] - mn) * kLog2e);
+            const float pv = __builtin_amdgcn_exp2f((sacc[v] - msafe) * kLog2e);
             ls += pv;
             const float ps = pv * 1024.0f;
             const _Float16 hp = (_Float16)ps;
