@@ -253,8 +253,10 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(const float* __res
     constexpr int CPR = D / 8;       // 16-byte chunks per V row
     constexpr int RPL = 64 / CPR;    // V rows per wavefront load
     constexpr int VL = 32 / RPL;     // loads per V block
-    // the V buffers, reused by the merge for the partial outputs of wavefronts 1 ..
-    constexpr int kLdsHalves = W * 32 * VR > (W - 1) * 32 * D * 2 ? W * 32 * VR : (W - 1) * 32 * D * 2;
+    // the V buffers, reused by the merge for the partial outputs of wavefronts 1 .. (rows of D + 4
+    // floats: the lanes' 16-byte stores of different queries on different banks)
+    constexpr int OR = D + 4;
+    constexpr int kLdsHalves = W * 32 * VR > (W - 1) * 32 * OR * 2 ? W * 32 * VR : (W - 1) * 32 * OR * 2;
     __shared__ __attribute__((aligned(16))) _Float16 vsall[kLdsHalves];
     __shared__ __attribute__((aligned(16))) float qx[W][4][32];
     const int T = MASKED ? t_host : *n_ctx, N = a.N, p0 = T - N;
@@ -266,7 +268,6 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(const float* __res
     // this lane's row for the transposed V reads: group g = lane / 16 (lane half h = g / 2, d 16 (g % 2)
     // on), lane L = lane % 16 of it: key 4 h + L / 4, d 16 (g % 2) + 4 (L % 4)
     const int vlane = (4 * h + ((lane & 15) >> 2)) * VR + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-    float* qw = qx[wave][0];
     const int* kb0 = kc + (size_t)kvh * (D / 2);
     const int* vb0 = vc + (size_t)kvh * (D / 2);
     h8 qb[KS], ql[KS];
@@ -428,31 +429,26 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(const float* __res
             pl[v >> 3][v & 7] = (_Float16)(ps - (float)hp);
         }
         l = l * alpha + ls;
-        if (h == 0) qw[j] = alpha;
-        waveSync();  // V block and the alphas staged
-        // rescale: this lane's accumulators hold queries 8 (v / 4) + 4 h + v % 4
+        waveSync();  // V block staged
+        // rescale: O^T, so this lane's accumulators all hold its own query j
 #pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-            const float4 al = *reinterpret_cast<const float4*>(qw + 8 * g4 + 4 * h);
-            const float alv[4] = {al.x, al.y, al.z, al.w};
+        for (int db = 0; db < DB; ++db)
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-#pragma unroll
-                for (int db = 0; db < DB; ++db) o[db][4 * g4 + e] *= alv[e];
-        }
+            for (int v = 0; v < 16; ++v) o[db][v] *= alpha;
 #pragma unroll
         for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
-                // V[16 mm + 8 (e / 4) + 4 h + e % 4][32 db + j], e = 0..7, by two transposed reads
-                // (ds_read_b64_tr_b16: in each group of 16 lanes, lane i receives element i % 4 of the
-                // four halves lanes 4 e + i / 4 address; lane L addresses V[key + L / 4][d0 + 4 (L % 4)])
+                // O^T += V^T P^T: the A operand V^T[32 db + j][keys 16 mm + 8 (e / 4) + 4 h + e % 4],
+                // e = 0..7, by two transposed reads (ds_read_b64_tr_b16: in each group of 16 lanes,
+                // lane i receives element i % 4 of the four halves lanes 4 e + i / 4 address; lane L
+                // addresses V[key + L / 4][d0 + 4 (L % 4)]); the B operand P^T, the lane's query j
                 const _Float16* vp = vs + vlane + 16 * mm * VR + 32 * db;
                 const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LdsS4)vp);
                 const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LdsS4)(vp + 8 * VR));
                 const h8 vbv = __builtin_bit_cast(h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[mm], vbv, o[db], 0, 0, 0);
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pl[mm], vbv, o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vbv, pa[mm], o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vbv, pl[mm], o[db], 0, 0, 0);
             }
         if (kb + W < bkend) {
 #pragma unroll
@@ -469,14 +465,16 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(const float* __res
         qx[wave][1][j] = m;
         qx[wave][2][j] = l;
     }
-    float* ob = reinterpret_cast<float*>(vsall);  // [W - 1][32 queries][D]
+    // lane (j, h) holds O^T[d][j] for d = 32 db + 8 (v / 4) + 4 h + v % 4: query j's row, four
+    // consecutive d per group of four v
+    float* ob = reinterpret_cast<float*>(vsall);  // [W - 1][32 queries][OR]
     if (wave > 0) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int qi = 8 * (v >> 2) + 4 * h + (v & 3);
+        for (int db = 0; db < DB; ++db)
 #pragma unroll
-            for (int db = 0; db < DB; ++db) ob[((wave - 1) * 32 + qi) * D + 32 * db + j] = o[db][v];
-        }
+            for (int g4 = 0; g4 < 4; ++g4)
+                *reinterpret_cast<float4*>(ob + ((wave - 1) * 32 + j) * OR + 32 * db + 8 * g4 + 4 * h) =
+                    make_float4(o[db][4 * g4], o[db][4 * g4 + 1], o[db][4 * g4 + 2], o[db][4 * g4 + 3]);
     }
     __syncthreads();
     if (wave != 0) return;
@@ -495,20 +493,25 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(const float* __res
         qx[0][0][j] = L;
     }
     waveSync();
+    if (i0 + j < N) {
+        const float inv = 1.0f / (qx[0][0][j] * 1024.0f);
+        const float c0 = qx[0][3][j];
+        float* orow = out + (size_t)(i0 + j) * a.q_tok + (size_t)head * D;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        const int qi = 8 * (v >> 2) + 4 * h + (v & 3);
-        if (i0 + qi < N) {
-            const float inv = 1.0f / (qx[0][0][qi] * 1024.0f);
-            const float c0 = qx[0][3][qi];
+        for (int db = 0; db < DB; ++db)
 #pragma unroll
-            for (int db = 0; db < DB; ++db) {
-                float acc = o[db][v] * c0;
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const int d = 32 * db + 8 * g4 + 4 * h;
+                float r[4];
 #pragma unroll
-                for (int w = 1; w < W; ++w) acc += ob[((w - 1) * 32 + qi) * D + 32 * db + j] * qx[w][3][qi];
-                out[(size_t)(i0 + qi) * a.q_tok + (size_t)head * D + 32 * db + j] = acc * inv;
+                for (int e = 0; e < 4; ++e) {
+                    float acc = o[db][4 * g4 + e] * c0;
+#pragma unroll
+                    for (int w = 1; w < W; ++w) acc += ob[((w - 1) * 32 + j) * OR + d + e] * qx[w][3][j];
+                    r[e] = acc * inv;
+                }
+                *reinterpret_cast<float4*>(orow + d) = make_float4(r[0], r[1], r[2], r[3]);
             }
-        }
     }
 }
 
