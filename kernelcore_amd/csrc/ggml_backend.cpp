@@ -41,6 +41,19 @@
 
 using T = kcGgmlTensor;
 
+namespace kcamd::ggml {
+// The structure of a node list as its signature reads it (each src slot a node index, a leaf -- a
+// tensor outside the list, numbered in first-seen order -- or none), kept while the same node array
+// with the same src links comes back, so that a call that launches the kept graph again spends its
+// host time on the fields alone.
+struct SigShape {
+    std::vector<const kcGgmlTensor*> nodes;
+    std::vector<const kcGgmlTensor*> srcs;  // per node, its 5 src links
+    std::vector<int64_t> ref;               // per node and src slot: index >= 0, -1 none, -2 - leaf id
+    std::vector<const kcGgmlTensor*> leaves;
+};
+}  // namespace kcamd::ggml
+
 struct kcGgmlBackend_st {
     kcGgmlConfig cfg{};
     kcStream_t stream = nullptr;
@@ -48,6 +61,8 @@ struct kcGgmlBackend_st {
     std::map<int, float*> ones;  // device float[n] of 1.0f: rms_norm without a weight, rope without factors
     kcGraph_t graph = nullptr;   // the kept graph, the signature of its nodes, the scratch it points into
     std::vector<uint64_t> sig;
+    kcamd::ggml::SigShape shape;     // the last call's node structure, and its signature
+    std::vector<uint64_t> sig_now;
     unsigned graph_gen = 0;
     unsigned graph_options = 0;  // the kernel options' generation the graph was recorded under
     long long graph_launches = 0;
@@ -1258,10 +1273,46 @@ E plan(const kcGgmlConfig& c, const T* const* nodes, int n, Plan& out) {
 
 // The nodes as a graph would be recorded from them: every field a launch or a fusion decision reads,
 // src links as node indices (or, for tensors outside the list, their first-seen order and fields).
-void signature(const T* const* nodes, int n, std::vector<uint64_t>& s) {
+// In two parts: the structure (sigShape, kept while the node array and its src links are the same)
+// and the fields in that order (sigValues).
+using kcamd::ggml::SigShape;
+constexpr int kSrcs = 5;
+
+bool sameShape(const SigShape& sh, const T* const* nodes, int n) {
+    if (sh.nodes.size() != size_t(n) || !std::equal(nodes, nodes + n, sh.nodes.begin())) return false;
+    for (int i = 0; i < n; ++i)
+        if (!std::equal(nodes[i]->src, nodes[i]->src + kSrcs, sh.srcs.begin() + size_t(i) * kSrcs)) return false;
+    return true;
+}
+
+void sigShape(const T* const* nodes, int n, SigShape& sh) {
+    sh.nodes.assign(nodes, nodes + n);
+    sh.srcs.clear();
+    sh.ref.clear();
+    sh.leaves.clear();
     std::unordered_map<const T*, int64_t> id;
+    id.reserve(size_t(n) * 2);
     for (int i = 0; i < n; ++i) id.emplace(nodes[i], i);
     std::unordered_map<const T*, int64_t> leaf;
+    for (int i = 0; i < n; ++i)
+        for (const T* src : nodes[i]->src) {
+            sh.srcs.push_back(src);
+            if (!src) {
+                sh.ref.push_back(-1);
+                continue;
+            }
+            const auto it = id.find(src);
+            if (it != id.end()) {
+                sh.ref.push_back(it->second);
+                continue;
+            }
+            const auto [lt, fresh] = leaf.emplace(src, int64_t(leaf.size()));
+            if (fresh) sh.leaves.push_back(src);
+            sh.ref.push_back(-2 - lt->second);
+        }
+}
+
+void sigValues(const SigShape& sh, std::vector<uint64_t>& s) {
     const auto put = [&s](const T* t) {
         s.push_back(uint64_t(uint32_t(t->op)) | uint64_t(uint32_t(t->type)) << 32);
         for (int d = 0; d < 4; ++d) s.push_back(uint64_t(t->ne[d]));
@@ -1272,22 +1323,26 @@ void signature(const T* const* nodes, int n, std::vector<uint64_t>& s) {
                     uint64_t(t->view != 0) << 34);
         s.push_back(uint64_t(uint32_t(t->uses)));
     };
-    s.push_back(uint64_t(n));
-    for (int i = 0; i < n; ++i) {
-        put(nodes[i]);
-        for (const T* src : nodes[i]->src) {
-            if (!src) {
+    s.clear();
+    s.push_back(uint64_t(sh.nodes.size()));
+    size_t r = 0;
+    int64_t next = 0;  // leaves put so far (a leaf's fields follow its first reference)
+    for (const T* node : sh.nodes) {
+        put(node);
+        for (int k = 0; k < kSrcs; ++k) {
+            const int64_t v = sh.ref[r++];
+            if (v == -1) {
                 s.push_back(~uint64_t(0));
-                continue;
+            } else if (v >= 0) {
+                s.push_back(uint64_t(v));
+            } else {
+                const int64_t lid = -2 - v;
+                s.push_back(uint64_t(1) << 62 | uint64_t(lid));
+                if (lid == next) {
+                    put(sh.leaves[size_t(lid)]);
+                    ++next;
+                }
             }
-            const auto it = id.find(src);
-            if (it != id.end()) {
-                s.push_back(uint64_t(it->second));
-                continue;
-            }
-            const auto [lt, fresh] = leaf.emplace(src, int64_t(leaf.size()));
-            s.push_back(uint64_t(1) << 62 | uint64_t(lt->second));
-            if (fresh) put(src);
         }
     }
 }
@@ -1333,15 +1388,22 @@ E collectTimes(kcGgmlBackend_st& be) {
 }
 
 E compute(kcGgmlBackend_st& be, const T* const* nodes, int n) {
-    if (E e = checkNodes(be.cfg, nodes, n); e != ok) return e;
+    if (n < 0 || (n > 0 && !nodes)) return bad("null node list or negative count");
+    for (int i = 0; i < n; ++i)
+        if (!nodes[i]) {
+            kcamd::setDetail("ggml backend: node %d is null", i);
+            return kc::Error::InvalidValue;
+        }
     const auto t0 = std::chrono::steady_clock::now();
     const bool prof = be.cfg.profile >= 1, each = be.cfg.profile >= 2;
     const bool graphs = be.cfg.graphs != 0 && !each;  // launches timed one by one: no graph
     const unsigned options = kcamd::optionsGeneration();  // read before the walk reads any option
-    std::vector<uint64_t> sig;
     if (graphs) {
-        signature(nodes, n, sig);
-        if (be.graph && be.graph_gen == be.rec.gen && be.graph_options == options && sig == be.sig) {  // the kept graph again
+        if (!sameShape(be.shape, nodes, n)) sigShape(nodes, n, be.shape);
+        sigValues(be.shape, be.sig_now);
+        // the kept graph again: the same fields as when it was recorded (and checked) -- what the
+        // checks read is in the signature
+        if (be.graph && be.graph_gen == be.rec.gen && be.graph_options == options && be.sig_now == be.sig) {
             const auto tr = std::chrono::steady_clock::now();
             if (E e = kcGraphLaunch(be.graph, be.stream); e != ok) return e;
             if (E e = kcStreamSynchronize(be.stream); e != ok) return e;
@@ -1355,7 +1417,7 @@ E compute(kcGgmlBackend_st& be, const T* const* nodes, int n) {
             return ok;
         }
     }
-    Plan pl;
+    Plan pl;  // (checks the nodes first)
     if (E e = plan(be.cfg, nodes, n, pl); e != ok) return e;
     if (E e = makeOnes(be, pl.ones); e != ok) return e;
     kcamd::mulmat::reset(be.rec);
@@ -1404,7 +1466,7 @@ E compute(kcGgmlBackend_st& be, const T* const* nodes, int n) {
             return l;
         }
         be.graph = g;
-        be.sig = std::move(sig);
+        be.sig = be.sig_now;
         be.graph_gen = be.rec.gen;
         be.graph_options = options;
         be.graph_launches = pl.launches;

@@ -454,10 +454,25 @@ def test_kept_graph_is_launched_again_for_new_inputs():
         prev = got
     st = graph_be.stats()
     assert (st["computes"], st["graphs_recorded"], st["graphs_reused"]) == (3, 1, 2)
+    # the same node array with one src link moved (the attention norm's MUL now reads the FFN norm's
+    # weight): recorded again, not the kept graph launched
+    mul = next(t for t in L.g.nodes if t.op == kc.GGML_OP["mul"] and
+               C.addressof(t.src[1].contents) == C.addressof(L.t["attn_norm"]))
+    mul.src[1] = C.pointer(L.t["ffn_norm"])
+    graph_be.compute(nodes)
+    got = L.get("out", np.float32)
+    kc.synchronize()
+    eager_be.compute(L.g.nodes)
+    assert np.array_equal(kq.bits(got), kq.bits(L.get("out", np.float32)))
+    assert not np.array_equal(kq.bits(got), kq.bits(prev))
+    st = graph_be.stats()
+    assert (st["computes"], st["graphs_recorded"], st["graphs_reused"]) == (4, 2, 2)
+    graph_be.compute(nodes)  # and that graph kept in turn
+    assert graph_be.stats()["graphs_reused"] == 3
     # another node list (the attention of one more token): recorded again
     L2 = Layer(shape, N, p0 + 1, seed=500)
     graph_be.compute(L2.g.nodes)
-    assert graph_be.stats()["graphs_recorded"] == 2
+    assert graph_be.stats()["graphs_recorded"] == 3
     for b in (graph_be, eager_be):
         b.close()
     L.free()
