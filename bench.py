@@ -220,7 +220,7 @@ def decode_bytes(w, cfg, ctx):
     return wb + kv + cfg["n_vocab"] * 4
 
 
-def ggml_backend_decode_run(cfg, n_ctx, n_decode, seed, reps, modes=(1, 0)):
+def ggml_backend_decode_run(cfg, n_ctx, n_decode, seed, reps, modes=(1, 0), profile=0):
     """The drop-in path: single-token decode steps of cfg through the ggml backend core
     (kcGgmlGraphCompute) on the graph llama.cpp builds for them (kernelcore_amd/ggml_graph.py: the
     reference op sequence, the backend's fusions, no driver-level fusion), at context n_ctx
@@ -229,7 +229,9 @@ def ggml_backend_decode_run(cfg, n_ctx, n_decode, seed, reps, modes=(1, 0)):
     host updates the position, cache row and mask inputs (three small copies) and calls
     graph_compute, which returns once the step has run. Weights N(0, 0.02) quantized on the device
     (the types of kcModelTensorInfo), norms N(1, 0.05), caches zero (the step time does not depend
-    on their values). Also timed: the same steps with graphs off (launches one by one)."""
+    on their values). Also timed: the same steps with graphs off (launches one by one). profile 1 / 2:
+    the backends made with GGML_KERNELCORE_PROFILE's setting, their host times per call and (2: every
+    launch timed alone, no graph) the device time per launch name added to the result."""
     from kernelcore_amd import ggml_graph as gg
 
     s = gg.LayerShape.of_model(cfg, (n_ctx + n_decode + 255) // 256 * 256)
@@ -271,7 +273,7 @@ def ggml_backend_decode_run(cfg, n_ctx, n_decode, seed, reps, modes=(1, 0)):
                        f"kcGgmlGraphCompute on llama.cpp's graph ({len(g.nodes)} nodes per step, KV view of {n_kv} rows)",
            "setup_s": round(setup_s, 1)}
     for graphs in modes:
-        be = kc.GgmlBackend(graphs=graphs)
+        be = kc.GgmlBackend(graphs=graphs, profile=profile)
         mask[:] = -np.inf
         for p in range(n_ctx - 4, n_ctx):  # warm-up (records the kept graph)
             step(p)
@@ -283,12 +285,19 @@ def ggml_backend_decode_run(cfg, n_ctx, n_decode, seed, reps, modes=(1, 0)):
                 step(p)
             times.append(time.perf_counter() - w0)
         st = be.stats()
+        prof = be.profile() if profile >= 2 else None
         be.close()
         ms = med(times) / n_decode * 1e3
         key = "kept_graph" if graphs else "eager"
         out[key] = {"tok_s": round(1e3 / ms, 1), "ms_per_token": round(ms, 4),
                     "launches_per_token": round(st["launches"] / st["computes"], 1),
                     "graphs_recorded": st["graphs_recorded"], "graphs_reused": st["graphs_reused"]}
+        if profile >= 1:  # the library's host clock per graph_compute call (warm-up calls included)
+            out[key]["profile"] = {f"{k}_per_call": round(st[k] / st["computes"], 4)
+                                   for k in ("compute_ms", "record_ms", "run_ms")}
+            out[key]["profile"]["calls"] = st["computes"]
+        if prof:  # device ms per launch name, summed over the calls
+            out[key]["profile"]["launches"] = {k: [n, round(v, 4)] for k, (n, v) in sorted(prof.items())}
     lg = np.empty(s.n_vocab, np.float32)
     kc.call("kcMemcpy", lg.ctypes.data, logits.data, lg.nbytes, kc.DEVICE_TO_HOST)
     out["finite"] = bool(np.all(np.isfinite(lg)))
@@ -575,6 +584,8 @@ def main():
                     help="run only the config-3 matmul leg (counter profiles); prints its JSON")
     ap.add_argument("--skip-ggml", action="store_true", help="skip the ggml-backend decode leg")
     ap.add_argument("--only-ggml", action="store_true", help="run only the ggml-backend decode leg; prints its JSON")
+    ap.add_argument("--ggml-profile", type=int, default=0,
+                    help="with --only-ggml: the backend decode legs with GGML_KERNELCORE_PROFILE's setting (1, 2)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -591,7 +602,8 @@ def main():
     def ggml_cfg5():
         # config 5 (Qwen3-8B shape: the per-head q / k norms, NEOX RoPE) through the backend: decode at
         # context 1024 onwards (a quarter of the model leg's steps), then the 1024-token prompt
-        d = ggml_backend_decode_run(QWEN3_8B, 1024, max(args.decode_steps5 // 4, 8), seed=9900, reps=reps, modes=modes)
+        d = ggml_backend_decode_run(QWEN3_8B, 1024, max(args.decode_steps5 // 4, 8), seed=9900, reps=reps, modes=modes,
+                                    profile=args.ggml_profile if args.only_ggml else 0)
         note(f"# ggml backend cfg5 decode done: {d[('kept_graph' if gr else 'eager')]['tok_s']} tok/s")
         p = ggml_backend_prefill_run(QWEN3_8B, 1024, seed=9950, reps=reps, graphs=gr)
         note(f"# ggml backend cfg5 prefill done: {p['prefill_tok_s']} tok/s")
@@ -599,7 +611,7 @@ def main():
 
     if args.only_ggml:
         res = {"ggml_backend_decode_cfg4": ggml_backend_decode_run(LLAMA32_3B, 512, args.decode_steps, seed=9700,
-                                                                   reps=reps, modes=modes),
+                                                                   reps=reps, modes=modes, profile=args.ggml_profile),
                "ggml_backend_prefill_cfg4": ggml_backend_prefill_run(LLAMA32_3B, 512, seed=9800, reps=reps, graphs=gr)}
         if not args.skip_cfg5:
             res["ggml_backend_decode_cfg5"], res["ggml_backend_prefill_cfg5"] = ggml_cfg5()
