@@ -715,18 +715,47 @@ __global__ void rope_kv_rows_kernel(const float* __restrict__ q, float* __restri
 // Residual add + RMS norm + per-256 quantization of a batch (add_sumsq_f.cu then norm_mul_q8k_f.cu
 // in one workgroup per row): x = a + (b [+ b2]) (a null: x = b, not stored), the per-32 sums of
 // squares in order, their total in block order, y = x r w quantized per 256 into the row's slot.
-// The row is loaded with all 256 threads (coalesced) into LDS, blocks of 32 padded to 36 floats
-// so that the per-block sums (one thread each, in order) read different banks.
+// regs (a row of at most four values per thread): each thread keeps its quad and the norm weights
+// of it in registers from the first loads on, the per-32 sums chained through the block's 8 lanes
+// (sumsq8: the same additions in the same order), and only those sums pass through LDS. Else the
+// row is loaded with every thread (coalesced) into LDS, blocks of 32 padded to 36 floats so that
+// the per-block sums (one thread each, in order) read different banks.
 template <bool A16>
 __global__ __launch_bounds__(1024) void add_norm_q8k_kernel(const float* a, const float* b, const float* b2, float* out,
                                                            const float* __restrict__ w, int* __restrict__ q, int n,
-                                                           float eps, ActF16 ao, int has_ao, float* __restrict__ y) {
+                                                           float eps, ActF16 ao, int has_ao, float* __restrict__ y,
+                                                           int regs) {
     extern __shared__ float xs[];  // n / 32 blocks of 36 floats, then n / 32 sums of squares
     const int nsb = n / 256, nb = n / 32;
     const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float* ss = xs + nb * 36;
     const size_t r0 = (size_t)row * n;
     const int nt = blockDim.x;
+    if (regs) {  // 4 nt >= n: thread t holds values 4t .. 4t + 3 = super-block t / 64, lane t % 64
+        const bool live = wave < nsb;  // wavefront-uniform (n is a multiple of 256)
+        const int i = live ? 4 * tid : 0;
+        float4 v = load4<A16>(b + r0 + i);
+        const float4 wv = load4<A16>(w + i);
+        if (b2) {
+            const float4 u = load4<A16>(b2 + r0 + i);
+            v.x += u.x, v.y += u.y, v.z += u.z, v.w += u.w;
+        }
+        if (a) {
+            const float4 x = load4<A16>(a + r0 + i);
+            v = make_float4(x.x + v.x, x.y + v.y, x.z + v.z, x.w + v.w);
+            if (live) store4<A16>(out + r0 + i, v);
+        }
+        const float xv[4] = {v.x, v.y, v.z, v.w};
+        const float sq = sumsq8(xv, tid & 7);
+        if (live && (tid & 7) == 7) ss[tid >> 3] = sq;
+        __syncthreads();
+        if (!live) return;
+        const float r = rmsScale(ss, nb, n, eps);
+        const float4 yv = make_float4(v.x * r * wv.x, v.y * r * wv.y, v.z * r * wv.z, v.w * r * wv.w);
+        if (y) store4<A16>(y + r0 + i, yv);
+        quant256Wave(yv.x, yv.y, yv.z, yv.w, q + (size_t)row * nsb * 85, nsb, wave, ao, has_ao != 0, row);
+        return;
+    }
     for (int i = 4 * tid; i < n; i += 4 * nt) {
         float4 v = load4<A16>(b + r0 + i);
         if (b2) {
@@ -1090,12 +1119,15 @@ int launchAddNormQ8K(const float* a, const float* b, const float* b2, float* out
     if (rows <= 0) return 0;
     const size_t lds = sizeof(float) * ((size_t)n / 32 * 37);
     if (n % 256 || lds > 65536) return fromHip(hipErrorInvalidValue, "add + norm: row length");
+    // the register form wherever a row is at most four values per thread (option addnorm_lds = 1:
+    // the LDS form always)
+    const int nth = waveThreads(n), regs = 4 * nth >= n && option("addnorm_lds") != 1;
     if (al16(b) && (!b2 || al16(b2)) && (!a || (al16(a) && al16(out))) && al16(w) && (!y || al16(y)))
-        hipLaunchKernelGGL(add_norm_q8k_kernel<true>, dim3(rows), dim3(waveThreads(n)), lds, s, a, b, b2, out, w, q, n,
-                           eps, ao ? *ao : ActF16{}, ao ? 1 : 0, y);
+        hipLaunchKernelGGL(add_norm_q8k_kernel<true>, dim3(rows), dim3(nth), lds, s, a, b, b2, out, w, q, n, eps,
+                           ao ? *ao : ActF16{}, ao ? 1 : 0, y, regs);
     else
-        hipLaunchKernelGGL(add_norm_q8k_kernel<false>, dim3(rows), dim3(waveThreads(n)), lds, s, a, b, b2, out, w, q, n,
-                           eps, ao ? *ao : ActF16{}, ao ? 1 : 0, y);
+        hipLaunchKernelGGL(add_norm_q8k_kernel<false>, dim3(rows), dim3(nth), lds, s, a, b, b2, out, w, q, n, eps,
+                           ao ? *ao : ActF16{}, ao ? 1 : 0, y, regs);
     return fromHip(hipGetLastError(), "add + norm");
 }
 

@@ -1257,7 +1257,7 @@ kcError_t kcSetKernelOption(const char* option, int value) noexcept {
     return gated<Need::Nothing>("kcSetKernelOption", [&](Runtime& r) {
         static const char* known[] = {"matvec_waves", "matvec_pipe", "matvec_nt", "matmul_path", "decode_path", "attn_path", "prefill_act", "swiglu_pre",
                                       "qkv_tiles", "matmul_waves", "ggml_extra_fusions", "matvec_af", "matmul_ws",
-                                      "matmul_split6", "qk_fuse"};
+                                      "matmul_split6", "qk_fuse", "addnorm_lds"};
         if (!option) return kc::Error::InvalidValue;
         bool found = false;
         for (const char* k : known) found |= std::strcmp(k, option) == 0;

@@ -180,6 +180,36 @@ def test_qwen3_prompt_norms_fused_bit_identical(head_dim, n_head, n_head_kv):
     assert rel_l2(got[0][0][0], lo) < 1e-2
 
 
+@pytest.mark.parametrize("n_embd", [256, 768, 3072, 4096])
+def test_prompt_add_norm_register_form_bit_identical(n_embd):
+    """The prompt's residual add + RMS norm + per-256 quantization with each row's values kept in
+    registers (the default up to four values per thread) against the LDS form (option addnorm_lds
+    = 1): the same logits and the same cache bits for a prompt and a continuing chunk (256 and 768
+    values: workgroups with wavefronts past the row's end)."""
+    cfg = dict(LLAMA, n_embd=n_embd, n_head=n_embd // 64, n_head_kv=2, n_ff=512, n_vocab=512)
+    w = random_weights(cfg, 23)
+    prompt = np.random.default_rng(6).integers(0, cfg["n_vocab"], 70 + 33).astype(np.int32)
+    got = {}
+    for lds in (1, 0):
+        kc.set_option("addnorm_lds", lds)
+        try:
+            m = kc.Model(**cfg)
+            for (tid, layer), data in w.items():
+                m.set_tensor(tid, layer, data)
+            lg = [m.forward(prompt[:70]), m.forward(prompt[70:])]
+            caches = [m.read_cache(li, which, 0, len(prompt)) for li in range(cfg["n_layer"]) for which in (0, 1)]
+            got[lds] = (lg, caches)
+            m.close()
+        finally:
+            kc.set_option("addnorm_lds", 0)
+    for a, b in zip(got[0][0], got[1][0]):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    for a, b in zip(got[0][1], got[1][1]):
+        assert np.array_equal(a, b)
+    lo = OracleModel(cfg, w).forward(prompt[:70])
+    assert rel_l2(got[0][0][0], lo) < 1e-2
+
+
 def test_model_3b_shape_two_layers():
     """Two layers at the full Llama-3.2-3B widths (3072 / 24 heads / 8 KV heads / 8192 FFN / 128256
     vocab): an 8-token prompt and two decode steps against the oracle."""
