@@ -527,8 +527,8 @@ __global__ void set_rows_kernel(const float* __restrict__ src, const int* __rest
 // RoPE of q (nh heads) and k (nkv heads) of a batch, and the fp16 stores of the roped k and of v
 // into the cache rows pos[t] (rope_ggml.cu, set_rows_f16.cu): one thread per (token, group of 4
 // heads, pair), which takes theta, its cosine and sine once for its heads (q heads first, then the
-// k heads with their v). Rows outside [0, dst_rows) are not stored. v2 (may be null): v's product
-// in two K ranges, stored as v + v2.
+// k heads with their v), all its loads issued before the first is used. Rows outside [0, dst_rows)
+// are not stored. v2 (may be null): v's product in two K ranges, stored as v + v2.
 __global__ void rope_qk_store_kernel(const float* __restrict__ q, float* __restrict__ qr, const float* __restrict__ k,
                                      const float* __restrict__ v, const float* __restrict__ v2,
                                      unsigned short* __restrict__ kc,
@@ -541,6 +541,28 @@ __global__ void rope_qk_store_kernel(const float* __restrict__ q, float* __restr
     const int i = (int)(idx % pairs);
     const long long tg = idx / pairs;
     const int hg = (int)(tg % ng), t = (int)(tg / ng);
+    // every load of the thread's four heads first (one memory round trip, not one per head)
+    float x0[4], x1[4], va[4], vb[4], wa[4], wb[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int h = hg * 4 + u;
+        x0[u] = x1[u] = va[u] = vb[u] = wa[u] = wb[u] = 0.0f;
+        if (h < nh) {
+            const size_t a = 2 * ((size_t)t * nh + h) * pairs + (size_t)i * m1;
+            x0[u] = q[a];
+            x1[u] = q[a + m2];
+        } else if (h < nh + nkv) {
+            const size_t a = 2 * ((size_t)t * nkv + (h - nh)) * pairs + (size_t)i * m1;
+            x0[u] = k[a];
+            x1[u] = k[a + m2];
+            va[u] = v[a];
+            vb[u] = v[a + m2];
+            if (v2) {
+                wa[u] = v2[a];
+                wb[u] = v2[a + m2];
+            }
+        }
+    }
     const int p = pos[t];
     const float theta = (float)p * exp2f(-(float)i / (float)pairs * log2_base) / ff[i];
     const float c = cosf(theta), sn = sinf(theta);
@@ -550,17 +572,14 @@ __global__ void rope_qk_store_kernel(const float* __restrict__ q, float* __restr
         const int h = hg * 4 + u;
         if (h < nh) {
             const size_t a = 2 * ((size_t)t * nh + h) * pairs + (size_t)i * m1;
-            const float x0 = q[a], x1 = q[a + m2];
-            qr[a] = x0 * c - x1 * sn;
-            qr[a + m2] = x0 * sn + x1 * c;
+            qr[a] = x0[u] * c - x1[u] * sn;
+            qr[a + m2] = x0[u] * sn + x1[u] * c;
         } else if (h < nh + nkv && store) {
             const int hk = h - nh;
-            const size_t a = 2 * ((size_t)t * nkv + hk) * pairs + (size_t)i * m1;
             const size_t e = (size_t)p * dst_row * 2 + 2 * (size_t)hk * pairs + (size_t)i * m1;
-            const float x0 = k[a], x1 = k[a + m2];
-            kc[e] = (unsigned short)f2h(x0 * c - x1 * sn);
-            kc[e + m2] = (unsigned short)f2h(x0 * sn + x1 * c);
-            const float v0 = v2 ? v[a] + v2[a] : v[a], v1 = v2 ? v[a + m2] + v2[a + m2] : v[a + m2];
+            kc[e] = (unsigned short)f2h(x0[u] * c - x1[u] * sn);
+            kc[e + m2] = (unsigned short)f2h(x0[u] * sn + x1[u] * c);
+            const float v0 = v2 ? va[u] + wa[u] : va[u], v1 = v2 ? vb[u] + wb[u] : vb[u];
             vc[e] = (unsigned short)f2h(v0);
             vc[e + m2] = (unsigned short)f2h(v1);
         }
@@ -578,12 +597,16 @@ __global__ void rope_qk_store_kernel(const float* __restrict__ q, float* __restr
 // thread t always pair t % pairs, of rows 256 / pairs apart. The same floats as the three launches,
 // bit for bit. hd 64 or 128 (lp = log2(pairs)), ff (the frequency factors) hd / 2 values.
 constexpr int kNormRopeThreads = 256;
-__global__ __launch_bounds__(kNormRopeThreads) void norm_rope_qk_store_kernel(
-    const float* __restrict__ q, float* __restrict__ qr, const float* __restrict__ k, const float* __restrict__ v,
-    const float* __restrict__ v2, const float* __restrict__ qw, const float* __restrict__ kw,
-    unsigned short* __restrict__ kc, unsigned short* __restrict__ vc, const int* __restrict__ pos,
-    const float* __restrict__ ff, int lp, int nh, int nkv, int n, float log2_base, int m1, int m2, int dst_row,
-    int dst_rows, float eps, int nq_blocks) {
+// One workgroup's 64 head rows of norm_rope_qk_store_kernel: q rows (ISQ) or k rows with their v.
+template <bool ISQ>
+__device__ __forceinline__ void normRopeRows(const float* __restrict__ q, float* __restrict__ qr,
+                                             const float* __restrict__ k, const float* __restrict__ v,
+                                             const float* __restrict__ v2, const float* __restrict__ qw,
+                                             const float* __restrict__ kw, unsigned short* __restrict__ kc,
+                                             unsigned short* __restrict__ vc, const int* __restrict__ pos,
+                                             const float* __restrict__ ff, int lp, int nh, int nkv, int n,
+                                             float log2_base, int m1, int m2, int dst_row, int dst_rows, float eps,
+                                             int nq_blocks) {
     extern __shared__ float4 nr_lds[];
     const int pairs = 1 << lp, hd = 2 * pairs, lq4 = lp - 1, q4 = hd / 4, stride = q4 + 1;
     float4* xs = nr_lds;                                       // 64 rows, padded
@@ -592,26 +615,64 @@ __global__ __launch_bounds__(kNormRopeThreads) void norm_rope_qk_store_kernel(
     long long* dst = reinterpret_cast<long long*>(tl + 64);    // per row: q row / cache offset, -1: no store
     float2* cs = reinterpret_cast<float2*>(dst + 64);          // [token - t0][pairs] (cos, sin)
     const int tid = threadIdx.x;
-    const bool isq = (int)blockIdx.x < nq_blocks;
-    const int nhd = isq ? nh : nkv, rows = n * nhd;
-    const int row0 = (isq ? (int)blockIdx.x : (int)blockIdx.x - nq_blocks) * 64;
+    const int nhd = ISQ ? nh : nkv, rows = n * nhd;
+    const int row0 = (ISQ ? (int)blockIdx.x : (int)blockIdx.x - nq_blocks) * 64;
     const int nr = min(64, rows - row0), nqw = nr * q4;
-    const float4* xb = reinterpret_cast<const float4*>((isq ? q : k) + (size_t)row0 * hd);
-#pragma unroll 4
-    for (int jj = tid; jj < nqw; jj += kNormRopeThreads) xs[(jj >> lq4) * stride + (jj & (q4 - 1))] = xb[jj];
-    // theta per (token, pair) of this workgroup's tokens t0 .. t0 + ntok - 1
+    const float4* xb = reinterpret_cast<const float4*>((ISQ ? q : k) + (size_t)row0 * hd);
     const int t0 = row0 / nhd, ntok = (row0 + nr - 1) / nhd - t0 + 1;
-    for (int u = tid; u < ntok * pairs; u += kNormRopeThreads) {
-        const int tt = u >> lp, i = u & (pairs - 1);
-        const float theta = (float)pos[t0 + tt] * exp2f(-(float)i / (float)pairs * log2_base) / ff[i];
+    const int i = tid & (pairs - 1), a = i * m1;  // this thread's pair: values a, a + m2 of a head row
+    const int rstep = kNormRopeThreads >> lp;     // the thread's rows: tid / pairs + j rstep
+    // Every global load is issued before any is used (one memory round trip): the 64 rows (at most
+    // 8 16-byte words per thread), the positions of the first 4 x 256 (token, pair) entries of the
+    // cos / sin table, and in a k workgroup the v (+ v2) values that the thread stores.
+    float4 xl[8];  // (clamped: past nqw a thread reloads the last word, which it does not store)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xl[j] = xb[min(tid + j * kNormRopeThreads, nqw - 1)];
+    const float fi = ff[i];  // entry u of the table has pair u % pairs = i (256 is a multiple of pairs)
+    const float* w = ISQ ? qw : kw;
+    const float wa_ = w[a], wb_ = w[a + m2];
+    int pp[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pp[j] = pos[t0 + min((tid + j * kNormRopeThreads) >> lp, ntok - 1)];
+    const int prow = ISQ ? 0 : pos[min((row0 + min(tid, nr - 1)) / nhd, n - 1)];
+    constexpr int kVr = 16;  // rows per thread at pairs = 64
+    float va[kVr], vb[kVr], wa[kVr], wb[kVr];
+    if (!ISQ) {  // (unconditional, clamped loads: a load under a condition is waited for at its end)
+        const float* v2p = v2 ? v2 : v;
+#pragma unroll
+        for (int j = 0; j < kVr; ++j) {
+            const size_t av = (size_t)(row0 + min((tid >> lp) + j * rstep, nr - 1)) * hd + a;
+            va[j] = v[av];
+            vb[j] = v[av + m2];
+            wa[j] = v2p[av];
+            wb[j] = v2p[av + m2];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {  // unconditional (a clamped word is stored again, the same value),
+        const int jj = min(tid + j * kNormRopeThreads, nqw - 1);  // so no load sinks into a branch
+        xs[(jj >> lq4) * stride + (jj & (q4 - 1))] = xl[j];
+    }
+    // theta per (token, pair) of this workgroup's tokens t0 .. t0 + ntok - 1
+    const float fr = exp2f(-(float)i / (float)pairs * log2_base);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int u = tid + j * kNormRopeThreads;
+        if (u < ntok * pairs) {
+            const float theta = (float)pp[j] * fr / fi;
+            cs[u] = make_float2(cosf(theta), sinf(theta));
+        }
+    }
+    for (int u = tid + 4 * kNormRopeThreads; u < ntok * pairs; u += kNormRopeThreads) {
+        const float theta = (float)pos[t0 + (u >> lp)] * fr / fi;
         cs[u] = make_float2(cosf(theta), sinf(theta));
     }
     __syncthreads();
     if (tid < nr) {
         const float4* xr = xs + tid * stride;
         float ss = 0.0f;
-        for (int i = 0; i < q4; ++i) {
-            const float4 x4 = xr[i];
+        for (int e = 0; e < q4; ++e) {
+            const float4 x4 = xr[e];
             ss += x4.x * x4.x;
             ss += x4.y * x4.y;
             ss += x4.z * x4.z;
@@ -620,36 +681,46 @@ __global__ __launch_bounds__(kNormRopeThreads) void norm_rope_qk_store_kernel(
         rr[tid] = 1.0f / sqrtf(ss / (float)hd + eps);
         const int row = row0 + tid, t = row / nhd, hh = row - t * nhd;
         tl[tid] = t - t0;
-        if (isq) {
-            dst[tid] = (long long)row * hd;
-        } else {
-            const int p = pos[t];
-            dst[tid] = p >= 0 && p < dst_rows ? (long long)p * dst_row * 2 + (long long)hh * hd : -1;
-        }
+        if (ISQ) dst[tid] = (long long)row * hd;
+        else dst[tid] = prow >= 0 && prow < dst_rows ? (long long)prow * dst_row * 2 + (long long)hh * hd : -1;
     }
     __syncthreads();
     const float* xf = reinterpret_cast<const float*>(xs);
-    const int i = tid & (pairs - 1), a = i * m1;  // this thread's pair: values a, a + m2 of a head row
-    const float* w = isq ? qw : kw;
-    const float wa = w[a], wb = w[a + m2];
-    for (int r = tid >> lp; r < nr; r += kNormRopeThreads >> lp) {
+#pragma unroll
+    for (int j = 0; j < kVr; ++j) {
+        const int r = (tid >> lp) + j * rstep;
+        if (j * rstep >= 64 || r >= nr) break;
         const float rv = rr[r];
-        const float x0 = xf[r * 4 * stride + a] * rv * wa, x1 = xf[r * 4 * stride + a + m2] * rv * wb;
+        const float x0 = xf[r * 4 * stride + a] * rv * wa_, x1 = xf[r * 4 * stride + a + m2] * rv * wb_;
         const float2 csv = cs[(tl[r] << lp) + i];
         const float y0 = x0 * csv.x - x1 * csv.y, y1 = x0 * csv.y + x1 * csv.x;
         const long long d = dst[r];
-        if (isq) {
+        if (ISQ) {
             qr[d + a] = y0;
             qr[d + a + m2] = y1;
         } else if (d >= 0) {
-            const size_t e = (size_t)d + a, av = (size_t)(row0 + r) * hd + a;
+            const size_t e = (size_t)d + a;
             kc[e] = (unsigned short)f2h(y0);
             kc[e + m2] = (unsigned short)f2h(y1);
-            const float v0 = v2 ? v[av] + v2[av] : v[av], v1 = v2 ? v[av + m2] + v2[av + m2] : v[av + m2];
+            const float v0 = v2 ? va[j] + wa[j] : va[j], v1 = v2 ? vb[j] + wb[j] : vb[j];
             vc[e] = (unsigned short)f2h(v0);
             vc[e + m2] = (unsigned short)f2h(v1);
         }
     }
+}
+
+__global__ __launch_bounds__(kNormRopeThreads) void norm_rope_qk_store_kernel(
+    const float* __restrict__ q, float* __restrict__ qr, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ v2, const float* __restrict__ qw, const float* __restrict__ kw,
+    unsigned short* __restrict__ kc, unsigned short* __restrict__ vc, const int* __restrict__ pos,
+    const float* __restrict__ ff, int lp, int nh, int nkv, int n, float log2_base, int m1, int m2, int dst_row,
+    int dst_rows, float eps, int nq_blocks) {
+    if ((int)blockIdx.x < nq_blocks)
+        normRopeRows<true>(q, qr, k, v, v2, qw, kw, kc, vc, pos, ff, lp, nh, nkv, n, log2_base, m1, m2, dst_row,
+                           dst_rows, eps, nq_blocks);
+    else
+        normRopeRows<false>(q, qr, k, v, v2, qw, kw, kc, vc, pos, ff, lp, nh, nkv, n, log2_base, m1, m2, dst_row,
+                            dst_rows, eps, nq_blocks);
 }
 
 // The ggml graph's ROPE(q), ROPE(k), SET_ROWS(k cache, roped k, idx) and SET_ROWS(v cache, v, idx)
@@ -670,6 +741,31 @@ __global__ void rope_kv_rows_kernel(const float* __restrict__ q, float* __restri
     const int i = (int)(id % pairs);
     const long long tg = id / pairs;
     const int hg = (int)(tg % ng), t = (int)(tg / ng);
+    // every load of the thread's four heads first (one memory round trip, not one per head); each
+    // thread reads and writes only its own elements, so in-place q / k / v stay correct
+    float x0[4], x1[4], va[4], vb[4], wa[4], wb[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int h = hg * 4 + u;
+        x0[u] = x1[u] = va[u] = vb[u] = wa[u] = wb[u] = 0.0f;
+        if (h < nh) {
+            const size_t a = 2 * ((size_t)t * nh + h) * pairs + (size_t)i * m1;
+            x0[u] = q[a];
+            x1[u] = q[a + m2];
+        } else if (h < nh + nkv) {
+            const int hk = h - nh;
+            const size_t a = 2 * ((size_t)t * nkv + hk) * pairs + (size_t)i * m1;
+            const size_t av = (size_t)t * src_v + 2 * (size_t)hk * pairs + (size_t)i * m1;
+            x0[u] = k[a];
+            x1[u] = k[a + m2];
+            va[u] = v[av];
+            vb[u] = v[av + m2];
+            if (v2) {
+                wa[u] = v2[av];
+                wb[u] = v2[av + m2];
+            }
+        }
+    }
     const float theta = (float)pos[t] * exp2f(-(float)i / (float)pairs * log2_base) / ff[i];
     const float c = cosf(theta), sn = sinf(theta);
     const int row = idx[2 * t];
@@ -679,27 +775,22 @@ __global__ void rope_kv_rows_kernel(const float* __restrict__ q, float* __restri
         const int h = hg * 4 + u;
         if (h < nh) {
             const size_t a = 2 * ((size_t)t * nh + h) * pairs + (size_t)i * m1;
-            const float x0 = q[a], x1 = q[a + m2];
-            qr[a] = x0 * c - x1 * sn;
-            qr[a + m2] = x0 * sn + x1 * c;
+            qr[a] = x0[u] * c - x1[u] * sn;
+            qr[a + m2] = x0[u] * sn + x1[u] * c;
         } else if (h < nh + nkv) {
             const int hk = h - nh;
             const size_t a = 2 * ((size_t)t * nkv + hk) * pairs + (size_t)i * m1;
-            const float x0 = k[a], x1 = k[a + m2];
-            const float y0 = x0 * c - x1 * sn, y1 = x0 * sn + x1 * c;
+            const float y0 = x0[u] * c - x1[u] * sn, y1 = x0[u] * sn + x1[u] * c;
             kr[a] = y0;
             kr[a + m2] = y1;
             const size_t o = 2 * (size_t)hk * pairs + (size_t)i * m1;
             const size_t av = (size_t)t * src_v + o;
-            float v0 = 0.0f, v1 = 0.0f;
+            float v0 = va[u], v1 = vb[u];
             if (v2) {  // the whole product, also back into v (stored or not)
-                v0 = v[av] + v2[av];
-                v1 = v[av + m2] + v2[av + m2];
+                v0 = va[u] + wa[u];
+                v1 = vb[u] + wb[u];
                 v[av] = v0;
                 v[av + m2] = v1;
-            } else if (store) {
-                v0 = v[av];
-                v1 = v[av + m2];
             }
             if (store) {
                 const size_t e = (size_t)row * k_row * 2 + o, f = (size_t)row * v_row * 2 + o;

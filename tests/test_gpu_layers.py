@@ -148,9 +148,9 @@ def test_norm_golden_fixture():
     B.free()
 
 
-@pytest.mark.parametrize("per256", [False, True])
-def test_silu_mul_q8(per256):
-    n, cols = 8192, 3
+@pytest.mark.parametrize("per256,n", [(False, 8192), (True, 8192), (True, 12288), (True, 256), (True, 1280)])
+def test_silu_mul_q8(per256, n):
+    cols = 3
     g, u = kq.randn(n * cols, 4, 3.0), kq.randn(n * cols, 5)
     B = Bufs()
     bg, bu, by = B.of(g), B.of(u), B.new(n * cols * 4)
