@@ -825,14 +825,13 @@ __global__ __launch_bounds__(1024) void add_norm_q8k_kernel(const float* a, cons
     if (regs) {  // 4 nt >= n: thread t holds values 4t .. 4t + 3 = super-block t / 64, lane t % 64
         const bool live = wave < nsb;  // wavefront-uniform (n is a multiple of 256)
         const int i = live ? 4 * tid : 0;
+        // the four loads unconditional (an absent b2 / a reads b again), all issued before any use
         float4 v = load4<A16>(b + r0 + i);
+        const float4 u = load4<A16>((b2 ? b2 : b) + r0 + i);
+        const float4 x = load4<A16>((a ? a : b) + r0 + i);
         const float4 wv = load4<A16>(w + i);
-        if (b2) {
-            const float4 u = load4<A16>(b2 + r0 + i);
-            v.x += u.x, v.y += u.y, v.z += u.z, v.w += u.w;
-        }
+        if (b2) v.x += u.x, v.y += u.y, v.z += u.z, v.w += u.w;
         if (a) {
-            const float4 x = load4<A16>(a + r0 + i);
             v = make_float4(x.x + v.x, x.y + v.y, x.z + v.z, x.w + v.w);
             if (live) store4<A16>(out + r0 + i, v);
         }

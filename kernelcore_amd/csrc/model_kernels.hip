@@ -542,8 +542,9 @@ __global__ __launch_bounds__(64 * kMaskWaves) void mask_summary_kernel(const uns
         bool live = false, nonzero = false;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const int k = b * 32 + 16 * (lane & 1) + 2 * e;  // keys k, k + 1
-            if (k >= T) break;
+            // keys k, k + 1; past T the load is clamped into the row and counts for nothing
+            // (unconditional: a load under a branch is waited for alone)
+            const int k = b * 32 + 16 * (lane & 1) + 2 * e;
             const int k0 = min(k, m_row2 - 2);  // (T = m_row2 odd: the row's last pair, key k at its end)
             const uint32_t w = *reinterpret_cast<const uint32_t*>(mr + k0);
 #pragma unroll
