@@ -1348,13 +1348,15 @@ bool matmulGroupSplitsQ6(const MmPart* parts, int nparts, int k, int ncols) {
     return mfmaWsFits(g, k / 256, ncols) && splitsQ6(g, nparts, k / 256);
 }
 
+bool matmulGroupReadsActOnly(int ncols, int k) { return ncols >= 64 && mfmaHUsable(ncols, k); }
+
 int launchMatmulGroup(const MmPart* parts, int nparts, const int* xq, int k, int ncols, int ks, int* used_ks,
                       hipStream_t s, const ActF16* pre, int* part_ks) {
     *used_ks = 1;
     if (part_ks)
         for (int i = 0; i < nparts && i < 3; ++i) part_ks[i] = 1;
     if (nparts < 1 || nparts > 3 || ks < 1 || ks > 2 || k % 256 != 0) return fromHip(hipErrorInvalidValue, "matmul group");
-    if (ncols >= 64 && mfmaHUsable(ncols, k)) {
+    if (matmulGroupReadsActOnly(ncols, k)) {
         if (ks > k / 256) ks = 1;
         if (pre) {
             *used_ks = ks;

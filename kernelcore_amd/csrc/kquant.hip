@@ -169,21 +169,23 @@ __global__ void quantize_k_kernel(const float* __restrict__ x, int* __restrict__
     int s16 = s4 + __shfl_xor(s4, 1);
     s16 += __shfl_xor(s16, 2);
     int s32 = s16 + __shfl_xor(s16, 4);
-    int* qc = q + (size_t)c * nsb * 85;
-    qc[s * 64 + lane] = word;
-    if ((lane & 3) == 0) qc[nsb * 65 + s * 16 + (lane >> 2)] = s16;
-    // Lane 0 gathers B_i (lanes 8i): words [B>>6 of sums 0-3 | of 4-7 | B&63 of 0-3 | of 4-7].
-    int pw[4] = {0, 0, 0, 0};
+    if (q) {  // the int8 slot (null: a caller whose products read only the MFMA layout)
+        int* qc = q + (size_t)c * nsb * 85;
+        qc[s * 64 + lane] = word;
+        if ((lane & 3) == 0) qc[nsb * 65 + s * 16 + (lane >> 2)] = s16;
+        // Lane 0 gathers B_i (lanes 8i): words [B>>6 of sums 0-3 | of 4-7 | B&63 of 0-3 | of 4-7].
+        int pw[4] = {0, 0, 0, 0};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int b = __shfl(s32, 8 * i);
-        const int sh = 8 * (i & 3);
-        pw[i >> 2] |= ((b >> 6) & 255) << sh;
-        pw[2 + (i >> 2)] |= (b & 63) << sh;
-    }
-    if (lane == 0) {
-        for (int i = 0; i < 4; ++i) qc[nsb * 81 + s * 4 + i] = pw[i];
-        reinterpret_cast<float*>(qc + nsb * 64)[s] = d;
+        for (int i = 0; i < 8; ++i) {
+            const int b = __shfl(s32, 8 * i);
+            const int sh = 8 * (i & 3);
+            pw[i >> 2] |= ((b >> 6) & 255) << sh;
+            pw[2 + (i >> 2)] |= (b & 63) << sh;
+        }
+        if (lane == 0) {
+            for (int i = 0; i < 4; ++i) qc[nsb * 81 + s * 4 + i] = pw[i];
+            reinterpret_cast<float*>(qc + nsb * 64)[s] = d;
+        }
     }
     if (has_ao) {
         const int k = nsb * 256;
@@ -409,6 +411,7 @@ int launchQuantizeCols(const float* x, int* q, int k, int ncols, hipStream_t s) 
 }
 
 int launchQuantizeColsK(const float* x, int* q, int k, int ncols, hipStream_t s, const ActF16* ao) {
+    if (!q && !ao) return fromHip(hipErrorInvalidValue, "quantize_cols_k: no output");
     const int nsb = k / 256;
     const long long waves = (long long)nsb * ncols;
     const dim3 grid((unsigned)((waves + 3) / 4));

@@ -72,6 +72,8 @@ int launchMatmulGroup(const MmPart* parts, int nparts, const int* xq, int k, int
                       hipStream_t s, const ActF16* pre = nullptr, int* part_ks = nullptr);
 // Whether a group of ncols >= 64 columns of k values runs on the fp16-activation MFMA kernel.
 bool mfmaHUsable(int ncols, int k);
+// launchMatmulGroup given the MFMA layout (pre) reads only that layout, never the int8 slots xq
+bool matmulGroupReadsActOnly(int ncols, int k);
 // The K ranges a launch of this shape and weight type takes (2 where one K range would leave compute
 // units idle).
 int matmulKs(int rows, int k, int ncols, bool q6);

@@ -172,21 +172,23 @@ __device__ __forceinline__ void quant256Wave(float y0, float y1, float y2, float
     if (d > 0.0f) id = 1.0f / d;
     else id = 0.0f;
     const int c0 = q8r(y0 * id), c1 = q8r(y1 * id), c2 = q8r(y2 * id), c3 = q8r(y3 * id);
-    qc[s * 64 + lane] = (c0 & 255) | ((c1 & 255) << 8) | ((c2 & 255) << 16) | ((c3 & 255) << 24);
     int s16 = c0 + c1 + c2 + c3;
     s16 += dppI<0xB1>(s16);
     s16 += dppI<0x4E>(s16);  // the 16 values of lanes 4g .. 4g + 3
-    if ((lane & 3) == 0) qc[nsb * 65 + s * 16 + (lane >> 2)] = s16;
     const int b32 = s16 + __shfl_down(s16, 4);  // lanes 8i: the sum of 32 values 32i .. 32i + 31
-    int pw[4] = {0, 0, 0, 0};
+    if (qc) {  // the int8 slot (null: a caller whose products read only the MFMA layout)
+        qc[s * 64 + lane] = (c0 & 255) | ((c1 & 255) << 8) | ((c2 & 255) << 16) | ((c3 & 255) << 24);
+        if ((lane & 3) == 0) qc[nsb * 65 + s * 16 + (lane >> 2)] = s16;
+        int pw[4] = {0, 0, 0, 0};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int b = __builtin_amdgcn_readlane(b32, 8 * i);
-        pw[i >> 2] |= ((b >> 6) & 255) << (8 * (i & 3));
-        pw[2 + (i >> 2)] |= (b & 63) << (8 * (i & 3));
+        for (int i = 0; i < 8; ++i) {
+            const int b = __builtin_amdgcn_readlane(b32, 8 * i);
+            pw[i >> 2] |= ((b >> 6) & 255) << (8 * (i & 3));
+            pw[2 + (i >> 2)] |= (b & 63) << (8 * (i & 3));
+        }
+        if (lane < 4) qc[nsb * 81 + s * 4 + lane] = lane == 0 ? pw[0] : (lane == 1 ? pw[1] : (lane == 2 ? pw[2] : pw[3]));
+        if (lane == 0) reinterpret_cast<float*>(qc + nsb * 64)[s] = d;
     }
-    if (lane < 4) qc[nsb * 81 + s * 4 + lane] = lane == 0 ? pw[0] : (lane == 1 ? pw[1] : (lane == 2 ? pw[2] : pw[3]));
-    if (lane == 0) reinterpret_cast<float*>(qc + nsb * 64)[s] = d;
     if (use_ao) actF16Store(ao, nsb, s, col, lane, c0, c1, c2, c3, b32, d);
 }
 
@@ -373,7 +375,7 @@ __global__ __launch_bounds__(1024) void silu_mul_q8k_kernel(const float* __restr
                                                            ActF16 ao, int has_ao) {
     const int nsb = n / 256;
     const int c = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    int* qc = q + (size_t)c * nsb * 85;
+    int* qc = q ? q + (size_t)c * nsb * 85 : nullptr;
     const int nw = blockDim.x >> 6;
     for (int sb = wave; sb < nsb; sb += nw) {
         const size_t o = (size_t)c * n + sb * 256 + 4 * lane;
@@ -843,7 +845,8 @@ __global__ __launch_bounds__(1024) void add_norm_q8k_kernel(const float* a, cons
         const float r = rmsScale(ss, nb, n, eps);
         const float4 yv = make_float4(v.x * r * wv.x, v.y * r * wv.y, v.z * r * wv.z, v.w * r * wv.w);
         if (y) store4<A16>(y + r0 + i, yv);
-        quant256Wave(yv.x, yv.y, yv.z, yv.w, q + (size_t)row * nsb * 85, nsb, wave, ao, has_ao != 0, row);
+        quant256Wave(yv.x, yv.y, yv.z, yv.w, q ? q + (size_t)row * nsb * 85 : nullptr, nsb, wave, ao, has_ao != 0,
+                     row);
         return;
     }
     for (int i = 4 * tid; i < n; i += 4 * nt) {
@@ -875,7 +878,7 @@ __global__ __launch_bounds__(1024) void add_norm_q8k_kernel(const float* a, cons
     }
     __syncthreads();
     const float r = rmsScale(ss, nb, n, eps);
-    int* qr = q + (size_t)row * nsb * 85;
+    int* qr = q ? q + (size_t)row * nsb * 85 : nullptr;
     for (int sb = wave; sb < nsb; sb += nt >> 6) {
         const int e = sb * 256 + 4 * lane;
         const float4 xv = *reinterpret_cast<const float4*>(xs + (e >> 5) * 36 + (e & 31));
@@ -1116,6 +1119,7 @@ int launchSiluMulQ8(bool per256, const kcSiluMulQ8FArgs& a, hipStream_t s) {
 
 int launchSiluMulQ8KAct(const kcSiluMulQ8FArgs& a, const ActF16* ao, hipStream_t s) {
     if (a.cols <= 0) return 0;
+    if (!a.q && !ao) return fromHip(hipErrorInvalidValue, "silu_mul_q8kf: no quantized output");
     if (al16(a.g) && al16(a.u) && (!a.y || al16(a.y)))
         hipLaunchKernelGGL(silu_mul_q8k_kernel<true>, dim3(a.cols), dim3(waveThreads(a.n)), 0, s, a.g, a.u, a.y, a.q,
                            a.n, a.cols, ao ? *ao : ActF16{}, ao ? 1 : 0);
@@ -1207,6 +1211,7 @@ int launchRopeKvRows(const RopeKvRows& r, hipStream_t s) {
 int launchAddNormQ8K(const float* a, const float* b, const float* b2, float* out, const float* w, int* q, int n,
                      int rows, float eps, hipStream_t s, const ActF16* ao, float* y) {
     if (rows <= 0) return 0;
+    if (!q && !ao) return fromHip(hipErrorInvalidValue, "add + norm: no quantized output");
     const size_t lds = sizeof(float) * ((size_t)n / 32 * 37);
     if (n % 256 || lds > 65536) return fromHip(hipErrorInvalidValue, "add + norm: row length");
     // the register form wherever a row is at most four values per thread (option addnorm_lds = 1:

@@ -210,6 +210,33 @@ def test_prompt_add_norm_register_form_bit_identical(n_embd):
     assert rel_l2(got[0][0][0], lo) < 1e-2
 
 
+@pytest.mark.parametrize("cfg", [LLAMA, QWEN], ids=["llama", "qwen3"])
+def test_prompt_without_int8_slots_bit_identical(cfg):
+    """A prompt whose quantizers write only the matrix-core operand layout (the default: no int8
+    slots where no product reads them) against one whose products convert the int8 slots themselves
+    (option prefill_act = 1): the same logits and cache bits, for a 70-token prompt (slots skipped)
+    and a 33-token continuation (under 64 columns: slots written and read)."""
+    w = random_weights(cfg, 29)
+    prompt = np.random.default_rng(8).integers(0, cfg["n_vocab"], 70 + 33).astype(np.int32)
+    got = {}
+    for act in (1, 0):
+        kc.set_option("prefill_act", act)
+        try:
+            m = kc.Model(**cfg)
+            for (tid, layer), data in w.items():
+                m.set_tensor(tid, layer, data)
+            lg = [m.forward(prompt[:70]), m.forward(prompt[70:])]
+            caches = [m.read_cache(li, which, 0, len(prompt)) for li in range(cfg["n_layer"]) for which in (0, 1)]
+            got[act] = (lg, caches)
+            m.close()
+        finally:
+            kc.set_option("prefill_act", 0)
+    for a, b in zip(got[0][0], got[1][0]):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    for a, b in zip(got[0][1], got[1][1]):
+        assert np.array_equal(a, b)
+
+
 def test_model_3b_shape_two_layers():
     """Two layers at the full Llama-3.2-3B widths (3072 / 24 heads / 8 KV heads / 8192 FFN / 128256
     vocab): an 8-token prompt and two decode steps against the oracle."""
