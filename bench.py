@@ -703,7 +703,8 @@ def main():
             "eager_kernel_us": round(r1["kernel_ms"] * 1e3, 3), "eager_floor_us": round(r1["floor_ms"] * 1e3, 3),
             "eager_achieved_gbs": round(b1 / (r1["kernel_ms"] * 1e-3) / 1e9, 1), "bytes": b1,
             "rotation": f"{copies1} weight copies",
-            "note": "kernel_us: the matvecs over the rotation replayed as one HIP graph (SURVEY method), per matvec; "
+            "note": "kernel_us: the matvecs over the rotation replayed as one HIP graph (the launch cost "
+                    "amortised over the graph), per matvec; "
                     "eager_kernel_us: the same launches one host call each; *_floor_us: the same launch counts of a "
                     "256-element vector_add (what a launch costs however small)"}
         if cpu:
